@@ -1,0 +1,417 @@
+#!/usr/bin/env python
+"""Benchmark of the quantized-linear hot path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--config C]
+    python bench.py --summarize-rocprof DIR     # digest a rocprofv3 --kernel-trace run
+
+Default workload: BASELINE.json configs[1], the talker decode linear stack.  28
+layers x {qkv 2048->4096, o 2048->2048, gate_up 2048->12288, down 6144->2048},
+each layer with its own seeded int8 weights (1.41 GB, > 5x the 256 MB Infinity
+Cache), bf16 activations, M in {1, 2, 4, 8}.  The 112 GEMMs of one M are captured
+into one HIP graph.  One step = one replay of the stack at each of the four M.
+
+Printed: one JSON line with the whole-step HBM throughput (algorithmic bytes /
+time), the per-M stack time next to the bf16 hipBLASLt baseline of the same
+stack, a roofline entry for the dominant kernel (gate_up, measured per launch
+with HIP events on its stream) and the reference's CPU path timed on a bounded
+sample on this host.
+
+Other configs (--config 0..4) print their own JSON line with the same keys.
+"""
+
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import os
+import statistics
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tts-inference_amd"))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E, published
+BF16_PEAK_TFLOPS = 2500.0       # dense bf16 MFMA, published
+FP8_PEAK_TFLOPS = 5000.0        # dense fp8 MFMA, published
+
+TALKER = [("qkv", 4096, 2048), ("o", 2048, 2048), ("gate_up", 12288, 2048), ("down", 2048, 6144)]
+PREDICTOR = [("qkv", 4096, 1024), ("o", 1024, 2048), ("gate_up", 6144, 1024), ("down", 1024, 3072)]
+
+
+def w8a16_bytes(m: int, n: int, k: int) -> int:
+    """Algorithmic HBM bytes of one W8A16 GEMM: int8 weight, bf16 scale, bf16 x in, bf16 y out."""
+    return n * k + 2 * n + 2 * m * k + 2 * m * n
+
+
+def fp8_bytes(m: int, n: int, k: int) -> int:
+    """fp8 W8A8: e4m3 weight, fp32 scale, bf16 x in (quantized once), bf16 y out."""
+    return n * k + 4 * n + 2 * m * k + 2 * m * n
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------------------
+# weights and inputs
+# ---------------------------------------------------------------------------------------
+
+def make_stack(torch, ops, shapes, layers: int, keep_bf16: bool, fp8: bool = False):
+    """Distinct seeded weights per (layer, linear): W ~ N(0, 0.02) fp32, seed 1000 + 16*layer + idx."""
+    stack = []
+    for layer in range(layers):
+        for idx, (name, n, k) in enumerate(shapes):
+            g = torch.Generator(device="cuda").manual_seed(1000 + 16 * layer + idx)
+            w = torch.randn(n, k, device="cuda", generator=g) * 0.02
+            if fp8:
+                q, s = ops.pack_fp8(w)
+            else:
+                q, s = ops.pack_int8(w, torch.bfloat16)
+            wb = w.to(torch.bfloat16) if keep_bf16 else None
+            stack.append({"layer": layer, "name": name, "n": n, "k": k, "q": q, "s": s, "w_bf16": wb})
+            del w
+    torch.cuda.synchronize()
+    return stack
+
+
+def make_inputs(torch, ks, ms, outliers: bool = False):
+    """bf16 activations ~ N(0, 1), seed 7 (+ 1% of entries at +/-20 with ``outliers``)."""
+    xs = {}
+    for m in ms:
+        for k in sorted(set(ks)):
+            g = torch.Generator(device="cuda").manual_seed(7 + 131 * m + k)
+            x = torch.randn(m, k, device="cuda", generator=g)
+            if outliers:
+                mask = torch.rand(m, k, device="cuda", generator=g) < 0.01
+                x = torch.where(mask, torch.sign(x) * 20.0, x)
+            xs[(m, k)] = x.to(torch.bfloat16)
+    return xs
+
+
+def capture(torch, fn):
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(torch, graph, steps: int, warmup: int) -> float:
+    """Mean ms per replay over ``steps`` replays, bracketed by synchronize, events on the replay stream."""
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+def per_launch_ms(torch, launches, reps: int) -> float:
+    """Average kernel duration of ``launches`` (callables of one kernel each), timed one by one with
+    HIP events recorded on the stream the kernel is launched on."""
+    stream = torch.cuda.current_stream()
+    pairs = []
+    for _ in range(reps):
+        for fn in launches:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record(stream)
+            fn()
+            b.record(stream)
+            pairs.append((a, b))
+    torch.cuda.synchronize()
+    times = [a.elapsed_time(b) for a, b in pairs]
+    return sum(times) / len(times)
+
+
+# ---------------------------------------------------------------------------------------
+# CPU baseline: the reference's CPU path, timed on this host
+# ---------------------------------------------------------------------------------------
+
+def cpu_baseline_w8a16(torch, stack, xs, ms, budget_s: float, layers_sample: int):
+    from oracle import cpu_path
+    threads = torch.get_num_threads()
+    sample = [e for e in stack if e["layer"] < layers_sample]
+    cpu = [(e, e["q"].cpu(), e["s"].cpu()) for e in sample]
+    xcpu = {key: v.cpu() for key, v in xs.items()}
+    total_bytes = 0
+    total_s = 0.0
+    started = time.perf_counter()
+    for m in ms:
+        for e, q, s in cpu:
+            x = xcpu[(m, e["k"])]
+            for _ in range(3):
+                cpu_path.naive_dequant_linear(x, q, s)
+            ts = []
+            for _ in range(10):
+                t0 = time.perf_counter()
+                cpu_path.naive_dequant_linear(x, q, s)
+                ts.append(time.perf_counter() - t0)
+                if time.perf_counter() - started > budget_s and len(ts) >= 3:
+                    break
+            total_s += statistics.median(ts)
+            total_bytes += w8a16_bytes(m, e["n"], e["k"])
+    return {
+        "value": round(total_bytes / total_s / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (f"reference CPU path F.linear(x_bf16, q.to(bf16)*scale[:,None]) (oracle/cpu_path.py) on "
+                   f"{layers_sample} of 28 talker layers x 4 linears x M in {list(ms)}, median of up to 10 "
+                   f"after 3 warm-ups, torch CPU with {threads} threads; "
+                   f"{total_s * 1e3:.1f} ms for {total_bytes / 1e6:.1f} MB"),
+    }
+
+
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+# ---------------------------------------------------------------------------------------
+# configs
+# ---------------------------------------------------------------------------------------
+
+def run_talker_stack(args, torch, ops):
+    """the 28-layer talker decode stack, int8 weight-only, M in {1, 2, 4, 8}."""
+    ms = (1, 2, 4, 8)
+    layers = 28
+    log(f"[bench] packing {layers}x4 talker weights (int8 + bf16 baseline copy)")
+    stack = make_stack(torch, ops, TALKER, layers, keep_bf16=True)
+    ops.reserve_workspace(torch.device("cuda"), max(
+        ops.workspace_bytes(ops.OP_W8A16, m, e["n"], e["k"]) for m in ms for e in stack[:4]))
+    xs = make_inputs(torch, [k for _, _, k in TALKER], ms)
+    int8_bytes = sum(e["q"].numel() for e in stack)
+
+    per_m = {}
+    total_bytes = 0
+    total_ms = 0.0
+    for m in ms:
+        log(f"[bench] M={m}: capture + time int8 stack and bf16 stack")
+        g_q = capture(torch, lambda m=m: [ops.w8a16_gemm(xs[(m, e["k"])], e["q"], e["s"]) for e in stack])
+        g_b = capture(torch, lambda m=m: [torch.nn.functional.linear(xs[(m, e["k"])], e["w_bf16"]) for e in stack])
+        t_q = time_graph(torch, g_q, args.steps, args.warmup)
+        t_b = time_graph(torch, g_b, max(5, args.steps // 2), args.warmup)
+        nbytes = sum(w8a16_bytes(m, e["n"], e["k"]) for e in stack)
+        total_bytes += nbytes
+        total_ms += t_q
+        per_m[str(m)] = {
+            "stack_us": round(t_q * 1e3, 2),
+            "GBps": round(nbytes / (t_q * 1e-3) / 1e9, 1),
+            "pct_of_hbm_peak": round(100 * nbytes / (t_q * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1),
+            "bf16_hipblaslt_stack_us": round(t_b * 1e3, 2),
+            "speedup_vs_bf16": round(t_b / t_q, 3),
+        }
+        del g_q, g_b
+        log(f"[bench] M={m}: {per_m[str(m)]}")
+
+    # Dominant kernel (gate_up, the largest share of the stack): per-launch duration over the
+    # 28 distinct gate_up weights, HIP events on the launch stream.
+    rm = 4
+    gate = [e for e in stack if e["name"] == "gate_up"]
+    launches = [lambda e=e: ops.w8a16_gemm(xs[(rm, e["k"])], e["q"], e["s"]) for e in gate]
+    dur_ms = per_launch_ms(torch, launches, reps=max(2, args.steps // 4))
+    g_bytes = w8a16_bytes(rm, 12288, 2048)
+    achieved = g_bytes / (dur_ms * 1e-3) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "kernel": "w8a16_skinny_kernel (gate_up 12288x2048, M=4)", "avg_launch_us": round(dur_ms * 1e3, 3),
+                "bytes_per_launch": g_bytes}
+
+    result = {
+        "metric": "int8 W-only decode GEMM HBM GB/s (% of peak) + linear-stack us/step, M=1..8",
+        "value": round(total_bytes / (total_ms * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "pct_of_hbm_peak": round(100 * total_bytes / (total_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(total_ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) weights per layer, N(0,1) bf16 activations)",
+        "config": {"workload": "configs[1]: talker decode linear stack, 28 layers x {qkv,o,gate_up,down}, "
+                               "int8 weight-only, one HIP graph per M", "layers": layers, "M": list(ms),
+                   "int8_weight_bytes": int8_bytes, "parallelism": "none (1 GPU)"},
+        "per_m": per_m,
+        "roofline": roofline,
+    }
+    if not args.no_cpu_baseline:
+        log("[bench] CPU baseline (reference CPU path on a 2-layer sample)")
+        result["cpu_baseline"] = cpu_baseline_w8a16(torch, stack, xs, ms, args.cpu_seconds, layers_sample=2)
+        result["cpu_baseline"]["cpu_model"] = cpu_model()
+    return result
+
+
+def run_single_linear(args, torch, ops):
+    """one gate_up linear, M=1, rotated over >= 512 MB of distinct weight copies."""
+    copies = 24
+    stack = make_stack(torch, ops, [("gate_up", 12288, 2048)], copies, keep_bf16=False)
+    xs = make_inputs(torch, [2048], [1])
+    g = capture(torch, lambda: [ops.w8a16_gemm(xs[(1, 2048)], e["q"], e["s"]) for e in stack])
+    t = time_graph(torch, g, args.steps, args.warmup)
+    nbytes = copies * w8a16_bytes(1, 12288, 2048)
+    dur_ms = per_launch_ms(torch, [lambda e=e: ops.w8a16_gemm(xs[(1, 2048)], e["q"], e["s"]) for e in stack], 2)
+    per = w8a16_bytes(1, 12288, 2048)
+    return {"metric": "int8 W-only GEMM HBM GB/s, single gate_up linear", "value": round(nbytes / (t * 1e-3) / 1e9, 1),
+            "unit": "GB/s", "ms_per_step": round(t, 4), "steps": args.steps, "warmup": args.warmup, "n_gpus": 1,
+            "config": {"workload": f"configs[0]: gate_up 12288x2048 M=1 x {copies} distinct copies per step"},
+            "roofline": {"bound": "hbm", "achieved": round(per / (dur_ms * 1e-3) / 1e9, 1), "peak": HBM_PEAK_GBPS,
+                         "unit": "GB/s", "frac": round(per / (dur_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                         "traffic": None, "avg_launch_us": round(dur_ms * 1e3, 3)}}
+
+
+def run_predictor(args, torch, ops):
+    """code-predictor stack, 5 layers, 15 prefix passes (prefix 2..16) per frame, batch 1..8."""
+    layers = 5
+    stack = make_stack(torch, ops, PREDICTOR, layers, keep_bf16=True)
+    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    out = {}
+    for b in (1, 8):
+        ms = [b * p for p in range(2, 17)]
+        xs = make_inputs(torch, [k for _, _, k in PREDICTOR], ms)
+        g_q = capture(torch, lambda: [ops.w8a16_gemm(xs[(m, e["k"])], e["q"], e["s"]) for m in ms for e in stack])
+        g_b = capture(torch, lambda: [torch.nn.functional.linear(xs[(m, e["k"])], e["w_bf16"])
+                                      for m in ms for e in stack])
+        t_q = time_graph(torch, g_q, args.steps, args.warmup)
+        t_b = time_graph(torch, g_b, args.steps, args.warmup)
+        out[f"batch{b}"] = {"frame_us": round(t_q * 1e3, 2), "pass_us": round(t_q * 1e3 / 15, 2),
+                            "bf16_frame_us": round(t_b * 1e3, 2), "speedup_vs_bf16": round(t_b / t_q, 3),
+                            "launches_per_frame": len(ms) * len(stack)}
+    return {"metric": "code-predictor linear stack us/frame", "value": out["batch1"]["frame_us"], "unit": "us",
+            "higher_is_better": False, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "config": {"workload": "configs[2]: 5 layers x 4 linears x 15 prefix passes, int8 weight-only"},
+            "per_batch": out}
+
+
+def run_prefill(args, torch, ops):
+    """talker shapes at M in {64, 256, 1024}: MFMA tile path vs hipBLASLt bf16."""
+    stack = make_stack(torch, ops, TALKER, 1, keep_bf16=True)
+    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    res = {}
+    for m in (64, 256, 1024):
+        xs = make_inputs(torch, [2048, 6144], [m])
+        for e in stack:
+            fq = lambda e=e: ops.w8a16_gemm(xs[(m, e["k"])], e["q"], e["s"])
+            fb = lambda e=e: torch.nn.functional.linear(xs[(m, e["k"])], e["w_bf16"])
+            gq = capture(torch, lambda: [fq() for _ in range(10)])
+            gb = capture(torch, lambda: [fb() for _ in range(10)])
+            tq = time_graph(torch, gq, args.steps, args.warmup) / 10
+            tb = time_graph(torch, gb, args.steps, args.warmup) / 10
+            fl = 2 * m * e["n"] * e["k"]
+            res[f"M{m}_{e['name']}"] = {"us": round(tq * 1e3, 2), "bf16_us": round(tb * 1e3, 2),
+                                        "speedup": round(tb / tq, 3),
+                                        "TFLOPs": round(fl / (tq * 1e-3) / 1e12, 1),
+                                        "mfma_util": round(fl / (tq * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
+    return {"metric": "prefill W8A16 MFMA utilisation / speedup vs bf16", "value": None, "unit": "TFLOP/s",
+            "n_gpus": 1, "config": {"workload": "configs[3]: talker shapes, M in {64, 256, 1024}"}, "shapes": res}
+
+
+def run_fp8(args, torch, ops):
+    """fp8 W8A8 on the talker shapes, M in {1, 8, 256}, x with 1% outliers at 20 sigma."""
+    stack = make_stack(torch, ops, TALKER, 1, keep_bf16=True, fp8=True)
+    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    res = {}
+    for m in (1, 8, 256):
+        xs = make_inputs(torch, [2048, 6144], [m], outliers=True)
+        for e in stack:
+            fq = lambda e=e: ops.fp8_linear(xs[(m, e["k"])], e["q"], e["s"])
+            fb = lambda e=e: torch.nn.functional.linear(xs[(m, e["k"])], e["w_bf16"])
+            gq = capture(torch, lambda: [fq() for _ in range(10)])
+            gb = capture(torch, lambda: [fb() for _ in range(10)])
+            tq = time_graph(torch, gq, args.steps, args.warmup) / 10
+            tb = time_graph(torch, gb, args.steps, args.warmup) / 10
+            nb = fp8_bytes(m, e["n"], e["k"])
+            res[f"M{m}_{e['name']}"] = {"us": round(tq * 1e3, 2), "bf16_us": round(tb * 1e3, 2),
+                                        "speedup": round(tb / tq, 3), "GBps": round(nb / (tq * 1e-3) / 1e9, 1)}
+    return {"metric": "fp8 W8A8 linear us and GB/s", "value": None, "unit": "GB/s", "n_gpus": 1,
+            "config": {"workload": "configs[4]: talker shapes, fp8 W8A8, M in {1, 8, 256}"}, "shapes": res}
+
+
+# ---------------------------------------------------------------------------------------
+# rocprofv3 digest
+# ---------------------------------------------------------------------------------------
+
+def summarize_rocprof(path: str) -> None:
+    """Average duration per (kernel, grid) from rocprofv3 --kernel-trace CSV output under ``path``."""
+    files = glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *kernel_trace.csv under {path}")
+    groups: dict[tuple[str, str], list[float]] = {}
+    for f in files:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                name = row.get("Kernel_Name") or row.get("KernelName") or "?"
+                grid = "x".join(row.get(c, "") for c in ("Grid_Size_X", "Grid_Size_Y", "Grid_Size_Z") if row.get(c))
+                if not grid:
+                    grid = row.get("Grid_Size", "?")
+                start = float(row.get("Start_Timestamp") or row.get("BeginNs") or 0)
+                end = float(row.get("End_Timestamp") or row.get("EndNs") or 0)
+                groups.setdefault((name[:110], grid), []).append((end - start) / 1e3)
+    rows = sorted(groups.items(), key=lambda kv: -sum(kv[1]))
+    total = sum(sum(v) for _, v in rows)
+    print(f"{'calls':>7} {'avg_us':>9} {'min_us':>9} {'total_us':>11} {'pct':>6}  grid  kernel")
+    for (name, grid), v in rows[:40]:
+        print(f"{len(v):7d} {sum(v) / len(v):9.3f} {min(v):9.3f} {sum(v):11.1f} {100 * sum(v) / total:5.1f}%  "
+              f"{grid}  {name}")
+
+
+# ---------------------------------------------------------------------------------------
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=1, choices=range(5), help="index into BASELINE.json configs")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=20.0, help="time budget of the CPU baseline sample")
+    ap.add_argument("--summarize-rocprof", metavar="DIR")
+    args = ap.parse_args()
+
+    if args.summarize_rocprof:
+        summarize_rocprof(args.summarize_rocprof)
+        return 0
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this path runs on one GPU: each GPU box has one MI355X and the quantized "
+                                   "linear has no collective; run with --gpus 1 (multi-GPU sharding is "
+                                   "described, not built)", "n_gpus": args.gpus}), flush=True)
+        return 2
+
+    import torch
+    from qtts_amd import ops
+
+    if not torch.cuda.is_available() or not ops.device_supported():
+        raise SystemExit("bench.py needs a gfx950 GPU")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    runner = {0: run_single_linear, 1: run_talker_stack, 2: run_predictor, 3: run_prefill, 4: run_fp8}[args.config]
+    with torch.inference_mode():
+        result = runner(args, torch, ops)
+    result["device"] = torch.cuda.get_device_name()
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,144 @@
+/*
+ * qtts_amd — C ABI of the MI355X (gfx950) quantized-linear hot path.
+ *
+ * One shared library, libqtts_amd.so, built from tts-inference_amd/csrc.  Every
+ * entry point takes plain device pointers, sizes in elements, leading dimensions
+ * in elements and a hipStream_t passed as void*.  Nothing here allocates device
+ * memory, synchronises the stream or reads device memory on the host, so every
+ * call can be captured into a hipGraph.  The caller owns every buffer.
+ *
+ * Return value: QTTS_OK (0) or a negative qtts_status; qtts_last_error() then
+ * holds a message for the calling thread.
+ */
+#ifndef QTTS_AMD_H
+#define QTTS_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QTTS_ABI_VERSION 1
+
+typedef enum {
+    QTTS_OK = 0,
+    QTTS_ERR_INVALID_ARGUMENT = -1, /* shapes, strides, dtypes: the reference raises ValueError */
+    QTTS_ERR_UNSUPPORTED = -2,      /* no gfx950 device / unsupported combination: RuntimeError */
+    QTTS_ERR_NOT_IMPLEMENTED = -3,  /* NotImplementedError */
+    QTTS_ERR_HIP = -4,              /* a HIP runtime call failed: RuntimeError */
+    QTTS_ERR_WORKSPACE = -5         /* workspace missing or too small: ValueError */
+} qtts_status;
+
+/* Element types.  Activations, outputs, biases and stored scales use these codes. */
+typedef enum { QTTS_F32 = 0, QTTS_BF16 = 1, QTTS_F16 = 2 } qtts_dtype;
+
+/* How `tensor / python_float` rounds in the reference's scale computations
+ * (qtts/quant/int8.py:54, qtts/quant/fp8.py:48, qtts/quant/fp8.py:77).
+ * QTTS_DIV_DEVICE: t * fl(1/c), what torch computes for a GPU tensor — the
+ *                  reference's production path, since it quantizes on the GPU.
+ * QTTS_DIV_IEEE:   t / c, what torch computes for a CPU tensor. */
+typedef enum { QTTS_DIV_DEVICE = 0, QTTS_DIV_IEEE = 1 } qtts_div_mode;
+
+/* Kernel family for the GEMMs.  AUTO picks by shape; the calibrator pins one. */
+typedef enum { QTTS_ALGO_AUTO = 0, QTTS_ALGO_SKINNY = 1, QTTS_ALGO_TILE = 2 } qtts_algo;
+
+/* Workspace owners for qtts_workspace_bytes. */
+typedef enum { QTTS_OP_W8A16 = 0, QTTS_OP_W8A8_FP8 = 1, QTTS_OP_FP8_LINEAR = 2 } qtts_op;
+
+/* --- housekeeping ------------------------------------------------------------ */
+
+int qtts_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* qtts_last_error(void);
+
+/* 1 if `device` is a gfx950 GPU this library can run on, 0 otherwise.
+ * Replaces the capability test of fp8_supported (qtts/quant/base.py:133-152)
+ * and the Triton check of kernel_available (qtts/quant/kernels.py:83-84). */
+int qtts_device_supported(int device);
+
+/* Bytes of workspace `op` needs for an [m, k] x [n, k]^T product with `algo`
+ * (QTTS_ALGO_AUTO: the largest any automatic choice uses).  The workspace holds
+ * split-K counters and partial sums.  It must be zero-filled before its first use
+ * with this library; every call leaves its counters at zero again (partial sums
+ * need no clearing), so one buffer serves any number of calls, including graph
+ * replays, with no memset.  Calls that share a workspace must be ordered (one
+ * stream); concurrent calls on one workspace race.  A buffer smaller than a
+ * call's automatic choice needs is not an error: the call then runs without
+ * split-K.  An explicit split count (algo bits 8-15) that does not fit is.
+ *
+ * `algo` for the GEMMs: a qtts_algo in bits 0-7; bits 8-15 force the number of
+ * K splits across workgroups and bits 16-23 the waves per workgroup of the
+ * skinny kernels (0 = automatic).  The calibrator uses these to time variants. */
+int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo);
+
+/* --- weight packers ------------------------------------------------------------ */
+
+/* Symmetric per-output-channel int8, replacing quantize_weight_per_channel
+ * (qtts/quant/int8.py:45-56) plus the stored-scale cast of
+ * Int8WeightOnlyMethod.process_weights (qtts/quant/int8.py:105):
+ *   scale[r] = max(amax_c |w[r,c]|, 1e-12) / 127         (fp32, div_mode)
+ *   q[r, c]  = clamp(round_half_even(w[r,c] / scale[r]), -127, 127)
+ * src: [n, k] of src_dtype with row stride ld_src.  q_out: [n, k] int8, row
+ * stride k.  scale_out: [n] of scale_dtype (rounded to nearest even from fp32).
+ * scale_f32_out: optional [n] fp32 copy of the unrounded scale (NULL to skip). */
+int qtts_pack_int8_rowwise(const void* src, int src_dtype, int64_t n, int64_t k, int64_t ld_src,
+                           int8_t* q_out, void* scale_out, int scale_dtype, float* scale_f32_out,
+                           int div_mode, void* stream);
+
+/* Symmetric per-output-channel OCP e4m3fn, replacing quantize_weight_fp8
+ * (qtts/quant/fp8.py:45-49):
+ *   scale[r] = max(amax_c |w[r,c]|, 1e-12) / 448 ; q = e4m3_rne(w / scale)
+ * q_out: [n, k] e4m3 bytes, row stride k; scale_out: [n] fp32. */
+int qtts_pack_fp8_e4m3_rowwise(const void* src, int src_dtype, int64_t n, int64_t k, int64_t ld_src,
+                               uint8_t* q_out, float* scale_out, int div_mode, void* stream);
+
+/* --- W8A16: int8 weights, bf16/fp16/fp32 activations ----------------------------- */
+
+/* y[m, n] = cast(sum_c x[m,c] * q[n,c] * f32(scale[n]) + f32(bias[n])), fp32
+ * accumulation, replacing w8_gemm (qtts/quant/kernels.py:138-178) and its kernel
+ * _w8_gemm_kernel (qtts/quant/kernels.py:89-135).
+ * x: [m, k] of x_dtype, row stride ldx.  q: [n, k] int8, row stride ldq.
+ * scale: [n] of scale_dtype.  bias: [n] of x_dtype, or NULL.  y: [m, n] of x_dtype,
+ * row stride ldy.  ws/ws_bytes: workspace (see qtts_workspace_bytes); may be NULL
+ * when the chosen kernel needs none. */
+int qtts_w8a16_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                    const int8_t* q, int64_t n, int64_t ldq,
+                    const void* scale, int scale_dtype, const void* bias,
+                    void* y, int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream);
+
+/* --- fp8 W8A8 --------------------------------------------------------------------- */
+
+/* Per-token e4m3 activation quantization, replacing the activation half of
+ * Fp8Method.apply (qtts/quant/fp8.py:77-78):
+ *   sx[r] = f32(max(amax_c |x[r,c]|, dtype(1e-6))) / 448  (amax and clamp in x_dtype)
+ *   qx[r, c] = e4m3_rne(f32(x[r,c]) / sx[r])
+ * qx: [m, k] e4m3 bytes, row stride k.  sx: [m] fp32. */
+int qtts_quant_act_fp8_rows(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                            uint8_t* qx, float* sx, int div_mode, void* stream);
+
+/* y[m, n] = cast(cast(sum_c qx[m,c] * qw[n,c] * sx[m] * sw[n]) + bias[n]), fp32
+ * accumulation on fp8 MFMA, replacing torch._scaled_mm with rowwise scales and the
+ * bias add that follows it (qtts/quant/fp8.py:79-89).  The product is rounded to
+ * out_dtype before the bias is added in out_dtype, as the reference does.
+ * qx: [m, k] e4m3, row stride ldqx.  qw: [n, k] e4m3, row stride ldqw.
+ * bias: [n] of out_dtype or NULL.  y: [m, n] of out_dtype (QTTS_BF16/F16/F32). */
+int qtts_w8a8_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx,
+                       const uint8_t* qw, int64_t n, int64_t ldqw, const float* sw,
+                       const void* bias, void* y, int out_dtype, int64_t ldy,
+                       int algo, void* ws, int64_t ws_bytes, void* stream);
+
+/* The whole of Fp8Method.apply (qtts/quant/fp8.py:72-89) in one call:
+ * qtts_quant_act_fp8_rows into the workspace, then qtts_w8a8_fp8_gemm.
+ * x: [m, k] of x_dtype; y: [m, n] of x_dtype; bias: [n] of x_dtype or NULL. */
+int qtts_fp8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                    const uint8_t* qw, int64_t n, int64_t ldqw, const float* sw,
+                    const void* bias, void* y, int64_t ldy, int div_mode,
+                    int algo, void* ws, int64_t ws_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QTTS_AMD_H */

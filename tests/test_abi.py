@@ -1,0 +1,106 @@
+"""The C ABI without a GPU: the library loads, exports every symbol the header
+declares, validates arguments before touching a device, and maps status codes to
+the reference's exception types."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from qtts_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qtts_amd.h")
+
+
+def _declared() -> list[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\*?\s+\*?(qtts_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_exported_set():
+    declared = _declared()
+    assert declared == sorted(_lib.EXPORTS), declared
+
+
+def test_library_exports_every_declared_symbol():
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    for name in _declared():
+        assert hasattr(L, name), f"{name} declared in include/qtts_amd.h but not exported"
+
+
+def test_abi_version_and_enums_match_header():
+    L = _lib.load()
+    assert L.qtts_abi_version() == _lib.ABI_VERSION
+    text = open(HEADER).read()
+    assert f"#define QTTS_ABI_VERSION {_lib.ABI_VERSION}" in text
+    for name, value in (("QTTS_ERR_INVALID_ARGUMENT", -1), ("QTTS_ERR_UNSUPPORTED", -2),
+                        ("QTTS_ERR_NOT_IMPLEMENTED", -3), ("QTTS_ERR_HIP", -4), ("QTTS_ERR_WORKSPACE", -5),
+                        ("QTTS_F32", 0), ("QTTS_BF16", 1), ("QTTS_F16", 2), ("QTTS_DIV_DEVICE", 0),
+                        ("QTTS_DIV_IEEE", 1), ("QTTS_ALGO_AUTO", 0), ("QTTS_ALGO_SKINNY", 1), ("QTTS_ALGO_TILE", 2)):
+        assert re.search(rf"\b{name}\s*=\s*{value}\b", text), name
+
+
+def test_argument_validation_precedes_device_use():
+    """Bad arguments are rejected with INVALID_ARGUMENT before any HIP call (works with no GPU)."""
+    L = _lib.load()
+    assert L.qtts_w8a16_gemm(None, 1, -1, 16, 16, None, 8, 16, None, 1, None, None, 8, 0, None, 0, None) == -1
+    assert "negative size" in _lib.last_error()
+    assert L.qtts_w8a16_gemm(None, 7, 1, 16, 16, None, 8, 16, None, 1, None, None, 8, 0, None, 0, None) == -1
+    assert L.qtts_w8a16_gemm(None, 1, 1, 16, 8, None, 8, 16, None, 1, None, None, 8, 0, None, 0, None) == -1
+    assert "leading dimension" in _lib.last_error()
+    assert L.qtts_w8a16_gemm(None, 1, 1, 16, 16, None, 8, 16, None, 1, None, None, 8, 9, None, 0, None) == -1
+    assert L.qtts_pack_int8_rowwise(None, 1, 4, 16, 16, None, None, 1, None, 5, None) == -1
+    assert L.qtts_quant_act_fp8_rows(None, 1, 2, 16, 8, None, None, 0, None) == -1
+    assert L.qtts_w8a8_fp8_gemm(None, None, 2, 32, 32, None, 4, 32, None, None, None, 9, 4, 0, None, 0, None) == -1
+    # empty problems are a no-op success, with no device needed
+    assert L.qtts_w8a16_gemm(None, 1, 0, 16, 16, None, 8, 16, None, 1, None, None, 8, 0, None, 0, None) == 0
+    assert L.qtts_pack_fp8_e4m3_rowwise(None, 1, 0, 16, 16, None, None, 0, None) == 0
+
+
+def test_null_pointers_rejected():
+    L = _lib.load()
+    assert L.qtts_w8a16_gemm(None, 1, 2, 16, 16, None, 8, 16, None, 1, None, None, 8, 0, None, 0, None) == -1
+    assert "null pointer" in _lib.last_error()
+
+
+def test_workspace_query():
+    L = _lib.load()
+    # one split needs no workspace; forced splits need the counter block plus partials
+    assert L.qtts_workspace_bytes(_lib.OP_W8A16, 4, 2048, 2048, _lib.algo_code(_lib.ALGO_SKINNY, 1)) == 0
+    n = L.qtts_workspace_bytes(_lib.OP_W8A16, 4, 2048, 2048, _lib.algo_code(_lib.ALGO_SKINNY, 4))
+    assert n == 65536 + (2048 // 16) * 4 * 64 * 16
+    assert L.qtts_workspace_bytes(_lib.OP_W8A16, 0, 2048, 2048, 0) == 0
+    assert L.qtts_workspace_bytes(9, 4, 2048, 2048, 0) == -1
+    assert L.qtts_workspace_bytes(_lib.OP_FP8_LINEAR, 8, 2048, 2048, 0) >= 8 * 2048 + 32
+    assert L.qtts_workspace_bytes(_lib.OP_W8A16, 4, 2048, 0, 0) >= 0  # K = 0 is a valid query
+
+
+def test_device_supported_without_gpu_is_false():
+    L = _lib.load()
+    assert L.qtts_device_supported(-1) == 0
+    assert L.qtts_device_supported(10_000) == 0
+
+
+def test_status_mapping():
+    _lib.check(_lib.OK, "x")
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_INVALID_ARGUMENT, "x")
+    with pytest.raises(ValueError):
+        _lib.check(_lib.ERR_WORKSPACE, "x")
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.ERR_NOT_IMPLEMENTED, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.ERR_UNSUPPORTED, "x")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.ERR_HIP, "x")
+
+
+def test_algo_code_packing():
+    assert _lib.algo_code(_lib.ALGO_SKINNY, 4, 8) == 1 | (4 << 8) | (8 << 16)
+    with pytest.raises(ValueError):
+        _lib.algo_code(_lib.ALGO_TILE, 300)

@@ -1,0 +1,238 @@
+"""GPU parity of the W8A16 and fp8 W8A8 GEMMs, through the C ABI.
+
+Reference: the fp64 dequantize-then-matmul of the oracle (oracle/qtts_oracle.c)
+on the same packed bytes and stored scales, at sizes it finishes in seconds;
+a torch fp32 GEMM on the GPU at the large prefill shapes.
+
+Tolerance (north star: max |err| <= 1e-2 x output RMS, bf16 outputs): every
+element must satisfy |y - ref| <= 1e-2 * RMS(ref) + ulp_bf16(ref) / 2.  The
+half-ulp term is what rounding even the exact result to bf16 costs: at a 4-sigma
+output (|y| in [4, 8), RMS ~0.9) it is 0.0156, already above 1e-2 * RMS, so no
+bf16-output kernel could meet the bar without it.  Errors of a real defect (a
+dropped K chunk, a wrong scale row, a missing bias) are O(RMS) and still fail.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TALKER = [(4096, 2048), (2048, 2048), (12288, 2048), (2048, 6144)]
+PREDICTOR = [(4096, 1024), (1024, 2048), (6144, 1024), (1024, 3072)]
+
+
+@pytest.fixture(scope="module")
+def ops():
+    from qtts_amd import ops as _ops
+    assert _ops.device_supported(), "GPU is not a gfx950"
+    _ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    return _ops
+
+
+def half_ulp(ref: np.ndarray, dtype: torch.dtype) -> np.ndarray:
+    mant = {torch.bfloat16: 8, torch.float16: 11, torch.float32: 24}[dtype]
+    a = np.abs(ref).astype(np.float64)
+    e = np.floor(np.log2(np.maximum(a, 1e-30)))
+    if dtype == torch.float16:
+        e = np.maximum(e, -14)
+    return np.ldexp(1.0, (e - (mant - 1)).astype(np.int64)) / 2
+
+
+def assert_close(y: torch.Tensor, ref: np.ndarray, what: str = "") -> float:
+    yv = y.float().cpu().numpy().astype(np.float64)
+    ref = np.asarray(ref, np.float64)
+    assert yv.shape == ref.shape, (yv.shape, ref.shape)
+    rms = float(np.sqrt(np.mean(ref * ref))) if ref.size else 0.0
+    err = np.abs(yv - ref)
+    bound = 1e-2 * rms + half_ulp(ref, y.dtype)
+    bad = err > bound
+    assert not bad.any(), (f"{what}: {int(bad.sum())} elements out of tolerance; max err {err.max():.4g}, "
+                           f"rms {rms:.4g}, worst at {np.unravel_index(np.argmax(err - bound), err.shape)}")
+    return float(err.max() / rms) if rms else 0.0
+
+
+def _make(m, n, k, dtype=torch.bfloat16, bias=False, seed=0):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(dtype)
+    x = torch.randn(m, k, device="cuda", generator=g).to(dtype)
+    b = (torch.randn(n, device="cuda", generator=g) * 0.1).to(dtype) if bias else None
+    return x, w, b
+
+
+def _oracle_w8a16(x, q, scale, b):
+    return O.w8a16_ref(x.float().cpu().numpy(), q.cpu().numpy(), scale.float().cpu().numpy(),
+                       None if b is None else b.float().cpu().numpy())
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+def test_w8a16_brute_force_small(ops, dtype):
+    """Tails in M, N and K, bias on and off, every dtype; includes the generic path (K % 16 != 0)."""
+    for m in (1, 2, 3):
+        for n in (1, 7, 16, 17, 33):
+            for k in (16, 64, 130, 257):
+                for has_bias in (False, True):
+                    x, w, b = _make(m, n, k, dtype, has_bias, seed=m * 1000 + n * 10 + k)
+                    q, s = ops.pack_int8(w, dtype)
+                    y = ops.w8a16_gemm(x, q, s, b)
+                    assert y.dtype == dtype and y.shape == (m, n)
+                    assert_close(y, _oracle_w8a16(x, q, s, b), f"m={m} n={n} k={k} bias={has_bias}")
+
+
+@pytest.mark.parametrize("n,k", TALKER + PREDICTOR)
+def test_w8a16_skinny_decode_shapes(ops, n, k):
+    for m in (1, 2, 4, 8, 16):
+        print(f"skinny n={n} k={k} m={m}", flush=True)
+        x, w, b = _make(m, n, k, seed=n + k + m)
+        q, s = ops.pack_int8(w, torch.bfloat16)
+        y = ops.w8a16_gemm(x, q, s, None, ops.algo_code(1))
+        assert_close(y, _oracle_w8a16(x, q, s, None), f"skinny m={m} n={n} k={k}")
+
+
+def test_w8a16_skinny_configs_agree(ops):
+    """Every split / wave count gives an in-tolerance, run-to-run deterministic answer."""
+    m, n, k = 5, 2048, 6144
+    x, w, b = _make(m, n, k, bias=True, seed=9)
+    q, s = ops.pack_int8(w, torch.bfloat16)
+    ref = _oracle_w8a16(x, q, s, b)
+    for splits in (1, 2, 3, 4, 8, 16):
+        for waves in (1, 2, 4, 8, 16):
+            algo = ops.algo_code(1, splits, waves)
+            y1 = ops.w8a16_gemm(x, q, s, b, algo)
+            y2 = ops.w8a16_gemm(x, q, s, b, algo)
+            assert torch.equal(y1, y2), f"non-deterministic at splits={splits} waves={waves}"
+            assert_close(y1, ref, f"splits={splits} waves={waves}")
+
+
+@pytest.mark.parametrize("m", [17, 32, 33, 64, 100, 128, 256])
+def test_w8a16_tile_vs_oracle(ops, m):
+    for n, k in ((2048, 2048), (1024, 3072), (130 * 16, 1024)):
+        x, w, b = _make(m, n, k, bias=(m % 2 == 1), seed=m + n)
+        q, s = ops.pack_int8(w, torch.bfloat16)
+        ref = _oracle_w8a16(x, q, s, b)
+        y = ops.w8a16_gemm(x, q, s, b, ops.algo_code(2))
+        assert_close(y, ref, f"tile m={m} n={n} k={k}")
+        for splits in (1, 2, 4):
+            y2 = ops.w8a16_gemm(x, q, s, b, ops.algo_code(2, splits))
+            assert_close(y2, ref, f"tile m={m} n={n} k={k} splits={splits}")
+
+
+@pytest.mark.parametrize("n,k", TALKER)
+def test_w8a16_prefill_full_shapes_vs_fp32(ops, n, k):
+    """configs[3] shapes at M in {64, 256, 1024} against a torch fp32 GEMM of the dequantized weight."""
+    for m in (64, 256, 1024):
+        x, w, _ = _make(m, n, k, seed=n * 3 + m)
+        q, s = ops.pack_int8(w, torch.bfloat16)
+        y = ops.w8a16_gemm(x, q, s)
+        ref = (x.float() @ (q.float() * s.float()[:, None]).t()).double().cpu().numpy()
+        assert_close(y, ref, f"prefill m={m} n={n} k={k}")
+
+
+def test_w8a16_hip_graph_replays(ops):
+    """Capture split-K GEMMs into a graph; every replay, between eager work, matches eager."""
+    x, w, b = _make(4, 2048, 2048, bias=True, seed=5)
+    q, s = ops.pack_int8(w, torch.bfloat16)
+    algo = ops.algo_code(1, 4)
+    eager = ops.w8a16_gemm(x, q, s, b, algo)
+    static_x = x.clone()
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        ops.w8a16_gemm(static_x, q, s, b, algo)
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = ops.w8a16_gemm(static_x, q, s, b, algo)
+    for i in range(5):
+        junk = ops.w8a16_gemm(x * (i + 2), q, s, b, algo)  # eager work sharing the workspace
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i} differs from eager"
+        assert_close(junk, _oracle_w8a16(x * (i + 2), q, s, b))
+
+
+def test_w8a16_errors(ops):
+    x, w, _ = _make(2, 32, 64)
+    q, s = ops.pack_int8(w, torch.bfloat16)
+    with pytest.raises(ValueError, match="K=48"):
+        ops.w8a16_gemm(x[:, :48], q, s)
+    with pytest.raises(ValueError):
+        ops.w8a16_gemm(torch.randn(17, 64, device="cuda", dtype=torch.bfloat16), q, s, None, ops.algo_code(1))
+    # an explicit split count with no room for it in the workspace is an error, not a silent downgrade
+    from qtts_amd import _lib
+    x2, w2, _ = _make(2, 64, 1024)
+    q2, s2 = ops.pack_int8(w2, torch.bfloat16)
+    y2 = torch.empty(2, 64, dtype=torch.bfloat16, device="cuda")
+    st = _lib.load().qtts_w8a16_gemm(x2.data_ptr(), 1, 2, 1024, 1024, q2.data_ptr(), 64, 1024, s2.data_ptr(), 1,
+                                     None, y2.data_ptr(), 64, ops.algo_code(1, 2), None, 0,
+                                     torch.cuda.current_stream().cuda_stream)
+    assert st == _lib.ERR_WORKSPACE
+
+
+def test_w8a16_empty(ops):
+    q = torch.zeros(8, 64, dtype=torch.int8, device="cuda")
+    s = torch.ones(8, dtype=torch.bfloat16, device="cuda")
+    y = ops.w8a16_gemm(torch.zeros(0, 64, dtype=torch.bfloat16, device="cuda"), q, s)
+    assert y.shape == (0, 8)
+    # K = 0: the sum is empty, the output is the bias (0 without one), as in the reference kernel
+    q0 = torch.zeros(8, 0, dtype=torch.int8, device="cuda")
+    b = torch.arange(8, dtype=torch.bfloat16, device="cuda")
+    y0 = ops.w8a16_gemm(torch.zeros(3, 0, dtype=torch.bfloat16, device="cuda"), q0, s, b)
+    assert torch.equal(y0, b.expand(3, 8))
+
+
+# ---- fp8 W8A8 -----------------------------------------------------------------------------
+
+def _oracle_w8a8(qx, sx, qw, sw, bias, out_dtype):
+    y = O.w8a8_ref(qx.view(torch.uint8).cpu().numpy(), sx.cpu().numpy(), qw.view(torch.uint8).cpu().numpy(),
+                   sw.cpu().numpy())
+    yt = torch.from_numpy(y).to(out_dtype)           # the product is rounded to out_dtype first
+    if bias is not None:
+        yt = yt + bias.cpu().to(out_dtype)            # then the bias is added in out_dtype
+    return yt.double().numpy()
+
+
+def _fp8_inputs(m, n, k, seed, outliers=True):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = torch.randn(m, k, device="cuda", generator=g)
+    if outliers:
+        mask = torch.rand(m, k, device="cuda", generator=g) < 0.01
+        x = torch.where(mask, torch.sign(x) * 20.0, x)
+    w = torch.randn(n, k, device="cuda", generator=g) * 0.02
+    return x.to(torch.bfloat16), w.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("n,k", TALKER)
+def test_fp8_gemm_vs_oracle(ops, n, k):
+    for m in (1, 8, 16, 17, 64):
+        x, w = _fp8_inputs(m, n, k, seed=n + m)
+        qw, sw = ops.pack_fp8(w)
+        qx, sx = ops.quant_act_fp8(x)
+        y = ops.w8a8_fp8_gemm(qx, sx, qw, sw, None, torch.bfloat16)
+        assert_close(y, _oracle_w8a8(qx, sx, qw, sw, None, torch.bfloat16), f"fp8 m={m} n={n} k={k}")
+
+
+def test_fp8_gemm_m256_vs_fp32(ops):
+    for n, k in TALKER:
+        x, w = _fp8_inputs(256, n, k, seed=n)
+        qw, sw = ops.pack_fp8(w)
+        qx, sx = ops.quant_act_fp8(x)
+        y = ops.w8a8_fp8_gemm(qx, sx, qw, sw, None, torch.bfloat16)
+        a = qx.float() * sx[:, None]
+        bm = qw.float() * sw[:, None]
+        ref = (a @ bm.t()).double().cpu().numpy()
+        assert_close(y, ref, f"fp8 m=256 n={n} k={k}")
+
+
+def test_fp8_small_and_odd(ops):
+    for m, n, k in ((1, 1, 32), (3, 17, 64), (2, 33, 130), (5, 16, 96), (20, 40, 256)):
+        x, w = _fp8_inputs(m, n, k, seed=m * n + k, outliers=False)
+        b = torch.randn(n, device="cuda").to(torch.bfloat16)
+        qw, sw = ops.pack_fp8(w)
+        y = ops.fp8_linear(x, qw, sw, b)
+        qx, sx = ops.quant_act_fp8(x)
+        assert_close(y, _oracle_w8a8(qx, sx, qw, sw, b, torch.bfloat16), f"fp8 m={m} n={n} k={k}")

@@ -1,0 +1,199 @@
+"""Pins the CPU oracle (oracle/) before anything is checked against it.
+
+Each check is chosen so that a plausible mistake in the oracle fails it:
+golden fixtures from torch evaluating the reference's expressions
+(tests/golden/make_golden.py), closed-form rows, an exhaustive e4m3 sweep
+against torch's float8_e4m3fn cast, and invariants of the fp64 GEMM.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from oracle import cpu_path
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def _load(name):
+    return np.load(os.path.join(GOLDEN, name + ".npz"))
+
+
+def _cases(z):
+    return sorted({k.rsplit(".", 1)[0] for k in z.files if k.endswith(".src")})
+
+
+MODES = {"ieee": O.DIV_IEEE, "device": O.DIV_DEVICE}
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_int8_pack_matches_golden(mode):
+    z = _load("int8_pack")
+    for case in _cases(z):
+        src = z[f"{case}.src"]
+        dt = O.DT_F32 if case.endswith(".f32") else O.DT_BF16
+        q, s32, sb = O.pack_int8(src, dt, O.DT_BF16, MODES[mode])
+        np.testing.assert_array_equal(q, z[f"{case}.{mode}.q"], err_msg=case)
+        np.testing.assert_array_equal(s32.view(np.uint32), z[f"{case}.{mode}.scale"].view(np.uint32), err_msg=case)
+        np.testing.assert_array_equal(sb, z[f"{case}.{mode}.scale_bf16"], err_msg=case)
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_fp8_pack_matches_golden(mode):
+    z = _load("fp8_pack")
+    for case in _cases(z):
+        src = z[f"{case}.src"]
+        dt = O.DT_F32 if case.endswith(".f32") else O.DT_BF16
+        q, s = O.pack_fp8(src, dt, MODES[mode])
+        np.testing.assert_array_equal(q, z[f"{case}.{mode}.q"], err_msg=case)
+        np.testing.assert_array_equal(s.view(np.uint32), z[f"{case}.{mode}.scale"].view(np.uint32), err_msg=case)
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_act_fp8_matches_golden(mode):
+    z = _load("act_fp8")
+    for case in sorted({k.split(".")[0] for k in z.files}):
+        qx, sx = O.quant_act_fp8(z[f"{case}.x"], O.DT_BF16, MODES[mode])
+        np.testing.assert_array_equal(qx, z[f"{case}.{mode}.q"], err_msg=case)
+        np.testing.assert_array_equal(sx.view(np.uint32), z[f"{case}.{mode}.scale"].view(np.uint32), err_msg=case)
+
+
+def test_int8_closed_forms():
+    k = 64
+    w = np.zeros((5, k), np.float32)
+    w[1, :9] = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5, -126.5]
+    w[2, 3] = -2.0
+    w[3, :] = 0.25
+    w[4, 0], w[4, 1] = 1.0, -1.0
+    q, s, sb = O.pack_int8(w, O.DT_F32, O.DT_F32, O.DIV_IEEE)
+    # all-zero row: amax clamps to 1e-12, q = 0
+    assert s[0] == np.float32(np.float32(1e-12) / np.float32(127.0))
+    assert not q[0].any()
+    # amax 127 -> scale exactly 1 -> round half to even
+    assert s[1] == 1.0
+    assert list(q[1, :9]) == [127, 0, 2, 2, 0, -2, -2, 126, -126]
+    # the absmax element always maps to +/-127, never -128
+    assert q[2, 3] == -127 and (q[3] == 127).all()
+    assert q[4, 0] == 127 and q[4, 1] == -127
+    assert q.min() >= -127
+
+
+def test_device_scale_is_reciprocal_multiply():
+    rng = np.random.default_rng(3)
+    w = rng.normal(0, 0.02, (4096, 32)).astype(np.float32)
+    _, s_dev, _ = O.pack_int8(w, O.DT_F32, O.DT_F32, O.DIV_DEVICE)
+    _, s_ieee, _ = O.pack_int8(w, O.DT_F32, O.DT_F32, O.DIV_IEEE)
+    amax = np.abs(w).max(axis=1)
+    np.testing.assert_array_equal(s_ieee, amax / np.float32(127.0))
+    np.testing.assert_array_equal(s_dev, amax * (np.float32(1.0) / np.float32(127.0)))
+    # The two semantics genuinely differ on some rows (else one mode is untested).
+    assert (s_dev != s_ieee).any()
+
+
+def _all_bf16_values() -> np.ndarray:
+    return O.bf16_bits_to_f32(np.arange(65536, dtype=np.uint32).astype(np.uint16))
+
+
+def test_e4m3_encode_exhaustive_bf16_vs_torch():
+    v = _all_bf16_values()
+    ours = O.e4m3_encode(v)
+    theirs = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(ours, theirs)
+
+
+def test_e4m3_encode_fp32_samples_vs_torch():
+    rng = np.random.default_rng(11)
+    v = np.concatenate([
+        rng.normal(0, 100, 20000), rng.normal(0, 1e-2, 20000),
+        rng.uniform(-470, 470, 20000), rng.normal(0, 1e-3, 5000),
+    ]).astype(np.float32)
+    # exact ties between neighbouring e4m3 values (normal and subnormal)
+    tab = O.e4m3_decode_table()
+    fin = np.sort(tab[np.isfinite(tab)])
+    mids = ((fin[1:].astype(np.float64) + fin[:-1]) / 2).astype(np.float32)
+    v = np.concatenate([v, mids, -mids, np.float32([464.0, 463.99997, 480.0, -464.0, np.inf, -np.inf, np.nan])])
+    ours = O.e4m3_encode(v)
+    theirs = torch.from_numpy(v).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    np.testing.assert_array_equal(ours, theirs)
+
+
+def test_e4m3_decode_table():
+    tab = O.e4m3_decode_table()
+    codes = torch.arange(256, dtype=torch.int32).to(torch.uint8).view(torch.float8_e4m3fn).float().numpy()
+    np.testing.assert_array_equal(np.isnan(tab), np.isnan(codes))
+    fin = ~np.isnan(tab)
+    np.testing.assert_array_equal(tab[fin], codes[fin])
+    # OCP E4M3 landmarks
+    assert tab[0x7E] == 448.0 and tab[0x01] == 2.0 ** -9 and tab[0x08] == 2.0 ** -6
+    assert tab[0x38] == 1.0 and tab[0xB8] == -1.0
+    assert np.isnan(tab[0x7F]) and np.isnan(tab[0xFF]) and np.isnan(tab).sum() == 2
+
+
+def test_gemm_oracle_matches_fp64_golden():
+    z = _load("gemm_small")
+    for case in sorted({k.split(".")[0] for k in z.files}):
+        x = O.bf16_bits_to_f32(z[f"{case}.x"])
+        s = O.bf16_bits_to_f32(z[f"{case}.scale_bf16"])
+        b = O.bf16_bits_to_f32(z[f"{case}.bias"]) if f"{case}.bias" in z.files else None
+        y = O.w8a16_ref(x, z[f"{case}.q"], s, b)
+        np.testing.assert_allclose(y, z[f"{case}.y_f64"], rtol=1e-12, atol=1e-12, err_msg=case)
+
+
+def test_gemm_oracle_invariants():
+    rng = np.random.default_rng(5)
+    m, n, k = 3, 7, 50
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    s = rng.uniform(0.001, 0.01, n).astype(np.float32)
+    b = rng.normal(0, 1, n).astype(np.float32)
+    y = O.w8a16_ref(x, q, s, b)
+    np.testing.assert_allclose(y, x.astype(np.float64) @ (q.astype(np.float64) * s[:, None].astype(np.float64)).T + b,
+                               rtol=1e-12, atol=1e-12)
+    # linearity in x, and one-hot x selects a scaled weight column (catches a transposed operand)
+    x2 = rng.normal(0, 1, (m, k)).astype(np.float32)
+    np.testing.assert_allclose(O.w8a16_ref(x + x2, q, s), O.w8a16_ref(x, q, s) + O.w8a16_ref(x2, q, s), rtol=1e-5, atol=1e-5)
+    e = np.zeros((1, k), np.float32); e[0, 9] = 1.0
+    np.testing.assert_allclose(O.w8a16_ref(e, q, s)[0], q[:, 9] * s.astype(np.float64))
+
+
+def test_w8a8_oracle_invariants():
+    rng = np.random.default_rng(6)
+    x = rng.normal(0, 1, (4, 96)).astype(np.float32)
+    w = rng.normal(0, 0.02, (9, 96)).astype(np.float32)
+    qx, sx = O.quant_act_fp8(O.f32_to_bf16_bits(x), O.DT_BF16)
+    qw, sw = O.pack_fp8(w)
+    y = O.w8a8_ref(qx, sx, qw, sw)
+    tab = O.e4m3_decode_table().astype(np.float64)
+    ref = (tab[qx] * sx[:, None]) @ (tab[qw] * sw[:, None]).T
+    np.testing.assert_allclose(y, ref, rtol=1e-12)
+    # quantization error of W8A8 against the unquantized product stays within a few %
+    exact = O.bf16_bits_to_f32(O.f32_to_bf16_bits(x)).astype(np.float64) @ w.T.astype(np.float64)
+    assert O.rel_err(y, exact) < 0.15
+
+
+def test_naive_cpu_path_matches_golden():
+    z = _load("gemm_small")
+    for case in sorted({k.split(".")[0] for k in z.files}):
+        x = torch.from_numpy(z[f"{case}.x"].view(np.int16)).view(torch.bfloat16)
+        s = torch.from_numpy(z[f"{case}.scale_bf16"].view(np.int16)).view(torch.bfloat16)
+        b = (torch.from_numpy(z[f"{case}.bias"].view(np.int16)).view(torch.bfloat16)
+             if f"{case}.bias" in z.files else None)
+        y = cpu_path.naive_dequant_linear(x, torch.from_numpy(z[f"{case}.q"]), s, b).float().numpy()
+        exp = O.bf16_bits_to_f32(z[f"{case}.y_naive_bf16"])
+        # bf16 GEMM accumulation order is library-dependent: allow one bf16 step.
+        np.testing.assert_allclose(y, exp, rtol=2 ** -7, atol=1e-6, err_msg=case)
+        # The reference's formula rounds the dequantized weight and the output to
+        # bf16, so it sits near (and on a 3-sigma output, just past) the 1e-2 bar.
+        assert O.rel_err(y, z[f"{case}.y_f64"]) < 2e-2
+
+
+def test_bf16_rounding_helpers():
+    v = np.float32([1.0, 1.00390625, 1.005859375, -3.0e-39, 65504.0, np.inf])
+    ours = O.f32_to_bf16_bits(v)
+    theirs = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    np.testing.assert_array_equal(ours, theirs)

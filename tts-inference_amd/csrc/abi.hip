@@ -1,0 +1,215 @@
+// C ABI entry points (include/qtts_amd.h): argument checks, device gating, error
+// strings and dispatch to the kernel launchers in pack.hip, w8a16.hip and fp8.hip.
+#include <hip/hip_runtime.h>
+
+#include <atomic>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "qtts_amd.h"
+
+// Launchers implemented next to their kernels.
+int qtts_launch_pack_int8(const void* src, int src_dtype, int64_t n, int64_t k, int64_t ld, int8_t* q,
+                          void* scale_out, int scale_dtype, float* scale_f32, int div_mode, hipStream_t st);
+int qtts_launch_pack_fp8(const void* src, int src_dtype, int64_t n, int64_t k, int64_t ld, uint8_t* q, float* scale,
+                         int div_mode, hipStream_t st);
+int qtts_launch_quant_act_fp8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld, uint8_t* qx, float* sx,
+                              int div_mode, hipStream_t st);
+int qtts_launch_w8a16(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* q, int64_t n,
+                      int64_t ldq, const void* scale, int scale_dtype, const void* bias, void* y, int64_t ldy,
+                      int algo, void* ws, int64_t ws_bytes, hipStream_t st);
+int64_t qtts_w8a16_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
+int qtts_launch_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const uint8_t* qw,
+                         int64_t n, int64_t ldqw, const float* sw, const void* bias, void* y, int out_dtype,
+                         int64_t ldy, int algo, void* ws, int64_t ws_bytes, hipStream_t st);
+int64_t qtts_fp8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
+
+static thread_local char g_last_error[512] = "";
+
+int qtts_set_error(int status, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return status;
+}
+
+int qtts_check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return qtts_set_error(QTTS_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return QTTS_OK;
+}
+
+// ---- device gating: gfx950 only ---------------------------------------------------------
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<int> g_dev_state[kMaxDevices];  // 0 unknown, 1 supported, 2 unsupported
+
+bool dtype_ok(int d) { return d == QTTS_F32 || d == QTTS_BF16 || d == QTTS_F16; }
+bool div_ok(int d) { return d == QTTS_DIV_DEVICE || d == QTTS_DIV_IEEE; }
+bool algo_ok(int a) {
+  const int f = a & 0xff;
+  return f == QTTS_ALGO_AUTO || f == QTTS_ALGO_SKINNY || f == QTTS_ALGO_TILE;
+}
+int64_t al256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+int current_device_check() {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return qtts_set_error(QTTS_ERR_UNSUPPORTED, "no HIP device: %s", hipGetErrorString(e));
+  if (qtts_device_supported(dev) != 1)
+    return qtts_set_error(QTTS_ERR_UNSUPPORTED, "device %d is not a gfx950 (MI355X-class) GPU", dev);
+  return QTTS_OK;
+}
+
+#define QTTS_REQUIRE(cond, ...) \
+  do {                          \
+    if (!(cond)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, __VA_ARGS__); \
+  } while (0)
+
+#define QTTS_TRY(expr)               \
+  do {                               \
+    int _s = (expr);                 \
+    if (_s != QTTS_OK) return _s;    \
+  } while (0)
+
+}  // namespace
+
+extern "C" {
+
+int qtts_abi_version(void) { return QTTS_ABI_VERSION; }
+
+const char* qtts_last_error(void) { return g_last_error; }
+
+int qtts_device_supported(int device) {
+  if (device < 0 || device >= kMaxDevices) return 0;
+  int s = g_dev_state[device].load(std::memory_order_acquire);
+  if (s == 0) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+      (void)hipGetLastError();
+      return 0;
+    }
+    s = (std::strncmp(prop.gcnArchName, "gfx950", 6) == 0) ? 1 : 2;
+    g_dev_state[device].store(s, std::memory_order_release);
+  }
+  return s == 1 ? 1 : 0;
+}
+
+int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo) {
+  if (m < 0 || n < 0 || k < 0 || !algo_ok(algo)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "bad workspace query");
+  if (m == 0 || n == 0) return 0;
+  switch (op) {
+    case QTTS_OP_W8A16: return qtts_w8a16_ws_bytes(m, n, k, algo);
+    case QTTS_OP_W8A8_FP8: return qtts_fp8_gemm_ws_bytes(m, n, k, algo);
+    case QTTS_OP_FP8_LINEAR: return al256(qtts_fp8_gemm_ws_bytes(m, n, k, algo)) + al256(m * k) + al256(m * 4);
+    default: return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "unknown op %d", op);
+  }
+}
+
+int qtts_pack_int8_rowwise(const void* src, int src_dtype, int64_t n, int64_t k, int64_t ld_src, int8_t* q_out,
+                           void* scale_out, int scale_dtype, float* scale_f32_out, int div_mode, void* stream) {
+  QTTS_REQUIRE(n >= 0 && k >= 0, "pack_int8_rowwise: negative size (n=%lld, k=%lld)", (long long)n, (long long)k);
+  QTTS_REQUIRE(dtype_ok(src_dtype) && dtype_ok(scale_dtype), "pack_int8_rowwise: bad dtype code");
+  QTTS_REQUIRE(div_ok(div_mode), "pack_int8_rowwise: bad div_mode %d", div_mode);
+  QTTS_REQUIRE(ld_src >= k, "pack_int8_rowwise: ld_src %lld < k %lld", (long long)ld_src, (long long)k);
+  QTTS_REQUIRE(n < (1ll << 31), "pack_int8_rowwise: n too large");
+  if (n == 0) return QTTS_OK;
+  QTTS_REQUIRE(scale_out && (k == 0 || (src && q_out)), "pack_int8_rowwise: null pointer");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_pack_int8(src, src_dtype, n, k, ld_src, q_out, scale_out, scale_dtype, scale_f32_out, div_mode,
+                               (hipStream_t)stream);
+}
+
+int qtts_pack_fp8_e4m3_rowwise(const void* src, int src_dtype, int64_t n, int64_t k, int64_t ld_src,
+                               uint8_t* q_out, float* scale_out, int div_mode, void* stream) {
+  QTTS_REQUIRE(n >= 0 && k >= 0, "pack_fp8_e4m3_rowwise: negative size");
+  QTTS_REQUIRE(dtype_ok(src_dtype), "pack_fp8_e4m3_rowwise: bad dtype code");
+  QTTS_REQUIRE(div_ok(div_mode), "pack_fp8_e4m3_rowwise: bad div_mode %d", div_mode);
+  QTTS_REQUIRE(ld_src >= k, "pack_fp8_e4m3_rowwise: ld_src < k");
+  QTTS_REQUIRE(n < (1ll << 31), "pack_fp8_e4m3_rowwise: n too large");
+  if (n == 0) return QTTS_OK;
+  QTTS_REQUIRE(scale_out && (k == 0 || (src && q_out)), "pack_fp8_e4m3_rowwise: null pointer");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_pack_fp8(src, src_dtype, n, k, ld_src, q_out, scale_out, div_mode, (hipStream_t)stream);
+}
+
+int qtts_w8a16_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* q, int64_t n,
+                    int64_t ldq, const void* scale, int scale_dtype, const void* bias, void* y, int64_t ldy, int algo,
+                    void* ws, int64_t ws_bytes, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a16_gemm: negative size (m=%lld, n=%lld, k=%lld)", (long long)m,
+               (long long)n, (long long)k);
+  QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "w8a16_gemm: size too large");
+  QTTS_REQUIRE(dtype_ok(x_dtype) && dtype_ok(scale_dtype), "w8a16_gemm: bad dtype code");
+  QTTS_REQUIRE(algo_ok(algo), "w8a16_gemm: bad algo %d", algo);
+  QTTS_REQUIRE(ldx >= k && ldq >= k && ldy >= n, "w8a16_gemm: leading dimension smaller than the row");
+  QTTS_REQUIRE(ws_bytes >= 0, "w8a16_gemm: negative workspace size");
+  if (m == 0 || n == 0) return QTTS_OK;
+  QTTS_REQUIRE(scale && y && (k == 0 || (x && q)), "w8a16_gemm: null pointer");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_w8a16(x, x_dtype, m, k, ldx, q, n, ldq, scale, scale_dtype, bias, y, ldy, algo, ws, ws_bytes,
+                           (hipStream_t)stream);
+}
+
+int qtts_quant_act_fp8_rows(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, uint8_t* qx, float* sx,
+                            int div_mode, void* stream) {
+  QTTS_REQUIRE(m >= 0 && k >= 0, "quant_act_fp8_rows: negative size");
+  QTTS_REQUIRE(m < (1ll << 31), "quant_act_fp8_rows: m too large");
+  QTTS_REQUIRE(dtype_ok(x_dtype), "quant_act_fp8_rows: bad dtype code");
+  QTTS_REQUIRE(div_ok(div_mode), "quant_act_fp8_rows: bad div_mode %d", div_mode);
+  QTTS_REQUIRE(ldx >= k, "quant_act_fp8_rows: ldx < k");
+  if (m == 0) return QTTS_OK;
+  QTTS_REQUIRE(sx && (k == 0 || (x && qx)), "quant_act_fp8_rows: null pointer");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_quant_act_fp8(x, x_dtype, m, k, ldx, qx, sx, div_mode, (hipStream_t)stream);
+}
+
+int qtts_w8a8_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const uint8_t* qw,
+                       int64_t n, int64_t ldqw, const float* sw, const void* bias, void* y, int out_dtype,
+                       int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a8_fp8_gemm: negative size");
+  QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "w8a8_fp8_gemm: size too large");
+  QTTS_REQUIRE(dtype_ok(out_dtype), "w8a8_fp8_gemm: bad dtype code");
+  QTTS_REQUIRE(algo_ok(algo), "w8a8_fp8_gemm: bad algo %d", algo);
+  QTTS_REQUIRE(ldqx >= k && ldqw >= k && ldy >= n, "w8a8_fp8_gemm: leading dimension smaller than the row");
+  QTTS_REQUIRE(ws_bytes >= 0, "w8a8_fp8_gemm: negative workspace size");
+  if (m == 0 || n == 0) return QTTS_OK;
+  QTTS_REQUIRE(sx && sw && y && (k == 0 || (qx && qw)), "w8a8_fp8_gemm: null pointer");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_fp8_gemm(qx, sx, m, k, ldqx, qw, n, ldqw, sw, bias, y, out_dtype, ldy, algo, ws, ws_bytes,
+                              (hipStream_t)stream);
+}
+
+int qtts_fp8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qw, int64_t n,
+                    int64_t ldqw, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode, int algo,
+                    void* ws, int64_t ws_bytes, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "fp8_linear: negative size");
+  QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "fp8_linear: size too large");
+  QTTS_REQUIRE(dtype_ok(x_dtype), "fp8_linear: bad dtype code");
+  QTTS_REQUIRE(div_ok(div_mode), "fp8_linear: bad div_mode %d", div_mode);
+  QTTS_REQUIRE(algo_ok(algo), "fp8_linear: bad algo %d", algo);
+  QTTS_REQUIRE(ldx >= k && ldqw >= k && ldy >= n, "fp8_linear: leading dimension smaller than the row");
+  if (m == 0 || n == 0) return QTTS_OK;
+  QTTS_REQUIRE(sw && y && (k == 0 || (x && qw)), "fp8_linear: null pointer");
+  // Layout: the GEMM's own workspace (split-K counters first) from the start, the
+  // quantized activations and their scales at the end.
+  const int64_t qx_bytes = al256(m * k), sx_bytes = al256(m * 4);
+  const int64_t gemm_ws = qtts_fp8_gemm_ws_bytes(m, n, k, algo);
+  QTTS_REQUIRE(ws != nullptr, "fp8_linear: a workspace of %lld bytes is required",
+               (long long)(qx_bytes + sx_bytes + gemm_ws));
+  const int64_t tail = (ws_bytes - qx_bytes - sx_bytes) & ~(int64_t)255;
+  if (tail < 0)
+    return qtts_set_error(QTTS_ERR_WORKSPACE, "fp8_linear: workspace of %lld bytes < %lld needed", (long long)ws_bytes,
+                          (long long)(qx_bytes + sx_bytes + gemm_ws));
+  QTTS_TRY(current_device_check());
+  uint8_t* qx = (uint8_t*)ws + tail;
+  float* sx = (float*)((char*)ws + tail + qx_bytes);
+  QTTS_TRY(qtts_launch_quant_act_fp8(x, x_dtype, m, k, ldx, qx, sx, div_mode, (hipStream_t)stream));
+  return qtts_launch_fp8_gemm(qx, sx, m, k, k, qw, n, ldqw, sw, bias, y, x_dtype, ldy, algo, tail > 0 ? ws : nullptr,
+                              tail, (hipStream_t)stream);
+}
+
+}  // extern "C"

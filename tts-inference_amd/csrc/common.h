@@ -1,0 +1,160 @@
+// Shared device helpers for the gfx950 quantized-linear kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "qtts_amd.h"
+
+typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8_t;
+typedef __attribute__((ext_vector_type(4))) float f32x4_t;
+typedef __attribute__((ext_vector_type(8))) int i32x8_t;
+typedef __attribute__((ext_vector_type(4))) int i32x4_t;
+
+namespace qtts {
+
+// Workspace layout shared by every op: a fixed block of split-K counters first
+// (one 32-bit counter per output tile, reset to zero by the workgroup that
+// consumes it), then op-specific scratch.  The counter block does not depend on
+// the shape, so one call's scratch can never overlap another call's counters.
+constexpr int64_t kCounterBytes = 65536;
+constexpr int64_t kMaxSplitTiles = kCounterBytes / 4;
+
+__host__ __device__ constexpr int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+// Reset a split-K counter: an agent-scope atomic store (written through to the
+// coherence point), so the next kernel's atomics see zero from any XCD.
+__device__ __forceinline__ void reset_counter(unsigned* c) {
+  __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---- scalar element access by dtype code ------------------------------------------
+
+struct bf16_t { uint16_t bits; };
+struct f16_t { uint16_t bits; };
+
+__device__ __forceinline__ float to_f32(float v) { return v; }
+__device__ __forceinline__ float to_f32(bf16_t v) { return __uint_as_float((uint32_t)v.bits << 16); }
+__device__ __forceinline__ float to_f32(f16_t v) {
+  _Float16 h;
+  __builtin_memcpy(&h, &v.bits, 2);
+  return (float)h;
+}
+
+// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+template <typename T> __device__ __forceinline__ T from_f32(float v);
+template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) { return bf16_t{f32_to_bf16_bits(v)}; }
+template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float v) {
+  _Float16 h = (_Float16)v;  // round to nearest even
+  f16_t r;
+  __builtin_memcpy(&r.bits, &h, 2);
+  return r;
+}
+
+// Round to T and widen back (identity for fp32).
+template <typename T> __device__ __forceinline__ float round_through(float v) { return to_f32(from_f32<T>(v)); }
+
+// ---- int8 -> 16-bit float vectors for the MFMA operands ---------------------------
+// Every int8 value is exact in bf16 and fp16.  Each byte goes through one
+// v_cvt_f32_i32 with an SDWA sign-extended byte select, then pairs are packed.
+
+__device__ __forceinline__ bf16x8_t i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+  bf16x8_t r;
+  r[0] = (__bf16)(float)(int8_t)(lo);
+  r[1] = (__bf16)(float)(int8_t)(lo >> 8);
+  r[2] = (__bf16)(float)(int8_t)(lo >> 16);
+  r[3] = (__bf16)(float)(int8_t)(lo >> 24);
+  r[4] = (__bf16)(float)(int8_t)(hi);
+  r[5] = (__bf16)(float)(int8_t)(hi >> 8);
+  r[6] = (__bf16)(float)(int8_t)(hi >> 16);
+  r[7] = (__bf16)(float)(int8_t)(hi >> 24);
+  return r;
+}
+
+__device__ __forceinline__ f16x8_t i8x8_to_f16x8(uint32_t lo, uint32_t hi) {
+  f16x8_t r;
+  r[0] = (_Float16)(float)(int8_t)(lo);
+  r[1] = (_Float16)(float)(int8_t)(lo >> 8);
+  r[2] = (_Float16)(float)(int8_t)(lo >> 16);
+  r[3] = (_Float16)(float)(int8_t)(lo >> 24);
+  r[4] = (_Float16)(float)(int8_t)(hi);
+  r[5] = (_Float16)(float)(int8_t)(hi >> 8);
+  r[6] = (_Float16)(float)(int8_t)(hi >> 16);
+  r[7] = (_Float16)(float)(int8_t)(hi >> 24);
+  return r;
+}
+
+// 16-bit activation element types mapped to their MFMA operand vector.
+template <typename XT> struct mfma16;
+template <> struct mfma16<bf16_t> {
+  typedef bf16x8_t vec;
+  static __device__ __forceinline__ vec from_i8(uint32_t lo, uint32_t hi) { return i8x8_to_bf16x8(lo, hi); }
+  static __device__ __forceinline__ f32x4_t mma(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct mfma16<f16_t> {
+  typedef f16x8_t vec;
+  static __device__ __forceinline__ vec from_i8(uint32_t lo, uint32_t hi) { return i8x8_to_f16x8(lo, hi); }
+  static __device__ __forceinline__ f32x4_t mma(vec a, vec b, f32x4_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// fp8 x fp8 (OCP e4m3 on gfx950) 16x16x128 MFMA, unit block scales (E8M0 127 = 2^0).
+__device__ __forceinline__ f32x4_t mma_fp8_16x16x128(i32x8_t a, i32x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
+}
+
+// ---- OCP e4m3fn encode (round to nearest even, non-saturating like torch's cast) ---
+
+__device__ __forceinline__ uint32_t e4m3_encode(float f) {
+  uint32_t u = __float_as_uint(f), s = (u >> 24) & 0x80u, a = u & 0x7fffffffu;
+  if (a >= 0x7f800000u) return s | 0x7fu;
+  if (a < 0x3c800000u) {  // below 2^-6: subnormal grid of 2^-9
+    float v = __uint_as_float(a) * 512.0f;
+    return s | (uint32_t)__builtin_rintf(v);
+  }
+  int32_t e = (int32_t)(a >> 23) - 120;
+  uint32_t mant = (a & 0x7fffffu) | 0x800000u;
+  uint32_t r = mant >> 20, rem = mant & 0xfffffu;
+  r += (rem > 0x80000u || (rem == 0x80000u && (r & 1u))) ? 1u : 0u;
+  if (r == 16u) { r = 8u; e++; }
+  uint32_t code = ((uint32_t)e << 3) | (r & 7u);
+  return s | ((e > 15 || code >= 0x7fu) ? 0x7fu : code);
+}
+
+// `num / c` with the reference's scalar-division semantics (qtts_div_mode).
+__device__ __forceinline__ float scalar_div(float num, float c, int div_mode) {
+  return div_mode == QTTS_DIV_DEVICE ? num * (1.0f / c) : num / c;
+}
+
+// ---- wave64 reductions ----------------------------------------------------------------
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace qtts
+
+// ---- host-side error plumbing (abi.hip) -------------------------------------------------
+
+int qtts_set_error(int status, const char* fmt, ...);
+int qtts_check_launch(const char* what);

@@ -1,0 +1,414 @@
+// fp8 (OCP e4m3) W8A8 GEMM for gfx950: y = ((qx*sx) @ (qw*sw)^T) [+ bias].
+//
+// Replaces torch._scaled_mm with rowwise scales and the bias add after it
+// (qtts/quant/fp8.py:79-89).  Both operands are already e4m3, so the weight bytes go
+// straight from HBM into v_mfma_scale_f32_16x16x128_f8f6f4 (unit block scales)
+// with no conversion at all:
+//
+//  * skinny (M <= 16): a wave owns a 16-row strip of qw; per 128-byte chunk of K a
+//    lane loads 32 weight bytes (two 128-bit loads) and the matching 32 activation
+//    bytes, and issues one MFMA.  Waves split K and meet in LDS; workgroups may
+//    split K further and meet through the workspace (last arrival reduces).
+//  * tile (M > 16): LDS-tiled, BM x 128 x 128, 4 waves in 2x2, double-buffered.
+//  * generic: any alignment / K; correctness path.
+//
+// Epilogue order follows the reference: the fp32 accumulator is scaled by
+// sx[m] * sw[n] and rounded to the output dtype, then the bias is added in the
+// output dtype (fp8.py:79-89 add the bias after _scaled_mm returns).
+#include <algorithm>
+
+#include "common.h"
+
+namespace qtts {
+
+__device__ __forceinline__ void fp8_decode_wg(int wg, int S, int& strip, int& split) {
+  const int group = wg / (8 * S), within = wg - group * 8 * S;
+  split = within >> 3;
+  strip = group * 8 + (within & 7);
+}
+
+template <typename OT>
+__device__ __forceinline__ void fp8_store(OT* __restrict__ y, int64_t ldy, int m, int n, float acc,
+                                          const float* __restrict__ sx, const float* __restrict__ sw,
+                                          const OT* __restrict__ bias) {
+  float v = round_through<OT>(acc * sx[m] * sw[n]);
+  if (bias) v += to_f32(bias[n]);
+  y[(int64_t)m * ldy + n] = from_f32<OT>(v);
+}
+
+// e4m3 decode for the generic path (OCP E4M3: bias 7, subnormal step 2^-9).
+__device__ __forceinline__ float e4m3_decode(uint32_t c) {
+  const uint32_t e = (c >> 3) & 15u, mnt = c & 7u;
+  float v;
+  if (e == 15u && mnt == 7u) v = __builtin_nanf("");
+  else if (e == 0u) v = (float)mnt * (1.0f / 512.0f);
+  else v = __uint_as_float(((e + 120u) << 23) | (mnt << 20));
+  return (c & 0x80u) ? -v : v;
+}
+
+// ------------------------------------------------------------------------------------
+
+template <typename OT, int WAVES, int U>
+__global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
+    const uint8_t* __restrict__ qx, const float* __restrict__ sx, int M, int K, int64_t ldqx,
+    const uint8_t* __restrict__ qw, int N, int64_t ldqw, const float* __restrict__ sw, const OT* __restrict__ bias,
+    OT* __restrict__ y, int64_t ldy, float* __restrict__ part, unsigned* __restrict__ counters, int strips, int S,
+    int cps) {
+  __shared__ f32x4_t red[WAVES > 1 ? WAVES - 1 : 1][64];
+  int strip, split;
+  fp8_decode_wg(blockIdx.x, S, strip, split);
+  if (strip >= strips) return;
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int r = lane & 15, g = lane >> 4;
+  const int n = strip * 16 + r;
+  const bool n_ok = n < N, m_ok = r < M;
+  const int nchunks = (K + 127) >> 7;
+  const int c0 = split * cps, c1 = min(c0 + cps, nchunks);
+  const uint8_t* wp = qw + (int64_t)(n_ok ? n : 0) * ldqw + 32 * g;
+  const uint8_t* xp = qx + (int64_t)(m_ok ? r : 0) * ldqx + 32 * g;
+  const i32x4_t zero = {0, 0, 0, 0};
+
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = c0 + wave; c < c1; c += WAVES * U) {
+    i32x4_t w0[U], w1[U], x0[U], x1[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int cc = c + u * WAVES;
+      const bool ok = cc < c1 && cc * 128 + 32 * g < K;
+      w0[u] = (ok && n_ok) ? *(const i32x4_t*)(wp + (int64_t)cc * 128) : zero;
+      w1[u] = (ok && n_ok) ? *(const i32x4_t*)(wp + (int64_t)cc * 128 + 16) : zero;
+      x0[u] = (ok && m_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * 128) : zero;
+      x1[u] = (ok && m_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * 128 + 16) : zero;
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const i32x8_t a = {w0[u][0], w0[u][1], w0[u][2], w0[u][3], w1[u][0], w1[u][1], w1[u][2], w1[u][3]};
+      const i32x8_t b = {x0[u][0], x0[u][1], x0[u][2], x0[u][3], x1[u][0], x1[u][1], x1[u][2], x1[u][3]};
+      acc = mma_fp8_16x16x128(a, b, acc);
+    }
+  }
+
+  if (WAVES > 1) {
+    if (wave > 0) red[wave - 1][lane] = acc;
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < WAVES - 1; ++w) acc += red[w][lane];
+  }
+
+  if (S > 1) {
+    float* pstrip = part + (int64_t)strip * S * 64 * 4;
+    *(f32x4_t*)(pstrip + ((int64_t)split * 64 + lane) * 4) = acc;
+    __threadfence();
+    unsigned prev = 0;
+    if (lane == 0) prev = atomicAdd(&counters[strip], 1u);
+    prev = __shfl(prev, 0, 64);
+    if (prev != (unsigned)(S - 1)) return;
+    __threadfence();
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    for (int s = 0; s < S; ++s) {
+      const f32x4_t t = *(const f32x4_t*)(pstrip + ((int64_t)s * 64 + lane) * 4);
+      a0 += t[0];
+      a1 += t[1];
+      a2 += t[2];
+      a3 += t[3];
+    }
+    if (lane == 0) reset_counter(&counters[strip]);
+    acc = f32x4_t{a0, a1, a2, a3};
+  }
+
+  if (m_ok) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int nn = strip * 16 + 4 * g + i;
+      if (nn < N) fp8_store(y, ldy, r, nn, acc[i], sx, sw, bias);
+    }
+  }
+}
+
+// ------------------------------------------------------------------------------------
+
+constexpr int kF8BN = 128, kF8BK = 128, kF8LdsK = kF8BK + 16;  // bytes
+
+template <typename OT, int BM>
+__global__ __launch_bounds__(256) void fp8_tile_kernel(
+    const uint8_t* __restrict__ qx, const float* __restrict__ sx, int M, int K, int64_t ldqx,
+    const uint8_t* __restrict__ qw, int N, int64_t ldqw, const float* __restrict__ sw, const OT* __restrict__ bias,
+    OT* __restrict__ y, int64_t ldy, float* __restrict__ part, unsigned* __restrict__ counters, int mtiles,
+    int ntiles, int S, int cps) {
+  constexpr int BN = kF8BN, BK = kF8BK, LK = kF8LdsK;
+  constexpr int TM = BM / 32, TN = 4;
+  constexpr int XL = BM * 8 / 256;  // 16-byte x chunks per thread per stage
+  constexpr int WL = BN * 8 / 256;  // 16-byte w chunks per thread per stage
+  __shared__ __align__(16) uint8_t As[2][BM][LK];
+  __shared__ __align__(16) uint8_t Bs[2][BN][LK];
+  __shared__ unsigned flag;
+
+  int tile, split;
+  fp8_decode_wg(blockIdx.x, S, tile, split);
+  if (tile >= mtiles * ntiles) return;
+  const int mt = tile % mtiles, nt = tile / mtiles;
+  const int m0 = mt * BM, n0 = nt * BN;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int c16 = lane & 15, g = lane >> 4;
+  const int nchunks = (K + BK - 1) / BK;
+  const int k0c = split * cps, k1c = min(k0c + cps, nchunks);
+  const i32x4_t zero = {0, 0, 0, 0};
+
+  i32x4_t xr[XL], wr[WL];
+  auto load_stage = [&](int kc) {
+#pragma unroll
+    for (int l = 0; l < XL; ++l) {
+      const int id = tid + 256 * l, row = id >> 3, col = (id & 7) * 16;
+      const int m = m0 + row, k = kc * BK + col;
+      xr[l] = (m < M && k < K) ? *(const i32x4_t*)(qx + (int64_t)m * ldqx + k) : zero;
+    }
+#pragma unroll
+    for (int l = 0; l < WL; ++l) {
+      const int id = tid + 256 * l, row = id >> 3, col = (id & 7) * 16;
+      const int n = n0 + row, k = kc * BK + col;
+      wr[l] = (n < N && k < K) ? *(const i32x4_t*)(qw + (int64_t)n * ldqw + k) : zero;
+    }
+  };
+  auto store_stage = [&](int buf) {
+#pragma unroll
+    for (int l = 0; l < XL; ++l) {
+      const int id = tid + 256 * l;
+      *(i32x4_t*)&As[buf][id >> 3][(id & 7) * 16] = xr[l];
+    }
+#pragma unroll
+    for (int l = 0; l < WL; ++l) {
+      const int id = tid + 256 * l;
+      *(i32x4_t*)&Bs[buf][id >> 3][(id & 7) * 16] = wr[l];
+    }
+  };
+
+  f32x4_t acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if (k0c < k1c) {
+    load_stage(k0c);
+    store_stage(0);
+  }
+  __syncthreads();
+  for (int kc = k0c; kc < k1c; ++kc) {
+    const int buf = (kc - k0c) & 1;
+    if (kc + 1 < k1c) load_stage(kc + 1);
+    i32x8_t a[TM], b[TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const uint8_t* p = &As[buf][wm * (BM / 2) + i * 16 + c16][g * 32];
+      const i32x4_t lo = *(const i32x4_t*)p, hi = *(const i32x4_t*)(p + 16);
+      a[i] = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const uint8_t* p = &Bs[buf][wn * 64 + j * 16 + c16][g * 32];
+      const i32x4_t lo = *(const i32x4_t*)p, hi = *(const i32x4_t*)(p + 16);
+      b[j] = i32x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = mma_fp8_16x16x128(a[i], b[j], acc[i][j]);
+    if (kc + 1 < k1c) store_stage(buf ^ 1);
+    __syncthreads();
+  }
+
+  if (S > 1) {
+    constexpr int NV = TM * TN * 4;
+    float* ptile = part + (int64_t)tile * S * 256 * NV;
+    float* mine = ptile + ((int64_t)split * 256 + tid) * NV;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) *(f32x4_t*)(mine + (i * TN + j) * 4) = acc[i][j];
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) flag = atomicAdd(&counters[tile], 1u);
+    __syncthreads();
+    if (flag != (unsigned)(S - 1)) return;
+    __threadfence();
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int s = 0; s < S; ++s) {
+      const float* src = ptile + ((int64_t)s * 256 + tid) * NV;
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] += *(const f32x4_t*)(src + (i * TN + j) * 4);
+    }
+    if (tid == 0) reset_counter(&counters[tile]);
+  }
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j) {
+      const int n = n0 + wn * 64 + j * 16 + c16;
+      if (n >= N) continue;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int m = m0 + wm * (BM / 2) + i * 16 + 4 * g + t;
+        if (m < M) fp8_store(y, ldy, m, n, acc[i][j][t], sx, sw, bias);
+      }
+    }
+}
+
+// ------------------------------------------------------------------------------------
+
+template <typename OT>
+__global__ __launch_bounds__(64) void fp8_generic_kernel(
+    const uint8_t* __restrict__ qx, const float* __restrict__ sx, int M, int K, int64_t ldqx,
+    const uint8_t* __restrict__ qw, int N, int64_t ldqw, const float* __restrict__ sw, const OT* __restrict__ bias,
+    OT* __restrict__ y, int64_t ldy) {
+  const int n = blockIdx.x, m0 = blockIdx.y * 4, lane = threadIdx.x;
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int k = lane; k < K; k += 64) {
+    const float w = e4m3_decode(qw[(int64_t)n * ldqw + k]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (m0 + i < M) acc[i] += e4m3_decode(qx[(int64_t)(m0 + i) * ldqx + k]) * w;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float s = wave_sum(acc[i]);
+    if (lane == 0 && m0 + i < M) fp8_store(y, ldy, m0 + i, n, s, sx, sw, bias);
+  }
+}
+
+}  // namespace qtts
+
+using namespace qtts;
+
+namespace {
+
+struct F8Cfg { int family, waves, S, cps, strips, bm, mtiles, ntiles; };
+
+F8Cfg fp8_cfg(int64_t m, int64_t n, int64_t k, int algo) {
+  F8Cfg c{};
+  c.family = algo & 0xff;
+  const int splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff;
+  if (c.family == QTTS_ALGO_AUTO) c.family = m <= 16 ? QTTS_ALGO_SKINNY : QTTS_ALGO_TILE;
+  if (c.family == QTTS_ALGO_SKINNY) {
+    c.strips = (int)((n + 15) / 16);
+    const int nchunks = std::max(1, (int)((k + 127) / 128));
+    c.waves = waves > 0 ? waves : 4;
+    int S = splits;
+    if (S <= 0) {
+      S = 1;
+      while (c.strips * S * 2 <= 1024 && nchunks / (S * 2) >= 2 * c.waves) S *= 2;
+    }
+    S = std::max(1, std::min(S, nchunks));
+    if (c.strips > kMaxSplitTiles) S = 1;
+    c.cps = (nchunks + S - 1) / S;
+    c.S = (nchunks + c.cps - 1) / c.cps;
+  } else {
+    c.bm = m <= 32 ? 32 : (m <= 64 ? 64 : 128);
+    c.mtiles = (int)((m + c.bm - 1) / c.bm);
+    c.ntiles = (int)((n + kF8BN - 1) / kF8BN);
+    const int nchunks = std::max(1, (int)((k + kF8BK - 1) / kF8BK));
+    int S = splits;
+    if (S <= 0) {
+      S = 1;
+      while (c.mtiles * c.ntiles * S * 2 <= 512 && nchunks / (S * 2) >= 4) S *= 2;
+    }
+    S = std::max(1, std::min(S, nchunks));
+    if ((int64_t)c.mtiles * c.ntiles > kMaxSplitTiles) S = 1;
+    c.cps = (nchunks + S - 1) / S;
+    c.S = (nchunks + c.cps - 1) / c.cps;
+  }
+  return c;
+}
+
+int64_t fp8_cfg_ws(const F8Cfg& c) {
+  if (c.S <= 1) return 0;
+  if (c.family == QTTS_ALGO_SKINNY) return kCounterBytes + (int64_t)c.strips * c.S * 64 * 16;
+  const int64_t tiles = (int64_t)c.mtiles * c.ntiles;
+  return kCounterBytes + tiles * c.S * 256 * (c.bm / 32) * 4 * 4 * 4;
+}
+
+}  // namespace
+
+int64_t qtts_fp8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
+  if ((algo & 0xff) == QTTS_ALGO_AUTO) {
+    const int rest = algo & ~0xff;
+    int64_t a = fp8_cfg_ws(fp8_cfg(std::min<int64_t>(m, 16), n, k, rest | QTTS_ALGO_SKINNY));
+    if (m > 16) a = std::max(a, fp8_cfg_ws(fp8_cfg(m, n, k, rest | QTTS_ALGO_TILE)));
+    return a;
+  }
+  return fp8_cfg_ws(fp8_cfg(m, n, k, algo));
+}
+
+template <typename OT>
+static int fp8_launch_typed(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const uint8_t* qw,
+                            int64_t n, int64_t ldqw, const float* sw, const OT* bias, OT* y, int64_t ldy, int algo,
+                            void* ws, int64_t ws_bytes, hipStream_t st) {
+  const bool aligned = ((uintptr_t)qx % 16 == 0) && ((uintptr_t)qw % 16 == 0) && (ldqx % 16 == 0) &&
+                       (ldqw % 16 == 0) && (k % 32 == 0) && k > 0;
+  if (!aligned) {
+    dim3 grid((unsigned)n, (unsigned)((m + 3) / 4));
+    fp8_generic_kernel<OT><<<grid, 64, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy);
+    return qtts_check_launch("w8a8_fp8_generic");
+  }
+  F8Cfg c = fp8_cfg(m, n, k, algo);
+  if (c.family == QTTS_ALGO_SKINNY && m > 16)
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "skinny fp8 kernel handles M <= 16, got M=%lld", (long long)m);
+  int64_t need = fp8_cfg_ws(c);
+  if (need > ws_bytes || (need > 0 && !ws)) {
+    if ((algo >> 8) & 0xff)
+      return qtts_set_error(QTTS_ERR_WORKSPACE, "w8a8 fp8 GEMM needs %lld workspace bytes, got %lld", (long long)need,
+                            (long long)ws_bytes);
+    c = fp8_cfg(m, n, k, c.family | (1 << 8) | (algo & 0xff0000));
+    need = 0;
+  }
+  unsigned* counters = (unsigned*)ws;
+  if (c.family == QTTS_ALGO_SKINNY) {
+    float* part = c.S > 1 ? (float*)((char*)ws + kCounterBytes) : nullptr;
+    const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8 * c.S;
+#define QTTS_F8S(W, U)                                                                                            \
+  fp8_skinny_kernel<OT, W, U><<<(unsigned)blocks, W * 64, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, \
+                                                                   bias, y, ldy, part, counters, c.strips, c.S, c.cps)
+    switch (c.waves) {
+      case 1: QTTS_F8S(1, 4); break;
+      case 2: QTTS_F8S(2, 4); break;
+      case 4: QTTS_F8S(4, 2); break;
+      case 8: QTTS_F8S(8, 2); break;
+      case 16: QTTS_F8S(16, 1); break;
+      default: return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8 skinny: waves must be 1, 2, 4, 8 or 16");
+    }
+#undef QTTS_F8S
+    return qtts_check_launch("w8a8_fp8_skinny");
+  }
+  const int64_t tiles = (int64_t)c.mtiles * c.ntiles;
+  float* part = c.S > 1 ? (float*)((char*)ws + kCounterBytes) : nullptr;
+  const int64_t blocks = (tiles + 7) / 8 * 8 * c.S;
+#define QTTS_F8T(BM)                                                                                             \
+  fp8_tile_kernel<OT, BM><<<(unsigned)blocks, 256, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, \
+                                                            y, ldy, part, counters, c.mtiles, c.ntiles, c.S, c.cps)
+  if (c.bm == 32) QTTS_F8T(32);
+  else if (c.bm == 64) QTTS_F8T(64);
+  else QTTS_F8T(128);
+#undef QTTS_F8T
+  return qtts_check_launch("w8a8_fp8_tile");
+}
+
+int qtts_launch_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const uint8_t* qw,
+                         int64_t n, int64_t ldqw, const float* sw, const void* bias, void* y, int out_dtype,
+                         int64_t ldy, int algo, void* ws, int64_t ws_bytes, hipStream_t st) {
+  if (out_dtype == QTTS_BF16)
+    return fp8_launch_typed<bf16_t>(qx, sx, m, k, ldqx, qw, n, ldqw, sw, (const bf16_t*)bias, (bf16_t*)y, ldy, algo, ws,
+                                    ws_bytes, st);
+  if (out_dtype == QTTS_F16)
+    return fp8_launch_typed<f16_t>(qx, sx, m, k, ldqx, qw, n, ldqw, sw, (const f16_t*)bias, (f16_t*)y, ldy, algo, ws,
+                                   ws_bytes, st);
+  return fp8_launch_typed<float>(qx, sx, m, k, ldqx, qw, n, ldqw, sw, (const float*)bias, (float*)y, ldy, algo, ws,
+                                 ws_bytes, st);
+}

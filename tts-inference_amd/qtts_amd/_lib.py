@@ -1,0 +1,126 @@
+"""ctypes binding of libqtts_amd.so (the C ABI declared in include/qtts_amd.h).
+
+The library is loaded from this package directory.  There is no fallback: if the
+library is missing or the device is not a gfx950, calls raise.  Status codes map
+to the exceptions the reference raises for the same conditions
+(qtts/quant/kernels.py:159-160 ValueError on a shape mismatch; qtts/quant/int8.py:71-73
+and qtts/quant/base.py:122-124 RuntimeError when the kernel or device is missing;
+qtts/quant/fp8.py:115-123 NotImplementedError).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libqtts_amd.so")
+
+ABI_VERSION = 1
+
+# qtts_status
+OK = 0
+ERR_INVALID_ARGUMENT = -1
+ERR_UNSUPPORTED = -2
+ERR_NOT_IMPLEMENTED = -3
+ERR_HIP = -4
+ERR_WORKSPACE = -5
+
+# qtts_dtype
+F32, BF16, F16 = 0, 1, 2
+# qtts_div_mode
+DIV_DEVICE, DIV_IEEE = 0, 1
+# qtts_algo (bits 0-7); bits 8-15 split count, bits 16-23 waves per workgroup
+ALGO_AUTO, ALGO_SKINNY, ALGO_TILE = 0, 1, 2
+# qtts_op
+OP_W8A16, OP_W8A8_FP8, OP_FP8_LINEAR = 0, 1, 2
+
+EXPORTS = (
+    "qtts_abi_version",
+    "qtts_last_error",
+    "qtts_device_supported",
+    "qtts_workspace_bytes",
+    "qtts_pack_int8_rowwise",
+    "qtts_pack_fp8_e4m3_rowwise",
+    "qtts_w8a16_gemm",
+    "qtts_quant_act_fp8_rows",
+    "qtts_w8a8_fp8_gemm",
+    "qtts_fp8_linear",
+)
+
+
+def algo_code(family: int = ALGO_AUTO, splits: int = 0, waves: int = 0) -> int:
+    if not (0 <= splits < 256 and 0 <= waves < 256):
+        raise ValueError("splits and waves must be in [0, 255]")
+    return family | (splits << 8) | (waves << 16)
+
+
+class QttsError(RuntimeError):
+    pass
+
+
+_lock = threading.Lock()
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Load and type the shared library (once per process)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python tts-inference_amd/build.py` "
+                "(hipcc, --offload-arch=gfx950)"
+            )
+        L = ctypes.CDLL(LIB_PATH)
+        p, i64, i32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int
+        L.qtts_abi_version.restype = i32
+        L.qtts_abi_version.argtypes = []
+        L.qtts_last_error.restype = ctypes.c_char_p
+        L.qtts_last_error.argtypes = []
+        L.qtts_device_supported.restype = i32
+        L.qtts_device_supported.argtypes = [i32]
+        L.qtts_workspace_bytes.restype = i64
+        L.qtts_workspace_bytes.argtypes = [i32, i64, i64, i64, i32]
+        L.qtts_pack_int8_rowwise.restype = i32
+        L.qtts_pack_int8_rowwise.argtypes = [p, i32, i64, i64, i64, p, p, i32, p, i32, p]
+        L.qtts_pack_fp8_e4m3_rowwise.restype = i32
+        L.qtts_pack_fp8_e4m3_rowwise.argtypes = [p, i32, i64, i64, i64, p, p, i32, p]
+        L.qtts_w8a16_gemm.restype = i32
+        L.qtts_w8a16_gemm.argtypes = [p, i32, i64, i64, i64, p, i64, i64, p, i32, p, p, i64, i32, p, i64, p]
+        L.qtts_quant_act_fp8_rows.restype = i32
+        L.qtts_quant_act_fp8_rows.argtypes = [p, i32, i64, i64, i64, p, p, i32, p]
+        L.qtts_w8a8_fp8_gemm.restype = i32
+        L.qtts_w8a8_fp8_gemm.argtypes = [p, p, i64, i64, i64, p, i64, i64, p, p, p, i32, i64, i32, p, i64, p]
+        L.qtts_fp8_linear.restype = i32
+        L.qtts_fp8_linear.argtypes = [p, i32, i64, i64, i64, p, i64, i64, p, p, p, i64, i32, i32, p, i64, p]
+        version = L.qtts_abi_version()
+        if version != ABI_VERSION:
+            raise RuntimeError(f"libqtts_amd ABI version {version}, expected {ABI_VERSION}; rebuild it")
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return load().qtts_last_error().decode(errors="replace")
+
+
+def check(status: int, what: str) -> None:
+    """Raise the exception the reference raises for the same condition."""
+    if status == OK:
+        return
+    msg = f"{what}: {last_error()}"
+    if status in (ERR_INVALID_ARGUMENT, ERR_WORKSPACE):
+        raise ValueError(msg)
+    if status == ERR_NOT_IMPLEMENTED:
+        raise NotImplementedError(msg)
+    raise QttsError(msg)
+
+
+def device_supported(device: int) -> bool:
+    return load().qtts_device_supported(int(device)) == 1

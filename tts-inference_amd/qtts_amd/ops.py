@@ -1,0 +1,255 @@
+"""torch-facing wrappers over the C ABI.
+
+Every function takes and returns torch tensors on a gfx950 device, launches on
+torch's current stream, allocates outputs through torch's caching allocator and
+never synchronises, so each one can be captured into a HIP graph.  There is no
+CPU or eager-PyTorch fallback: a missing library or an unsupported device raises.
+"""
+
+from __future__ import annotations
+
+import threading
+
+import torch
+
+from . import _lib
+from ._lib import ALGO_AUTO, DIV_DEVICE, DIV_IEEE, OP_W8A16, OP_W8A8_FP8, algo_code  # noqa: F401
+
+_DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
+
+
+def dtype_code(dtype: torch.dtype) -> int:
+    try:
+        return _DTYPES[dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {dtype}; expected float32, bfloat16 or float16") from None
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _require_cuda(*tensors: torch.Tensor | None) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(f"expected a GPU tensor, got one on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    assert dev is not None
+    return dev
+
+
+def device_supported(device: torch.device | int | None = None) -> bool:
+    """Whether ``device`` (default: the current one) is a gfx950 this library runs on."""
+    if not torch.cuda.is_available():
+        return False
+    if device is None:
+        idx = torch.cuda.current_device()
+    elif isinstance(device, int):
+        idx = device
+    else:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+    return _lib.device_supported(idx)
+
+
+# ---- workspace ---------------------------------------------------------------------------
+# One zero-filled byte buffer per device.  The kernels that use it (split-K meeting
+# points) leave it zero-filled again, so it is allocated and cleared once, outside
+# any graph capture, and then shared by every call on that device.  Calls that
+# share it must be stream-ordered, which holds for one engine thread on one stream.
+
+_ws_lock = threading.Lock()
+_workspaces: dict[int, torch.Tensor] = {}
+# Outgrown workspaces are never freed: a HIP graph captured earlier still holds
+# their address and keeps using them on every replay.
+_retired: list[torch.Tensor] = []
+
+
+def reserve_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
+    """Grow the device's workspace to at least ``nbytes`` (call outside capture)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    with _ws_lock:
+        ws = _workspaces.get(idx)
+        if nbytes <= 0:
+            return ws
+        if ws is None or ws.numel() < nbytes:
+            if torch.cuda.is_current_stream_capturing():
+                return ws
+            size = max(nbytes, 0 if ws is None else ws.numel())
+            size = (size + (1 << 20) - 1) & ~((1 << 20) - 1)
+            if ws is not None:
+                _retired.append(ws)
+            ws = torch.zeros(size, dtype=torch.uint8, device=torch.device("cuda", idx))
+            _workspaces[idx] = ws
+        return ws
+
+
+def workspace_bytes(op: int, m: int, n: int, k: int, algo: int = ALGO_AUTO) -> int:
+    v = _lib.load().qtts_workspace_bytes(op, m, n, k, algo)
+    if v < 0:
+        _lib.check(int(v), "workspace_bytes")
+    return int(v)
+
+
+def _ws_for(device: torch.device) -> tuple[int | None, int]:
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get(idx)
+    return (None, 0) if ws is None else (ws.data_ptr(), ws.numel())
+
+
+# ---- packers -----------------------------------------------------------------------------
+
+def pack_int8(weight: torch.Tensor, scale_dtype: torch.dtype | None = None, div_mode: int = DIV_DEVICE,
+              want_f32_scale: bool = False):
+    """Per-output-channel symmetric int8 (qtts/quant/int8.py:45-56).
+
+    Returns ``(q [N,K] int8, scale [N] scale_dtype)`` and, with ``want_f32_scale``,
+    the unrounded fp32 scale as a third element.  ``scale_dtype`` defaults to fp32
+    (the return of quantize_weight_per_channel); Int8WeightOnlyMethod stores it in
+    the weight dtype (qtts/quant/int8.py:105).
+    """
+    if weight.dim() != 2:
+        raise ValueError(f"expected a 2-D weight, got shape {tuple(weight.shape)}")
+    dev = _require_cuda(weight)
+    w = weight.detach()
+    if w.stride(1) != 1:
+        w = w.contiguous()
+    n, k = w.shape
+    sdt = torch.float32 if scale_dtype is None else scale_dtype
+    q = torch.empty((n, k), dtype=torch.int8, device=dev)
+    scale = torch.empty(n, dtype=sdt, device=dev)
+    s32 = torch.empty(n, dtype=torch.float32, device=dev) if want_f32_scale else None
+    st = _lib.load().qtts_pack_int8_rowwise(
+        _ptr(w), dtype_code(w.dtype), n, k, w.stride(0), _ptr(q), _ptr(scale), dtype_code(sdt), _ptr(s32),
+        div_mode, _stream(dev))
+    _lib.check(st, "pack_int8_rowwise")
+    return (q, scale, s32) if want_f32_scale else (q, scale)
+
+
+def pack_fp8(weight: torch.Tensor, div_mode: int = DIV_DEVICE):
+    """Per-output-channel e4m3 (qtts/quant/fp8.py:45-49): ``(q [N,K] float8_e4m3fn, scale [N] fp32)``."""
+    if weight.dim() != 2:
+        raise ValueError(f"expected a 2-D weight, got shape {tuple(weight.shape)}")
+    dev = _require_cuda(weight)
+    w = weight.detach()
+    if w.stride(1) != 1:
+        w = w.contiguous()
+    n, k = w.shape
+    q = torch.empty((n, k), dtype=torch.float8_e4m3fn, device=dev)
+    scale = torch.empty(n, dtype=torch.float32, device=dev)
+    st = _lib.load().qtts_pack_fp8_e4m3_rowwise(_ptr(w), dtype_code(w.dtype), n, k, w.stride(0), _ptr(q), _ptr(scale),
+                                               div_mode, _stream(dev))
+    _lib.check(st, "pack_fp8_e4m3_rowwise")
+    return q, scale
+
+
+# ---- GEMMs --------------------------------------------------------------------------------
+
+def _flatten(x: torch.Tensor) -> torch.Tensor:
+    rows = 1
+    for d in x.shape[:-1]:
+        rows *= d
+    a = x.reshape(rows, x.shape[-1])
+    if a.stride(-1) != 1 or (a.shape[0] > 1 and a.stride(0) < a.shape[1]):
+        a = a.contiguous()
+    return a
+
+
+def w8a16_gemm(x: torch.Tensor, q: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None = None,
+               algo: int = ALGO_AUTO) -> torch.Tensor:
+    """``x @ (q * scale)^T + bias`` with q dequantized in registers (qtts/quant/kernels.py:138-178).
+
+    x ``[..., K]`` float (bf16/fp16/fp32), q ``[N, K]`` int8, scale ``[N]``, bias ``[N]`` in
+    x's dtype or None.  Returns a fresh ``[..., N]`` tensor in x's dtype.
+    """
+    shape = x.shape
+    a = _flatten(x)
+    rows, k = a.shape
+    if q.dim() != 2 or q.dtype != torch.int8:
+        raise ValueError(f"weight must be a 2-D int8 tensor, got {q.dtype} {tuple(q.shape)}")
+    n = q.shape[0]
+    if q.shape[1] != k:
+        raise ValueError(f"weight is [{n}, {q.shape[1]}] but x has K={k}")
+    if q.stride(1) != 1:
+        q = q.contiguous()
+    if scale.numel() != n:
+        raise ValueError(f"scale has {scale.numel()} entries for {n} output channels")
+    if bias is not None:
+        if bias.numel() != n:
+            raise ValueError(f"bias has {bias.numel()} entries for {n} output channels")
+        if bias.dtype != a.dtype:
+            bias = bias.to(a.dtype)
+        bias = bias.contiguous()
+    dev = _require_cuda(a, q, scale, bias)
+    scale = scale.contiguous()
+    out = torch.empty((rows, n), dtype=a.dtype, device=dev)
+    ws, ws_n = _ws_for(dev)
+    st = _lib.load().qtts_w8a16_gemm(
+        _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else k, _ptr(q), n, q.stride(0),
+        _ptr(scale), dtype_code(scale.dtype), _ptr(bias), _ptr(out), n, algo, ws, ws_n, _stream(dev))
+    _lib.check(st, "w8a16_gemm")
+    return out.reshape(*shape[:-1], n)
+
+
+def quant_act_fp8(x: torch.Tensor, div_mode: int = DIV_DEVICE):
+    """Per-token e4m3 activations (qtts/quant/fp8.py:77-78): ``(qx [M,K] e4m3, sx [M] fp32)``."""
+    a = _flatten(x)
+    m, k = a.shape
+    dev = _require_cuda(a)
+    qx = torch.empty((m, k), dtype=torch.float8_e4m3fn, device=dev)
+    sx = torch.empty(m, dtype=torch.float32, device=dev)
+    st = _lib.load().qtts_quant_act_fp8_rows(_ptr(a), dtype_code(a.dtype), m, k, a.stride(0) if m > 1 else k,
+                                             _ptr(qx), _ptr(sx), div_mode, _stream(dev))
+    _lib.check(st, "quant_act_fp8_rows")
+    return qx, sx
+
+
+def w8a8_fp8_gemm(qx: torch.Tensor, sx: torch.Tensor, qw: torch.Tensor, sw: torch.Tensor,
+                  bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                  algo: int = ALGO_AUTO) -> torch.Tensor:
+    """``(qx*sx) @ (qw*sw)^T`` rounded to out_dtype, then ``+ bias`` in out_dtype (qtts/quant/fp8.py:79-89).
+
+    qx ``[M, K]`` e4m3, sx ``[M]`` fp32, qw ``[N, K]`` e4m3 (row-major), sw ``[N]`` fp32.
+    """
+    if qx.dim() != 2 or qw.dim() != 2:
+        raise ValueError("qx and qw must be 2-D")
+    m, k = qx.shape
+    n = qw.shape[0]
+    if qw.shape[1] != k:
+        raise ValueError(f"weight is [{n}, {qw.shape[1]}] but x has K={k}")
+    if qx.stride(1) != 1:
+        qx = qx.contiguous()
+    if qw.stride(1) != 1:
+        qw = qw.contiguous()
+    if sx.numel() != m or sw.numel() != n:
+        raise ValueError("scale sizes do not match the operands")
+    sx = sx.reshape(-1).to(torch.float32).contiguous()
+    sw = sw.reshape(-1).to(torch.float32).contiguous()
+    if bias is not None:
+        bias = bias.to(out_dtype).contiguous()
+    dev = _require_cuda(qx, sx, qw, sw, bias)
+    out = torch.empty((m, n), dtype=out_dtype, device=dev)
+    ws, ws_n = _ws_for(dev)
+    st = _lib.load().qtts_w8a8_fp8_gemm(
+        _ptr(qx), _ptr(sx), m, k, qx.stride(0) if m > 1 else k, _ptr(qw), n, qw.stride(0), _ptr(sw), _ptr(bias),
+        _ptr(out), dtype_code(out_dtype), n, algo, ws, ws_n, _stream(dev))
+    _lib.check(st, "w8a8_fp8_gemm")
+    return out
+
+
+def fp8_linear(x: torch.Tensor, qw: torch.Tensor, sw: torch.Tensor, bias: torch.Tensor | None = None,
+               div_mode: int = DIV_DEVICE, algo: int = ALGO_AUTO) -> torch.Tensor:
+    """The whole of Fp8Method.apply (qtts/quant/fp8.py:72-89): quantize x per token, fp8 GEMM."""
+    shape = x.shape
+    qx, sx = quant_act_fp8(x, div_mode)
+    out = w8a8_fp8_gemm(qx, sx, qw, sw, bias, x.dtype, algo)
+    return out.reshape(*shape[:-1], qw.shape[0])

@@ -1,0 +1,135 @@
+"""int8 quantization methods (qtts/quant/int8.py).
+
+``Int8WeightOnlyMethod`` (W8A16) stores the weight as int8 with one scale per
+output channel, keeps activations in the model dtype, and runs the gfx950 fused
+dequantize-in-registers GEMM.  With ``calibrate`` it times, per layer shape, the
+HIP kernel candidates against the unquantized F.linear (hipBLASLt on ROCm) inside
+a HIP graph and keeps the fastest; a layer where no candidate wins by 5% keeps
+its original weight and GEMM (qtts/quant/int8.py:79-111).
+
+``Int8Method`` (W8A8 on int8 MFMA) is not built yet on this backend.
+"""
+
+from __future__ import annotations
+
+import logging
+
+import torch
+import torch.nn.functional as F
+
+from .. import _lib, ops
+from .base import QuantMethodBase
+from .calibrate import pick_fastest
+from .kernels import kernel_available
+
+logger = logging.getLogger("qtts_amd.quant.int8")
+
+_INT8_MAX = 127.0
+
+#: Row counts the kernel choice is tuned for: each call uses the entry of the
+#: smallest bucket that holds its row count (decode rows 1..16 go to the skinny
+#: kernel, prefill rows to the tile kernel).
+M_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256, 1024)
+
+#: Per (N, K, bucket) algo codes chosen by calibration; absent means automatic.
+_ALGO: dict[tuple[int, int, int], int] = {}
+
+
+def bucket_of(rows: int) -> int:
+    for b in M_BUCKETS:
+        if rows <= b:
+            return b
+    return M_BUCKETS[-1]
+
+
+def quantize_weight_per_channel(weight: torch.Tensor, div_mode: int = _lib.DIV_DEVICE):
+    """Symmetric per-output-channel int8 on the GPU: ``(q [N,K] int8, scale [N] fp32)``.
+
+    Bit-exact with qtts/quant/int8.py:53-55 evaluated by torch on the GPU
+    (``div_mode=DIV_DEVICE``) or on the CPU (``DIV_IEEE``).
+    """
+    return ops.pack_int8(weight, torch.float32, div_mode)
+
+
+def _candidates(rows: int) -> dict[str, int]:
+    """Kernel configurations worth timing at ``rows``."""
+    if rows <= 16:
+        c = {"skinny": _lib.algo_code(_lib.ALGO_SKINNY)}
+        for s in (1, 2, 4, 8):
+            c[f"skinny_s{s}"] = _lib.algo_code(_lib.ALGO_SKINNY, splits=s)
+        return c
+    c = {"tile": _lib.algo_code(_lib.ALGO_TILE)}
+    for s in (1, 2, 4):
+        c[f"tile_s{s}"] = _lib.algo_code(_lib.ALGO_TILE, splits=s)
+    return c
+
+
+class Int8WeightOnlyMethod(QuantMethodBase):
+    """int8 weights, model-dtype activations, dequantized inside the GEMM."""
+
+    name = "int8_weight_only"
+
+    def __init__(self, calibrate: bool = True, calibration_batch: int = 16, div_mode: int = _lib.DIV_DEVICE) -> None:
+        available, reason = kernel_available()
+        if not available:
+            raise RuntimeError(f"int8 weight-only needs the gfx950 fused kernel: {reason}")
+        self.calibrate = calibrate
+        self.calibration_batch = calibration_batch
+        self.div_mode = div_mode
+        self.quantized = 0
+        self.declined = 0
+
+    def _profitable(self, layer, q: torch.Tensor, scale: torch.Tensor) -> bool:
+        if not self.calibrate:
+            return True
+        weight = layer.weight
+        if not torch.cuda.is_available() or weight.device.type != "cuda":
+            return False
+        rows = max(1, self.calibration_batch)
+        n, k = layer.out_features, layer.in_features
+        gen = torch.Generator(device=weight.device).manual_seed(0)
+        x = torch.randn(rows, k, device=weight.device, dtype=weight.dtype, generator=gen)
+        ops.reserve_workspace(weight.device, ops.workspace_bytes(_lib.OP_W8A16, rows, n, k))
+        cands = {name: (lambda a=algo: ops.w8a16_gemm(x, q, scale, None, a)) for name, algo in _candidates(rows).items()}
+        best = pick_fastest(cands, lambda: F.linear(x, weight, None),
+                            key=("int8_wo", n, k, rows, str(weight.dtype)))
+        if best is not None:
+            _ALGO.setdefault((n, k, bucket_of(rows)), _candidates(rows)[best])
+        return best is not None
+
+    def process_weights(self, layer) -> None:
+        weight = layer.weight
+        q, scale = ops.pack_int8(weight, weight.dtype, self.div_mode)
+        if not self._profitable(layer, q, scale):
+            self.declined += 1
+            # Leaving quant_method unset keeps the layer on F.linear.
+            layer.register_buffer("int8_weight", None, persistent=False)
+            return
+        ops.reserve_workspace(weight.device, max(
+            ops.workspace_bytes(_lib.OP_W8A16, m, layer.out_features, layer.in_features) for m in (16, 64, 128)))
+        layer.register_buffer("int8_weight", q, persistent=False)
+        layer.register_buffer("int8_scale", scale, persistent=False)
+        # Drop the full-precision weight, or the memory report would claim a saving it did not make.
+        layer.weight = torch.nn.Parameter(torch.empty(0, dtype=weight.dtype, device=weight.device),
+                                          requires_grad=False)
+        self.quantized += 1
+
+    def applies_to(self, layer) -> bool:
+        return getattr(layer, "int8_weight", None) is not None
+
+    def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        q = layer.int8_weight
+        rows = x.numel() // x.shape[-1] if x.shape[-1] else 0
+        algo = _ALGO.get((q.shape[0], q.shape[1], bucket_of(rows)), _lib.ALGO_AUTO)
+        return ops.w8a16_gemm(x, q, layer.int8_scale, bias, algo)
+
+
+class Int8Method(QuantMethodBase):
+    """W8A8 int8 (qtts/quant/int8.py:120-155): not built on this backend yet."""
+
+    name = "int8"
+
+    def __init__(self) -> None:
+        raise NotImplementedError(
+            "int8 W8A8 is not implemented on the gfx950 backend yet; use --quant-method int8_weight_only "
+            "(same weight footprint, faster at decode batch sizes) or fp8 for W8A8")

@@ -1,0 +1,32 @@
+"""The fused dequantize-in-registers GEMM and its availability check.
+
+Mirrors qtts/quant/kernels.py:83-84 (``kernel_available``) and :138-178
+(``w8_gemm``), backed by the hand-written gfx950 kernels in libqtts_amd.so
+instead of a Triton kernel.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from .. import _lib, ops
+
+
+def kernel_available() -> tuple[bool, str]:
+    """(True, "") when libqtts_amd.so loads and the current device is a gfx950."""
+    try:
+        _lib.load()
+    except Exception as exc:
+        return False, f"libqtts_amd unavailable: {exc}"
+    if not torch.cuda.is_available():
+        return False, "no GPU visible"
+    if not ops.device_supported():
+        name = torch.cuda.get_device_name()
+        return False, f"device {name!r} is not a gfx950 (MI355X-class) GPU"
+    return True, ""
+
+
+def w8_gemm(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None = None,
+            algo: int = _lib.ALGO_AUTO) -> torch.Tensor:
+    """``x @ (weight * scale).T + bias``, dequantizing ``weight`` in registers."""
+    return ops.w8a16_gemm(x, weight, scale, bias, algo)
