@@ -43,6 +43,9 @@ typedef enum { QTTS_DIV_DEVICE = 0, QTTS_DIV_IEEE = 1 } qtts_div_mode;
 /* Kernel family for the GEMMs.  AUTO picks by shape; the calibrator pins one. */
 typedef enum { QTTS_ALGO_AUTO = 0, QTTS_ALGO_SKINNY = 1, QTTS_ALGO_TILE = 2 } qtts_algo;
 
+/* Strip layouts (see qtts_to_strips). */
+typedef enum { QTTS_STRIP_INT8 = 0, QTTS_STRIP_FP8 = 1 } qtts_strip_kind;
+
 /* Workspace owners for qtts_workspace_bytes. */
 typedef enum { QTTS_OP_W8A16 = 0, QTTS_OP_W8A8_FP8 = 1, QTTS_OP_FP8_LINEAR = 2 } qtts_op;
 
@@ -94,6 +97,21 @@ int qtts_pack_int8_rowwise(const void* src, int src_dtype, int64_t n, int64_t k,
 int qtts_pack_fp8_e4m3_rowwise(const void* src, int src_dtype, int64_t n, int64_t k, int64_t ld_src,
                                uint8_t* q_out, float* scale_out, int div_mode, void* stream);
 
+/* --- strip layout ------------------------------------------------------------------ */
+
+/* The [n, k] weight bytes re-tiled so that each wavefront load of the GEMM kernels
+ * is one contiguous 1 KiB: 16-row strips, CH-column chunks (CH = 64 for
+ * QTTS_STRIP_INT8, 128 for QTTS_STRIP_FP8), block (s, c) of 16*CH bytes at
+ * (s * ceil(k/CH) + c) * 16 * CH; inside it, half h and lane l (0..63) own the 16
+ * bytes at h*1024 + l*16 = row 16s + l%16, columns CH*c + (l/16)*(CH/4) + 16h .. +15.
+ * Rows >= n and columns >= k are zero.  A pure permutation of the packer's output:
+ * qtts_from_strips recovers the row-major bytes exactly.  No counterpart in the
+ * reference, whose Triton kernel reads the row-major buffer (qtts/quant/kernels.py:108-117);
+ * the quant methods store this layout in place of it. */
+int64_t qtts_strip_bytes(int64_t n, int64_t k, int kind);
+int qtts_to_strips(const void* src, int64_t n, int64_t k, int64_t ld_src, int kind, void* dst, void* stream);
+int qtts_from_strips(const void* src, int64_t n, int64_t k, int kind, void* dst, int64_t ld_dst, void* stream);
+
 /* --- W8A16: int8 weights, bf16/fp16/fp32 activations ----------------------------- */
 
 /* y[m, n] = cast(sum_c x[m,c] * q[n,c] * f32(scale[n]) + f32(bias[n])), fp32
@@ -107,6 +125,13 @@ int qtts_w8a16_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
                     const int8_t* q, int64_t n, int64_t ldq,
                     const void* scale, int scale_dtype, const void* bias,
                     void* y, int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream);
+
+/* qtts_w8a16_gemm with the weight in the QTTS_STRIP_INT8 layout (qs, qtts_strip_bytes
+ * bytes).  x must be bf16 or fp16 with 16-byte aligned rows and k % 16 == 0. */
+int qtts_w8a16_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                           const int8_t* qs, int64_t n, const void* scale, int scale_dtype,
+                           const void* bias, void* y, int64_t ldy, int algo, void* ws,
+                           int64_t ws_bytes, void* stream);
 
 /* --- fp8 W8A8 --------------------------------------------------------------------- */
 
@@ -136,6 +161,17 @@ int qtts_fp8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
                     const uint8_t* qw, int64_t n, int64_t ldqw, const float* sw,
                     const void* bias, void* y, int64_t ldy, int div_mode,
                     int algo, void* ws, int64_t ws_bytes, void* stream);
+
+/* qtts_w8a8_fp8_gemm and qtts_fp8_linear with the weight in the QTTS_STRIP_FP8
+ * layout.  Activation rows must be 16-byte aligned and k % 32 == 0. */
+int qtts_w8a8_fp8_gemm_strips(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx,
+                              const uint8_t* qws, int64_t n, const float* sw, const void* bias,
+                              void* y, int out_dtype, int64_t ldy, int algo, void* ws,
+                              int64_t ws_bytes, void* stream);
+int qtts_fp8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                           const uint8_t* qws, int64_t n, const float* sw, const void* bias,
+                           void* y, int64_t ldy, int div_mode, int algo, void* ws, int64_t ws_bytes,
+                           void* stream);
 
 #ifdef __cplusplus
 }

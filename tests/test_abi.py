@@ -80,6 +80,15 @@ def test_workspace_query():
     assert L.qtts_workspace_bytes(_lib.OP_W8A16, 4, 2048, 0, 0) >= 0  # K = 0 is a valid query
 
 
+def test_strip_bytes():
+    L = _lib.load()
+    assert L.qtts_strip_bytes(2048, 2048, _lib.STRIP_INT8) == 2048 * 2048
+    assert L.qtts_strip_bytes(17, 100, _lib.STRIP_INT8) == 2 * 2 * 1024
+    assert L.qtts_strip_bytes(17, 100, _lib.STRIP_FP8) == 2 * 1 * 2048
+    assert L.qtts_strip_bytes(0, 100, _lib.STRIP_FP8) == 0
+    assert L.qtts_strip_bytes(16, 16, 7) == -1
+
+
 def test_device_supported_without_gpu_is_false():
     L = _lib.load()
     assert L.qtts_device_supported(-1) == 0

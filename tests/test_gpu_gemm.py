@@ -243,3 +243,112 @@ def test_fp8_small_and_odd(ops):
         qx, sx = ops.quant_act_fp8(x)
         ref, inter = _oracle_w8a8(qx, sx, qw, sw, b)
         assert_close(y, ref, f"fp8 m={m} n={n} k={k}", inter)
+
+
+# ---- strip layout ---------------------------------------------------------------------------
+
+def _strips_numpy(q: np.ndarray, ch: int) -> np.ndarray:
+    """The strip layout written straight from its definition (include/qtts_amd.h)."""
+    n, k = q.shape
+    strips, nch = -(-n // 16), -(-k // ch)
+    pad = np.zeros((strips * 16, nch * ch), q.dtype)
+    pad[:n, :k] = q
+    out = np.zeros(strips * nch * 16 * ch, q.dtype)
+    for s in range(strips):
+        for c in range(nch):
+            base = (s * nch + c) * 16 * ch
+            for h in range(ch // 64):
+                for lane in range(64):
+                    row = 16 * s + lane % 16
+                    col = c * ch + (lane // 16) * (ch // 4) + 16 * h
+                    off = base + h * 1024 + lane * 16
+                    out[off:off + 16] = pad[row, col:col + 16]
+    return out
+
+
+@pytest.mark.parametrize("kind,ch", [(0, 64), (1, 128)])
+def test_strip_layout_definition_and_roundtrip(ops, kind, ch):
+    rng = np.random.default_rng(kind)
+    for n, k in ((1, 16), (16, 64), (17, 100), (33, 130), (40, 256), (5, 2048)):
+        q = rng.integers(-127, 128, (n, k)).astype(np.int8)
+        qt = torch.from_numpy(q).cuda()
+        if kind == 1:
+            qt = qt.view(torch.float8_e4m3fn)
+        qs = ops.to_strips(qt, kind)
+        assert qs.numel() == ops.strip_bytes(n, k, kind)
+        got = qs.reshape(-1).view(torch.int8).cpu().numpy()
+        np.testing.assert_array_equal(got, _strips_numpy(q, ch), err_msg=f"n={n} k={k}")
+        back = ops.from_strips(qs, n, k, kind)
+        assert torch.equal(back.view(torch.int8), torch.from_numpy(q).cuda())
+
+
+@pytest.mark.parametrize("n,k", TALKER + PREDICTOR)
+def test_w8a16_strips_decode_shapes(ops, n, k):
+    for m in (1, 2, 4, 8, 16):
+        print(f"strips n={n} k={k} m={m}", flush=True)
+        x, w, b = _make(m, n, k, bias=(m == 4), seed=n + 3 * k + m)
+        q, s = ops.pack_int8(w, torch.bfloat16)
+        qs = ops.to_strips(q)
+        ref = _oracle_w8a16(x, q, s, b)
+        y = ops.w8a16_gemm_strips(x, qs, n, s, b)
+        assert_close(y, ref, f"strips auto m={m} n={n} k={k}")
+        for splits, waves in ((1, 4), (2, 8), (4, 16), (3, 2)):
+            y2 = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, splits, waves))
+            assert_close(y2, ref, f"strips m={m} n={n} k={k} S={splits} W={waves}")
+
+
+def test_w8a16_strips_ragged_and_tile(ops):
+    for m, n, k in ((3, 17, 16), (5, 100, 80), (1, 33, 2064), (16, 1000, 1008), (17, 100, 80), (64, 2040, 2048),
+                    (130, 1030, 1040), (256, 2048, 2048)):
+        x, w, b = _make(m, n, k, bias=True, seed=m * 7 + n + k)
+        q, s = ops.pack_int8(w, torch.bfloat16)
+        qs = ops.to_strips(q)
+        y = ops.w8a16_gemm_strips(x, qs, n, s, b)
+        assert_close(y, _oracle_w8a16(x, q, s, b), f"strips m={m} n={n} k={k}")
+        if m > 16:
+            for splits in (1, 2, 4):
+                y2 = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits))
+                assert_close(y2, _oracle_w8a16(x, q, s, b), f"strips tile m={m} n={n} k={k} S={splits}")
+
+
+def test_w8a16_strips_graph_replays_split(ops):
+    x, w, b = _make(8, 2048, 6144, bias=True, seed=77)
+    q, s = ops.pack_int8(w, torch.bfloat16)
+    qs = ops.to_strips(q)
+    algo = ops.algo_code(1, 4, 8)
+    eager = ops.w8a16_gemm_strips(x, qs, 2048, s, b, algo)
+    assert torch.equal(eager, ops.w8a16_gemm_strips(x, qs, 2048, s, b, algo)), "split-K result is not deterministic"
+    static_x = x.clone()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        ops.w8a16_gemm_strips(static_x, qs, 2048, s, b, algo)
+    torch.cuda.current_stream().wait_stream(st)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = ops.w8a16_gemm_strips(static_x, qs, 2048, s, b, algo)
+    for i in range(4):
+        ops.w8a16_gemm_strips(x * 3, qs, 2048, s, b, ops.algo_code(1, 2, 16))  # another split count in between
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+
+
+@pytest.mark.parametrize("n,k", TALKER)
+def test_fp8_strips_vs_oracle(ops, n, k):
+    for m in (1, 8, 16, 17, 256):
+        x, w = _fp8_inputs(m, n, k, seed=n + m + 1)
+        qw, sw = ops.pack_fp8(w)
+        qws = ops.to_strips(qw)
+        qx, sx = ops.quant_act_fp8(x)
+        ref, _ = _oracle_w8a8(qx, sx, qw, sw, None) if m <= 64 else (None, None)
+        if ref is None:
+            ref = ((qx.float() * sx[:, None]) @ (qw.float() * sw[:, None]).t()).double().cpu().numpy()
+        y = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, None, torch.bfloat16)
+        assert_close(y, ref, f"fp8 strips m={m} n={n} k={k}")
+        if m <= 16:
+            for splits, waves in ((1, 4), (2, 8), (4, 16)):
+                y2 = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, None, torch.bfloat16, ops.algo_code(1, splits, waves))
+                assert_close(y2, ref, f"fp8 strips m={m} n={n} k={k} S={splits} W={waves}")
+        y3 = ops.fp8_linear_strips(x, qws, n, sw)
+        assert torch.equal(y3, y)

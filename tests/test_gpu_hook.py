@@ -39,7 +39,8 @@ class TalkerLayer(nn.Module):
 
 def _expected_int8(layer, x):
     """Dequantize-then-matmul in fp32 of the packed buffers (the oracle formula on the GPU)."""
-    w = layer.int8_weight.float() * layer.int8_scale.float()[:, None]
+    from qtts_amd.quant.int8 import int8_weight_rowmajor
+    w = int8_weight_rowmajor(layer).float() * layer.int8_scale.float()[:, None]
     y = x.float() @ w.t()
     if layer.bias is not None:
         y = y + layer.bias.float()
@@ -99,15 +100,16 @@ def test_fp8_hook():
     model = TalkerLayer()
     report = apply_quantization(QuantConfig(method="fp8"), talker=model)
     assert report["talker"]["converted"] == 5
+    from qtts_amd.quant.fp8 import fp8_weight_rowmajor
     layer = model.text_proj_fc1
-    assert layer.fp8_weight.shape == (2048, 2048) and layer.fp8_weight.stride() == (1, 2048)  # [K, N] view
+    qw = fp8_weight_rowmajor(layer)
+    assert qw.shape == (2048, 2048) and layer.fp8_weight.numel() == 2048 * 2048
     for m in (1, 8, 256):
         x = torch.randn(m, 2048, device="cuda").to(torch.bfloat16)
         y = layer(x)
         qx, sx = ops.quant_act_fp8(x)
         ref = O.w8a8_ref(qx.view(torch.uint8).cpu().numpy(), sx.cpu().numpy(),
-                         layer.fp8_weight.t().contiguous().view(torch.uint8).cpu().numpy(),
-                         layer.fp8_scale.reshape(-1).cpu().numpy())
+                         qw.view(torch.uint8).cpu().numpy(), layer.fp8_scale.reshape(-1).cpu().numpy())
         # the reference rounds the scaled product to bf16, then adds the bias in bf16
         assert_close(y, ref + layer.bias.double().cpu().numpy(), f"fp8 m={m}", inter=ref)
 

@@ -7,6 +7,7 @@
 #include <cstdio>
 #include <cstring>
 
+#include "layout.h"
 #include "qtts_amd.h"
 
 // Launchers implemented next to their kernels.
@@ -17,12 +18,14 @@ int qtts_launch_pack_fp8(const void* src, int src_dtype, int64_t n, int64_t k, i
 int qtts_launch_quant_act_fp8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld, uint8_t* qx, float* sx,
                               int div_mode, hipStream_t st);
 int qtts_launch_w8a16(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* q, int64_t n,
-                      int64_t ldq, const void* scale, int scale_dtype, const void* bias, void* y, int64_t ldy,
-                      int algo, void* ws, int64_t ws_bytes, hipStream_t st);
+                      int64_t ldq, int layout, const void* scale, int scale_dtype, const void* bias, void* y,
+                      int64_t ldy, int algo, void* ws, int64_t ws_bytes, hipStream_t st);
 int64_t qtts_w8a16_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
 int qtts_launch_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const uint8_t* qw,
-                         int64_t n, int64_t ldqw, const float* sw, const void* bias, void* y, int out_dtype,
-                         int64_t ldy, int algo, void* ws, int64_t ws_bytes, hipStream_t st);
+                         int64_t n, int64_t ldqw, int layout, const float* sw, const void* bias, void* y,
+                         int out_dtype, int64_t ldy, int algo, void* ws, int64_t ws_bytes, hipStream_t st);
+int qtts_launch_to_strips(const void* src, int64_t n, int64_t k, int64_t ld, void* dst, int kind, hipStream_t st);
+int qtts_launch_from_strips(const void* src, int64_t n, int64_t k, void* dst, int64_t ld, int kind, hipStream_t st);
 int64_t qtts_fp8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
 
 static thread_local char g_last_error[512] = "";
@@ -150,8 +153,25 @@ int qtts_w8a16_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(scale && y && (k == 0 || (x && q)), "w8a16_gemm: null pointer");
   QTTS_TRY(current_device_check());
-  return qtts_launch_w8a16(x, x_dtype, m, k, ldx, q, n, ldq, scale, scale_dtype, bias, y, ldy, algo, ws, ws_bytes,
-                           (hipStream_t)stream);
+  return qtts_launch_w8a16(x, x_dtype, m, k, ldx, q, n, ldq, qtts::kLayoutRowMajor, scale, scale_dtype, bias, y, ldy,
+                           algo, ws, ws_bytes, (hipStream_t)stream);
+}
+
+int qtts_w8a16_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs, int64_t n,
+                           const void* scale, int scale_dtype, const void* bias, void* y, int64_t ldy, int algo,
+                           void* ws, int64_t ws_bytes, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a16_gemm_strips: negative size (m=%lld, n=%lld, k=%lld)", (long long)m,
+               (long long)n, (long long)k);
+  QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "w8a16_gemm_strips: size too large");
+  QTTS_REQUIRE(dtype_ok(x_dtype) && dtype_ok(scale_dtype), "w8a16_gemm_strips: bad dtype code");
+  QTTS_REQUIRE(algo_ok(algo), "w8a16_gemm_strips: bad algo %d", algo);
+  QTTS_REQUIRE(ldx >= k && ldy >= n, "w8a16_gemm_strips: leading dimension smaller than the row");
+  QTTS_REQUIRE(ws_bytes >= 0, "w8a16_gemm_strips: negative workspace size");
+  if (m == 0 || n == 0) return QTTS_OK;
+  QTTS_REQUIRE(scale && y && x && qs, "w8a16_gemm_strips: null pointer");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_w8a16(x, x_dtype, m, k, ldx, qs, n, 0, qtts::kLayoutStrips, scale, scale_dtype, bias, y, ldy,
+                           algo, ws, ws_bytes, (hipStream_t)stream);
 }
 
 int qtts_quant_act_fp8_rows(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, uint8_t* qx, float* sx,
@@ -179,19 +199,36 @@ int qtts_w8a8_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t k,
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(sx && sw && y && (k == 0 || (qx && qw)), "w8a8_fp8_gemm: null pointer");
   QTTS_TRY(current_device_check());
-  return qtts_launch_fp8_gemm(qx, sx, m, k, ldqx, qw, n, ldqw, sw, bias, y, out_dtype, ldy, algo, ws, ws_bytes,
-                              (hipStream_t)stream);
+  return qtts_launch_fp8_gemm(qx, sx, m, k, ldqx, qw, n, ldqw, qtts::kLayoutRowMajor, sw, bias, y, out_dtype, ldy,
+                              algo, ws, ws_bytes, (hipStream_t)stream);
 }
 
-int qtts_fp8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qw, int64_t n,
-                    int64_t ldqw, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode, int algo,
-                    void* ws, int64_t ws_bytes, void* stream) {
+int qtts_w8a8_fp8_gemm_strips(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx,
+                              const uint8_t* qws, int64_t n, const float* sw, const void* bias, void* y, int out_dtype,
+                              int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a8_fp8_gemm_strips: negative size");
+  QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "w8a8_fp8_gemm_strips: size too large");
+  QTTS_REQUIRE(dtype_ok(out_dtype), "w8a8_fp8_gemm_strips: bad dtype code");
+  QTTS_REQUIRE(algo_ok(algo), "w8a8_fp8_gemm_strips: bad algo %d", algo);
+  QTTS_REQUIRE(ldqx >= k && ldy >= n, "w8a8_fp8_gemm_strips: leading dimension smaller than the row");
+  QTTS_REQUIRE(ws_bytes >= 0, "w8a8_fp8_gemm_strips: negative workspace size");
+  if (m == 0 || n == 0) return QTTS_OK;
+  QTTS_REQUIRE(qx && sx && qws && sw && y, "w8a8_fp8_gemm_strips: null pointer");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_fp8_gemm(qx, sx, m, k, ldqx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y, out_dtype, ldy, algo,
+                              ws, ws_bytes, (hipStream_t)stream);
+}
+
+static int fp8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qw,
+                           int64_t n, int64_t ldqw, int layout, const float* sw, const void* bias, void* y,
+                           int64_t ldy, int div_mode, int algo, void* ws, int64_t ws_bytes, void* stream) {
   QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "fp8_linear: negative size");
   QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "fp8_linear: size too large");
   QTTS_REQUIRE(dtype_ok(x_dtype), "fp8_linear: bad dtype code");
   QTTS_REQUIRE(div_ok(div_mode), "fp8_linear: bad div_mode %d", div_mode);
   QTTS_REQUIRE(algo_ok(algo), "fp8_linear: bad algo %d", algo);
-  QTTS_REQUIRE(ldx >= k && ldqw >= k && ldy >= n, "fp8_linear: leading dimension smaller than the row");
+  QTTS_REQUIRE(ldx >= k && (layout == qtts::kLayoutStrips || ldqw >= k) && ldy >= n,
+               "fp8_linear: leading dimension smaller than the row");
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(sw && y && (k == 0 || (x && qw)), "fp8_linear: null pointer");
   // Layout: the GEMM's own workspace (split-K counters first) from the start, the
@@ -201,15 +238,55 @@ int qtts_fp8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
   QTTS_REQUIRE(ws != nullptr, "fp8_linear: a workspace of %lld bytes is required",
                (long long)(qx_bytes + sx_bytes + gemm_ws));
   const int64_t tail = (ws_bytes - qx_bytes - sx_bytes) & ~(int64_t)255;
-  if (tail < 0)
+  if (ws_bytes < qx_bytes + sx_bytes)
     return qtts_set_error(QTTS_ERR_WORKSPACE, "fp8_linear: workspace of %lld bytes < %lld needed", (long long)ws_bytes,
                           (long long)(qx_bytes + sx_bytes + gemm_ws));
   QTTS_TRY(current_device_check());
   uint8_t* qx = (uint8_t*)ws + tail;
   float* sx = (float*)((char*)ws + tail + qx_bytes);
   QTTS_TRY(qtts_launch_quant_act_fp8(x, x_dtype, m, k, ldx, qx, sx, div_mode, (hipStream_t)stream));
-  return qtts_launch_fp8_gemm(qx, sx, m, k, k, qw, n, ldqw, sw, bias, y, x_dtype, ldy, algo, tail > 0 ? ws : nullptr,
-                              tail, (hipStream_t)stream);
+  return qtts_launch_fp8_gemm(qx, sx, m, k, k, qw, n, ldqw, layout, sw, bias, y, x_dtype, ldy, algo,
+                              tail > 0 ? ws : nullptr, tail, (hipStream_t)stream);
+}
+
+int qtts_fp8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qw, int64_t n,
+                    int64_t ldqw, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode, int algo,
+                    void* ws, int64_t ws_bytes, void* stream) {
+  return fp8_linear_impl(x, x_dtype, m, k, ldx, qw, n, ldqw, qtts::kLayoutRowMajor, sw, bias, y, ldy, div_mode, algo, ws,
+                         ws_bytes, stream);
+}
+
+int qtts_fp8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
+                           int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode, int algo,
+                           void* ws, int64_t ws_bytes, void* stream) {
+  return fp8_linear_impl(x, x_dtype, m, k, ldx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y, ldy, div_mode, algo, ws,
+                         ws_bytes, stream);
+}
+
+int64_t qtts_strip_bytes(int64_t n, int64_t k, int kind) {
+  if (n < 0 || k < 0 || (kind != QTTS_STRIP_INT8 && kind != QTTS_STRIP_FP8))
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "strip_bytes: bad arguments");
+  return qtts::strip_bytes(n, k, kind);
+}
+
+int qtts_to_strips(const void* src, int64_t n, int64_t k, int64_t ld_src, int kind, void* dst, void* stream) {
+  QTTS_REQUIRE(n >= 0 && k >= 0 && ld_src >= k, "to_strips: bad sizes");
+  QTTS_REQUIRE(kind == QTTS_STRIP_INT8 || kind == QTTS_STRIP_FP8, "to_strips: bad kind %d", kind);
+  if (n == 0 || k == 0) return QTTS_OK;
+  QTTS_REQUIRE(src && dst, "to_strips: null pointer");
+  QTTS_REQUIRE((uintptr_t)dst % 16 == 0, "to_strips: destination must be 16-byte aligned");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_to_strips(src, n, k, ld_src, dst, kind, (hipStream_t)stream);
+}
+
+int qtts_from_strips(const void* src, int64_t n, int64_t k, int kind, void* dst, int64_t ld_dst, void* stream) {
+  QTTS_REQUIRE(n >= 0 && k >= 0 && ld_dst >= k, "from_strips: bad sizes");
+  QTTS_REQUIRE(kind == QTTS_STRIP_INT8 || kind == QTTS_STRIP_FP8, "from_strips: bad kind %d", kind);
+  if (n == 0 || k == 0) return QTTS_OK;
+  QTTS_REQUIRE(src && dst, "from_strips: null pointer");
+  QTTS_REQUIRE((uintptr_t)src % 16 == 0, "from_strips: source must be 16-byte aligned");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_from_strips(src, n, k, dst, ld_dst, kind, (hipStream_t)stream);
 }
 
 }  // extern "C"

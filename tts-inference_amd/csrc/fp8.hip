@@ -12,20 +12,19 @@
 //  * tile (M > 16): LDS-tiled, BM x 128 x 128, 4 waves in 2x2, double-buffered.
 //  * generic: any alignment / K; correctness path.
 //
+// Weights come row-major [N, K] or in the strip layout of layout.h (128-byte
+// chunks: each lane's 32 bytes are two 1 KiB-contiguous wave loads).
+//
 // Epilogue order follows the reference: the fp32 accumulator is scaled by
 // sx[m] * sw[n] and rounded to the output dtype, then the bias is added in the
 // output dtype (fp8.py:79-89 add the bias after _scaled_mm returns).
 #include <algorithm>
 
 #include "common.h"
+#include "layout.h"
+#include "splitk.h"
 
 namespace qtts {
-
-__device__ __forceinline__ void fp8_decode_wg(int wg, int S, int& strip, int& split) {
-  const int group = wg / (8 * S), within = wg - group * 8 * S;
-  split = within >> 3;
-  strip = group * 8 + (within & 7);
-}
 
 template <typename OT>
 __device__ __forceinline__ void fp8_store(OT* __restrict__ y, int64_t ldy, int m, int n, float acc,
@@ -48,45 +47,90 @@ __device__ __forceinline__ float e4m3_decode(uint32_t c) {
 
 // ------------------------------------------------------------------------------------
 
-template <typename OT, int WAVES, int U>
+template <typename OT, int WAVES, int U, int LAYOUT>
 __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
-    const uint8_t* __restrict__ qx, const float* __restrict__ sx, int M, int K, int64_t ldqx,
-    const uint8_t* __restrict__ qw, int N, int64_t ldqw, const float* __restrict__ sw, const OT* __restrict__ bias,
+    const uint8_t* __restrict__ qx, const float* sx, int M, int K, int64_t ldqx,
+    const uint8_t* __restrict__ qw, int N, int64_t ldqw, const float* sw, const OT* bias,
     OT* __restrict__ y, int64_t ldy, float* __restrict__ part, unsigned* __restrict__ counters, int strips, int S,
     int cps) {
   __shared__ f32x4_t red[WAVES > 1 ? WAVES - 1 : 1][64];
   int strip, split;
-  fp8_decode_wg(blockIdx.x, S, strip, split);
+  decode_wg(blockIdx.x, S, strip, split);
   if (strip >= strips) return;
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // wave index through readfirstlane: provably uniform, so per-wave bounds stay scalar
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int n = strip * 16 + r;
   const bool n_ok = n < N, m_ok = r < M;
   const int nchunks = (K + 127) >> 7;
   const int c0 = split * cps, c1 = min(c0 + cps, nchunks);
-  const uint8_t* wp = qw + (int64_t)(n_ok ? n : 0) * ldqw + 32 * g;
+  const int cw = (c1 - c0 + WAVES - 1) / WAVES;
+  const int wc0 = c0 + wave * cw, wc1 = min(wc0 + cw, c1);
+  const uint8_t* wp;
+  int64_t wstride, whalf;
+  if constexpr (LAYOUT == kLayoutStrips) {
+    wp = qw + (int64_t)strip * nchunks * 2048 + lane * 16;
+    wstride = 2048;
+    whalf = 1024;
+  } else {
+    wp = qw + (int64_t)(n_ok ? n : 0) * ldqw + 32 * g;
+    wstride = 128;
+    whalf = 16;
+  }
   const uint8_t* xp = qx + (int64_t)(m_ok ? r : 0) * ldqx + 32 * g;
   const i32x4_t zero = {0, 0, 0, 0};
 
-  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c = c0 + wave; c < c1; c += WAVES * U) {
-    i32x4_t w0[U], w1[U], x0[U], x1[U];
+  // A group of U chunks is issued in full before any of it is consumed.
+  i32x4_t w0[U], w1[U], x0[U], x1[U];
+  auto issue = [&](int c) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const int cc = c + u * WAVES;
-      const bool ok = cc < c1 && cc * 128 + 32 * g < K;
-      w0[u] = (ok && n_ok) ? *(const i32x4_t*)(wp + (int64_t)cc * 128) : zero;
-      w1[u] = (ok && n_ok) ? *(const i32x4_t*)(wp + (int64_t)cc * 128 + 16) : zero;
+      const int cc = c + u;
+      const bool live = cc < wc1;
+      const bool ok = live && cc * 128 + 32 * g < K;
+      const bool wok = LAYOUT == kLayoutStrips ? live : (ok && n_ok);
+      w0[u] = wok ? *(const i32x4_t*)(wp + (int64_t)cc * wstride) : zero;
+      w1[u] = wok ? *(const i32x4_t*)(wp + (int64_t)cc * wstride + whalf) : zero;
       x0[u] = (ok && m_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * 128) : zero;
       x1[u] = (ok && m_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * 128 + 16) : zero;
     }
+  };
+  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto consume = [&](int c) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const i32x8_t a = {w0[u][0], w0[u][1], w0[u][2], w0[u][3], w1[u][0], w1[u][1], w1[u][2], w1[u][3]};
-      const i32x8_t b = {x0[u][0], x0[u][1], x0[u][2], x0[u][3], x1[u][0], x1[u][1], x1[u][2], x1[u][3]};
-      acc = mma_fp8_16x16x128(a, b, acc);
+      if (c + u < wc1) {
+        const i32x8_t a = {w0[u][0], w0[u][1], w0[u][2], w0[u][3], w1[u][0], w1[u][1], w1[u][2], w1[u][3]};
+        const i32x8_t b = {x0[u][0], x0[u][1], x0[u][2], x0[u][3], x1[u][0], x1[u][1], x1[u][2], x1[u][3]};
+        acc = mma_fp8_16x16x128(a, b, acc);
+      }
     }
+  };
+  // Epilogue operands as raw bits, loaded unconditionally (see w8a16.hip).
+  uint32_t sxv, swv[4], bi[4];
+  auto issue_epilogue = [&]() {
+    sxv = *(const uint32_t*)(sx + min(r, M - 1));
+    const OT* bsrc = bias ? bias : y;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int nn = min(strip * 16 + 4 * g + i, N - 1);
+      swv[i] = *(const uint32_t*)(sw + nn);
+      if constexpr (sizeof(OT) == 2) bi[i] = *(const uint16_t*)(bsrc + nn);
+      else bi[i] = *(const uint32_t*)(bsrc + nn);
+    }
+  };
+  if (wc1 - wc0 <= U) {
+    issue(wc0);
+    issue_epilogue();
+    __builtin_amdgcn_sched_barrier(0);  // every load in flight before the first wait
+    consume(wc0);
+  } else {
+    for (int c = wc0; c < wc1; c += U) {
+      issue(c);
+      consume(c);
+    }
+    issue_epilogue();
   }
 
   if (WAVES > 1) {
@@ -98,31 +142,24 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
   }
 
   if (S > 1) {
-    float* pstrip = part + (int64_t)strip * S * 64 * 4;
-    *(f32x4_t*)(pstrip + ((int64_t)split * 64 + lane) * 4) = acc;
-    __threadfence();
-    unsigned prev = 0;
-    if (lane == 0) prev = atomicAdd(&counters[strip], 1u);
-    prev = __shfl(prev, 0, 64);
-    if (prev != (unsigned)(S - 1)) return;
-    __threadfence();
-    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-    for (int s = 0; s < S; ++s) {
-      const f32x4_t t = *(const f32x4_t*)(pstrip + ((int64_t)s * 64 + lane) * 4);
-      a0 += t[0];
-      a1 += t[1];
-      a2 += t[2];
-      a3 += t[3];
-    }
-    if (lane == 0) reset_counter(&counters[strip]);
-    acc = f32x4_t{a0, a1, a2, a3};
+    float a[4] = {acc[0], acc[1], acc[2], acc[3]};
+    if (!splitk_meet<4>(a, part + (int64_t)strip * S * 64 * 4, &counters[strip], S, split, lane, 64, nullptr))
+      return;
+    acc = f32x4_t{a[0], a[1], a[2], a[3]};
   }
 
   if (m_ok) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int nn = strip * 16 + 4 * g + i;
-      if (nn < N) fp8_store(y, ldy, r, nn, acc[i], sx, sw, bias);
+      if (nn < N) {
+        float v = round_through<OT>(acc[i] * __uint_as_float(sxv) * __uint_as_float(swv[i]));
+        if (bias) {
+          if constexpr (sizeof(OT) == 2) v += to_f32(OT{(uint16_t)bi[i]});
+          else v += __uint_as_float(bi[i]);
+        }
+        y[(int64_t)r * ldy + nn] = from_f32<OT>(v);
+      }
     }
   }
 }
@@ -131,7 +168,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
 
 constexpr int kF8BN = 128, kF8BK = 128, kF8LdsK = kF8BK + 16;  // bytes
 
-template <typename OT, int BM>
+template <typename OT, int BM, int LAYOUT>
 __global__ __launch_bounds__(256) void fp8_tile_kernel(
     const uint8_t* __restrict__ qx, const float* __restrict__ sx, int M, int K, int64_t ldqx,
     const uint8_t* __restrict__ qw, int N, int64_t ldqw, const float* __restrict__ sw, const OT* __restrict__ bias,
@@ -146,8 +183,9 @@ __global__ __launch_bounds__(256) void fp8_tile_kernel(
   __shared__ unsigned flag;
 
   int tile, split;
-  fp8_decode_wg(blockIdx.x, S, tile, split);
+  decode_wg(blockIdx.x, S, tile, split);
   if (tile >= mtiles * ntiles) return;
+  const int strips = (N + 15) / 16;
   const int mt = tile % mtiles, nt = tile / mtiles;
   const int m0 = mt * BM, n0 = nt * BN;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -167,9 +205,16 @@ __global__ __launch_bounds__(256) void fp8_tile_kernel(
     }
 #pragma unroll
     for (int l = 0; l < WL; ++l) {
-      const int id = tid + 256 * l, row = id >> 3, col = (id & 7) * 16;
-      const int n = n0 + row, k = kc * BK + col;
-      wr[l] = (n < N && k < K) ? *(const i32x4_t*)(qw + (int64_t)n * ldqw + k) : zero;
+      const int id = tid + 256 * l;
+      if constexpr (LAYOUT == kLayoutStrips) {
+        // 8 strips x one chunk = 8 blocks of 2 KiB; unit (id & 127) of block id / 128
+        const int s = n0 / 16 + (id >> 7);
+        wr[l] = s < strips ? *(const i32x4_t*)(qw + ((int64_t)s * nchunks + kc) * 2048 + (id & 127) * 16) : zero;
+      } else {
+        const int row = id >> 3, col = (id & 7) * 16;
+        const int n = n0 + row, k = kc * BK + col;
+        wr[l] = (n < N && k < K) ? *(const i32x4_t*)(qw + (int64_t)n * ldqw + k) : zero;
+      }
     }
   };
   auto store_stage = [&](int buf) {
@@ -181,7 +226,12 @@ __global__ __launch_bounds__(256) void fp8_tile_kernel(
 #pragma unroll
     for (int l = 0; l < WL; ++l) {
       const int id = tid + 256 * l;
-      *(i32x4_t*)&Bs[buf][id >> 3][(id & 7) * 16] = wr[l];
+      if constexpr (LAYOUT == kLayoutStrips) {
+        const int slot = id & 63, h = (id >> 6) & 1;
+        *(i32x4_t*)&Bs[buf][(id >> 7) * 16 + (slot & 15)][(slot >> 4) * 32 + h * 16] = wr[l];
+      } else {
+        *(i32x4_t*)&Bs[buf][id >> 3][(id & 7) * 16] = wr[l];
+      }
     }
   };
 
@@ -222,30 +272,21 @@ __global__ __launch_bounds__(256) void fp8_tile_kernel(
 
   if (S > 1) {
     constexpr int NV = TM * TN * 4;
-    float* ptile = part + (int64_t)tile * S * 256 * NV;
-    float* mine = ptile + ((int64_t)split * 256 + tid) * NV;
+    float a[NV];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) *(f32x4_t*)(mine + (i * TN + j) * 4) = acc[i][j];
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) flag = atomicAdd(&counters[tile], 1u);
-    __syncthreads();
-    if (flag != (unsigned)(S - 1)) return;
-    __threadfence();
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int t = 0; t < 4; ++t) a[(i * TN + j) * 4 + t] = acc[i][j][t];
+    if (!splitk_meet<NV>(a, part + (int64_t)tile * S * 256 * NV, &counters[tile], S, split, tid, 256, &flag))
+      return;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int s = 0; s < S; ++s) {
-      const float* src = ptile + ((int64_t)s * 256 + tid) * NV;
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-      for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] += *(const f32x4_t*)(src + (i * TN + j) * 4);
-    }
-    if (tid == 0) reset_counter(&counters[tile]);
+        for (int t = 0; t < 4; ++t) acc[i][j][t] = a[(i * TN + j) * 4 + t];
   }
 
 #pragma unroll
@@ -292,6 +333,8 @@ namespace {
 
 struct F8Cfg { int family, waves, S, cps, strips, bm, mtiles, ntiles; };
 
+constexpr int kF8CPW = 4;  // 128-byte chunks a wave keeps in flight at once
+
 F8Cfg fp8_cfg(int64_t m, int64_t n, int64_t k, int algo) {
   F8Cfg c{};
   c.family = algo & 0xff;
@@ -300,12 +343,16 @@ F8Cfg fp8_cfg(int64_t m, int64_t n, int64_t k, int algo) {
   if (c.family == QTTS_ALGO_SKINNY) {
     c.strips = (int)((n + 15) / 16);
     const int nchunks = std::max(1, (int)((k + 127) / 128));
-    c.waves = waves > 0 ? waves : 4;
-    int S = splits;
+    int W = waves, S = splits;
+    if (W <= 0) {
+      W = 1;
+      while (W < 16 && ((nchunks + W - 1) / W > kF8CPW || (int64_t)c.strips * W < 2048)) W *= 2;
+    }
     if (S <= 0) {
       S = 1;
-      while (c.strips * S * 2 <= 1024 && nchunks / (S * 2) >= 2 * c.waves) S *= 2;
+      while ((nchunks + S * W - 1) / (S * W) > kF8CPW) S *= 2;
     }
+    c.waves = W;
     S = std::max(1, std::min(S, nchunks));
     if (c.strips > kMaxSplitTiles) S = 1;
     c.cps = (nchunks + S - 1) / S;
@@ -347,52 +394,45 @@ int64_t qtts_fp8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
   return fp8_cfg_ws(fp8_cfg(m, n, k, algo));
 }
 
-template <typename OT>
-static int fp8_launch_typed(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const uint8_t* qw,
-                            int64_t n, int64_t ldqw, const float* sw, const OT* bias, OT* y, int64_t ldy, int algo,
-                            void* ws, int64_t ws_bytes, hipStream_t st) {
-  const bool aligned = ((uintptr_t)qx % 16 == 0) && ((uintptr_t)qw % 16 == 0) && (ldqx % 16 == 0) &&
-                       (ldqw % 16 == 0) && (k % 32 == 0) && k > 0;
-  if (!aligned) {
-    dim3 grid((unsigned)n, (unsigned)((m + 3) / 4));
-    fp8_generic_kernel<OT><<<grid, 64, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy);
-    return qtts_check_launch("w8a8_fp8_generic");
-  }
+template <typename OT, int LAYOUT>
+static int fp8_launch_fast(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const uint8_t* qw,
+                           int64_t n, int64_t ldqw, const float* sw, const OT* bias, OT* y, int64_t ldy, int algo,
+                           void* ws, int64_t ws_bytes, hipStream_t st) {
   F8Cfg c = fp8_cfg(m, n, k, algo);
   if (c.family == QTTS_ALGO_SKINNY && m > 16)
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "skinny fp8 kernel handles M <= 16, got M=%lld", (long long)m);
-  int64_t need = fp8_cfg_ws(c);
+  const int64_t need = fp8_cfg_ws(c);
   if (need > ws_bytes || (need > 0 && !ws)) {
     if ((algo >> 8) & 0xff)
       return qtts_set_error(QTTS_ERR_WORKSPACE, "w8a8 fp8 GEMM needs %lld workspace bytes, got %lld", (long long)need,
                             (long long)ws_bytes);
     c = fp8_cfg(m, n, k, c.family | (1 << 8) | (algo & 0xff0000));
-    need = 0;
   }
   unsigned* counters = (unsigned*)ws;
+  float* part = ws ? (float*)((char*)ws + kCounterBytes) : nullptr;
   if (c.family == QTTS_ALGO_SKINNY) {
-    float* part = c.S > 1 ? (float*)((char*)ws + kCounterBytes) : nullptr;
     const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8 * c.S;
-#define QTTS_F8S(W, U)                                                                                            \
-  fp8_skinny_kernel<OT, W, U><<<(unsigned)blocks, W * 64, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, \
-                                                                   bias, y, ldy, part, counters, c.strips, c.S, c.cps)
+#define QTTS_F8S(W, U)                                                                                             \
+  fp8_skinny_kernel<OT, W, U, LAYOUT><<<(unsigned)blocks, W * 64, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, \
+                                                                           ldqw, sw, bias, y, ldy, part, counters,   \
+                                                                           c.strips, c.S, c.cps)
     switch (c.waves) {
-      case 1: QTTS_F8S(1, 4); break;
-      case 2: QTTS_F8S(2, 4); break;
-      case 4: QTTS_F8S(4, 2); break;
-      case 8: QTTS_F8S(8, 2); break;
-      case 16: QTTS_F8S(16, 1); break;
+      case 1: QTTS_F8S(1, kF8CPW); break;
+      case 2: QTTS_F8S(2, kF8CPW); break;
+      case 4: QTTS_F8S(4, kF8CPW); break;
+      case 8: QTTS_F8S(8, kF8CPW); break;
+      case 16: QTTS_F8S(16, kF8CPW); break;
       default: return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8 skinny: waves must be 1, 2, 4, 8 or 16");
     }
 #undef QTTS_F8S
     return qtts_check_launch("w8a8_fp8_skinny");
   }
   const int64_t tiles = (int64_t)c.mtiles * c.ntiles;
-  float* part = c.S > 1 ? (float*)((char*)ws + kCounterBytes) : nullptr;
   const int64_t blocks = (tiles + 7) / 8 * 8 * c.S;
-#define QTTS_F8T(BM)                                                                                             \
-  fp8_tile_kernel<OT, BM><<<(unsigned)blocks, 256, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, \
-                                                            y, ldy, part, counters, c.mtiles, c.ntiles, c.S, c.cps)
+#define QTTS_F8T(BM)                                                                                           \
+  fp8_tile_kernel<OT, BM, LAYOUT><<<(unsigned)blocks, 256, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, \
+                                                                    bias, y, ldy, part, counters, c.mtiles, c.ntiles,  \
+                                                                    c.S, c.cps)
   if (c.bm == 32) QTTS_F8T(32);
   else if (c.bm == 64) QTTS_F8T(64);
   else QTTS_F8T(128);
@@ -400,15 +440,37 @@ static int fp8_launch_typed(const uint8_t* qx, const float* sx, int64_t m, int64
   return qtts_check_launch("w8a8_fp8_tile");
 }
 
+template <typename OT>
+static int fp8_launch_typed(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const uint8_t* qw,
+                            int64_t n, int64_t ldqw, int layout, const float* sw, const OT* bias, OT* y, int64_t ldy,
+                            int algo, void* ws, int64_t ws_bytes, hipStream_t st) {
+  const bool x_ok = ((uintptr_t)qx % 16 == 0) && (ldqx % 16 == 0) && (k % 32 == 0) && k > 0;
+  if (layout == kLayoutStrips) {
+    if (!x_ok)
+      return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
+                            "strip-layout fp8 weights need 16-byte aligned activation rows and K %% 32 == 0");
+    return fp8_launch_fast<OT, kLayoutStrips>(qx, sx, m, k, ldqx, qw, n, ldqw, sw, bias, y, ldy, algo, ws, ws_bytes,
+                                              st);
+  }
+  if (!x_ok || (uintptr_t)qw % 16 != 0 || ldqw % 16 != 0) {
+    dim3 grid((unsigned)n, (unsigned)((m + 3) / 4));
+    fp8_generic_kernel<OT><<<grid, 64, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy);
+    return qtts_check_launch("w8a8_fp8_generic");
+  }
+  return fp8_launch_fast<OT, kLayoutRowMajor>(qx, sx, m, k, ldqx, qw, n, ldqw, sw, bias, y, ldy, algo, ws, ws_bytes,
+                                              st);
+}
+
+// layout: kLayoutRowMajor (qw [n, k], row stride ldqw) or kLayoutStrips (ldqw ignored).
 int qtts_launch_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const uint8_t* qw,
-                         int64_t n, int64_t ldqw, const float* sw, const void* bias, void* y, int out_dtype,
-                         int64_t ldy, int algo, void* ws, int64_t ws_bytes, hipStream_t st) {
+                         int64_t n, int64_t ldqw, int layout, const float* sw, const void* bias, void* y,
+                         int out_dtype, int64_t ldy, int algo, void* ws, int64_t ws_bytes, hipStream_t st) {
   if (out_dtype == QTTS_BF16)
-    return fp8_launch_typed<bf16_t>(qx, sx, m, k, ldqx, qw, n, ldqw, sw, (const bf16_t*)bias, (bf16_t*)y, ldy, algo, ws,
-                                    ws_bytes, st);
+    return fp8_launch_typed<bf16_t>(qx, sx, m, k, ldqx, qw, n, ldqw, layout, sw, (const bf16_t*)bias, (bf16_t*)y, ldy,
+                                    algo, ws, ws_bytes, st);
   if (out_dtype == QTTS_F16)
-    return fp8_launch_typed<f16_t>(qx, sx, m, k, ldqx, qw, n, ldqw, sw, (const f16_t*)bias, (f16_t*)y, ldy, algo, ws,
-                                   ws_bytes, st);
-  return fp8_launch_typed<float>(qx, sx, m, k, ldqx, qw, n, ldqw, sw, (const float*)bias, (float*)y, ldy, algo, ws,
-                                 ws_bytes, st);
+    return fp8_launch_typed<f16_t>(qx, sx, m, k, ldqx, qw, n, ldqw, layout, sw, (const f16_t*)bias, (f16_t*)y, ldy,
+                                   algo, ws, ws_bytes, st);
+  return fp8_launch_typed<float>(qx, sx, m, k, ldqx, qw, n, ldqw, layout, sw, (const float*)bias, (float*)y, ldy, algo,
+                                 ws, ws_bytes, st);
 }

@@ -1,0 +1,79 @@
+// Split-K across workgroups without a second launch and without cache-wide fences.
+//
+// The S workgroups that share one output tile each publish their fp32 partial into
+// their own slot of the workspace and bump the tile's counter; the workgroup that
+// draws S-1 from the counter sums every slot in split order (so the result does not
+// depend on arrival order) and runs the epilogue, then resets the counter to zero.
+//
+// Ordering uses only per-access coherence: slots are written and read with
+// agent-scope atomic stores and loads (write-through / coherent loads, sc1), and an
+// explicit vmcnt(0) wait makes the slot stores complete before the counter update.
+// No buffer_wbl2 / buffer_inv, which write back or invalidate a whole L2 and cost
+// more than the split saves.  decode_wg additionally places all splits of a tile on
+// the same XCD, so every access of one meeting goes through one L2.
+#pragma once
+
+#include "common.h"
+
+namespace qtts {
+
+// Workgroup id -> (tile, split): all splits of a tile share wg % 8, i.e. run on the
+// same XCD (the dispatcher deals consecutive workgroups to the 8 XCDs round-robin).
+__device__ __forceinline__ void decode_wg(int wg, int S, int& tile, int& split) {
+  const int group = wg / (8 * S), within = wg - group * 8 * S;
+  split = within >> 3;
+  tile = group * 8 + (within & 7);
+}
+
+// Wait until every outstanding vector-memory operation of this wave has completed
+// (s_waitcnt vmcnt(0); expcnt and lgkmcnt left at their maxima).  The signal fences
+// keep the compiler from moving memory operations across the wait.
+__device__ __forceinline__ void wait_vmem() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// One meeting.  `slots` points at the tile's S slots of nthreads * NV floats each;
+// every participating thread calls this with its NV accumulator values.  Returns
+// true in the last-arriving workgroup, whose threads then hold the full sums.
+// `flag` is a __shared__ word (used when nthreads > 64).
+template <int NV>
+__device__ __forceinline__ bool splitk_meet(float (&acc)[NV], float* __restrict__ slots,
+                                            unsigned* __restrict__ counter, int S, int split, int tid,
+                                            int nthreads, unsigned* flag) {
+  float* mine = slots + ((int64_t)split * nthreads + tid) * NV;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) store_coherent(mine + v, acc[v]);
+  wait_vmem();
+  unsigned prev = 0;
+  if (nthreads > 64) {
+    __syncthreads();  // every wave's stores have completed (each waited above)
+    if (tid == 0) *flag = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    prev = *flag;
+  } else {
+    if (tid == 0) prev = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    prev = __shfl(prev, 0, 64);
+  }
+  if (prev != (unsigned)(S - 1)) return false;
+#pragma unroll
+  for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
+  for (int s = 0; s < S; ++s) {
+    const float* src = slots + ((int64_t)s * nthreads + tid) * NV;
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc[v] += load_coherent(src + v);
+  }
+  if (tid == 0) reset_counter(counter);
+  return true;
+}
+
+}  // namespace qtts

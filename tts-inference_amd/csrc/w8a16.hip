@@ -1,79 +1,65 @@
 // int8 weight-only (W8A16) GEMM for gfx950: y = x @ (q * scale)^T + bias.
 //
 // Replaces the Triton kernel _w8_gemm_kernel (qtts/quant/kernels.py:89-135) with
-// three hand-written kernels:
+// three hand-written kernels.  Weights come either row-major [N, K] (the
+// reference's buffer layout) or in the strip layout of layout.h, where every
+// wavefront load is one contiguous 1 KiB; the quant methods store the latter.
 //
-//  * skinny (M <= 16, the decode rows): every wave owns a 16-row strip of q and a
-//    share of K.  A lane loads 16 contiguous weight bytes per 64-byte chunk (one
-//    128-bit load; a wave covers 16 rows x 64 B), turns them into bf16 in
-//    registers (int8 is exact in bf16), and feeds two v_mfma_f32_16x16x32_bf16 with
-//    the activations as the 16-column B operand (rows >= M are zero).  Waves of a
-//    workgroup split K and meet in LDS; workgroups may split K further and meet
-//    through a workspace, where the last-arriving workgroup of a strip sums the
-//    partials in split order and runs the epilogue (no second launch).
+//  * skinny (M <= 16, decode rows): a workgroup owns a 16-row strip of q and a K
+//    range; its waves split that range into contiguous runs.  Per 64-column chunk a
+//    lane loads 16 weight bytes (one 128-bit load), converts them to bf16 in
+//    registers (int8 is exact in bf16) and issues two v_mfma_f32_16x16x32_bf16 with
+//    the activations as the 16-column B operand (rows >= M are zero).  A wave
+//    issues all loads of its share (up to 8 chunks) before consuming any, and the
+//    epilogue's scale and bias are fetched first, so a call costs one memory round
+//    trip.  Waves meet in LDS; workgroups that split K further meet through the
+//    workspace (splitk.h) with no second launch.
 //  * tile (M > 16, prefill rows): LDS-tiled bf16 MFMA GEMM, BM x 128 x 64 tiles,
-//    4 waves in 2x2, double-buffered LDS, the weight tile dequantized to bf16 on
+//    4 waves in 2x2, double-buffered LDS; the weight tile is dequantized to bf16 on
 //    its way into LDS.
-//  * generic: any dtype (fp32 activations included) and any alignment; one wave
-//    per output column, lanes stride K.  Correctness path for odd shapes.
+//  * generic: any dtype (fp32 activations included) and any alignment; one wave per
+//    output column, lanes stride K.  Correctness path for odd shapes (row-major only).
 //
-// Numerics match the reference kernel's order of operations: products of the
-// activation and the exact int8 weight accumulate in fp32, then the fp32 sum is
-// multiplied by f32(scale[n]), f32(bias[n]) is added, and the result is rounded
-// to the activation dtype once (qtts/quant/kernels.py:113-135).
+// Numerics follow the reference kernel: products of the activation and the exact
+// int8 weight accumulate in fp32, the fp32 sum is multiplied by f32(scale[n]),
+// f32(bias[n]) is added, and the result is rounded once to the activation dtype
+// (qtts/quant/kernels.py:113-135).
 #include <algorithm>
 #include <type_traits>
 
 #include "common.h"
+#include "layout.h"
+#include "splitk.h"
 
 namespace qtts {
 
-// Workgroup id -> (strip, split) such that all splits of one strip share
-// wg % 8, i.e. run on the same XCD (the dispatcher deals workgroups to the 8
-// XCDs round-robin), so their partials meet in one L2.
-__device__ __forceinline__ void decode_wg(int wg, int S, int& strip, int& split) {
-  const int group = wg / (8 * S), within = wg - group * 8 * S;
-  split = within >> 3;
-  strip = group * 8 + (within & 7);
+// Raw element bits, zero-extended to 32: a load whose value is not needed until the
+// epilogue, with no conversion the compiler could schedule (and wait for) early.
+// The load is a relaxed atomic (workgroup scope: an ordinary cached load in the
+// ISA) because compilers do not sink atomic loads towards their use; a plain load
+// of an epilogue-only value gets moved to the end of the kernel, where its latency
+// becomes a second round trip.
+template <typename T> __device__ __forceinline__ uint32_t load_bits(const T* p) {
+  if constexpr (sizeof(T) == 2)
+    return __hip_atomic_load((uint16_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else
+    return __hip_atomic_load((uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
+  if constexpr (std::is_same<T, float>::value) return __uint_as_float(b);
+  else return to_f32(T{(uint16_t)b});
 }
 
-// Split-K meeting point.  Each workgroup stores its partial (`nv` floats per
-// participating thread) into its slot, then bumps the strip's counter; the last
-// arrival reads every slot back in split order.  The counter is reset by the
-// last arrival, so the workspace stays zero between calls.
-template <int NV>
-__device__ __forceinline__ bool splitk_arrive(float (&acc)[NV], float* __restrict__ part, unsigned* __restrict__ counter,
-                                              int S, int split, int tid, int nthreads, unsigned* flag_lds) {
-  float* mine = part + ((int64_t)split * nthreads + tid) * NV;
-#pragma unroll
-  for (int v = 0; v < NV; v += 4) *(f32x4_t*)(mine + v) = f32x4_t{acc[v], acc[v + 1], acc[v + 2], acc[v + 3]};
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) *flag_lds = atomicAdd(counter, 1u);
-  __syncthreads();
-  if (*flag_lds != (unsigned)(S - 1)) return false;
-  __threadfence();
-#pragma unroll
-  for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
-  for (int s = 0; s < S; ++s) {
-    const float* src = part + ((int64_t)s * nthreads + tid) * NV;
-#pragma unroll
-    for (int v = 0; v < NV; v += 4) {
-      f32x4_t t = *(const f32x4_t*)(src + v);
-      acc[v] += t[0];
-      acc[v + 1] += t[1];
-      acc[v + 2] += t[2];
-      acc[v + 3] += t[3];
-    }
-  }
-  if (tid == 0) reset_counter(counter);
-  return true;
+__device__ __forceinline__ float load_scale(const void* s, int dt, int n) {
+  if (dt == QTTS_BF16) return to_f32(((const bf16_t*)s)[n]);
+  if (dt == QTTS_F16) return to_f32(((const f16_t*)s)[n]);
+  return ((const float*)s)[n];
 }
 
-template <typename XT, typename ST>
-__device__ __forceinline__ void store_out(XT* __restrict__ y, int64_t ldy, int m, int n, float acc,
-                                          const ST* __restrict__ scale, const XT* __restrict__ bias) {
-  float v = acc * to_f32(scale[n]);
+template <typename XT>
+__device__ __forceinline__ void store_out(XT* __restrict__ y, int64_t ldy, int m, int n, float acc, const void* scale,
+                                          int scale_dt, const XT* __restrict__ bias) {
+  float v = acc * load_scale(scale, scale_dt, n);
   if (bias) v += to_f32(bias[n]);
   y[(int64_t)m * ldy + n] = from_f32<XT>(v);
 }
@@ -82,79 +68,124 @@ __device__ __forceinline__ void store_out(XT* __restrict__ y, int64_t ldy, int m
 // skinny: M <= 16
 // ------------------------------------------------------------------------------------
 
-template <typename XT, typename ST, int WAVES, int U>
-__global__ __launch_bounds__(WAVES * 64) void w8a16_skinny_kernel(
+template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK>
+__global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ q, int N, int64_t ldq,
-    const ST* __restrict__ scale, const XT* __restrict__ bias, XT* __restrict__ y, int64_t ldy,
+    const ST* scale, const XT* bias, XT* __restrict__ y, int64_t ldy,
     float* __restrict__ part, unsigned* __restrict__ counters, int strips, int S, int cps) {
   typedef mfma16<XT> MM;
   typedef typename MM::vec V;
-  __shared__ f32x4_t red[WAVES > 1 ? WAVES - 1 : 1][64];
+  __shared__ f32x4_t red[W > 1 ? W - 1 : 1][64];
 
   int strip, split;
   decode_wg(blockIdx.x, S, strip, split);
   if (strip >= strips) return;
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // wave index through readfirstlane: provably uniform, so per-wave bounds stay scalar
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
   const int n = strip * 16 + r;
   const bool n_ok = n < N, m_ok = r < M;
   const int nchunks = (K + 63) >> 6;
-  const int c0 = split * cps;
-  const int c1 = min(c0 + cps, nchunks);
-  const int8_t* qp = q + (int64_t)(n_ok ? n : 0) * ldq + 16 * g;
+  const int c0 = split * cps, c1 = min(c0 + cps, nchunks);
+  const int cw = (c1 - c0 + W - 1) / W;  // <= CPW, guaranteed by the launcher
+  const int wc0 = c0 + wave * cw, wc1 = min(wc0 + cw, c1);
+
+  const int8_t* wp;
+  int64_t wstride;
+  if constexpr (LAYOUT == kLayoutStrips) {
+    wp = q + (int64_t)strip * nchunks * 1024 + lane * 16;
+    wstride = 1024;
+  } else {
+    wp = q + (int64_t)(n_ok ? n : 0) * ldq + 16 * g;
+    wstride = 64;
+  }
   const XT* xp = x + (int64_t)(m_ok ? r : 0) * ldx + 16 * g;
   const i32x4_t zero = {0, 0, 0, 0};
 
+  // A group of CPW chunks is issued in full before any of it is consumed.  With
+  // FULLK (K % 64 == 0, strip layout) the loads are branch-free: chunk indices past
+  // the wave's range are clamped to its last chunk (consume skips them), and rows of
+  // x past M read row 0 instead (they only feed D columns that are never stored).
+  i32x4_t w[CPW], xa[CPW], xb[CPW];
+  auto issue = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) {
+      if constexpr (FULLK) {
+        const int c = min(base + u, wc1 - 1);
+        w[u] = *(const i32x4_t*)(wp + (int64_t)c * wstride);
+        xa[u] = *(const i32x4_t*)(xp + (int64_t)c * 64);
+        xb[u] = *(const i32x4_t*)(xp + (int64_t)c * 64 + 8);
+      } else {
+        const int c = base + u;
+        const bool live = c < wc1;  // wave-uniform
+        const bool kin = c * 64 + 16 * g < K;
+        if (LAYOUT == kLayoutStrips) w[u] = live ? *(const i32x4_t*)(wp + (int64_t)c * wstride) : zero;
+        else w[u] = (live && n_ok && kin) ? *(const i32x4_t*)(wp + (int64_t)c * wstride) : zero;
+        xa[u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp + (int64_t)c * 64) : zero;
+        xb[u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp + (int64_t)c * 64 + 8) : zero;
+      }
+    }
+  };
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  for (int c = c0 + wave; c < c1; c += WAVES * U) {
-    i32x4_t wv[U], xa[U], xb[U];
+  auto consume = [&](int base) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int cc = c + u * WAVES;
-      const bool ok = cc < c1 && cc * 64 + 16 * g < K;
-      wv[u] = (ok && n_ok) ? *(const i32x4_t*)(qp + (int64_t)cc * 64) : zero;
-      xa[u] = (ok && m_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * 64) : zero;
-      xb[u] = (ok && m_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * 64 + 8) : zero;
+    for (int u = 0; u < CPW; ++u) {
+      if constexpr (FULLK) {
+        // Unconditional MFMAs on zeroed weights past the range: a branch here would
+        // let the compiler sink the loads into it, one round trip per chunk.
+        const bool live = base + u < wc1;
+        const i32x4_t wv = live ? w[u] : zero;
+        const V wlo = MM::from_i8((uint32_t)wv[0], (uint32_t)wv[1]);
+        const V whi = MM::from_i8((uint32_t)wv[2], (uint32_t)wv[3]);
+        acc = MM::mma(wlo, __builtin_bit_cast(V, xa[u]), acc);
+        acc = MM::mma(whi, __builtin_bit_cast(V, xb[u]), acc);
+      } else if (base + u < wc1) {
+        const V wlo = MM::from_i8((uint32_t)w[u][0], (uint32_t)w[u][1]);
+        const V whi = MM::from_i8((uint32_t)w[u][2], (uint32_t)w[u][3]);
+        acc = MM::mma(wlo, __builtin_bit_cast(V, xa[u]), acc);
+        acc = MM::mma(whi, __builtin_bit_cast(V, xb[u]), acc);
+      }
     }
+  };
+  // Epilogue operands: raw bits, loaded unconditionally (clamped index; y stands in
+  // for a missing bias), so nothing needs their values before the epilogue.
+  uint32_t sc[4], bi[4];
+  auto issue_epilogue = [&]() {
+    const XT* bsrc = bias ? bias : y;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const V wlo = MM::from_i8((uint32_t)wv[u][0], (uint32_t)wv[u][1]);
-      const V whi = MM::from_i8((uint32_t)wv[u][2], (uint32_t)wv[u][3]);
-      acc = MM::mma(wlo, __builtin_bit_cast(V, xa[u]), acc);
-      acc = MM::mma(whi, __builtin_bit_cast(V, xb[u]), acc);
+    for (int i = 0; i < 4; ++i) {
+      const int nn = min(strip * 16 + 4 * g + i, N - 1);
+      sc[i] = load_bits(scale + nn);
+      bi[i] = load_bits(bsrc + nn);
     }
+  };
+
+  // One group per wave, no loop: the host sizes the grid so a wave's share fits
+  // (a loop's back edge would make the compiler wait for every load in flight at
+  // its head).  Epilogue operands go first; the whole call is one round trip.
+  issue_epilogue();
+  if (wc0 < wc1) {  // wave-uniform: waves past the K range only reduce
+    issue(wc0);
+    // Keep the scheduler from interleaving loads with the MFMAs: every load must
+    // be in flight before the first wait.
+    __builtin_amdgcn_sched_barrier(0);
+    consume(wc0);
   }
 
-  if (WAVES > 1) {
+  if (W > 1) {
     if (wave > 0) red[wave - 1][lane] = acc;
     __syncthreads();
     if (wave > 0) return;
 #pragma unroll
-    for (int w = 0; w < WAVES - 1; ++w) acc += red[w][lane];
+    for (int w = 0; w < W - 1; ++w) acc += red[w][lane];
   }
 
   if (S > 1) {
     float a[4] = {acc[0], acc[1], acc[2], acc[3]};
-    // Only wave 0 is left; it is the whole "workgroup" of the meeting.
-    float* pstrip = part + (int64_t)strip * S * 64 * 4;
-    float* mine = pstrip + ((int64_t)split * 64 + lane) * 4;
-    *(f32x4_t*)mine = acc;
-    __threadfence();
-    unsigned prev = 0;
-    if (lane == 0) prev = atomicAdd(&counters[strip], 1u);
-    prev = __shfl(prev, 0, 64);
-    if (prev != (unsigned)(S - 1)) return;
-    __threadfence();
-    a[0] = a[1] = a[2] = a[3] = 0.0f;
-    for (int s = 0; s < S; ++s) {
-      const f32x4_t t = *(const f32x4_t*)(pstrip + ((int64_t)s * 64 + lane) * 4);
-      a[0] += t[0];
-      a[1] += t[1];
-      a[2] += t[2];
-      a[3] += t[3];
-    }
-    if (lane == 0) reset_counter(&counters[strip]);
+    // Only wave 0 is left: the meeting has 64 participants per workgroup.
+    if (!splitk_meet<4>(a, part + (int64_t)strip * S * 64 * 4, &counters[strip], S, split, lane, 64, nullptr))
+      return;
     acc = f32x4_t{a[0], a[1], a[2], a[3]};
   }
 
@@ -164,7 +195,11 @@ __global__ __launch_bounds__(WAVES * 64) void w8a16_skinny_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int nn = strip * 16 + 4 * g + i;
-      if (nn < N) store_out(y, ldy, r, nn, acc[i], scale, bias);
+      if (nn < N) {
+        float v = acc[i] * bits_to_f32<ST>(sc[i]);
+        if (bias) v += bits_to_f32<XT>(bi[i]);
+        y[(int64_t)r * ldy + nn] = from_f32<XT>(v);
+      }
     }
   }
 }
@@ -175,10 +210,10 @@ __global__ __launch_bounds__(WAVES * 64) void w8a16_skinny_kernel(
 
 constexpr int kTileBN = 128, kTileBK = 64, kTileLdsK = kTileBK + 8;  // padded LDS row, in elements
 
-template <typename XT, typename ST, int BM>
+template <typename XT, int BM, int LAYOUT>
 __global__ __launch_bounds__(256) void w8a16_tile_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ q, int N, int64_t ldq,
-    const ST* __restrict__ scale, const XT* __restrict__ bias, XT* __restrict__ y, int64_t ldy,
+    const void* __restrict__ scale, int scale_dt, const XT* __restrict__ bias, XT* __restrict__ y, int64_t ldy,
     float* __restrict__ part, unsigned* __restrict__ counters, int mtiles, int ntiles, int S, int cps) {
   typedef mfma16<XT> MM;
   typedef typename MM::vec V;
@@ -199,6 +234,7 @@ __global__ __launch_bounds__(256) void w8a16_tile_kernel(
   const int wm = wave >> 1, wn = wave & 1;
   const int c16 = lane & 15, g = lane >> 4;
   const int nchunks = (K + BK - 1) / BK;
+  const int strips = (N + 15) / 16;
   const int k0c = split * cps;
   const int k1c = min(k0c + cps, nchunks);
   const i32x4_t zero = {0, 0, 0, 0};
@@ -213,9 +249,16 @@ __global__ __launch_bounds__(256) void w8a16_tile_kernel(
     }
 #pragma unroll
     for (int l = 0; l < 2; ++l) {
-      const int id = tid + 256 * l, row = id >> 2, col = (id & 3) * 16;
-      const int n = n0 + row, k = kc * BK + col;
-      wr[l] = (n < N && k < K) ? *(const i32x4_t*)(q + (int64_t)n * ldq + k) : zero;
+      const int id = tid + 256 * l;
+      if constexpr (LAYOUT == kLayoutStrips) {
+        // 8 strips x one chunk = 8 contiguous 1 KiB blocks; slot (id & 63) of block id / 64
+        const int s = n0 / 16 + (id >> 6);
+        wr[l] = s < strips ? *(const i32x4_t*)(q + ((int64_t)s * nchunks + kc) * 1024 + (id & 63) * 16) : zero;
+      } else {
+        const int row = id >> 2, col = (id & 3) * 16;
+        const int n = n0 + row, k = kc * BK + col;
+        wr[l] = (n < N && k < K) ? *(const i32x4_t*)(q + (int64_t)n * ldq + k) : zero;
+      }
     }
   };
   auto store_stage = [&](int buf) {
@@ -226,7 +269,15 @@ __global__ __launch_bounds__(256) void w8a16_tile_kernel(
     }
 #pragma unroll
     for (int l = 0; l < 2; ++l) {
-      const int id = tid + 256 * l, row = id >> 2, col = (id & 3) * 16;
+      const int id = tid + 256 * l;
+      int row, col;
+      if constexpr (LAYOUT == kLayoutStrips) {
+        row = (id >> 6) * 16 + (id & 15);
+        col = ((id & 63) >> 4) * 16;
+      } else {
+        row = id >> 2;
+        col = (id & 3) * 16;
+      }
       const V lo = MM::from_i8((uint32_t)wr[l][0], (uint32_t)wr[l][1]);
       const V hi = MM::from_i8((uint32_t)wr[l][2], (uint32_t)wr[l][3]);
       *(V*)&Bs[buf][row][col] = lo;
@@ -265,15 +316,16 @@ __global__ __launch_bounds__(256) void w8a16_tile_kernel(
   }
 
   if (S > 1) {
-    float a[TM * TN * 4];
+    constexpr int NV = TM * TN * 4;
+    float a[NV];
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int t = 0; t < 4; ++t) a[(i * TN + j) * 4 + t] = acc[i][j][t];
-    float* ptile = part + (int64_t)tile * S * 256 * (TM * TN * 4);
-    if (!splitk_arrive<TM * TN * 4>(a, ptile, &counters[tile], S, split, tid, 256, &flag)) return;
+    if (!splitk_meet<NV>(a, part + (int64_t)tile * S * 256 * NV, &counters[tile], S, split, tid, 256, &flag))
+      return;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -293,21 +345,21 @@ __global__ __launch_bounds__(256) void w8a16_tile_kernel(
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
         const int m = m0 + wm * (BM / 2) + i * 16 + 4 * g + t;
-        if (m < M) store_out(y, ldy, m, n, acc[i][j][t], scale, bias);
+        if (m < M) store_out(y, ldy, m, n, acc[i][j][t], scale, scale_dt, bias);
       }
     }
 }
 
 // ------------------------------------------------------------------------------------
-// generic: any dtype, any alignment
+// generic: any dtype, any alignment, row-major weights
 // ------------------------------------------------------------------------------------
 
 constexpr int kGenericRows = 4;
 
-template <typename XT, typename ST>
+template <typename XT>
 __global__ __launch_bounds__(64) void w8a16_generic_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ q, int N, int64_t ldq,
-    const ST* __restrict__ scale, const XT* __restrict__ bias, XT* __restrict__ y, int64_t ldy) {
+    const void* __restrict__ scale, int scale_dt, const XT* __restrict__ bias, XT* __restrict__ y, int64_t ldy) {
   const int n = blockIdx.x, m0 = blockIdx.y * kGenericRows, lane = threadIdx.x;
   float acc[kGenericRows] = {0.0f, 0.0f, 0.0f, 0.0f};
   const int8_t* qr = q + (int64_t)n * ldq;
@@ -320,7 +372,7 @@ __global__ __launch_bounds__(64) void w8a16_generic_kernel(
 #pragma unroll
   for (int i = 0; i < kGenericRows; ++i) {
     const float s = wave_sum(acc[i]);
-    if (lane == 0 && m0 + i < M) store_out(y, ldy, m0 + i, n, s, scale, bias);
+    if (lane == 0 && m0 + i < M) store_out(y, ldy, m0 + i, n, s, scale, scale_dt, bias);
   }
 }
 
@@ -335,22 +387,32 @@ namespace {
 struct SkinnyCfg { int waves, S, cps, strips; };
 struct TileCfg { int bm, S, cps, mtiles, ntiles; };
 
-SkinnyCfg skinny_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int waves_req) {
+constexpr int kSkinnyCPW = 4;    // chunks a wave keeps in flight at once
+constexpr int kSkinnyCPW16 = 4;  // the same for 1024-thread workgroups (128 VGPRs per lane)
+
+SkinnyCfg skinny_cfg(int64_t n, int64_t k, int splits_req, int waves_req) {
   SkinnyCfg c;
   c.strips = (int)((n + 15) / 16);
   const int nchunks = std::max(1, (int)((k + 63) / 64));
-  c.waves = waves_req > 0 ? waves_req : 4;
-  int S = splits_req;
-  if (S <= 0) {
-    // Aim for >= 1024 workgroups (4 per CU) while keeping >= 2 chunks per wave.
-    S = 1;
-    while (c.strips * S * 2 <= 1024 && nchunks / (S * 2) >= 2 * c.waves) S *= 2;
+  int W = waves_req, S = splits_req;
+  if (W <= 0) {
+    // Enough waves to cover the chip (>= 2048 in all) while each wave's share of a
+    // strip fits one in-flight group of kSkinnyCPW chunks.
+    W = 1;
+    while (W < 16 && ((nchunks + W - 1) / W > kSkinnyCPW || (int64_t)c.strips * W < 2048)) W *= 2;
   }
+  if (S <= 0) {
+    S = 1;
+    while ((nchunks + S * W - 1) / (S * W) > kSkinnyCPW) S *= 2;
+  }
+  c.waves = W;
+  const int cpw = W == 16 ? kSkinnyCPW16 : kSkinnyCPW;
+  // The kernel runs one group of cpw chunks per wave: raise S until a wave's share
+  // fits (a requested split count is a minimum).
+  S = std::max(S, (nchunks + W * cpw - 1) / (W * cpw));
   S = std::max(1, std::min(S, nchunks));
-  if (c.strips > kMaxSplitTiles) S = 1;
   c.cps = (nchunks + S - 1) / S;
   c.S = (nchunks + c.cps - 1) / c.cps;
-  (void)m;
   return c;
 }
 
@@ -373,10 +435,7 @@ TileCfg tile_cfg(int64_t m, int64_t n, int64_t k, int splits_req) {
   return c;
 }
 
-int64_t skinny_ws(const SkinnyCfg& c) {
-  if (c.S <= 1) return 0;
-  return kCounterBytes + (int64_t)c.strips * c.S * 64 * 4 * 4;
-}
+int64_t skinny_ws(const SkinnyCfg& c) { return c.S <= 1 ? 0 : kCounterBytes + (int64_t)c.strips * c.S * 64 * 4 * 4; }
 
 int64_t tile_ws(const TileCfg& c) {
   if (c.S <= 1) return 0;
@@ -391,53 +450,64 @@ bool grid_ok(int64_t blocks) { return blocks > 0 && blocks < (int64_t)1 << 31; }
 int64_t qtts_w8a16_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
   const int family = algo & 0xff, splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff;
   int64_t ws = 0;
-  if (family == QTTS_ALGO_SKINNY || family == QTTS_ALGO_AUTO) ws = std::max(ws, skinny_ws(skinny_cfg(std::min<int64_t>(m, 16), n, k, splits, waves)));
+  if (family == QTTS_ALGO_SKINNY || family == QTTS_ALGO_AUTO) ws = std::max(ws, skinny_ws(skinny_cfg(n, k, splits, waves)));
   if (family == QTTS_ALGO_TILE || (family == QTTS_ALGO_AUTO && m > 16)) ws = std::max(ws, tile_ws(tile_cfg(m, n, k, splits)));
   return ws;
 }
 
-template <typename XT, typename ST>
-static int launch_typed(const XT* x, int64_t m, int64_t k, int64_t ldx, const int8_t* q, int64_t n, int64_t ldq,
-                        const ST* scale, const XT* bias, XT* y, int64_t ldy, int algo, void* ws, int64_t ws_bytes,
-                        hipStream_t st, bool fast_ok) {
+template <typename XT, int LAYOUT>
+static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int8_t* q, int64_t n, int64_t ldq,
+                       const void* scale, int sdt, const XT* bias, XT* y, int64_t ldy, int algo, void* ws,
+                       int64_t ws_bytes, hipStream_t st) {
   int family = algo & 0xff;
   const int splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff;
   if (family == QTTS_ALGO_AUTO) family = m <= 16 ? QTTS_ALGO_SKINNY : QTTS_ALGO_TILE;
   if (family == QTTS_ALGO_SKINNY && m > 16)
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "skinny W8A16 kernel handles M <= 16, got M=%lld", (long long)m);
-  if (std::is_same<XT, float>::value || !fast_ok) {
-    dim3 grid((unsigned)n, (unsigned)((m + kGenericRows - 1) / kGenericRows));
-    w8a16_generic_kernel<XT, ST><<<grid, 64, 0, st>>>(x, (int)m, (int)k, ldx, q, (int)n, ldq, scale, bias, y, ldy);
-    return qtts_check_launch("w8a16_generic");
-  }
-  if constexpr (!std::is_same<XT, float>::value) {
+  unsigned* counters = (unsigned*)ws;
+  float* part = ws ? (float*)((char*)ws + kCounterBytes) : nullptr;
   if (family == QTTS_ALGO_SKINNY) {
-    SkinnyCfg c = skinny_cfg(m, n, k, splits, waves);
+    SkinnyCfg c = skinny_cfg(n, k, splits, waves);
     const int64_t need = skinny_ws(c);
     if (need > ws_bytes || (need > 0 && !ws)) {
       if (splits > 0)
         return qtts_set_error(QTTS_ERR_WORKSPACE, "w8a16 skinny with %d splits needs %lld workspace bytes, got %lld",
                               c.S, (long long)need, (long long)ws_bytes);
-      c = skinny_cfg(m, n, k, 1, waves);  // no workspace: one split
+      c = skinny_cfg(n, k, 1, waves);  // no room for a split: one workgroup per strip
     }
-    unsigned* counters = (unsigned*)ws;
-    float* part = c.S > 1 ? (float*)((char*)ws + kCounterBytes) : nullptr;
+    if (c.S > 1 && c.strips > kMaxSplitTiles)
+      return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: N=%lld with K=%lld needs a split-K over more "
+                            "output strips than the workspace counter block holds", (long long)n, (long long)k);
     const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8 * c.S;
     if (!grid_ok(blocks)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16: N too large");
-#define QTTS_SKINNY(W, U)                                                                                \
-  w8a16_skinny_kernel<XT, ST, W, U><<<(unsigned)blocks, W * 64, 0, st>>>(x, (int)m, (int)k, ldx, q, (int)n, ldq, \
-                                                                         scale, bias, y, ldy, part, counters,  \
-                                                                         c.strips, c.S, c.cps)
+#define QTTS_SKINNY_T(ST, W, CPW)                                                                             \
+  do {                                                                                                        \
+    if (LAYOUT == kLayoutStrips && k % 64 == 0)                                                               \
+      w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, true><<<(unsigned)blocks, W * 64, 0, st>>>(                 \
+          x, (int)m, (int)k, ldx, q, (int)n, ldq, (const ST*)scale, bias, y, ldy, part, counters, c.strips, c.S, \
+          c.cps);                                                                                             \
+    else                                                                                                      \
+      w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, false><<<(unsigned)blocks, W * 64, 0, st>>>(                \
+          x, (int)m, (int)k, ldx, q, (int)n, ldq, (const ST*)scale, bias, y, ldy, part, counters, c.strips, c.S, \
+          c.cps);                                                                                             \
+  } while (0)
+#define QTTS_SKINNY(W, CPW)                                         \
+  do {                                                              \
+    if (sdt == QTTS_BF16) QTTS_SKINNY_T(bf16_t, W, CPW);            \
+    else if (sdt == QTTS_F16) QTTS_SKINNY_T(f16_t, W, CPW);         \
+    else QTTS_SKINNY_T(float, W, CPW);                              \
+  } while (0)
     switch (c.waves) {
-      case 1: QTTS_SKINNY(1, 4); break;
-      case 2: QTTS_SKINNY(2, 4); break;
-      case 4: QTTS_SKINNY(4, 4); break;
-      case 8: QTTS_SKINNY(8, 2); break;
-      case 16: QTTS_SKINNY(16, 1); break;
+      case 1: QTTS_SKINNY(1, kSkinnyCPW); break;
+      case 2: QTTS_SKINNY(2, kSkinnyCPW); break;
+      case 4: QTTS_SKINNY(4, kSkinnyCPW); break;
+      case 8: QTTS_SKINNY(8, kSkinnyCPW); break;
+      case 16: QTTS_SKINNY(16, kSkinnyCPW16); break;
       default:
         return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: waves per workgroup must be 1, 2, 4, 8 or 16");
     }
 #undef QTTS_SKINNY
+#undef QTTS_SKINNY_T
     return qtts_check_launch("w8a16_skinny");
   }
   TileCfg c = tile_cfg(m, n, k, splits);
@@ -449,41 +519,52 @@ static int launch_typed(const XT* x, int64_t m, int64_t k, int64_t ldx, const in
     c = tile_cfg(m, n, k, 1);
   }
   const int64_t tiles = (int64_t)c.mtiles * c.ntiles;
-  unsigned* counters = (unsigned*)ws;
-  float* part = c.S > 1 ? (float*)((char*)ws + kCounterBytes) : nullptr;
   const int64_t blocks = (tiles + 7) / 8 * 8 * c.S;
   if (!grid_ok(blocks)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16: problem too large");
-#define QTTS_TILE(BM)                                                                                       \
-  w8a16_tile_kernel<XT, ST, BM><<<(unsigned)blocks, 256, 0, st>>>(x, (int)m, (int)k, ldx, q, (int)n, ldq, scale, \
-                                                                  bias, y, ldy, part, counters, c.mtiles,      \
-                                                                  c.ntiles, c.S, c.cps)
+#define QTTS_TILE(BM)                                                                                          \
+  w8a16_tile_kernel<XT, BM, LAYOUT><<<(unsigned)blocks, 256, 0, st>>>(x, (int)m, (int)k, ldx, q, (int)n, ldq, scale, \
+                                                                      sdt, bias, y, ldy, part, counters, c.mtiles, \
+                                                                      c.ntiles, c.S, c.cps)
   if (c.bm == 32) QTTS_TILE(32);
   else if (c.bm == 64) QTTS_TILE(64);
   else QTTS_TILE(128);
 #undef QTTS_TILE
   return qtts_check_launch("w8a16_tile");
-  }
-  return QTTS_OK;
 }
 
+// layout: kLayoutRowMajor (q [n, k], row stride ldq) or kLayoutStrips (ldq ignored).
 int qtts_launch_w8a16(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* q, int64_t n,
-                      int64_t ldq, const void* scale, int scale_dtype, const void* bias, void* y, int64_t ldy,
-                      int algo, void* ws, int64_t ws_bytes, hipStream_t st) {
-  const bool aligned = ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 16 == 0) && (ldx % 8 == 0) && (ldq % 16 == 0) &&
-                       (k % 16 == 0) && k > 0;
-#define QTTS_DISPATCH_SCALE(XT, FAST)                                                                          \
-  do {                                                                                                         \
-    if (scale_dtype == QTTS_F32)                                                                               \
-      return launch_typed<XT, float>((const XT*)x, m, k, ldx, q, n, ldq, (const float*)scale, (const XT*)bias, \
-                                     (XT*)y, ldy, algo, ws, ws_bytes, st, FAST);                               \
-    if (scale_dtype == QTTS_BF16)                                                                              \
-      return launch_typed<XT, bf16_t>((const XT*)x, m, k, ldx, q, n, ldq, (const bf16_t*)scale,               \
-                                      (const XT*)bias, (XT*)y, ldy, algo, ws, ws_bytes, st, FAST);            \
-    return launch_typed<XT, f16_t>((const XT*)x, m, k, ldx, q, n, ldq, (const f16_t*)scale, (const XT*)bias,   \
-                                   (XT*)y, ldy, algo, ws, ws_bytes, st, FAST);                                 \
-  } while (0)
-  if (x_dtype == QTTS_BF16) QTTS_DISPATCH_SCALE(bf16_t, aligned);
-  if (x_dtype == QTTS_F16) QTTS_DISPATCH_SCALE(f16_t, aligned);
-  QTTS_DISPATCH_SCALE(float, false);
-#undef QTTS_DISPATCH_SCALE
+                      int64_t ldq, int layout, const void* scale, int scale_dtype, const void* bias, void* y,
+                      int64_t ldy, int algo, void* ws, int64_t ws_bytes, hipStream_t st) {
+  const bool x_ok = ((uintptr_t)x % 16 == 0) && (ldx % 8 == 0) && k > 0 && (k % 16 == 0);
+  const bool q_ok = layout == kLayoutStrips || (((uintptr_t)q % 16 == 0) && (ldq % 16 == 0));
+  const bool fast = x_ok && q_ok && x_dtype != QTTS_F32;
+  if (!fast) {
+    if (layout == kLayoutStrips)
+      return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
+                            "strip-layout weights need bf16/fp16 activations with 16-byte aligned rows and K %% 16 == 0");
+    dim3 grid((unsigned)n, (unsigned)((m + kGenericRows - 1) / kGenericRows));
+    if (x_dtype == QTTS_BF16)
+      w8a16_generic_kernel<bf16_t><<<grid, 64, 0, st>>>((const bf16_t*)x, (int)m, (int)k, ldx, q, (int)n, ldq, scale,
+                                                        scale_dtype, (const bf16_t*)bias, (bf16_t*)y, ldy);
+    else if (x_dtype == QTTS_F16)
+      w8a16_generic_kernel<f16_t><<<grid, 64, 0, st>>>((const f16_t*)x, (int)m, (int)k, ldx, q, (int)n, ldq, scale,
+                                                       scale_dtype, (const f16_t*)bias, (f16_t*)y, ldy);
+    else
+      w8a16_generic_kernel<float><<<grid, 64, 0, st>>>((const float*)x, (int)m, (int)k, ldx, q, (int)n, ldq, scale,
+                                                       scale_dtype, (const float*)bias, (float*)y, ldy);
+    return qtts_check_launch("w8a16_generic");
+  }
+  if (x_dtype == QTTS_BF16) {
+    if (layout == kLayoutStrips)
+      return launch_fast<bf16_t, kLayoutStrips>((const bf16_t*)x, m, k, ldx, q, n, ldq, scale, scale_dtype,
+                                                (const bf16_t*)bias, (bf16_t*)y, ldy, algo, ws, ws_bytes, st);
+    return launch_fast<bf16_t, kLayoutRowMajor>((const bf16_t*)x, m, k, ldx, q, n, ldq, scale, scale_dtype,
+                                                (const bf16_t*)bias, (bf16_t*)y, ldy, algo, ws, ws_bytes, st);
+  }
+  if (layout == kLayoutStrips)
+    return launch_fast<f16_t, kLayoutStrips>((const f16_t*)x, m, k, ldx, q, n, ldq, scale, scale_dtype,
+                                             (const f16_t*)bias, (f16_t*)y, ldy, algo, ws, ws_bytes, st);
+  return launch_fast<f16_t, kLayoutRowMajor>((const f16_t*)x, m, k, ldx, q, n, ldq, scale, scale_dtype,
+                                             (const f16_t*)bias, (f16_t*)y, ldy, algo, ws, ws_bytes, st);
 }

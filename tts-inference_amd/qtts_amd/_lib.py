@@ -35,6 +35,8 @@ DIV_DEVICE, DIV_IEEE = 0, 1
 ALGO_AUTO, ALGO_SKINNY, ALGO_TILE = 0, 1, 2
 # qtts_op
 OP_W8A16, OP_W8A8_FP8, OP_FP8_LINEAR = 0, 1, 2
+# qtts_strip_kind
+STRIP_INT8, STRIP_FP8 = 0, 1
 
 EXPORTS = (
     "qtts_abi_version",
@@ -47,6 +49,12 @@ EXPORTS = (
     "qtts_quant_act_fp8_rows",
     "qtts_w8a8_fp8_gemm",
     "qtts_fp8_linear",
+    "qtts_strip_bytes",
+    "qtts_to_strips",
+    "qtts_from_strips",
+    "qtts_w8a16_gemm_strips",
+    "qtts_w8a8_fp8_gemm_strips",
+    "qtts_fp8_linear_strips",
 )
 
 
@@ -99,6 +107,18 @@ def load() -> ctypes.CDLL:
         L.qtts_w8a8_fp8_gemm.argtypes = [p, p, i64, i64, i64, p, i64, i64, p, p, p, i32, i64, i32, p, i64, p]
         L.qtts_fp8_linear.restype = i32
         L.qtts_fp8_linear.argtypes = [p, i32, i64, i64, i64, p, i64, i64, p, p, p, i64, i32, i32, p, i64, p]
+        L.qtts_strip_bytes.restype = i64
+        L.qtts_strip_bytes.argtypes = [i64, i64, i32]
+        L.qtts_to_strips.restype = i32
+        L.qtts_to_strips.argtypes = [p, i64, i64, i64, i32, p, p]
+        L.qtts_from_strips.restype = i32
+        L.qtts_from_strips.argtypes = [p, i64, i64, i32, p, i64, p]
+        L.qtts_w8a16_gemm_strips.restype = i32
+        L.qtts_w8a16_gemm_strips.argtypes = [p, i32, i64, i64, i64, p, i64, p, i32, p, p, i64, i32, p, i64, p]
+        L.qtts_w8a8_fp8_gemm_strips.restype = i32
+        L.qtts_w8a8_fp8_gemm_strips.argtypes = [p, p, i64, i64, i64, p, i64, p, p, p, i32, i64, i32, p, i64, p]
+        L.qtts_fp8_linear_strips.restype = i32
+        L.qtts_fp8_linear_strips.argtypes = [p, i32, i64, i64, i64, p, i64, p, p, p, i64, i32, i32, p, i64, p]
         version = L.qtts_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"libqtts_amd ABI version {version}, expected {ABI_VERSION}; rebuild it")

@@ -13,7 +13,8 @@ import threading
 import torch
 
 from . import _lib
-from ._lib import ALGO_AUTO, DIV_DEVICE, DIV_IEEE, OP_W8A16, OP_W8A8_FP8, algo_code  # noqa: F401
+from ._lib import (ALGO_AUTO, DIV_DEVICE, DIV_IEEE, OP_FP8_LINEAR, OP_W8A16, OP_W8A8_FP8,  # noqa: F401
+                   STRIP_FP8, STRIP_INT8, algo_code)
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
@@ -253,3 +254,105 @@ def fp8_linear(x: torch.Tensor, qw: torch.Tensor, sw: torch.Tensor, bias: torch.
     qx, sx = quant_act_fp8(x, div_mode)
     out = w8a8_fp8_gemm(qx, sx, qw, sw, bias, x.dtype, algo)
     return out.reshape(*shape[:-1], qw.shape[0])
+
+
+# ---- strip layout ----------------------------------------------------------------------
+# The GEMM kernels read weights fastest in the strip layout (include/qtts_amd.h): a
+# permutation of the packer's row-major bytes in which every wavefront load is one
+# contiguous 1 KiB.  The quant methods keep only this copy; from_strips recovers
+# the row-major bytes bit for bit.
+
+def strip_bytes(n: int, k: int, kind: int) -> int:
+    v = _lib.load().qtts_strip_bytes(n, k, kind)
+    if v < 0:
+        _lib.check(int(v), "strip_bytes")
+    return int(v)
+
+
+def to_strips(q: torch.Tensor, kind: int | None = None) -> torch.Tensor:
+    """Row-major ``[N, K]`` int8 / e4m3 weight -> strip layout (same dtype; ``[N, K]`` when no padding
+    is needed, else 1-D)."""
+    if q.dim() != 2:
+        raise ValueError("expected a 2-D weight")
+    if kind is None:
+        kind = STRIP_FP8 if q.dtype == torch.float8_e4m3fn else STRIP_INT8
+    dev = _require_cuda(q)
+    if q.stride(1) != 1:
+        q = q.contiguous()
+    n, k = q.shape
+    nbytes = strip_bytes(n, k, kind)
+    out = torch.empty(nbytes, dtype=q.dtype, device=dev)
+    st = _lib.load().qtts_to_strips(_ptr(q), n, k, q.stride(0), kind, _ptr(out), _stream(dev))
+    _lib.check(st, "to_strips")
+    return out.view(n, k) if nbytes == n * k else out
+
+
+def from_strips(qs: torch.Tensor, n: int, k: int, kind: int | None = None) -> torch.Tensor:
+    """Strip layout -> row-major ``[N, K]`` (the packer's bytes)."""
+    if kind is None:
+        kind = STRIP_FP8 if qs.dtype == torch.float8_e4m3fn else STRIP_INT8
+    dev = _require_cuda(qs)
+    out = torch.empty((n, k), dtype=qs.dtype, device=dev)
+    st = _lib.load().qtts_from_strips(_ptr(qs), n, k, kind, _ptr(out), k, _stream(dev))
+    _lib.check(st, "from_strips")
+    return out
+
+
+def w8a16_gemm_strips(x: torch.Tensor, qs: torch.Tensor, n: int, scale: torch.Tensor,
+                      bias: torch.Tensor | None = None, algo: int = ALGO_AUTO) -> torch.Tensor:
+    """``w8a16_gemm`` with the int8 weight in the strip layout (``n`` output channels)."""
+    shape = x.shape
+    a = _flatten(x)
+    rows, k = a.shape
+    if qs.dtype != torch.int8 or qs.numel() != strip_bytes(n, k, STRIP_INT8):
+        raise ValueError(f"weight is not an int8 strip-layout [{n}, {k}] buffer")
+    if scale.numel() != n:
+        raise ValueError(f"scale has {scale.numel()} entries for {n} output channels")
+    if bias is not None:
+        if bias.numel() != n:
+            raise ValueError(f"bias has {bias.numel()} entries for {n} output channels")
+        bias = bias.to(a.dtype).contiguous()
+    if a.data_ptr() % 16 or (rows > 1 and a.stride(0) % 8):
+        a = a.contiguous() if a.data_ptr() % 16 == 0 else a.clone()
+    dev = _require_cuda(a, qs, scale, bias)
+    scale = scale.contiguous()
+    out = torch.empty((rows, n), dtype=a.dtype, device=dev)
+    ws, ws_n = _ws_for(dev)
+    st = _lib.load().qtts_w8a16_gemm_strips(
+        _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else k, _ptr(qs), n, _ptr(scale),
+        dtype_code(scale.dtype), _ptr(bias), _ptr(out), n, algo, ws, ws_n, _stream(dev))
+    _lib.check(st, "w8a16_gemm_strips")
+    return out.reshape(*shape[:-1], n)
+
+
+def w8a8_fp8_gemm_strips(qx: torch.Tensor, sx: torch.Tensor, qws: torch.Tensor, n: int, sw: torch.Tensor,
+                         bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                         algo: int = ALGO_AUTO) -> torch.Tensor:
+    """``w8a8_fp8_gemm`` with the e4m3 weight in the strip layout."""
+    m, k = qx.shape
+    if qws.numel() != strip_bytes(n, k, STRIP_FP8):
+        raise ValueError(f"weight is not an e4m3 strip-layout [{n}, {k}] buffer")
+    if qx.stride(1) != 1:
+        qx = qx.contiguous()
+    sx = sx.reshape(-1).to(torch.float32).contiguous()
+    sw = sw.reshape(-1).to(torch.float32).contiguous()
+    if bias is not None:
+        bias = bias.to(out_dtype).contiguous()
+    dev = _require_cuda(qx, sx, qws, sw, bias)
+    out = torch.empty((m, n), dtype=out_dtype, device=dev)
+    ws, ws_n = _ws_for(dev)
+    st = _lib.load().qtts_w8a8_fp8_gemm_strips(
+        _ptr(qx), _ptr(sx), m, k, qx.stride(0) if m > 1 else k, _ptr(qws), n, _ptr(sw), _ptr(bias), _ptr(out),
+        dtype_code(out_dtype), n, algo, ws, ws_n, _stream(dev))
+    _lib.check(st, "w8a8_fp8_gemm_strips")
+    return out
+
+
+def fp8_linear_strips(x: torch.Tensor, qws: torch.Tensor, n: int, sw: torch.Tensor,
+                      bias: torch.Tensor | None = None, div_mode: int = DIV_DEVICE,
+                      algo: int = ALGO_AUTO) -> torch.Tensor:
+    """Fp8Method.apply (qtts/quant/fp8.py:72-89) with the e4m3 weight in the strip layout."""
+    shape = x.shape
+    qx, sx = quant_act_fp8(x, div_mode)
+    out = w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, bias, x.dtype, algo)
+    return out.reshape(*shape[:-1], n)

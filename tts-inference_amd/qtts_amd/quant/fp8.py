@@ -35,9 +35,16 @@ class Fp8Method(QuantMethodBase):
     def process_weights(self, layer) -> None:
         weight = layer.weight
         q, scale = quantize_weight_fp8(weight, self.div_mode)
-        # Same buffers as the reference: the [K, N] column-major view of the
-        # row-major [N, K] bytes, and the scale as [1, N] fp32.
-        layer.register_buffer("fp8_weight", q.t(), persistent=False)
+        # The reference keeps the [K, N] column-major view of the packed bytes for
+        # _scaled_mm; this backend keeps the MFMA-native strip layout of the same
+        # bytes instead (fp8_weight_rowmajor recovers them).  The scale is [1, N]
+        # fp32 as in the reference.
+        if layer.in_features % 32 == 0:
+            layer.register_buffer("fp8_weight", ops.to_strips(q, _lib.STRIP_FP8), persistent=False)
+            layer.fp8_layout = "strips"
+        else:  # the strip kernels need K % 32 == 0; keep the reference's [K, N] view
+            layer.register_buffer("fp8_weight", q.t(), persistent=False)
+            layer.fp8_layout = "rowmajor"
         layer.register_buffer("fp8_scale", scale.reshape(1, -1), persistent=False)
         ops.reserve_workspace(weight.device, max(
             ops.workspace_bytes(_lib.OP_W8A8_FP8, m, layer.out_features, layer.in_features) for m in (16, 64, 256)))
@@ -48,7 +55,17 @@ class Fp8Method(QuantMethodBase):
         return getattr(layer, "fp8_weight", None) is not None
 
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        if layer.fp8_layout == "strips":
+            return ops.fp8_linear_strips(x, layer.fp8_weight, layer.out_features, layer.fp8_scale.reshape(-1), bias,
+                                         self.div_mode)
         return ops.fp8_linear(x, layer.fp8_weight.t(), layer.fp8_scale.reshape(-1), bias, self.div_mode)
+
+
+def fp8_weight_rowmajor(layer) -> torch.Tensor:
+    """The packer's row-major ``[N, K]`` e4m3 bytes of a converted layer."""
+    if getattr(layer, "fp8_layout", "rowmajor") == "strips":
+        return ops.from_strips(layer.fp8_weight, layer.out_features, layer.in_features, _lib.STRIP_FP8)
+    return layer.fp8_weight.t()
 
 
 class Fp8WeightOnlyMethod(QuantMethodBase):

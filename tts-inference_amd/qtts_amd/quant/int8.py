@@ -55,13 +55,26 @@ def _candidates(rows: int) -> dict[str, int]:
     """Kernel configurations worth timing at ``rows``."""
     if rows <= 16:
         c = {"skinny": _lib.algo_code(_lib.ALGO_SKINNY)}
-        for s in (1, 2, 4, 8):
-            c[f"skinny_s{s}"] = _lib.algo_code(_lib.ALGO_SKINNY, splits=s)
+        for s in (1, 2, 4):
+            for w in (4, 8, 16):
+                c[f"skinny_s{s}_w{w}"] = _lib.algo_code(_lib.ALGO_SKINNY, splits=s, waves=w)
         return c
     c = {"tile": _lib.algo_code(_lib.ALGO_TILE)}
     for s in (1, 2, 4):
         c[f"tile_s{s}"] = _lib.algo_code(_lib.ALGO_TILE, splits=s)
     return c
+
+
+def int8_weight_rowmajor(layer) -> torch.Tensor:
+    """The packer's row-major ``[N, K]`` int8 bytes of a converted layer."""
+    if getattr(layer, "int8_layout", "rowmajor") == "strips":
+        return ops.from_strips(layer.int8_weight, layer.out_features, layer.in_features, _lib.STRIP_INT8)
+    return layer.int8_weight
+
+
+def _strips_ok(layer) -> bool:
+    """The strip kernels take 16-bit activations and K % 16 == 0; other layers stay row-major."""
+    return layer.in_features % 16 == 0 and layer.weight.dtype in (torch.bfloat16, torch.float16)
 
 
 class Int8WeightOnlyMethod(QuantMethodBase):
@@ -89,8 +102,14 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         n, k = layer.out_features, layer.in_features
         gen = torch.Generator(device=weight.device).manual_seed(0)
         x = torch.randn(rows, k, device=weight.device, dtype=weight.dtype, generator=gen)
-        ops.reserve_workspace(weight.device, ops.workspace_bytes(_lib.OP_W8A16, rows, n, k))
-        cands = {name: (lambda a=algo: ops.w8a16_gemm(x, q, scale, None, a)) for name, algo in _candidates(rows).items()}
+        cands_algo = _candidates(rows)
+        ops.reserve_workspace(weight.device, max(ops.workspace_bytes(_lib.OP_W8A16, rows, n, k, a)
+                                                 for a in cands_algo.values()))
+        if _strips_ok(layer):
+            cands = {name: (lambda a=algo: ops.w8a16_gemm_strips(x, q, n, scale, None, a))
+                     for name, algo in cands_algo.items()}
+        else:
+            cands = {name: (lambda a=algo: ops.w8a16_gemm(x, q, scale, None, a)) for name, algo in cands_algo.items()}
         best = pick_fastest(cands, lambda: F.linear(x, weight, None),
                             key=("int8_wo", n, k, rows, str(weight.dtype)))
         if best is not None:
@@ -100,6 +119,11 @@ class Int8WeightOnlyMethod(QuantMethodBase):
     def process_weights(self, layer) -> None:
         weight = layer.weight
         q, scale = ops.pack_int8(weight, weight.dtype, self.div_mode)
+        # Keep the MFMA-native strip layout only: a permutation of the packed bytes
+        # (int8_weight_rowmajor recovers them), read by 1 KiB-contiguous wave loads.
+        layout = "strips" if _strips_ok(layer) else "rowmajor"
+        if layout == "strips":
+            q = ops.to_strips(q, _lib.STRIP_INT8)
         if not self._profitable(layer, q, scale):
             self.declined += 1
             # Leaving quant_method unset keeps the layer on F.linear.
@@ -109,6 +133,7 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             ops.workspace_bytes(_lib.OP_W8A16, m, layer.out_features, layer.in_features) for m in (16, 64, 128)))
         layer.register_buffer("int8_weight", q, persistent=False)
         layer.register_buffer("int8_scale", scale, persistent=False)
+        layer.int8_layout = layout
         # Drop the full-precision weight, or the memory report would claim a saving it did not make.
         layer.weight = torch.nn.Parameter(torch.empty(0, dtype=weight.dtype, device=weight.device),
                                           requires_grad=False)
@@ -118,10 +143,15 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         return getattr(layer, "int8_weight", None) is not None
 
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
-        q = layer.int8_weight
-        rows = x.numel() // x.shape[-1] if x.shape[-1] else 0
-        algo = _ALGO.get((q.shape[0], q.shape[1], bucket_of(rows)), _lib.ALGO_AUTO)
-        return ops.w8a16_gemm(x, q, layer.int8_scale, bias, algo)
+        n, k = layer.out_features, layer.in_features
+        rows = x.numel() // k if k else 0
+        algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
+        if layer.int8_layout == "strips":
+            if x.dtype in (torch.bfloat16, torch.float16):
+                return ops.w8a16_gemm_strips(x, layer.int8_weight, n, layer.int8_scale, bias, algo)
+            # e.g. fp32 activations into a bf16-calibrated layer: correct, not fast
+            return ops.w8a16_gemm(x, int8_weight_rowmajor(layer), layer.int8_scale, bias)
+        return ops.w8a16_gemm(x, layer.int8_weight, layer.int8_scale, bias, algo)
 
 
 class Int8Method(QuantMethodBase):
