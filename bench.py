@@ -12,8 +12,8 @@ into one HIP graph.  One step = one replay of the stack at each of the four M.
 
 Printed: one JSON line with the whole-step HBM throughput (algorithmic bytes /
 time), the per-M stack time next to the bf16 hipBLASLt baseline of the same
-stack, a roofline entry for the dominant kernel (gate_up, measured per launch
-with HIP events on its stream) and the reference's CPU path timed on a bounded
+stack, a roofline entry for the dominant kernel (gate_up: device duration of each
+launch from HIP events bound to its dispatch) and the reference's CPU path timed on a bounded
 sample on this host.
 
 Other configs (--config 0..4) print their own JSON line with the same keys.
@@ -60,8 +60,12 @@ def log(msg: str) -> None:
 # weights and inputs
 # ---------------------------------------------------------------------------------------
 
-def make_stack(torch, ops, shapes, layers: int, keep_bf16: bool, fp8: bool = False):
-    """Distinct seeded weights per (layer, linear): W ~ N(0, 0.02) fp32, seed 1000 + 16*layer + idx."""
+def make_stack(torch, ops, shapes, layers: int, keep_bf16: bool, fp8: bool = False, keep_rowmajor: int = 0):
+    """Distinct seeded weights per (layer, linear): W ~ N(0, 0.02) fp32, seed 1000 + 16*layer + idx.
+
+    Each entry holds the packed weight in the strip layout the quant methods store
+    (``qs``) and its scale; the row-major packed bytes (``q``) are kept for the first
+    ``keep_rowmajor`` layers only (the CPU baseline's sample)."""
     stack = []
     for layer in range(layers):
         for idx, (name, n, k) in enumerate(shapes):
@@ -71,9 +75,11 @@ def make_stack(torch, ops, shapes, layers: int, keep_bf16: bool, fp8: bool = Fal
                 q, s = ops.pack_fp8(w)
             else:
                 q, s = ops.pack_int8(w, torch.bfloat16)
+            qs = ops.to_strips(q)
             wb = w.to(torch.bfloat16) if keep_bf16 else None
-            stack.append({"layer": layer, "name": name, "n": n, "k": k, "q": q, "s": s, "w_bf16": wb})
-            del w
+            stack.append({"layer": layer, "name": name, "n": n, "k": k, "qs": qs, "s": s, "w_bf16": wb,
+                          "q": q if layer < keep_rowmajor else None})
+            del w, q
     torch.cuda.synchronize()
     return stack
 
@@ -120,21 +126,18 @@ def time_graph(torch, graph, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
-def per_launch_ms(torch, launches, reps: int) -> float:
-    """Average kernel duration of ``launches`` (callables of one kernel each), timed one by one with
-    HIP events recorded on the stream the kernel is launched on."""
-    stream = torch.cuda.current_stream()
-    pairs = []
-    for _ in range(reps):
-        for fn in launches:
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record(stream)
-            fn()
-            b.record(stream)
-            pairs.append((a, b))
-    torch.cuda.synchronize()
-    times = [a.elapsed_time(b) for a, b in pairs]
-    return sum(times) / len(times)
+def kernel_ms(ops, launches, reps: int) -> float:
+    """Mean device duration of the kernels ``launches`` start (callables of one kernel each), over
+    ``reps`` passes: each kernel's own start/stop timestamps, taken by HIP events that
+    hipExtLaunchKernel binds to its dispatch on the stream it is launched on."""
+    with ops.KernelTimer(max_launches=len(launches) * reps + 16) as t:
+        for _ in range(reps):
+            for fn in launches:
+                fn()
+    if t.launches != len(launches) * reps or t.untimed:
+        raise RuntimeError(f"kernel timer saw {t.launches} kernels (+{t.untimed} untimed), "
+                           f"expected {len(launches) * reps}")
+    return t.mean_ms
 
 
 # ---------------------------------------------------------------------------------------
@@ -195,18 +198,19 @@ def run_talker_stack(args, torch, ops):
     ms = (1, 2, 4, 8)
     layers = 28
     log(f"[bench] packing {layers}x4 talker weights (int8 + bf16 baseline copy)")
-    stack = make_stack(torch, ops, TALKER, layers, keep_bf16=True)
+    stack = make_stack(torch, ops, TALKER, layers, keep_bf16=True, keep_rowmajor=2)
     ops.reserve_workspace(torch.device("cuda"), max(
         ops.workspace_bytes(ops.OP_W8A16, m, e["n"], e["k"]) for m in ms for e in stack[:4]))
     xs = make_inputs(torch, [k for _, _, k in TALKER], ms)
-    int8_bytes = sum(e["q"].numel() for e in stack)
+    int8_bytes = sum(e["n"] * e["k"] for e in stack)
 
     per_m = {}
     total_bytes = 0
     total_ms = 0.0
     for m in ms:
         log(f"[bench] M={m}: capture + time int8 stack and bf16 stack")
-        g_q = capture(torch, lambda m=m: [ops.w8a16_gemm(xs[(m, e["k"])], e["q"], e["s"]) for e in stack])
+        g_q = capture(torch, lambda m=m: [ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"])
+                                          for e in stack])
         g_b = capture(torch, lambda m=m: [torch.nn.functional.linear(xs[(m, e["k"])], e["w_bf16"]) for e in stack])
         t_q = time_graph(torch, g_q, args.steps, args.warmup)
         t_b = time_graph(torch, g_b, max(5, args.steps // 2), args.warmup)
@@ -223,18 +227,19 @@ def run_talker_stack(args, torch, ops):
         del g_q, g_b
         log(f"[bench] M={m}: {per_m[str(m)]}")
 
-    # Dominant kernel (gate_up, the largest share of the stack): per-launch duration over the
-    # 28 distinct gate_up weights, HIP events on the launch stream.
-    rm = 4
+    # Dominant kernel: gate_up, the largest share of the stack.  Its mean device duration over
+    # the 28 distinct gate_up weights at each M of the step (the same mix the graphs replay),
+    # from kernel-bound HIP event timestamps; algorithmic bytes averaged over the same mix.
     gate = [e for e in stack if e["name"] == "gate_up"]
-    launches = [lambda e=e: ops.w8a16_gemm(xs[(rm, e["k"])], e["q"], e["s"]) for e in gate]
-    dur_ms = per_launch_ms(torch, launches, reps=max(2, args.steps // 4))
-    g_bytes = w8a16_bytes(rm, 12288, 2048)
+    launches = [lambda e=e, m=m: ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"])
+                for m in ms for e in gate]
+    dur_ms = kernel_ms(ops, launches, reps=max(2, args.steps // 4))
+    g_bytes = statistics.mean(w8a16_bytes(m, 12288, 2048) for m in ms)
     achieved = g_bytes / (dur_ms * 1e-3) / 1e9
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                 "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                "kernel": "w8a16_skinny_kernel (gate_up 12288x2048, M=4)", "avg_launch_us": round(dur_ms * 1e3, 3),
-                "bytes_per_launch": g_bytes}
+                "kernel": "w8a16_skinny_kernel (gate_up 12288x2048, M in 1,2,4,8)",
+                "avg_launch_us": round(dur_ms * 1e3, 3), "bytes_per_launch": round(g_bytes)}
 
     result = {
         "metric": "int8 W-only decode GEMM HBM GB/s (% of peak) + linear-stack us/step, M=1..8",
@@ -268,10 +273,11 @@ def run_single_linear(args, torch, ops):
     copies = 24
     stack = make_stack(torch, ops, [("gate_up", 12288, 2048)], copies, keep_bf16=False)
     xs = make_inputs(torch, [2048], [1])
-    g = capture(torch, lambda: [ops.w8a16_gemm(xs[(1, 2048)], e["q"], e["s"]) for e in stack])
+    g = capture(torch, lambda: [ops.w8a16_gemm_strips(xs[(1, 2048)], e["qs"], e["n"], e["s"]) for e in stack])
     t = time_graph(torch, g, args.steps, args.warmup)
     nbytes = copies * w8a16_bytes(1, 12288, 2048)
-    dur_ms = per_launch_ms(torch, [lambda e=e: ops.w8a16_gemm(xs[(1, 2048)], e["q"], e["s"]) for e in stack], 2)
+    dur_ms = kernel_ms(ops, [lambda e=e: ops.w8a16_gemm_strips(xs[(1, 2048)], e["qs"], e["n"], e["s"])
+                             for e in stack], 2)
     per = w8a16_bytes(1, 12288, 2048)
     return {"metric": "int8 W-only GEMM HBM GB/s, single gate_up linear", "value": round(nbytes / (t * 1e-3) / 1e9, 1),
             "unit": "GB/s", "ms_per_step": round(t, 4), "steps": args.steps, "warmup": args.warmup, "n_gpus": 1,
@@ -290,7 +296,8 @@ def run_predictor(args, torch, ops):
     for b in (1, 8):
         ms = [b * p for p in range(2, 17)]
         xs = make_inputs(torch, [k for _, _, k in PREDICTOR], ms)
-        g_q = capture(torch, lambda: [ops.w8a16_gemm(xs[(m, e["k"])], e["q"], e["s"]) for m in ms for e in stack])
+        g_q = capture(torch, lambda: [ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"])
+                                      for m in ms for e in stack])
         g_b = capture(torch, lambda: [torch.nn.functional.linear(xs[(m, e["k"])], e["w_bf16"])
                                       for m in ms for e in stack])
         t_q = time_graph(torch, g_q, args.steps, args.warmup)
@@ -312,7 +319,7 @@ def run_prefill(args, torch, ops):
     for m in (64, 256, 1024):
         xs = make_inputs(torch, [2048, 6144], [m])
         for e in stack:
-            fq = lambda e=e: ops.w8a16_gemm(xs[(m, e["k"])], e["q"], e["s"])
+            fq = lambda e=e: ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"])
             fb = lambda e=e: torch.nn.functional.linear(xs[(m, e["k"])], e["w_bf16"])
             gq = capture(torch, lambda: [fq() for _ in range(10)])
             gb = capture(torch, lambda: [fb() for _ in range(10)])
@@ -335,7 +342,7 @@ def run_fp8(args, torch, ops):
     for m in (1, 8, 256):
         xs = make_inputs(torch, [2048, 6144], [m], outliers=True)
         for e in stack:
-            fq = lambda e=e: ops.fp8_linear(xs[(m, e["k"])], e["q"], e["s"])
+            fq = lambda e=e: ops.fp8_linear_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"])
             fb = lambda e=e: torch.nn.functional.linear(xs[(m, e["k"])], e["w_bf16"])
             gq = capture(torch, lambda: [fq() for _ in range(10)])
             gb = capture(torch, lambda: [fb() for _ in range(10)])
@@ -346,6 +353,41 @@ def run_fp8(args, torch, ops):
                                         "speedup": round(tb / tq, 3), "GBps": round(nb / (tq * 1e-3) / 1e9, 1)}
     return {"metric": "fp8 W8A8 linear us and GB/s", "value": None, "unit": "GB/s", "n_gpus": 1,
             "config": {"workload": "configs[4]: talker shapes, fp8 W8A8, M in {1, 8, 256}"}, "shapes": res}
+
+
+def run_traffic_probe(args, torch, ops):
+    """Kernels for a rocprofv3 --pmc pass: a 256 MiB device copy (known bytes, the counters' scale)
+    and the dominant kernel of configs[1] (gate_up over its 28 distinct weights at M = 1, 2, 4, 8),
+    launched eagerly so each dispatch carries its own counters."""
+    ms = (1, 2, 4, 8)
+    stack = make_stack(torch, ops, [("gate_up", 12288, 2048)], 28, keep_bf16=False)
+    xs = make_inputs(torch, [2048], ms)
+    src = torch.ones(128 << 20, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    for m in ms:
+        for e in stack:
+            ops.w8a16_gemm_strips(xs[(m, 2048)], e["qs"], e["n"], e["s"])
+    torch.cuda.synchronize()
+    return {"probe": "traffic", "copy_bytes_each_way": src.numel() * 2, "gate_up_launches": len(ms) * len(stack),
+            "gate_up_algorithmic_bytes_mean": round(statistics.mean(w8a16_bytes(m, 12288, 2048) for m in ms))}
+
+
+def summarize_pmc(path: str) -> None:
+    """Mean counter value per (kernel, grid, counter) from rocprofv3 --pmc CSV output under ``path``."""
+    files = glob.glob(os.path.join(path, "**", "*counter_collection.csv"), recursive=True)
+    if not files:
+        raise SystemExit(f"no *counter_collection.csv under {path}")
+    groups: dict[tuple[str, str, str], list[float]] = {}
+    for f in files:
+        with open(f, newline="") as fh:
+            for row in csv.DictReader(fh):
+                key = ((row.get("Kernel_Name") or "?")[:110], row.get("Grid_Size", "?"), row.get("Counter_Name", "?"))
+                groups.setdefault(key, []).append(float(row.get("Counter_Value") or 0))
+    print(f"{'dispatches':>10} {'mean':>14} {'min':>14} {'max':>14}  counter  grid  kernel")
+    for (name, grid, ctr), v in sorted(groups.items(), key=lambda kv: (kv[0][2], -statistics.mean(kv[1]))):
+        print(f"{len(v):10d} {statistics.mean(v):14.1f} {min(v):14.1f} {max(v):14.1f}  {ctr}  {grid}  {name}")
 
 
 # ---------------------------------------------------------------------------------------
@@ -387,10 +429,16 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="time budget of the CPU baseline sample")
     ap.add_argument("--summarize-rocprof", metavar="DIR")
+    ap.add_argument("--summarize-pmc", metavar="DIR", help="digest a rocprofv3 --pmc run")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="launch only the kernels a rocprofv3 --pmc pass measures (copy + gate_up)")
     args = ap.parse_args()
 
     if args.summarize_rocprof:
         summarize_rocprof(args.summarize_rocprof)
+        return 0
+    if args.summarize_pmc:
+        summarize_pmc(args.summarize_pmc)
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
@@ -406,6 +454,8 @@ def main() -> int:
         raise SystemExit("bench.py needs a gfx950 GPU")
     torch.backends.cuda.matmul.allow_tf32 = False
     runner = {0: run_single_linear, 1: run_talker_stack, 2: run_predictor, 3: run_prefill, 4: run_fp8}[args.config]
+    if args.traffic_probe:
+        runner = run_traffic_probe
     with torch.inference_mode():
         result = runner(args, torch, ops)
     result["device"] = torch.cuda.get_device_name()

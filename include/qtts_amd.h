@@ -71,9 +71,12 @@ int qtts_device_supported(int device);
  * call's automatic choice needs is not an error: the call then runs without
  * split-K.  An explicit split count (algo bits 8-15) that does not fit is.
  *
- * `algo` for the GEMMs: a qtts_algo in bits 0-7; bits 8-15 force the number of
- * K splits across workgroups and bits 16-23 the waves per workgroup of the
- * skinny kernels (0 = automatic).  The calibrator uses these to time variants. */
+ * `algo` for the GEMMs: a qtts_algo in bits 0-7; bits 8-15 set the number of K
+ * splits across workgroups (a minimum for the skinny kernels, which add splits
+ * until each wave's share fits its in-flight group), bits 16-23 the waves per
+ * workgroup of the skinny kernels (1, 2, 4, 8, 16) and bits 24-30 their chunks in
+ * flight per wave (4 or 8; 4 or 6 with 16 waves); 0 = automatic.  The calibrator
+ * uses these to time variants. */
 int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo);
 
 /* --- weight packers ------------------------------------------------------------ */
@@ -172,6 +175,17 @@ int qtts_fp8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, int
                            const uint8_t* qws, int64_t n, const float* sw, const void* bias,
                            void* y, int64_t ldy, int div_mode, int algo, void* ws, int64_t ws_bytes,
                            void* stream);
+
+/* Kernel timer.  No counterpart in the reference: benchmark instrumentation.
+ * Between qtts_kernel_timer_begin and qtts_kernel_timer_end, each kernel the
+ * library launches on a stream that is not capturing a graph records a start and
+ * stop event bound to that kernel's dispatch (hipExtLaunchKernel), up to
+ * max_launches kernels.  qtts_kernel_timer_end waits for them and returns the
+ * summed kernel durations, the number of kernels timed and the number launched
+ * after the pool ran out.  One timer per process; calls that overlap from several
+ * threads all land in the same pool. */
+int qtts_kernel_timer_begin(int max_launches);
+int qtts_kernel_timer_end(double* total_ms, int64_t* launches, int64_t* untimed);
 
 #ifdef __cplusplus
 }

@@ -113,3 +113,13 @@ def test_algo_code_packing():
     assert _lib.algo_code(_lib.ALGO_SKINNY, 4, 8) == 1 | (4 << 8) | (8 << 16)
     with pytest.raises(ValueError):
         _lib.algo_code(_lib.ALGO_TILE, 300)
+
+
+def test_kernel_timer_argument_checks():
+    L = _lib.load()
+    assert L.qtts_kernel_timer_begin(0) == _lib.ERR_INVALID_ARGUMENT
+    assert L.qtts_kernel_timer_begin((1 << 20) + 1) == _lib.ERR_INVALID_ARGUMENT
+    ms, n, u = ctypes.c_double(), ctypes.c_int64(), ctypes.c_int64()
+    assert L.qtts_kernel_timer_end(ctypes.byref(ms), ctypes.byref(n), ctypes.byref(u)) == _lib.ERR_INVALID_ARGUMENT
+    assert "not armed" in _lib.last_error()
+    assert L.qtts_kernel_timer_end(None, ctypes.byref(n), ctypes.byref(u)) == _lib.ERR_INVALID_ARGUMENT

@@ -292,9 +292,9 @@ def test_w8a16_strips_decode_shapes(ops, n, k):
         ref = _oracle_w8a16(x, q, s, b)
         y = ops.w8a16_gemm_strips(x, qs, n, s, b)
         assert_close(y, ref, f"strips auto m={m} n={n} k={k}")
-        for splits, waves in ((1, 4), (2, 8), (4, 16), (3, 2)):
-            y2 = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, splits, waves))
-            assert_close(y2, ref, f"strips m={m} n={n} k={k} S={splits} W={waves}")
+        for splits, waves, cpw in ((1, 4, 4), (2, 8, 8), (4, 16, 6), (3, 2, 8), (1, 16, 4), (1, 1, 4)):
+            y2 = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, splits, waves, cpw))
+            assert_close(y2, ref, f"strips m={m} n={n} k={k} S={splits} W={waves} C={cpw}")
 
 
 def test_w8a16_strips_ragged_and_tile(ops):
@@ -352,3 +352,36 @@ def test_fp8_strips_vs_oracle(ops, n, k):
                 assert_close(y2, ref, f"fp8 strips m={m} n={n} k={k} S={splits} W={waves}")
         y3 = ops.fp8_linear_strips(x, qws, n, sw)
         assert torch.equal(y3, y)
+
+
+def test_kernel_timer_times_eager_launches_only(ops):
+    """The bench's kernel timer: one event pair per eager launch, none for captured launches,
+    and the timed launches still compute the same result."""
+    x, w, b = _make(4, 2048, 2048, bias=True, seed=91)
+    q, s = ops.pack_int8(w, torch.bfloat16)
+    qs = ops.to_strips(q)
+    ref = ops.w8a16_gemm_strips(x, qs, 2048, s, b)
+    with ops.KernelTimer(max_launches=8) as t:
+        outs = [ops.w8a16_gemm_strips(x, qs, 2048, s, b) for _ in range(5)]
+    assert t.launches == 5 and t.untimed == 0
+    assert 0.0 < t.mean_ms < 10.0, t.mean_ms
+    for o in outs:
+        assert torch.equal(o, ref)
+    with ops.KernelTimer(max_launches=2) as t:
+        for _ in range(3):
+            ops.w8a16_gemm_strips(x, qs, 2048, s, b)
+    assert t.launches == 2 and t.untimed == 1
+    static_x = x.clone()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        ops.w8a16_gemm_strips(static_x, qs, 2048, s, b)
+    torch.cuda.current_stream().wait_stream(st)
+    graph = torch.cuda.CUDAGraph()
+    with ops.KernelTimer(max_launches=4) as t:
+        with torch.cuda.graph(graph):
+            out = ops.w8a16_gemm_strips(static_x, qs, 2048, s, b)
+    assert t.launches == 0 and t.untimed == 0
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)

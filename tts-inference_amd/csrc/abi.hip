@@ -6,6 +6,8 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
+#include <vector>
 
 #include "layout.h"
 #include "qtts_amd.h"
@@ -42,6 +44,44 @@ int qtts_check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return qtts_set_error(QTTS_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
   return QTTS_OK;
+}
+
+// ---- kernel timer -----------------------------------------------------------------------
+// Armed by qtts_kernel_timer_begin with a fixed pool of event pairs; qtts::launch takes
+// the next pair for each launch that is not being captured into a graph.
+
+namespace {
+std::mutex g_timer_mu;
+std::atomic<bool> g_timer_armed{false};
+std::vector<hipEvent_t> g_timer_events;  // start0, stop0, start1, stop1, ...
+size_t g_timer_used = 0;
+int64_t g_timer_untimed = 0;
+
+void timer_release() {
+  for (hipEvent_t e : g_timer_events) (void)hipEventDestroy(e);
+  g_timer_events.clear();
+  g_timer_used = 0;
+}
+}  // namespace
+
+bool qtts_timer_slot(hipStream_t st, hipEvent_t* start, hipEvent_t* stop) {
+  if (!g_timer_armed.load(std::memory_order_acquire)) return false;
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) != hipSuccess) {
+    (void)hipGetLastError();
+    return false;
+  }
+  if (cs != hipStreamCaptureStatusNone) return false;
+  std::lock_guard<std::mutex> lock(g_timer_mu);
+  if (!g_timer_armed.load(std::memory_order_relaxed)) return false;
+  if (g_timer_used + 2 > g_timer_events.size()) {
+    g_timer_untimed++;
+    return false;
+  }
+  *start = g_timer_events[g_timer_used];
+  *stop = g_timer_events[g_timer_used + 1];
+  g_timer_used += 2;
+  return true;
 }
 
 // ---- device gating: gfx950 only ---------------------------------------------------------
@@ -287,6 +327,52 @@ int qtts_from_strips(const void* src, int64_t n, int64_t k, int kind, void* dst,
   QTTS_REQUIRE((uintptr_t)src % 16 == 0, "from_strips: source must be 16-byte aligned");
   QTTS_TRY(current_device_check());
   return qtts_launch_from_strips(src, n, k, dst, ld_dst, kind, (hipStream_t)stream);
+}
+
+int qtts_kernel_timer_begin(int max_launches) {
+  QTTS_REQUIRE(max_launches > 0 && max_launches <= (1 << 20), "kernel timer: max_launches must be in [1, 2^20]");
+  std::lock_guard<std::mutex> lock(g_timer_mu);
+  if (g_timer_armed.load(std::memory_order_relaxed))
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "kernel timer: already armed");
+  timer_release();
+  g_timer_events.reserve(2 * (size_t)max_launches);
+  for (int i = 0; i < 2 * max_launches; ++i) {
+    hipEvent_t e = nullptr;
+    hipError_t err = hipEventCreate(&e);
+    if (err != hipSuccess) {
+      timer_release();
+      return qtts_set_error(QTTS_ERR_HIP, "kernel timer: hipEventCreate failed: %s", hipGetErrorString(err));
+    }
+    g_timer_events.push_back(e);
+  }
+  g_timer_untimed = 0;
+  g_timer_armed.store(true, std::memory_order_release);
+  return QTTS_OK;
+}
+
+int qtts_kernel_timer_end(double* total_ms, int64_t* launches, int64_t* untimed) {
+  QTTS_REQUIRE(total_ms && launches && untimed, "kernel timer: null pointer");
+  std::lock_guard<std::mutex> lock(g_timer_mu);
+  if (!g_timer_armed.load(std::memory_order_relaxed))
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "kernel timer: not armed");
+  g_timer_armed.store(false, std::memory_order_release);
+  double sum = 0.0;
+  int status = QTTS_OK;
+  for (size_t i = 0; i + 1 < g_timer_used; i += 2) {
+    float ms = 0.0f;
+    hipError_t err = hipEventSynchronize(g_timer_events[i + 1]);
+    if (err == hipSuccess) err = hipEventElapsedTime(&ms, g_timer_events[i], g_timer_events[i + 1]);
+    if (err != hipSuccess) {
+      status = qtts_set_error(QTTS_ERR_HIP, "kernel timer: %s", hipGetErrorString(err));
+      break;
+    }
+    sum += ms;
+  }
+  *total_ms = sum;
+  *launches = (int64_t)(g_timer_used / 2);
+  *untimed = g_timer_untimed;
+  timer_release();
+  return status;
 }
 
 }  // extern "C"

@@ -158,3 +158,27 @@ __device__ __forceinline__ float wave_sum(float v) {
 
 int qtts_set_error(int status, const char* fmt, ...);
 int qtts_check_launch(const char* what);
+
+// ---- kernel launches and the kernel timer (abi.hip) -------------------------------------
+// Every kernel of the library is launched through qtts::launch.  While the kernel
+// timer is armed (qtts_kernel_timer_begin), each launch outside stream capture
+// takes a start/stop event pair that hipExtLaunchKernel binds to the kernel's own
+// dispatch, so the elapsed time is the kernel's duration, without launch gaps or
+// the cost of separate event records.
+
+#include <hip/hip_ext.h>
+
+bool qtts_timer_slot(hipStream_t st, hipEvent_t* start, hipEvent_t* stop);
+
+namespace qtts {
+
+template <typename... Params, typename... Args>
+inline void launch(void (*kernel)(Params...), dim3 grid, dim3 block, uint32_t shmem, hipStream_t st,
+                   Args... args) {
+  static_assert(sizeof...(Params) == sizeof...(Args), "kernel argument count");
+  hipEvent_t a = nullptr, b = nullptr;
+  qtts_timer_slot(st, &a, &b);
+  hipExtLaunchKernelGGL(kernel, grid, block, shmem, st, a, b, 0u, static_cast<Params>(args)...);
+}
+
+}  // namespace qtts

@@ -413,7 +413,7 @@ static int fp8_launch_fast(const uint8_t* qx, const float* sx, int64_t m, int64_
   if (c.family == QTTS_ALGO_SKINNY) {
     const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8 * c.S;
 #define QTTS_F8S(W, U)                                                                                             \
-  fp8_skinny_kernel<OT, W, U, LAYOUT><<<(unsigned)blocks, W * 64, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, \
+  qtts::launch(&fp8_skinny_kernel<OT, W, U, LAYOUT>, dim3((unsigned)blocks), dim3(W * 64), 0, st, qx, sx, (int)m, (int)k, ldqx, qw, (int)n, \
                                                                            ldqw, sw, bias, y, ldy, part, counters,   \
                                                                            c.strips, c.S, c.cps)
     switch (c.waves) {
@@ -430,7 +430,7 @@ static int fp8_launch_fast(const uint8_t* qx, const float* sx, int64_t m, int64_
   const int64_t tiles = (int64_t)c.mtiles * c.ntiles;
   const int64_t blocks = (tiles + 7) / 8 * 8 * c.S;
 #define QTTS_F8T(BM)                                                                                           \
-  fp8_tile_kernel<OT, BM, LAYOUT><<<(unsigned)blocks, 256, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, \
+  qtts::launch(&fp8_tile_kernel<OT, BM, LAYOUT>, dim3((unsigned)blocks), dim3(256), 0, st, qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, \
                                                                     bias, y, ldy, part, counters, c.mtiles, c.ntiles,  \
                                                                     c.S, c.cps)
   if (c.bm == 32) QTTS_F8T(32);
@@ -454,7 +454,7 @@ static int fp8_launch_typed(const uint8_t* qx, const float* sx, int64_t m, int64
   }
   if (!x_ok || (uintptr_t)qw % 16 != 0 || ldqw % 16 != 0) {
     dim3 grid((unsigned)n, (unsigned)((m + 3) / 4));
-    fp8_generic_kernel<OT><<<grid, 64, 0, st>>>(qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy);
+    qtts::launch(&fp8_generic_kernel<OT>, dim3(grid), dim3(64), 0, st, qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy);
     return qtts_check_launch("w8a8_fp8_generic");
   }
   return fp8_launch_fast<OT, kLayoutRowMajor>(qx, sx, m, k, ldqx, qw, n, ldqw, sw, bias, y, ldy, algo, ws, ws_bytes,

@@ -55,7 +55,7 @@ int qtts_launch_to_strips(const void* src, int64_t n, int64_t k, int64_t ld, voi
   const int64_t units = strip_bytes(n, k, kind) / 16;
   if (units == 0) return QTTS_OK;
   const int64_t blocks = (units + 255) / 256;
-  to_strips_kernel<<<(unsigned)blocks, 256, 0, st>>>((const uint8_t*)src, n, k, ld, (uint8_t*)dst, units,
+  qtts::launch(&to_strips_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (const uint8_t*)src, n, k, ld, (uint8_t*)dst, units,
                                                      strip_nchunks(k, kind), kind);
   return qtts_check_launch("to_strips");
 }
@@ -64,7 +64,7 @@ int qtts_launch_from_strips(const void* src, int64_t n, int64_t k, void* dst, in
   const int64_t units = strip_bytes(n, k, kind) / 16;
   if (units == 0) return QTTS_OK;
   const int64_t blocks = (units + 255) / 256;
-  from_strips_kernel<<<(unsigned)blocks, 256, 0, st>>>((const uint8_t*)src, n, k, (uint8_t*)dst, ld, units,
+  qtts::launch(&from_strips_kernel, dim3((unsigned)blocks), dim3(256), 0, st, (const uint8_t*)src, n, k, (uint8_t*)dst, ld, units,
                                                        strip_nchunks(k, kind), kind);
   return qtts_check_launch("from_strips");
 }

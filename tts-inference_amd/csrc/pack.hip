@@ -90,13 +90,13 @@ int qtts_launch_pack_int8(const void* src, int src_dtype, int64_t n, int64_t k, 
 #define QTTS_PACK_I8(ST, DT)                                                                         \
   do {                                                                                               \
     if (scale_dtype == QTTS_F32)                                                                     \
-      pack_int8_kernel<ST, float><<<grid, block, 0, st>>>((const ST*)src, k, ld, q, (float*)scale_out, \
+      qtts::launch(&pack_int8_kernel<ST, float>, dim3(grid), dim3(block), 0, st, (const ST*)src, k, ld, q, (float*)scale_out, \
                                                           scale_f32, div_mode);                      \
     else if (scale_dtype == QTTS_BF16)                                                               \
-      pack_int8_kernel<ST, bf16_t><<<grid, block, 0, st>>>((const ST*)src, k, ld, q, (bf16_t*)scale_out, \
+      qtts::launch(&pack_int8_kernel<ST, bf16_t>, dim3(grid), dim3(block), 0, st, (const ST*)src, k, ld, q, (bf16_t*)scale_out, \
                                                            scale_f32, div_mode);                     \
     else                                                                                             \
-      pack_int8_kernel<ST, f16_t><<<grid, block, 0, st>>>((const ST*)src, k, ld, q, (f16_t*)scale_out, \
+      qtts::launch(&pack_int8_kernel<ST, f16_t>, dim3(grid), dim3(block), 0, st, (const ST*)src, k, ld, q, (f16_t*)scale_out, \
                                                           scale_f32, div_mode);                      \
   } while (0)
   if (src_dtype == QTTS_F32) QTTS_PACK_I8(float, 0);
@@ -109,17 +109,17 @@ int qtts_launch_pack_int8(const void* src, int src_dtype, int64_t n, int64_t k, 
 int qtts_launch_pack_fp8(const void* src, int src_dtype, int64_t n, int64_t k, int64_t ld, uint8_t* q,
                          float* scale, int div_mode, hipStream_t st) {
   dim3 grid((unsigned)n), block(kPackThreads);
-  if (src_dtype == QTTS_F32) pack_fp8_kernel<float><<<grid, block, 0, st>>>((const float*)src, k, ld, q, scale, div_mode);
-  else if (src_dtype == QTTS_BF16) pack_fp8_kernel<bf16_t><<<grid, block, 0, st>>>((const bf16_t*)src, k, ld, q, scale, div_mode);
-  else pack_fp8_kernel<f16_t><<<grid, block, 0, st>>>((const f16_t*)src, k, ld, q, scale, div_mode);
+  if (src_dtype == QTTS_F32) qtts::launch(&pack_fp8_kernel<float>, dim3(grid), dim3(block), 0, st, (const float*)src, k, ld, q, scale, div_mode);
+  else if (src_dtype == QTTS_BF16) qtts::launch(&pack_fp8_kernel<bf16_t>, dim3(grid), dim3(block), 0, st, (const bf16_t*)src, k, ld, q, scale, div_mode);
+  else qtts::launch(&pack_fp8_kernel<f16_t>, dim3(grid), dim3(block), 0, st, (const f16_t*)src, k, ld, q, scale, div_mode);
   return qtts_check_launch("pack_fp8_e4m3_rowwise");
 }
 
 int qtts_launch_quant_act_fp8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld, uint8_t* qx,
                               float* sx, int div_mode, hipStream_t st) {
   dim3 grid((unsigned)m), block(kPackThreads);
-  if (x_dtype == QTTS_F32) quant_act_fp8_kernel<float><<<grid, block, 0, st>>>((const float*)x, k, ld, qx, sx, div_mode);
-  else if (x_dtype == QTTS_BF16) quant_act_fp8_kernel<bf16_t><<<grid, block, 0, st>>>((const bf16_t*)x, k, ld, qx, sx, div_mode);
-  else quant_act_fp8_kernel<f16_t><<<grid, block, 0, st>>>((const f16_t*)x, k, ld, qx, sx, div_mode);
+  if (x_dtype == QTTS_F32) qtts::launch(&quant_act_fp8_kernel<float>, dim3(grid), dim3(block), 0, st, (const float*)x, k, ld, qx, sx, div_mode);
+  else if (x_dtype == QTTS_BF16) qtts::launch(&quant_act_fp8_kernel<bf16_t>, dim3(grid), dim3(block), 0, st, (const bf16_t*)x, k, ld, qx, sx, div_mode);
+  else qtts::launch(&quant_act_fp8_kernel<f16_t>, dim3(grid), dim3(block), 0, st, (const f16_t*)x, k, ld, qx, sx, div_mode);
   return qtts_check_launch("quant_act_fp8_rows");
 }

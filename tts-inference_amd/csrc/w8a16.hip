@@ -384,33 +384,36 @@ using namespace qtts;
 
 namespace {
 
-struct SkinnyCfg { int waves, S, cps, strips; };
+struct SkinnyCfg { int waves, cpw, S, cps, strips; };
 struct TileCfg { int bm, S, cps, mtiles, ntiles; };
 
-constexpr int kSkinnyCPW = 4;    // chunks a wave keeps in flight at once
-constexpr int kSkinnyCPW16 = 4;  // the same for 1024-thread workgroups (128 VGPRs per lane)
+// Chunks (64 columns, 1 KiB of a strip) a wave keeps in flight at once.  Instantiated
+// as 4 or 8 for workgroups of up to 8 waves and 4 or 6 for 16 waves (1024 threads
+// leave 128 VGPRs per lane).
+constexpr int kSkinnyCPWMax = 8, kSkinnyCPWMax16 = 6;
 
-SkinnyCfg skinny_cfg(int64_t n, int64_t k, int splits_req, int waves_req) {
+bool skinny_cpw_ok(int w, int cpw) { return w == 16 ? (cpw == 4 || cpw == 6) : (cpw == 4 || cpw == 8); }
+
+SkinnyCfg skinny_cfg(int64_t n, int64_t k, int splits_req, int waves_req, int cpw_req) {
   SkinnyCfg c;
   c.strips = (int)((n + 15) / 16);
   const int nchunks = std::max(1, (int)((k + 63) / 64));
-  int W = waves_req, S = splits_req;
+  int W = waves_req, S = splits_req, C = cpw_req;
   if (W <= 0) {
-    // Enough waves to cover the chip (>= 2048 in all) while each wave's share of a
-    // strip fits one in-flight group of kSkinnyCPW chunks.
+    // Few, fat waves: the fewest waves (of 8 chunks in flight each, 6 at 16 waves)
+    // that cover a strip's K without a split.  Measured on the talker and code-
+    // predictor shapes this beats more, thinner waves at every M in 1..16.
     W = 1;
-    while (W < 16 && ((nchunks + W - 1) / W > kSkinnyCPW || (int64_t)c.strips * W < 2048)) W *= 2;
+    while (W < 16 && W * kSkinnyCPWMax < nchunks) W *= 2;
   }
-  if (S <= 0) {
-    S = 1;
-    while ((nchunks + S * W - 1) / (S * W) > kSkinnyCPW) S *= 2;
-  }
+  if (C <= 0) C = W == 16 ? kSkinnyCPWMax16 : kSkinnyCPWMax;
   c.waves = W;
-  const int cpw = W == 16 ? kSkinnyCPW16 : kSkinnyCPW;
-  // The kernel runs one group of cpw chunks per wave: raise S until a wave's share
+  c.cpw = C;
+  // The kernel runs one group of C chunks per wave: raise S until a wave's share
   // fits (a requested split count is a minimum).
-  S = std::max(S, (nchunks + W * cpw - 1) / (W * cpw));
-  S = std::max(1, std::min(S, nchunks));
+  S = std::max(S, 1);
+  S = std::max(S, (nchunks + W * C - 1) / (W * C));
+  S = std::min(S, nchunks);
   c.cps = (nchunks + S - 1) / S;
   c.S = (nchunks + c.cps - 1) / c.cps;
   return c;
@@ -450,7 +453,9 @@ bool grid_ok(int64_t blocks) { return blocks > 0 && blocks < (int64_t)1 << 31; }
 int64_t qtts_w8a16_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
   const int family = algo & 0xff, splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff;
   int64_t ws = 0;
-  if (family == QTTS_ALGO_SKINNY || family == QTTS_ALGO_AUTO) ws = std::max(ws, skinny_ws(skinny_cfg(n, k, splits, waves)));
+  const int cpw = (algo >> 24) & 0xff;
+  if (family == QTTS_ALGO_SKINNY || family == QTTS_ALGO_AUTO)
+    ws = std::max(ws, skinny_ws(skinny_cfg(n, k, splits, waves, cpw)));
   if (family == QTTS_ALGO_TILE || (family == QTTS_ALGO_AUTO && m > 16)) ws = std::max(ws, tile_ws(tile_cfg(m, n, k, splits)));
   return ws;
 }
@@ -467,13 +472,21 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
   unsigned* counters = (unsigned*)ws;
   float* part = ws ? (float*)((char*)ws + kCounterBytes) : nullptr;
   if (family == QTTS_ALGO_SKINNY) {
-    SkinnyCfg c = skinny_cfg(n, k, splits, waves);
+    const int cpw = (algo >> 24) & 0xff;
+    SkinnyCfg c = skinny_cfg(n, k, splits, waves, cpw);
+    if (!skinny_cpw_ok(c.waves, c.cpw))
+      return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: %d chunks per wave is not built for %d waves",
+                            c.cpw, c.waves);
     const int64_t need = skinny_ws(c);
     if (need > ws_bytes || (need > 0 && !ws)) {
       if (splits > 0)
         return qtts_set_error(QTTS_ERR_WORKSPACE, "w8a16 skinny with %d splits needs %lld workspace bytes, got %lld",
                               c.S, (long long)need, (long long)ws_bytes);
-      c = skinny_cfg(n, k, 1, waves);  // no room for a split: one workgroup per strip
+      // No room for a split: give each wave a longer run instead.
+      c = skinny_cfg(n, k, 1, 16, c.waves == 16 ? kSkinnyCPWMax16 : c.cpw);
+      if (c.S > 1)
+        return qtts_set_error(QTTS_ERR_WORKSPACE, "w8a16 skinny: K=%lld needs a split-K workspace of %lld bytes",
+                              (long long)k, (long long)skinny_ws(c));
     }
     if (c.S > 1 && c.strips > kMaxSplitTiles)
       return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: N=%lld with K=%lld needs a split-K over more "
@@ -483,11 +496,11 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
 #define QTTS_SKINNY_T(ST, W, CPW)                                                                             \
   do {                                                                                                        \
     if (LAYOUT == kLayoutStrips && k % 64 == 0)                                                               \
-      w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, true><<<(unsigned)blocks, W * 64, 0, st>>>(                 \
+      qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, true>, dim3((unsigned)blocks), dim3(W * 64), 0, st,                  \
           x, (int)m, (int)k, ldx, q, (int)n, ldq, (const ST*)scale, bias, y, ldy, part, counters, c.strips, c.S, \
           c.cps);                                                                                             \
     else                                                                                                      \
-      w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, false><<<(unsigned)blocks, W * 64, 0, st>>>(                \
+      qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, false>, dim3((unsigned)blocks), dim3(W * 64), 0, st,                 \
           x, (int)m, (int)k, ldx, q, (int)n, ldq, (const ST*)scale, bias, y, ldy, part, counters, c.strips, c.S, \
           c.cps);                                                                                             \
   } while (0)
@@ -497,12 +510,17 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
     else if (sdt == QTTS_F16) QTTS_SKINNY_T(f16_t, W, CPW);         \
     else QTTS_SKINNY_T(float, W, CPW);                              \
   } while (0)
-    switch (c.waves) {
-      case 1: QTTS_SKINNY(1, kSkinnyCPW); break;
-      case 2: QTTS_SKINNY(2, kSkinnyCPW); break;
-      case 4: QTTS_SKINNY(4, kSkinnyCPW); break;
-      case 8: QTTS_SKINNY(8, kSkinnyCPW); break;
-      case 16: QTTS_SKINNY(16, kSkinnyCPW16); break;
+    switch (c.waves * 16 + c.cpw) {
+      case 1 * 16 + 4: QTTS_SKINNY(1, 4); break;
+      case 1 * 16 + 8: QTTS_SKINNY(1, 8); break;
+      case 2 * 16 + 4: QTTS_SKINNY(2, 4); break;
+      case 2 * 16 + 8: QTTS_SKINNY(2, 8); break;
+      case 4 * 16 + 4: QTTS_SKINNY(4, 4); break;
+      case 4 * 16 + 8: QTTS_SKINNY(4, 8); break;
+      case 8 * 16 + 4: QTTS_SKINNY(8, 4); break;
+      case 8 * 16 + 8: QTTS_SKINNY(8, 8); break;
+      case 16 * 16 + 4: QTTS_SKINNY(16, 4); break;
+      case 16 * 16 + 6: QTTS_SKINNY(16, 6); break;
       default:
         return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: waves per workgroup must be 1, 2, 4, 8 or 16");
     }
@@ -522,7 +540,7 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
   const int64_t blocks = (tiles + 7) / 8 * 8 * c.S;
   if (!grid_ok(blocks)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16: problem too large");
 #define QTTS_TILE(BM)                                                                                          \
-  w8a16_tile_kernel<XT, BM, LAYOUT><<<(unsigned)blocks, 256, 0, st>>>(x, (int)m, (int)k, ldx, q, (int)n, ldq, scale, \
+  qtts::launch(&w8a16_tile_kernel<XT, BM, LAYOUT>, dim3((unsigned)blocks), dim3(256), 0, st, x, (int)m, (int)k, ldx, q, (int)n, ldq, scale, \
                                                                       sdt, bias, y, ldy, part, counters, c.mtiles, \
                                                                       c.ntiles, c.S, c.cps)
   if (c.bm == 32) QTTS_TILE(32);
@@ -545,13 +563,13 @@ int qtts_launch_w8a16(const void* x, int x_dtype, int64_t m, int64_t k, int64_t 
                             "strip-layout weights need bf16/fp16 activations with 16-byte aligned rows and K %% 16 == 0");
     dim3 grid((unsigned)n, (unsigned)((m + kGenericRows - 1) / kGenericRows));
     if (x_dtype == QTTS_BF16)
-      w8a16_generic_kernel<bf16_t><<<grid, 64, 0, st>>>((const bf16_t*)x, (int)m, (int)k, ldx, q, (int)n, ldq, scale,
+      qtts::launch(&w8a16_generic_kernel<bf16_t>, dim3(grid), dim3(64), 0, st, (const bf16_t*)x, (int)m, (int)k, ldx, q, (int)n, ldq, scale,
                                                         scale_dtype, (const bf16_t*)bias, (bf16_t*)y, ldy);
     else if (x_dtype == QTTS_F16)
-      w8a16_generic_kernel<f16_t><<<grid, 64, 0, st>>>((const f16_t*)x, (int)m, (int)k, ldx, q, (int)n, ldq, scale,
+      qtts::launch(&w8a16_generic_kernel<f16_t>, dim3(grid), dim3(64), 0, st, (const f16_t*)x, (int)m, (int)k, ldx, q, (int)n, ldq, scale,
                                                        scale_dtype, (const f16_t*)bias, (f16_t*)y, ldy);
     else
-      w8a16_generic_kernel<float><<<grid, 64, 0, st>>>((const float*)x, (int)m, (int)k, ldx, q, (int)n, ldq, scale,
+      qtts::launch(&w8a16_generic_kernel<float>, dim3(grid), dim3(64), 0, st, (const float*)x, (int)m, (int)k, ldx, q, (int)n, ldq, scale,
                                                        scale_dtype, (const float*)bias, (float*)y, ldy);
     return qtts_check_launch("w8a16_generic");
   }

@@ -31,7 +31,8 @@ ERR_WORKSPACE = -5
 F32, BF16, F16 = 0, 1, 2
 # qtts_div_mode
 DIV_DEVICE, DIV_IEEE = 0, 1
-# qtts_algo (bits 0-7); bits 8-15 split count, bits 16-23 waves per workgroup
+# qtts_algo (bits 0-7); bits 8-15 split count, bits 16-23 waves per workgroup,
+# bits 24-31 chunks per wave of the skinny kernels (0 = automatic)
 ALGO_AUTO, ALGO_SKINNY, ALGO_TILE = 0, 1, 2
 # qtts_op
 OP_W8A16, OP_W8A8_FP8, OP_FP8_LINEAR = 0, 1, 2
@@ -55,13 +56,15 @@ EXPORTS = (
     "qtts_w8a16_gemm_strips",
     "qtts_w8a8_fp8_gemm_strips",
     "qtts_fp8_linear_strips",
+    "qtts_kernel_timer_begin",
+    "qtts_kernel_timer_end",
 )
 
 
-def algo_code(family: int = ALGO_AUTO, splits: int = 0, waves: int = 0) -> int:
-    if not (0 <= splits < 256 and 0 <= waves < 256):
-        raise ValueError("splits and waves must be in [0, 255]")
-    return family | (splits << 8) | (waves << 16)
+def algo_code(family: int = ALGO_AUTO, splits: int = 0, waves: int = 0, cpw: int = 0) -> int:
+    if not (0 <= splits < 256 and 0 <= waves < 256 and 0 <= cpw < 128):
+        raise ValueError("splits and waves must be in [0, 255], cpw in [0, 127]")
+    return family | (splits << 8) | (waves << 16) | (cpw << 24)
 
 
 class QttsError(RuntimeError):
@@ -119,6 +122,11 @@ def load() -> ctypes.CDLL:
         L.qtts_w8a8_fp8_gemm_strips.argtypes = [p, p, i64, i64, i64, p, i64, p, p, p, i32, i64, i32, p, i64, p]
         L.qtts_fp8_linear_strips.restype = i32
         L.qtts_fp8_linear_strips.argtypes = [p, i32, i64, i64, i64, p, i64, p, p, p, i64, i32, i32, p, i64, p]
+        L.qtts_kernel_timer_begin.restype = i32
+        L.qtts_kernel_timer_begin.argtypes = [i32]
+        L.qtts_kernel_timer_end.restype = i32
+        L.qtts_kernel_timer_end.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64),
+                                            ctypes.POINTER(i64)]
         version = L.qtts_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"libqtts_amd ABI version {version}, expected {ABI_VERSION}; rebuild it")

@@ -356,3 +356,33 @@ def fp8_linear_strips(x: torch.Tensor, qws: torch.Tensor, n: int, sw: torch.Tens
     qx, sx = quant_act_fp8(x, div_mode)
     out = w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, bias, x.dtype, algo)
     return out.reshape(*shape[:-1], n)
+
+
+class KernelTimer:
+    """Summed device durations of the kernels this library launches inside the block.
+
+    Each kernel launched outside graph capture gets a start/stop event pair bound to
+    its own dispatch (``hipExtLaunchKernel``), so ``total_ms / launches`` is the mean
+    kernel duration with no launch gaps.  ``untimed`` counts launches past the pool.
+    """
+
+    def __init__(self, max_launches: int = 4096) -> None:
+        self.max_launches = int(max_launches)
+        self.total_ms = 0.0
+        self.launches = 0
+        self.untimed = 0
+
+    def __enter__(self) -> "KernelTimer":
+        _lib.check(_lib.load().qtts_kernel_timer_begin(self.max_launches), "kernel_timer_begin")
+        return self
+
+    def __exit__(self, *exc) -> None:
+        import ctypes
+        ms, n, u = ctypes.c_double(), ctypes.c_int64(), ctypes.c_int64()
+        _lib.check(_lib.load().qtts_kernel_timer_end(ctypes.byref(ms), ctypes.byref(n), ctypes.byref(u)),
+                   "kernel_timer_end")
+        self.total_ms, self.launches, self.untimed = ms.value, n.value, u.value
+
+    @property
+    def mean_ms(self) -> float:
+        return self.total_ms / self.launches if self.launches else float("nan")
