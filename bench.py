@@ -126,6 +126,19 @@ def time_graph(torch, graph, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
+def committed_traffic(name: str) -> tuple[int | None, str | None]:
+    """HBM bytes per launch from a committed rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE,
+    each scaled by what the counter reads for a copy of known size) under profiles/."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1]), f"profiles/{name}"
+    except OSError:
+        pass
+    return None, None
+
+
 def kernel_ms(ops, launches, reps: int) -> float:
     """Mean device duration of the kernels ``launches`` start (callables of one kernel each), over
     ``reps`` passes: each kernel's own start/stop timestamps, taken by HIP events that
@@ -236,8 +249,9 @@ def run_talker_stack(args, torch, ops):
     dur_ms = kernel_ms(ops, launches, reps=max(2, args.steps // 4))
     g_bytes = statistics.mean(w8a16_bytes(m, 12288, 2048) for m in ms)
     achieved = g_bytes / (dur_ms * 1e-3) / 1e9
+    traffic, traffic_src = committed_traffic("w8a16_skinny_gate_up_pmc.md")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_src,
                 "kernel": "w8a16_skinny_kernel (gate_up 12288x2048, M in 1,2,4,8)",
                 "avg_launch_us": round(dur_ms * 1e3, 3), "bytes_per_launch": round(g_bytes)}
 
