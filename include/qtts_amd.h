@@ -73,10 +73,12 @@ int qtts_device_supported(int device);
  *
  * `algo` for the GEMMs: a qtts_algo in bits 0-7; bits 8-15 set the number of K
  * splits across workgroups (a minimum for the skinny kernels, which add splits
- * until each wave's share fits its in-flight group), bits 16-23 the waves per
- * workgroup of the skinny kernels (1, 2, 4, 8, 16) and bits 24-30 their chunks in
- * flight per wave (4 or 8; 4 or 6 with 16 waves); 0 = automatic.  The calibrator
- * uses these to time variants. */
+ * until each wave's share fits its in-flight group).  For the skinny kernels, bits
+ * 16-23 are the waves per workgroup (1, 2, 4, 8, 16) and bits 24-30 the chunks in
+ * flight per wave (4 or 8; 4 or 6 with 16 waves).  For the tile kernel on strip
+ * weights, bits 16-23 are the LDS pipeline stages (2, 3, 4, 6, 8) and bits 24-30
+ * the tile shape: bits 24-27 log2(BM / 16) in 1..3, bits 28-30 log2(BN / 32) in
+ * 1..3.  0 = automatic everywhere.  The calibrator uses these to time variants. */
 int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo);
 
 /* --- weight packers ------------------------------------------------------------ */

@@ -385,3 +385,62 @@ def test_kernel_timer_times_eager_launches_only(ops):
     graph.replay()
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("m", [17, 33, 64, 65, 128, 129, 256])
+def test_w8a16_strips_tile_vs_oracle(ops, m):
+    """The pipelined strip-layout tile kernel (M > 16, K % 64 == 0): ragged M and N, every scale dtype,
+    fp16 activations, forced split counts."""
+    for n, k, sdt, xdt in ((2048, 2048, torch.bfloat16, torch.bfloat16), (1000, 1024, torch.float32, torch.bfloat16),
+                           (2080, 3072, torch.float16, torch.float16), (24, 64, torch.bfloat16, torch.bfloat16)):
+        print(f"strips tile m={m} n={n} k={k} scale={sdt} x={xdt}", flush=True)
+        x, w, b = _make(m, n, k, dtype=xdt, bias=(m % 2 == 1), seed=m * 5 + n + k)
+        q, s = ops.pack_int8(w, sdt)
+        qs = ops.to_strips(q)
+        ref = _oracle_w8a16(x, q, s, b)
+        y = ops.w8a16_gemm_strips(x, qs, n, s, b)
+        assert_close(y, ref, f"strips tile auto m={m} n={n} k={k}")
+        for splits in (1, 2, 3, 4):
+            y2 = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits))
+            assert_close(y2, ref, f"strips tile m={m} n={n} k={k} S={splits}")
+            if splits > 1:
+                assert torch.equal(y2, ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits))), \
+                    f"split-K not deterministic m={m} n={n} k={k} S={splits}"
+
+
+@pytest.mark.parametrize("n,k", TALKER + PREDICTOR)
+def test_w8a16_strips_prefill_vs_fp32(ops, n, k):
+    """configs[3] rows (and the batch-8 code-predictor rows) on the strip layout against a torch fp32
+    GEMM of the dequantized weight."""
+    for m in (48, 120, 256, 1024):
+        print(f"strips prefill m={m} n={n} k={k}", flush=True)
+        x, w, b = _make(m, n, k, bias=(m == 120), seed=n * 7 + m)
+        q, s = ops.pack_int8(w, torch.bfloat16)
+        qs = ops.to_strips(q)
+        y = ops.w8a16_gemm_strips(x, qs, n, s, b)
+        ref = x.float() @ (q.float() * s.float()[:, None]).t()
+        if b is not None:
+            ref = ref + b.float()
+        assert_close(y, ref.double().cpu().numpy(), f"strips prefill m={m} n={n} k={k}")
+
+
+def test_w8a16_strips_tile_graph_replays_split(ops):
+    x, w, b = _make(40, 1024, 3072, bias=True, seed=78)
+    q, s = ops.pack_int8(w, torch.bfloat16)
+    qs = ops.to_strips(q)
+    algo = ops.algo_code(2, 4)
+    eager = ops.w8a16_gemm_strips(x, qs, 1024, s, b, algo)
+    static_x = x.clone()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        ops.w8a16_gemm_strips(static_x, qs, 1024, s, b, algo)
+    torch.cuda.current_stream().wait_stream(st)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = ops.w8a16_gemm_strips(static_x, qs, 1024, s, b, algo)
+    for i in range(4):
+        ops.w8a16_gemm_strips(x * 2, qs, 1024, s, b, ops.algo_code(2, 3))  # another split count in between
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"

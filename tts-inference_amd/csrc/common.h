@@ -42,22 +42,27 @@ __device__ __forceinline__ float to_f32(f16_t v) {
   return (float)h;
 }
 
-// fp32 -> bf16 bits, round to nearest even (NaN kept quiet).
-__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return (uint16_t)(u >> 16);
-}
+// fp32 -> 16-bit float, round to nearest even, by the hardware conversions
+// (v_cvt_pk_bf16_f32 on gfx950, v_cvt_f16_f32): branch-free, NaN becomes a quiet NaN.
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
+typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
 template <typename T> __device__ __forceinline__ T from_f32(float v);
 template <> __device__ __forceinline__ float from_f32<float>(float v) { return v; }
-template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) { return bf16_t{f32_to_bf16_bits(v)}; }
+template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
+  return bf16_t{__builtin_bit_cast(uint16_t, (__bf16)v)};
+}
 template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float v) {
-  _Float16 h = (_Float16)v;  // round to nearest even
-  f16_t r;
-  __builtin_memcpy(&r.bits, &h, 2);
-  return r;
+  return f16_t{__builtin_bit_cast(uint16_t, (_Float16)v)};
+}
+
+// Two values rounded to T and packed low-first into 32 bits (one conversion for bf16).
+template <typename T> __device__ __forceinline__ uint32_t pack2_f32(float a, float b);
+template <> __device__ __forceinline__ uint32_t pack2_f32<bf16_t>(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
+}
+template <> __device__ __forceinline__ uint32_t pack2_f32<f16_t>(float a, float b) {
+  return (uint32_t)from_f32<f16_t>(a).bits | ((uint32_t)from_f32<f16_t>(b).bits << 16);
 }
 
 // Round to T and widen back (identity for fp32).

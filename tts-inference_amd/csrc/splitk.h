@@ -42,17 +42,19 @@ __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One meeting.  `slots` points at the tile's S slots of nthreads * NV floats each;
-// every participating thread calls this with its NV accumulator values.  Returns
+// One meeting.  `slots` points at the tile's S slots of nthreads * NV floats each,
+// stored value-major (value v of thread t at v * nthreads + t) so that each store or
+// load instruction of a wave covers 64 consecutive floats; every participating
+// thread calls this with its NV accumulator values.  Returns
 // true in the last-arriving workgroup, whose threads then hold the full sums.
 // `flag` is a __shared__ word (used when nthreads > 64).
 template <int NV>
 __device__ __forceinline__ bool splitk_meet(float (&acc)[NV], float* __restrict__ slots,
                                             unsigned* __restrict__ counter, int S, int split, int tid,
                                             int nthreads, unsigned* flag) {
-  float* mine = slots + ((int64_t)split * nthreads + tid) * NV;
+  float* mine = slots + (int64_t)split * nthreads * NV + tid;
 #pragma unroll
-  for (int v = 0; v < NV; ++v) store_coherent(mine + v, acc[v]);
+  for (int v = 0; v < NV; ++v) store_coherent(mine + (int64_t)v * nthreads, acc[v]);
   wait_vmem();
   unsigned prev = 0;
   if (nthreads > 64) {
@@ -68,9 +70,15 @@ __device__ __forceinline__ bool splitk_meet(float (&acc)[NV], float* __restrict_
 #pragma unroll
   for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
   for (int s = 0; s < S; ++s) {
-    const float* src = slots + ((int64_t)s * nthreads + tid) * NV;
+    // All of a slot's loads go out before any is consumed: the scheduler keeps atomic
+    // loads in order and would otherwise wait for each one before the next.
+    const float* src = slots + (int64_t)s * nthreads * NV + tid;
+    float part[NV];
 #pragma unroll
-    for (int v = 0; v < NV; ++v) acc[v] += load_coherent(src + v);
+    for (int v = 0; v < NV; ++v) part[v] = load_coherent(src + (int64_t)v * nthreads);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int v = 0; v < NV; ++v) acc[v] += part[v];
   }
   if (tid == 0) reset_counter(counter);
   return true;

@@ -450,13 +450,21 @@ bool grid_ok(int64_t blocks) { return blocks > 0 && blocks < (int64_t)1 << 31; }
 
 }  // namespace
 
+int64_t qtts_w8a16_pipe_ws_bytes(int64_t m, int64_t n, int64_t k, int splits, int shape);
+int qtts_launch_w8a16_pipe(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
+                           int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
+                           int splits, int stages, int shape, void* ws, int64_t ws_bytes, hipStream_t st);
+
 int64_t qtts_w8a16_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
   const int family = algo & 0xff, splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff;
   int64_t ws = 0;
   const int cpw = (algo >> 24) & 0xff;
   if (family == QTTS_ALGO_SKINNY || family == QTTS_ALGO_AUTO)
     ws = std::max(ws, skinny_ws(skinny_cfg(n, k, splits, waves, cpw)));
-  if (family == QTTS_ALGO_TILE || (family == QTTS_ALGO_AUTO && m > 16)) ws = std::max(ws, tile_ws(tile_cfg(m, n, k, splits)));
+  if (family == QTTS_ALGO_TILE || (family == QTTS_ALGO_AUTO && m > 16)) {
+    ws = std::max(ws, tile_ws(tile_cfg(m, n, k, splits)));
+    if (k % 64 == 0) ws = std::max(ws, qtts_w8a16_pipe_ws_bytes(m, n, k, splits, (algo >> 24) & 0xff));
+  }
   return ws;
 }
 
@@ -528,6 +536,9 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
 #undef QTTS_SKINNY_T
     return qtts_check_launch("w8a16_skinny");
   }
+  if (LAYOUT == kLayoutStrips && k % 64 == 0)
+    return qtts_launch_w8a16_pipe(x, std::is_same<XT, bf16_t>::value ? QTTS_BF16 : QTTS_F16, m, k, ldx, q, n, scale,
+                                  sdt, bias, y, ldy, splits, waves, (algo >> 24) & 0xff, ws, ws_bytes, st);
   TileCfg c = tile_cfg(m, n, k, splits);
   const int64_t need = tile_ws(c);
   if (need > ws_bytes || (need > 0 && !ws)) {
