@@ -444,3 +444,46 @@ def test_w8a16_strips_tile_graph_replays_split(ops):
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i}"
+
+
+@pytest.mark.parametrize("m", [17, 40, 128, 200])
+def test_fp8_strips_tile_vs_oracle(ops, m):
+    """The pipelined fp8 tile kernel (M > 16, K % 128 == 0): ragged M and N, bias, every output dtype,
+    forced tile shapes and split counts."""
+    for n, k, odt in ((2048, 2048, torch.bfloat16), (1000, 1024, torch.float16), (24, 256, torch.float32),
+                      (2080, 3072, torch.bfloat16)):
+        print(f"fp8 strips tile m={m} n={n} k={k} out={odt}", flush=True)
+        x, w = _fp8_inputs(m, n, k, seed=m * 3 + n + k)
+        b = (torch.randn(n, device="cuda") * 0.1).to(odt)
+        qw, sw = ops.pack_fp8(w)
+        qws = ops.to_strips(qw)
+        qx, sx = ops.quant_act_fp8(x)
+        ref, inter = _oracle_w8a8(qx, sx, qw, sw, b)
+        y = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, odt)
+        assert_close(y, ref, f"fp8 strips tile auto m={m} n={n} k={k}", inter)
+        for splits, stages, shape in ((1, 2, 0x11), (2, 3, 0x22), (3, 4, 0x21), (4, 3, 0x12)):
+            algo = ops.algo_code(2, splits, stages, shape)
+            y2 = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, odt, algo)
+            assert_close(y2, ref, f"fp8 strips tile m={m} n={n} k={k} S={splits} P={stages} shape={shape:#x}", inter)
+            if splits > 1:
+                assert torch.equal(y2, ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, odt, algo)), \
+                    f"fp8 split-K not deterministic m={m} n={n} k={k} S={splits}"
+
+
+def test_w8a16_strips_tile_forced_shapes(ops):
+    """Every tile shape and stage count the tile kernel is built for, against the oracle."""
+    m, n, k = 70, 520, 1024
+    x, w, b = _make(m, n, k, bias=True, seed=4242)
+    q, s = ops.pack_int8(w, torch.bfloat16)
+    qs = ops.to_strips(q)
+    ref = _oracle_w8a16(x, q, s, b)
+    for bmc in (1, 2, 3):
+        for bnc in (1, 2, 3):
+            for stages in (2, 3, 4, 6, 8):
+                algo = ops.algo_code(2, 2, stages, bmc | (bnc << 4))
+                try:
+                    y = ops.w8a16_gemm_strips(x, qs, n, s, b, algo)
+                except ValueError as e:
+                    assert "stages are not built" in str(e), e
+                    continue
+                assert_close(y, ref, f"tile BM={16 << bmc} BN={32 << bnc} P={stages}")

@@ -19,6 +19,7 @@
 // sx[m] * sw[n] and rounded to the output dtype, then the bias is added in the
 // output dtype (fp8.py:79-89 add the bias after _scaled_mm returns).
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 #include "layout.h"
@@ -384,14 +385,24 @@ int64_t fp8_cfg_ws(const F8Cfg& c) {
 
 }  // namespace
 
+int64_t qtts_fp8_pipe_ws_bytes(int64_t m, int64_t n, int64_t k, int splits, int shape);
+int qtts_launch_fp8_pipe(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const uint8_t* qs,
+                         int64_t n, const float* sw, const void* bias, void* y, int out_dtype, int64_t ldy, int splits,
+                         int stages, int shape, void* ws, int64_t ws_bytes, hipStream_t st);
+
 int64_t qtts_fp8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
+  int64_t a;
   if ((algo & 0xff) == QTTS_ALGO_AUTO) {
     const int rest = algo & ~0xff;
-    int64_t a = fp8_cfg_ws(fp8_cfg(std::min<int64_t>(m, 16), n, k, rest | QTTS_ALGO_SKINNY));
+    a = fp8_cfg_ws(fp8_cfg(std::min<int64_t>(m, 16), n, k, rest | QTTS_ALGO_SKINNY));
     if (m > 16) a = std::max(a, fp8_cfg_ws(fp8_cfg(m, n, k, rest | QTTS_ALGO_TILE)));
-    return a;
+  } else {
+    a = fp8_cfg_ws(fp8_cfg(m, n, k, algo));
   }
-  return fp8_cfg_ws(fp8_cfg(m, n, k, algo));
+  const int family = algo & 0xff;
+  if (k % 128 == 0 && (family == QTTS_ALGO_TILE || (family == QTTS_ALGO_AUTO && m > 16)))
+    a = std::max(a, qtts_fp8_pipe_ws_bytes(m, n, k, (algo >> 8) & 0xff, (algo >> 24) & 0xff));
+  return a;
 }
 
 template <typename OT, int LAYOUT>
@@ -401,6 +412,11 @@ static int fp8_launch_fast(const uint8_t* qx, const float* sx, int64_t m, int64_
   F8Cfg c = fp8_cfg(m, n, k, algo);
   if (c.family == QTTS_ALGO_SKINNY && m > 16)
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "skinny fp8 kernel handles M <= 16, got M=%lld", (long long)m);
+  if (LAYOUT == kLayoutStrips && c.family == QTTS_ALGO_TILE && k % 128 == 0) {
+    constexpr int odt = std::is_same<OT, bf16_t>::value ? QTTS_BF16 : (std::is_same<OT, f16_t>::value ? QTTS_F16 : QTTS_F32);
+    return qtts_launch_fp8_pipe(qx, sx, m, k, ldqx, qw, n, sw, bias, y, odt, ldy, (algo >> 8) & 0xff,
+                                (algo >> 16) & 0xff, (algo >> 24) & 0xff, ws, ws_bytes, st);
+  }
   const int64_t need = fp8_cfg_ws(c);
   if (need > ws_bytes || (need > 0 && !ws)) {
     if ((algo >> 8) & 0xff)

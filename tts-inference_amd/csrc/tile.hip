@@ -3,10 +3,9 @@
 // Replaces _w8_gemm_kernel (qtts/quant/kernels.py:89-135) for M > 16 when K % 64 == 0.
 //
 // A workgroup of 4 waves owns a BM x BN output tile and a K range; it walks the K
-// range in 64-column stages through a 4-deep LDS ring.  Stage loads are direct
-// global -> LDS transfers (global_load_lds_dwordx4, 16 bytes per lane), so three
-// stages are in flight while the fourth is consumed, with no registers held for
-// them.  Every load writes one 1 KiB MFMA fragment in lane order:
+// range in 64-column stages through a P-deep LDS ring.  Stage loads are direct
+// global -> LDS transfers (global_load_lds_dwordx4, 16 bytes per lane), so P-1
+// stages are in flight while one is consumed, with no registers held for them.  Every load writes one 1 KiB MFMA fragment in lane order:
 //   * activation fragment (m-block mb, half h): lane l carries
 //     x[m0 + 16 mb + l % 16][k + 16 (l / 16) + 8 h .. + 7]  (8 bf16);
 //   * weight fragment (strip sb): the strip layout's 1 KiB block, lane l carries
@@ -29,34 +28,10 @@
 
 #include "common.h"
 #include "layout.h"
+#include "pipe.h"
 #include "splitk.h"
 
 namespace qtts {
-
-typedef __attribute__((address_space(3))) void lds_void_t;
-typedef __attribute__((address_space(1))) void gbl_void_t;
-
-// One 16-byte-per-lane direct load: lane l's 16 bytes land at lds_wave + 16 l.
-__device__ __forceinline__ void load_to_lds16(const void* src, void* lds_wave) {
-  __builtin_amdgcn_global_load_lds((gbl_void_t*)src, (lds_void_t*)lds_wave, 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(N), expcnt and lgkmcnt left at their maxima.
-template <int N> __device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt is 6 bits");
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
-
-// Workgroup barrier without a memory fence: stage visibility is established by each
-// wave's own vmcnt wait before it; the signal fences keep the compiler from moving
-// LDS accesses across it.
-__device__ __forceinline__ void barrier_only() {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  __builtin_amdgcn_s_barrier();
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-}
 
 // Scale bits with no branch on the dtype: always 16-bit loads (an fp32 scale is read
 // as its two halves), so no join waits for the loads before the epilogue needs them.
@@ -76,22 +51,6 @@ __device__ __forceinline__ float scale_bits_to_f32(uint32_t b, int dt) {
 }
 
 template <typename XT> __device__ __forceinline__ float xbits_to_f32(uint32_t b) { return to_f32(XT{(uint16_t)b}); }
-
-// vmcnt(A * FPW) for the largest A <= min(ahead, AMAX): wait until at most `ahead`
-// stages of this wave's loads are still in flight.
-template <int FPW, int AMAX> __device__ __forceinline__ void wait_stages(int ahead) {
-  if constexpr (AMAX > 0) {
-    if (ahead >= AMAX) {
-      wait_vmcnt<AMAX * FPW>();
-      return;
-    }
-    wait_stages<FPW, AMAX - 1>(ahead);
-  } else {
-    wait_vmcnt<0>();
-  }
-}
-
-constexpr int kLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
 
 template <typename XT, int BM, int BN, int P>
 __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
