@@ -29,6 +29,10 @@ int qtts_launch_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t 
 int qtts_launch_to_strips(const void* src, int64_t n, int64_t k, int64_t ld, void* dst, int kind, hipStream_t st);
 int qtts_launch_from_strips(const void* src, int64_t n, int64_t k, void* dst, int64_t ld, int kind, hipStream_t st);
 int64_t qtts_fp8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
+int qtts_fp8_fused_ok(int64_t m, int64_t n, int64_t k);
+int qtts_launch_fp8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
+                                 int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
+                                 hipStream_t st);
 
 static thread_local char g_last_error[512] = "";
 
@@ -271,6 +275,13 @@ static int fp8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, int
                "fp8_linear: leading dimension smaller than the row");
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(sw && y && (k == 0 || (x && qw)), "fp8_linear: null pointer");
+  // Decode rows on strip weights: quantization fused into the GEMM, one kernel, no
+  // workspace (an explicit split count or wave count keeps the two-kernel path).
+  if (layout == qtts::kLayoutStrips && (algo & 0xff) != QTTS_ALGO_TILE && (algo >> 8) == 0 && x_dtype != QTTS_F32 &&
+      (uintptr_t)x % 16 == 0 && ldx % 8 == 0 && qtts_fp8_fused_ok(m, n, k)) {
+    QTTS_TRY(current_device_check());
+    return qtts_launch_fp8_linear_fused(x, x_dtype, m, k, ldx, qw, n, sw, bias, y, ldy, div_mode, (hipStream_t)stream);
+  }
   // Layout: the GEMM's own workspace (split-K counters first) from the start, the
   // quantized activations and their scales at the end.
   const int64_t qx_bytes = al256(m * k), sx_bytes = al256(m * 4);

@@ -138,6 +138,16 @@ __device__ __forceinline__ uint32_t e4m3_encode(float f) {
   return s | ((e > 15 || code >= 0x7fu) ? 0x7fu : code);
 }
 
+// x / s, correctly rounded, from rs = RN(1/s): q0 = RN(x rs) is within an ulp of the
+// quotient, the residual x - q0 s is exact in one FMA, and one FMA step with rs
+// rounds the corrected quotient (Markstein's theorem).  An exact q0 (zero residual)
+// is returned as is, which keeps the sign of a zero quotient.
+__device__ __forceinline__ float div_by(float x, float s, float rs) {
+  const float q0 = x * rs;
+  const float r = __builtin_fmaf(-q0, s, x);
+  return r == 0.0f ? q0 : __builtin_fmaf(r, rs, q0);
+}
+
 // `num / c` with the reference's scalar-division semantics (qtts_div_mode).
 __device__ __forceinline__ float scalar_div(float num, float c, int div_mode) {
   return div_mode == QTTS_DIV_DEVICE ? num * (1.0f / c) : num / c;

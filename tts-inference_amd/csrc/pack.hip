@@ -80,6 +80,65 @@ __global__ __launch_bounds__(kPackThreads) void quant_act_fp8_kernel(
   if (threadIdx.x == 0) sx[r] = s;
 }
 
+// Vectorized quant_act_fp8_kernel for 16-bit activations with 16-byte aligned rows and
+// k % 8 == 0: every thread loads up to V 8-element vectors of its row at once (one
+// memory round trip), the row maximum goes through one LDS exchange, and the codes
+// come from a correctly rounded quotient (the row's reciprocal plus one FMA
+// correction) and v_cvt_pk_fp8_f32 -- the same codes as the scalar kernel.
+template <typename XT, int V>
+__global__ __launch_bounds__(kPackThreads) void quant_act_fp8_vec_kernel(
+    const XT* __restrict__ x, int64_t k, int64_t ld, uint8_t* __restrict__ qx,
+    float* __restrict__ sx, int div_mode) {
+  __shared__ float red[kPackThreads / 64];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nv = (int)(k >> 3);
+  const XT* row = x + r * ld;
+  i32x4_t v[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int idx = tid + kPackThreads * j;
+    v[j] = *(const i32x4_t*)(row + 8 * (int64_t)min(idx, nv - 1));  // clamped: in the row
+  }
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    if (tid + kPackThreads * j < nv) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t pr = (uint32_t)v[j][e];
+        mx = fmaxf(mx, fmaxf(fabsf(to_f32(XT{(uint16_t)pr})), fabsf(to_f32(XT{(uint16_t)(pr >> 16)}))));
+      }
+    }
+  }
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kPackThreads / 64; ++w) mx = fmaxf(mx, red[w]);
+  const float s = scalar_div(fmaxf(mx, round_through<XT>(1e-6f)), 448.0f, div_mode);
+  const float rs = 1.0f / s;
+  uint8_t* qrow = qx + r * k;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int idx = tid + kPackThreads * j;
+    if (idx < nv) {
+      uint32_t w[2];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t p0 = (uint32_t)v[j][2 * h], p1 = (uint32_t)v[j][2 * h + 1];
+        const uint32_t c01 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+            div_by(to_f32(XT{(uint16_t)p0}), s, rs), div_by(to_f32(XT{(uint16_t)(p0 >> 16)}), s, rs), 0, false);
+        const uint32_t c23 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(
+            div_by(to_f32(XT{(uint16_t)p1}), s, rs), div_by(to_f32(XT{(uint16_t)(p1 >> 16)}), s, rs), 0, false);
+        w[h] = (c01 & 0xffffu) | (c23 << 16);
+      }
+      *(uint2*)(qrow + 8 * (int64_t)idx) = make_uint2(w[0], w[1]);
+    }
+  }
+  if (tid == 0) sx[r] = s;
+}
+
 }  // namespace qtts
 
 using namespace qtts;
@@ -118,6 +177,23 @@ int qtts_launch_pack_fp8(const void* src, int src_dtype, int64_t n, int64_t k, i
 int qtts_launch_quant_act_fp8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld, uint8_t* qx,
                               float* sx, int div_mode, hipStream_t st) {
   dim3 grid((unsigned)m), block(kPackThreads);
+  const int64_t nv = k / 8;
+  if (x_dtype != QTTS_F32 && k % 8 == 0 && k > 0 && (uintptr_t)x % 16 == 0 && ld % 8 == 0 && (uintptr_t)qx % 8 == 0 &&
+      nv <= 4 * kPackThreads) {
+#define QTTS_QA_VEC(XT)                                                                                          \
+  do {                                                                                                           \
+    if (nv <= kPackThreads)                                                                                      \
+      qtts::launch(&quant_act_fp8_vec_kernel<XT, 1>, grid, block, 0, st, (const XT*)x, k, ld, qx, sx, div_mode); \
+    else if (nv <= 2 * kPackThreads)                                                                             \
+      qtts::launch(&quant_act_fp8_vec_kernel<XT, 2>, grid, block, 0, st, (const XT*)x, k, ld, qx, sx, div_mode); \
+    else                                                                                                         \
+      qtts::launch(&quant_act_fp8_vec_kernel<XT, 4>, grid, block, 0, st, (const XT*)x, k, ld, qx, sx, div_mode); \
+  } while (0)
+    if (x_dtype == QTTS_BF16) QTTS_QA_VEC(bf16_t);
+    else QTTS_QA_VEC(f16_t);
+#undef QTTS_QA_VEC
+    return qtts_check_launch("quant_act_fp8_rows");
+  }
   if (x_dtype == QTTS_F32) qtts::launch(&quant_act_fp8_kernel<float>, dim3(grid), dim3(block), 0, st, (const float*)x, k, ld, qx, sx, div_mode);
   else if (x_dtype == QTTS_BF16) qtts::launch(&quant_act_fp8_kernel<bf16_t>, dim3(grid), dim3(block), 0, st, (const bf16_t*)x, k, ld, qx, sx, div_mode);
   else qtts::launch(&quant_act_fp8_kernel<f16_t>, dim3(grid), dim3(block), 0, st, (const f16_t*)x, k, ld, qx, sx, div_mode);

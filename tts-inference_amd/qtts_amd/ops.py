@@ -351,10 +351,33 @@ def w8a8_fp8_gemm_strips(qx: torch.Tensor, sx: torch.Tensor, qws: torch.Tensor, 
 def fp8_linear_strips(x: torch.Tensor, qws: torch.Tensor, n: int, sw: torch.Tensor,
                       bias: torch.Tensor | None = None, div_mode: int = DIV_DEVICE,
                       algo: int = ALGO_AUTO) -> torch.Tensor:
-    """Fp8Method.apply (qtts/quant/fp8.py:72-89) with the e4m3 weight in the strip layout."""
+    """Fp8Method.apply (qtts/quant/fp8.py:72-89) with the e4m3 weight in the strip layout.
+
+    One C call: decode rows (M <= 16) run a single kernel that quantizes x per token
+    inside the GEMM; other rows quantize into the workspace first.
+    """
     shape = x.shape
-    qx, sx = quant_act_fp8(x, div_mode)
-    out = w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, bias, x.dtype, algo)
+    a = _flatten(x)
+    rows, k = a.shape
+    if qws.numel() != strip_bytes(n, k, STRIP_FP8):
+        raise ValueError(f"weight is not an e4m3 strip-layout [{n}, {k}] buffer")
+    if sw.numel() != n:
+        raise ValueError(f"scale has {sw.numel()} entries for {n} output channels")
+    if bias is not None:
+        if bias.numel() != n:
+            raise ValueError(f"bias has {bias.numel()} entries for {n} output channels")
+        bias = bias.to(a.dtype).contiguous()
+    if a.data_ptr() % 16 or (rows > 1 and a.stride(0) % 8):
+        a = a.contiguous() if a.data_ptr() % 16 == 0 else a.clone()
+    sw = sw.reshape(-1).to(torch.float32).contiguous()
+    dev = _require_cuda(a, qws, sw, bias)
+    out = torch.empty((rows, n), dtype=a.dtype, device=dev)
+    reserve_workspace(dev, workspace_bytes(OP_FP8_LINEAR, rows, n, k, algo))
+    ws, ws_n = _ws_for(dev)
+    st = _lib.load().qtts_fp8_linear_strips(
+        _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else k, _ptr(qws), n, _ptr(sw), _ptr(bias),
+        _ptr(out), n, div_mode, algo, ws, ws_n, _stream(dev))
+    _lib.check(st, "fp8_linear_strips")
     return out.reshape(*shape[:-1], n)
 
 
