@@ -529,3 +529,34 @@ def test_fp8_linear_fused_matches_two_kernel_path(ops, n, k):
     qx, sx = ops.quant_act_fp8(x, ops.DIV_IEEE)
     two = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, None, torch.float16, ops.algo_code(1, 1, waves))
     assert torch.equal(y, two), f"fused fp16 / IEEE differs: n={n} k={k}"
+
+
+@pytest.mark.parametrize("n,k", TALKER + PREDICTOR)
+def test_w8a16_strips_skinny_blocks(ops, n, k):
+    """The skinny kernel with 2 and 4 m-blocks (17 <= M <= 64 on strip weights): the automatic choice and
+    every built (waves, chunks) pair, forced splits, bias, against the oracle."""
+    for m in (17, 24, 32, 33, 48, 64):
+        print(f"skinny blocks n={n} k={k} m={m}", flush=True)
+        x, w, b = _make(m, n, k, bias=(m % 2 == 0), seed=n + 11 * m + k)
+        q, s = ops.pack_int8(w, torch.bfloat16)
+        qs = ops.to_strips(q)
+        ref = _oracle_w8a16(x, q, s, b)
+        assert_close(ops.w8a16_gemm_strips(x, qs, n, s, b), ref, f"auto m={m} n={n} k={k}")
+        combos = ((1, 4, 8), (1, 8, 8), (1, 16, 4), (2, 8, 4), (3, 4, 8)) if m <= 32 else ((1, 8, 4), (2, 4, 4), (3, 8, 4))
+        for splits, waves, cpw in combos:
+            y = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, splits, waves, cpw))
+            assert_close(y, ref, f"skinny m={m} n={n} k={k} S={splits} W={waves} C={cpw}")
+
+
+def test_w8a16_strips_skinny_blocks_dtypes(ops):
+    for sdt, xdt in ((torch.float32, torch.bfloat16), (torch.float16, torch.float16)):
+        for m in (20, 40):
+            x, w, b = _make(m, 1000, 1024, dtype=xdt, bias=True, seed=m + 7)
+            q, s = ops.pack_int8(w, sdt)
+            qs = ops.to_strips(q)
+            assert_close(ops.w8a16_gemm_strips(x, qs, 1000, s, b), _oracle_w8a16(x, q, s, b),
+                         f"skinny blocks m={m} scale={sdt} x={xdt}")
+    x, w, _ = _make(65, 64, 128)
+    q, s = ops.pack_int8(w, torch.bfloat16)
+    with pytest.raises(ValueError, match="M <= 64"):
+        ops.w8a16_gemm_strips(x, ops.to_strips(q), 64, s, None, ops.algo_code(1))

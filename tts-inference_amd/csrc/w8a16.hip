@@ -65,17 +65,19 @@ __device__ __forceinline__ void store_out(XT* __restrict__ y, int64_t ldy, int m
 }
 
 // ------------------------------------------------------------------------------------
-// skinny: M <= 16
+// skinny: M <= 16 * MB (MB m-blocks of 16 activation rows; MB > 1 on strip weights
+// with K % 64 == 0 only)
 // ------------------------------------------------------------------------------------
 
-template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK>
+template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1>
 __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ q, int N, int64_t ldq,
     const ST* scale, const XT* bias, XT* __restrict__ y, int64_t ldy,
     float* __restrict__ part, unsigned* __restrict__ counters, int strips, int S, int cps) {
   typedef mfma16<XT> MM;
   typedef typename MM::vec V;
-  __shared__ f32x4_t red[W > 1 ? W - 1 : 1][64];
+  static_assert(MB == 1 || (FULLK && LAYOUT == kLayoutStrips), "several m-blocks need full-K strip weights");
+  __shared__ f32x4_t red[W > 1 ? W - 1 : 1][MB][64];
 
   int strip, split;
   decode_wg(blockIdx.x, S, strip, split);
@@ -100,34 +102,42 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     wp = q + (int64_t)(n_ok ? n : 0) * ldq + 16 * g;
     wstride = 64;
   }
-  const XT* xp = x + (int64_t)(m_ok ? r : 0) * ldx + 16 * g;
+  // Activation row r + 16 mb of each m-block; rows past M read row 0 (full K) or are
+  // zero (ragged K): they only feed D columns that are never stored.
+  const XT* xp[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) xp[mb] = x + (int64_t)(r + 16 * mb < M ? r + 16 * mb : 0) * ldx + 16 * g;
   const i32x4_t zero = {0, 0, 0, 0};
 
   // A group of CPW chunks is issued in full before any of it is consumed.  With
   // FULLK (K % 64 == 0, strip layout) the loads are branch-free: chunk indices past
-  // the wave's range are clamped to its last chunk (consume skips them), and rows of
-  // x past M read row 0 instead (they only feed D columns that are never stored).
-  i32x4_t w[CPW], xa[CPW], xb[CPW];
+  // the wave's range are clamped to its last chunk (consume zeroes their weights).
+  i32x4_t w[CPW], xa[MB][CPW], xb[MB][CPW];
   auto issue = [&](int base) {
 #pragma unroll
     for (int u = 0; u < CPW; ++u) {
       if constexpr (FULLK) {
         const int c = min(base + u, wc1 - 1);
         w[u] = *(const i32x4_t*)(wp + (int64_t)c * wstride);
-        xa[u] = *(const i32x4_t*)(xp + (int64_t)c * 64);
-        xb[u] = *(const i32x4_t*)(xp + (int64_t)c * 64 + 8);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          xa[mb][u] = *(const i32x4_t*)(xp[mb] + (int64_t)c * 64);
+          xb[mb][u] = *(const i32x4_t*)(xp[mb] + (int64_t)c * 64 + 8);
+        }
       } else {
         const int c = base + u;
         const bool live = c < wc1;  // wave-uniform
         const bool kin = c * 64 + 16 * g < K;
         if (LAYOUT == kLayoutStrips) w[u] = live ? *(const i32x4_t*)(wp + (int64_t)c * wstride) : zero;
         else w[u] = (live && n_ok && kin) ? *(const i32x4_t*)(wp + (int64_t)c * wstride) : zero;
-        xa[u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp + (int64_t)c * 64) : zero;
-        xb[u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp + (int64_t)c * 64 + 8) : zero;
+        xa[0][u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp[0] + (int64_t)c * 64) : zero;
+        xb[0][u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp[0] + (int64_t)c * 64 + 8) : zero;
       }
     }
   };
-  f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x4_t acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   auto consume = [&](int base) {
 #pragma unroll
     for (int u = 0; u < CPW; ++u) {
@@ -138,13 +148,15 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
         const i32x4_t wv = live ? w[u] : zero;
         const V wlo = MM::from_i8((uint32_t)wv[0], (uint32_t)wv[1]);
         const V whi = MM::from_i8((uint32_t)wv[2], (uint32_t)wv[3]);
-        acc = MM::mma(wlo, __builtin_bit_cast(V, xa[u]), acc);
-        acc = MM::mma(whi, __builtin_bit_cast(V, xb[u]), acc);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[mb] = MM::mma(wlo, __builtin_bit_cast(V, xa[mb][u]), acc[mb]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[mb] = MM::mma(whi, __builtin_bit_cast(V, xb[mb][u]), acc[mb]);
       } else if (base + u < wc1) {
         const V wlo = MM::from_i8((uint32_t)w[u][0], (uint32_t)w[u][1]);
         const V whi = MM::from_i8((uint32_t)w[u][2], (uint32_t)w[u][3]);
-        acc = MM::mma(wlo, __builtin_bit_cast(V, xa[u]), acc);
-        acc = MM::mma(whi, __builtin_bit_cast(V, xb[u]), acc);
+        acc[0] = MM::mma(wlo, __builtin_bit_cast(V, xa[0][u]), acc[0]);
+        acc[0] = MM::mma(whi, __builtin_bit_cast(V, xb[0][u]), acc[0]);
       }
     }
   };
@@ -174,31 +186,46 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   }
 
   if (W > 1) {
-    if (wave > 0) red[wave - 1][lane] = acc;
+    if (wave > 0) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) red[wave - 1][mb][lane] = acc[mb];
+    }
     __syncthreads();
     if (wave > 0) return;
 #pragma unroll
-    for (int w = 0; w < W - 1; ++w) acc += red[w][lane];
+    for (int w = 0; w < W - 1; ++w)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[mb] += red[w][mb][lane];
   }
 
   if (S > 1) {
-    float a[4] = {acc[0], acc[1], acc[2], acc[3]};
+    float a[4 * MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[4 * mb + i] = acc[mb][i];
     // Only wave 0 is left: the meeting has 64 participants per workgroup.
-    if (!splitk_meet<4>(a, part + (int64_t)strip * S * 64 * 4, &counters[strip], S, split, lane, 64, nullptr))
+    if (!splitk_meet<4 * MB>(a, part + (int64_t)strip * S * 64 * 4 * MB, &counters[strip], S, split, lane, 64,
+                             nullptr))
       return;
-    acc = f32x4_t{a[0], a[1], a[2], a[3]};
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{a[4 * mb], a[4 * mb + 1], a[4 * mb + 2], a[4 * mb + 3]};
   }
 
   // D layout of the 16x16 MFMA: lane (r, g) holds rows 4g..4g+3 (weight rows n) of
-  // column r (activation row m).
-  if (m_ok) {
+  // column r (activation row m = r + 16 mb).
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int nn = strip * 16 + 4 * g + i;
-      if (nn < N) {
-        float v = acc[i] * bits_to_f32<ST>(sc[i]);
-        if (bias) v += bits_to_f32<XT>(bi[i]);
-        y[(int64_t)r * ldy + nn] = from_f32<XT>(v);
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = r + 16 * mb;
+    if (m < M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int nn = strip * 16 + 4 * g + i;
+        if (nn < N) {
+          float v = acc[mb][i] * bits_to_f32<ST>(sc[i]);
+          if (bias) v += bits_to_f32<XT>(bi[i]);
+          y[(int64_t)m * ldy + nn] = from_f32<XT>(v);
+        }
       }
     }
   }
@@ -384,29 +411,46 @@ using namespace qtts;
 
 namespace {
 
-struct SkinnyCfg { int waves, cpw, S, cps, strips; };
+struct SkinnyCfg { int mb, waves, cpw, S, cps, strips; };
 struct TileCfg { int bm, S, cps, mtiles, ntiles; };
 
-// Chunks (64 columns, 1 KiB of a strip) a wave keeps in flight at once.  Instantiated
-// as 4 or 8 for workgroups of up to 8 waves and 4 or 6 for 16 waves (1024 threads
-// leave 128 VGPRs per lane).
-constexpr int kSkinnyCPWMax = 8, kSkinnyCPWMax16 = 6;
+// The skinny kernels take up to kSkinnyMaxM rows on strip weights.  The automatic
+// choice keeps them up to 32 rows (two m-blocks) for weights of at most 9 MiB and
+// otherwise moves to the tile kernel past 16 rows: measured on the talker and
+// code-predictor shapes at M = 16..96, where the tile kernel wins on the 12-25 MB
+// weights from 24 rows and everywhere from 48.
+constexpr int kSkinnyMaxM = 64, kSkinnyAutoMaxM = 32;
+constexpr int64_t kSkinnyAutoMaxBytes = 9 << 20;
 
-bool skinny_cpw_ok(int w, int cpw) { return w == 16 ? (cpw == 4 || cpw == 6) : (cpw == 4 || cpw == 8); }
+// m-blocks of 16 activation rows a skinny call carries.
+int skinny_mb(int64_t m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
 
-SkinnyCfg skinny_cfg(int64_t n, int64_t k, int splits_req, int waves_req, int cpw_req) {
+// Chunks (64 columns, 1 KiB of a strip) a wave keeps in flight at once; a chunk holds
+// 4 + 8 MB registers a lane.  Built: MB = 1: 4 or 8 (4 or 6 at 16 waves, whose 1024
+// threads leave 128 registers a lane); MB = 2: 4 or 8 (4 at 16 waves); MB = 4: 4, at
+// most 8 waves.
+bool skinny_cpw_ok(int mb, int w, int cpw) {
+  if (mb == 1) return w == 16 ? (cpw == 4 || cpw == 6) : (cpw == 4 || cpw == 8);
+  if (mb == 2) return w == 16 ? cpw == 4 : (cpw == 4 || cpw == 8);
+  return mb == 4 && w <= 8 && cpw == 4;
+}
+int skinny_cpw_max(int mb, int w) { return mb == 1 ? (w == 16 ? 6 : 8) : (mb == 2 ? (w == 16 ? 4 : 8) : 4); }
+int skinny_waves_max(int mb) { return mb == 4 ? 8 : 16; }
+
+SkinnyCfg skinny_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int waves_req, int cpw_req) {
   SkinnyCfg c;
+  c.mb = skinny_mb(m);
   c.strips = (int)((n + 15) / 16);
   const int nchunks = std::max(1, (int)((k + 63) / 64));
   int W = waves_req, S = splits_req, C = cpw_req;
   if (W <= 0) {
-    // Few, fat waves: the fewest waves (of 8 chunks in flight each, 6 at 16 waves)
-    // that cover a strip's K without a split.  Measured on the talker and code-
-    // predictor shapes this beats more, thinner waves at every M in 1..16.
+    // Few, fat waves: the fewest waves (with the most chunks in flight each) that
+    // cover a strip's K without a split.  Measured on the talker and code-predictor
+    // shapes this beats more, thinner waves at every M in 1..16.
     W = 1;
-    while (W < 16 && W * kSkinnyCPWMax < nchunks) W *= 2;
+    while (W < skinny_waves_max(c.mb) && W * skinny_cpw_max(c.mb, W) < nchunks) W *= 2;
   }
-  if (C <= 0) C = W == 16 ? kSkinnyCPWMax16 : kSkinnyCPWMax;
+  if (C <= 0) C = skinny_cpw_max(c.mb, W);
   c.waves = W;
   c.cpw = C;
   // The kernel runs one group of C chunks per wave: raise S until a wave's share
@@ -438,7 +482,9 @@ TileCfg tile_cfg(int64_t m, int64_t n, int64_t k, int splits_req) {
   return c;
 }
 
-int64_t skinny_ws(const SkinnyCfg& c) { return c.S <= 1 ? 0 : kCounterBytes + (int64_t)c.strips * c.S * 64 * 4 * 4; }
+int64_t skinny_ws(const SkinnyCfg& c) {
+  return c.S <= 1 ? 0 : kCounterBytes + (int64_t)c.strips * c.S * 64 * 4 * c.mb * 4;
+}
 
 int64_t tile_ws(const TileCfg& c) {
   if (c.S <= 1) return 0;
@@ -460,7 +506,7 @@ int64_t qtts_w8a16_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
   int64_t ws = 0;
   const int cpw = (algo >> 24) & 0xff;
   if (family == QTTS_ALGO_SKINNY || family == QTTS_ALGO_AUTO)
-    ws = std::max(ws, skinny_ws(skinny_cfg(n, k, splits, waves, cpw)));
+    ws = std::max(ws, skinny_ws(skinny_cfg(std::min<int64_t>(m, kSkinnyMaxM), n, k, splits, waves, cpw)));
   if (family == QTTS_ALGO_TILE || (family == QTTS_ALGO_AUTO && m > 16)) {
     ws = std::max(ws, tile_ws(tile_cfg(m, n, k, splits)));
     if (k % 64 == 0) ws = std::max(ws, qtts_w8a16_pipe_ws_bytes(m, n, k, splits, (algo >> 24) & 0xff));
@@ -474,24 +520,31 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
                        int64_t ws_bytes, hipStream_t st) {
   int family = algo & 0xff;
   const int splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff;
-  if (family == QTTS_ALGO_AUTO) family = m <= 16 ? QTTS_ALGO_SKINNY : QTTS_ALGO_TILE;
-  if (family == QTTS_ALGO_SKINNY && m > 16)
-    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "skinny W8A16 kernel handles M <= 16, got M=%lld", (long long)m);
+  const bool wide_ok = LAYOUT == kLayoutStrips && k % 64 == 0;  // skinny beyond 16 rows
+  if (family == QTTS_ALGO_AUTO)
+    family = (m <= 16 || (wide_ok && m <= kSkinnyAutoMaxM && n * k <= kSkinnyAutoMaxBytes)) ? QTTS_ALGO_SKINNY
+                                                                                          : QTTS_ALGO_TILE;
+  if (family == QTTS_ALGO_SKINNY && m > 16 && !(wide_ok && m <= kSkinnyMaxM))
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
+                          "skinny W8A16 kernel handles M <= 16 (M <= %d on strip weights with K %% 64 == 0), got M=%lld",
+                          kSkinnyMaxM, (long long)m);
   unsigned* counters = (unsigned*)ws;
   float* part = ws ? (float*)((char*)ws + kCounterBytes) : nullptr;
   if (family == QTTS_ALGO_SKINNY) {
     const int cpw = (algo >> 24) & 0xff;
-    SkinnyCfg c = skinny_cfg(n, k, splits, waves, cpw);
-    if (!skinny_cpw_ok(c.waves, c.cpw))
-      return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: %d chunks per wave is not built for %d waves",
-                            c.cpw, c.waves);
+    SkinnyCfg c = skinny_cfg(m, n, k, splits, waves, cpw);
+    if (!skinny_cpw_ok(c.mb, c.waves, c.cpw))
+      return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
+                            "w8a16 skinny: %d chunks per wave is not built for %d waves and %d m-blocks", c.cpw,
+                            c.waves, c.mb);
     const int64_t need = skinny_ws(c);
     if (need > ws_bytes || (need > 0 && !ws)) {
       if (splits > 0)
         return qtts_set_error(QTTS_ERR_WORKSPACE, "w8a16 skinny with %d splits needs %lld workspace bytes, got %lld",
                               c.S, (long long)need, (long long)ws_bytes);
       // No room for a split: give each wave a longer run instead.
-      c = skinny_cfg(n, k, 1, 16, c.waves == 16 ? kSkinnyCPWMax16 : c.cpw);
+      const int wmax = skinny_waves_max(c.mb);
+      c = skinny_cfg(m, n, k, 1, wmax, skinny_cpw_max(c.mb, wmax));
       if (c.S > 1)
         return qtts_set_error(QTTS_ERR_WORKSPACE, "w8a16 skinny: K=%lld needs a split-K workspace of %lld bytes",
                               (long long)k, (long long)skinny_ws(c));
@@ -501,39 +554,66 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
                             "output strips than the workspace counter block holds", (long long)n, (long long)k);
     const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8 * c.S;
     if (!grid_ok(blocks)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16: N too large");
-#define QTTS_SKINNY_T(ST, W, CPW)                                                                             \
-  do {                                                                                                        \
-    if (LAYOUT == kLayoutStrips && k % 64 == 0)                                                               \
-      qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, true>, dim3((unsigned)blocks), dim3(W * 64), 0, st,                  \
-          x, (int)m, (int)k, ldx, q, (int)n, ldq, (const ST*)scale, bias, y, ldy, part, counters, c.strips, c.S, \
-          c.cps);                                                                                             \
-    else                                                                                                      \
-      qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, false>, dim3((unsigned)blocks), dim3(W * 64), 0, st,                 \
-          x, (int)m, (int)k, ldx, q, (int)n, ldq, (const ST*)scale, bias, y, ldy, part, counters, c.strips, c.S, \
-          c.cps);                                                                                             \
+#define QTTS_SK(ST, W, CPW, FK, MBV)                                                                              \
+  qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, FK, MBV>, dim3((unsigned)blocks), dim3(W * 64), 0, st, \
+               x, (int)m, (int)k, ldx, q, (int)n, ldq, (const ST*)scale, bias, y, ldy, part, counters, c.strips,    \
+               c.S, c.cps)
+#define QTTS_SK_ST(W, CPW, FK, MBV)                           \
+  do {                                                        \
+    if (sdt == QTTS_BF16) QTTS_SK(bf16_t, W, CPW, FK, MBV);   \
+    else if (sdt == QTTS_F16) QTTS_SK(f16_t, W, CPW, FK, MBV); \
+    else QTTS_SK(float, W, CPW, FK, MBV);                     \
   } while (0)
-#define QTTS_SKINNY(W, CPW)                                         \
-  do {                                                              \
-    if (sdt == QTTS_BF16) QTTS_SKINNY_T(bf16_t, W, CPW);            \
-    else if (sdt == QTTS_F16) QTTS_SKINNY_T(f16_t, W, CPW);         \
-    else QTTS_SKINNY_T(float, W, CPW);                              \
+#define QTTS_SK1(W, CPW)                                                 \
+  do {                                                                   \
+    if (wide_ok) QTTS_SK_ST(W, CPW, true, 1);                            \
+    else QTTS_SK_ST(W, CPW, false, 1);                                   \
   } while (0)
-    switch (c.waves * 16 + c.cpw) {
-      case 1 * 16 + 4: QTTS_SKINNY(1, 4); break;
-      case 1 * 16 + 8: QTTS_SKINNY(1, 8); break;
-      case 2 * 16 + 4: QTTS_SKINNY(2, 4); break;
-      case 2 * 16 + 8: QTTS_SKINNY(2, 8); break;
-      case 4 * 16 + 4: QTTS_SKINNY(4, 4); break;
-      case 4 * 16 + 8: QTTS_SKINNY(4, 8); break;
-      case 8 * 16 + 4: QTTS_SKINNY(8, 4); break;
-      case 8 * 16 + 8: QTTS_SKINNY(8, 8); break;
-      case 16 * 16 + 4: QTTS_SKINNY(16, 4); break;
-      case 16 * 16 + 6: QTTS_SKINNY(16, 6); break;
-      default:
-        return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: waves per workgroup must be 1, 2, 4, 8 or 16");
+    const int key = c.waves * 16 + c.cpw;
+    if (c.mb == 1) {
+      switch (key) {
+        case 1 * 16 + 4: QTTS_SK1(1, 4); break;
+        case 1 * 16 + 8: QTTS_SK1(1, 8); break;
+        case 2 * 16 + 4: QTTS_SK1(2, 4); break;
+        case 2 * 16 + 8: QTTS_SK1(2, 8); break;
+        case 4 * 16 + 4: QTTS_SK1(4, 4); break;
+        case 4 * 16 + 8: QTTS_SK1(4, 8); break;
+        case 8 * 16 + 4: QTTS_SK1(8, 4); break;
+        case 8 * 16 + 8: QTTS_SK1(8, 8); break;
+        case 16 * 16 + 4: QTTS_SK1(16, 4); break;
+        case 16 * 16 + 6: QTTS_SK1(16, 6); break;
+        default:
+          return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: waves per workgroup must be 1, 2, 4, 8 or 16");
+      }
+    } else if constexpr (LAYOUT == kLayoutStrips) {
+      if (c.mb == 2) {
+        switch (key) {
+          case 1 * 16 + 4: QTTS_SK_ST(1, 4, true, 2); break;
+          case 1 * 16 + 8: QTTS_SK_ST(1, 8, true, 2); break;
+          case 2 * 16 + 4: QTTS_SK_ST(2, 4, true, 2); break;
+          case 2 * 16 + 8: QTTS_SK_ST(2, 8, true, 2); break;
+          case 4 * 16 + 4: QTTS_SK_ST(4, 4, true, 2); break;
+          case 4 * 16 + 8: QTTS_SK_ST(4, 8, true, 2); break;
+          case 8 * 16 + 4: QTTS_SK_ST(8, 4, true, 2); break;
+          case 8 * 16 + 8: QTTS_SK_ST(8, 8, true, 2); break;
+          case 16 * 16 + 4: QTTS_SK_ST(16, 4, true, 2); break;
+          default:
+            return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: unsupported waves/chunks for 2 m-blocks");
+        }
+      } else {
+        switch (key) {
+          case 1 * 16 + 4: QTTS_SK_ST(1, 4, true, 4); break;
+          case 2 * 16 + 4: QTTS_SK_ST(2, 4, true, 4); break;
+          case 4 * 16 + 4: QTTS_SK_ST(4, 4, true, 4); break;
+          case 8 * 16 + 4: QTTS_SK_ST(8, 4, true, 4); break;
+          default:
+            return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: unsupported waves/chunks for 4 m-blocks");
+        }
+      }
     }
-#undef QTTS_SKINNY
-#undef QTTS_SKINNY_T
+#undef QTTS_SK1
+#undef QTTS_SK_ST
+#undef QTTS_SK
     return qtts_check_launch("w8a16_skinny");
   }
   if (LAYOUT == kLayoutStrips && k % 64 == 0)

@@ -52,16 +52,21 @@ def quantize_weight_per_channel(weight: torch.Tensor, div_mode: int = _lib.DIV_D
 
 
 def _candidates(rows: int) -> dict[str, int]:
-    """Kernel configurations worth timing at ``rows``."""
-    if rows <= 16:
-        c = {"skinny": _lib.algo_code(_lib.ALGO_SKINNY)}
+    """Kernel configurations worth timing at ``rows`` (the algo bits of include/qtts_amd.h)."""
+    c: dict[str, int] = {}
+    if rows <= 64:  # skinny: up to 16 rows, or 64 on strip weights
+        c["skinny"] = _lib.algo_code(_lib.ALGO_SKINNY)
         for s in (1, 2, 4):
             for w in (4, 8, 16):
                 c[f"skinny_s{s}_w{w}"] = _lib.algo_code(_lib.ALGO_SKINNY, splits=s, waves=w)
-        return c
-    c = {"tile": _lib.algo_code(_lib.ALGO_TILE)}
-    for s in (1, 2, 4):
-        c[f"tile_s{s}"] = _lib.algo_code(_lib.ALGO_TILE, splits=s)
+    if rows > 16:  # tile: split counts, stages and tile shapes (BM 32/64/128 x BN 64/128)
+        c["tile"] = _lib.algo_code(_lib.ALGO_TILE)
+        for s in (1, 2, 4):
+            c[f"tile_s{s}"] = _lib.algo_code(_lib.ALGO_TILE, splits=s)
+        for bm in (1, 2, 3):
+            for bn in (1, 2):
+                for p in (3, 4):
+                    c[f"tile_bm{16 << bm}_bn{32 << bn}_p{p}"] = _lib.algo_code(_lib.ALGO_TILE, 0, p, bm | (bn << 4))
     return c
 
 
