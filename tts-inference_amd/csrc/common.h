@@ -70,19 +70,34 @@ template <typename T> __device__ __forceinline__ float round_through(float v) { 
 
 // ---- int8 -> 16-bit float vectors for the MFMA operands ---------------------------
 // Every int8 value is exact in bf16 and fp16.  Each byte goes through one
-// v_cvt_f32_i32 with an SDWA sign-extended byte select, then pairs are packed.
+// v_cvt_f32_i32 with an SDWA sign-extended byte select (written out: the compiler
+// shifts bytes 1 and 3 first, an extra instruction each), then pairs are rounded
+// into bf16 by one v_cvt_pk_bf16_f32 (exact: the floats are small integers).
+
+template <int B> __device__ __forceinline__ float sbyte_to_f32(uint32_t w) {
+  float r;
+  if constexpr (B == 0)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0" : "=v"(r) : "v"(w));
+  else if constexpr (B == 1)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1" : "=v"(r) : "v"(w));
+  else if constexpr (B == 2)
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2" : "=v"(r) : "v"(w));
+  else
+    asm("v_cvt_f32_i32_sdwa %0, sext(%1) dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3" : "=v"(r) : "v"(w));
+  return r;
+}
+
+__device__ __forceinline__ uint32_t sbytes_to_bf16x2(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t{a, b}), bf16x2_t));
+}
 
 __device__ __forceinline__ bf16x8_t i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
-  bf16x8_t r;
-  r[0] = (__bf16)(float)(int8_t)(lo);
-  r[1] = (__bf16)(float)(int8_t)(lo >> 8);
-  r[2] = (__bf16)(float)(int8_t)(lo >> 16);
-  r[3] = (__bf16)(float)(int8_t)(lo >> 24);
-  r[4] = (__bf16)(float)(int8_t)(hi);
-  r[5] = (__bf16)(float)(int8_t)(hi >> 8);
-  r[6] = (__bf16)(float)(int8_t)(hi >> 16);
-  r[7] = (__bf16)(float)(int8_t)(hi >> 24);
-  return r;
+  typedef __attribute__((ext_vector_type(4))) uint32_t u4;
+  const u4 v = {sbytes_to_bf16x2(sbyte_to_f32<0>(lo), sbyte_to_f32<1>(lo)),
+                sbytes_to_bf16x2(sbyte_to_f32<2>(lo), sbyte_to_f32<3>(lo)),
+                sbytes_to_bf16x2(sbyte_to_f32<0>(hi), sbyte_to_f32<1>(hi)),
+                sbytes_to_bf16x2(sbyte_to_f32<2>(hi), sbyte_to_f32<3>(hi))};
+  return __builtin_bit_cast(bf16x8_t, v);
 }
 
 __device__ __forceinline__ f16x8_t i8x8_to_f16x8(uint32_t lo, uint32_t hi) {

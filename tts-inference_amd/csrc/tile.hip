@@ -14,9 +14,12 @@
 // int8 half h of a weight fragment pairs with activation half h: together they
 // cover the stage's 64 K columns in two v_mfma_f32_16x16x32 steps.
 //
-// Wave w owns output columns [n0 + w BN/4, n0 + (w+1) BN/4) for all BM rows, so
-// each weight fragment is dequantized (int8 -> bf16, exact) by exactly one wave
-// and feeds 2 * BM/16 MFMAs.  Rows past M and strips past N are read clamped and
+// The 4 waves form a WM x (4/WM) grid over the tile.  With WM = 1 each wave owns
+// BN/4 output columns for all BM rows, so each weight fragment is dequantized
+// (int8 -> bf16, exact) by exactly one wave, but every wave reads all of the tile's
+// activation fragments from LDS; WM = 2 halves those activation reads (LDS
+// bandwidth, not the matrix cores, bounds the 1 x 4 grid on the larger tiles) at the
+// cost of dequantizing each weight fragment twice.  Rows past M and strips past N are read clamped and
 // never stored; K must be a multiple of 64 (the strip layout pads N, not K).
 //
 // Tiles are numbered n-fastest, and the dispatcher deals consecutive workgroups to
@@ -52,21 +55,24 @@ __device__ __forceinline__ float scale_bits_to_f32(uint32_t b, int dt) {
 
 template <typename XT> __device__ __forceinline__ float xbits_to_f32(uint32_t b) { return to_f32(XT{(uint16_t)b}); }
 
-template <typename XT, int BM, int BN, int P>
+template <typename XT, int BM, int BN, int P, int WM>
 __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ qs, int N,
     const void* __restrict__ scale, int sdt, const XT* __restrict__ bias, XT* __restrict__ y, int64_t ldy,
     float* __restrict__ part, unsigned* __restrict__ counters, int mtiles, int ntiles, int S, int cps) {
   typedef mfma16<XT> MM;
   typedef typename MM::vec V;
-  constexpr int MB = BM / 16;          // 16-row m-blocks per tile
-  constexpr int NB = BN / 64;          // 16-column strips per wave
-  constexpr int XF = 2 * MB;           // activation fragments per stage
+  constexpr int WN = 4 / WM;           // the 4 waves form a WM x WN grid over the tile
+  constexpr int TMB = BM / 16;         // 16-row m-blocks per tile
+  constexpr int MB = TMB / WM;         // 16-row m-blocks per wave
+  constexpr int NB = BN / 16 / WN;     // 16-column strips per wave
+  constexpr int XF = 2 * TMB;          // activation fragments per stage
   constexpr int WF = BN / 16;          // weight fragments per stage
   constexpr int F = XF + WF;
   constexpr int FPW = F / 4;           // fragments each wave loads per stage
   constexpr int SB = F * 1024;         // stage bytes
   static_assert(F % 4 == 0, "fragments must split evenly over 4 waves");
+  static_assert((WM == 1 || WM == 2) && MB >= 1 && NB >= 1, "wave grid must cover the tile");
   static_assert(P >= 2 && P * SB + 64 <= kLdsBytes, "stage ring must fit in LDS");
   static_assert((P - 2) * FPW < 64, "vmcnt is 6 bits");
   __shared__ __align__(1024) uint8_t ring[P * SB];
@@ -79,6 +85,7 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
   const int m0 = mt * BM, n0 = nt * BN;
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int wm = wave / WN, wn = wave % WN;  // this wave's m-blocks wm*MB.., strips wn*NB..
   const int c16 = lane & 15, g = lane >> 4;
   const int nchunks = K >> 6;
   const int strips = (N + 15) >> 4;
@@ -94,7 +101,7 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
       for (int t = 0; t < 4; ++t) {
-        const int n = min(n0 + (wave * NB + nb) * 16 + 4 * g + t, N - 1);
+        const int n = min(n0 + (wn * NB + nb) * 16 + 4 * g + t, N - 1);
         scb[nb][t] = load_scale_bits(scale, sdt, n);
         bib[nb][t] = __hip_atomic_load((uint16_t*)bsrc + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
       }
@@ -129,21 +136,35 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
+  // One stage: every operand read from LDS first, then strip by strip the MFMAs of
+  // strip nb, with the dequantization of strip nb+1 issued ahead of them (independent
+  // VALU work the wave can issue while the matrix pipe runs), h = 0 before h = 1 so
+  // that consecutive MFMAs never share an accumulator.
   auto compute = [&](const uint8_t* stage) {
     V xa[MB][2];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) xa[mb][h] = *(const V*)(stage + (2 * mb + h) * 1024 + lane * 16);
+      for (int h = 0; h < 2; ++h) xa[mb][h] = *(const V*)(stage + (2 * (wm * MB + mb) + h) * 1024 + lane * 16);
+    i32x4_t wq[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) wq[nb] = *(const i32x4_t*)(stage + (XF + wn * NB + nb) * 1024 + lane * 16);
+    V cur[2], nxt[2];
+    cur[0] = MM::from_i8((uint32_t)wq[0][0], (uint32_t)wq[0][1]);
+    cur[1] = MM::from_i8((uint32_t)wq[0][2], (uint32_t)wq[0][3]);
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
-      const i32x4_t wq = *(const i32x4_t*)(stage + (XF + wave * NB + nb) * 1024 + lane * 16);
-      const V lo = MM::from_i8((uint32_t)wq[0], (uint32_t)wq[1]);
-      const V hi = MM::from_i8((uint32_t)wq[2], (uint32_t)wq[3]);
+      if (nb + 1 < NB) {
+        nxt[0] = MM::from_i8((uint32_t)wq[nb + 1][0], (uint32_t)wq[nb + 1][1]);
+        nxt[1] = MM::from_i8((uint32_t)wq[nb + 1][2], (uint32_t)wq[nb + 1][3]);
+      }
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        acc[nb][mb] = MM::mma(lo, xa[mb][0], acc[nb][mb]);
-        acc[nb][mb] = MM::mma(hi, xa[mb][1], acc[nb][mb]);
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = MM::mma(cur[h], xa[mb][h], acc[nb][mb]);
+      if (nb + 1 < NB) {
+        cur[0] = nxt[0];
+        cur[1] = nxt[1];
       }
     }
   };
@@ -187,7 +208,7 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
   // column c16 (activation row m): four consecutive outputs of one row of y.
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
-    const int nbase = n0 + (wave * NB + nb) * 16 + 4 * g;
+    const int nbase = n0 + (wn * NB + nb) * 16 + 4 * g;
     float sc[4], bi[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
@@ -196,7 +217,7 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
     }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      const int m = m0 + mb * 16 + c16;
+      const int m = m0 + (wm * MB + mb) * 16 + c16;
       if (m >= M) continue;
       XT* yr = y + (int64_t)m * ldy;
       float v[4];
@@ -221,7 +242,7 @@ using namespace qtts;
 
 namespace {
 
-struct PipeCfg { int bm, bn, P, S, cps, mtiles, ntiles; };
+struct PipeCfg { int bm, bn, P, wm, S, cps, mtiles, ntiles; };
 
 constexpr int pipe_stage_bytes_c(int bm, int bn) { return (bm / 8 + bn / 16) * 1024; }
 
@@ -235,18 +256,24 @@ bool pipe_p_ok(int bm, int bn, int p) {
 // Automatic tile choice, from a sweep of BM x BN x stages x splits over the talker
 // and code-predictor shapes at M = 32..1024 (within 3% of the per-shape best on
 // average): 32 x 64 tiles with 4 stages up to M = 128, 64 x 128 with 3 stages
-// above; then split K until there are 256 workgroups, keeping >= 8 chunks a split.
-// shape_req (algo bits 24-31): bits 0-3 log2(BM / 16) in 1..3, bits 4-6 log2(BN / 32) in
-// 1..3; 0 = automatic.
+// above, 128 x 128 from M = 512 when that still makes 512 tiles; then split K until
+// there are 256 workgroups, keeping >= 8 chunks a split.
+// shape_req (algo bits 24-30): bits 0-1 log2(BM / 16) in 1..3, bit 2 a 2 x 2 wave grid
+// (else 1 x 4), bits 4-6 log2(BN / 32) in 1..3; 0 = automatic.
 PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int stages_req, int shape_req = 0) {
   PipeCfg c;
   const int nchunks = std::max(1, (int)(k / 64));
+  c.wm = 1;
   if (shape_req != 0) {
-    c.bm = 16 << (shape_req & 15);
+    c.bm = 16 << (shape_req & 3);
     c.bn = 32 << ((shape_req >> 4) & 7);
+    c.wm = (shape_req >> 2) & 1 ? 2 : 1;
   } else if (m <= 128) {
     c.bm = 32;
     c.bn = 64;
+  } else if (m >= 512 && ((m + 127) / 128) * ((n + 127) / 128) >= 512) {
+    c.bm = 128;  // enough 128 x 128 tiles to fill the GPU twice: fewer re-reads per MFMA
+    c.bn = 128;
   } else {
     c.bm = 64;
     c.bn = 128;
@@ -278,31 +305,37 @@ struct PipeArgs {
   void* y; int64_t ldy; float* part; unsigned* counters;
 };
 
-template <typename XT, int BM, int BN, int P>
+template <typename XT, int BM, int BN, int P, int WM>
 void launch_pipe_p(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
   if constexpr (P * pipe_stage_bytes_c(BM, BN) + 64 <= kLdsBytes) {
-    qtts::launch(&w8a16_pipe_kernel<XT, BM, BN, P>, dim3(blocks), dim3(256), 0, st, (const XT*)a.x, (int)a.m,
+    qtts::launch(&w8a16_pipe_kernel<XT, BM, BN, P, WM>, dim3(blocks), dim3(256), 0, st, (const XT*)a.x, (int)a.m,
                  (int)a.k, a.ldx, a.qs, (int)a.n, a.scale, a.sdt, (const XT*)a.bias, (XT*)a.y, a.ldy, a.part,
                  a.counters, c.mtiles, c.ntiles, c.S, c.cps);
   }
 }
 
-template <typename XT, int BM, int BN>
+template <typename XT, int BM, int BN, int WM>
 void launch_pipe_stages(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
   switch (c.P) {
-    case 2: launch_pipe_p<XT, BM, BN, 2>(c, a, blocks, st); break;
-    case 3: launch_pipe_p<XT, BM, BN, 3>(c, a, blocks, st); break;
-    case 4: launch_pipe_p<XT, BM, BN, 4>(c, a, blocks, st); break;
-    case 6: launch_pipe_p<XT, BM, BN, 6>(c, a, blocks, st); break;
-    default: launch_pipe_p<XT, BM, BN, 8>(c, a, blocks, st); break;
+    case 2: launch_pipe_p<XT, BM, BN, 2, WM>(c, a, blocks, st); break;
+    case 3: launch_pipe_p<XT, BM, BN, 3, WM>(c, a, blocks, st); break;
+    case 4: launch_pipe_p<XT, BM, BN, 4, WM>(c, a, blocks, st); break;
+    case 6: launch_pipe_p<XT, BM, BN, 6, WM>(c, a, blocks, st); break;
+    default: launch_pipe_p<XT, BM, BN, 8, WM>(c, a, blocks, st); break;
   }
+}
+
+template <typename XT, int BM, int BN>
+void launch_pipe_grid(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
+  if (c.wm == 2) launch_pipe_stages<XT, BM, BN, 2>(c, a, blocks, st);
+  else launch_pipe_stages<XT, BM, BN, 1>(c, a, blocks, st);
 }
 
 template <typename XT, int BM>
 void launch_pipe_bn(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
-  if (c.bn == 256) launch_pipe_stages<XT, BM, 256>(c, a, blocks, st);
-  else if (c.bn == 128) launch_pipe_stages<XT, BM, 128>(c, a, blocks, st);
-  else launch_pipe_stages<XT, BM, 64>(c, a, blocks, st);
+  if (c.bn == 256) launch_pipe_grid<XT, BM, 256>(c, a, blocks, st);
+  else if (c.bn == 128) launch_pipe_grid<XT, BM, 128>(c, a, blocks, st);
+  else launch_pipe_grid<XT, BM, 64>(c, a, blocks, st);
 }
 
 template <typename XT>
@@ -316,8 +349,8 @@ void launch_pipe_bm(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStr
 
 bool pipe_shape_ok(int shape) {
   if (shape == 0) return true;
-  const int b = shape & 15, c = (shape >> 4) & 7;
-  return (shape >> 7) == 0 && b >= 1 && b <= 3 && c >= 1 && c <= 3;
+  const int b = shape & 3, c = (shape >> 4) & 7;
+  return (shape >> 7) == 0 && (shape & 8) == 0 && b >= 1 && c >= 1 && c <= 3;
 }
 
 int64_t qtts_w8a16_pipe_ws_bytes(int64_t m, int64_t n, int64_t k, int splits, int shape) {
