@@ -47,7 +47,13 @@ typedef enum { QTTS_ALGO_AUTO = 0, QTTS_ALGO_SKINNY = 1, QTTS_ALGO_TILE = 2 } qt
 typedef enum { QTTS_STRIP_INT8 = 0, QTTS_STRIP_FP8 = 1 } qtts_strip_kind;
 
 /* Workspace owners for qtts_workspace_bytes. */
-typedef enum { QTTS_OP_W8A16 = 0, QTTS_OP_W8A8_FP8 = 1, QTTS_OP_FP8_LINEAR = 2 } qtts_op;
+typedef enum {
+    QTTS_OP_W8A16 = 0,
+    QTTS_OP_W8A8_FP8 = 1,
+    QTTS_OP_FP8_LINEAR = 2,
+    QTTS_OP_W8A8_INT8 = 3,
+    QTTS_OP_INT8_LINEAR = 4
+} qtts_op;
 
 /* --- housekeeping ------------------------------------------------------------ */
 
@@ -75,10 +81,13 @@ int qtts_device_supported(int device);
  * splits across workgroups (a minimum for the skinny kernels, which add splits
  * until each wave's share fits its in-flight group).  For the skinny kernels, bits
  * 16-23 are the waves per workgroup (1, 2, 4, 8, 16) and bits 24-30 the chunks in
- * flight per wave (4 or 8; 4 or 6 with 16 waves).  For the tile kernel on strip
- * weights, bits 16-23 are the LDS pipeline stages (2, 3, 4, 6, 8) and bits 24-30
- * the tile shape: bits 24-27 log2(BM / 16) in 1..3, bits 28-30 log2(BN / 32) in
- * 1..3.  0 = automatic everywhere.  The calibrator uses these to time variants. */
+ * flight per wave (4 or 8; 4 or 6 with 16 waves).  For the tile kernels, bits
+ * 16-23 are the LDS pipeline stages (2, 3, 4, 6, 8; the int8 W8A8 tile builds 2-4)
+ * and bits 24-30 a tile shape code c: bits 28-30 (c >> 4) log2(BN / 32) in 1..3;
+ * for W8A16 bits 24-25 (c & 3) log2(BM / 16) in 1..3 and bit 26 (c & 4) a 2 x 2
+ * wave grid in place of 1 x 4; for W8A8 (fp8, int8) bits 24-27 (c & 15)
+ * log2(BM / 16) in 1..3.  0 = automatic everywhere.  The calibrator uses these to
+ * time variants. */
 int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo);
 
 /* --- weight packers ------------------------------------------------------------ */
@@ -177,6 +186,55 @@ int qtts_fp8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, int
                            const uint8_t* qws, int64_t n, const float* sw, const void* bias,
                            void* y, int64_t ldy, int div_mode, int algo, void* ws, int64_t ws_bytes,
                            void* stream);
+
+/* --- int8 W8A8 -------------------------------------------------------------------- */
+
+/* Per-token int8 activation quantization, replacing the activation half of
+ * Int8Method.apply (qtts/quant/int8.py:146-149).  Every step is in x_dtype, as the
+ * reference computes it on an x_dtype tensor:
+ *   s[r]      = dtype(max(amax_c |x[r,c]|, dtype(1e-6)) / 127)           (div_mode)
+ *   qx[r, c]  = clamp(round_half_even(dtype(f32(x[r,c]) / s[r])), -127, 127)
+ * A NaN quotient (0 / 0 when an fp16 scale underflows to zero) stores code 0.
+ * qx: [m, k] int8, row stride k.  sx: [m] fp32 (the x_dtype scale, widened exactly). */
+int qtts_quant_act_int8_rows(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                             int8_t* qx, float* sx, int div_mode, void* stream);
+
+/* y[m, n] = cast(((f32(acc) * sx[m]) * sw[n]) + f32(bias[n])), acc = sum_c qx[m,c] * qw[n,c]
+ * in exact int32 on int8 MFMA, replacing torch._int_mm and the fp32 epilogue that
+ * follows it (qtts/quant/int8.py:151-160).  Each fp32 step rounds on its own and the
+ * result is rounded once to out_dtype, so the output is bit-identical to the
+ * reference's for the same codes and scales (K <= 133,000 keeps acc from wrapping;
+ * torch._int_mm wraps the same way past it).
+ * qx: [m, k] int8, row stride ldqx.  qw: [n, k] int8, row stride ldqw (the
+ * reference stores the transpose, [k, n]).  sx: [m] fp32.  sw: [n] fp32 (the
+ * unrounded per-channel scale, int8.py:140).  bias: [n] of out_dtype or NULL.
+ * y: [m, n] of out_dtype.  algo as for the other GEMMs: SKINNY serves any m, TILE
+ * needs k % 128 == 0 and 16-byte aligned rows (else the skinny kernel runs). */
+int qtts_w8a8_int8_gemm(const int8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx,
+                        const int8_t* qw, int64_t n, int64_t ldqw, const float* sw,
+                        const void* bias, void* y, int out_dtype, int64_t ldy,
+                        int algo, void* ws, int64_t ws_bytes, void* stream);
+
+/* The whole of Int8Method.apply (qtts/quant/int8.py:145-160) in one call:
+ * qtts_quant_act_int8_rows into the workspace, then qtts_w8a8_int8_gemm.  The
+ * reference's padding to 17 rows for torch._int_mm (int8.py:150-155) has no
+ * counterpart: every m runs as is.  x: [m, k] of x_dtype; y: [m, n] of x_dtype;
+ * bias: [n] of x_dtype or NULL.  Workspace: qtts_workspace_bytes(QTTS_OP_INT8_LINEAR). */
+int qtts_int8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                     const int8_t* qw, int64_t n, int64_t ldqw, const float* sw,
+                     const void* bias, void* y, int64_t ldy, int div_mode,
+                     int algo, void* ws, int64_t ws_bytes, void* stream);
+
+/* qtts_w8a8_int8_gemm and qtts_int8_linear with the weight in the QTTS_STRIP_INT8
+ * layout.  Activation rows must be 16-byte aligned and k % 16 == 0. */
+int qtts_w8a8_int8_gemm_strips(const int8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx,
+                               const int8_t* qws, int64_t n, const float* sw, const void* bias,
+                               void* y, int out_dtype, int64_t ldy, int algo, void* ws,
+                               int64_t ws_bytes, void* stream);
+int qtts_int8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                            const int8_t* qws, int64_t n, const float* sw, const void* bias,
+                            void* y, int64_t ldy, int div_mode, int algo, void* ws, int64_t ws_bytes,
+                            void* stream);
 
 /* Kernel timer.  No counterpart in the reference: benchmark instrumentation.
  * Between qtts_kernel_timer_begin and qtts_kernel_timer_end, each kernel the

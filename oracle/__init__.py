@@ -56,6 +56,10 @@ def lib() -> ctypes.CDLL:
         L.oracle_w8a16_ref_f64.argtypes = [p, i64, i64, p, i64, p, p, p]
         L.oracle_w8a8_ref_f64.restype = None
         L.oracle_w8a8_ref_f64.argtypes = [p, p, i64, i64, p, i64, p, p, p]
+        L.oracle_quant_act_int8.restype = None
+        L.oracle_quant_act_int8.argtypes = [p, i32, i64, i64, i64, p, p, i32]
+        L.oracle_int8_linear_out.restype = None
+        L.oracle_int8_linear_out.argtypes = [p, p, i64, i64, p, i64, p, p, i32, p]
         _lib = L
     return _lib
 
@@ -161,6 +165,33 @@ def w8a8_ref(qx: np.ndarray, sx: np.ndarray, qw: np.ndarray, sw: np.ndarray,
     n = qw.shape[0]
     y = np.empty((m, n), np.float64)
     lib().oracle_w8a8_ref_f64(_ptr(qx), _ptr(sx), m, k, _ptr(qw), n, _ptr(sw), _ptr(b), _ptr(y))
+    return y
+
+
+def quant_act_int8(x: np.ndarray, x_dtype: int = DT_BF16, div_mode: int = DIV_DEVICE):
+    """Per-token int8 activation quantization (qtts/quant/int8.py:147-149): (qx int8, sx fp32)."""
+    x = _src(x, x_dtype)
+    m, k = x.shape
+    qx = np.empty((m, k), np.int8)
+    sx = np.empty(m, np.float32)
+    lib().oracle_quant_act_int8(_ptr(x), x_dtype, m, k, k, _ptr(qx), _ptr(sx), div_mode)
+    return qx, sx
+
+
+def int8_linear_out(qx: np.ndarray, sx: np.ndarray, qw: np.ndarray, sw: np.ndarray,
+                    bias: np.ndarray | None = None, out_dtype: int = DT_BF16) -> np.ndarray:
+    """torch._int_mm + the fp32 epilogue of Int8Method.apply (qtts/quant/int8.py:151-160).
+
+    Exact: returns out_dtype bits (uint16) or fp32 values.  bias in out_dtype's encoding."""
+    qx = np.ascontiguousarray(qx, np.int8)
+    qw = np.ascontiguousarray(qw, np.int8)
+    sx = np.ascontiguousarray(sx, np.float32)
+    sw = np.ascontiguousarray(sw, np.float32)
+    b = None if bias is None else _src(bias, out_dtype)
+    m, k = qx.shape
+    n = qw.shape[0]
+    y = np.empty((m, n), np.float32 if out_dtype == DT_F32 else np.uint16)
+    lib().oracle_int8_linear_out(_ptr(qx), _ptr(sx), m, k, _ptr(qw), n, _ptr(sw), _ptr(b), out_dtype, _ptr(y))
     return y
 
 

@@ -230,3 +230,56 @@ void oracle_w8a8_ref_f64(const uint8_t* qx, const float* sx, int64_t m, int64_t 
             y[i * n + j] = acc;
         }
 }
+
+/* Restates the activation quantization inside Int8Method.apply, qtts/quant/int8.py:147-149,
+ * where every step runs on a tensor of x's dtype and so rounds to it:
+ *   scale_x = dtype(dtype(amax(|x|, dim=1)).clamp_min(dtype(1e-6)) / 127)
+ *   q       = clamp(round_half_even(dtype(f32(x) / f32(scale_x))), -127, 127)
+ * A NaN quotient (0 / 0 once an fp16 scale underflows to zero) becomes code 0, what
+ * the float -> int8 conversion of torch's GPU kernels gives it.  sx holds the scale
+ * widened to fp32. */
+void oracle_quant_act_int8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld,
+                           int8_t* qx, float* sx, int div_mode) {
+    float floor_v = round_to(1e-6f, x_dtype);
+    for (int64_t r = 0; r < m; ++r) {
+        float amax = 0.0f;
+        for (int64_t c = 0; c < k; ++c) {
+            float a = fabsf(load_elem(x, x_dtype, r * ld + c));
+            if (a > amax) amax = a;
+        }
+        if (amax < floor_v) amax = floor_v;
+        float s = round_to(scalar_div(amax, 127.0f, div_mode), x_dtype);
+        for (int64_t c = 0; c < k; ++c) {
+            float v = rintf(round_to(load_elem(x, x_dtype, r * ld + c) / s, x_dtype));
+            if (isnan(v)) v = 0.0f;
+            if (v > 127.0f) v = 127.0f;
+            if (v < -127.0f) v = -127.0f;
+            qx[r * k + c] = (int8_t)v;
+        }
+        sx[r] = s;
+    }
+}
+
+/* Restates torch._int_mm and the fp32 epilogue of Int8Method.apply,
+ * qtts/quant/int8.py:151-160:
+ *   acc = qx @ qw^T                 exact integer sum, taken modulo 2^32 as int32
+ *   out = (f32(acc) * sx[i]) * sw[j] [+ f32(bias[j])]   each step one fp32 rounding
+ *   y   = out rounded to out_dtype (bits for bf16 / f16, fp32 values otherwise)
+ * qw is [n, k] (the reference multiplies by its [k, n] transpose).  bias: [n] in
+ * out_dtype or NULL. */
+void oracle_int8_linear_out(const int8_t* qx, const float* sx, int64_t m, int64_t k,
+                            const int8_t* qw, int64_t n, const float* sw, const void* bias,
+                            int out_dtype, void* y) {
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            int64_t acc = 0;
+            for (int64_t c = 0; c < k; ++c) acc += (int64_t)qx[i * k + c] * (int64_t)qw[j * k + c];
+            int32_t a32 = (int32_t)(uint32_t)(uint64_t)acc;
+            float v = (float)a32 * sx[i];
+            v = v * sw[j];
+            if (bias) v = v + load_elem(bias, out_dtype, j);
+            if (out_dtype == ORACLE_DT_BF16) ((uint16_t*)y)[i * n + j] = oracle_f32_to_bf16(v);
+            else if (out_dtype == ORACLE_DT_F16) ((uint16_t*)y)[i * n + j] = oracle_f32_to_f16(v);
+            else ((float*)y)[i * n + j] = v;
+        }
+}

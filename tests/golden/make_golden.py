@@ -10,6 +10,7 @@ own expressions, character for character where the expression is device-neutral:
 * fp8 packer:   qtts/quant/fp8.py:47-49
 * fp8 activations: qtts/quant/fp8.py:77-78
 * naive W8A16 formula: examples/kernels/tune_w8_gemm.py:79
+* int8 W8A8 (Int8Method.apply): qtts/quant/int8.py:146-160, torch._int_mm included
 
 Two division semantics are recorded for every scale (see oracle/qtts_oracle.c):
 ``ieee`` is the literal CPU evaluation of ``tensor / python_float``; ``device`` is
@@ -59,6 +60,32 @@ def ref_act_fp8(x: torch.Tensor, mode: str):
     amax = flat.abs().amax(dim=1, keepdim=True).clamp_min(1e-6).float()
     scale_x = _scalar_div(amax, 448.0, mode)
     return (flat.float() / scale_x).to(torch.float8_e4m3fn), scale_x.reshape(-1)
+
+
+def ref_act_int8(x: torch.Tensor, mode: str):
+    """int8.py:146-149 on an x-dtype tensor; the scale stays in x's dtype."""
+    flat = x.reshape(-1, x.shape[-1]).contiguous()
+    scale_x = _scalar_div(flat.abs().amax(dim=1, keepdim=True).clamp_min(1e-6), 127.0, mode)
+    q = (flat / scale_x).round().clamp_(-127.0, 127.0).to(torch.int8)
+    return q, scale_x.reshape(-1)
+
+
+def ref_int8_linear(x: torch.Tensor, int8_weight_t: torch.Tensor, int8_scale: torch.Tensor,
+                    bias: torch.Tensor | None, mode: str) -> torch.Tensor:
+    """int8.py:145-160 with the same row padding for torch._int_mm."""
+    q, scale_x = ref_act_int8(x, mode)
+    scale_x = scale_x.reshape(-1, 1)
+    rows = q.shape[0]
+    padded = rows < 17
+    if padded:
+        q = torch.cat([q, q.new_zeros(17 - rows, q.shape[1])], dim=0)
+    acc = torch._int_mm(q, int8_weight_t)
+    if padded:
+        acc = acc[:rows]
+    out = acc.float() * scale_x.float() * int8_scale.reshape(1, -1)
+    if bias is not None:
+        out += bias.float()
+    return out.to(x.dtype)
 
 
 def special_rows(k: int) -> np.ndarray:
@@ -163,8 +190,69 @@ def main() -> None:
         gemm[f"{name}.y_f64"] = y64.numpy()
         gemm[f"{name}.y_naive_bf16"] = bf16_bits(naive)
     np.savez_compressed(os.path.join(HERE, "gemm_small.npz"), **gemm)
-    for f in ("int8_pack", "fp8_pack", "act_fp8", "gemm_small"):
+    int8_w8a8_fixtures()
+    for f in ("int8_pack", "fp8_pack", "act_fp8", "gemm_small", "int8_w8a8"):
         print(f, os.path.getsize(os.path.join(HERE, f + ".npz")), "bytes")
+
+
+_TORCH_DT = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}
+
+
+def _bits(t: torch.Tensor) -> np.ndarray:
+    """bf16 / fp16 tensors as their uint16 bit patterns, fp32 as values."""
+    if t.dtype == torch.float32:
+        return t.contiguous().numpy().copy()
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16).copy()
+
+
+def act_int8_rows(rng: np.random.Generator, m: int, k: int) -> np.ndarray:
+    """N(0,1) rows with 1% outliers at 20 sigma; from 4 rows on an all-zero row, a row
+    below the 1e-6 clamp, and a row of exact half-way quotients (amax 127 makes the
+    scale 1 or a hair below it: 0.5, 1.5, ... then sit on rounding ties)."""
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    idx = rng.random((m, k)) < 0.01
+    x[idx] = np.where(rng.random(int(idx.sum())) < 0.5, -20.0, 20.0)
+    if m >= 4:
+        x[1] = 0.0
+        x[2] = rng.normal(0, 1, k).astype(np.float32) * np.float32(1e-7)
+        x[3] = (np.arange(k, dtype=np.float32) % 16) - np.float32(7.5)
+        x[3, 0] = 127.0
+    return x
+
+
+def int8_w8a8_fixtures() -> None:
+    """Int8Method.apply: per-token activation codes and scales in each activation
+    dtype, and whole linears (x -> y) through torch._int_mm."""
+    rng = np.random.default_rng(20240715)
+    out: dict[str, np.ndarray] = {}
+    for name, (m, k) in {"a1x2048": (1, 2048), "a8x2048": (8, 2048), "a5x130": (5, 130),
+                         "a16x1024": (16, 1024)}.items():
+        x32 = act_int8_rows(rng, m, k)
+        for dt, tdt in _TORCH_DT.items():
+            x = torch.from_numpy(x32).to(tdt)
+            out[f"act.{name}.{dt}.x"] = _bits(x)
+            for mode in ("ieee", "device"):
+                q, s = ref_act_int8(x, mode)
+                out[f"act.{name}.{dt}.{mode}.q"] = q.numpy()
+                out[f"act.{name}.{dt}.{mode}.scale"] = s.float().numpy()
+    for name, (m, n, k, has_bias, dt) in {"l1x33x256.bf16": (1, 33, 256, True, "bf16"),
+                                          "l3x16x64.bf16": (3, 16, 64, False, "bf16"),
+                                          "l20x40x384.bf16": (20, 40, 384, True, "bf16"),
+                                          "l2x24x130.f16": (2, 24, 130, True, "f16"),
+                                          "l5x48x256.f32": (5, 48, 256, True, "f32")}.items():
+        tdt = _TORCH_DT[dt]
+        w = torch.from_numpy(rng.normal(0, 0.02, (n, k)).astype(np.float32)).to(tdt)
+        x = torch.from_numpy(act_int8_rows(rng, m, k)).to(tdt)
+        bias = torch.from_numpy(rng.normal(0, 0.1, n).astype(np.float32)).to(tdt) if has_bias else None
+        q, scale = ref_int8(w, "device")
+        out[f"lin.{name}.x"] = _bits(x)
+        out[f"lin.{name}.qw"] = q.numpy()
+        out[f"lin.{name}.sw"] = scale.numpy()
+        if bias is not None:
+            out[f"lin.{name}.bias"] = _bits(bias)
+        for mode in ("ieee", "device"):
+            out[f"lin.{name}.{mode}.y"] = _bits(ref_int8_linear(x, q.t().contiguous(), scale, bias, mode))
+    np.savez_compressed(os.path.join(HERE, "int8_w8a8.npz"), **out)
 
 
 if __name__ == "__main__":

@@ -197,3 +197,94 @@ def test_bf16_rounding_helpers():
     ours = O.f32_to_bf16_bits(v)
     theirs = torch.from_numpy(v).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
     np.testing.assert_array_equal(ours, theirs)
+
+
+# ---- int8 W8A8 (Int8Method.apply, qtts/quant/int8.py:146-160) ---------------------------
+
+_I8_DT = {"bf16": O.DT_BF16, "f16": O.DT_F16, "f32": O.DT_F32}
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_act_int8_matches_golden(mode):
+    z = _load("int8_w8a8")
+    cases = sorted({k.rsplit(".", 1)[0] for k in z.files if k.startswith("act.") and k.endswith(".x")})
+    assert len(cases) == 12
+    for case in cases:
+        dt = _I8_DT[case.rsplit(".", 1)[1]]
+        q, s = O.quant_act_int8(z[f"{case}.x"], dt, MODES[mode])
+        np.testing.assert_array_equal(q, z[f"{case}.{mode}.q"], err_msg=case)
+        np.testing.assert_array_equal(s.view(np.uint32), z[f"{case}.{mode}.scale"].view(np.uint32), err_msg=case)
+
+
+@pytest.mark.parametrize("mode", list(MODES))
+def test_int8_linear_matches_golden(mode):
+    z = _load("int8_w8a8")
+    cases = sorted({k.rsplit(".", 1)[0] for k in z.files if k.startswith("lin.") and k.endswith(".x")})
+    assert len(cases) == 5
+    for case in cases:
+        dt = _I8_DT[case.rsplit(".", 1)[1]]
+        qx, sx = O.quant_act_int8(z[f"{case}.x"], dt, MODES[mode])
+        bias = z[f"{case}.bias"] if f"{case}.bias" in z.files else None
+        y = O.int8_linear_out(qx, sx, z[f"{case}.qw"], z[f"{case}.sw"], bias, dt)
+        want = z[f"{case}.{mode}.y"]
+        np.testing.assert_array_equal(y.view(np.uint32) if dt == O.DT_F32 else y,
+                                      want.view(np.uint32) if dt == O.DT_F32 else want, err_msg=case)
+
+
+def test_act_int8_closed_forms():
+    """Rows whose codes follow from the definition alone."""
+    k = 16
+    # amax 127 in fp32: scale = 127 * fl(1/127) (device) or exactly 1 (ieee); ties go to even
+    x = np.zeros((1, k), np.float32)
+    x[0, :8] = [127.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 126.5]
+    q, s = O.quant_act_int8(x, O.DT_F32, O.DIV_IEEE)
+    assert s[0] == np.float32(1.0)
+    np.testing.assert_array_equal(q[0, :8], [127, 0, 2, 2, 0, -2, -2, 126])
+    # an all-zero row: scale = dtype(1e-6) / 127, every code 0
+    for dt, floor in ((O.DT_F32, np.float32(1e-6)), (O.DT_BF16, O.bf16_bits_to_f32(O.f32_to_bf16_bits(
+            np.float32([1e-6])))[0])):
+        z0 = np.zeros((1, k), np.float32 if dt == O.DT_F32 else np.uint16)
+        q, s = O.quant_act_int8(z0, dt, O.DIV_IEEE)
+        assert not q.any()
+        want = np.float32(floor) / np.float32(127.0)
+        if dt == O.DT_BF16:
+            want = O.bf16_bits_to_f32(O.f32_to_bf16_bits(np.float32([want])))[0]
+        assert s[0] == want
+    # bf16 double rounding: amax 384 gives the bf16 scale 384/127 -> 3.03125; then
+    # 204 / 3.03125 = 67.299 rounds to bf16 67.5 and half-to-even gives 68, and
+    # 202 / 3.03125 = 66.639 rounds to 66.5 and then 66 (rounding the fp32 quotients
+    # directly would give 67 and 67); the absmax itself, 384 / 3.03125 = 126.68, rounds
+    # to bf16 126.5 and then to 126, not 127
+    xb = O.f32_to_bf16_bits(np.array([[384.0, 204.0, 202.0] + [0.0] * 13], np.float32))
+    q, s = O.quant_act_int8(xb, O.DT_BF16, O.DIV_IEEE)
+    assert s[0] == np.float32(3.03125)
+    np.testing.assert_array_equal(q[0, :3], [126, 68, 66])
+    # fp16 scale underflow: amax 2e-6 gives scale 0; nonzero codes saturate, 0/0 gives 0
+    xh = np.zeros((1, k), np.float16)
+    xh[0, 0], xh[0, 1] = 2e-6, -1e-6
+    q, s = O.quant_act_int8(xh.view(np.uint16), O.DT_F16, O.DIV_DEVICE)
+    assert s[0] == 0.0
+    np.testing.assert_array_equal(q[0, :3], [127, -127, 0])
+
+
+def test_int8_linear_oracle_invariants():
+    """The integer product against numpy's int64 matmul (a transposed operand or a dropped
+    term fails it), and the epilogue order: (acc * sx) * sw, then + bias, rounded once."""
+    rng = np.random.default_rng(5)
+    m, n, k = 3, 7, 96
+    qx = rng.integers(-127, 128, (m, k)).astype(np.int8)
+    qw = rng.integers(-127, 128, (n, k)).astype(np.int8)
+    ones_m, ones_n = np.ones(m, np.float32), np.ones(n, np.float32)
+    y = O.int8_linear_out(qx, ones_m, qw, ones_n, None, O.DT_F32)
+    acc = qx.astype(np.int64) @ qw.astype(np.int64).T
+    np.testing.assert_array_equal(y, acc.astype(np.float32))
+    sx = rng.uniform(0.001, 0.1, m).astype(np.float32)
+    sw = rng.uniform(0.001, 0.1, n).astype(np.float32)
+    bias = rng.normal(0, 1, n).astype(np.float32)
+    y = O.int8_linear_out(qx, sx, qw, sw, bias, O.DT_F32)
+    want = (acc.astype(np.float32) * sx[:, None]).astype(np.float32) * sw[None, :] + bias[None, :]
+    np.testing.assert_array_equal(y, want.astype(np.float32))
+    yb = O.int8_linear_out(qx, sx, qw, sw, O.f32_to_bf16_bits(bias), O.DT_BF16)
+    bb = O.bf16_bits_to_f32(O.f32_to_bf16_bits(bias))
+    np.testing.assert_array_equal(
+        yb, O.f32_to_bf16_bits((acc.astype(np.float32) * sx[:, None]) * sw[None, :] + bb[None, :]))

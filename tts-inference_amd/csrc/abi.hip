@@ -1,7 +1,9 @@
 // C ABI entry points (include/qtts_amd.h): argument checks, device gating, error
-// strings and dispatch to the kernel launchers in pack.hip, w8a16.hip and fp8.hip.
+// strings and dispatch to the kernel launchers in pack.hip, w8a16.hip, fp8.hip and
+// w8a8_int8.hip.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <atomic>
 #include <cstdarg>
 #include <cstdio>
@@ -9,6 +11,7 @@
 #include <mutex>
 #include <vector>
 
+#include "common.h"
 #include "layout.h"
 #include "qtts_amd.h"
 
@@ -30,6 +33,12 @@ int qtts_launch_to_strips(const void* src, int64_t n, int64_t k, int64_t ld, voi
 int qtts_launch_from_strips(const void* src, int64_t n, int64_t k, void* dst, int64_t ld, int kind, hipStream_t st);
 int64_t qtts_fp8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
 int qtts_fp8_fused_ok(int64_t m, int64_t n, int64_t k);
+int qtts_launch_quant_act_int8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld, int8_t* qx, float* sx,
+                               int div_mode, hipStream_t st);
+int qtts_launch_int8_gemm(const int8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const int8_t* qw,
+                          int64_t n, int64_t ldqw, int layout, const float* sw, const void* bias, void* y,
+                          int out_dtype, int64_t ldy, int algo, void* ws, int64_t ws_bytes, hipStream_t st);
+int64_t qtts_int8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
 int qtts_launch_fp8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
                                  int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
                                  hipStream_t st);
@@ -103,6 +112,13 @@ bool algo_ok(int a) {
 }
 int64_t al256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
+// Workspace of the one-call linears: the GEMM's own part (its split-K counter block
+// always reserved, so the quantized activations never land on counters that later
+// calls expect at zero), then the activation codes and their scales.
+int64_t linear_ws(int64_t gemm_ws, int64_t m, int64_t k) {
+  return al256(std::max<int64_t>(gemm_ws, qtts::kCounterBytes)) + al256(m * k) + al256(m * 4);
+}
+
 int current_device_check() {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
@@ -152,7 +168,9 @@ int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo) 
   switch (op) {
     case QTTS_OP_W8A16: return qtts_w8a16_ws_bytes(m, n, k, algo);
     case QTTS_OP_W8A8_FP8: return qtts_fp8_gemm_ws_bytes(m, n, k, algo);
-    case QTTS_OP_FP8_LINEAR: return al256(qtts_fp8_gemm_ws_bytes(m, n, k, algo)) + al256(m * k) + al256(m * 4);
+    case QTTS_OP_FP8_LINEAR: return linear_ws(qtts_fp8_gemm_ws_bytes(m, n, k, algo), m, k);
+    case QTTS_OP_W8A8_INT8: return qtts_int8_gemm_ws_bytes(m, n, k, algo);
+    case QTTS_OP_INT8_LINEAR: return linear_ws(qtts_int8_gemm_ws_bytes(m, n, k, algo), m, k);
     default: return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "unknown op %d", op);
   }
 }
@@ -285,13 +303,12 @@ static int fp8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, int
   // Layout: the GEMM's own workspace (split-K counters first) from the start, the
   // quantized activations and their scales at the end.
   const int64_t qx_bytes = al256(m * k), sx_bytes = al256(m * 4);
-  const int64_t gemm_ws = qtts_fp8_gemm_ws_bytes(m, n, k, algo);
-  QTTS_REQUIRE(ws != nullptr, "fp8_linear: a workspace of %lld bytes is required",
-               (long long)(qx_bytes + sx_bytes + gemm_ws));
-  const int64_t tail = (ws_bytes - qx_bytes - sx_bytes) & ~(int64_t)255;
-  if (ws_bytes < qx_bytes + sx_bytes)
+  const int64_t need = linear_ws(qtts_fp8_gemm_ws_bytes(m, n, k, algo), m, k);
+  QTTS_REQUIRE(ws != nullptr, "fp8_linear: a workspace of %lld bytes is required", (long long)need);
+  if (ws_bytes < qtts::kCounterBytes + qx_bytes + sx_bytes)
     return qtts_set_error(QTTS_ERR_WORKSPACE, "fp8_linear: workspace of %lld bytes < %lld needed", (long long)ws_bytes,
-                          (long long)(qx_bytes + sx_bytes + gemm_ws));
+                          (long long)need);
+  const int64_t tail = (ws_bytes - qx_bytes - sx_bytes) & ~(int64_t)255;
   QTTS_TRY(current_device_check());
   uint8_t* qx = (uint8_t*)ws + tail;
   float* sx = (float*)((char*)ws + tail + qx_bytes);
@@ -312,6 +329,95 @@ int qtts_fp8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, int
                            void* ws, int64_t ws_bytes, void* stream) {
   return fp8_linear_impl(x, x_dtype, m, k, ldx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y, ldy, div_mode, algo, ws,
                          ws_bytes, stream);
+}
+
+int qtts_quant_act_int8_rows(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qx, float* sx,
+                             int div_mode, void* stream) {
+  QTTS_REQUIRE(m >= 0 && k >= 0, "quant_act_int8_rows: negative size");
+  QTTS_REQUIRE(m < (1ll << 31), "quant_act_int8_rows: m too large");
+  QTTS_REQUIRE(dtype_ok(x_dtype), "quant_act_int8_rows: bad dtype code");
+  QTTS_REQUIRE(div_ok(div_mode), "quant_act_int8_rows: bad div_mode %d", div_mode);
+  QTTS_REQUIRE(ldx >= k, "quant_act_int8_rows: ldx < k");
+  if (m == 0) return QTTS_OK;
+  QTTS_REQUIRE(sx && (k == 0 || (x && qx)), "quant_act_int8_rows: null pointer");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_quant_act_int8(x, x_dtype, m, k, ldx, qx, sx, div_mode, (hipStream_t)stream);
+}
+
+static int int8_gemm_impl(const char* what, const int8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx,
+                          const int8_t* qw, int64_t n, int64_t ldqw, int layout, const float* sw, const void* bias,
+                          void* y, int out_dtype, int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "%s: negative size", what);
+  QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "%s: size too large", what);
+  QTTS_REQUIRE(dtype_ok(out_dtype), "%s: bad dtype code", what);
+  QTTS_REQUIRE(algo_ok(algo), "%s: bad algo %d", what, algo);
+  QTTS_REQUIRE(ldqx >= k && (layout == qtts::kLayoutStrips || ldqw >= k) && ldy >= n,
+               "%s: leading dimension smaller than the row", what);
+  QTTS_REQUIRE(ws_bytes >= 0, "%s: negative workspace size", what);
+  if (m == 0 || n == 0) return QTTS_OK;
+  QTTS_REQUIRE(sx && sw && y && (k == 0 || (qx && qw)), "%s: null pointer", what);
+  QTTS_TRY(current_device_check());
+  return qtts_launch_int8_gemm(qx, sx, m, k, ldqx, qw, n, ldqw, layout, sw, bias, y, out_dtype, ldy, algo, ws, ws_bytes,
+                               (hipStream_t)stream);
+}
+
+int qtts_w8a8_int8_gemm(const int8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const int8_t* qw,
+                        int64_t n, int64_t ldqw, const float* sw, const void* bias, void* y, int out_dtype,
+                        int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  return int8_gemm_impl("w8a8_int8_gemm", qx, sx, m, k, ldqx, qw, n, ldqw, qtts::kLayoutRowMajor, sw, bias, y,
+                        out_dtype, ldy, algo, ws, ws_bytes, stream);
+}
+
+int qtts_w8a8_int8_gemm_strips(const int8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx,
+                               const int8_t* qws, int64_t n, const float* sw, const void* bias, void* y, int out_dtype,
+                               int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  return int8_gemm_impl("w8a8_int8_gemm_strips", qx, sx, m, k, ldqx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y,
+                        out_dtype, ldy, algo, ws, ws_bytes, stream);
+}
+
+static int int8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qw,
+                            int64_t n, int64_t ldqw, int layout, const float* sw, const void* bias, void* y,
+                            int64_t ldy, int div_mode, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "int8_linear: negative size");
+  QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "int8_linear: size too large");
+  QTTS_REQUIRE(dtype_ok(x_dtype), "int8_linear: bad dtype code");
+  QTTS_REQUIRE(div_ok(div_mode), "int8_linear: bad div_mode %d", div_mode);
+  QTTS_REQUIRE(algo_ok(algo), "int8_linear: bad algo %d", algo);
+  QTTS_REQUIRE(ldx >= k && (layout == qtts::kLayoutStrips || ldqw >= k) && ldy >= n,
+               "int8_linear: leading dimension smaller than the row");
+  QTTS_REQUIRE(ws_bytes >= 0, "int8_linear: negative workspace size");
+  if (m == 0 || n == 0) return QTTS_OK;
+  QTTS_REQUIRE(sw && y && (k == 0 || (x && qw)), "int8_linear: null pointer");
+  // Layout: the GEMM's own workspace (split-K counters first) from the start, the
+  // quantized activations (rows of k bytes, 16-byte aligned when k % 16 == 0) and
+  // their scales at the end.
+  const int64_t qx_bytes = al256(m * k), sx_bytes = al256(m * 4);
+  const int64_t need = linear_ws(qtts_int8_gemm_ws_bytes(m, n, k, algo), m, k);
+  QTTS_REQUIRE(ws != nullptr, "int8_linear: a workspace of %lld bytes is required", (long long)need);
+  if (ws_bytes < qtts::kCounterBytes + qx_bytes + sx_bytes)
+    return qtts_set_error(QTTS_ERR_WORKSPACE, "int8_linear: workspace of %lld bytes < %lld needed", (long long)ws_bytes,
+                          (long long)need);
+  const int64_t tail = (ws_bytes - qx_bytes - sx_bytes) & ~(int64_t)255;
+  QTTS_TRY(current_device_check());
+  int8_t* qx = (int8_t*)ws + tail;
+  float* sx = (float*)((char*)ws + tail + qx_bytes);
+  QTTS_TRY(qtts_launch_quant_act_int8(x, x_dtype, m, k, ldx, qx, sx, div_mode, (hipStream_t)stream));
+  return qtts_launch_int8_gemm(qx, sx, m, k, k, qw, n, ldqw, layout, sw, bias, y, x_dtype, ldy, algo,
+                               tail > 0 ? ws : nullptr, tail, (hipStream_t)stream);
+}
+
+int qtts_int8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qw, int64_t n,
+                     int64_t ldqw, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode, int algo,
+                     void* ws, int64_t ws_bytes, void* stream) {
+  return int8_linear_impl(x, x_dtype, m, k, ldx, qw, n, ldqw, qtts::kLayoutRowMajor, sw, bias, y, ldy, div_mode, algo,
+                          ws, ws_bytes, stream);
+}
+
+int qtts_int8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qws,
+                            int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode, int algo,
+                            void* ws, int64_t ws_bytes, void* stream) {
+  return int8_linear_impl(x, x_dtype, m, k, ldx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y, ldy, div_mode, algo, ws,
+                          ws_bytes, stream);
 }
 
 int64_t qtts_strip_bytes(int64_t n, int64_t k, int kind) {

@@ -135,6 +135,24 @@ __device__ __forceinline__ f32x4_t mma_fp8_16x16x128(i32x8_t a, i32x8_t b, f32x4
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, c, 0, 0, 0, 127, 0, 127);
 }
 
+// int8 x int8 -> int32 16x16x64 MFMA.  Integer accumulation is exact (and wraps
+// modulo 2^32 past |sum| >= 2^31, which needs K > 133,000 at +-127 codes), so any
+// K order and any split give the same result.
+__device__ __forceinline__ i32x4_t mma_i8_16x16x64(i32x4_t a, i32x4_t b, i32x4_t c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// The fp32 epilogue of Int8Method.apply (qtts/quant/int8.py:157-160): the int32
+// accumulator converted to fp32, times the token scale, times the channel scale,
+// plus the bias, each step rounded on its own (the reference runs them as separate
+// elementwise kernels, so nothing may fuse into an FMA here).
+__device__ __forceinline__ float int8_epilogue(int acc, float sx, float sw, float bias, bool has_bias) {
+#pragma clang fp contract(off)
+  float v = (float)acc * sx;
+  v = v * sw;
+  return has_bias ? v + bias : v;
+}
+
 // ---- OCP e4m3fn encode (round to nearest even, non-saturating like torch's cast) ---
 
 __device__ __forceinline__ uint32_t e4m3_encode(float f) {

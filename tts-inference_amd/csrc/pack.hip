@@ -1,6 +1,6 @@
 // Weight packers and per-token activation quantization.
 //
-// Load-time packers (int8, e4m3) and the run-time fp8 activation quantizer.  One
+// Load-time packers (int8, e4m3) and the run-time fp8 and int8 activation quantizers.  One
 // workgroup of 256 threads owns one row: a coalesced pass finds the row's absmax,
 // a second pass divides, rounds and stores.  All arithmetic is IEEE fp32 (hipcc's
 // default correctly-rounded division; no fast-math), so results are bit-exact with
@@ -139,6 +139,90 @@ __global__ __launch_bounds__(kPackThreads) void quant_act_fp8_vec_kernel(
   if (tid == 0) sx[r] = s;
 }
 
+// ---- int8 activations: Int8Method.apply, qtts/quant/int8.py:147-149 ----------------
+// Everything happens in the activation dtype XT: the absmax, the 1e-6 clamp, the
+// division by 127 (div_mode) and the quotient x / scale, each rounded to XT as torch
+// rounds an XT tensor op; .round() is half-to-even on that XT value.  The scale is
+// stored widened to fp32 (exact).  A NaN quotient (0 / 0, which the fp16 scale of a
+// row with absmax below ~3.8e-6 produces, since that scale rounds to zero) stores
+// code 0, what the reference's float -> int8 cast gives it.
+
+template <typename XT> __device__ __forceinline__ float int8_act_scale(float amax, int div_mode) {
+  return round_through<XT>(scalar_div(fmaxf(amax, round_through<XT>(1e-6f)), 127.0f, div_mode));
+}
+
+template <typename XT> __device__ __forceinline__ int int8_act_code(float x, float s) {
+  const float v = __builtin_rintf(round_through<XT>(x / s));
+  return v != v ? 0 : (int)fminf(fmaxf(v, -127.0f), 127.0f);
+}
+
+template <typename XT>
+__global__ __launch_bounds__(kPackThreads) void quant_act_int8_kernel(
+    const XT* __restrict__ x, int64_t k, int64_t ld, int8_t* __restrict__ qx, float* __restrict__ sx,
+    int div_mode) {
+  __shared__ float red[4];
+  const int64_t r = blockIdx.x;
+  const XT* row = x + r * ld;
+  const float s = int8_act_scale<XT>(row_absmax(row, k, red), div_mode);
+  int8_t* qrow = qx + r * k;
+  for (int64_t c = threadIdx.x; c < k; c += kPackThreads) qrow[c] = (int8_t)int8_act_code<XT>(to_f32(row[c]), s);
+  if (threadIdx.x == 0) sx[r] = s;
+}
+
+// Vectorized form for 16-bit activations with 16-byte aligned rows and k % 8 == 0:
+// each thread holds up to V 8-element vectors of the row in registers across both
+// passes, so the row is read once.
+template <typename XT, int V>
+__global__ __launch_bounds__(kPackThreads) void quant_act_int8_vec_kernel(
+    const XT* __restrict__ x, int64_t k, int64_t ld, int8_t* __restrict__ qx, float* __restrict__ sx,
+    int div_mode) {
+  __shared__ float red[kPackThreads / 64];
+  const int64_t r = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int nv = (int)(k >> 3);
+  const XT* row = x + r * ld;
+  i32x4_t v[V];
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int idx = tid + kPackThreads * j;
+    v[j] = *(const i32x4_t*)(row + 8 * (int64_t)min(idx, nv - 1));  // clamped: in the row
+  }
+  float mx = 0.0f;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    if (tid + kPackThreads * j < nv) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t pr = (uint32_t)v[j][e];
+        mx = fmaxf(mx, fmaxf(fabsf(to_f32(XT{(uint16_t)pr})), fabsf(to_f32(XT{(uint16_t)(pr >> 16)}))));
+      }
+    }
+  }
+  mx = wave_max(mx);
+  if ((tid & 63) == 0) red[tid >> 6] = mx;
+  __syncthreads();
+#pragma unroll
+  for (int w = 0; w < kPackThreads / 64; ++w) mx = fmaxf(mx, red[w]);
+  const float s = int8_act_scale<XT>(mx, div_mode);
+  int8_t* qrow = qx + r * k;
+#pragma unroll
+  for (int j = 0; j < V; ++j) {
+    const int idx = tid + kPackThreads * j;
+    if (idx < nv) {
+      uint32_t w[2] = {0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t pr = (uint32_t)v[j][e];
+        const uint32_t c0 = (uint32_t)int8_act_code<XT>(to_f32(XT{(uint16_t)pr}), s) & 0xffu;
+        const uint32_t c1 = (uint32_t)int8_act_code<XT>(to_f32(XT{(uint16_t)(pr >> 16)}), s) & 0xffu;
+        w[e >> 1] |= (c0 | (c1 << 8)) << (16 * (e & 1));
+      }
+      *(uint2*)(qrow + 8 * (int64_t)idx) = make_uint2(w[0], w[1]);
+    }
+  }
+  if (tid == 0) sx[r] = s;
+}
+
 }  // namespace qtts
 
 using namespace qtts;
@@ -198,4 +282,33 @@ int qtts_launch_quant_act_fp8(const void* x, int x_dtype, int64_t m, int64_t k, 
   else if (x_dtype == QTTS_BF16) qtts::launch(&quant_act_fp8_kernel<bf16_t>, dim3(grid), dim3(block), 0, st, (const bf16_t*)x, k, ld, qx, sx, div_mode);
   else qtts::launch(&quant_act_fp8_kernel<f16_t>, dim3(grid), dim3(block), 0, st, (const f16_t*)x, k, ld, qx, sx, div_mode);
   return qtts_check_launch("quant_act_fp8_rows");
+}
+
+int qtts_launch_quant_act_int8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld, int8_t* qx,
+                               float* sx, int div_mode, hipStream_t st) {
+  dim3 grid((unsigned)m), block(kPackThreads);
+  const int64_t nv = k / 8;
+  if (x_dtype != QTTS_F32 && k % 8 == 0 && k > 0 && (uintptr_t)x % 16 == 0 && ld % 8 == 0 && (uintptr_t)qx % 8 == 0 &&
+      nv <= 4 * kPackThreads) {
+#define QTTS_QA8_VEC(XT)                                                                                          \
+  do {                                                                                                            \
+    if (nv <= kPackThreads)                                                                                       \
+      qtts::launch(&quant_act_int8_vec_kernel<XT, 1>, grid, block, 0, st, (const XT*)x, k, ld, qx, sx, div_mode); \
+    else if (nv <= 2 * kPackThreads)                                                                              \
+      qtts::launch(&quant_act_int8_vec_kernel<XT, 2>, grid, block, 0, st, (const XT*)x, k, ld, qx, sx, div_mode); \
+    else                                                                                                          \
+      qtts::launch(&quant_act_int8_vec_kernel<XT, 4>, grid, block, 0, st, (const XT*)x, k, ld, qx, sx, div_mode); \
+  } while (0)
+    if (x_dtype == QTTS_BF16) QTTS_QA8_VEC(bf16_t);
+    else QTTS_QA8_VEC(f16_t);
+#undef QTTS_QA8_VEC
+    return qtts_check_launch("quant_act_int8_rows");
+  }
+  if (x_dtype == QTTS_F32)
+    qtts::launch(&quant_act_int8_kernel<float>, grid, block, 0, st, (const float*)x, k, ld, qx, sx, div_mode);
+  else if (x_dtype == QTTS_BF16)
+    qtts::launch(&quant_act_int8_kernel<bf16_t>, grid, block, 0, st, (const bf16_t*)x, k, ld, qx, sx, div_mode);
+  else
+    qtts::launch(&quant_act_int8_kernel<f16_t>, grid, block, 0, st, (const f16_t*)x, k, ld, qx, sx, div_mode);
+  return qtts_check_launch("quant_act_int8_rows");
 }

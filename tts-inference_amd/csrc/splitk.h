@@ -34,25 +34,31 @@ __device__ __forceinline__ void wait_vmem() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
-__device__ __forceinline__ void store_coherent(float* p, float v) {
+template <typename T> __device__ __forceinline__ void store_coherent(T* p, T v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ float load_coherent(const float* p) {
-  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+template <typename T> __device__ __forceinline__ T load_coherent(const T* p) {
+  return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// One meeting.  `slots` points at the tile's S slots of nthreads * NV floats each,
+// Partial-sum addition: fp32 for the float GEMMs; int32 for the int8 GEMM, wrapping
+// modulo 2^32 like the matrix cores' own accumulation (so the split order cannot
+// change an integer result).
+__device__ __forceinline__ float meet_add(float a, float b) { return a + b; }
+__device__ __forceinline__ int meet_add(int a, int b) { return (int)((unsigned)a + (unsigned)b); }
+
+// One meeting.  `slots` points at the tile's S slots of nthreads * NV values each,
 // stored value-major (value v of thread t at v * nthreads + t) so that each store or
-// load instruction of a wave covers 64 consecutive floats; every participating
+// load instruction of a wave covers 64 consecutive values; every participating
 // thread calls this with its NV accumulator values.  Returns
 // true in the last-arriving workgroup, whose threads then hold the full sums.
 // `flag` is a __shared__ word (used when nthreads > 64).
-template <int NV>
-__device__ __forceinline__ bool splitk_meet(float (&acc)[NV], float* __restrict__ slots,
+template <int NV, typename T>
+__device__ __forceinline__ bool splitk_meet(T (&acc)[NV], T* __restrict__ slots,
                                             unsigned* __restrict__ counter, int S, int split, int tid,
                                             int nthreads, unsigned* flag) {
-  float* mine = slots + (int64_t)split * nthreads * NV + tid;
+  T* mine = slots + (int64_t)split * nthreads * NV + tid;
 #pragma unroll
   for (int v = 0; v < NV; ++v) store_coherent(mine + (int64_t)v * nthreads, acc[v]);
   wait_vmem();
@@ -68,17 +74,17 @@ __device__ __forceinline__ bool splitk_meet(float (&acc)[NV], float* __restrict_
   }
   if (prev != (unsigned)(S - 1)) return false;
 #pragma unroll
-  for (int v = 0; v < NV; ++v) acc[v] = 0.0f;
+  for (int v = 0; v < NV; ++v) acc[v] = T(0);
   for (int s = 0; s < S; ++s) {
     // All of a slot's loads go out before any is consumed: the scheduler keeps atomic
     // loads in order and would otherwise wait for each one before the next.
-    const float* src = slots + (int64_t)s * nthreads * NV + tid;
-    float part[NV];
+    const T* src = slots + (int64_t)s * nthreads * NV + tid;
+    T part[NV];
 #pragma unroll
     for (int v = 0; v < NV; ++v) part[v] = load_coherent(src + (int64_t)v * nthreads);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int v = 0; v < NV; ++v) acc[v] += part[v];
+    for (int v = 0; v < NV; ++v) acc[v] = meet_add(acc[v], part[v]);
   }
   if (tid == 0) reset_counter(counter);
   return true;

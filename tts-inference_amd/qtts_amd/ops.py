@@ -13,8 +13,8 @@ import threading
 import torch
 
 from . import _lib
-from ._lib import (ALGO_AUTO, DIV_DEVICE, DIV_IEEE, OP_FP8_LINEAR, OP_W8A16, OP_W8A8_FP8,  # noqa: F401
-                   STRIP_FP8, STRIP_INT8, algo_code)
+from ._lib import (ALGO_AUTO, DIV_DEVICE, DIV_IEEE, OP_FP8_LINEAR, OP_INT8_LINEAR, OP_W8A16,  # noqa: F401
+                   OP_W8A8_FP8, OP_W8A8_INT8, STRIP_FP8, STRIP_INT8, algo_code)
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
@@ -379,6 +379,140 @@ def fp8_linear_strips(x: torch.Tensor, qws: torch.Tensor, n: int, sw: torch.Tens
         _ptr(out), n, div_mode, algo, ws, ws_n, _stream(dev))
     _lib.check(st, "fp8_linear_strips")
     return out.reshape(*shape[:-1], n)
+
+
+# ---- int8 W8A8 (Int8Method, qtts/quant/int8.py:129-160) --------------------------------
+
+def quant_act_int8(x: torch.Tensor, div_mode: int = DIV_DEVICE):
+    """Per-token int8 activations (qtts/quant/int8.py:146-149): ``(qx [M,K] int8, sx [M] fp32)``.
+
+    The scale is computed in x's dtype as the reference does and returned widened to
+    fp32 (exactly)."""
+    a = _flatten(x)
+    m, k = a.shape
+    dev = _require_cuda(a)
+    qx = torch.empty((m, k), dtype=torch.int8, device=dev)
+    sx = torch.empty(m, dtype=torch.float32, device=dev)
+    st = _lib.load().qtts_quant_act_int8_rows(_ptr(a), dtype_code(a.dtype), m, k, a.stride(0) if m > 1 else k,
+                                              _ptr(qx), _ptr(sx), div_mode, _stream(dev))
+    _lib.check(st, "quant_act_int8_rows")
+    return qx, sx
+
+
+def _int8_gemm_args(qx, sx, sw, bias, m, n, out_dtype):
+    if qx.dtype != torch.int8:
+        raise ValueError(f"activations must be int8, got {qx.dtype}")
+    if qx.stride(1) != 1:
+        qx = qx.contiguous()
+    if sx.numel() != m or sw.numel() != n:
+        raise ValueError("scale sizes do not match the operands")
+    sx = sx.reshape(-1).to(torch.float32).contiguous()
+    sw = sw.reshape(-1).to(torch.float32).contiguous()
+    if bias is not None:
+        if bias.numel() != n:
+            raise ValueError(f"bias has {bias.numel()} entries for {n} output channels")
+        bias = bias.to(out_dtype).contiguous()
+    return qx, sx, sw, bias
+
+
+def w8a8_int8_gemm(qx: torch.Tensor, sx: torch.Tensor, qw: torch.Tensor, sw: torch.Tensor,
+                   bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                   algo: int = ALGO_AUTO) -> torch.Tensor:
+    """``((f32(qx @ qw^T) * sx) * sw + bias)`` rounded once to out_dtype (qtts/quant/int8.py:151-160).
+
+    qx ``[M, K]`` int8, sx ``[M]`` fp32, qw ``[N, K]`` int8 (row-major; the reference keeps
+    the transpose), sw ``[N]`` fp32.  The int32 accumulation is exact.
+    """
+    if qx.dim() != 2 or qw.dim() != 2 or qw.dtype != torch.int8:
+        raise ValueError("qx and qw must be 2-D int8 tensors")
+    m, k = qx.shape
+    n = qw.shape[0]
+    if qw.shape[1] != k:
+        raise ValueError(f"weight is [{n}, {qw.shape[1]}] but x has K={k}")
+    if qw.stride(1) != 1:
+        qw = qw.contiguous()
+    qx, sx, sw, bias = _int8_gemm_args(qx, sx, sw, bias, m, n, out_dtype)
+    dev = _require_cuda(qx, sx, qw, sw, bias)
+    out = torch.empty((m, n), dtype=out_dtype, device=dev)
+    ws, ws_n = _ws_for(dev)
+    st = _lib.load().qtts_w8a8_int8_gemm(
+        _ptr(qx), _ptr(sx), m, k, qx.stride(0) if m > 1 else k, _ptr(qw), n, qw.stride(0), _ptr(sw), _ptr(bias),
+        _ptr(out), dtype_code(out_dtype), n, algo, ws, ws_n, _stream(dev))
+    _lib.check(st, "w8a8_int8_gemm")
+    return out
+
+
+def w8a8_int8_gemm_strips(qx: torch.Tensor, sx: torch.Tensor, qws: torch.Tensor, n: int, sw: torch.Tensor,
+                          bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16,
+                          algo: int = ALGO_AUTO) -> torch.Tensor:
+    """``w8a8_int8_gemm`` with the int8 weight in the strip layout."""
+    if qx.dim() != 2:
+        raise ValueError("qx must be 2-D")
+    m, k = qx.shape
+    if qws.dtype != torch.int8 or qws.numel() != strip_bytes(n, k, STRIP_INT8):
+        raise ValueError(f"weight is not an int8 strip-layout [{n}, {k}] buffer")
+    qx, sx, sw, bias = _int8_gemm_args(qx, sx, sw, bias, m, n, out_dtype)
+    dev = _require_cuda(qx, sx, qws, sw, bias)
+    out = torch.empty((m, n), dtype=out_dtype, device=dev)
+    ws, ws_n = _ws_for(dev)
+    st = _lib.load().qtts_w8a8_int8_gemm_strips(
+        _ptr(qx), _ptr(sx), m, k, qx.stride(0) if m > 1 else k, _ptr(qws), n, _ptr(sw), _ptr(bias), _ptr(out),
+        dtype_code(out_dtype), n, algo, ws, ws_n, _stream(dev))
+    _lib.check(st, "w8a8_int8_gemm_strips")
+    return out
+
+
+def _int8_linear(x, qw, n, ldqw, sw, bias, div_mode, algo, strips):
+    shape = x.shape
+    a = _flatten(x)
+    rows, k = a.shape
+    if sw.numel() != n:
+        raise ValueError(f"scale has {sw.numel()} entries for {n} output channels")
+    if bias is not None:
+        if bias.numel() != n:
+            raise ValueError(f"bias has {bias.numel()} entries for {n} output channels")
+        bias = bias.to(a.dtype).contiguous()
+    if a.data_ptr() % 16 or (rows > 1 and a.stride(0) % 8):
+        a = a.contiguous() if a.data_ptr() % 16 == 0 else a.clone()
+    sw = sw.reshape(-1).to(torch.float32).contiguous()
+    dev = _require_cuda(a, qw, sw, bias)
+    out = torch.empty((rows, n), dtype=a.dtype, device=dev)
+    reserve_workspace(dev, workspace_bytes(OP_INT8_LINEAR, rows, n, k, algo))
+    ws, ws_n = _ws_for(dev)
+    lib = _lib.load()
+    if strips:
+        st = lib.qtts_int8_linear_strips(
+            _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else k, _ptr(qw), n, _ptr(sw), _ptr(bias),
+            _ptr(out), n, div_mode, algo, ws, ws_n, _stream(dev))
+    else:
+        st = lib.qtts_int8_linear(
+            _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else k, _ptr(qw), n, ldqw, _ptr(sw),
+            _ptr(bias), _ptr(out), n, div_mode, algo, ws, ws_n, _stream(dev))
+    _lib.check(st, "int8_linear_strips" if strips else "int8_linear")
+    return out.reshape(*shape[:-1], n)
+
+
+def int8_linear(x: torch.Tensor, qw: torch.Tensor, sw: torch.Tensor, bias: torch.Tensor | None = None,
+                div_mode: int = DIV_DEVICE, algo: int = ALGO_AUTO) -> torch.Tensor:
+    """The whole of Int8Method.apply (qtts/quant/int8.py:145-160) in one C call: quantize x
+    per token into the workspace, then the int8 GEMM.  qw ``[N, K]`` int8 row-major."""
+    if qw.dim() != 2 or qw.dtype != torch.int8:
+        raise ValueError(f"weight must be a 2-D int8 tensor, got {qw.dtype} {tuple(qw.shape)}")
+    if qw.shape[1] != x.shape[-1]:
+        raise ValueError(f"weight is [{qw.shape[0]}, {qw.shape[1]}] but x has K={x.shape[-1]}")
+    if qw.stride(1) != 1:
+        qw = qw.contiguous()
+    return _int8_linear(x, qw, qw.shape[0], qw.stride(0), sw, bias, div_mode, algo, strips=False)
+
+
+def int8_linear_strips(x: torch.Tensor, qws: torch.Tensor, n: int, sw: torch.Tensor,
+                       bias: torch.Tensor | None = None, div_mode: int = DIV_DEVICE,
+                       algo: int = ALGO_AUTO) -> torch.Tensor:
+    """Int8Method.apply (qtts/quant/int8.py:145-160) with the int8 weight in the strip layout."""
+    k = x.shape[-1]
+    if qws.dtype != torch.int8 or qws.numel() != strip_bytes(n, k, STRIP_INT8):
+        raise ValueError(f"weight is not an int8 strip-layout [{n}, {k}] buffer")
+    return _int8_linear(x, qws, n, 0, sw, bias, div_mode, algo, strips=True)
 
 
 class KernelTimer:

@@ -7,7 +7,10 @@ HIP kernel candidates against the unquantized F.linear (hipBLASLt on ROCm) insid
 a HIP graph and keeps the fastest; a layer where no candidate wins by 5% keeps
 its original weight and GEMM (qtts/quant/int8.py:79-111).
 
-``Int8Method`` (W8A8 on int8 MFMA) is not built yet on this backend.
+``Int8Method`` (W8A8) quantizes activations per token at run time and multiplies
+int8 codes on the int8 matrix cores (v_mfma_i32_16x16x64_i8) with exact int32
+accumulation and the reference's fp32 epilogue, so its output is bit-identical to
+the reference's torch._int_mm path for the same weights (qtts/quant/int8.py:129-160).
 """
 
 from __future__ import annotations
@@ -160,11 +163,42 @@ class Int8WeightOnlyMethod(QuantMethodBase):
 
 
 class Int8Method(QuantMethodBase):
-    """W8A8 int8 (qtts/quant/int8.py:120-155): not built on this backend yet."""
+    """W8A8: per-token activation scales, per-channel weight scales, int8 GEMM (qtts/quant/int8.py:129-160).
+
+    ``process_weights`` packs the weight exactly as quantize_weight_per_channel does
+    and keeps the unrounded fp32 scale (int8.py:136-140); the codes go into the strip
+    layout when K % 16 == 0 (row-major otherwise) instead of the reference's [K, N]
+    transpose for torch._int_mm.  ``apply`` is one C call: per-token quantization in
+    the activation dtype, the int8 GEMM, and ``(f32(acc) * sx) * sw + bias`` rounded
+    once to the activation dtype.  No row padding (int8.py:150-155) is needed.
+    """
 
     name = "int8"
 
-    def __init__(self) -> None:
-        raise NotImplementedError(
-            "int8 W8A8 is not implemented on the gfx950 backend yet; use --quant-method int8_weight_only "
-            "(same weight footprint, faster at decode batch sizes) or fp8 for W8A8")
+    def __init__(self, div_mode: int = _lib.DIV_DEVICE) -> None:
+        self.div_mode = div_mode
+
+    def process_weights(self, layer) -> None:
+        weight = layer.weight
+        q, scale = quantize_weight_per_channel(weight, self.div_mode)
+        n, k = layer.out_features, layer.in_features
+        if k % 16 == 0:
+            layer.register_buffer("int8_weight", ops.to_strips(q, _lib.STRIP_INT8), persistent=False)
+            layer.int8_layout = "strips"
+        else:
+            layer.register_buffer("int8_weight", q, persistent=False)
+            layer.int8_layout = "rowmajor"
+        layer.register_buffer("int8_scale", scale, persistent=False)
+        ops.reserve_workspace(weight.device, max(
+            ops.workspace_bytes(_lib.OP_INT8_LINEAR, m, n, k) for m in (16, 64, 256, 1024)))
+        layer.weight = torch.nn.Parameter(torch.empty(0, dtype=weight.dtype, device=weight.device),
+                                          requires_grad=False)
+
+    def applies_to(self, layer) -> bool:
+        return getattr(layer, "int8_weight", None) is not None
+
+    def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        if layer.int8_layout == "strips":
+            return ops.int8_linear_strips(x, layer.int8_weight, layer.out_features, layer.int8_scale, bias,
+                                          self.div_mode)
+        return ops.int8_linear(x, layer.int8_weight, layer.int8_scale, bias, self.div_mode)
