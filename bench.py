@@ -16,7 +16,8 @@ stack, a roofline entry for the dominant kernel (gate_up: device duration of eac
 launch from HIP events bound to its dispatch) and the reference's CPU path timed on a bounded
 sample on this host.
 
-Other configs (--config 0..4) print their own JSON line with the same keys.
+Other configs (--config 0..4) print their own JSON line with the same keys;
+--int8-w8a8 times the int8 W8A8 linear (Int8Method) on the talker shapes.
 """
 
 from __future__ import annotations
@@ -37,6 +38,7 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBPS = 8000.0          # MI355X HBM3E, published
 BF16_PEAK_TFLOPS = 2500.0       # dense bf16 MFMA, published
 FP8_PEAK_TFLOPS = 5000.0        # dense fp8 MFMA, published
+INT8_PEAK_TOPS = 5000.0         # dense int8 MFMA, published
 
 TALKER = [("qkv", 4096, 2048), ("o", 2048, 2048), ("gate_up", 12288, 2048), ("down", 2048, 6144)]
 PREDICTOR = [("qkv", 4096, 1024), ("o", 1024, 2048), ("gate_up", 6144, 1024), ("down", 1024, 3072)]
@@ -60,7 +62,8 @@ def log(msg: str) -> None:
 # weights and inputs
 # ---------------------------------------------------------------------------------------
 
-def make_stack(torch, ops, shapes, layers: int, keep_bf16: bool, fp8: bool = False, keep_rowmajor: int = 0):
+def make_stack(torch, ops, shapes, layers: int, keep_bf16: bool, fp8: bool = False, keep_rowmajor: int = 0,
+               f32_scale: bool = False):
     """Distinct seeded weights per (layer, linear): W ~ N(0, 0.02) fp32, seed 1000 + 16*layer + idx.
 
     Each entry holds the packed weight in the strip layout the quant methods store
@@ -74,7 +77,7 @@ def make_stack(torch, ops, shapes, layers: int, keep_bf16: bool, fp8: bool = Fal
             if fp8:
                 q, s = ops.pack_fp8(w)
             else:
-                q, s = ops.pack_int8(w, torch.bfloat16)
+                q, s = ops.pack_int8(w, torch.float32 if f32_scale else torch.bfloat16)
             qs = ops.to_strips(q)
             wb = w.to(torch.bfloat16) if keep_bf16 else None
             stack.append({"layer": layer, "name": name, "n": n, "k": k, "qs": qs, "s": s, "w_bf16": wb,
@@ -369,6 +372,35 @@ def run_fp8(args, torch, ops):
             "config": {"workload": "configs[4]: talker shapes, fp8 W8A8, M in {1, 8, 256}"}, "shapes": res}
 
 
+def run_int8_w8a8(args, torch, ops):
+    """int8 W8A8 (Int8Method) on the talker shapes, M in {1, 8, 64, 256, 1024}: the one-call linear
+    (per-token quantization + int8 MFMA GEMM) against hipBLASLt bf16 and the W8A16 kernel on the
+    same int8 codes."""
+    stack = make_stack(torch, ops, TALKER, 1, keep_bf16=True, f32_scale=True)
+    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    res = {}
+    for m in (1, 8, 64, 256, 1024):
+        xs = make_inputs(torch, [2048, 6144], [m], outliers=True)
+        for e in stack:
+            x = xs[(m, e["k"])]
+            s_b = e["s"].to(torch.bfloat16)
+            fq = lambda e=e, x=x: ops.int8_linear_strips(x, e["qs"], e["n"], e["s"])
+            fw = lambda e=e, x=x, s_b=s_b: ops.w8a16_gemm_strips(x, e["qs"], e["n"], s_b)
+            fb = lambda e=e, x=x: torch.nn.functional.linear(x, e["w_bf16"])
+            tq, tw, tb = (time_graph(torch, capture(torch, lambda f=f: [f() for _ in range(10)]), args.steps,
+                                     args.warmup) / 10 for f in (fq, fw, fb))
+            fl = 2 * m * e["n"] * e["k"]
+            nb = fp8_bytes(m, e["n"], e["k"])
+            res[f"M{m}_{e['name']}"] = {"us": round(tq * 1e3, 2), "w8a16_us": round(tw * 1e3, 2),
+                                        "bf16_us": round(tb * 1e3, 2), "speedup": round(tb / tq, 3),
+                                        "GBps": round(nb / (tq * 1e-3) / 1e9, 1),
+                                        "TOPs": round(fl / (tq * 1e-3) / 1e12, 1),
+                                        "int8_mfma_util": round(fl / (tq * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
+    return {"metric": "int8 W8A8 linear us, GB/s and int8 MFMA utilisation", "value": None, "unit": "us",
+            "n_gpus": 1, "config": {"workload": "talker shapes, int8 W8A8 (Int8Method), M in {1, 8, 64, 256, 1024}"},
+            "shapes": res}
+
+
 def run_traffic_probe(args, torch, ops):
     """Kernels for a rocprofv3 --pmc pass: a 256 MiB device copy (known bytes, the counters' scale)
     and the dominant kernel of configs[1] (gate_up over its 28 distinct weights at M = 1, 2, 4, 8),
@@ -444,6 +476,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="time budget of the CPU baseline sample")
     ap.add_argument("--summarize-rocprof", metavar="DIR")
     ap.add_argument("--summarize-pmc", metavar="DIR", help="digest a rocprofv3 --pmc run")
+    ap.add_argument("--int8-w8a8", action="store_true",
+                    help="time the int8 W8A8 linear (Int8Method) on the talker shapes instead of a config")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="launch only the kernels a rocprofv3 --pmc pass measures (copy + gate_up)")
     args = ap.parse_args()
@@ -470,6 +504,8 @@ def main() -> int:
     runner = {0: run_single_linear, 1: run_talker_stack, 2: run_predictor, 3: run_prefill, 4: run_fp8}[args.config]
     if args.traffic_probe:
         runner = run_traffic_probe
+    if args.int8_w8a8:
+        runner = run_int8_w8a8
     with torch.inference_mode():
         result = runner(args, torch, ops)
     result["device"] = torch.cuda.get_device_name()

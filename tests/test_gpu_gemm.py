@@ -297,6 +297,26 @@ def test_w8a16_strips_decode_shapes(ops, n, k):
             assert_close(y2, ref, f"strips m={m} n={n} k={k} S={splits} W={waves} C={cpw}")
 
 
+@pytest.mark.parametrize("xdt,sdt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
+                                      (torch.bfloat16, torch.float32)])
+def test_w8a16_strips_staged_rows_match_direct(ops, xdt, sdt):
+    """Decode rows (M <= 8) stage their activation rows through LDS; algo bit 30 loads them
+    straight from global memory instead.  Same operands in the same order: equal bits, for
+    every (waves, chunks) pair built with staging, ragged N and a bias, and the oracle bound."""
+    for (n, k) in ((2048, 2048), (2048, 6144), (1000, 1024), (1030, 3072), (48, 512)):
+        for m in (1, 2, 3, 4, 5, 8):
+            x, w, b = _make(m, n, k, dtype=xdt, bias=(m % 2 == 1), seed=n + k + m)
+            q, s = ops.pack_int8(w, sdt)
+            qs = ops.to_strips(q)
+            ref = _oracle_w8a16(x, q, s, b)
+            for splits, waves, cpw in ((0, 0, 0), (1, 1, 8), (1, 2, 8), (1, 4, 8), (2, 8, 8), (1, 16, 6)):
+                staged = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, splits, waves, cpw))
+                direct = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, splits, waves, cpw | 0x40))
+                what = f"m={m} n={n} k={k} S={splits} W={waves} C={cpw} {xdt} {sdt}"
+                assert torch.equal(staged, direct), what
+                assert_close(staged, ref, what)
+
+
 def test_w8a16_strips_ragged_and_tile(ops):
     for m, n, k in ((3, 17, 16), (5, 100, 80), (1, 33, 2064), (16, 1000, 1008), (17, 100, 80), (64, 2040, 2048),
                     (130, 1030, 1040), (256, 2048, 2048)):

@@ -1,0 +1,244 @@
+// The W8A16 skinny kernel (decode rows), shared by w8a16.hip (activation operands
+// loaded straight from global memory) and w8a16_xrows.hip (activation rows staged
+// through LDS).  See w8a16.hip for the kernel family as a whole.
+#pragma once
+
+#include <type_traits>
+
+#include "common.h"
+#include "layout.h"
+#include "splitk.h"
+
+namespace qtts {
+
+// Raw element bits, zero-extended to 32: a load whose value is not needed until the
+// epilogue, with no conversion the compiler could schedule (and wait for) early.
+// The load is a relaxed atomic (workgroup scope: an ordinary cached load in the
+// ISA) because compilers do not sink atomic loads towards their use; a plain load
+// of an epilogue-only value gets moved to the end of the kernel, where its latency
+// becomes a second round trip.
+template <typename T> __device__ __forceinline__ uint32_t load_bits(const T* p) {
+  if constexpr (sizeof(T) == 2)
+    return __hip_atomic_load((uint16_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  else
+    return __hip_atomic_load((uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
+  if constexpr (std::is_same<T, float>::value) return __uint_as_float(b);
+  else return to_f32(T{(uint16_t)b});
+}
+
+// ------------------------------------------------------------------------------------
+// skinny: M <= 16 * MB (MB m-blocks of 16 activation rows; MB > 1 on strip weights
+// with K % 64 == 0 only)
+// ------------------------------------------------------------------------------------
+
+// MX > 0 (one m-block, full-K strip weights, M <= MX): the activation operands come
+// through LDS instead of one 16-byte global load per lane and MFMA.  Each wave loads
+// the MX rows of its own K range once, 16 bytes a lane with no duplicates (rows past
+// M repeat row M - 1), writes them to a wave-private LDS block and reads its MFMA
+// B operands from there.  The MFMA operand layout gives lanes of rows >= M copies of
+// row 0's data, so direct loads fetch (16 / M)x the activation bytes through the
+// vector memory path the weight stream needs; staged, that path carries M rows once.
+template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1, int MX = 0>
+__global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
+    const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ q, int N, int64_t ldq,
+    const ST* scale, const XT* bias, XT* __restrict__ y, int64_t ldy,
+    float* __restrict__ part, unsigned* __restrict__ counters, int strips, int S, int cps) {
+  typedef mfma16<XT> MM;
+  typedef typename MM::vec V;
+  static_assert(MB == 1 || (FULLK && LAYOUT == kLayoutStrips), "several m-blocks need full-K strip weights");
+  static_assert(MX == 0 || (MB == 1 && FULLK && LAYOUT == kLayoutStrips), "staged rows need one m-block, full K");
+  __shared__ f32x4_t red[W > 1 ? W - 1 : 1][MB][64];
+  __shared__ __align__(16) uint16_t xrow[MX > 0 ? W : 1][MX > 0 ? MX : 1][MX > 0 ? CPW * 64 : 8];
+
+  int strip, split;
+  decode_wg(blockIdx.x, S, strip, split);
+  if (strip >= strips) return;
+
+  // wave index through readfirstlane: provably uniform, so per-wave bounds stay scalar
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r = lane & 15, g = lane >> 4;
+  const int n = strip * 16 + r;
+  const bool n_ok = n < N, m_ok = r < M;
+  const int nchunks = (K + 63) >> 6;
+  const int c0 = split * cps, c1 = min(c0 + cps, nchunks);
+  const int cw = (c1 - c0 + W - 1) / W;  // <= CPW, guaranteed by the launcher
+  const int wc0 = c0 + wave * cw, wc1 = min(wc0 + cw, c1);
+
+  const int8_t* wp;
+  int64_t wstride;
+  if constexpr (LAYOUT == kLayoutStrips) {
+    wp = q + (int64_t)strip * nchunks * 1024 + lane * 16;
+    wstride = 1024;
+  } else {
+    wp = q + (int64_t)(n_ok ? n : 0) * ldq + 16 * g;
+    wstride = 64;
+  }
+  // Activation row r + 16 mb of each m-block; rows past M read row 0 (full K) or are
+  // zero (ragged K): they only feed D columns that are never stored.
+  const XT* xp[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) xp[mb] = x + (int64_t)(r + 16 * mb < M ? r + 16 * mb : 0) * ldx + 16 * g;
+  const i32x4_t zero = {0, 0, 0, 0};
+
+  // A group of CPW chunks is issued in full before any of it is consumed.  With
+  // FULLK (K % 64 == 0, strip layout) the loads are branch-free: chunk indices past
+  // the wave's range are clamped to its last chunk (consume zeroes their weights).
+  i32x4_t w[CPW], xa[MB][CPW], xb[MB][CPW];
+  auto issue = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) {
+      if constexpr (FULLK) {
+        const int c = min(base + u, wc1 - 1);
+        w[u] = *(const i32x4_t*)(wp + (int64_t)c * wstride);
+        if constexpr (MX == 0) {
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) {
+            xa[mb][u] = *(const i32x4_t*)(xp[mb] + (int64_t)c * 64);
+            xb[mb][u] = *(const i32x4_t*)(xp[mb] + (int64_t)c * 64 + 8);
+          }
+        }
+      } else {
+        const int c = base + u;
+        const bool live = c < wc1;  // wave-uniform
+        const bool kin = c * 64 + 16 * g < K;
+        if (LAYOUT == kLayoutStrips) w[u] = live ? *(const i32x4_t*)(wp + (int64_t)c * wstride) : zero;
+        else w[u] = (live && n_ok && kin) ? *(const i32x4_t*)(wp + (int64_t)c * wstride) : zero;
+        xa[0][u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp[0] + (int64_t)c * 64) : zero;
+        xb[0][u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp[0] + (int64_t)c * 64 + 8) : zero;
+      }
+    }
+  };
+  f32x4_t acc[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  auto consume = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < CPW; ++u) {
+      if constexpr (FULLK) {
+        // Unconditional MFMAs on zeroed weights past the range: a branch here would
+        // let the compiler sink the loads into it, one round trip per chunk.
+        const bool live = base + u < wc1;
+        const i32x4_t wv = live ? w[u] : zero;
+        const V wlo = MM::from_i8((uint32_t)wv[0], (uint32_t)wv[1]);
+        const V whi = MM::from_i8((uint32_t)wv[2], (uint32_t)wv[3]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[mb] = MM::mma(wlo, __builtin_bit_cast(V, xa[mb][u]), acc[mb]);
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) acc[mb] = MM::mma(whi, __builtin_bit_cast(V, xb[mb][u]), acc[mb]);
+      } else if (base + u < wc1) {
+        const V wlo = MM::from_i8((uint32_t)w[u][0], (uint32_t)w[u][1]);
+        const V whi = MM::from_i8((uint32_t)w[u][2], (uint32_t)w[u][3]);
+        acc[0] = MM::mma(wlo, __builtin_bit_cast(V, xa[0][u]), acc[0]);
+        acc[0] = MM::mma(whi, __builtin_bit_cast(V, xb[0][u]), acc[0]);
+      }
+    }
+  };
+  // Epilogue operands: raw bits, loaded unconditionally (clamped index; y stands in
+  // for a missing bias), so nothing needs their values before the epilogue.
+  uint32_t sc[4] = {0u, 0u, 0u, 0u}, bi[4] = {0u, 0u, 0u, 0u};
+  auto issue_epilogue = [&]() {
+    const XT* bsrc = bias ? bias : y;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int nn = min(strip * 16 + 4 * g + i, N - 1);
+      sc[i] = load_bits(scale + nn);
+      bi[i] = load_bits(bsrc + nn);
+    }
+  };
+
+  // Staged activation rows (MX > 0): lane l holds elements 8 l .. 8 l + 7 of the
+  // wave's K range of each row; lanes past the range repeat its last 8 elements.
+  i32x4_t xr[MX > 0 ? MX : 1];
+  auto issue_x = [&]() {
+    if constexpr (MX > 0) {
+      const int e = min(8 * lane, (wc1 - wc0) * 64 - 8);
+#pragma unroll
+      for (int m = 0; m < MX; ++m)
+        xr[m] = *(const i32x4_t*)(x + (int64_t)min(m, M - 1) * ldx + (int64_t)wc0 * 64 + e);
+    }
+  };
+  auto stage_x = [&]() {
+    if constexpr (MX > 0) {
+      const int e = min(8 * lane, (wc1 - wc0) * 64 - 8);
+#pragma unroll
+      for (int m = 0; m < MX; ++m) *(i32x4_t*)&xrow[wave][m][e] = xr[m];
+      // B operand of lane (r, g): row r (rows >= M read row 0; their D columns are
+      // never stored), elements 64 u + 16 g .. + 15 of chunk u of the range.
+      const int rr = r < M ? r : 0;
+#pragma unroll
+      for (int u = 0; u < CPW; ++u) {
+        const int cu = min(u, wc1 - wc0 - 1);
+        xa[0][u] = *(const i32x4_t*)&xrow[wave][rr][64 * cu + 16 * g];
+        xb[0][u] = *(const i32x4_t*)&xrow[wave][rr][64 * cu + 16 * g + 8];
+      }
+    }
+  };
+
+  // One group per wave, no loop: the host sizes the grid so a wave's share fits
+  // (a loop's back edge would make the compiler wait for every load in flight at
+  // its head); the whole call is one round trip.  The epilogue operands are fetched
+  // after the weights: a compute unit's vector memory instructions pass its address
+  // unit in issue order, and the weight stream is the critical path.  (Every wave
+  // fetches them: a branch on the wave index would end in a wait for all loads.)
+  if (wc0 < wc1) {  // wave-uniform: waves past the K range only reduce
+    issue_x();
+    issue(wc0);
+    issue_epilogue();
+    // Keep the scheduler from interleaving loads with the MFMAs: every load must
+    // be in flight before the first wait.
+    __builtin_amdgcn_sched_barrier(0);
+    stage_x();  // waits for the activation rows only; the weights stay in flight
+    consume(wc0);
+  } else {
+    issue_epilogue();
+  }
+
+  if (W > 1) {
+    if (wave > 0) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) red[wave - 1][mb][lane] = acc[mb];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int w = 0; w < W - 1; ++w)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[mb] += red[w][mb][lane];
+  }
+
+  if (S > 1) {
+    float a[4 * MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) a[4 * mb + i] = acc[mb][i];
+    // Only wave 0 is left: the meeting has 64 participants per workgroup.
+    if (!splitk_meet<4 * MB>(a, part + (int64_t)strip * S * 64 * 4 * MB, &counters[strip], S, split, lane, 64,
+                             nullptr))
+      return;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{a[4 * mb], a[4 * mb + 1], a[4 * mb + 2], a[4 * mb + 3]};
+  }
+
+  // D layout of the 16x16 MFMA: lane (r, g) holds rows 4g..4g+3 (weight rows n) of
+  // column r (activation row m = r + 16 mb).
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int m = r + 16 * mb;
+    if (m < M) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int nn = strip * 16 + 4 * g + i;
+        if (nn < N) {
+          float v = acc[mb][i] * bits_to_f32<ST>(sc[i]);
+          if (bias) v += bits_to_f32<XT>(bi[i]);
+          y[(int64_t)m * ldy + nn] = from_f32<XT>(v);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace qtts

@@ -29,26 +29,10 @@
 
 #include "common.h"
 #include "layout.h"
+#include "skinny.h"
 #include "splitk.h"
 
 namespace qtts {
-
-// Raw element bits, zero-extended to 32: a load whose value is not needed until the
-// epilogue, with no conversion the compiler could schedule (and wait for) early.
-// The load is a relaxed atomic (workgroup scope: an ordinary cached load in the
-// ISA) because compilers do not sink atomic loads towards their use; a plain load
-// of an epilogue-only value gets moved to the end of the kernel, where its latency
-// becomes a second round trip.
-template <typename T> __device__ __forceinline__ uint32_t load_bits(const T* p) {
-  if constexpr (sizeof(T) == 2)
-    return __hip_atomic_load((uint16_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  else
-    return __hip_atomic_load((uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-}
-template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
-  if constexpr (std::is_same<T, float>::value) return __uint_as_float(b);
-  else return to_f32(T{(uint16_t)b});
-}
 
 __device__ __forceinline__ float load_scale(const void* s, int dt, int n) {
   if (dt == QTTS_BF16) return to_f32(((const bf16_t*)s)[n]);
@@ -62,173 +46,6 @@ __device__ __forceinline__ void store_out(XT* __restrict__ y, int64_t ldy, int m
   float v = acc * load_scale(scale, scale_dt, n);
   if (bias) v += to_f32(bias[n]);
   y[(int64_t)m * ldy + n] = from_f32<XT>(v);
-}
-
-// ------------------------------------------------------------------------------------
-// skinny: M <= 16 * MB (MB m-blocks of 16 activation rows; MB > 1 on strip weights
-// with K % 64 == 0 only)
-// ------------------------------------------------------------------------------------
-
-template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1>
-__global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
-    const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ q, int N, int64_t ldq,
-    const ST* scale, const XT* bias, XT* __restrict__ y, int64_t ldy,
-    float* __restrict__ part, unsigned* __restrict__ counters, int strips, int S, int cps) {
-  typedef mfma16<XT> MM;
-  typedef typename MM::vec V;
-  static_assert(MB == 1 || (FULLK && LAYOUT == kLayoutStrips), "several m-blocks need full-K strip weights");
-  __shared__ f32x4_t red[W > 1 ? W - 1 : 1][MB][64];
-
-  int strip, split;
-  decode_wg(blockIdx.x, S, strip, split);
-  if (strip >= strips) return;
-
-  // wave index through readfirstlane: provably uniform, so per-wave bounds stay scalar
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r = lane & 15, g = lane >> 4;
-  const int n = strip * 16 + r;
-  const bool n_ok = n < N, m_ok = r < M;
-  const int nchunks = (K + 63) >> 6;
-  const int c0 = split * cps, c1 = min(c0 + cps, nchunks);
-  const int cw = (c1 - c0 + W - 1) / W;  // <= CPW, guaranteed by the launcher
-  const int wc0 = c0 + wave * cw, wc1 = min(wc0 + cw, c1);
-
-  const int8_t* wp;
-  int64_t wstride;
-  if constexpr (LAYOUT == kLayoutStrips) {
-    wp = q + (int64_t)strip * nchunks * 1024 + lane * 16;
-    wstride = 1024;
-  } else {
-    wp = q + (int64_t)(n_ok ? n : 0) * ldq + 16 * g;
-    wstride = 64;
-  }
-  // Activation row r + 16 mb of each m-block; rows past M read row 0 (full K) or are
-  // zero (ragged K): they only feed D columns that are never stored.
-  const XT* xp[MB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) xp[mb] = x + (int64_t)(r + 16 * mb < M ? r + 16 * mb : 0) * ldx + 16 * g;
-  const i32x4_t zero = {0, 0, 0, 0};
-
-  // A group of CPW chunks is issued in full before any of it is consumed.  With
-  // FULLK (K % 64 == 0, strip layout) the loads are branch-free: chunk indices past
-  // the wave's range are clamped to its last chunk (consume zeroes their weights).
-  i32x4_t w[CPW], xa[MB][CPW], xb[MB][CPW];
-  auto issue = [&](int base) {
-#pragma unroll
-    for (int u = 0; u < CPW; ++u) {
-      if constexpr (FULLK) {
-        const int c = min(base + u, wc1 - 1);
-        w[u] = *(const i32x4_t*)(wp + (int64_t)c * wstride);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) {
-          xa[mb][u] = *(const i32x4_t*)(xp[mb] + (int64_t)c * 64);
-          xb[mb][u] = *(const i32x4_t*)(xp[mb] + (int64_t)c * 64 + 8);
-        }
-      } else {
-        const int c = base + u;
-        const bool live = c < wc1;  // wave-uniform
-        const bool kin = c * 64 + 16 * g < K;
-        if (LAYOUT == kLayoutStrips) w[u] = live ? *(const i32x4_t*)(wp + (int64_t)c * wstride) : zero;
-        else w[u] = (live && n_ok && kin) ? *(const i32x4_t*)(wp + (int64_t)c * wstride) : zero;
-        xa[0][u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp[0] + (int64_t)c * 64) : zero;
-        xb[0][u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp[0] + (int64_t)c * 64 + 8) : zero;
-      }
-    }
-  };
-  f32x4_t acc[MB];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  auto consume = [&](int base) {
-#pragma unroll
-    for (int u = 0; u < CPW; ++u) {
-      if constexpr (FULLK) {
-        // Unconditional MFMAs on zeroed weights past the range: a branch here would
-        // let the compiler sink the loads into it, one round trip per chunk.
-        const bool live = base + u < wc1;
-        const i32x4_t wv = live ? w[u] : zero;
-        const V wlo = MM::from_i8((uint32_t)wv[0], (uint32_t)wv[1]);
-        const V whi = MM::from_i8((uint32_t)wv[2], (uint32_t)wv[3]);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb] = MM::mma(wlo, __builtin_bit_cast(V, xa[mb][u]), acc[mb]);
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[mb] = MM::mma(whi, __builtin_bit_cast(V, xb[mb][u]), acc[mb]);
-      } else if (base + u < wc1) {
-        const V wlo = MM::from_i8((uint32_t)w[u][0], (uint32_t)w[u][1]);
-        const V whi = MM::from_i8((uint32_t)w[u][2], (uint32_t)w[u][3]);
-        acc[0] = MM::mma(wlo, __builtin_bit_cast(V, xa[0][u]), acc[0]);
-        acc[0] = MM::mma(whi, __builtin_bit_cast(V, xb[0][u]), acc[0]);
-      }
-    }
-  };
-  // Epilogue operands: raw bits, loaded unconditionally (clamped index; y stands in
-  // for a missing bias), so nothing needs their values before the epilogue.
-  uint32_t sc[4], bi[4];
-  auto issue_epilogue = [&]() {
-    const XT* bsrc = bias ? bias : y;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int nn = min(strip * 16 + 4 * g + i, N - 1);
-      sc[i] = load_bits(scale + nn);
-      bi[i] = load_bits(bsrc + nn);
-    }
-  };
-
-  // One group per wave, no loop: the host sizes the grid so a wave's share fits
-  // (a loop's back edge would make the compiler wait for every load in flight at
-  // its head).  Epilogue operands go first; the whole call is one round trip.
-  issue_epilogue();
-  if (wc0 < wc1) {  // wave-uniform: waves past the K range only reduce
-    issue(wc0);
-    // Keep the scheduler from interleaving loads with the MFMAs: every load must
-    // be in flight before the first wait.
-    __builtin_amdgcn_sched_barrier(0);
-    consume(wc0);
-  }
-
-  if (W > 1) {
-    if (wave > 0) {
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) red[wave - 1][mb][lane] = acc[mb];
-    }
-    __syncthreads();
-    if (wave > 0) return;
-#pragma unroll
-    for (int w = 0; w < W - 1; ++w)
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[mb] += red[w][mb][lane];
-  }
-
-  if (S > 1) {
-    float a[4 * MB];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) a[4 * mb + i] = acc[mb][i];
-    // Only wave 0 is left: the meeting has 64 participants per workgroup.
-    if (!splitk_meet<4 * MB>(a, part + (int64_t)strip * S * 64 * 4 * MB, &counters[strip], S, split, lane, 64,
-                             nullptr))
-      return;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{a[4 * mb], a[4 * mb + 1], a[4 * mb + 2], a[4 * mb + 3]};
-  }
-
-  // D layout of the 16x16 MFMA: lane (r, g) holds rows 4g..4g+3 (weight rows n) of
-  // column r (activation row m = r + 16 mb).
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-    const int m = r + 16 * mb;
-    if (m < M) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int nn = strip * 16 + 4 * g + i;
-        if (nn < N) {
-          float v = acc[mb][i] * bits_to_f32<ST>(sc[i]);
-          if (bias) v += bits_to_f32<XT>(bi[i]);
-          y[(int64_t)m * ldy + nn] = from_f32<XT>(v);
-        }
-      }
-    }
-  }
 }
 
 // ------------------------------------------------------------------------------------
@@ -497,6 +314,10 @@ bool grid_ok(int64_t blocks) { return blocks > 0 && blocks < (int64_t)1 << 31; }
 }  // namespace
 
 int64_t qtts_w8a16_pipe_ws_bytes(int64_t m, int64_t n, int64_t k, int splits, int shape);
+int qtts_launch_w8a16_skinny_xrows(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
+                                   int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
+                                   int waves, int cpw, float* part, unsigned* counters, int strips, int S, int cps,
+                                   unsigned blocks, hipStream_t st);
 int qtts_launch_w8a16_pipe(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
                            int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
                            int splits, int stages, int shape, void* ws, int64_t ws_bytes, hipStream_t st);
@@ -504,7 +325,7 @@ int qtts_launch_w8a16_pipe(const void* x, int x_dtype, int64_t m, int64_t k, int
 int64_t qtts_w8a16_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
   const int family = algo & 0xff, splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff;
   int64_t ws = 0;
-  const int cpw = (algo >> 24) & 0xff;
+  const int cpw = (algo >> 24) & 0x3f;
   if (family == QTTS_ALGO_SKINNY || family == QTTS_ALGO_AUTO)
     ws = std::max(ws, skinny_ws(skinny_cfg(std::min<int64_t>(m, kSkinnyMaxM), n, k, splits, waves, cpw)));
   if (family == QTTS_ALGO_TILE || (family == QTTS_ALGO_AUTO && m > 16)) {
@@ -531,7 +352,8 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
   unsigned* counters = (unsigned*)ws;
   float* part = ws ? (float*)((char*)ws + kCounterBytes) : nullptr;
   if (family == QTTS_ALGO_SKINNY) {
-    const int cpw = (algo >> 24) & 0xff;
+    const int cpw = (algo >> 24) & 0x3f;
+    const bool direct_x = (algo >> 24) & 0x40;
     SkinnyCfg c = skinny_cfg(m, n, k, splits, waves, cpw);
     if (!skinny_cpw_ok(c.mb, c.waves, c.cpw))
       return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
@@ -569,6 +391,14 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
     if (wide_ok) QTTS_SK_ST(W, CPW, true, 1);                            \
     else QTTS_SK_ST(W, CPW, false, 1);                                   \
   } while (0)
+    // Up to 8 rows on full-K strip weights: activation rows staged through LDS, when
+    // built for this (waves, chunks) pair and not switched off by algo bit 30.
+    if (c.mb == 1 && wide_ok && m <= 8 && !direct_x) {
+      const int rc = qtts_launch_w8a16_skinny_xrows(x, std::is_same<XT, bf16_t>::value ? QTTS_BF16 : QTTS_F16, m, k,
+                                                    ldx, q, n, scale, sdt, bias, y, ldy, c.waves, c.cpw, part,
+                                                    counters, c.strips, c.S, c.cps, (unsigned)blocks, st);
+      if (rc != 1) return rc;
+    }
     const int key = c.waves * 16 + c.cpw;
     if (c.mb == 1) {
       switch (key) {

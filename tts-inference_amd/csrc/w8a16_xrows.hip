@@ -1,0 +1,78 @@
+// The W8A16 skinny kernel with its activation rows staged through LDS (skinny.h,
+// MX > 0): decode calls of up to 8 rows on full-K strip weights.  Kept apart from
+// w8a16.hip so the two instantiation sets compile in parallel.
+#include "skinny.h"
+
+using namespace qtts;
+
+namespace {
+
+template <typename XT, typename ST, int W, int CPW, int MX>
+void launch_xrows(const void* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qs, int64_t n, const void* scale,
+                  const void* bias, void* y, int64_t ldy, float* part, unsigned* counters, int strips, int S, int cps,
+                  unsigned blocks, hipStream_t st) {
+  qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, kLayoutStrips, true, 1, MX>, dim3(blocks), dim3(W * 64), 0, st,
+               (const XT*)x, (int)m, (int)k, ldx, qs, (int)n, (int64_t)0, (const ST*)scale, (const XT*)bias, (XT*)y,
+               ldy, part, counters, strips, S, cps);
+}
+
+template <typename XT, typename ST, int W, int CPW>
+void launch_mx(int mx, const void* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qs, int64_t n,
+               const void* scale, const void* bias, void* y, int64_t ldy, float* part, unsigned* counters, int strips,
+               int S, int cps, unsigned blocks, hipStream_t st) {
+  if (mx == 1)
+    launch_xrows<XT, ST, W, CPW, 1>(x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, strips, S, cps, blocks, st);
+  else if (mx == 4)
+    launch_xrows<XT, ST, W, CPW, 4>(x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, strips, S, cps, blocks, st);
+  else
+    launch_xrows<XT, ST, W, CPW, 8>(x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, strips, S, cps, blocks, st);
+}
+
+template <typename XT, typename ST>
+int launch_wc(int waves, int cpw, int mx, const void* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
+              int64_t n, const void* scale, const void* bias, void* y, int64_t ldy, float* part, unsigned* counters,
+              int strips, int S, int cps, unsigned blocks, hipStream_t st) {
+#define QTTS_XR(W, CPW) \
+  launch_mx<XT, ST, W, CPW>(mx, x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, strips, S, cps, blocks, st)
+  switch (waves * 16 + cpw) {
+    case 1 * 16 + 8: QTTS_XR(1, 8); break;
+    case 2 * 16 + 8: QTTS_XR(2, 8); break;
+    case 4 * 16 + 8: QTTS_XR(4, 8); break;
+    case 8 * 16 + 8: QTTS_XR(8, 8); break;
+    case 16 * 16 + 6: QTTS_XR(16, 6); break;
+    default: return 1;
+  }
+#undef QTTS_XR
+  return QTTS_OK;
+}
+
+}  // namespace
+
+// Launches the staged-row skinny kernel for m <= 8 rows of 16-bit activations on full-K
+// strip weights.  Returns QTTS_OK after a launch, 1 when (waves, cpw) is not built with
+// staged rows (the caller then loads the activations directly), or an error status.
+int qtts_launch_w8a16_skinny_xrows(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
+                                   int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
+                                   int waves, int cpw, float* part, unsigned* counters, int strips, int S, int cps,
+                                   unsigned blocks, hipStream_t st) {
+  if (m < 1 || m > 8) return 1;
+  const int mx = m == 1 ? 1 : (m <= 4 ? 4 : 8);
+  int rc;
+#define QTTS_XR_ST(XT)                                                                                                \
+  do {                                                                                                                \
+    if (sdt == QTTS_BF16)                                                                                             \
+      rc = launch_wc<XT, bf16_t>(waves, cpw, mx, x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, strips, S, \
+                                 cps, blocks, st);                                                                    \
+    else if (sdt == QTTS_F16)                                                                                         \
+      rc = launch_wc<XT, f16_t>(waves, cpw, mx, x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, strips, S,  \
+                                cps, blocks, st);                                                                     \
+    else                                                                                                              \
+      rc = launch_wc<XT, float>(waves, cpw, mx, x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, strips, S,  \
+                                cps, blocks, st);                                                                     \
+  } while (0)
+  if (x_dtype == QTTS_BF16) QTTS_XR_ST(bf16_t);
+  else QTTS_XR_ST(f16_t);
+#undef QTTS_XR_ST
+  if (rc != QTTS_OK) return rc;
+  return qtts_check_launch("w8a16_skinny");
+}
