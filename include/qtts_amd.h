@@ -80,8 +80,12 @@ int qtts_device_supported(int device);
  * `algo` for the GEMMs: a qtts_algo in bits 0-7; bits 8-15 set the number of K
  * splits across workgroups (a minimum for the skinny kernels, which add splits
  * until each wave's share fits its in-flight group).  For the skinny kernels, bits
- * 16-23 are the waves per workgroup (1, 2, 4, 8, 16) and bits 24-30 the chunks in
- * flight per wave (4 or 8; 4 or 6 with 16 waves).  For the tile kernels, bits
+ * 16-23 are the waves per workgroup (1, 2, 4, 8, 16) and bits 24-29 the chunks in
+ * flight per wave (4 or 8; 4 or 6 with 16 waves; W8A16 calls of up to 8 rows on
+ * strip weights with K % 64 == 0 also take 12 with 8 waves).  Those W8A16 calls
+ * stage their activation rows through
+ * LDS; bit 30 makes them load the MFMA operands straight from memory instead (same
+ * bits out, for timing both).  For the tile kernels, bits
  * 16-23 are the LDS pipeline stages (2, 3, 4, 6, 8; the int8 W8A8 tile builds 2-4)
  * and bits 24-30 a tile shape code c: bits 28-30 (c >> 4) log2(BN / 32) in 1..3;
  * for W8A16 bits 24-25 (c & 3) log2(BM / 16) in 1..3 and bit 26 (c & 4) a 2 x 2

@@ -309,12 +309,17 @@ def test_w8a16_strips_staged_rows_match_direct(ops, xdt, sdt):
             q, s = ops.pack_int8(w, sdt)
             qs = ops.to_strips(q)
             ref = _oracle_w8a16(x, q, s, b)
-            for splits, waves, cpw in ((0, 0, 0), (1, 1, 8), (1, 2, 8), (1, 4, 8), (2, 8, 8), (1, 16, 6)):
+            # the automatic choice (its waves may differ from the direct kernel's: oracle only)
+            assert_close(ops.w8a16_gemm_strips(x, qs, n, s, b), ref, f"auto m={m} n={n} k={k} {xdt} {sdt}")
+            for splits, waves, cpw in ((1, 1, 8), (1, 2, 8), (1, 4, 8), (2, 8, 8), (1, 16, 6)):
                 staged = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, splits, waves, cpw))
                 direct = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, splits, waves, cpw | 0x40))
                 what = f"m={m} n={n} k={k} S={splits} W={waves} C={cpw} {xdt} {sdt}"
                 assert torch.equal(staged, direct), what
                 assert_close(staged, ref, what)
+            # 8 waves of 12 chunks: staged only (the automatic choice for K = 6144 from 2 rows)
+            y = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, 0, 8, 12))
+            assert_close(y, ref, f"m={m} n={n} k={k} W=8 C=12 {xdt} {sdt}")
 
 
 def test_w8a16_strips_ragged_and_tile(ops):

@@ -148,22 +148,30 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     }
   };
 
-  // Staged activation rows (MX > 0): lane l holds elements 8 l .. 8 l + 7 of the
-  // wave's K range of each row; lanes past the range repeat its last 8 elements.
-  i32x4_t xr[MX > 0 ? MX : 1];
+  // Staged activation rows (MX > 0): vector v of lane l holds elements
+  // 512 v + 8 l .. + 7 of the wave's K range of each row (XV vectors cover CPW
+  // chunks); lanes past the range repeat its last 8 elements.
+  constexpr int XV = (CPW * 64 + 511) / 512;
+  i32x4_t xr[MX > 0 ? MX : 1][XV];
   auto issue_x = [&]() {
     if constexpr (MX > 0) {
-      const int e = min(8 * lane, (wc1 - wc0) * 64 - 8);
 #pragma unroll
-      for (int m = 0; m < MX; ++m)
-        xr[m] = *(const i32x4_t*)(x + (int64_t)min(m, M - 1) * ldx + (int64_t)wc0 * 64 + e);
+      for (int v = 0; v < XV; ++v) {
+        const int e = min(512 * v + 8 * lane, (wc1 - wc0) * 64 - 8);
+#pragma unroll
+        for (int m = 0; m < MX; ++m)
+          xr[m][v] = *(const i32x4_t*)(x + (int64_t)min(m, M - 1) * ldx + (int64_t)wc0 * 64 + e);
+      }
     }
   };
   auto stage_x = [&]() {
     if constexpr (MX > 0) {
-      const int e = min(8 * lane, (wc1 - wc0) * 64 - 8);
 #pragma unroll
-      for (int m = 0; m < MX; ++m) *(i32x4_t*)&xrow[wave][m][e] = xr[m];
+      for (int v = 0; v < XV; ++v) {
+        const int e = min(512 * v + 8 * lane, (wc1 - wc0) * 64 - 8);
+#pragma unroll
+        for (int m = 0; m < MX; ++m) *(i32x4_t*)&xrow[wave][m][e] = xr[m][v];
+      }
       // B operand of lane (r, g): row r (rows >= M read row 0; their D columns are
       // never stored), elements 64 u + 16 g .. + 15 of chunk u of the range.
       const int rr = r < M ? r : 0;

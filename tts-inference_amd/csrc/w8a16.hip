@@ -318,6 +318,7 @@ int qtts_launch_w8a16_skinny_xrows(const void* x, int x_dtype, int64_t m, int64_
                                    int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
                                    int waves, int cpw, float* part, unsigned* counters, int strips, int S, int cps,
                                    unsigned blocks, hipStream_t st);
+int qtts_w8a16_xrows_built(int waves, int cpw);
 int qtts_launch_w8a16_pipe(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
                            int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
                            int splits, int stages, int shape, void* ws, int64_t ws_bytes, hipStream_t st);
@@ -355,7 +356,12 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
     const int cpw = (algo >> 24) & 0x3f;
     const bool direct_x = (algo >> 24) & 0x40;
     SkinnyCfg c = skinny_cfg(m, n, k, splits, waves, cpw);
-    if (!skinny_cpw_ok(c.mb, c.waves, c.cpw))
+    const bool staged = c.mb == 1 && wide_ok && m <= 8 && !direct_x;
+    // Staged rows from 2 rows up: 8 waves of 12 chunks beat 16 of 6 (measured on the
+    // talker down projection, K = 6144, M = 2..8).
+    if (staged && m >= 2 && waves == 0 && cpw == 0 && c.waves == 16 && c.S == 1 && 8 * 12 >= (k + 63) / 64)
+      c = skinny_cfg(m, n, k, splits, 8, 12);
+    if (!skinny_cpw_ok(c.mb, c.waves, c.cpw) && !(staged && qtts_w8a16_xrows_built(c.waves, c.cpw)))
       return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
                             "w8a16 skinny: %d chunks per wave is not built for %d waves and %d m-blocks", c.cpw,
                             c.waves, c.mb);
@@ -393,7 +399,7 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
   } while (0)
     // Up to 8 rows on full-K strip weights: activation rows staged through LDS, when
     // built for this (waves, chunks) pair and not switched off by algo bit 30.
-    if (c.mb == 1 && wide_ok && m <= 8 && !direct_x) {
+    if (staged) {
       const int rc = qtts_launch_w8a16_skinny_xrows(x, std::is_same<XT, bf16_t>::value ? QTTS_BF16 : QTTS_F16, m, k,
                                                     ldx, q, n, scale, sdt, bias, y, ldy, c.waves, c.cpw, part,
                                                     counters, c.strips, c.S, c.cps, (unsigned)blocks, st);

@@ -34,12 +34,13 @@ int launch_wc(int waves, int cpw, int mx, const void* x, int64_t m, int64_t k, i
               int strips, int S, int cps, unsigned blocks, hipStream_t st) {
 #define QTTS_XR(W, CPW) \
   launch_mx<XT, ST, W, CPW>(mx, x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, strips, S, cps, blocks, st)
-  switch (waves * 16 + cpw) {
-    case 1 * 16 + 8: QTTS_XR(1, 8); break;
-    case 2 * 16 + 8: QTTS_XR(2, 8); break;
-    case 4 * 16 + 8: QTTS_XR(4, 8); break;
-    case 8 * 16 + 8: QTTS_XR(8, 8); break;
-    case 16 * 16 + 6: QTTS_XR(16, 6); break;
+  switch (waves * 64 + cpw) {  // the pairs qtts_w8a16_xrows_built lists
+    case 1 * 64 + 8: QTTS_XR(1, 8); break;
+    case 2 * 64 + 8: QTTS_XR(2, 8); break;
+    case 4 * 64 + 8: QTTS_XR(4, 8); break;
+    case 8 * 64 + 8: QTTS_XR(8, 8); break;
+    case 16 * 64 + 6: QTTS_XR(16, 6); break;
+    case 8 * 64 + 12: QTTS_XR(8, 12); break;
     default: return 1;
   }
 #undef QTTS_XR
@@ -75,4 +76,15 @@ int qtts_launch_w8a16_skinny_xrows(const void* x, int x_dtype, int64_t m, int64_
 #undef QTTS_XR_ST
   if (rc != QTTS_OK) return rc;
   return qtts_check_launch("w8a16_skinny");
+}
+
+// (waves, chunks per wave) pairs built with staged rows.  Staged rows hold no
+// activation registers per chunk, so longer runs than the direct kernel's fit.
+int qtts_w8a16_xrows_built(int waves, int cpw) {
+  switch (waves * 64 + cpw) {
+    case 1 * 64 + 8: case 2 * 64 + 8: case 4 * 64 + 8: case 8 * 64 + 8: case 16 * 64 + 6: case 8 * 64 + 12:
+      return 1;
+    default:
+      return 0;
+  }
 }
