@@ -52,7 +52,8 @@ typedef enum {
     QTTS_OP_W8A8_FP8 = 1,
     QTTS_OP_FP8_LINEAR = 2,
     QTTS_OP_W8A8_INT8 = 3,
-    QTTS_OP_INT8_LINEAR = 4
+    QTTS_OP_INT8_LINEAR = 4,
+    QTTS_OP_FP8W = 5
 } qtts_op;
 
 /* --- housekeeping ------------------------------------------------------------ */
@@ -239,6 +240,22 @@ int qtts_int8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, in
                             const int8_t* qws, int64_t n, const float* sw, const void* bias,
                             void* y, int64_t ldy, int div_mode, int algo, void* ws, int64_t ws_bytes,
                             void* stream);
+
+/* --- fp8 weight-only: e4m3 weights, bf16 / fp16 activations ---------------------- */
+
+/* y[m, n] = cast(sum_c x[m,c] * e4m3(q[n,c]) * scale[n] + f32(bias[n])): the fused
+ * kernel Fp8WeightOnlyMethod names as the home for fp8 weights (qtts/quant/fp8.py:92-123;
+ * the reference itself raises NotImplementedError), with the W8A16 GEMM's arithmetic
+ * (qtts/quant/kernels.py:113-135): fp32 accumulation of exact e4m3 x activation
+ * products, times the fp32 scale, plus the bias, one rounding to x_dtype.
+ * qs: the e4m3 codes of qtts_pack_fp8_e4m3_rowwise, permuted by qtts_to_strips with
+ * kind QTTS_STRIP_INT8 (the 64-column strips the W8A16 kernels read).  x: bf16 or
+ * fp16 with 16-byte aligned rows; k % 64 == 0.  scale: [n] fp32.  bias: [n] of x_dtype
+ * or NULL.  algo as for qtts_w8a16_gemm_strips (the skinny kernel takes M <= 16).
+ * Workspace: qtts_workspace_bytes(QTTS_OP_FP8W). */
+int qtts_fp8w_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                          const uint8_t* qs, int64_t n, const float* scale, const void* bias,
+                          void* y, int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream);
 
 /* Kernel timer.  No counterpart in the reference: benchmark instrumentation.
  * Between qtts_kernel_timer_begin and qtts_kernel_timer_end, each kernel the

@@ -56,6 +56,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_w8a16_ref_f64.argtypes = [p, i64, i64, p, i64, p, p, p]
         L.oracle_w8a8_ref_f64.restype = None
         L.oracle_w8a8_ref_f64.argtypes = [p, p, i64, i64, p, i64, p, p, p]
+        L.oracle_fp8w_ref_f64.restype = None
+        L.oracle_fp8w_ref_f64.argtypes = [p, i64, i64, p, i64, p, p, p]
         L.oracle_quant_act_int8.restype = None
         L.oracle_quant_act_int8.argtypes = [p, i32, i64, i64, i64, p, p, i32]
         L.oracle_int8_linear_out.restype = None
@@ -165,6 +167,21 @@ def w8a8_ref(qx: np.ndarray, sx: np.ndarray, qw: np.ndarray, sw: np.ndarray,
     n = qw.shape[0]
     y = np.empty((m, n), np.float64)
     lib().oracle_w8a8_ref_f64(_ptr(qx), _ptr(sx), m, k, _ptr(qw), n, _ptr(sw), _ptr(b), _ptr(y))
+    return y
+
+
+def fp8w_ref(x_f32: np.ndarray, q: np.ndarray, scale_f32: np.ndarray,
+             bias_f32: np.ndarray | None = None) -> np.ndarray:
+    """fp64 x @ (e4m3(q) * scale)^T + bias: the fp8 weight-only formula (qtts/quant/fp8.py:92-123
+    with qtts/quant/kernels.py:113-135).  q: e4m3 codes as uint8."""
+    x = np.ascontiguousarray(x_f32, np.float32)
+    q = np.ascontiguousarray(q, np.uint8)
+    s = np.ascontiguousarray(scale_f32, np.float32)
+    b = None if bias_f32 is None else np.ascontiguousarray(bias_f32, np.float32)
+    m, k = x.shape
+    n = q.shape[0]
+    y = np.empty((m, n), np.float64)
+    lib().oracle_fp8w_ref_f64(_ptr(x), m, k, _ptr(q), n, _ptr(s), _ptr(b), _ptr(y))
     return y
 
 

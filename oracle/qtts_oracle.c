@@ -283,3 +283,22 @@ void oracle_int8_linear_out(const int8_t* qx, const float* sx, int64_t m, int64_
             else ((float*)y)[i * n + j] = v;
         }
 }
+
+/* fp8 weight-only oracle (the fused kernel qtts/quant/fp8.py:92-123 calls for, with the
+ * W8A16 formula of qtts/quant/kernels.py:113-135): dequantize-then-matmul in fp64,
+ *   y[i, j] = sum_c x[i, c] * e4m3(q[j, c]) * scale[j] + bias[j]
+ * x fp32 [m, k] (callers widen bf16 first), q e4m3 codes [n, k], scale fp32 [n],
+ * bias fp32 [n] or NULL. */
+void oracle_fp8w_ref_f64(const float* x, int64_t m, int64_t k, const uint8_t* q, int64_t n,
+                         const float* scale, const float* bias, double* y) {
+    double lut[256];
+    for (int c = 0; c < 256; ++c) lut[c] = (double)oracle_e4m3_decode((uint8_t)c);
+    for (int64_t i = 0; i < m; ++i)
+        for (int64_t j = 0; j < n; ++j) {
+            double acc = 0.0;
+            for (int64_t c = 0; c < k; ++c) acc += (double)x[i * k + c] * lut[q[j * k + c]];
+            acc *= (double)scale[j];
+            if (bias) acc += (double)bias[j];
+            y[i * n + j] = acc;
+        }
+}

@@ -288,3 +288,21 @@ def test_int8_linear_oracle_invariants():
     bb = O.bf16_bits_to_f32(O.f32_to_bf16_bits(bias))
     np.testing.assert_array_equal(
         yb, O.f32_to_bf16_bits((acc.astype(np.float32) * sx[:, None]) * sw[None, :] + bb[None, :]))
+
+
+def test_fp8w_oracle_matches_numpy_and_one_hot():
+    """The fp8 weight-only oracle against numpy's matmul of the decoded codes (the decode
+    table is pinned above against the OCP spec), and one-hot rows that read single codes."""
+    rng = np.random.default_rng(11)
+    m, n, k = 3, 9, 70
+    finite = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], np.uint8)
+    q = rng.choice(finite, (n, k)).astype(np.uint8)
+    x = rng.normal(0, 1, (m, k)).astype(np.float32)
+    s = rng.uniform(0.001, 0.01, n).astype(np.float32)
+    b = rng.normal(0, 0.1, n).astype(np.float32)
+    lut = O.e4m3_decode_table().astype(np.float64)
+    want = x.astype(np.float64) @ (lut[q] * s.astype(np.float64)[:, None]).T + b
+    np.testing.assert_allclose(O.fp8w_ref(x, q, s, b), want, rtol=1e-12, atol=1e-12)
+    eye = np.eye(k, dtype=np.float32)[:5]
+    y = O.fp8w_ref(eye, q, np.ones(n, np.float32))
+    np.testing.assert_array_equal(y, lut[q[:, :5]].T)

@@ -39,6 +39,10 @@ int qtts_launch_int8_gemm(const int8_t* qx, const float* sx, int64_t m, int64_t 
                           int64_t n, int64_t ldqw, int layout, const float* sw, const void* bias, void* y,
                           int out_dtype, int64_t ldy, int algo, void* ws, int64_t ws_bytes, hipStream_t st);
 int64_t qtts_int8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
+int64_t qtts_fp8w_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
+int qtts_launch_fp8w(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n,
+                     const float* scale, const void* bias, void* y, int64_t ldy, int algo, void* ws, int64_t ws_bytes,
+                     hipStream_t st);
 int qtts_launch_fp8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
                                  int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
                                  hipStream_t st);
@@ -171,6 +175,7 @@ int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo) 
     case QTTS_OP_FP8_LINEAR: return linear_ws(qtts_fp8_gemm_ws_bytes(m, n, k, algo), m, k);
     case QTTS_OP_W8A8_INT8: return qtts_int8_gemm_ws_bytes(m, n, k, algo);
     case QTTS_OP_INT8_LINEAR: return linear_ws(qtts_int8_gemm_ws_bytes(m, n, k, algo), m, k);
+    case QTTS_OP_FP8W: return qtts_fp8w_ws_bytes(m, n, k, algo);
     default: return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "unknown op %d", op);
   }
 }
@@ -418,6 +423,24 @@ int qtts_int8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, in
                             void* ws, int64_t ws_bytes, void* stream) {
   return int8_linear_impl(x, x_dtype, m, k, ldx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y, ldy, div_mode, algo, ws,
                           ws_bytes, stream);
+}
+
+int qtts_fp8w_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n,
+                          const float* scale, const void* bias, void* y, int64_t ldy, int algo, void* ws,
+                          int64_t ws_bytes, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "fp8w_gemm_strips: negative size (m=%lld, n=%lld, k=%lld)", (long long)m,
+               (long long)n, (long long)k);
+  QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "fp8w_gemm_strips: size too large");
+  QTTS_REQUIRE(x_dtype == QTTS_BF16 || x_dtype == QTTS_F16, "fp8w_gemm_strips: activations must be bf16 or fp16");
+  QTTS_REQUIRE(algo_ok(algo), "fp8w_gemm_strips: bad algo %d", algo);
+  QTTS_REQUIRE(k % 64 == 0, "fp8w_gemm_strips: K %% 64 != 0 (K=%lld)", (long long)k);
+  QTTS_REQUIRE(ldx >= k && ldy >= n, "fp8w_gemm_strips: leading dimension smaller than the row");
+  QTTS_REQUIRE(ws_bytes >= 0, "fp8w_gemm_strips: negative workspace size");
+  if (m == 0 || n == 0) return QTTS_OK;
+  QTTS_REQUIRE(x && qs && scale && y, "fp8w_gemm_strips: null pointer");
+  QTTS_REQUIRE((uintptr_t)x % 16 == 0 && (m == 1 || ldx % 8 == 0), "fp8w_gemm_strips: activation rows must be 16-byte aligned");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_fp8w(x, x_dtype, m, k, ldx, qs, n, scale, bias, y, ldy, algo, ws, ws_bytes, (hipStream_t)stream);
 }
 
 int64_t qtts_strip_bytes(int64_t n, int64_t k, int kind) {

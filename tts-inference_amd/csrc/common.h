@@ -113,11 +113,35 @@ __device__ __forceinline__ f16x8_t i8x8_to_f16x8(uint32_t lo, uint32_t hi) {
   return r;
 }
 
+// ---- OCP e4m3 -> 16-bit float vectors (fp8 weight-only GEMM) ---------------------
+// Every e4m3 value (3 mantissa bits, exponents 2^-9 .. 2^8) is exact in bf16 and
+// fp16.  v_cvt_scalef32_pk_{bf16,f16}_fp8 converts two codes per instruction; the
+// unit scale leaves the values unchanged.
+
+__device__ __forceinline__ bf16x8_t e4m3x8_to_bf16x8(uint32_t lo, uint32_t hi) {
+  typedef __attribute__((ext_vector_type(4))) uint32_t u4;
+  const u4 v = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true))};
+  return __builtin_bit_cast(bf16x8_t, v);
+}
+
+__device__ __forceinline__ f16x8_t e4m3x8_to_f16x8(uint32_t lo, uint32_t hi) {
+  typedef __attribute__((ext_vector_type(4))) uint32_t u4;
+  const u4 v = {__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, false)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(lo, 1.0f, true)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, false)),
+                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(hi, 1.0f, true))};
+  return __builtin_bit_cast(f16x8_t, v);
+}
+
 // 16-bit activation element types mapped to their MFMA operand vector.
 template <typename XT> struct mfma16;
 template <> struct mfma16<bf16_t> {
   typedef bf16x8_t vec;
   static __device__ __forceinline__ vec from_i8(uint32_t lo, uint32_t hi) { return i8x8_to_bf16x8(lo, hi); }
+  static __device__ __forceinline__ vec from_e4m3(uint32_t lo, uint32_t hi) { return e4m3x8_to_bf16x8(lo, hi); }
   static __device__ __forceinline__ f32x4_t mma(vec a, vec b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
@@ -125,10 +149,18 @@ template <> struct mfma16<bf16_t> {
 template <> struct mfma16<f16_t> {
   typedef f16x8_t vec;
   static __device__ __forceinline__ vec from_i8(uint32_t lo, uint32_t hi) { return i8x8_to_f16x8(lo, hi); }
+  static __device__ __forceinline__ vec from_e4m3(uint32_t lo, uint32_t hi) { return e4m3x8_to_f16x8(lo, hi); }
   static __device__ __forceinline__ f32x4_t mma(vec a, vec b, f32x4_t c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
 };
+
+// Weight codes (8 per call: two packed dwords) to the MFMA operand: int8, or OCP
+// e4m3 for the fp8 weight-only kernels (F8W).
+template <bool F8W, typename XT> __device__ __forceinline__ typename mfma16<XT>::vec wcvt(uint32_t lo, uint32_t hi) {
+  if constexpr (F8W) return mfma16<XT>::from_e4m3(lo, hi);
+  else return mfma16<XT>::from_i8(lo, hi);
+}
 
 // fp8 x fp8 (OCP e4m3 on gfx950) 16x16x128 MFMA, unit block scales (E8M0 127 = 2^0).
 __device__ __forceinline__ f32x4_t mma_fp8_16x16x128(i32x8_t a, i32x8_t b, f32x4_t c) {

@@ -3,6 +3,7 @@
 // through LDS).  See w8a16.hip for the kernel family as a whole.
 #pragma once
 
+#include <algorithm>
 #include <type_traits>
 
 #include "common.h"
@@ -40,7 +41,8 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 // B operands from there.  The MFMA operand layout gives lanes of rows >= M copies of
 // row 0's data, so direct loads fetch (16 / M)x the activation bytes through the
 // vector memory path the weight stream needs; staged, that path carries M rows once.
-template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1, int MX = 0>
+// F8W: the weight codes are OCP e4m3 (fp8 weight-only) instead of int8.
+template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1, int MX = 0, bool F8W = false>
 __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ q, int N, int64_t ldq,
     const ST* scale, const XT* bias, XT* __restrict__ y, int64_t ldy,
@@ -121,15 +123,15 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
         // let the compiler sink the loads into it, one round trip per chunk.
         const bool live = base + u < wc1;
         const i32x4_t wv = live ? w[u] : zero;
-        const V wlo = MM::from_i8((uint32_t)wv[0], (uint32_t)wv[1]);
-        const V whi = MM::from_i8((uint32_t)wv[2], (uint32_t)wv[3]);
+        const V wlo = wcvt<F8W, XT>((uint32_t)wv[0], (uint32_t)wv[1]);
+        const V whi = wcvt<F8W, XT>((uint32_t)wv[2], (uint32_t)wv[3]);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[mb] = MM::mma(wlo, __builtin_bit_cast(V, xa[mb][u]), acc[mb]);
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[mb] = MM::mma(whi, __builtin_bit_cast(V, xb[mb][u]), acc[mb]);
       } else if (base + u < wc1) {
-        const V wlo = MM::from_i8((uint32_t)w[u][0], (uint32_t)w[u][1]);
-        const V whi = MM::from_i8((uint32_t)w[u][2], (uint32_t)w[u][3]);
+        const V wlo = wcvt<F8W, XT>((uint32_t)w[u][0], (uint32_t)w[u][1]);
+        const V whi = wcvt<F8W, XT>((uint32_t)w[u][2], (uint32_t)w[u][3]);
         acc[0] = MM::mma(wlo, __builtin_bit_cast(V, xa[0][u]), acc[0]);
         acc[0] = MM::mma(whi, __builtin_bit_cast(V, xb[0][u]), acc[0]);
       }
@@ -247,6 +249,63 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       }
     }
   }
+}
+
+// ---- host side: the skinny configuration ------------------------------------------
+
+struct SkinnyCfg { int mb, waves, cpw, S, cps, strips; };
+
+// The skinny kernels take up to kSkinnyMaxM rows on strip weights.  The automatic
+// choice keeps them up to 32 rows (two m-blocks) for weights of at most 9 MiB and
+// otherwise moves to the tile kernel past 16 rows: measured on the talker and
+// code-predictor shapes at M = 16..96, where the tile kernel wins on the 12-25 MB
+// weights from 24 rows and everywhere from 48.
+constexpr int kSkinnyMaxM = 64, kSkinnyAutoMaxM = 32;
+constexpr int64_t kSkinnyAutoMaxBytes = 9 << 20;
+
+// m-blocks of 16 activation rows a skinny call carries.
+inline int skinny_mb(int64_t m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
+
+// Chunks (64 columns, 1 KiB of a strip) a wave keeps in flight at once; a chunk holds
+// 4 + 8 MB registers a lane.  Built: MB = 1: 4 or 8 (4 or 6 at 16 waves, whose 1024
+// threads leave 128 registers a lane); MB = 2: 4 or 8 (4 at 16 waves); MB = 4: 4, at
+// most 8 waves.
+inline bool skinny_cpw_ok(int mb, int w, int cpw) {
+  if (mb == 1) return w == 16 ? (cpw == 4 || cpw == 6) : (cpw == 4 || cpw == 8);
+  if (mb == 2) return w == 16 ? cpw == 4 : (cpw == 4 || cpw == 8);
+  return mb == 4 && w <= 8 && cpw == 4;
+}
+inline int skinny_cpw_max(int mb, int w) { return mb == 1 ? (w == 16 ? 6 : 8) : (mb == 2 ? (w == 16 ? 4 : 8) : 4); }
+inline int skinny_waves_max(int mb) { return mb == 4 ? 8 : 16; }
+
+inline SkinnyCfg skinny_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int waves_req, int cpw_req) {
+  SkinnyCfg c;
+  c.mb = skinny_mb(m);
+  c.strips = (int)((n + 15) / 16);
+  const int nchunks = std::max(1, (int)((k + 63) / 64));
+  int W = waves_req, S = splits_req, C = cpw_req;
+  if (W <= 0) {
+    // Few, fat waves: the fewest waves (with the most chunks in flight each) that
+    // cover a strip's K without a split.  Measured on the talker and code-predictor
+    // shapes this beats more, thinner waves at every M in 1..16.
+    W = 1;
+    while (W < skinny_waves_max(c.mb) && W * skinny_cpw_max(c.mb, W) < nchunks) W *= 2;
+  }
+  if (C <= 0) C = skinny_cpw_max(c.mb, W);
+  c.waves = W;
+  c.cpw = C;
+  // The kernel runs one group of C chunks per wave: raise S until a wave's share
+  // fits (a requested split count is a minimum).
+  S = std::max(S, 1);
+  S = std::max(S, (nchunks + W * C - 1) / (W * C));
+  S = std::min(S, nchunks);
+  c.cps = (nchunks + S - 1) / S;
+  c.S = (nchunks + c.cps - 1) / c.cps;
+  return c;
+}
+
+inline int64_t skinny_ws(const SkinnyCfg& c) {
+  return c.S <= 1 ? 0 : kCounterBytes + (int64_t)c.strips * c.S * 64 * 4 * c.mb * 4;
 }
 
 }  // namespace qtts

@@ -1,357 +1,9 @@
-// W8A16 GEMM for prefill-sized rows (M > 16) on strip-layout weights, gfx950.
-//
-// Replaces _w8_gemm_kernel (qtts/quant/kernels.py:89-135) for M > 16 when K % 64 == 0.
-//
-// A workgroup of 4 waves owns a BM x BN output tile and a K range; it walks the K
-// range in 64-column stages through a P-deep LDS ring.  Stage loads are direct
-// global -> LDS transfers (global_load_lds_dwordx4, 16 bytes per lane), so P-1
-// stages are in flight while one is consumed, with no registers held for them.  Every load writes one 1 KiB MFMA fragment in lane order:
-//   * activation fragment (m-block mb, half h): lane l carries
-//     x[m0 + 16 mb + l % 16][k + 16 (l / 16) + 8 h .. + 7]  (8 bf16);
-//   * weight fragment (strip sb): the strip layout's 1 KiB block, lane l carries
-//     w[n0 + 16 sb + l % 16][k + 16 (l / 16) .. + 15]  (16 int8).
-// So every MFMA operand read is one conflict-free ds_read_b128 at lane * 16.  The
-// int8 half h of a weight fragment pairs with activation half h: together they
-// cover the stage's 64 K columns in two v_mfma_f32_16x16x32 steps.
-//
-// The 4 waves form a WM x (4/WM) grid over the tile.  With WM = 1 each wave owns
-// BN/4 output columns for all BM rows, so each weight fragment is dequantized
-// (int8 -> bf16, exact) by exactly one wave, but every wave reads all of the tile's
-// activation fragments from LDS; WM = 2 halves those activation reads (LDS
-// bandwidth, not the matrix cores, bounds the 1 x 4 grid on the larger tiles) at the
-// cost of dequantizing each weight fragment twice.  Rows past M and strips past N are read clamped and
-// never stored; K must be a multiple of 64 (the strip layout pads N, not K).
-//
-// Tiles are numbered n-fastest, and the dispatcher deals consecutive workgroups to
-// the 8 XCDs in turn, so each XCD works through its own n-columns of the weight for
-// every m-tile: the weight is read once from HBM and its re-reads across m-tiles
-// hit that XCD's L2.  Split-K, for shapes with too few tiles to fill the GPU, meets
-// through the workspace in the same launch (splitk.h).
-#include <algorithm>
-
-#include "common.h"
-#include "layout.h"
-#include "pipe.h"
-#include "splitk.h"
-
-namespace qtts {
-
-// Scale bits with no branch on the dtype: always 16-bit loads (an fp32 scale is read
-// as its two halves), so no join waits for the loads before the epilogue needs them.
-__device__ __forceinline__ uint32_t load_scale_bits(const void* s, int dt, int n) {
-  const bool f32 = dt == QTTS_F32;
-  const uint16_t* p = (const uint16_t*)s;
-  const uint32_t lo = __hip_atomic_load((uint16_t*)p + (f32 ? 2 * n : n), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  const uint32_t hi = __hip_atomic_load((uint16_t*)p + (f32 ? 2 * n + 1 : n), __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_WORKGROUP);
-  return f32 ? (lo | (hi << 16)) : lo;
-}
-
-__device__ __forceinline__ float scale_bits_to_f32(uint32_t b, int dt) {
-  if (dt == QTTS_F32) return __uint_as_float(b);
-  if (dt == QTTS_BF16) return to_f32(bf16_t{(uint16_t)b});
-  return to_f32(f16_t{(uint16_t)b});
-}
-
-template <typename XT> __device__ __forceinline__ float xbits_to_f32(uint32_t b) { return to_f32(XT{(uint16_t)b}); }
-
-template <typename XT, int BM, int BN, int P, int WM>
-__global__ __launch_bounds__(256) void w8a16_pipe_kernel(
-    const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ qs, int N,
-    const void* __restrict__ scale, int sdt, const XT* __restrict__ bias, XT* __restrict__ y, int64_t ldy,
-    float* __restrict__ part, unsigned* __restrict__ counters, int mtiles, int ntiles, int S, int cps) {
-  typedef mfma16<XT> MM;
-  typedef typename MM::vec V;
-  constexpr int WN = 4 / WM;           // the 4 waves form a WM x WN grid over the tile
-  constexpr int TMB = BM / 16;         // 16-row m-blocks per tile
-  constexpr int MB = TMB / WM;         // 16-row m-blocks per wave
-  constexpr int NB = BN / 16 / WN;     // 16-column strips per wave
-  constexpr int XF = 2 * TMB;          // activation fragments per stage
-  constexpr int WF = BN / 16;          // weight fragments per stage
-  constexpr int F = XF + WF;
-  constexpr int FPW = F / 4;           // fragments each wave loads per stage
-  constexpr int SB = F * 1024;         // stage bytes
-  static_assert(F % 4 == 0, "fragments must split evenly over 4 waves");
-  static_assert((WM == 1 || WM == 2) && MB >= 1 && NB >= 1, "wave grid must cover the tile");
-  static_assert(P >= 2 && P * SB + 64 <= kLdsBytes, "stage ring must fit in LDS");
-  static_assert((P - 2) * FPW < 64, "vmcnt is 6 bits");
-  __shared__ __align__(1024) uint8_t ring[P * SB];
-  __shared__ unsigned flag;
-
-  int tile, split;
-  decode_wg(blockIdx.x, S, tile, split);
-  if (tile >= mtiles * ntiles) return;
-  const int nt = tile % ntiles, mt = tile / ntiles;
-  const int m0 = mt * BM, n0 = nt * BN;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int wm = wave / WN, wn = wave % WN;  // this wave's m-blocks wm*MB.., strips wn*NB..
-  const int c16 = lane & 15, g = lane >> 4;
-  const int nchunks = K >> 6;
-  const int strips = (N + 15) >> 4;
-  const int kc0 = split * cps;
-  const int nk = min(cps, nchunks - kc0);
-
-  // Epilogue operands first (raw bits; loads the compiler will not sink): they are
-  // the oldest loads in flight, so the first stage wait covers them.
-  uint32_t scb[NB][4], bib[NB][4];
-  {
-    const XT* bsrc = bias ? bias : y;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int n = min(n0 + (wn * NB + nb) * 16 + 4 * g + t, N - 1);
-        scb[nb][t] = load_scale_bits(scale, sdt, n);
-        bib[nb][t] = __hip_atomic_load((uint16_t*)bsrc + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
-  }
-
-  // This wave's fragments: per-lane source at chunk kc0 and the per-chunk stride.
-  const uint8_t* src[FPW];
-  int64_t stride[FPW];
-#pragma unroll
-  for (int j = 0; j < FPW; ++j) {
-    const int f = wave * FPW + j;
-    if (f < XF) {
-      const int mb = f >> 1, h = f & 1;
-      const int m = min(m0 + mb * 16 + c16, M - 1);
-      src[j] = (const uint8_t*)(x + (int64_t)m * ldx + (int64_t)kc0 * 64 + 16 * g + 8 * h);
-      stride[j] = 64 * (int64_t)sizeof(XT);
-    } else {
-      const int s = min(n0 / 16 + (f - XF), strips - 1);
-      src[j] = (const uint8_t*)qs + ((int64_t)s * nchunks + kc0) * 1024 + lane * 16;
-      stride[j] = 1024;
-    }
-  }
-
-  auto issue = [&](uint8_t* stage, int i) {
-#pragma unroll
-    for (int j = 0; j < FPW; ++j) load_to_lds16(src[j] + (int64_t)i * stride[j], stage + (wave * FPW + j) * 1024);
-  };
-
-  f32x4_t acc[NB][MB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-
-  // One stage: every operand read from LDS first, then strip by strip the MFMAs of
-  // strip nb, with the dequantization of strip nb+1 issued ahead of them (independent
-  // VALU work the wave can issue while the matrix pipe runs), h = 0 before h = 1 so
-  // that consecutive MFMAs never share an accumulator.
-  auto compute = [&](const uint8_t* stage) {
-    V xa[MB][2];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) xa[mb][h] = *(const V*)(stage + (2 * (wm * MB + mb) + h) * 1024 + lane * 16);
-    i32x4_t wq[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) wq[nb] = *(const i32x4_t*)(stage + (XF + wn * NB + nb) * 1024 + lane * 16);
-    V cur[2], nxt[2];
-    cur[0] = MM::from_i8((uint32_t)wq[0][0], (uint32_t)wq[0][1]);
-    cur[1] = MM::from_i8((uint32_t)wq[0][2], (uint32_t)wq[0][3]);
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      if (nb + 1 < NB) {
-        nxt[0] = MM::from_i8((uint32_t)wq[nb + 1][0], (uint32_t)wq[nb + 1][1]);
-        nxt[1] = MM::from_i8((uint32_t)wq[nb + 1][2], (uint32_t)wq[nb + 1][3]);
-      }
-#pragma unroll
-      for (int h = 0; h < 2; ++h)
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = MM::mma(cur[h], xa[mb][h], acc[nb][mb]);
-      if (nb + 1 < NB) {
-        cur[0] = nxt[0];
-        cur[1] = nxt[1];
-      }
-    }
-  };
-
-  // Stage i: wait for this wave's loads of stage i (up to P-2 later stages may stay
-  // in flight), barrier (every wave's loads of stage i have landed, and every wave
-  // is done with stage i-1, whose buffer the next issue reuses), issue stage i+P-1,
-  // consume stage i.
-  for (int p = 0; p < P - 1; ++p)
-    if (p < nk) issue(ring + p * SB, p);
-  int cur = 0, nxt = P - 1;
-  for (int i = 0; i < nk; ++i) {
-    wait_stages<FPW, P - 2>(nk - 1 - i);
-    barrier_only();
-    if (i + P - 1 < nk) issue(ring + nxt * SB, i + P - 1);
-    compute(ring + cur * SB);
-    cur = cur + 1 == P ? 0 : cur + 1;
-    nxt = nxt + 1 == P ? 0 : nxt + 1;
-  }
-
-  if (S > 1) {
-    constexpr int NV = NB * MB * 4;
-    float a[NV];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) a[(nb * MB + mb) * 4 + t] = acc[nb][mb][t];
-    if (!splitk_meet<NV>(a, part + (int64_t)tile * S * 256 * NV, &counters[tile], S, split, tid, 256, &flag))
-      return;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int t = 0; t < 4; ++t) acc[nb][mb][t] = a[(nb * MB + mb) * 4 + t];
-  }
-
-  // D of each 16x16 MFMA: lane (c16, g) holds rows 4g..4g+3 (weight rows n) of
-  // column c16 (activation row m): four consecutive outputs of one row of y.
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int nbase = n0 + (wn * NB + nb) * 16 + 4 * g;
-    float sc[4], bi[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      sc[t] = scale_bits_to_f32(scb[nb][t], sdt);
-      bi[t] = bias ? xbits_to_f32<XT>(bib[nb][t]) : 0.0f;
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      const int m = m0 + (wm * MB + mb) * 16 + c16;
-      if (m >= M) continue;
-      XT* yr = y + (int64_t)m * ldy;
-      float v[4];
-#pragma unroll
-      for (int t = 0; t < 4; ++t) v[t] = bias ? acc[nb][mb][t] * sc[t] + bi[t] : acc[nb][mb][t] * sc[t];
-      const uint32_t lo = pack2_f32<XT>(v[0], v[1]), hi = pack2_f32<XT>(v[2], v[3]);
-      if (nbase + 3 < N && ((uintptr_t)(yr + nbase) & 7) == 0) {
-        *(uint2*)(yr + nbase) = make_uint2(lo, hi);
-      } else {
-        const uint16_t o[4] = {(uint16_t)lo, (uint16_t)(lo >> 16), (uint16_t)hi, (uint16_t)(hi >> 16)};
-#pragma unroll
-        for (int t = 0; t < 4; ++t)
-          if (nbase + t < N) yr[nbase + t] = XT{o[t]};
-      }
-    }
-  }
-}
-
-}  // namespace qtts
+// W8A16 GEMM for prefill-sized rows (M > 16) on strip-layout int8 weights, gfx950:
+// the pipelined tile kernel of tile_w8a16.h.  Replaces _w8_gemm_kernel
+// (qtts/quant/kernels.py:89-135) for M > 16 when K % 64 == 0.
+#include "tile_w8a16.h"
 
 using namespace qtts;
-
-namespace {
-
-struct PipeCfg { int bm, bn, P, wm, S, cps, mtiles, ntiles; };
-
-constexpr int pipe_stage_bytes_c(int bm, int bn) { return (bm / 8 + bn / 16) * 1024; }
-
-// Stage counts built per tile shape; a calibrator may pick one through algo bits 16-23.
-bool pipe_p_ok(int bm, int bn, int p) {
-  if (p != 2 && p != 3 && p != 4 && p != 6 && p != 8) return false;
-  const int fpw = (bm / 8 + bn / 16) / 4;
-  return p * pipe_stage_bytes_c(bm, bn) + 64 <= kLdsBytes && (p - 2) * fpw < 64;
-}
-
-// Automatic tile choice, from a sweep of BM x BN x stages x splits over the talker
-// and code-predictor shapes at M = 32..1024 (within 3% of the per-shape best on
-// average): 32 x 64 tiles with 4 stages up to M = 128, 64 x 128 with 3 stages
-// above, 128 x 128 from M = 512 when that still makes 512 tiles; then split K until
-// there are 256 workgroups, keeping >= 8 chunks a split.
-// shape_req (algo bits 24-30): bits 0-1 log2(BM / 16) in 1..3, bit 2 a 2 x 2 wave grid
-// (else 1 x 4), bits 4-6 log2(BN / 32) in 1..3; 0 = automatic.
-PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int stages_req, int shape_req = 0) {
-  PipeCfg c;
-  const int nchunks = std::max(1, (int)(k / 64));
-  c.wm = 1;
-  if (shape_req != 0) {
-    c.bm = 16 << (shape_req & 3);
-    c.bn = 32 << ((shape_req >> 4) & 7);
-    c.wm = (shape_req >> 2) & 1 ? 2 : 1;
-  } else if (m <= 128) {
-    c.bm = 32;
-    c.bn = 64;
-  } else if (m >= 512 && ((m + 127) / 128) * ((n + 127) / 128) >= 512) {
-    c.bm = 128;  // enough 128 x 128 tiles to fill the GPU twice: fewer re-reads per MFMA
-    c.bn = 128;
-  } else {
-    c.bm = 64;
-    c.bn = 128;
-  }
-  c.mtiles = (int)((m + c.bm - 1) / c.bm);
-  c.ntiles = (int)((n + c.bn - 1) / c.bn);
-  c.P = stages_req > 0 ? stages_req : (c.bm * c.bn <= 32 * 64 ? 4 : 3);
-  const int64_t tiles = (int64_t)c.mtiles * c.ntiles;
-  int S = splits_req;
-  if (S <= 0) {
-    S = 1;
-    while (tiles * S < 256 && nchunks / (S * 2) >= 8) S *= 2;
-  }
-  S = std::max(1, std::min(S, nchunks));
-  if (tiles > kMaxSplitTiles) S = 1;
-  c.cps = (nchunks + S - 1) / S;
-  c.S = (nchunks + c.cps - 1) / c.cps;
-  return c;
-}
-
-int64_t pipe_ws(const PipeCfg& c) {
-  if (c.S <= 1) return 0;
-  const int64_t nv = (int64_t)(c.bn / 64) * (c.bm / 16) * 4;
-  return kCounterBytes + (int64_t)c.mtiles * c.ntiles * c.S * 256 * nv * 4;
-}
-
-struct PipeArgs {
-  const void* x; int64_t m, k, ldx; const int8_t* qs; int64_t n; const void* scale; int sdt; const void* bias;
-  void* y; int64_t ldy; float* part; unsigned* counters;
-};
-
-template <typename XT, int BM, int BN, int P, int WM>
-void launch_pipe_p(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
-  if constexpr (P * pipe_stage_bytes_c(BM, BN) + 64 <= kLdsBytes) {
-    qtts::launch(&w8a16_pipe_kernel<XT, BM, BN, P, WM>, dim3(blocks), dim3(256), 0, st, (const XT*)a.x, (int)a.m,
-                 (int)a.k, a.ldx, a.qs, (int)a.n, a.scale, a.sdt, (const XT*)a.bias, (XT*)a.y, a.ldy, a.part,
-                 a.counters, c.mtiles, c.ntiles, c.S, c.cps);
-  }
-}
-
-template <typename XT, int BM, int BN, int WM>
-void launch_pipe_stages(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
-  switch (c.P) {
-    case 2: launch_pipe_p<XT, BM, BN, 2, WM>(c, a, blocks, st); break;
-    case 3: launch_pipe_p<XT, BM, BN, 3, WM>(c, a, blocks, st); break;
-    case 4: launch_pipe_p<XT, BM, BN, 4, WM>(c, a, blocks, st); break;
-    case 6: launch_pipe_p<XT, BM, BN, 6, WM>(c, a, blocks, st); break;
-    default: launch_pipe_p<XT, BM, BN, 8, WM>(c, a, blocks, st); break;
-  }
-}
-
-template <typename XT, int BM, int BN>
-void launch_pipe_grid(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
-  if (c.wm == 2) launch_pipe_stages<XT, BM, BN, 2>(c, a, blocks, st);
-  else launch_pipe_stages<XT, BM, BN, 1>(c, a, blocks, st);
-}
-
-template <typename XT, int BM>
-void launch_pipe_bn(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
-  if (c.bn == 256) launch_pipe_grid<XT, BM, 256>(c, a, blocks, st);
-  else if (c.bn == 128) launch_pipe_grid<XT, BM, 128>(c, a, blocks, st);
-  else launch_pipe_grid<XT, BM, 64>(c, a, blocks, st);
-}
-
-template <typename XT>
-void launch_pipe_bm(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
-  if (c.bm == 32) launch_pipe_bn<XT, 32>(c, a, blocks, st);
-  else if (c.bm == 64) launch_pipe_bn<XT, 64>(c, a, blocks, st);
-  else launch_pipe_bn<XT, 128>(c, a, blocks, st);
-}
-
-}  // namespace
-
-bool pipe_shape_ok(int shape) {
-  if (shape == 0) return true;
-  const int b = shape & 3, c = (shape >> 4) & 7;
-  return (shape >> 7) == 0 && (shape & 8) == 0 && b >= 1 && c >= 1 && c <= 3;
-}
 
 int64_t qtts_w8a16_pipe_ws_bytes(int64_t m, int64_t n, int64_t k, int splits, int shape) {
   if (!pipe_shape_ok(shape)) return 0;
@@ -362,27 +14,6 @@ int64_t qtts_w8a16_pipe_ws_bytes(int64_t m, int64_t n, int64_t k, int splits, in
 int qtts_launch_w8a16_pipe(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
                            int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
                            int splits, int stages, int shape, void* ws, int64_t ws_bytes, hipStream_t st) {
-  if (!pipe_shape_ok(shape))
-    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 tile: bad tile shape code %d", shape);
-  PipeCfg c = pipe_cfg(m, n, k, splits, stages, shape);
-  if (!pipe_p_ok(c.bm, c.bn, c.P))
-    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 tile: %d stages are not built for a %dx%d tile", c.P, c.bm,
-                          c.bn);
-  const int64_t need = pipe_ws(c);
-  if (need > ws_bytes || (need > 0 && !ws)) {
-    if (splits > 0)
-      return qtts_set_error(QTTS_ERR_WORKSPACE, "w8a16 tile with %d splits needs %lld workspace bytes, got %lld", c.S,
-                            (long long)need, (long long)ws_bytes);
-    c = pipe_cfg(m, n, k, 1, stages, shape);
-  }
-  const int64_t tiles = (int64_t)c.mtiles * c.ntiles;
-  const int64_t blocks = (tiles + 7) / 8 * 8 * c.S;
-  if (blocks <= 0 || blocks >= ((int64_t)1 << 31))
-    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 tile: problem too large");
-  unsigned* counters = (unsigned*)ws;
-  float* part = ws ? (float*)((char*)ws + kCounterBytes) : nullptr;
-  const PipeArgs a{x, m, k, ldx, qs, n, scale, sdt, bias, y, ldy, part, counters};
-  if (x_dtype == QTTS_BF16) launch_pipe_bm<bf16_t>(c, a, (unsigned)blocks, st);
-  else launch_pipe_bm<f16_t>(c, a, (unsigned)blocks, st);
-  return qtts_check_launch("w8a16_tile");
+  return w8a16_pipe_launch<false>("w8a16_tile", x, x_dtype, m, k, ldx, qs, n, scale, sdt, bias, y, ldy, splits,
+                                  stages, shape, ws, ws_bytes, st);
 }

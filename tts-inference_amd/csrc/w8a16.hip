@@ -228,57 +228,7 @@ using namespace qtts;
 
 namespace {
 
-struct SkinnyCfg { int mb, waves, cpw, S, cps, strips; };
 struct TileCfg { int bm, S, cps, mtiles, ntiles; };
-
-// The skinny kernels take up to kSkinnyMaxM rows on strip weights.  The automatic
-// choice keeps them up to 32 rows (two m-blocks) for weights of at most 9 MiB and
-// otherwise moves to the tile kernel past 16 rows: measured on the talker and
-// code-predictor shapes at M = 16..96, where the tile kernel wins on the 12-25 MB
-// weights from 24 rows and everywhere from 48.
-constexpr int kSkinnyMaxM = 64, kSkinnyAutoMaxM = 32;
-constexpr int64_t kSkinnyAutoMaxBytes = 9 << 20;
-
-// m-blocks of 16 activation rows a skinny call carries.
-int skinny_mb(int64_t m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }
-
-// Chunks (64 columns, 1 KiB of a strip) a wave keeps in flight at once; a chunk holds
-// 4 + 8 MB registers a lane.  Built: MB = 1: 4 or 8 (4 or 6 at 16 waves, whose 1024
-// threads leave 128 registers a lane); MB = 2: 4 or 8 (4 at 16 waves); MB = 4: 4, at
-// most 8 waves.
-bool skinny_cpw_ok(int mb, int w, int cpw) {
-  if (mb == 1) return w == 16 ? (cpw == 4 || cpw == 6) : (cpw == 4 || cpw == 8);
-  if (mb == 2) return w == 16 ? cpw == 4 : (cpw == 4 || cpw == 8);
-  return mb == 4 && w <= 8 && cpw == 4;
-}
-int skinny_cpw_max(int mb, int w) { return mb == 1 ? (w == 16 ? 6 : 8) : (mb == 2 ? (w == 16 ? 4 : 8) : 4); }
-int skinny_waves_max(int mb) { return mb == 4 ? 8 : 16; }
-
-SkinnyCfg skinny_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int waves_req, int cpw_req) {
-  SkinnyCfg c;
-  c.mb = skinny_mb(m);
-  c.strips = (int)((n + 15) / 16);
-  const int nchunks = std::max(1, (int)((k + 63) / 64));
-  int W = waves_req, S = splits_req, C = cpw_req;
-  if (W <= 0) {
-    // Few, fat waves: the fewest waves (with the most chunks in flight each) that
-    // cover a strip's K without a split.  Measured on the talker and code-predictor
-    // shapes this beats more, thinner waves at every M in 1..16.
-    W = 1;
-    while (W < skinny_waves_max(c.mb) && W * skinny_cpw_max(c.mb, W) < nchunks) W *= 2;
-  }
-  if (C <= 0) C = skinny_cpw_max(c.mb, W);
-  c.waves = W;
-  c.cpw = C;
-  // The kernel runs one group of C chunks per wave: raise S until a wave's share
-  // fits (a requested split count is a minimum).
-  S = std::max(S, 1);
-  S = std::max(S, (nchunks + W * C - 1) / (W * C));
-  S = std::min(S, nchunks);
-  c.cps = (nchunks + S - 1) / S;
-  c.S = (nchunks + c.cps - 1) / c.cps;
-  return c;
-}
 
 TileCfg tile_cfg(int64_t m, int64_t n, int64_t k, int splits_req) {
   TileCfg c;
@@ -297,10 +247,6 @@ TileCfg tile_cfg(int64_t m, int64_t n, int64_t k, int splits_req) {
   c.cps = (nchunks + S - 1) / S;
   c.S = (nchunks + c.cps - 1) / c.cps;
   return c;
-}
-
-int64_t skinny_ws(const SkinnyCfg& c) {
-  return c.S <= 1 ? 0 : kCounterBytes + (int64_t)c.strips * c.S * 64 * 4 * c.mb * 4;
 }
 
 int64_t tile_ws(const TileCfg& c) {

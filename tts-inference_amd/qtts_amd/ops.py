@@ -13,8 +13,8 @@ import threading
 import torch
 
 from . import _lib
-from ._lib import (ALGO_AUTO, DIV_DEVICE, DIV_IEEE, OP_FP8_LINEAR, OP_INT8_LINEAR, OP_W8A16,  # noqa: F401
-                   OP_W8A8_FP8, OP_W8A8_INT8, STRIP_FP8, STRIP_INT8, algo_code)
+from ._lib import (ALGO_AUTO, DIV_DEVICE, DIV_IEEE, OP_FP8_LINEAR, OP_FP8W, OP_INT8_LINEAR,  # noqa: F401
+                   OP_W8A16, OP_W8A8_FP8, OP_W8A8_INT8, STRIP_FP8, STRIP_INT8, algo_code)
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
@@ -513,6 +513,46 @@ def int8_linear_strips(x: torch.Tensor, qws: torch.Tensor, n: int, sw: torch.Ten
     if qws.dtype != torch.int8 or qws.numel() != strip_bytes(n, k, STRIP_INT8):
         raise ValueError(f"weight is not an int8 strip-layout [{n}, {k}] buffer")
     return _int8_linear(x, qws, n, 0, sw, bias, div_mode, algo, strips=True)
+
+
+# ---- fp8 weight-only (Fp8WeightOnlyMethod, qtts/quant/fp8.py:92-123) -------------------
+
+def fp8w_strips(q: torch.Tensor) -> torch.Tensor:
+    """e4m3 ``[N, K]`` codes -> the 64-column strip layout the fp8 weight-only kernels read
+    (``uint8``; ``[N, K]`` when no padding is needed, else 1-D)."""
+    if q.dtype not in (torch.float8_e4m3fn, torch.uint8):
+        raise ValueError(f"expected e4m3 codes, got {q.dtype}")
+    return to_strips(q.view(torch.uint8), STRIP_INT8)
+
+
+def fp8w_gemm_strips(x: torch.Tensor, qs: torch.Tensor, n: int, scale: torch.Tensor,
+                     bias: torch.Tensor | None = None, algo: int = ALGO_AUTO) -> torch.Tensor:
+    """``x @ (e4m3(q) * scale)^T + bias`` with the codes converted in registers.
+
+    x ``[..., K]`` bf16 / fp16 (K % 64 == 0), qs from :func:`fp8w_strips`, scale ``[N]``
+    fp32, bias ``[N]`` or None.  Returns a fresh ``[..., N]`` tensor in x's dtype."""
+    shape = x.shape
+    a = _flatten(x)
+    rows, k = a.shape
+    if qs.element_size() != 1 or qs.numel() != strip_bytes(n, k, STRIP_INT8):
+        raise ValueError(f"weight is not a 64-column strip-layout [{n}, {k}] buffer of e4m3 codes")
+    if scale.numel() != n:
+        raise ValueError(f"scale has {scale.numel()} entries for {n} output channels")
+    if bias is not None:
+        if bias.numel() != n:
+            raise ValueError(f"bias has {bias.numel()} entries for {n} output channels")
+        bias = bias.to(a.dtype).contiguous()
+    if a.data_ptr() % 16 or (rows > 1 and a.stride(0) % 8):
+        a = a.contiguous() if a.data_ptr() % 16 == 0 else a.clone()
+    scale = scale.reshape(-1).to(torch.float32).contiguous()
+    dev = _require_cuda(a, qs, scale, bias)
+    out = torch.empty((rows, n), dtype=a.dtype, device=dev)
+    ws, ws_n = _ws_for(dev)
+    st = _lib.load().qtts_fp8w_gemm_strips(
+        _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else k, _ptr(qs), n, _ptr(scale), _ptr(bias),
+        _ptr(out), n, algo, ws, ws_n, _stream(dev))
+    _lib.check(st, "fp8w_gemm_strips")
+    return out.reshape(*shape[:-1], n)
 
 
 class KernelTimer:

@@ -97,7 +97,9 @@ def build_method(config: QuantConfig, calibration_batch: int = 16) -> QuantMetho
         supported, reason = fp8_supported()
         if not supported:
             raise RuntimeError(f"fp8 quantization unavailable: {reason}")
-        return Fp8WeightOnlyMethod() if method.endswith("_weight_only") else Fp8Method()
+        if method == "fp8_weight_only":
+            return Fp8WeightOnlyMethod(calibrate=config.calibrate, calibration_batch=calibration_batch)
+        return Fp8Method()
     if method == "int8_weight_only":
         return Int8WeightOnlyMethod(calibrate=config.calibrate, calibration_batch=calibration_batch)
     if method == "int8":

@@ -5,16 +5,23 @@ activations quantized at run time, and a gfx950 fp8 MFMA GEMM with the rowwise x
 columnwise scale epilogue in place of torch._scaled_mm.  It is applied
 uniformly, as in the reference (qtts/quant/fp8.py:52-89).
 
-``Fp8WeightOnlyMethod`` raises NotImplementedError, as the reference does
-(qtts/quant/fp8.py:92-123).
+``Fp8WeightOnlyMethod`` (fp8 weights, bf16 / fp16 activations) is the fused kernel
+the reference's stub names as the right home for fp8 weights (qtts/quant/fp8.py:92-123,
+where it raises NotImplementedError because Triton could not load e4m3): the W8A16
+kernels with the e4m3 codes converted in registers.  Calibrated per layer shape
+like the int8 weight-only method.
 """
 
 from __future__ import annotations
 
 import torch
 
+import torch.nn.functional as F
+
 from .. import _lib, ops
 from .base import QuantMethodBase
+from .calibrate import pick_fastest
+from .kernels import kernel_available
 
 _FP8_MAX = 448.0
 
@@ -68,12 +75,104 @@ def fp8_weight_rowmajor(layer) -> torch.Tensor:
     return layer.fp8_weight.t()
 
 
+#: Per (N, K, bucket) algo codes chosen by calibration for fp8 weight-only layers.
+_FP8W_ALGO: dict[tuple[int, int, int], int] = {}
+
+
+def _fp8w_candidates(rows: int) -> dict[str, int]:
+    """Kernel configurations worth timing at ``rows`` (the algo bits of include/qtts_amd.h)."""
+    c: dict[str, int] = {}
+    if rows <= 16:
+        c["skinny"] = _lib.algo_code(_lib.ALGO_SKINNY)
+        for s in (1, 2, 4):
+            for w in (4, 8, 16):
+                c[f"skinny_s{s}_w{w}"] = _lib.algo_code(_lib.ALGO_SKINNY, splits=s, waves=w)
+    else:
+        c["tile"] = _lib.algo_code(_lib.ALGO_TILE)
+        for s in (1, 2, 4):
+            c[f"tile_s{s}"] = _lib.algo_code(_lib.ALGO_TILE, splits=s)
+        for bm in (1, 2, 3):
+            for bn in (1, 2):
+                c[f"tile_bm{16 << bm}_bn{32 << bn}"] = _lib.algo_code(_lib.ALGO_TILE, 0, 0, bm | (bn << 4))
+    return c
+
+
+def fp8w_weight_rowmajor(layer) -> torch.Tensor:
+    """The packer's row-major ``[N, K]`` e4m3 codes of an fp8 weight-only layer."""
+    q = ops.from_strips(layer.fp8w_weight, layer.out_features, layer.in_features, _lib.STRIP_INT8)
+    return q.view(torch.float8_e4m3fn)
+
+
 class Fp8WeightOnlyMethod(QuantMethodBase):
-    """fp8 weights with model-dtype activations: not implemented, as in the reference."""
+    """fp8 (e4m3) weights, bf16 / fp16 activations, converted inside the GEMM.
+
+    The weight is packed as quantize_weight_fp8 packs it (qtts/quant/fp8.py:45-49: per
+    channel fp32 scale, e4m3 codes) and stored in the 64-column strip layout
+    (``fp8w_weight``, ``fp8w_scale``).  Layers the kernels cannot take (K % 64 != 0 or
+    a non-16-bit weight dtype) and, with ``calibrate``, layers where no kernel
+    configuration beats F.linear by 5% keep their weight and F.linear.
+    """
 
     name = "fp8_weight_only"
 
-    def __init__(self) -> None:
-        raise NotImplementedError(
-            "fp8 weight-only is not implemented: use --quant-method int8_weight_only for the same "
-            "footprint, or --quant-method fp8 for the W8A8 hardware path.")
+    def __init__(self, calibrate: bool = True, calibration_batch: int = 16, div_mode: int = _lib.DIV_DEVICE) -> None:
+        available, reason = kernel_available()
+        if not available:
+            raise RuntimeError(f"fp8 weight-only needs the gfx950 fused kernel: {reason}")
+        self.calibrate = calibrate
+        self.calibration_batch = calibration_batch
+        self.div_mode = div_mode
+        self.quantized = 0
+        self.declined = 0
+
+    def _profitable(self, layer, qs: torch.Tensor, scale: torch.Tensor) -> bool:
+        if not self.calibrate:
+            return True
+        weight = layer.weight
+        rows = max(1, self.calibration_batch)
+        n, k = layer.out_features, layer.in_features
+        gen = torch.Generator(device=weight.device).manual_seed(0)
+        x = torch.randn(rows, k, device=weight.device, dtype=weight.dtype, generator=gen)
+        algos = _fp8w_candidates(rows)
+        ops.reserve_workspace(weight.device, max(ops.workspace_bytes(_lib.OP_FP8W, rows, n, k, a)
+                                                 for a in algos.values()))
+        cands = {name: (lambda a=algo: ops.fp8w_gemm_strips(x, qs, n, scale, None, a)) for name, algo in algos.items()}
+        best = pick_fastest(cands, lambda: F.linear(x, weight, None), key=("fp8_wo", n, k, rows, str(weight.dtype)))
+        if best is not None:
+            from .int8 import bucket_of
+            _FP8W_ALGO.setdefault((n, k, bucket_of(rows)), algos[best])
+        return best is not None
+
+    def _decline(self, layer) -> None:
+        self.declined += 1
+        layer.register_buffer("fp8w_weight", None, persistent=False)
+
+    def process_weights(self, layer) -> None:
+        weight = layer.weight
+        if layer.in_features % 64 or weight.dtype not in (torch.bfloat16, torch.float16):
+            self._decline(layer)
+            return
+        q, scale = quantize_weight_fp8(weight, self.div_mode)
+        qs = ops.fp8w_strips(q)
+        if not self._profitable(layer, qs, scale):
+            self._decline(layer)
+            return
+        ops.reserve_workspace(weight.device, max(
+            ops.workspace_bytes(_lib.OP_FP8W, m, layer.out_features, layer.in_features) for m in (16, 64, 128)))
+        layer.register_buffer("fp8w_weight", qs, persistent=False)
+        layer.register_buffer("fp8w_scale", scale, persistent=False)
+        layer.weight = torch.nn.Parameter(torch.empty(0, dtype=weight.dtype, device=weight.device),
+                                          requires_grad=False)
+        self.quantized += 1
+
+    def applies_to(self, layer) -> bool:
+        return getattr(layer, "fp8w_weight", None) is not None
+
+    def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        if x.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError(f"fp8 weight-only layers take bf16 or fp16 activations, got {x.dtype}")
+        from .int8 import bucket_of
+        n, k = layer.out_features, layer.in_features
+        rows = x.numel() // k if k else 0
+        algo = _FP8W_ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
+        return ops.fp8w_gemm_strips(x, layer.fp8w_weight, n, layer.fp8w_scale, bias, algo)
