@@ -17,7 +17,8 @@ launch from HIP events bound to its dispatch) and the reference's CPU path timed
 sample on this host.
 
 Other configs (--config 0..4) print their own JSON line with the same keys;
---int8-w8a8 times the int8 W8A8 linear (Int8Method) on the talker shapes.
+--int8-w8a8 times the int8 W8A8 linear (Int8Method) on the talker shapes; --fp8w the
+configs[1] decode stack with fp8 weight-only weights (Fp8WeightOnlyMethod).
 """
 
 from __future__ import annotations
@@ -401,6 +402,35 @@ def run_int8_w8a8(args, torch, ops):
             "shapes": res}
 
 
+def run_fp8w_stack(args, torch, ops):
+    """The configs[1] talker decode stack with fp8 (e4m3) weight-only weights (Fp8WeightOnlyMethod):
+    the same 1.41 GB of 8-bit codes, converted with v_cvt_scalef32_pk_bf16_fp8 instead of from int8."""
+    ms = (1, 2, 4, 8)
+    layers = 28
+    stack = []
+    for layer in range(layers):
+        for idx, (name, n, k) in enumerate(TALKER):
+            g = torch.Generator(device="cuda").manual_seed(1000 + 16 * layer + idx)
+            w = torch.randn(n, k, device="cuda", generator=g) * 0.02
+            q, s = ops.pack_fp8(w)
+            stack.append({"name": name, "n": n, "k": k, "qs": ops.fp8w_strips(q), "s": s})
+            del w, q
+    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    xs = make_inputs(torch, [k for _, _, k in TALKER], ms)
+    per_m = {}
+    for m in ms:
+        g_q = capture(torch, lambda m=m: [ops.fp8w_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"]) for e in stack])
+        t_q = time_graph(torch, g_q, args.steps, args.warmup)
+        nbytes = sum(fp8_bytes(m, e["n"], e["k"]) for e in stack)
+        per_m[str(m)] = {"stack_us": round(t_q * 1e3, 2), "GBps": round(nbytes / (t_q * 1e-3) / 1e9, 1),
+                         "pct_of_hbm_peak": round(100 * nbytes / (t_q * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1)}
+        del g_q
+        log(f"[bench] fp8 weight-only M={m}: {per_m[str(m)]}")
+    return {"metric": "fp8 weight-only decode linear-stack us/step and HBM GB/s", "value": None, "unit": "GB/s",
+            "n_gpus": 1, "config": {"workload": "configs[1] shapes with e4m3 weight-only weights, 28 layers, "
+                                                "one HIP graph per M", "M": list(ms)}, "per_m": per_m}
+
+
 def run_traffic_probe(args, torch, ops):
     """Kernels for a rocprofv3 --pmc pass: a 256 MiB device copy (known bytes, the counters' scale)
     and the dominant kernel of configs[1] (gate_up over its 28 distinct weights at M = 1, 2, 4, 8),
@@ -478,6 +508,8 @@ def main() -> int:
     ap.add_argument("--summarize-pmc", metavar="DIR", help="digest a rocprofv3 --pmc run")
     ap.add_argument("--int8-w8a8", action="store_true",
                     help="time the int8 W8A8 linear (Int8Method) on the talker shapes instead of a config")
+    ap.add_argument("--fp8w", action="store_true",
+                    help="time the configs[1] decode stack with fp8 weight-only weights instead of a config")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="launch only the kernels a rocprofv3 --pmc pass measures (copy + gate_up)")
     args = ap.parse_args()
@@ -506,6 +538,8 @@ def main() -> int:
         runner = run_traffic_probe
     if args.int8_w8a8:
         runner = run_int8_w8a8
+    if args.fp8w:
+        runner = run_fp8w_stack
     with torch.inference_mode():
         result = runner(args, torch, ops)
     result["device"] = torch.cuda.get_device_name()
