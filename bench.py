@@ -18,7 +18,8 @@ sample on this host.
 
 Other configs (--config 0..4) print their own JSON line with the same keys;
 --int8-w8a8 times the int8 W8A8 linear (Int8Method) on the talker shapes; --fp8w the
-configs[1] decode stack with fp8 weight-only weights (Fp8WeightOnlyMethod).
+configs[1] decode stack with fp8 weight-only weights (Fp8WeightOnlyMethod); --mlp the
+talker MLP with its activation fused into the down projection.
 """
 
 from __future__ import annotations
@@ -431,6 +432,49 @@ def run_fp8w_stack(args, torch, ops):
                                                 "one HIP graph per M", "M": list(ms)}, "per_m": per_m}
 
 
+def run_mlp(args, torch, ops):
+    """The talker MLP at decode (GatedMLP.forward, qtts/layers/activation.py:142-147): 28 layers of
+    gate_up -> silu(gate) * up -> down, int8 weight-only, one HIP graph per M.  Three versions:
+    torch's activation between the two int8 GEMMs (the reference's composition), the activation
+    handed to the down projection (fused into its kernel at M <= 2, one activation kernel above),
+    and bf16 hipBLASLt throughout."""
+    import torch.nn.functional as F
+    ms = (1, 2, 4, 8)
+    layers = 28
+    shapes = [s_ for s_ in TALKER if s_[0] in ("gate_up", "down")]
+    stack = make_stack(torch, ops, shapes, layers, keep_bf16=True)
+    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    xs = make_inputs(torch, [2048], ms)
+    pairs = [(stack[2 * i], stack[2 * i + 1]) for i in range(layers)]
+
+    def act(gu):
+        gate, up = gu.split([6144, 6144], dim=-1)
+        return F.silu(gate) * up
+
+    per_m = {}
+    for m in ms:
+        x = xs[(m, 2048)]
+        composed = lambda: [ops.w8a16_gemm_strips(act(ops.w8a16_gemm_strips(x, g["qs"], g["n"], g["s"])), d["qs"], d["n"],
+                                                  d["s"]) for g, d in pairs]
+        fused = lambda: [ops.w8a16_silu_mul_gemm_strips(ops.w8a16_gemm_strips(x, g["qs"], g["n"], g["s"]), d["qs"],
+                                                        d["n"], d["s"]) for g, d in pairs]
+        bf16 = lambda: [F.linear(act(F.linear(x, g["w_bf16"])), d["w_bf16"]) for g, d in pairs]
+        t = {}
+        for name, fn in (("composed", composed), ("fused", fused), ("bf16", bf16)):
+            graph = capture(torch, fn)
+            t[name] = time_graph(torch, graph, args.steps, args.warmup)
+            del graph
+        per_m[str(m)] = {"int8_torch_activation_us": round(t["composed"] * 1e3, 2),
+                         "int8_fused_activation_us": round(t["fused"] * 1e3, 2),
+                         "bf16_hipblaslt_us": round(t["bf16"] * 1e3, 2),
+                         "fused_vs_composed": round(t["composed"] / t["fused"], 3),
+                         "fused_vs_bf16": round(t["bf16"] / t["fused"], 3)}
+        log(f"[bench] MLP M={m}: {per_m[str(m)]}")
+    return {"metric": "talker MLP decode us/step (gate_up, silu*up, down; 28 layers)", "value": None, "unit": "us",
+            "n_gpus": 1, "config": {"workload": "talker GatedMLP x 28 layers, int8 weight-only, one HIP graph per M",
+                                    "M": list(ms)}, "per_m": per_m}
+
+
 def run_traffic_probe(args, torch, ops):
     """Kernels for a rocprofv3 --pmc pass: a 256 MiB device copy (known bytes, the counters' scale)
     and the dominant kernel of configs[1] (gate_up over its 28 distinct weights at M = 1, 2, 4, 8),
@@ -510,6 +554,8 @@ def main() -> int:
                     help="time the int8 W8A8 linear (Int8Method) on the talker shapes instead of a config")
     ap.add_argument("--fp8w", action="store_true",
                     help="time the configs[1] decode stack with fp8 weight-only weights instead of a config")
+    ap.add_argument("--mlp", action="store_true",
+                    help="time the talker MLP (gate_up, silu*up, down) with the activation fused into down")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="launch only the kernels a rocprofv3 --pmc pass measures (copy + gate_up)")
     args = ap.parse_args()
@@ -540,6 +586,8 @@ def main() -> int:
         runner = run_int8_w8a8
     if args.fp8w:
         runner = run_fp8w_stack
+    if args.mlp:
+        runner = run_mlp
     with torch.inference_mode():
         result = runner(args, torch, ops)
     result["device"] = torch.cuda.get_device_name()

@@ -53,7 +53,8 @@ typedef enum {
     QTTS_OP_FP8_LINEAR = 2,
     QTTS_OP_W8A8_INT8 = 3,
     QTTS_OP_INT8_LINEAR = 4,
-    QTTS_OP_FP8W = 5
+    QTTS_OP_FP8W = 5,
+    QTTS_OP_W8A16_SILU = 6
 } qtts_op;
 
 /* --- housekeeping ------------------------------------------------------------ */
@@ -151,6 +152,28 @@ int qtts_w8a16_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int
                            const int8_t* qs, int64_t n, const void* scale, int scale_dtype,
                            const void* bias, void* y, int64_t ldy, int algo, void* ws,
                            int64_t ws_bytes, void* stream);
+
+/* --- GatedMLP: activation and down projection ----------------------------------- */
+
+/* The activation of GatedMLP.forward (qtts/layers/activation.py:142-147) in one pass:
+ *   h[r, c] = dtype(dtype(silu(g)) * u),  g = gate_up[r, c], u = gate_up[r, k + c],
+ *   silu(g) = g / (1 + exp(-g)) in fp32
+ * with torch's rounding for `F.silu(gate) * up` on x_dtype tensors (two kernels there).
+ * gate_up: [m, 2k] of x_dtype, row stride ld_gate_up (the fused gate_up_proj output,
+ * gate then up).  h: [m, k], row stride ldh. */
+int qtts_silu_mul(const void* gate_up, int x_dtype, int64_t m, int64_t k, int64_t ld_gate_up,
+                  void* h, int64_t ldh, void* stream);
+
+/* down_proj(F.silu(gate) * up) with an int8 weight-only down projection on strip
+ * weights: qtts_w8a16_gemm_strips of qtts_silu_mul's output, in one call.  A single
+ * decode row (m == 1, k % 64 == 0) has the activation computed inside the GEMM kernel
+ * while it stages its activation row; other calls run qtts_silu_mul into the workspace
+ * first.  Same bits either way.  x_dtype bf16 or fp16; workspace: qtts_workspace_bytes(QTTS_OP_W8A16_SILU). */
+int qtts_w8a16_silu_mul_gemm_strips(const void* gate_up, int x_dtype, int64_t m, int64_t k,
+                                    int64_t ld_gate_up, const int8_t* qs, int64_t n,
+                                    const void* scale, int scale_dtype, const void* bias,
+                                    void* y, int64_t ldy, int algo, void* ws, int64_t ws_bytes,
+                                    void* stream);
 
 /* --- fp8 W8A8 --------------------------------------------------------------------- */
 

@@ -58,6 +58,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_w8a8_ref_f64.argtypes = [p, p, i64, i64, p, i64, p, p, p]
         L.oracle_fp8w_ref_f64.restype = None
         L.oracle_fp8w_ref_f64.argtypes = [p, i64, i64, p, i64, p, p, p]
+        L.oracle_silu_mul.restype = None
+        L.oracle_silu_mul.argtypes = [p, i32, i64, i64, i64, p]
         L.oracle_quant_act_int8.restype = None
         L.oracle_quant_act_int8.argtypes = [p, i32, i64, i64, i64, p, p, i32]
         L.oracle_int8_linear_out.restype = None
@@ -183,6 +185,16 @@ def fp8w_ref(x_f32: np.ndarray, q: np.ndarray, scale_f32: np.ndarray,
     y = np.empty((m, n), np.float64)
     lib().oracle_fp8w_ref_f64(_ptr(x), m, k, _ptr(q), n, _ptr(s), _ptr(b), _ptr(y))
     return y
+
+
+def silu_mul(gate_up: np.ndarray, dtype: int = DT_BF16) -> np.ndarray:
+    """``F.silu(gate) * up`` of a fused [m, 2k] gate_up (qtts/layers/activation.py:147)."""
+    gu = _src(gate_up, dtype)
+    m, k2 = gu.shape
+    k = k2 // 2
+    h = np.empty((m, k), np.float32 if dtype == DT_F32 else np.uint16)
+    lib().oracle_silu_mul(_ptr(gu), dtype, m, k, k2, _ptr(h))
+    return h
 
 
 def quant_act_int8(x: np.ndarray, x_dtype: int = DT_BF16, div_mode: int = DIV_DEVICE):

@@ -302,3 +302,20 @@ void oracle_fp8w_ref_f64(const float* x, int64_t m, int64_t k, const uint8_t* q,
             y[i * n + j] = acc;
         }
 }
+
+/* GatedMLP's activation, qtts/layers/activation.py:147 (`F.silu(gate) * up` on tensors
+ * of the activation dtype): silu in fp32 with torch's formula g / (1 + exp(-g)) rounded
+ * to the dtype, then the product in fp32 rounded to the dtype.  gate_up: [m, 2k] (gate
+ * then up), row stride ld; h: [m, k].  Values travel as bf16 / fp16 bits or fp32. */
+void oracle_silu_mul(const void* gate_up, int dtype, int64_t m, int64_t k, int64_t ld, void* h) {
+    for (int64_t r = 0; r < m; ++r)
+        for (int64_t c = 0; c < k; ++c) {
+            float g = load_elem(gate_up, dtype, r * ld + c);
+            float u = load_elem(gate_up, dtype, r * ld + k + c);
+            float s = round_to(g / (1.0f + expf(-g)), dtype);
+            float v = s * u;
+            if (dtype == ORACLE_DT_BF16) ((uint16_t*)h)[r * k + c] = oracle_f32_to_bf16(v);
+            else if (dtype == ORACLE_DT_F16) ((uint16_t*)h)[r * k + c] = oracle_f32_to_f16(v);
+            else ((float*)h)[r * k + c] = v;
+        }
+}

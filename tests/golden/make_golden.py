@@ -11,6 +11,7 @@ own expressions, character for character where the expression is device-neutral:
 * fp8 activations: qtts/quant/fp8.py:77-78
 * naive W8A16 formula: examples/kernels/tune_w8_gemm.py:79
 * int8 W8A8 (Int8Method.apply): qtts/quant/int8.py:146-160, torch._int_mm included
+* GatedMLP's activation: qtts/layers/activation.py:147 (F.silu(gate) * up)
 
 Two division semantics are recorded for every scale (see oracle/qtts_oracle.c):
 ``ieee`` is the literal CPU evaluation of ``tensor / python_float``; ``device`` is
@@ -191,7 +192,8 @@ def main() -> None:
         gemm[f"{name}.y_naive_bf16"] = bf16_bits(naive)
     np.savez_compressed(os.path.join(HERE, "gemm_small.npz"), **gemm)
     int8_w8a8_fixtures()
-    for f in ("int8_pack", "fp8_pack", "act_fp8", "gemm_small", "int8_w8a8"):
+    silu_mul_fixtures()
+    for f in ("int8_pack", "fp8_pack", "act_fp8", "gemm_small", "int8_w8a8", "silu_mul"):
         print(f, os.path.getsize(os.path.join(HERE, f + ".npz")), "bytes")
 
 
@@ -253,6 +255,25 @@ def int8_w8a8_fixtures() -> None:
         for mode in ("ieee", "device"):
             out[f"lin.{name}.{mode}.y"] = _bits(ref_int8_linear(x, q.t().contiguous(), scale, bias, mode))
     np.savez_compressed(os.path.join(HERE, "int8_w8a8.npz"), **out)
+
+
+def silu_mul_fixtures() -> None:
+    """GatedMLP's activation on a fused gate_up output, each dtype: N(0, 3) values, a
+    sweep through silu's range, and the extremes (+-0, large magnitudes, the smallest
+    normals)."""
+    rng = np.random.default_rng(20240801)
+    out: dict[str, np.ndarray] = {}
+    k = 1024
+    gu = rng.normal(0, 3, (6, 2 * k)).astype(np.float32)
+    gu[0, :k] = np.linspace(-30, 30, k, dtype=np.float32)
+    gu[1, :8] = [0.0, -0.0, 88.0, -88.0, 1e-30, -1e-30, 1e4, -1e4]
+    gu[2, k:] = 1.0
+    for dt, tdt in _TORCH_DT.items():
+        x = torch.from_numpy(gu).to(tdt)
+        gate, up = x[:, :k], x[:, k:]
+        out[f"{dt}.gate_up"] = _bits(x)
+        out[f"{dt}.h"] = _bits(F.silu(gate) * up)
+    np.savez_compressed(os.path.join(HERE, "silu_mul.npz"), **out)
 
 
 if __name__ == "__main__":

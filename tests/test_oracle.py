@@ -306,3 +306,37 @@ def test_fp8w_oracle_matches_numpy_and_one_hot():
     eye = np.eye(k, dtype=np.float32)[:5]
     y = O.fp8w_ref(eye, q, np.ones(n, np.float32))
     np.testing.assert_array_equal(y, lut[q[:, :5]].T)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_silu_mul_oracle_matches_golden(dt):
+    """GatedMLP's activation against torch-CPU's F.silu(gate) * up.  The exp of the two
+    libraries may differ in the last bit of an fp32 result, which the rounding to a
+    16-bit dtype nearly always absorbs: every element within one ulp of the output dtype,
+    and at most one in a thousand not exact."""
+    z = _load("silu_mul")
+    code = {"bf16": O.DT_BF16, "f16": O.DT_F16, "f32": O.DT_F32}[dt]
+    h = O.silu_mul(z[f"{dt}.gate_up"], code)
+    want = z[f"{dt}.h"]
+    if dt == "f32":
+        got, ref = h.astype(np.float64), want.astype(np.float64)
+        assert np.all(np.abs(got - ref) <= 2.0 ** -22 * np.maximum(np.abs(ref), 1e-30))
+        return
+    diff = np.abs(h.astype(np.int32) - want.astype(np.int32))
+    same_sign = (h >> 15) == (want >> 15)
+    assert np.all((diff <= 1) & same_sign | (diff == 0)), dt
+    assert np.count_nonzero(diff) <= h.size // 1000, (dt, np.count_nonzero(diff))
+
+
+def test_silu_mul_oracle_closed_forms():
+    """silu(0) = 0; silu(g) -> g for large g and -> -0 for very negative g; up = 1 gives silu itself;
+    up = 0 gives zeros of the right sign."""
+    k = 8
+    gu = np.zeros((1, 2 * k), np.float32)
+    gu[0, :k] = [0.0, 100.0, -100.0, 1.0, -1.0, 2.0, 30.0, -30.0]
+    gu[0, k:] = 1.0
+    h = O.silu_mul(gu, O.DT_F32)[0]
+    g = gu[0, :k].astype(np.float64)
+    finite = np.arange(k) != 2  # exp(100) overflows fp32: -100 / inf is -0 there, as in torch
+    np.testing.assert_allclose(h[finite], (g / (1.0 + np.exp(-g)))[finite], rtol=3e-7)
+    assert h[0] == 0.0 and h[1] == 100.0 and h[2] == 0.0 and np.signbit(h[2])

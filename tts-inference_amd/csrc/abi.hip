@@ -43,6 +43,12 @@ int64_t qtts_fp8w_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
 int qtts_launch_fp8w(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n,
                      const float* scale, const void* bias, void* y, int64_t ldy, int algo, void* ws, int64_t ws_bytes,
                      hipStream_t st);
+int qtts_launch_silu_mul(const void* gu, int x_dtype, int64_t m, int64_t k, int64_t ld, void* h, int64_t ldh,
+                         hipStream_t st);
+int64_t qtts_w8a16_silu_ws_bytes(int64_t m, int64_t n, int64_t k, int algo, int x_dtype);
+int qtts_launch_w8a16_silu(const void* gu, int x_dtype, int64_t m, int64_t k, int64_t ld, const int8_t* qs, int64_t n,
+                           const void* scale, int sdt, const void* bias, void* y, int64_t ldy, int algo, void* ws,
+                           int64_t ws_bytes, hipStream_t st);
 int qtts_launch_fp8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
                                  int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
                                  hipStream_t st);
@@ -176,6 +182,7 @@ int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo) 
     case QTTS_OP_W8A8_INT8: return qtts_int8_gemm_ws_bytes(m, n, k, algo);
     case QTTS_OP_INT8_LINEAR: return linear_ws(qtts_int8_gemm_ws_bytes(m, n, k, algo), m, k);
     case QTTS_OP_FP8W: return qtts_fp8w_ws_bytes(m, n, k, algo);
+    case QTTS_OP_W8A16_SILU: return qtts_w8a16_silu_ws_bytes(m, n, k, algo, QTTS_BF16);
     default: return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "unknown op %d", op);
   }
 }
@@ -423,6 +430,36 @@ int qtts_int8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, in
                             void* ws, int64_t ws_bytes, void* stream) {
   return int8_linear_impl(x, x_dtype, m, k, ldx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y, ldy, div_mode, algo, ws,
                           ws_bytes, stream);
+}
+
+int qtts_silu_mul(const void* gate_up, int x_dtype, int64_t m, int64_t k, int64_t ld_gate_up, void* h, int64_t ldh,
+                  void* stream) {
+  QTTS_REQUIRE(m >= 0 && k >= 0, "silu_mul: negative size");
+  QTTS_REQUIRE(m < 65536 && k < (1ll << 31), "silu_mul: size too large");
+  QTTS_REQUIRE(dtype_ok(x_dtype), "silu_mul: bad dtype code");
+  QTTS_REQUIRE(ld_gate_up >= 2 * k && ldh >= k, "silu_mul: leading dimension smaller than the row");
+  if (m == 0 || k == 0) return QTTS_OK;
+  QTTS_REQUIRE(gate_up && h, "silu_mul: null pointer");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_silu_mul(gate_up, x_dtype, m, k, ld_gate_up, h, ldh, (hipStream_t)stream);
+}
+
+int qtts_w8a16_silu_mul_gemm_strips(const void* gate_up, int x_dtype, int64_t m, int64_t k, int64_t ld_gate_up,
+                                    const int8_t* qs, int64_t n, const void* scale, int scale_dtype, const void* bias,
+                                    void* y, int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a16_silu_mul_gemm_strips: negative size");
+  QTTS_REQUIRE(m < 65536 && n < (1ll << 31) && k < (1ll << 30), "w8a16_silu_mul_gemm_strips: size too large");
+  QTTS_REQUIRE(x_dtype == QTTS_BF16 || x_dtype == QTTS_F16, "w8a16_silu_mul_gemm_strips: activations must be bf16 or fp16");
+  QTTS_REQUIRE(dtype_ok(scale_dtype), "w8a16_silu_mul_gemm_strips: bad scale dtype code");
+  QTTS_REQUIRE(algo_ok(algo), "w8a16_silu_mul_gemm_strips: bad algo %d", algo);
+  QTTS_REQUIRE(k % 16 == 0, "w8a16_silu_mul_gemm_strips: K %% 16 != 0 (K=%lld)", (long long)k);
+  QTTS_REQUIRE(ld_gate_up >= 2 * k && ldy >= n, "w8a16_silu_mul_gemm_strips: leading dimension smaller than the row");
+  QTTS_REQUIRE(ws_bytes >= 0, "w8a16_silu_mul_gemm_strips: negative workspace size");
+  if (m == 0 || n == 0) return QTTS_OK;
+  QTTS_REQUIRE(gate_up && qs && scale && y, "w8a16_silu_mul_gemm_strips: null pointer");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_w8a16_silu(gate_up, x_dtype, m, k, ld_gate_up, qs, n, scale, scale_dtype, bias, y, ldy, algo, ws,
+                                ws_bytes, (hipStream_t)stream);
 }
 
 int qtts_fp8w_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n,

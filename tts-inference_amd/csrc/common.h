@@ -185,6 +185,27 @@ __device__ __forceinline__ float int8_epilogue(int acc, float sx, float sw, floa
   return has_bias ? v + bias : v;
 }
 
+// GatedMLP's activation, qtts/layers/activation.py:147, `F.silu(gate) * up` on tensors
+// of dtype T: silu in fp32 with torch's formula x / (1 + exp(-x)), rounded to T; the
+// product in fp32, rounded to T.
+template <typename T> __device__ __forceinline__ float silu_mul(float g, float u) {
+  const float s = round_through<T>(g / (1.0f + expf(-g)));
+  return round_through<T>(s * u);
+}
+
+// Eight 16-bit values of type T packed in an i32x4: silu_mul element by element.
+template <typename T> __device__ __forceinline__ i32x4_t silu_mul8(i32x4_t g, i32x4_t u) {
+  i32x4_t r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t gp = (uint32_t)g[i], up = (uint32_t)u[i];
+    const float lo = silu_mul<T>(to_f32(T{(uint16_t)gp}), to_f32(T{(uint16_t)up}));
+    const float hi = silu_mul<T>(to_f32(T{(uint16_t)(gp >> 16)}), to_f32(T{(uint16_t)(up >> 16)}));
+    r[i] = (int)pack2_f32<T>(lo, hi);
+  }
+  return r;
+}
+
 // ---- OCP e4m3fn encode (round to nearest even, non-saturating like torch's cast) ---
 
 __device__ __forceinline__ uint32_t e4m3_encode(float f) {

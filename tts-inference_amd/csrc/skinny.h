@@ -42,7 +42,11 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 // row 0's data, so direct loads fetch (16 / M)x the activation bytes through the
 // vector memory path the weight stream needs; staged, that path carries M rows once.
 // F8W: the weight codes are OCP e4m3 (fp8 weight-only) instead of int8.
-template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1, int MX = 0, bool F8W = false>
+// SILU (staged rows only): x is GatedMLP's fused gate_up output, [M, 2K] with row
+// stride ldx; the kernel multiplies by silu(gate) * up (gate = columns [0, K), up =
+// [K, 2K)), computed while the rows are staged (qtts/layers/activation.py:142-147).
+template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1, int MX = 0, bool F8W = false,
+          bool SILU = false>
 __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ q, int N, int64_t ldq,
     const ST* scale, const XT* bias, XT* __restrict__ y, int64_t ldy,
@@ -51,6 +55,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   typedef typename MM::vec V;
   static_assert(MB == 1 || (FULLK && LAYOUT == kLayoutStrips), "several m-blocks need full-K strip weights");
   static_assert(MX == 0 || (MB == 1 && FULLK && LAYOUT == kLayoutStrips), "staged rows need one m-block, full K");
+  static_assert(!SILU || MX > 0, "the activation prologue runs on staged rows");
   __shared__ f32x4_t red[W > 1 ? W - 1 : 1][MB][64];
   __shared__ __align__(16) uint16_t xrow[MX > 0 ? W : 1][MX > 0 ? MX : 1][MX > 0 ? CPW * 64 : 8];
 
@@ -154,15 +159,18 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   // 512 v + 8 l .. + 7 of the wave's K range of each row (XV vectors cover CPW
   // chunks); lanes past the range repeat its last 8 elements.
   constexpr int XV = (CPW * 64 + 511) / 512;
-  i32x4_t xr[MX > 0 ? MX : 1][XV];
+  i32x4_t xr[MX > 0 ? MX : 1][XV], xu[SILU ? MX : 1][SILU ? XV : 1];
   auto issue_x = [&]() {
     if constexpr (MX > 0) {
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
         const int e = min(512 * v + 8 * lane, (wc1 - wc0) * 64 - 8);
 #pragma unroll
-        for (int m = 0; m < MX; ++m)
-          xr[m][v] = *(const i32x4_t*)(x + (int64_t)min(m, M - 1) * ldx + (int64_t)wc0 * 64 + e);
+        for (int m = 0; m < MX; ++m) {
+          const XT* row = x + (int64_t)min(m, M - 1) * ldx + (int64_t)wc0 * 64 + e;
+          xr[m][v] = *(const i32x4_t*)row;
+          if constexpr (SILU) xu[m][v] = *(const i32x4_t*)(row + K);
+        }
       }
     }
   };
@@ -172,7 +180,10 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       for (int v = 0; v < XV; ++v) {
         const int e = min(512 * v + 8 * lane, (wc1 - wc0) * 64 - 8);
 #pragma unroll
-        for (int m = 0; m < MX; ++m) *(i32x4_t*)&xrow[wave][m][e] = xr[m][v];
+        for (int m = 0; m < MX; ++m) {
+          if constexpr (SILU) *(i32x4_t*)&xrow[wave][m][e] = silu_mul8<XT>(xr[m][v], xu[m][v]);
+          else *(i32x4_t*)&xrow[wave][m][e] = xr[m][v];
+        }
       }
       // B operand of lane (r, g): row r (rows >= M read row 0; their D columns are
       // never stored), elements 64 u + 16 g .. + 15 of chunk u of the range.

@@ -14,7 +14,7 @@ import torch
 
 from . import _lib
 from ._lib import (ALGO_AUTO, DIV_DEVICE, DIV_IEEE, OP_FP8_LINEAR, OP_FP8W, OP_INT8_LINEAR,  # noqa: F401
-                   OP_W8A16, OP_W8A8_FP8, OP_W8A8_INT8, STRIP_FP8, STRIP_INT8, algo_code)
+                   OP_W8A16, OP_W8A16_SILU, OP_W8A8_FP8, OP_W8A8_INT8, STRIP_FP8, STRIP_INT8, algo_code)
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
@@ -552,6 +552,58 @@ def fp8w_gemm_strips(x: torch.Tensor, qs: torch.Tensor, n: int, scale: torch.Ten
         _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else k, _ptr(qs), n, _ptr(scale), _ptr(bias),
         _ptr(out), n, algo, ws, ws_n, _stream(dev))
     _lib.check(st, "fp8w_gemm_strips")
+    return out.reshape(*shape[:-1], n)
+
+
+# ---- GatedMLP (qtts/layers/activation.py:142-147) ------------------------------------
+
+def _gate_up_rows(gate_up: torch.Tensor) -> torch.Tensor:
+    a = _flatten(gate_up)
+    if a.shape[1] % 2:
+        raise ValueError(f"gate_up has an odd last dimension {a.shape[1]}; expected [..., 2 * intermediate]")
+    return a
+
+
+def silu_mul(gate_up: torch.Tensor) -> torch.Tensor:
+    """``F.silu(gate) * up`` of a fused ``[..., 2I]`` gate_up output in one kernel, with torch's
+    rounding for the two-kernel expression.  Returns ``[..., I]`` in gate_up's dtype."""
+    shape = gate_up.shape
+    a = _gate_up_rows(gate_up)
+    rows, k = a.shape[0], a.shape[1] // 2
+    dev = _require_cuda(a)
+    out = torch.empty((rows, k), dtype=a.dtype, device=dev)
+    st = _lib.load().qtts_silu_mul(_ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else 2 * k,
+                                   _ptr(out), k, _stream(dev))
+    _lib.check(st, "silu_mul")
+    return out.reshape(*shape[:-1], k)
+
+
+def w8a16_silu_mul_gemm_strips(gate_up: torch.Tensor, qs: torch.Tensor, n: int, scale: torch.Tensor,
+                               bias: torch.Tensor | None = None, algo: int = ALGO_AUTO) -> torch.Tensor:
+    """``down(F.silu(gate) * up)`` for an int8 strip-layout down projection, one call: a single
+    decode row has the activation computed inside the GEMM kernel."""
+    shape = gate_up.shape
+    a = _gate_up_rows(gate_up)
+    rows, k = a.shape[0], a.shape[1] // 2
+    if qs.dtype != torch.int8 or qs.numel() != strip_bytes(n, k, STRIP_INT8):
+        raise ValueError(f"weight is not an int8 strip-layout [{n}, {k}] buffer")
+    if scale.numel() != n:
+        raise ValueError(f"scale has {scale.numel()} entries for {n} output channels")
+    if bias is not None:
+        if bias.numel() != n:
+            raise ValueError(f"bias has {bias.numel()} entries for {n} output channels")
+        bias = bias.to(a.dtype).contiguous()
+    if a.data_ptr() % 16 or (rows > 1 and a.stride(0) % 8):
+        a = a.contiguous() if a.data_ptr() % 16 == 0 else a.clone()
+    dev = _require_cuda(a, qs, scale, bias)
+    scale = scale.contiguous()
+    out = torch.empty((rows, n), dtype=a.dtype, device=dev)
+    reserve_workspace(dev, workspace_bytes(OP_W8A16_SILU, rows, n, k, algo))
+    ws, ws_n = _ws_for(dev)
+    st = _lib.load().qtts_w8a16_silu_mul_gemm_strips(
+        _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else 2 * k, _ptr(qs), n, _ptr(scale),
+        dtype_code(scale.dtype), _ptr(bias), _ptr(out), n, algo, ws, ws_n, _stream(dev))
+    _lib.check(st, "w8a16_silu_mul_gemm_strips")
     return out.reshape(*shape[:-1], n)
 
 

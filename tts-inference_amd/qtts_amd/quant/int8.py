@@ -161,6 +161,18 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             return ops.w8a16_gemm(x, int8_weight_rowmajor(layer), layer.int8_scale, bias)
         return ops.w8a16_gemm(x, layer.int8_weight, layer.int8_scale, bias, algo)
 
+    def apply_silu_mul(self, layer, gate_up: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        """``layer(F.silu(gate) * up)`` from GatedMLP's fused gate_up output (qtts/layers/activation.py:
+        142-147): on strip weights one call, with the activation inside the GEMM for a single row."""
+        n, k = layer.out_features, layer.in_features
+        if gate_up.shape[-1] != 2 * k:
+            raise ValueError(f"gate_up has {gate_up.shape[-1]} columns for a down projection with K={k}")
+        if layer.int8_layout == "strips" and gate_up.dtype in (torch.bfloat16, torch.float16):
+            rows = gate_up.numel() // (2 * k) if k else 0
+            algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
+            return ops.w8a16_silu_mul_gemm_strips(gate_up, layer.int8_weight, n, layer.int8_scale, bias, algo)
+        return self.apply(layer, ops.silu_mul(gate_up), bias)
+
 
 class Int8Method(QuantMethodBase):
     """W8A8: per-token activation scales, per-channel weight scales, int8 GEMM (qtts/quant/int8.py:129-160).
