@@ -54,8 +54,12 @@ typedef enum {
     QTTS_OP_W8A8_INT8 = 3,
     QTTS_OP_INT8_LINEAR = 4,
     QTTS_OP_FP8W = 5,
-    QTTS_OP_W8A16_SILU = 6
+    QTTS_OP_W8A16_SILU = 6,
+    QTTS_OP_W8A16_FUSED = 7
 } qtts_op;
+
+/* What qtts_w8a16_fused_gemm_strips applies to its activations before the GEMM. */
+typedef enum { QTTS_PRO_NONE = 0, QTTS_PRO_SILU_MUL = 1, QTTS_PRO_RMS_NORM = 2 } qtts_prologue;
 
 /* --- housekeeping ------------------------------------------------------------ */
 
@@ -174,6 +178,40 @@ int qtts_w8a16_silu_mul_gemm_strips(const void* gate_up, int x_dtype, int64_t m,
                                     const void* scale, int scale_dtype, const void* bias,
                                     void* y, int64_t ldy, int algo, void* ws, int64_t ws_bytes,
                                     void* stream);
+
+/* --- the decoder layer around the W8A16 GEMM -------------------------------------- */
+
+/* RMSNorm._fused_forward (qtts/layers/norm.py:50-76, 103-118), one row per call row:
+ *   inv = 1 / sqrt(sum_c f32(x[r,c])^2 / k + eps)   (fp32, correctly rounded)
+ *   y[r, c] = dtype((f32(x[r,c]) * inv) * f32(weight[c]))
+ * x, y: [m, k] of x_dtype (row strides ldx, ldy); weight: [k] of x_dtype. */
+int qtts_rms_norm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const void* weight,
+                  float eps, void* y, int64_t ldy, void* stream);
+
+/* One W8A16 linear of the talker's decoder layer (qtts/models/talker.py:246-271) with
+ * its neighbours, on strip weights (k % 64 == 0, bf16 / fp16 activations):
+ *   y = [residual +] linear(prologue(x))
+ *   prologue QTTS_PRO_NONE:     x [m, k];
+ *            QTTS_PRO_SILU_MUL: x is the gate_up output [m, 2k], h = silu(gate) * up
+ *                               as qtts_silu_mul (GatedMLP.forward, activation.py:142-147);
+ *            QTTS_PRO_RMS_NORM: x [m, k], h = qtts_rms_norm(x, norm_weight, eps)
+ *                               (input_layernorm before qkv_proj, post_attention_layernorm
+ *                               before gate_up_proj);
+ *   residual: [m, n] of x_dtype, row stride ldr, or NULL; y = dtype(f32(residual) +
+ *   f32(linear)), the linear rounded to x_dtype first, as `residual + o_proj(...)`
+ *   (talker.py:270-271).  residual may be y itself (an in-place hidden-state update).
+ * Fused into the GEMM launch (prologue computed while the activation row is staged,
+ * residual added in the epilogue): SiLU and RMSNorm for m == 1 (RMSNorm without a
+ * residual and without split-K), the residual for m <= 8.  Otherwise the separate
+ * kernels run around qtts_w8a16_gemm_strips, through the workspace.  SiLU and the
+ * residual give the same bits either way; a fused RMSNorm sums its squares in another
+ * order than qtts_rms_norm.  scale_dtype: x_dtype or fp32 for the fused launches (any
+ * for the separate ones).  Workspace: qtts_workspace_bytes(QTTS_OP_W8A16_FUSED). */
+int qtts_w8a16_fused_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                                 int prologue, const void* norm_weight, float eps,
+                                 const int8_t* qs, int64_t n, const void* scale, int scale_dtype,
+                                 const void* bias, const void* residual, int64_t ldr, void* y,
+                                 int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream);
 
 /* --- fp8 W8A8 --------------------------------------------------------------------- */
 

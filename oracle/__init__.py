@@ -60,6 +60,8 @@ def lib() -> ctypes.CDLL:
         L.oracle_fp8w_ref_f64.argtypes = [p, i64, i64, p, i64, p, p, p]
         L.oracle_silu_mul.restype = None
         L.oracle_silu_mul.argtypes = [p, i32, i64, i64, i64, p]
+        L.oracle_rms_norm_f64.restype = None
+        L.oracle_rms_norm_f64.argtypes = [p, i32, i64, i64, i64, p, ctypes.c_double, p]
         L.oracle_quant_act_int8.restype = None
         L.oracle_quant_act_int8.argtypes = [p, i32, i64, i64, i64, p, p, i32]
         L.oracle_int8_linear_out.restype = None
@@ -195,6 +197,17 @@ def silu_mul(gate_up: np.ndarray, dtype: int = DT_BF16) -> np.ndarray:
     h = np.empty((m, k), np.float32 if dtype == DT_F32 else np.uint16)
     lib().oracle_silu_mul(_ptr(gu), dtype, m, k, k2, _ptr(h))
     return h
+
+
+def rms_norm(x: np.ndarray, w: np.ndarray, eps: float, dtype: int = DT_BF16) -> np.ndarray:
+    """RMSNorm in fp64 (qtts/layers/norm.py:50-76): x * inv_rms * w, unrounded.  x and w in
+    dtype's encoding (uint16 bits for bf16 / fp16)."""
+    xs = _src(x, dtype)
+    ws = np.ascontiguousarray(_src(np.atleast_2d(w), dtype)[0])
+    m, k = xs.shape
+    y = np.empty((m, k), np.float64)
+    lib().oracle_rms_norm_f64(_ptr(xs), dtype, m, k, k, _ptr(ws), float(eps), _ptr(y))
+    return y
 
 
 def quant_act_int8(x: np.ndarray, x_dtype: int = DT_BF16, div_mode: int = DIV_DEVICE):

@@ -307,6 +307,25 @@ void oracle_fp8w_ref_f64(const float* x, int64_t m, int64_t k, const uint8_t* q,
  * of the activation dtype): silu in fp32 with torch's formula g / (1 + exp(-g)) rounded
  * to the dtype, then the product in fp32 rounded to the dtype.  gate_up: [m, 2k] (gate
  * then up), row stride ld; h: [m, k].  Values travel as bf16 / fp16 bits or fp32. */
+/* RMSNorm (qtts/layers/norm.py:50-76): y = x * (1 / sqrt(mean(x^2) + eps)) * w, the sum of
+ * squares and every product in fp64 (the reference reduces in fp32 in an order of its
+ * block's choosing, so its result is this value rounded to the dtype, give or take
+ * one unit in the last place).  x: [m, k] of dtype, row stride ld; w: [k] of dtype;
+ * y: [m, k] fp64. */
+void oracle_rms_norm_f64(const void* x, int dtype, int64_t m, int64_t k, int64_t ld, const void* w, double eps,
+                         double* y) {
+    for (int64_t r = 0; r < m; ++r) {
+        double ss = 0.0;
+        for (int64_t c = 0; c < k; ++c) {
+            const double v = load_elem(x, dtype, r * ld + c);
+            ss += v * v;
+        }
+        const double inv = 1.0 / sqrt(ss / (double)k + eps);
+        for (int64_t c = 0; c < k; ++c)
+            y[r * k + c] = (double)load_elem(x, dtype, r * ld + c) * inv * (double)load_elem(w, dtype, c);
+    }
+}
+
 void oracle_silu_mul(const void* gate_up, int dtype, int64_t m, int64_t k, int64_t ld, void* h) {
     for (int64_t r = 0; r < m; ++r)
         for (int64_t c = 0; c < k; ++c) {

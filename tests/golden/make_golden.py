@@ -193,7 +193,8 @@ def main() -> None:
     np.savez_compressed(os.path.join(HERE, "gemm_small.npz"), **gemm)
     int8_w8a8_fixtures()
     silu_mul_fixtures()
-    for f in ("int8_pack", "fp8_pack", "act_fp8", "gemm_small", "int8_w8a8", "silu_mul"):
+    rms_norm_fixtures()
+    for f in ("int8_pack", "fp8_pack", "act_fp8", "gemm_small", "int8_w8a8", "silu_mul", "rms_norm"):
         print(f, os.path.getsize(os.path.join(HERE, f + ".npz")), "bytes")
 
 
@@ -274,6 +275,34 @@ def silu_mul_fixtures() -> None:
         out[f"{dt}.gate_up"] = _bits(x)
         out[f"{dt}.h"] = _bits(F.silu(gate) * up)
     np.savez_compressed(os.path.join(HERE, "silu_mul.npz"), **out)
+
+
+def rms_norm_fixtures() -> None:
+    """RMSNorm's eager form (qtts/layers/norm.py:120-133, transformers' Qwen3RMSNorm order)
+    on torch-CPU, each dtype, for the talker (2048), predictor (1024) and codec (512)
+    widths: N(0, 1) rows, a row of 20-sigma outliers, a constant row, a row near zero
+    (eps dominates) and a one-hot row."""
+    rng = np.random.default_rng(20240901)
+    out: dict[str, np.ndarray] = {}
+    eps = 1e-6
+    for width in (2048, 1024, 512):
+        x = rng.normal(0, 1, (6, width)).astype(np.float32)
+        x[1, rng.choice(width, 8, replace=False)] *= 20.0
+        x[2, :] = 0.75
+        x[3, :] *= 1e-4
+        x[4, :] = 0.0
+        x[4, 7] = -3.0
+        w = rng.normal(1.0, 0.2, width).astype(np.float32)
+        for dt, tdt in _TORCH_DT.items():
+            xt, wt = torch.from_numpy(x).to(tdt), torch.from_numpy(w).to(tdt)
+            x32 = xt.to(torch.float32)
+            var = x32.pow(2).mean(-1, keepdim=True)
+            y = (wt.to(torch.float32) * (x32 * torch.rsqrt(var + eps))).to(tdt)
+            out[f"{dt}.{width}.x"] = _bits(xt)
+            out[f"{dt}.{width}.w"] = _bits(wt)
+            out[f"{dt}.{width}.y"] = _bits(y)
+    out["eps"] = np.array(eps, np.float64)
+    np.savez_compressed(os.path.join(HERE, "rms_norm.npz"), **out)
 
 
 if __name__ == "__main__":

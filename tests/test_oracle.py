@@ -340,3 +340,62 @@ def test_silu_mul_oracle_closed_forms():
     finite = np.arange(k) != 2  # exp(100) overflows fp32: -100 / inf is -0 there, as in torch
     np.testing.assert_allclose(h[finite], (g / (1.0 + np.exp(-g)))[finite], rtol=3e-7)
     assert h[0] == 0.0 and h[1] == 100.0 and h[2] == 0.0 and np.signbit(h[2])
+
+
+# ---- RMSNorm (qtts/layers/norm.py:50-76) ----------------------------------------------
+
+def _ulp16(v: np.ndarray, dt: str) -> np.ndarray:
+    """One unit in the last place of bf16 / fp16 at |v| (normal range)."""
+    a = np.maximum(np.abs(v), 1e-30)
+    if dt == "bf16":
+        return 2.0 ** (np.floor(np.log2(a)) - 7)
+    return 2.0 ** (np.maximum(np.floor(np.log2(a)), -14) - 10)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+def test_rms_norm_oracle_matches_golden(dt):
+    """The fp64 oracle against torch-CPU's eager RMSNorm (the reference's eager path, the one
+    its parity suite runs): every torch output within one unit in the last place of the
+    oracle's value, and at most one in a hundred not the oracle's value rounded."""
+    z = _load("rms_norm")
+    code = {"bf16": O.DT_BF16, "f16": O.DT_F16, "f32": O.DT_F32}[dt]
+    eps = float(z["eps"])
+    for width in (2048, 1024, 512):
+        x, w, want = z[f"{dt}.{width}.x"], z[f"{dt}.{width}.w"], z[f"{dt}.{width}.y"]
+        ref = O.rms_norm(x, w, eps, code)
+        if dt == "f32":
+            np.testing.assert_allclose(want, ref, rtol=1e-6, atol=1e-30)
+            continue
+        got = (O.bf16_bits_to_f32(want) if dt == "bf16" else want.view(np.float16).astype(np.float32)).astype(np.float64)
+        assert np.all(np.abs(got - ref) <= _ulp16(ref, dt)), (dt, width)
+        rounded = O.f32_to_bf16_bits(ref.astype(np.float32)) if dt == "bf16" else ref.astype(np.float16).view(np.uint16)
+        assert np.count_nonzero(rounded != want) <= want.size // 100, (dt, width, np.count_nonzero(rounded != want))
+
+
+def test_rms_norm_oracle_closed_forms():
+    """A constant row c gives c w / sqrt(c^2 + eps); a one-hot row a e_j gives
+    a w_j / sqrt(a^2 / k + eps) at j and zeros elsewhere; with eps = 0 the result does not
+    change when the row is scaled by a power of two; strides and the weight index follow
+    the textbook formula on a random matrix."""
+    k = 64
+    w = np.linspace(0.5, 1.5, k, dtype=np.float32)
+    w64 = w.astype(np.float64)
+    x = np.zeros((3, k), np.float32)
+    x[0, :] = 0.75
+    x[1, 9] = -3.0
+    x[2, :] = np.sin(np.arange(k)).astype(np.float32)
+    eps = 1e-6
+    y = O.rms_norm(x, w, eps, O.DT_F32)
+    np.testing.assert_allclose(y[0], 0.75 * w64 / np.sqrt(0.5625 + eps), rtol=1e-14)
+    want1 = np.zeros(k)
+    want1[9] = -3.0 * w64[9] / np.sqrt(9.0 / k + eps)
+    np.testing.assert_allclose(y[1], want1, rtol=1e-14, atol=0)
+    y0 = O.rms_norm(x, w, 0.0, O.DT_F32)
+    y8 = O.rms_norm(x * 8.0, w, 0.0, O.DT_F32)
+    np.testing.assert_allclose(y8, y0, rtol=1e-14)
+    rng = np.random.default_rng(3)
+    xr = rng.normal(0, 2, (5, 96)).astype(np.float32)
+    wr = rng.normal(1, 0.3, 96).astype(np.float32)
+    x64 = xr.astype(np.float64)
+    textbook = x64 / np.sqrt(np.mean(x64 * x64, axis=1, keepdims=True) + 1e-5) * wr.astype(np.float64)
+    np.testing.assert_allclose(O.rms_norm(xr, wr, 1e-5, O.DT_F32), textbook, rtol=1e-13)

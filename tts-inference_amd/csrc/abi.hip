@@ -49,6 +49,13 @@ int64_t qtts_w8a16_silu_ws_bytes(int64_t m, int64_t n, int64_t k, int algo, int 
 int qtts_launch_w8a16_silu(const void* gu, int x_dtype, int64_t m, int64_t k, int64_t ld, const int8_t* qs, int64_t n,
                            const void* scale, int sdt, const void* bias, void* y, int64_t ldy, int algo, void* ws,
                            int64_t ws_bytes, hipStream_t st);
+int qtts_launch_rms_norm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const void* w, float eps,
+                         void* y, int64_t ldy, hipStream_t st);
+int64_t qtts_w8a16_fused_ws_bytes(int64_t m, int64_t n, int64_t k, int algo, int x_dtype);
+int qtts_launch_w8a16_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int pro, const void* nw,
+                            float eps, const int8_t* qs, int64_t n, const void* scale, int sdt, const void* bias,
+                            const void* res, int64_t ldr, void* y, int64_t ldy, int algo, void* ws, int64_t ws_bytes,
+                            hipStream_t st);
 int qtts_launch_fp8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
                                  int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
                                  hipStream_t st);
@@ -122,6 +129,15 @@ bool algo_ok(int a) {
 }
 int64_t al256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
+// Whether the byte spans of two [rows, cols] matrices (row strides lda, ldb, elements
+// of esz bytes) intersect.
+bool ranges_overlap(const void* a, int64_t rows_a, int64_t lda, const void* b, int64_t rows_b, int64_t ldb,
+                    int64_t cols, int64_t esz) {
+  const uintptr_t a0 = (uintptr_t)a, a1 = a0 + (uintptr_t)(((rows_a - 1) * lda + cols) * esz);
+  const uintptr_t b0 = (uintptr_t)b, b1 = b0 + (uintptr_t)(((rows_b - 1) * ldb + cols) * esz);
+  return a0 < b1 && b0 < a1;
+}
+
 // Workspace of the one-call linears: the GEMM's own part (its split-K counter block
 // always reserved, so the quantized activations never land on counters that later
 // calls expect at zero), then the activation codes and their scales.
@@ -183,6 +199,7 @@ int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo) 
     case QTTS_OP_INT8_LINEAR: return linear_ws(qtts_int8_gemm_ws_bytes(m, n, k, algo), m, k);
     case QTTS_OP_FP8W: return qtts_fp8w_ws_bytes(m, n, k, algo);
     case QTTS_OP_W8A16_SILU: return qtts_w8a16_silu_ws_bytes(m, n, k, algo, QTTS_BF16);
+    case QTTS_OP_W8A16_FUSED: return qtts_w8a16_fused_ws_bytes(m, n, k, algo, QTTS_BF16);
     default: return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "unknown op %d", op);
   }
 }
@@ -460,6 +477,46 @@ int qtts_w8a16_silu_mul_gemm_strips(const void* gate_up, int x_dtype, int64_t m,
   QTTS_TRY(current_device_check());
   return qtts_launch_w8a16_silu(gate_up, x_dtype, m, k, ld_gate_up, qs, n, scale, scale_dtype, bias, y, ldy, algo, ws,
                                 ws_bytes, (hipStream_t)stream);
+}
+
+int qtts_rms_norm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const void* weight, float eps, void* y,
+                  int64_t ldy, void* stream) {
+  QTTS_REQUIRE(m >= 0 && k >= 0, "rms_norm: negative size");
+  QTTS_REQUIRE(m < (1ll << 31) && k < (1ll << 31), "rms_norm: size too large");
+  QTTS_REQUIRE(dtype_ok(x_dtype), "rms_norm: bad dtype code");
+  QTTS_REQUIRE(ldx >= k && ldy >= k, "rms_norm: leading dimension smaller than the row");
+  if (m == 0 || k == 0) return QTTS_OK;
+  QTTS_REQUIRE(x && weight && y, "rms_norm: null pointer");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_rms_norm(x, x_dtype, m, k, ldx, weight, eps, y, ldy, (hipStream_t)stream);
+}
+
+int qtts_w8a16_fused_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int prologue,
+                                 const void* norm_weight, float eps, const int8_t* qs, int64_t n, const void* scale,
+                                 int scale_dtype, const void* bias, const void* residual, int64_t ldr, void* y,
+                                 int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a16_fused_gemm_strips: negative size");
+  QTTS_REQUIRE(m < 65536 && n < (1ll << 31) && k < (1ll << 30), "w8a16_fused_gemm_strips: size too large");
+  QTTS_REQUIRE(x_dtype == QTTS_BF16 || x_dtype == QTTS_F16, "w8a16_fused_gemm_strips: activations must be bf16 or fp16");
+  QTTS_REQUIRE(dtype_ok(scale_dtype), "w8a16_fused_gemm_strips: bad scale dtype code");
+  QTTS_REQUIRE(algo_ok(algo), "w8a16_fused_gemm_strips: bad algo %d", algo);
+  QTTS_REQUIRE(prologue == QTTS_PRO_NONE || prologue == QTTS_PRO_SILU_MUL || prologue == QTTS_PRO_RMS_NORM,
+               "w8a16_fused_gemm_strips: bad prologue %d", prologue);
+  QTTS_REQUIRE(k % 64 == 0, "w8a16_fused_gemm_strips: K %% 64 != 0 (K=%lld)", (long long)k);
+  QTTS_REQUIRE(ldx >= (prologue == QTTS_PRO_SILU_MUL ? 2 * k : k) && ldy >= n && (!residual || ldr >= n),
+               "w8a16_fused_gemm_strips: leading dimension smaller than the row");
+  QTTS_REQUIRE(ws_bytes >= 0, "w8a16_fused_gemm_strips: negative workspace size");
+  if (m == 0 || n == 0) return QTTS_OK;
+  QTTS_REQUIRE(x && qs && scale && y && (prologue != QTTS_PRO_RMS_NORM || norm_weight),
+               "w8a16_fused_gemm_strips: null pointer");
+  QTTS_REQUIRE(prologue != QTTS_PRO_NONE || ((uintptr_t)x % 16 == 0 && (m == 1 || ldx % 8 == 0)),
+               "w8a16_fused_gemm_strips: activation rows must be 16-byte aligned");
+  QTTS_REQUIRE(!residual || residual == y || !ranges_overlap(residual, m, ldr, y, m, ldy, n, 2),
+               "w8a16_fused_gemm_strips: residual overlaps y without being y");
+  QTTS_REQUIRE(!residual || residual != y || ldr == ldy, "w8a16_fused_gemm_strips: residual is y with another stride");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_w8a16_fused(x, x_dtype, m, k, ldx, prologue, norm_weight, eps, qs, n, scale, scale_dtype, bias,
+                                 residual, ldr, y, ldy, algo, ws, ws_bytes, (hipStream_t)stream);
 }
 
 int qtts_fp8w_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n,

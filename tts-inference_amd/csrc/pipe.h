@@ -22,6 +22,14 @@ template <int N> __device__ __forceinline__ void wait_vmcnt() {
   __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
+// s_waitcnt lgkmcnt(0), vmcnt and expcnt left at their maxima: this wave's LDS
+// accesses are complete (before a barrier that publishes them to other waves).
+__device__ __forceinline__ void wait_lgkmcnt0() {
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  __builtin_amdgcn_s_waitcnt(15 | (3 << 14) | (7 << 4));
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+}
+
 // Workgroup barrier without a memory fence: stage visibility is established by each
 // wave's own vmcnt wait before it; the signal fences keep the compiler from moving
 // LDS accesses across it.

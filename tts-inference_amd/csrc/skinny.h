@@ -8,6 +8,7 @@
 
 #include "common.h"
 #include "layout.h"
+#include "pipe.h"
 #include "splitk.h"
 
 namespace qtts {
@@ -42,21 +43,36 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 // row 0's data, so direct loads fetch (16 / M)x the activation bytes through the
 // vector memory path the weight stream needs; staged, that path carries M rows once.
 // F8W: the weight codes are OCP e4m3 (fp8 weight-only) instead of int8.
-// SILU (staged rows only): x is GatedMLP's fused gate_up output, [M, 2K] with row
-// stride ldx; the kernel multiplies by silu(gate) * up (gate = columns [0, K), up =
-// [K, 2K)), computed while the rows are staged (qtts/layers/activation.py:142-147).
+// PRO (staged rows only), a prologue computed while the rows are staged:
+//   kProSiluMul: x is GatedMLP's fused gate_up output, [M, 2K] with row stride ldx, and
+//     the GEMM multiplies silu(gate) * up (gate = columns [0, K), up = [K, 2K);
+//     qtts/layers/activation.py:142-147);
+//   kProRmsNorm (one row, no split: S == 1): the GEMM multiplies RMSNorm(x) with
+//     weight aux and epsilon eps (qtts/layers/norm.py:50-76).  Each wave sums x^2 over
+//     its own K range, the workgroup adds the W partials in wave order behind one
+//     fence-free barrier (the weights stay in flight), and each wave normalizes its
+//     range as it stages it.
+// RES (staged rows only): y = residual + the linear's output, the output rounded to
+// XT first, as `residual + linear(x)` computes it (qtts/models/talker.py:270-271).
+enum : int { kProNone = 0, kProSiluMul = 1, kProRmsNorm = 2 };
+
 template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1, int MX = 0, bool F8W = false,
-          bool SILU = false>
+          int PRO = kProNone, bool RES = false>
 __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ q, int N, int64_t ldq,
-    const ST* scale, const XT* bias, XT* __restrict__ y, int64_t ldy,
-    float* __restrict__ part, unsigned* __restrict__ counters, int strips, int S, int cps) {
+    const ST* scale, const XT* bias, XT* y, int64_t ldy,
+    float* __restrict__ part, unsigned* __restrict__ counters, int strips, int S, int cps,
+    const XT* __restrict__ aux, float eps, const XT* res, int64_t ldr) {
   typedef mfma16<XT> MM;
   typedef typename MM::vec V;
   static_assert(MB == 1 || (FULLK && LAYOUT == kLayoutStrips), "several m-blocks need full-K strip weights");
   static_assert(MX == 0 || (MB == 1 && FULLK && LAYOUT == kLayoutStrips), "staged rows need one m-block, full K");
-  static_assert(!SILU || MX > 0, "the activation prologue runs on staged rows");
+  static_assert(PRO == kProNone || MX > 0, "a prologue runs on staged rows");
+  static_assert(PRO != kProRmsNorm || MX == 1, "the norm prologue takes one row");
+  static_assert(!RES || MX > 0, "the residual epilogue is built with staged rows");
+  constexpr bool SILU = PRO == kProSiluMul, NORM = PRO == kProRmsNorm;
   __shared__ f32x4_t red[W > 1 ? W - 1 : 1][MB][64];
+  __shared__ float nss[NORM ? W : 1];
   __shared__ __align__(16) uint16_t xrow[MX > 0 ? W : 1][MX > 0 ? MX : 1][MX > 0 ? CPW * 64 : 8];
 
   int strip, split;
@@ -144,7 +160,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   };
   // Epilogue operands: raw bits, loaded unconditionally (clamped index; y stands in
   // for a missing bias), so nothing needs their values before the epilogue.
-  uint32_t sc[4] = {0u, 0u, 0u, 0u}, bi[4] = {0u, 0u, 0u, 0u};
+  uint32_t sc[4] = {0u, 0u, 0u, 0u}, bi[4] = {0u, 0u, 0u, 0u}, rb[RES ? 4 : 1] = {0u};
   auto issue_epilogue = [&]() {
     const XT* bsrc = bias ? bias : y;
 #pragma unroll
@@ -152,6 +168,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       const int nn = min(strip * 16 + 4 * g + i, N - 1);
       sc[i] = load_bits(scale + nn);
       bi[i] = load_bits(bsrc + nn);
+      if constexpr (RES) rb[i] = load_bits(res + (int64_t)min(r, M - 1) * ldr + nn);
     }
   };
 
@@ -159,7 +176,8 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   // 512 v + 8 l .. + 7 of the wave's K range of each row (XV vectors cover CPW
   // chunks); lanes past the range repeat its last 8 elements.
   constexpr int XV = (CPW * 64 + 511) / 512;
-  i32x4_t xr[MX > 0 ? MX : 1][XV], xu[SILU ? MX : 1][SILU ? XV : 1];
+  // SILU: xu holds the up half; NORM: xu holds the norm weight over the same range.
+  i32x4_t xr[MX > 0 ? MX : 1][XV], xu[SILU || NORM ? MX : 1][SILU || NORM ? XV : 1];
   auto issue_x = [&]() {
     if constexpr (MX > 0) {
 #pragma unroll
@@ -170,12 +188,47 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
           const XT* row = x + (int64_t)min(m, M - 1) * ldx + (int64_t)wc0 * 64 + e;
           xr[m][v] = *(const i32x4_t*)row;
           if constexpr (SILU) xu[m][v] = *(const i32x4_t*)(row + K);
+          if constexpr (NORM) xu[m][v] = *(const i32x4_t*)(aux + (int64_t)wc0 * 64 + e);
         }
       }
     }
   };
-  auto stage_x = [&]() {
-    if constexpr (MX > 0) {
+  // NORM, before the barrier: this wave's sum of x^2 over its range (fp32, lane
+  // partials over its vectors in element order, then the wave's butterfly).
+  auto norm_partial = [&]() {
+    float ss = 0.0f;
+#pragma unroll
+    for (int v = 0; v < XV; ++v) {
+      if (512 * v + 8 * lane < (wc1 - wc0) * 64) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t p = (uint32_t)xr[0][v][e];
+          const float a = to_f32(XT{(uint16_t)p}), b = to_f32(XT{(uint16_t)(p >> 16)});
+          ss = __builtin_fmaf(a, a, ss);
+          ss = __builtin_fmaf(b, b, ss);
+        }
+      }
+    }
+    return wave_sum(ss);
+  };
+  // Writes the wave's staged rows to LDS (NORM: x * inv * weight, rounded to XT as
+  // the reference's fused norm stores it) and reads the MFMA B operands back.
+  auto stage_x = [&](float inv) {
+    if constexpr (NORM) {
+#pragma unroll
+      for (int v = 0; v < XV; ++v) {
+        const int e = min(512 * v + 8 * lane, (wc1 - wc0) * 64 - 8);
+        i32x4_t o;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t p = (uint32_t)xr[0][v][i], w2 = (uint32_t)xu[0][v][i];
+          const float h0 = (to_f32(XT{(uint16_t)p}) * inv) * to_f32(XT{(uint16_t)w2});
+          const float h1 = (to_f32(XT{(uint16_t)(p >> 16)}) * inv) * to_f32(XT{(uint16_t)(w2 >> 16)});
+          o[i] = (int)pack2_f32<XT>(h0, h1);
+        }
+        *(i32x4_t*)&xrow[wave][0][e] = o;
+      }
+    } else if constexpr (MX > 0) {
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
         const int e = min(512 * v + 8 * lane, (wc1 - wc0) * 64 - 8);
@@ -185,6 +238,8 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
           else *(i32x4_t*)&xrow[wave][m][e] = xr[m][v];
         }
       }
+    }
+    if constexpr (MX > 0) {
       // B operand of lane (r, g): row r (rows >= M read row 0; their D columns are
       // never stored), elements 64 u + 16 g .. + 15 of chunk u of the range.
       const int rr = r < M ? r : 0;
@@ -210,10 +265,31 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     // Keep the scheduler from interleaving loads with the MFMAs: every load must
     // be in flight before the first wait.
     __builtin_amdgcn_sched_barrier(0);
-    stage_x();  // waits for the activation rows only; the weights stay in flight
-    consume(wc0);
+    if constexpr (NORM) {
+      const float ss = norm_partial();  // waits for the activation row only
+      if (lane == 0) nss[wave] = ss;
+    } else {
+      stage_x(0.0f);  // waits for the activation rows only; the weights stay in flight
+      consume(wc0);
+    }
   } else {
     issue_epilogue();
+    if constexpr (NORM) {
+      if (lane == 0) nss[wave] = 0.0f;
+    }
+  }
+  if constexpr (NORM) {
+    // variance = sum / K; inv = 1 / sqrt(variance + eps), both correctly rounded.
+    wait_lgkmcnt0();
+    barrier_only();
+    float ss = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) ss += nss[w];
+    const float inv = 1.0f / __builtin_sqrtf(ss / (float)K + eps);
+    if (wc0 < wc1) {
+      stage_x(inv);
+      consume(wc0);
+    }
   }
 
   if (W > 1) {
@@ -255,6 +331,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
         if (nn < N) {
           float v = acc[mb][i] * bits_to_f32<ST>(sc[i]);
           if (bias) v += bits_to_f32<XT>(bi[i]);
+          if constexpr (RES) v = bits_to_f32<XT>(rb[i]) + round_through<XT>(v);
           y[(int64_t)m * ldy + nn] = from_f32<XT>(v);
         }
       }

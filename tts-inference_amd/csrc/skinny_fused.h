@@ -1,0 +1,67 @@
+// Launch plumbing of the W8A16 skinny kernel's fused variants (skinny.h: PRO, RES):
+// one row set of template instantiations per (prologue, residual, staged rows), each
+// built in one translation unit (w8a16_fused.hip, w8a16_fused_res.hip).
+#pragma once
+
+#include "skinny.h"
+
+namespace qtts {
+
+struct FusedArgs {
+  const void* x;
+  int64_t m, k, ldx;
+  const int8_t* qs;
+  int64_t n;
+  const void* scale;
+  const void* bias;
+  const void* aux;  // the norm weight (kProRmsNorm)
+  float eps;
+  const void* res;  // residual rows (RES)
+  int64_t ldr;
+  void* y;
+  int64_t ldy;
+  float* part;
+  unsigned* counters;
+  SkinnyCfg c;
+  unsigned blocks;
+  hipStream_t st;
+};
+
+template <typename XT, typename ST, int W, int CPW, int MX, int PRO, bool RES>
+void launch_fused_one(const FusedArgs& a) {
+  launch(&w8a16_skinny_kernel<XT, ST, W, CPW, kLayoutStrips, true, 1, MX, false, PRO, RES>, dim3(a.blocks),
+         dim3(W * 64), 0, a.st, (const XT*)a.x, (int)a.m, (int)a.k, a.ldx, a.qs, (int)a.n, (int64_t)0,
+         (const ST*)a.scale, (const XT*)a.bias, (XT*)a.y, a.ldy, a.part, a.counters, a.c.strips, a.c.S, a.c.cps,
+         (const XT*)a.aux, a.eps, (const XT*)a.res, a.ldr);
+}
+
+// The (waves, chunks) pairs built with staged rows (qtts_w8a16_xrows_built).
+template <typename XT, typename ST, int MX, int PRO, bool RES>
+int launch_fused_wc(const FusedArgs& a) {
+  switch (a.c.waves * 64 + a.c.cpw) {
+    case 1 * 64 + 8: launch_fused_one<XT, ST, 1, 8, MX, PRO, RES>(a); break;
+    case 2 * 64 + 8: launch_fused_one<XT, ST, 2, 8, MX, PRO, RES>(a); break;
+    case 4 * 64 + 8: launch_fused_one<XT, ST, 4, 8, MX, PRO, RES>(a); break;
+    case 8 * 64 + 8: launch_fused_one<XT, ST, 8, 8, MX, PRO, RES>(a); break;
+    case 16 * 64 + 6: launch_fused_one<XT, ST, 16, 6, MX, PRO, RES>(a); break;
+    case 8 * 64 + 12: launch_fused_one<XT, ST, 8, 12, MX, PRO, RES>(a); break;
+    default: return 1;
+  }
+  return 0;
+}
+
+// Returns 0 after a launch, 1 when the combination is not built.  Scales are either
+// of the activation dtype (Int8WeightOnlyMethod) or fp32.
+template <int PRO, bool RES, int MX>
+int launch_fused(int x_dtype, bool f32_scale, const FusedArgs& a) {
+  if (x_dtype == QTTS_BF16)
+    return f32_scale ? launch_fused_wc<bf16_t, float, MX, PRO, RES>(a) : launch_fused_wc<bf16_t, bf16_t, MX, PRO, RES>(a);
+  return f32_scale ? launch_fused_wc<f16_t, float, MX, PRO, RES>(a) : launch_fused_wc<f16_t, f16_t, MX, PRO, RES>(a);
+}
+
+// Residual-only variants (w8a16_fused_res.hip) for 1, 4 and 8 staged rows.
+extern template int launch_fused<kProNone, true, 1>(int, bool, const FusedArgs&);
+extern template int launch_fused<kProNone, true, 4>(int, bool, const FusedArgs&);
+extern template int launch_fused<kProNone, true, 8>(int, bool, const FusedArgs&);
+
+}  // namespace qtts

@@ -35,7 +35,9 @@ DIV_DEVICE, DIV_IEEE = 0, 1
 # bits 24-31 chunks per wave of the skinny kernels (0 = automatic)
 ALGO_AUTO, ALGO_SKINNY, ALGO_TILE = 0, 1, 2
 # qtts_op
-OP_W8A16, OP_W8A8_FP8, OP_FP8_LINEAR, OP_W8A8_INT8, OP_INT8_LINEAR, OP_FP8W, OP_W8A16_SILU = 0, 1, 2, 3, 4, 5, 6
+OP_W8A16, OP_W8A8_FP8, OP_FP8_LINEAR, OP_W8A8_INT8, OP_INT8_LINEAR, OP_FP8W, OP_W8A16_SILU, OP_W8A16_FUSED = range(8)
+# qtts_prologue
+PRO_NONE, PRO_SILU_MUL, PRO_RMS_NORM = 0, 1, 2
 # qtts_strip_kind
 STRIP_INT8, STRIP_FP8 = 0, 1
 
@@ -64,6 +66,8 @@ EXPORTS = (
     "qtts_fp8w_gemm_strips",
     "qtts_silu_mul",
     "qtts_w8a16_silu_mul_gemm_strips",
+    "qtts_rms_norm",
+    "qtts_w8a16_fused_gemm_strips",
     "qtts_kernel_timer_begin",
     "qtts_kernel_timer_end",
 )
@@ -146,6 +150,11 @@ def load() -> ctypes.CDLL:
         L.qtts_silu_mul.argtypes = [p, i32, i64, i64, i64, p, i64, p]
         L.qtts_w8a16_silu_mul_gemm_strips.restype = i32
         L.qtts_w8a16_silu_mul_gemm_strips.argtypes = [p, i32, i64, i64, i64, p, i64, p, i32, p, p, i64, i32, p, i64, p]
+        L.qtts_rms_norm.restype = i32
+        L.qtts_rms_norm.argtypes = [p, i32, i64, i64, i64, p, ctypes.c_float, p, i64, p]
+        L.qtts_w8a16_fused_gemm_strips.restype = i32
+        L.qtts_w8a16_fused_gemm_strips.argtypes = [p, i32, i64, i64, i64, i32, p, ctypes.c_float, p, i64, p, i32, p,
+                                                   p, i64, p, i64, i32, p, i64, p]
         L.qtts_kernel_timer_begin.restype = i32
         L.qtts_kernel_timer_begin.argtypes = [i32]
         L.qtts_kernel_timer_end.restype = i32

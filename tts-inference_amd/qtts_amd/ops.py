@@ -14,7 +14,8 @@ import torch
 
 from . import _lib
 from ._lib import (ALGO_AUTO, DIV_DEVICE, DIV_IEEE, OP_FP8_LINEAR, OP_FP8W, OP_INT8_LINEAR,  # noqa: F401
-                   OP_W8A16, OP_W8A16_SILU, OP_W8A8_FP8, OP_W8A8_INT8, STRIP_FP8, STRIP_INT8, algo_code)
+                   OP_W8A16, OP_W8A16_FUSED, OP_W8A16_SILU, OP_W8A8_FP8, OP_W8A8_INT8, PRO_NONE, PRO_RMS_NORM,
+                   PRO_SILU_MUL, STRIP_FP8, STRIP_INT8, algo_code)
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
@@ -605,6 +606,76 @@ def w8a16_silu_mul_gemm_strips(gate_up: torch.Tensor, qs: torch.Tensor, n: int, 
         dtype_code(scale.dtype), _ptr(bias), _ptr(out), n, algo, ws, ws_n, _stream(dev))
     _lib.check(st, "w8a16_silu_mul_gemm_strips")
     return out.reshape(*shape[:-1], n)
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """RMSNorm over the last dimension (qtts/layers/norm.py:50-76): fp32 sum of squares,
+    ``inv = 1 / sqrt(mean + eps)``, ``(x * inv) * weight`` rounded to x's dtype."""
+    shape = x.shape
+    a = _flatten(x)
+    rows, k = a.shape
+    if weight.numel() != k:
+        raise ValueError(f"norm weight has {weight.numel()} entries for rows of {k}")
+    dev = _require_cuda(a, weight)
+    w = weight.to(a.dtype).contiguous()
+    out = torch.empty((rows, k), dtype=a.dtype, device=dev)
+    st = _lib.load().qtts_rms_norm(_ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else k, _ptr(w),
+                                   float(eps), _ptr(out), k, _stream(dev))
+    _lib.check(st, "rms_norm")
+    return out.reshape(shape)
+
+
+def w8a16_fused_gemm_strips(x: torch.Tensor, qs: torch.Tensor, n: int, scale: torch.Tensor,
+                            bias: torch.Tensor | None = None, *, prologue: int = PRO_NONE,
+                            norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                            residual: torch.Tensor | None = None, out: torch.Tensor | None = None,
+                            algo: int = ALGO_AUTO) -> torch.Tensor:
+    """``[residual +] linear(prologue(x))`` for an int8 strip-layout linear in one call
+    (qtts/models/talker.py:246-271).  ``prologue``: PRO_NONE, PRO_SILU_MUL (x is the fused
+    ``[..., 2K]`` gate_up output) or PRO_RMS_NORM (with ``norm_weight`` and ``eps``).
+    ``residual`` is ``[..., n]`` of x's dtype; ``out`` may be the residual itself."""
+    shape = x.shape
+    a = _gate_up_rows(x) if prologue == PRO_SILU_MUL else _flatten(x)
+    rows = a.shape[0]
+    k = a.shape[1] // 2 if prologue == PRO_SILU_MUL else a.shape[1]
+    if qs.dtype != torch.int8 or qs.numel() != strip_bytes(n, k, STRIP_INT8):
+        raise ValueError(f"weight is not an int8 strip-layout [{n}, {k}] buffer")
+    if scale.numel() != n:
+        raise ValueError(f"scale has {scale.numel()} entries for {n} output channels")
+    if bias is not None:
+        if bias.numel() != n:
+            raise ValueError(f"bias has {bias.numel()} entries for {n} output channels")
+        bias = bias.to(a.dtype).contiguous()
+    if prologue == PRO_RMS_NORM:
+        if norm_weight is None or norm_weight.numel() != k:
+            raise ValueError(f"RMSNorm prologue needs a norm weight of {k} entries")
+        norm_weight = norm_weight.to(a.dtype).contiguous()
+    if a.data_ptr() % 16 or (rows > 1 and a.stride(0) % 8):
+        a = a.contiguous() if a.data_ptr() % 16 == 0 else a.clone()
+    res = None
+    if residual is not None:
+        res = _flatten(residual)
+        if res.shape != (rows, n) or res.dtype != a.dtype:
+            raise ValueError(f"residual must be [{rows}, {n}] of {a.dtype}, got {tuple(res.shape)} {res.dtype}")
+    dev = _require_cuda(a, qs, scale, bias, norm_weight, res)
+    scale = scale.contiguous()
+    if out is None:
+        y = torch.empty((rows, n), dtype=a.dtype, device=dev)
+    else:
+        y = _flatten(out)
+        if y.shape != (rows, n) or y.dtype != a.dtype or y.data_ptr() != out.data_ptr():
+            raise ValueError(f"out must be a [{rows}, {n}] {a.dtype} tensor")
+    reserve_workspace(dev, workspace_bytes(OP_W8A16_FUSED, rows, n, k, algo))
+    ws, ws_n = _ws_for(dev)
+    st = _lib.load().qtts_w8a16_fused_gemm_strips(
+        _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else a.shape[1], int(prologue),
+        _ptr(norm_weight), float(eps), _ptr(qs), n, _ptr(scale), dtype_code(scale.dtype), _ptr(bias), _ptr(res),
+        res.stride(0) if res is not None and rows > 1 else n, _ptr(y), y.stride(0) if rows > 1 else n, algo, ws, ws_n,
+        _stream(dev))
+    _lib.check(st, "w8a16_fused_gemm_strips")
+    if out is not None:
+        return out
+    return y.reshape(*shape[:-1], n)
 
 
 class KernelTimer:
