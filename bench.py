@@ -475,6 +475,144 @@ def run_mlp(args, torch, ops):
                                     "M": list(ms)}, "per_m": per_m}
 
 
+def make_chain_inputs(torch, ops, stack, layers, m, attn, norms):
+    """Buffers and chain links of the decode step as the talker runs it (qtts/models/talker.py:246-271):
+    launch 0 is input_layernorm + qkv_proj of layer 0; launch l + 1 runs layer l's o_proj + residual,
+    post_attention_layernorm + gate_up_proj + SiLU * mul, down_proj + residual and layer l + 1's
+    input_layernorm + qkv_proj.  The attention between qkv and o is not part of this path: every
+    layer's o_proj reads the same synthetic attention output ``attn``."""
+    L = ops.ChainLink
+    bf = dict(dtype=torch.bfloat16, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(17 + m)
+    h_in = torch.randn(m, 2048, generator=g, device="cuda").to(torch.bfloat16)
+    qkv = [torch.empty(m, 4096, **bf) for _ in range(layers)]
+    h1 = [torch.empty(m, 2048, **bf) for _ in range(layers)]
+    act = [torch.empty(m, 6144, **bf) for _ in range(layers)]
+    h2 = [torch.empty(m, 2048, **bf) for _ in range(layers)]
+    ent = lambda layer, i: stack[4 * layer + i]  # noqa: E731  (qkv, o, gate_up, down)
+    w_in, w_post = norms
+    launches = [[L(h_in, ent(0, 0)["qs"], 4096, ent(0, 0)["s"], qkv[0], prologue=ops.PRO_RMS_NORM,
+                   norm_weight=w_in[0])]]
+    for layer in range(layers):
+        h_prev = h_in if layer == 0 else h2[layer - 1]
+        links = [L(attn, ent(layer, 1)["qs"], 2048, ent(layer, 1)["s"], h1[layer], epilogue=ops.EPI_RESIDUAL,
+                   residual=h_prev),
+                 L(h1[layer], ent(layer, 2)["qs"], 12288, ent(layer, 2)["s"], act[layer], prologue=ops.PRO_RMS_NORM,
+                   norm_weight=w_post[layer], epilogue=ops.EPI_SILU_MUL, after=0),
+                 L(act[layer], ent(layer, 3)["qs"], 2048, ent(layer, 3)["s"], h2[layer], epilogue=ops.EPI_RESIDUAL,
+                   residual=h1[layer], after=1)]
+        if layer + 1 < layers:
+            links.append(L(h2[layer], ent(layer + 1, 0)["qs"], 4096, ent(layer + 1, 0)["s"], qkv[layer + 1],
+                           prologue=ops.PRO_RMS_NORM, norm_weight=w_in[layer + 1], after=2))
+        launches.append(links)
+    return h_in, launches
+
+
+def run_talker_chain(args, torch, ops):
+    """The talker decode step's linears with their real data flow, int8 weight-only, 28 layers,
+    M in {1, 2, 4, 8}: one persistent chain launch per layer (qtts_w8a16_chain_strips) against the
+    same computation as one fused kernel per linear (qtts_w8a16_fused_gemm_strips: RMSNorm
+    prologues, SiLU * mul prologue, residual epilogues) and against bf16 torch (hipBLASLt
+    F.linear, F.rms_norm, F.silu, adds).  The attention between qkv_proj and o_proj is not part
+    of the path; o_proj reads a fixed synthetic attention output."""
+    import torch.nn.functional as F
+    ms = (1, 2, 4, 8)
+    layers = 28
+    eps = 1e-6
+    log(f"[bench] packing {layers}x4 talker weights (int8 + bf16 baseline copy)")
+    stack = make_stack(torch, ops, TALKER, layers, keep_bf16=True)
+    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    g = torch.Generator(device="cuda").manual_seed(5)
+    w_in = [(1 + 0.1 * torch.randn(2048, generator=g, device="cuda")).to(torch.bfloat16) for _ in range(layers)]
+    w_post = [(1 + 0.1 * torch.randn(2048, generator=g, device="cuda")).to(torch.bfloat16) for _ in range(layers)]
+    xs = make_inputs(torch, [2048], ms)
+    ent = lambda layer, i: stack[4 * layer + i]  # noqa: E731
+    nbytes_of = {m: sum(w8a16_bytes(m, e["n"], e["k"]) for e in stack) for m in ms}
+
+    def per_linear(h_in, attn):
+        qkv = ops.w8a16_fused_gemm_strips(h_in, ent(0, 0)["qs"], 4096, ent(0, 0)["s"], prologue=ops.PRO_RMS_NORM,
+                                          norm_weight=w_in[0], eps=eps)
+        h = h_in
+        for layer in range(layers):
+            h1 = ops.w8a16_fused_gemm_strips(attn, ent(layer, 1)["qs"], 2048, ent(layer, 1)["s"], residual=h)
+            gu = ops.w8a16_fused_gemm_strips(h1, ent(layer, 2)["qs"], 12288, ent(layer, 2)["s"],
+                                             prologue=ops.PRO_RMS_NORM, norm_weight=w_post[layer], eps=eps)
+            h = ops.w8a16_fused_gemm_strips(gu, ent(layer, 3)["qs"], 2048, ent(layer, 3)["s"],
+                                            prologue=ops.PRO_SILU_MUL, residual=h1)
+            if layer + 1 < layers:
+                qkv = ops.w8a16_fused_gemm_strips(h, ent(layer + 1, 0)["qs"], 4096, ent(layer + 1, 0)["s"],
+                                                  prologue=ops.PRO_RMS_NORM, norm_weight=w_in[layer + 1], eps=eps)
+        return h, qkv
+
+    def bf16(h_in, attn):
+        qkv = F.linear(F.rms_norm(h_in, (2048,), w_in[0], eps), ent(0, 0)["w_bf16"])
+        h = h_in
+        for layer in range(layers):
+            h1 = h + F.linear(attn, ent(layer, 1)["w_bf16"])
+            gu = F.linear(F.rms_norm(h1, (2048,), w_post[layer], eps), ent(layer, 2)["w_bf16"])
+            gate, up = gu.split([6144, 6144], dim=-1)
+            h = h1 + F.linear(F.silu(gate) * up, ent(layer, 3)["w_bf16"])
+            if layer + 1 < layers:
+                qkv = F.linear(F.rms_norm(h, (2048,), w_in[layer + 1], eps), ent(layer + 1, 0)["w_bf16"])
+        return h, qkv
+
+    per_m = {}
+    total_bytes, total_ms = 0, 0.0
+    layer_bytes, layer_ms = [], []
+    for m in ms:
+        attn = xs[(m, 2048)]
+        h_in, launches = make_chain_inputs(torch, ops, stack, layers, m, attn, (w_in, w_post))
+        plans = [ops.ChainPlan(links) for links in launches]
+        g_c = capture(torch, lambda: [plan() for plan in plans])
+        g_p = capture(torch, lambda: per_linear(h_in, attn))
+        g_b = capture(torch, lambda: bf16(h_in, attn))
+        t_c = time_graph(torch, g_c, args.steps, args.warmup)
+        t_p = time_graph(torch, g_p, args.steps, args.warmup)
+        t_b = time_graph(torch, g_b, max(5, args.steps // 2), args.warmup)
+        if any(plan.timed_out() for plan in plans):
+            raise RuntimeError("a chain launch gave up waiting for a link")
+        full = [plan for plan, links in zip(plans, launches) if len(links) == 4]
+        dur = kernel_ms(ops, full, reps=2)
+        layer_ms.append(dur)
+        layer_bytes.append(sum(w8a16_bytes(m, ln.n, ln.x.shape[1]) for ln in launches[1]))
+        nbytes = nbytes_of[m]
+        total_bytes += nbytes
+        total_ms += t_c
+        per_m[str(m)] = {
+            "chain_us": round(t_c * 1e3, 2),
+            "GBps": round(nbytes / (t_c * 1e-3) / 1e9, 1),
+            "pct_of_hbm_peak": round(100 * nbytes / (t_c * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1),
+            "per_linear_fused_us": round(t_p * 1e3, 2),
+            "bf16_torch_us": round(t_b * 1e3, 2),
+            "chain_vs_per_linear": round(t_p / t_c, 3),
+            "chain_vs_bf16": round(t_b / t_c, 3),
+            "chain_launch_us": round(dur * 1e3, 3),
+        }
+        del g_c, g_p, g_b
+        log(f"[bench] chain M={m}: {per_m[str(m)]}")
+    dur_ms = statistics.mean(layer_ms)
+    lb = statistics.mean(layer_bytes)
+    achieved = lb / (dur_ms * 1e-3) / 1e9
+    return {
+        "metric": "int8 W-only decode GEMM HBM GB/s (% of peak) + linear-stack us/step, M=1..8",
+        "value": round(total_bytes / (total_ms * 1e-3) / 1e9, 1),
+        "unit": "GB/s",
+        "pct_of_hbm_peak": round(100 * total_bytes / (total_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1),
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int8 weights x bf16 activations, fp32 accumulate",
+        "data": "synthetic (seeded N(0,0.02) weights per layer, N(0,1) bf16 activations)",
+        "config": {"workload": "talker decode step's linears with their data flow: 28 layers x {norm+qkv, "
+                               "o+residual, norm+gate_up+silu*mul, down+residual}, one chain launch per layer, "
+                               "one HIP graph per M", "layers": layers, "M": list(ms)},
+        "per_m": per_m,
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "w8a16_chain_kernel (o, gate_up, down, next qkv of one layer; M in 1,2,4,8)",
+                     "avg_launch_us": round(dur_ms * 1e3, 3), "bytes_per_launch": round(lb)},
+    }
+
+
 def run_traffic_probe(args, torch, ops):
     """Kernels for a rocprofv3 --pmc pass: a 256 MiB device copy (known bytes, the counters' scale)
     and the dominant kernel of configs[1] (gate_up over its 28 distinct weights at M = 1, 2, 4, 8),
@@ -556,6 +694,8 @@ def main() -> int:
                     help="time the configs[1] decode stack with fp8 weight-only weights instead of a config")
     ap.add_argument("--mlp", action="store_true",
                     help="time the talker MLP (gate_up, silu*up, down) with the activation fused into down")
+    ap.add_argument("--chain", action="store_true",
+                    help="time the talker decode step's linears as one chain launch per layer")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="launch only the kernels a rocprofv3 --pmc pass measures (copy + gate_up)")
     args = ap.parse_args()
@@ -588,6 +728,8 @@ def main() -> int:
         runner = run_fp8w_stack
     if args.mlp:
         runner = run_mlp
+    if args.chain:
+        runner = run_talker_chain
     with torch.inference_mode():
         result = runner(args, torch, ops)
     result["device"] = torch.cuda.get_device_name()

@@ -213,6 +213,79 @@ int qtts_w8a16_fused_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t 
                                  const void* bias, const void* residual, int64_t ldr, void* y,
                                  int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream);
 
+/* --- a chain of dependent decode linears in one launch ------------------------------ */
+
+#define QTTS_CHAIN_MAX_LINKS 8
+#define QTTS_CHAIN_MAX_ROWS 8
+#define QTTS_CHAIN_MAX_ITEMS 65536
+/* A chain's control block (qtts_w8a16_chain_ctl_bytes): a timeout flag at byte
+ * QTTS_CHAIN_TIMEOUT_BYTE (sticky: set when a wait gave up, cleared only by the caller),
+ * then one completion flag per work item, QTTS_CHAIN_FLAG_STRIDE bytes apart, from byte
+ * QTTS_CHAIN_FLAGS_BYTE. */
+#define QTTS_CHAIN_TIMEOUT_BYTE 0
+#define QTTS_CHAIN_FLAGS_BYTE 256
+#define QTTS_CHAIN_FLAG_STRIDE 256
+
+/* What a chain link does with its output. */
+typedef enum {
+    QTTS_EPI_STORE = 0,     /* y = linear(h) */
+    QTTS_EPI_RESIDUAL = 1,  /* y = dtype(f32(residual) + f32(dtype(linear(h)))) */
+    QTTS_EPI_SILU_MUL = 2   /* y[:, c] = dtype(dtype(silu(g)) * u), g = dtype(linear(h))[:, c],
+                               u = dtype(linear(h))[:, n/2 + c]: y is [m, n/2] */
+} qtts_epilogue;
+
+/* One W8A16 linear of a chain (qtts_w8a16_chain_strips).
+ *   h = x                         (prologue QTTS_PRO_NONE)
+ *   h = qtts_rms_norm(x, norm_weight, eps)   (QTTS_PRO_RMS_NORM; sums in another order)
+ * x: [m, k] of x_dtype, 16-byte aligned rows (stride ldx).  qs: int8 strip weights of
+ * [n, k] (qtts_to_strips, QTTS_STRIP_INT8).  scale [n] of scale_dtype, bias [n] of
+ * x_dtype or NULL.  residual: [m, n] of x_dtype, 8-byte aligned rows (stride ldr); may be
+ * y itself.  y: 8-byte aligned rows (stride ldy).  after: the index of an earlier link
+ * whose output this link reads (x or residual), or -1; links that write what another
+ * link reads must be ordered through `after` (directly or transitively), and so must a
+ * link that overwrites what another one reads. */
+typedef struct {
+    const void* x;
+    int64_t ldx;
+    const int8_t* qs;
+    int64_t n, k;
+    const void* scale;
+    const void* bias;
+    int prologue;
+    const void* norm_weight;
+    float eps;
+    int epilogue;
+    const void* residual;
+    int64_t ldr;
+    void* y;
+    int64_t ldy;
+    int after;
+} qtts_chain_link;
+
+/* Bytes of the control block a chain of these links needs (negative: invalid chain). */
+int64_t qtts_w8a16_chain_ctl_bytes(const qtts_chain_link* links, int count, int64_t m);
+
+/* The linears of a talker decoder layer between two attention calls
+ * (qtts/models/talker.py:246-271): o_proj with the residual add, gate_up_proj after
+ * post_attention_layernorm with GatedMLP's SiLU * mul (qtts/layers/activation.py:142-147),
+ * down_proj with the residual add, and the next layer's qkv_proj after its
+ * input_layernorm, in ONE persistent launch of the W8A16 GEMM arithmetic
+ * (qtts/quant/kernels.py:113-135): each linear's weights stream in while the link it
+ * waits for finishes.  No counterpart in the reference, which launches one kernel per
+ * linear, norm and activation; results are those of the separate calls within the
+ * GEMM tolerance (the K split differs).  x_dtype bf16 (QTTS_ERR_UNSUPPORTED otherwise),
+ * scale_dtype bf16 or fp32.  count 1..8 links, m 0..8 rows, n % 16 == 0, k % 64 == 0,
+ * k <= 8192 (k <= 3072 with QTTS_EPI_SILU_MUL, which also needs n % 32 == 0).
+ * ctl: this chain's own control block, 256-byte aligned, zero-filled before its first
+ * launch and used by launches of this same chain only (the same links, rows and algo;
+ * no clearing between launches or graph replays).  algo bits 8-23: workgroups (0, or
+ * more than fit on the device at once: as many as fit).  Every workgroup must be
+ * resident together, so a chain must not share the device with a concurrent persistent
+ * kernel that waits on it; a wait that cannot end gives up after about a second and
+ * raises the timeout flag.  Launches of one chain must be ordered (one stream). */
+int qtts_w8a16_chain_strips(const qtts_chain_link* links, int count, int x_dtype, int scale_dtype,
+                            int64_t m, int algo, void* ctl, int64_t ctl_bytes, void* stream);
+
 /* --- fp8 W8A8 --------------------------------------------------------------------- */
 
 /* Per-token e4m3 activation quantization, replacing the activation half of

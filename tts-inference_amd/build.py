@@ -39,6 +39,15 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-file additions.  chain.hip: its single-lane ticket atomics must not go through
+# the atomic optimizer, which turns them into wave-reduced atomics whose result is
+# waited for at once (the ticket for the next work item is meant to arrive while the
+# current one runs).
+FILE_FLAGS = {
+    "chain.hip": ["-mllvm", "-amdgpu-atomic-optimizer-strategy=None"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and os.path.exists(cand):
@@ -67,7 +76,7 @@ def build(verbose: bool = False) -> str:
     for src in sources:
         obj = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([cc, *HIPCC_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([cc, *HIPCC_FLAGS, *FILE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj])
     workers = min(len(cmds), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(workers) as pool:
         list(pool.map(lambda c: _run(c, verbose), cmds))

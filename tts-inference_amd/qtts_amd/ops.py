@@ -8,14 +8,16 @@ CPU or eager-PyTorch fallback: a missing library or an unsupported device raises
 
 from __future__ import annotations
 
+import dataclasses
 import threading
 
 import torch
 
 from . import _lib
-from ._lib import (ALGO_AUTO, DIV_DEVICE, DIV_IEEE, OP_FP8_LINEAR, OP_FP8W, OP_INT8_LINEAR,  # noqa: F401
-                   OP_W8A16, OP_W8A16_FUSED, OP_W8A16_SILU, OP_W8A8_FP8, OP_W8A8_INT8, PRO_NONE, PRO_RMS_NORM,
-                   PRO_SILU_MUL, STRIP_FP8, STRIP_INT8, algo_code)
+from ._lib import (ALGO_AUTO, CHAIN_MAX_LINKS, CHAIN_MAX_ROWS, CHAIN_TIMEOUT_BYTE, DIV_DEVICE,  # noqa: F401
+                   DIV_IEEE, EPI_RESIDUAL, EPI_SILU_MUL, EPI_STORE, OP_FP8_LINEAR, OP_FP8W, OP_INT8_LINEAR,
+                   OP_W8A16, OP_W8A16_FUSED, OP_W8A16_SILU, OP_W8A8_FP8, OP_W8A8_INT8, PRO_NONE,
+                   PRO_RMS_NORM, PRO_SILU_MUL, STRIP_FP8, STRIP_INT8, algo_code)
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
@@ -676,6 +678,131 @@ def w8a16_fused_gemm_strips(x: torch.Tensor, qs: torch.Tensor, n: int, scale: to
     if out is not None:
         return out
     return y.reshape(*shape[:-1], n)
+
+
+@dataclasses.dataclass
+class ChainLink:
+    """One int8 weight-only linear of a chain (``w8a16_chain``): ``out = epilogue(linear(prologue(x)))``.
+
+    ``x`` is ``[m, k]`` bf16 (rows may be strided, 16-byte aligned); ``qs`` the int8 strip
+    weight of ``[n, k]`` with its ``scale``; ``out`` a preallocated ``[m, n]`` tensor
+    (``[m, n // 2]`` with EPI_SILU_MUL).  ``prologue``: PRO_NONE or PRO_RMS_NORM (with
+    ``norm_weight`` and ``eps``).  ``epilogue``: EPI_STORE, EPI_RESIDUAL (``out = residual
+    + linear``; ``residual`` may be ``out``) or EPI_SILU_MUL (``out = silu(gate) * up`` of
+    the two output halves).  ``after``: index of the earlier link whose output this one
+    reads, or -1."""
+
+    x: torch.Tensor
+    qs: torch.Tensor
+    n: int
+    scale: torch.Tensor
+    out: torch.Tensor
+    bias: torch.Tensor | None = None
+    prologue: int = PRO_NONE
+    norm_weight: torch.Tensor | None = None
+    eps: float = 1e-6
+    epilogue: int = EPI_STORE
+    residual: torch.Tensor | None = None
+    after: int = -1
+
+
+def _rows2d(t: torch.Tensor, what: str) -> torch.Tensor:
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{what} must be a 2-D tensor with unit column stride, got {tuple(t.shape)}")
+    return t
+
+
+class ChainPlan:
+    """Dependent int8 weight-only linears prepared for one persistent launch each time the plan
+    is called (``qtts_w8a16_chain_strips``): the talker decoder layer's o_proj + residual,
+    post_attention_layernorm + gate_up_proj + SiLU * mul, down_proj + residual and the next
+    layer's input_layernorm + qkv_proj (qtts/models/talker.py:246-271) with no launch
+    boundary between them.  Calling it writes every link's ``out`` on the current stream.
+
+    The plan owns the chain's control block (per-item completion flags, zero-filled once
+    here, never cleared again), so build it outside graph capture and call it inside as
+    often as needed; the tensors of its links must stay where they are.  ``algo`` bits
+    8-23: workgroups (0: as many as fit at once)."""
+
+    def __init__(self, links: list[ChainLink], algo: int = 0) -> None:
+        if not 1 <= len(links) <= CHAIN_MAX_LINKS:
+            raise ValueError(f"a chain has 1..{CHAIN_MAX_LINKS} links, got {len(links)}")
+        m = links[0].x.shape[0] if links[0].x.dim() == 2 else -1
+        arr = (_lib.ChainLinkC * len(links))()
+        keep, tensors = [], []
+        for i, ln in enumerate(links):
+            x = _rows2d(ln.x, f"link {i} x")
+            out = _rows2d(ln.out, f"link {i} out")
+            k = x.shape[1]
+            n = int(ln.n)
+            if x.shape[0] != m:
+                raise ValueError(f"link {i} has {x.shape[0]} rows, link 0 has {m}")
+            if x.dtype != torch.bfloat16:
+                raise ValueError(f"link {i}: the chain takes bf16 activations, got {x.dtype}")
+            if ln.qs.dtype != torch.int8 or ln.qs.numel() != strip_bytes(n, k, STRIP_INT8):
+                raise ValueError(f"link {i}: weight is not an int8 strip-layout [{n}, {k}] buffer")
+            if ln.scale.numel() != n or ln.scale.dtype not in (torch.bfloat16, torch.float32):
+                raise ValueError(f"link {i}: scale must hold {n} bf16 or fp32 entries")
+            if ln.scale.dtype != links[0].scale.dtype:
+                raise ValueError("every link's scale must have the same dtype")
+            ocols = n // 2 if ln.epilogue == EPI_SILU_MUL else n
+            if out.shape != (m, ocols) or out.dtype != x.dtype:
+                raise ValueError(f"link {i}: out must be [{m}, {ocols}] {x.dtype}, got {tuple(out.shape)} {out.dtype}")
+            bias = None
+            if ln.bias is not None:
+                if ln.bias.numel() != n:
+                    raise ValueError(f"link {i}: bias has {ln.bias.numel()} entries for {n} outputs")
+                bias = ln.bias.to(x.dtype).contiguous()
+            nw = None
+            if ln.prologue == PRO_RMS_NORM:
+                if ln.norm_weight is None or ln.norm_weight.numel() != k:
+                    raise ValueError(f"link {i}: the RMSNorm prologue needs a norm weight of {k} entries")
+                nw = ln.norm_weight.to(x.dtype).contiguous()
+            res = None
+            if ln.epilogue == EPI_RESIDUAL:
+                if ln.residual is None:
+                    raise ValueError(f"link {i}: the residual epilogue needs a residual")
+                res = _rows2d(ln.residual, f"link {i} residual")
+                if res.shape != (m, n) or res.dtype != x.dtype:
+                    raise ValueError(f"link {i}: residual must be [{m}, {n}] {x.dtype}")
+            scale = ln.scale.contiguous()
+            keep += [x, out, ln.qs, scale, bias, nw, res]
+            tensors += [x, out, ln.qs, scale, bias, nw, res]
+            c = arr[i]
+            c.x, c.ldx, c.qs, c.n, c.k = x.data_ptr(), x.stride(0), ln.qs.data_ptr(), n, k
+            c.scale, c.bias, c.prologue = scale.data_ptr(), _ptr(bias), int(ln.prologue)
+            c.norm_weight, c.eps, c.epilogue = _ptr(nw), float(ln.eps), int(ln.epilogue)
+            c.residual, c.ldr = _ptr(res), (res.stride(0) if res is not None else n)
+            c.y, c.ldy, c.after = out.data_ptr(), out.stride(0), int(ln.after)
+        self.device = _require_cuda(*tensors)
+        nbytes = _lib.load().qtts_w8a16_chain_ctl_bytes(arr, len(links), m)
+        if nbytes < 0:
+            _lib.check(int(nbytes), "w8a16_chain_ctl_bytes")
+        self.ctl = torch.zeros((nbytes + 3) // 4, dtype=torch.int32, device=self.device)
+        self.m, self.algo, self.count = m, int(algo), len(links)
+        self.x_dtype, self.s_dtype = dtype_code(links[0].x.dtype), dtype_code(links[0].scale.dtype)
+        self._arr, self._keep = arr, keep
+
+    def __call__(self) -> None:
+        st = _lib.load().qtts_w8a16_chain_strips(self._arr, self.count, self.x_dtype, self.s_dtype, self.m, self.algo,
+                                                 self.ctl.data_ptr(), self.ctl.numel() * 4, _stream(self.device))
+        _lib.check(st, "w8a16_chain_strips")
+
+    def timed_out(self, clear: bool = True) -> bool:
+        """Whether a launch of this chain gave up waiting for a link (the control block's sticky
+        timeout flag; reads device memory, so call it outside graph capture)."""
+        flag = self.ctl[CHAIN_TIMEOUT_BYTE // 4:CHAIN_TIMEOUT_BYTE // 4 + 1]
+        hit = bool(flag.any().item())
+        if clear and hit:
+            flag.zero_()
+        return hit
+
+
+def w8a16_chain(links: list[ChainLink], algo: int = 0) -> ChainPlan:
+    """Prepare and launch a chain once (``ChainPlan``); returns the plan for further launches."""
+    plan = ChainPlan(links, algo)
+    plan()
+    return plan
 
 
 class KernelTimer:
