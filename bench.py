@@ -510,11 +510,12 @@ def make_chain_inputs(torch, ops, stack, layers, m, attn, norms):
 
 def run_talker_chain(args, torch, ops):
     """The talker decode step's linears with their real data flow, int8 weight-only, 28 layers,
-    M in {1, 2, 4, 8}: one persistent chain launch per layer (qtts_w8a16_chain_strips) against the
-    same computation as one fused kernel per linear (qtts_w8a16_fused_gemm_strips: RMSNorm
-    prologues, SiLU * mul prologue, residual epilogues) and against bf16 torch (hipBLASLt
-    F.linear, F.rms_norm, F.silu, adds).  The attention between qkv_proj and o_proj is not part
-    of the path; o_proj reads a fixed synthetic attention output."""
+    M in {1, 2, 4, 8}, three ways: one fused kernel per linear (input_layernorm + qkv_proj,
+    o_proj + residual, post_attention_layernorm + gate_up_proj + SiLU * mul, down_proj +
+    residual: qtts_w8a16_fused_gemm_strips and qtts_w8a16_gate_up_silu_strips), one persistent
+    chain launch per layer (qtts_w8a16_chain_strips), and bf16 torch (hipBLASLt F.linear,
+    F.rms_norm, F.silu, adds).  The attention between qkv_proj and o_proj is not part of the
+    path; o_proj reads a fixed synthetic attention output."""
     import torch.nn.functional as F
     ms = (1, 2, 4, 8)
     layers = 28
@@ -535,10 +536,9 @@ def run_talker_chain(args, torch, ops):
         h = h_in
         for layer in range(layers):
             h1 = ops.w8a16_fused_gemm_strips(attn, ent(layer, 1)["qs"], 2048, ent(layer, 1)["s"], residual=h)
-            gu = ops.w8a16_fused_gemm_strips(h1, ent(layer, 2)["qs"], 12288, ent(layer, 2)["s"],
-                                             prologue=ops.PRO_RMS_NORM, norm_weight=w_post[layer], eps=eps)
-            h = ops.w8a16_fused_gemm_strips(gu, ent(layer, 3)["qs"], 2048, ent(layer, 3)["s"],
-                                            prologue=ops.PRO_SILU_MUL, residual=h1)
+            act = ops.w8a16_gate_up_silu_strips(h1, ent(layer, 2)["qs"], 12288, ent(layer, 2)["s"],
+                                                prologue=ops.PRO_RMS_NORM, norm_weight=w_post[layer], eps=eps)
+            h = ops.w8a16_fused_gemm_strips(act, ent(layer, 3)["qs"], 2048, ent(layer, 3)["s"], residual=h1)
             if layer + 1 < layers:
                 qkv = ops.w8a16_fused_gemm_strips(h, ent(layer + 1, 0)["qs"], 4096, ent(layer + 1, 0)["s"],
                                                   prologue=ops.PRO_RMS_NORM, norm_weight=w_in[layer + 1], eps=eps)

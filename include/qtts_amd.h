@@ -200,8 +200,8 @@ int qtts_rms_norm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
  *   residual: [m, n] of x_dtype, row stride ldr, or NULL; y = dtype(f32(residual) +
  *   f32(linear)), the linear rounded to x_dtype first, as `residual + o_proj(...)`
  *   (talker.py:270-271).  residual may be y itself (an in-place hidden-state update).
- * Fused into the GEMM launch (prologue computed while the activation row is staged,
- * residual added in the epilogue): SiLU and RMSNorm for m == 1 (RMSNorm without a
+ * Fused into the GEMM launch (prologue computed while the activation rows are staged,
+ * residual added in the epilogue): SiLU for m == 1, RMSNorm for m <= 8 (without a
  * residual and without split-K), the residual for m <= 8.  Otherwise the separate
  * kernels run around qtts_w8a16_gemm_strips, through the workspace.  SiLU and the
  * residual give the same bits either way; a fused RMSNorm sums its squares in another
@@ -212,6 +212,24 @@ int qtts_w8a16_fused_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t 
                                  const int8_t* qs, int64_t n, const void* scale, int scale_dtype,
                                  const void* bias, const void* residual, int64_t ldr, void* y,
                                  int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream);
+
+/* GatedMLP's gate_up_proj and activation (qtts/layers/activation.py:142-147), optionally
+ * after post_attention_layernorm (qtts/models/talker.py:271), on int8 strip weights:
+ *   h = x (QTTS_PRO_NONE) or qtts_rms_norm(x, norm_weight, eps) (QTTS_PRO_RMS_NORM),
+ *   g | u = w8a16_linear(h) (qs: the fused [n, k] gate_up weight, gate rows first),
+ *   act[r, c] = dtype(dtype(silu(g[r, c])) * u[r, c])   for c < n / 2
+ * with the rounding of qtts_w8a16_fused_gemm_strips followed by qtts_silu_mul.  Up to 8
+ * decode rows with n % 32 == 0 run as ONE launch (a workgroup holds gate strip s and up
+ * strip s + n/32 and writes the activation from its epilogue; the gate_up output is
+ * never stored); otherwise the prologue, the GEMM and qtts_silu_mul run in turn through
+ * the workspace.  No counterpart in the reference, which stores gate_up and runs the
+ * activation as two more kernels.  x: [m, k] bf16 / fp16, 16-byte aligned rows, k % 64 == 0.
+ * act: [m, n / 2], row stride ldact.  Workspace: qtts_workspace_bytes(QTTS_OP_W8A16_FUSED). */
+int qtts_w8a16_gate_up_silu_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                                   int prologue, const void* norm_weight, float eps,
+                                   const int8_t* qs, int64_t n, const void* scale, int scale_dtype,
+                                   const void* bias, void* act, int64_t ldact, int algo, void* ws,
+                                   int64_t ws_bytes, void* stream);
 
 /* --- a chain of dependent decode linears in one launch ------------------------------ */
 

@@ -51,6 +51,10 @@ int qtts_launch_w8a16_silu(const void* gu, int x_dtype, int64_t m, int64_t k, in
                            int64_t ws_bytes, hipStream_t st);
 int qtts_launch_rms_norm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const void* w, float eps,
                          void* y, int64_t ldy, hipStream_t st);
+int qtts_launch_w8a16_gate_up_silu(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int pro,
+                                   const void* nw, float eps, const int8_t* qs, int64_t n, const void* scale, int sdt,
+                                   const void* bias, void* act, int64_t ldact, int algo, void* ws, int64_t ws_bytes,
+                                   hipStream_t st);
 int64_t qtts_w8a16_fused_ws_bytes(int64_t m, int64_t n, int64_t k, int algo, int x_dtype);
 int qtts_launch_w8a16_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int pro, const void* nw,
                             float eps, const int8_t* qs, int64_t n, const void* scale, int sdt, const void* bias,
@@ -517,6 +521,32 @@ int qtts_w8a16_fused_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t 
   QTTS_TRY(current_device_check());
   return qtts_launch_w8a16_fused(x, x_dtype, m, k, ldx, prologue, norm_weight, eps, qs, n, scale, scale_dtype, bias,
                                  residual, ldr, y, ldy, algo, ws, ws_bytes, (hipStream_t)stream);
+}
+
+int qtts_w8a16_gate_up_silu_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int prologue,
+                                   const void* norm_weight, float eps, const int8_t* qs, int64_t n, const void* scale,
+                                   int scale_dtype, const void* bias, void* act, int64_t ldact, int algo, void* ws,
+                                   int64_t ws_bytes, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a16_gate_up_silu_strips: negative size");
+  QTTS_REQUIRE(m < 65536 && n < (1ll << 31) && k < (1ll << 30), "w8a16_gate_up_silu_strips: size too large");
+  QTTS_REQUIRE(x_dtype == QTTS_BF16 || x_dtype == QTTS_F16,
+               "w8a16_gate_up_silu_strips: activations must be bf16 or fp16");
+  QTTS_REQUIRE(dtype_ok(scale_dtype), "w8a16_gate_up_silu_strips: bad scale dtype code");
+  QTTS_REQUIRE(algo_ok(algo), "w8a16_gate_up_silu_strips: bad algo %d", algo);
+  QTTS_REQUIRE(prologue == QTTS_PRO_NONE || prologue == QTTS_PRO_RMS_NORM,
+               "w8a16_gate_up_silu_strips: prologue must be none or RMSNorm, got %d", prologue);
+  QTTS_REQUIRE(k % 64 == 0, "w8a16_gate_up_silu_strips: K %% 64 != 0 (K=%lld)", (long long)k);
+  QTTS_REQUIRE(n % 2 == 0, "w8a16_gate_up_silu_strips: gate_up width %lld is odd", (long long)n);
+  QTTS_REQUIRE(ldx >= k && ldact >= n / 2, "w8a16_gate_up_silu_strips: leading dimension smaller than the row");
+  QTTS_REQUIRE(ws_bytes >= 0, "w8a16_gate_up_silu_strips: negative workspace size");
+  if (m == 0 || n == 0) return QTTS_OK;
+  QTTS_REQUIRE(x && qs && scale && act && (prologue != QTTS_PRO_RMS_NORM || norm_weight),
+               "w8a16_gate_up_silu_strips: null pointer");
+  QTTS_REQUIRE((uintptr_t)x % 16 == 0 && (m == 1 || ldx % 8 == 0),
+               "w8a16_gate_up_silu_strips: activation rows must be 16-byte aligned");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_w8a16_gate_up_silu(x, x_dtype, m, k, ldx, prologue, norm_weight, eps, qs, n, scale, scale_dtype,
+                                        bias, act, ldact, algo, ws, ws_bytes, (hipStream_t)stream);
 }
 
 int qtts_fp8w_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n,

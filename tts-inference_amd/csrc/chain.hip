@@ -276,7 +276,7 @@ __device__ __forceinline__ void chain_item(const ChainArgs& a, const ChainLink& 
           }
         }
       }
-      ss = wave_sum(ss);
+      ss = wave_sum_rows(ss);
       if (lane == 0) nss[wave * 8 + m] = ss;
     }
     wait_lgkmcnt0();

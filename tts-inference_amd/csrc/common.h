@@ -253,6 +253,27 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// v + v of the lane DPP control CTRL names (a VALU operation, no LDS round trip).
+template <int CTRL> __device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes, uniform result, without the LDS permutes __shfl_xor compiles to:
+// within each row of 16 lanes by DPP (swap neighbours, swap pairs, mirror each half row,
+// mirror the row), then the four row sums read out lane by lane, ((r0 + r1) + (r2 + r3)).
+__device__ __forceinline__ float wave_sum_rows(float v) {
+  v = dpp_add<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v = dpp_add<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v = dpp_add<0x141>(v);  // row_half_mirror
+  v = dpp_add<0x140>(v);  // row_mirror
+  const int b = __builtin_bit_cast(int, v);
+  const float r0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0));
+  const float r1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16));
+  const float r2 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32));
+  const float r3 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
 }  // namespace qtts
 
 // ---- host-side error plumbing (abi.hip) -------------------------------------------------

@@ -47,17 +47,24 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 //   kProSiluMul: x is GatedMLP's fused gate_up output, [M, 2K] with row stride ldx, and
 //     the GEMM multiplies silu(gate) * up (gate = columns [0, K), up = [K, 2K);
 //     qtts/layers/activation.py:142-147);
-//   kProRmsNorm (one row, no split: S == 1): the GEMM multiplies RMSNorm(x) with
-//     weight aux and epsilon eps (qtts/layers/norm.py:50-76).  Each wave sums x^2 over
-//     its own K range, the workgroup adds the W partials in wave order behind one
-//     fence-free barrier (the weights stay in flight), and each wave normalizes its
-//     range as it stages it.
+//   kProRmsNorm (no split: S == 1): the GEMM multiplies RMSNorm(x) with weight aux
+//     and epsilon eps (qtts/layers/norm.py:50-76), row by row.  Each wave sums x^2 over
+//     its own K range, the workgroup adds the W partials of each row in wave order
+//     behind one fence-free barrier (the weights stay in flight), and each wave
+//     normalizes its range as it stages it.
 // RES (staged rows only): y = residual + the linear's output, the output rounded to
 // XT first, as `residual + linear(x)` computes it (qtts/models/talker.py:270-271).
+// PAIR (staged rows, no split): GatedMLP's gate_up_proj followed by its activation
+//   (qtts/layers/activation.py:142-147).  q holds the fused [N, K] gate_up weight
+//   (gate rows, then up rows); workgroup s runs gate strip s and up strip s + N/32:
+//   each wave loads both strips' chunks of its K range and feeds each staged B operand
+//   to two MFMAs, and the workgroup stores y[:, c] = XT(XT(silu(g)) * u) for g, u the
+//   linear's outputs of columns c and c + N/2 rounded to XT: y is [M, N/2].  The
+//   gate_up output itself is never stored.
 enum : int { kProNone = 0, kProSiluMul = 1, kProRmsNorm = 2 };
 
 template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1, int MX = 0, bool F8W = false,
-          int PRO = kProNone, bool RES = false>
+          int PRO = kProNone, bool RES = false, bool PAIR = false>
 __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ q, int N, int64_t ldq,
     const ST* scale, const XT* bias, XT* y, int64_t ldy,
@@ -68,11 +75,12 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   static_assert(MB == 1 || (FULLK && LAYOUT == kLayoutStrips), "several m-blocks need full-K strip weights");
   static_assert(MX == 0 || (MB == 1 && FULLK && LAYOUT == kLayoutStrips), "staged rows need one m-block, full K");
   static_assert(PRO == kProNone || MX > 0, "a prologue runs on staged rows");
-  static_assert(PRO != kProRmsNorm || MX == 1, "the norm prologue takes one row");
   static_assert(!RES || MX > 0, "the residual epilogue is built with staged rows");
+  static_assert(!PAIR || (MX > 0 && !RES && PRO != kProSiluMul), "the SiLU pair epilogue runs on staged rows");
   constexpr bool SILU = PRO == kProSiluMul, NORM = PRO == kProRmsNorm;
-  __shared__ f32x4_t red[W > 1 ? W - 1 : 1][MB][64];
-  __shared__ float nss[NORM ? W : 1];
+  constexpr int NA = PAIR ? 2 : 1;  // accumulators a wave carries: gate (and up)
+  __shared__ f32x4_t red[W > 1 ? W - 1 : 1][MB * NA][64];
+  __shared__ float nss[NORM ? W : 1][NORM ? MX : 1];
   __shared__ __align__(16) uint16_t xrow[MX > 0 ? W : 1][MX > 0 ? MX : 1][MX > 0 ? CPW * 64 : 8];
 
   int strip, split;
@@ -91,6 +99,8 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
 
   const int8_t* wp;
   int64_t wstride;
+  // PAIR: the up strip is strip + strips (strips = the gate strips, N/32).
+  const int64_t up_off = PAIR ? (int64_t)strips * nchunks * 1024 : 0;
   if constexpr (LAYOUT == kLayoutStrips) {
     wp = q + (int64_t)strip * nchunks * 1024 + lane * 16;
     wstride = 1024;
@@ -108,13 +118,14 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   // A group of CPW chunks is issued in full before any of it is consumed.  With
   // FULLK (K % 64 == 0, strip layout) the loads are branch-free: chunk indices past
   // the wave's range are clamped to its last chunk (consume zeroes their weights).
-  i32x4_t w[CPW], xa[MB][CPW], xb[MB][CPW];
+  i32x4_t w[CPW], wu[PAIR ? CPW : 1], xa[MB][CPW], xb[MB][CPW];
   auto issue = [&](int base) {
 #pragma unroll
     for (int u = 0; u < CPW; ++u) {
       if constexpr (FULLK) {
         const int c = min(base + u, wc1 - 1);
         w[u] = *(const i32x4_t*)(wp + (int64_t)c * wstride);
+        if constexpr (PAIR) wu[u] = *(const i32x4_t*)(wp + up_off + (int64_t)c * wstride);
         if constexpr (MX == 0) {
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) {
@@ -133,9 +144,10 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       }
     }
   };
-  f32x4_t acc[MB];
+  f32x4_t acc[MB], up[PAIR ? MB : 1];  // PAIR: up holds the up strip's sums
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (PAIR) up[0] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   auto consume = [&](int base) {
 #pragma unroll
     for (int u = 0; u < CPW; ++u) {
@@ -146,6 +158,16 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
         const i32x4_t wv = live ? w[u] : zero;
         const V wlo = wcvt<F8W, XT>((uint32_t)wv[0], (uint32_t)wv[1]);
         const V whi = wcvt<F8W, XT>((uint32_t)wv[2], (uint32_t)wv[3]);
+        if constexpr (PAIR) {  // the up strip's chunk on the same B operands, in the same order
+          const i32x4_t uv = live ? wu[u] : zero;
+          const V ulo = wcvt<F8W, XT>((uint32_t)uv[0], (uint32_t)uv[1]);
+          const V uhi = wcvt<F8W, XT>((uint32_t)uv[2], (uint32_t)uv[3]);
+          acc[0] = MM::mma(wlo, __builtin_bit_cast(V, xa[0][u]), acc[0]);
+          up[0] = MM::mma(ulo, __builtin_bit_cast(V, xa[0][u]), up[0]);
+          acc[0] = MM::mma(whi, __builtin_bit_cast(V, xb[0][u]), acc[0]);
+          up[0] = MM::mma(uhi, __builtin_bit_cast(V, xb[0][u]), up[0]);
+          continue;
+        }
 #pragma unroll
         for (int mb = 0; mb < MB; ++mb) acc[mb] = MM::mma(wlo, __builtin_bit_cast(V, xa[mb][u]), acc[mb]);
 #pragma unroll
@@ -161,6 +183,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   // Epilogue operands: raw bits, loaded unconditionally (clamped index; y stands in
   // for a missing bias), so nothing needs their values before the epilogue.
   uint32_t sc[4] = {0u, 0u, 0u, 0u}, bi[4] = {0u, 0u, 0u, 0u}, rb[RES ? 4 : 1] = {0u};
+  uint32_t su[PAIR ? 4 : 1] = {0u}, bu[PAIR ? 4 : 1] = {0u};  // PAIR: the up rows' scale and bias
   auto issue_epilogue = [&]() {
     const XT* bsrc = bias ? bias : y;
 #pragma unroll
@@ -169,6 +192,11 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       sc[i] = load_bits(scale + nn);
       bi[i] = load_bits(bsrc + nn);
       if constexpr (RES) rb[i] = load_bits(res + (int64_t)min(r, M - 1) * ldr + nn);
+      if constexpr (PAIR) {
+        const int nu = min(nn + (N >> 1), N - 1);
+        su[i] = load_bits(scale + nu);
+        bu[i] = load_bits(bsrc + nu);
+      }
     }
   };
 
@@ -176,8 +204,8 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   // 512 v + 8 l .. + 7 of the wave's K range of each row (XV vectors cover CPW
   // chunks); lanes past the range repeat its last 8 elements.
   constexpr int XV = (CPW * 64 + 511) / 512;
-  // SILU: xu holds the up half; NORM: xu holds the norm weight over the same range.
-  i32x4_t xr[MX > 0 ? MX : 1][XV], xu[SILU || NORM ? MX : 1][SILU || NORM ? XV : 1];
+  // SILU: xu holds the up half; NORM: xu[0] holds the norm weight over the same range.
+  i32x4_t xr[MX > 0 ? MX : 1][XV], xu[SILU ? MX : 1][SILU || NORM ? XV : 1];
   auto issue_x = [&]() {
     if constexpr (MX > 0) {
 #pragma unroll
@@ -188,45 +216,50 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
           const XT* row = x + (int64_t)min(m, M - 1) * ldx + (int64_t)wc0 * 64 + e;
           xr[m][v] = *(const i32x4_t*)row;
           if constexpr (SILU) xu[m][v] = *(const i32x4_t*)(row + K);
-          if constexpr (NORM) xu[m][v] = *(const i32x4_t*)(aux + (int64_t)wc0 * 64 + e);
+          if constexpr (NORM) {
+            if (m == 0) xu[0][v] = *(const i32x4_t*)(aux + (int64_t)wc0 * 64 + e);
+          }
         }
       }
     }
   };
-  // NORM, before the barrier: this wave's sum of x^2 over its range (fp32, lane
-  // partials over its vectors in element order, then the wave's butterfly).
-  auto norm_partial = [&]() {
+  // NORM, before the barrier: this wave's sum of x^2 over its range for row m (fp32,
+  // lane partials over its vectors in element order, then the wave's butterfly).
+  auto norm_partial = [&](int m) {
     float ss = 0.0f;
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
       if (512 * v + 8 * lane < (wc1 - wc0) * 64) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t p = (uint32_t)xr[0][v][e];
+          const uint32_t p = (uint32_t)xr[m][v][e];
           const float a = to_f32(XT{(uint16_t)p}), b = to_f32(XT{(uint16_t)(p >> 16)});
           ss = __builtin_fmaf(a, a, ss);
           ss = __builtin_fmaf(b, b, ss);
         }
       }
     }
-    return wave_sum(ss);
+    return wave_sum_rows(ss);
   };
   // Writes the wave's staged rows to LDS (NORM: x * inv * weight, rounded to XT as
   // the reference's fused norm stores it) and reads the MFMA B operands back.
-  auto stage_x = [&](float inv) {
+  auto stage_x = [&](const float* inv) {
     if constexpr (NORM) {
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
         const int e = min(512 * v + 8 * lane, (wc1 - wc0) * 64 - 8);
-        i32x4_t o;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t p = (uint32_t)xr[0][v][i], w2 = (uint32_t)xu[0][v][i];
-          const float h0 = (to_f32(XT{(uint16_t)p}) * inv) * to_f32(XT{(uint16_t)w2});
-          const float h1 = (to_f32(XT{(uint16_t)(p >> 16)}) * inv) * to_f32(XT{(uint16_t)(w2 >> 16)});
-          o[i] = (int)pack2_f32<XT>(h0, h1);
+        for (int m = 0; m < MX; ++m) {
+          i32x4_t o;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t p = (uint32_t)xr[m][v][i], w2 = (uint32_t)xu[0][v][i];
+            const float h0 = (to_f32(XT{(uint16_t)p}) * inv[m]) * to_f32(XT{(uint16_t)w2});
+            const float h1 = (to_f32(XT{(uint16_t)(p >> 16)}) * inv[m]) * to_f32(XT{(uint16_t)(w2 >> 16)});
+            o[i] = (int)pack2_f32<XT>(h0, h1);
+          }
+          *(i32x4_t*)&xrow[wave][m][e] = o;
         }
-        *(i32x4_t*)&xrow[wave][0][e] = o;
       }
     } else if constexpr (MX > 0) {
 #pragma unroll
@@ -266,26 +299,40 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     // be in flight before the first wait.
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (NORM) {
-      const float ss = norm_partial();  // waits for the activation row only
-      if (lane == 0) nss[wave] = ss;
+#pragma unroll
+      for (int m = 0; m < MX; ++m) {  // waits for the activation rows only
+        const float ss = norm_partial(m);
+        if (lane == 0) nss[wave][m] = ss;
+      }
     } else {
-      stage_x(0.0f);  // waits for the activation rows only; the weights stay in flight
+      stage_x(nullptr);  // waits for the activation rows only; the weights stay in flight
       consume(wc0);
     }
   } else {
     issue_epilogue();
     if constexpr (NORM) {
-      if (lane == 0) nss[wave] = 0.0f;
+      if (lane == 0)
+#pragma unroll
+        for (int m = 0; m < MX; ++m) nss[wave][m] = 0.0f;
     }
   }
   if constexpr (NORM) {
-    // variance = sum / K; inv = 1 / sqrt(variance + eps), both correctly rounded.
+    // variance = sum / K; inv = 1 / sqrt(variance + eps), both correctly rounded; lane m
+    // computes row m's (the wave partials added in wave order), every lane reads them.
     wait_lgkmcnt0();
     barrier_only();
-    float ss = 0.0f;
+    float mine;
+    {
+      const int mr = lane < MX ? lane : 0;
+      float ss = 0.0f;
 #pragma unroll
-    for (int w = 0; w < W; ++w) ss += nss[w];
-    const float inv = 1.0f / __builtin_sqrtf(ss / (float)K + eps);
+      for (int w = 0; w < W; ++w) ss += nss[w][mr];
+      mine = 1.0f / __builtin_sqrtf(ss / (float)K + eps);
+    }
+    float inv[MX];
+#pragma unroll
+    for (int m = 0; m < MX; ++m)
+      inv[m] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), m));
     if (wc0 < wc1) {
       stage_x(inv);
       consume(wc0);
@@ -296,13 +343,16 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     if (wave > 0) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) red[wave - 1][mb][lane] = acc[mb];
+      if constexpr (PAIR) red[wave - 1][1][lane] = up[0];
     }
     __syncthreads();
     if (wave > 0) return;
 #pragma unroll
-    for (int w = 0; w < W - 1; ++w)
+    for (int w = 0; w < W - 1; ++w) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) acc[mb] += red[w][mb][lane];
+      if constexpr (PAIR) up[0] += red[w][1][lane];
+    }
   }
 
   if (S > 1) {
@@ -328,10 +378,15 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int nn = strip * 16 + 4 * g + i;
-        if (nn < N) {
+        if (nn < (PAIR ? N >> 1 : N)) {
           float v = acc[mb][i] * bits_to_f32<ST>(sc[i]);
           if (bias) v += bits_to_f32<XT>(bi[i]);
           if constexpr (RES) v = bits_to_f32<XT>(rb[i]) + round_through<XT>(v);
+          if constexpr (PAIR) {
+            float u = up[0][i] * bits_to_f32<ST>(su[i]);
+            if (bias) u += bits_to_f32<XT>(bu[i]);
+            v = silu_mul<XT>(round_through<XT>(v), round_through<XT>(u));
+          }
           y[(int64_t)m * ldy + nn] = from_f32<XT>(v);
         }
       }

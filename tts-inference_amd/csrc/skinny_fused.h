@@ -27,9 +27,9 @@ struct FusedArgs {
   hipStream_t st;
 };
 
-template <typename XT, typename ST, int W, int CPW, int MX, int PRO, bool RES>
+template <typename XT, typename ST, int W, int CPW, int MX, int PRO, bool RES, bool PAIR = false>
 void launch_fused_one(const FusedArgs& a) {
-  launch(&w8a16_skinny_kernel<XT, ST, W, CPW, kLayoutStrips, true, 1, MX, false, PRO, RES>, dim3(a.blocks),
+  launch(&w8a16_skinny_kernel<XT, ST, W, CPW, kLayoutStrips, true, 1, MX, false, PRO, RES, PAIR>, dim3(a.blocks),
          dim3(W * 64), 0, a.st, (const XT*)a.x, (int)a.m, (int)a.k, a.ldx, a.qs, (int)a.n, (int64_t)0,
          (const ST*)a.scale, (const XT*)a.bias, (XT*)a.y, a.ldy, a.part, a.counters, a.c.strips, a.c.S, a.c.cps,
          (const XT*)a.aux, a.eps, (const XT*)a.res, a.ldr);
@@ -50,18 +50,60 @@ int launch_fused_wc(const FusedArgs& a) {
   return 0;
 }
 
+// The SiLU-pair variants (PAIR): each wave carries both strips' chunks.  Built: 2, 4,
+// 8 and 16 waves of 4 chunks (the automatic choice: as many waves as the plain GEMM
+// of the same K would run, each with half its chunks, so the same weight bytes per
+// wave), and 1, 2, 4 and 8 waves of 8 chunks.
+template <typename XT, typename ST, int MX, int PRO>
+int launch_pair_wc(const FusedArgs& a) {
+  switch (a.c.waves * 64 + a.c.cpw) {
+    case 2 * 64 + 4: launch_fused_one<XT, ST, 2, 4, MX, PRO, false, true>(a); break;
+    case 4 * 64 + 4: launch_fused_one<XT, ST, 4, 4, MX, PRO, false, true>(a); break;
+    case 8 * 64 + 4: launch_fused_one<XT, ST, 8, 4, MX, PRO, false, true>(a); break;
+    case 16 * 64 + 4: launch_fused_one<XT, ST, 16, 4, MX, PRO, false, true>(a); break;
+    case 1 * 64 + 8: launch_fused_one<XT, ST, 1, 8, MX, PRO, false, true>(a); break;
+    case 2 * 64 + 8: launch_fused_one<XT, ST, 2, 8, MX, PRO, false, true>(a); break;
+    case 4 * 64 + 8: launch_fused_one<XT, ST, 4, 8, MX, PRO, false, true>(a); break;
+    case 8 * 64 + 8: launch_fused_one<XT, ST, 8, 8, MX, PRO, false, true>(a); break;
+    default: return 1;
+  }
+  return 0;
+}
+inline bool pair_built(int waves, int cpw) {
+  return (cpw == 4 && (waves == 2 || waves == 4 || waves == 8 || waves == 16)) ||
+         (cpw == 8 && (waves == 1 || waves == 2 || waves == 4 || waves == 8));
+}
+
 // Returns 0 after a launch, 1 when the combination is not built.  Scales are either
 // of the activation dtype (Int8WeightOnlyMethod) or fp32.
-template <int PRO, bool RES, int MX>
+template <int PRO, bool RES, int MX, bool PAIR = false>
 int launch_fused(int x_dtype, bool f32_scale, const FusedArgs& a) {
-  if (x_dtype == QTTS_BF16)
-    return f32_scale ? launch_fused_wc<bf16_t, float, MX, PRO, RES>(a) : launch_fused_wc<bf16_t, bf16_t, MX, PRO, RES>(a);
-  return f32_scale ? launch_fused_wc<f16_t, float, MX, PRO, RES>(a) : launch_fused_wc<f16_t, f16_t, MX, PRO, RES>(a);
+  if constexpr (PAIR) {
+    if (x_dtype == QTTS_BF16)
+      return f32_scale ? launch_pair_wc<bf16_t, float, MX, PRO>(a) : launch_pair_wc<bf16_t, bf16_t, MX, PRO>(a);
+    return f32_scale ? launch_pair_wc<f16_t, float, MX, PRO>(a) : launch_pair_wc<f16_t, f16_t, MX, PRO>(a);
+  } else {
+    if (x_dtype == QTTS_BF16)
+      return f32_scale ? launch_fused_wc<bf16_t, float, MX, PRO, RES>(a)
+                       : launch_fused_wc<bf16_t, bf16_t, MX, PRO, RES>(a);
+    return f32_scale ? launch_fused_wc<f16_t, float, MX, PRO, RES>(a) : launch_fused_wc<f16_t, f16_t, MX, PRO, RES>(a);
+  }
 }
 
 // Residual-only variants (w8a16_fused_res.hip) for 1, 4 and 8 staged rows.
 extern template int launch_fused<kProNone, true, 1>(int, bool, const FusedArgs&);
 extern template int launch_fused<kProNone, true, 4>(int, bool, const FusedArgs&);
 extern template int launch_fused<kProNone, true, 8>(int, bool, const FusedArgs&);
+// RMSNorm prologue for 4 and 8 staged rows (w8a16_fused_norm.hip).
+extern template int launch_fused<kProRmsNorm, false, 4>(int, bool, const FusedArgs&);
+extern template int launch_fused<kProRmsNorm, false, 8>(int, bool, const FusedArgs&);
+// SiLU-pair gate_up, with or without the RMSNorm prologue (w8a16_fused_pair.hip,
+// w8a16_fused_pair_norm.hip).
+extern template int launch_fused<kProNone, false, 1, true>(int, bool, const FusedArgs&);
+extern template int launch_fused<kProNone, false, 4, true>(int, bool, const FusedArgs&);
+extern template int launch_fused<kProNone, false, 8, true>(int, bool, const FusedArgs&);
+extern template int launch_fused<kProRmsNorm, false, 1, true>(int, bool, const FusedArgs&);
+extern template int launch_fused<kProRmsNorm, false, 4, true>(int, bool, const FusedArgs&);
+extern template int launch_fused<kProRmsNorm, false, 8, true>(int, bool, const FusedArgs&);
 
 }  // namespace qtts

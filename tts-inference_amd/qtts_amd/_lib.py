@@ -73,6 +73,7 @@ EXPORTS = (
     "qtts_w8a16_silu_mul_gemm_strips",
     "qtts_rms_norm",
     "qtts_w8a16_fused_gemm_strips",
+    "qtts_w8a16_gate_up_silu_strips",
     "qtts_w8a16_chain_ctl_bytes",
     "qtts_w8a16_chain_strips",
     "qtts_kernel_timer_begin",
@@ -189,6 +190,9 @@ def load() -> ctypes.CDLL:
         L.qtts_w8a16_chain_ctl_bytes.argtypes = [ctypes.POINTER(ChainLinkC), i32, i64]
         L.qtts_w8a16_chain_strips.restype = i32
         L.qtts_w8a16_chain_strips.argtypes = [ctypes.POINTER(ChainLinkC), i32, i32, i32, i64, i32, p, i64, p]
+        L.qtts_w8a16_gate_up_silu_strips.restype = i32
+        L.qtts_w8a16_gate_up_silu_strips.argtypes = [p, i32, i64, i64, i64, i32, p, ctypes.c_float, p, i64, p, i32,
+                                                     p, p, i64, i32, p, i64, p]
         L.qtts_kernel_timer_begin.restype = i32
         L.qtts_kernel_timer_begin.argtypes = [i32]
         L.qtts_kernel_timer_end.restype = i32

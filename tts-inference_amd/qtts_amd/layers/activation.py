@@ -1,12 +1,14 @@
-"""GatedMLP whose activation can run inside the down projection (qtts/layers/activation.py:121-147).
+"""GatedMLP whose activation runs inside its GEMMs (qtts/layers/activation.py:121-147).
 
 Same constructor and forward contract as the reference's ``GatedMLP``: ``gate_up_proj``
 (a ``MergedLinear`` of [intermediate, intermediate], gate first) or ``gate_proj`` /
-``up_proj``, then ``down_proj(F.silu(gate) * up)``.  When ``down_proj``'s quant method
-has ``apply_silu_mul`` (the int8 weight-only method), the fused gate_up output goes to
-it whole: a single decode row has ``silu(gate) * up`` computed inside the down GEMM
-kernel, other calls one activation kernel, with torch's rounding either way.  Any other down
-projection gets ``F.silu(gate) * up`` first, exactly as the reference computes it.
+``up_proj``, then ``down_proj(F.silu(gate) * up)``.  When ``gate_up_proj``'s quant method
+has ``apply_gate_up_silu`` (the int8 weight-only method), it returns ``silu(gate) * up``
+itself: decode rows get it from the gate_up GEMM's epilogue, which never stores the
+gate_up output.  Otherwise, when ``down_proj``'s quant method has ``apply_silu_mul``, the
+fused gate_up output goes to it whole (a single decode row has the activation computed
+inside the down GEMM).  Torch's rounding either way.  Any other MLP gets
+``F.silu(gate) * up`` first, exactly as the reference computes it.
 
 ``fuse_gated_mlps(model)`` gives the reference's own ``GatedMLP`` instances (anything
 with ``gate_up_proj``, ``down_proj`` and ``fuse``) this forward, so a model built from
@@ -25,9 +27,15 @@ from .linear import LinearBase, MergedLinear
 
 
 def gated_mlp_forward(mlp: nn.Module, x: torch.Tensor) -> torch.Tensor:
-    """The forward of GatedMLP (activation.py:142-147), with the activation handed to the down
-    projection's quant method when it can fuse it."""
+    """The forward of GatedMLP (activation.py:142-147): the activation computed by gate_up_proj's
+    quant method when it can (from the GEMM's epilogue), else handed to the down projection's."""
     if mlp.fuse:
+        up_method = getattr(mlp.gate_up_proj, "quant_method", None)
+        pair = getattr(up_method, "apply_gate_up_silu", None)
+        if pair is not None:
+            act = pair(mlp.gate_up_proj, x, mlp.gate_up_proj.bias)
+            if act is not None:
+                return mlp.down_proj(act)
         gate_up = mlp.gate_up_proj(x)
         method = getattr(mlp.down_proj, "quant_method", None)
         fused = getattr(method, "apply_silu_mul", None)

@@ -680,6 +680,46 @@ def w8a16_fused_gemm_strips(x: torch.Tensor, qs: torch.Tensor, n: int, scale: to
     return y.reshape(*shape[:-1], n)
 
 
+def w8a16_gate_up_silu_strips(x: torch.Tensor, qs: torch.Tensor, n: int, scale: torch.Tensor,
+                              bias: torch.Tensor | None = None, *, prologue: int = PRO_NONE,
+                              norm_weight: torch.Tensor | None = None, eps: float = 1e-6,
+                              algo: int = ALGO_AUTO) -> torch.Tensor:
+    """``F.silu(gate) * up`` of GatedMLP's fused ``gate_up_proj(prologue(x))`` (qtts/layers/activation.py:
+    142-147) on an int8 strip-layout ``[n, K]`` gate_up weight; returns ``[..., n // 2]``.  Up to 8
+    rows run as one kernel with the activation in the GEMM's epilogue (the gate_up output is never
+    stored).  ``prologue``: PRO_NONE or PRO_RMS_NORM (with ``norm_weight`` and ``eps``)."""
+    shape = x.shape
+    a = _flatten(x)
+    rows, k = a.shape
+    if n % 2:
+        raise ValueError(f"gate_up width {n} is odd")
+    if qs.dtype != torch.int8 or qs.numel() != strip_bytes(n, k, STRIP_INT8):
+        raise ValueError(f"weight is not an int8 strip-layout [{n}, {k}] buffer")
+    if scale.numel() != n:
+        raise ValueError(f"scale has {scale.numel()} entries for {n} output channels")
+    if bias is not None:
+        if bias.numel() != n:
+            raise ValueError(f"bias has {bias.numel()} entries for {n} output channels")
+        bias = bias.to(a.dtype).contiguous()
+    if prologue == PRO_RMS_NORM:
+        if norm_weight is None or norm_weight.numel() != k:
+            raise ValueError(f"RMSNorm prologue needs a norm weight of {k} entries")
+        norm_weight = norm_weight.to(a.dtype).contiguous()
+    if a.data_ptr() % 16 or (rows > 1 and a.stride(0) % 8):
+        a = a.contiguous() if a.data_ptr() % 16 == 0 else a.clone()
+    dev = _require_cuda(a, qs, scale, bias, norm_weight)
+    scale = scale.contiguous()
+    act = torch.empty((rows, n // 2), dtype=a.dtype, device=dev)
+    reserve_workspace(dev, workspace_bytes(OP_W8A16_FUSED, rows, n, k, algo))
+    ws, ws_n = _ws_for(dev)
+    st = _lib.load().qtts_w8a16_gate_up_silu_strips(
+        _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else k, int(prologue), _ptr(norm_weight),
+        float(eps), _ptr(qs), n, _ptr(scale), dtype_code(scale.dtype), _ptr(bias), _ptr(act), n // 2, algo, ws, ws_n,
+        _stream(dev))
+    _lib.check(st, "w8a16_gate_up_silu_strips")
+    return act.reshape(*shape[:-1], n // 2)
+
+
 @dataclasses.dataclass
 class ChainLink:
     """One int8 weight-only linear of a chain (``w8a16_chain``): ``out = epilogue(linear(prologue(x)))``.

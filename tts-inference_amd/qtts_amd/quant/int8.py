@@ -161,6 +161,19 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             return ops.w8a16_gemm(x, int8_weight_rowmajor(layer), layer.int8_scale, bias)
         return ops.w8a16_gemm(x, layer.int8_weight, layer.int8_scale, bias, algo)
 
+    def apply_gate_up_silu(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor | None:
+        """``F.silu(gate) * up`` of this fused gate_up layer's output (qtts/layers/activation.py:142-147)
+        in one call; on strip weights with 16-bit activations, decode rows get the activation from
+        the GEMM's epilogue.  None when this layer cannot (the caller then runs the plain path)."""
+        if layer.int8_layout != "strips" or x.dtype not in (torch.bfloat16, torch.float16):
+            return None
+        n, k = layer.out_features, layer.in_features
+        if n % 2:
+            return None
+        rows = x.numel() // k if k else 0
+        algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
+        return ops.w8a16_gate_up_silu_strips(x, layer.int8_weight, n, layer.int8_scale, bias, algo=algo)
+
     def apply_silu_mul(self, layer, gate_up: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
         """``layer(F.silu(gate) * up)`` from GatedMLP's fused gate_up output (qtts/layers/activation.py:
         142-147): on strip weights one call, with the activation inside the GEMM for a single row."""
