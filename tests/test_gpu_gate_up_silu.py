@@ -167,3 +167,59 @@ def test_gate_up_silu_errors(ops):
         ops.w8a16_gate_up_silu_strips(x, qs, n, s, prologue=ops.PRO_RMS_NORM)  # no norm weight
     empty = ops.w8a16_gate_up_silu_strips(x[:0], qs, n, s)
     assert empty.shape == (0, n // 2)
+
+
+def test_decoder_helpers_fuse_int8_layers(ops, monkeypatch):
+    """qtts_amd.layers.decoder on int8 weight-only layers: norm + qkv, o + residual, and norm + MLP +
+    residual each run as fused launches (two for the MLP) and agree with the reference's composition
+    within the W8A16 bound, stage by stage."""
+    from torch import nn
+
+    from qtts_amd.layers import GatedMLP, LinearBase
+    from qtts_amd.layers.decoder import linear_residual, norm_linear, norm_mlp_residual
+    from qtts_amd.quant.int8 import Int8WeightOnlyMethod
+
+    class Norm(nn.Module):
+        def __init__(self, n):
+            super().__init__()
+            self.weight = nn.Parameter((1 + 0.1 * torch.randn(n, device="cuda")).to(torch.bfloat16),
+                                       requires_grad=False)
+            self.eps = 1e-6
+
+        def forward(self, x):
+            return ops.rms_norm(x, self.weight, self.eps)
+
+    calls = {"fused": 0, "pair": 0}
+    real_fused, real_pair = ops.w8a16_fused_gemm_strips, ops.w8a16_gate_up_silu_strips
+    monkeypatch.setattr(ops, "w8a16_fused_gemm_strips",
+                        lambda *a, **k: calls.__setitem__("fused", calls["fused"] + 1) or real_fused(*a, **k))
+    monkeypatch.setattr(ops, "w8a16_gate_up_silu_strips",
+                        lambda *a, **k: calls.__setitem__("pair", calls["pair"] + 1) or real_pair(*a, **k))
+    torch.manual_seed(1)
+    method = Int8WeightOnlyMethod(calibrate=False)
+    qkv = LinearBase(2048, 4096, dtype=torch.bfloat16, device="cuda")
+    o = LinearBase(2048, 2048, dtype=torch.bfloat16, device="cuda")
+    mlp = GatedMLP(2048, 6144, dtype=torch.bfloat16, device="cuda")
+    with torch.no_grad():
+        for mod in (qkv, o, mlp):
+            for p in mod.parameters():
+                p.normal_(0.0, 0.02)
+    for lin in (qkv, o, mlp.gate_up_proj, mlp.down_proj):
+        method.process_weights(lin)
+        lin.quant_method = method
+    n_in, n_post = Norm(2048), Norm(2048)
+
+    def check(got, want, what):
+        ref = want.double().cpu().numpy()
+        err = np.abs(got.double().cpu().numpy() - ref)
+        assert (err <= 2 * _bound(ref, torch.bfloat16)).all(), f"{what}: max err {err.max():.3g}"
+
+    for m in (1, 4, 8):
+        h = (torch.randn(m, 1, 2048, device="cuda") * 2).to(torch.bfloat16)
+        attn = torch.randn(m, 1, 2048, device="cuda").to(torch.bfloat16)
+        check(norm_linear(n_in, qkv, h), qkv(n_in(h)), f"m={m} norm+qkv")
+        h1 = linear_residual(o, attn, h)
+        check(h1, h + o(attn), f"m={m} o+residual")
+        gate, up = mlp.gate_up_proj.split(mlp.gate_up_proj(n_post(h1)))
+        check(norm_mlp_residual(n_post, mlp, h1), h1 + mlp.down_proj(F.silu(gate) * up), f"m={m} mlp")
+    assert calls == {"fused": 9, "pair": 3}, calls
