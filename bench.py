@@ -221,6 +221,7 @@ def run_talker_stack(args, torch, ops):
         ops.workspace_bytes(ops.OP_W8A16, m, e["n"], e["k"]) for m in ms for e in stack[:4]))
     xs = make_inputs(torch, [k for _, _, k in TALKER], ms)
     int8_bytes = sum(e["n"] * e["k"] for e in stack)
+    flows, _ = layer_flows(torch, ops, stack, layers)
 
     per_m = {}
     total_bytes = 0
@@ -242,7 +243,18 @@ def run_talker_stack(args, torch, ops):
             "bf16_hipblaslt_stack_us": round(t_b * 1e3, 2),
             "speedup_vs_bf16": round(t_b / t_q, 3),
         }
-        del g_q, g_b
+        # The same weights in the decode step's data flow: norms, SiLU and residual adds fused
+        # into the GEMMs, against bf16 torch doing the same.
+        attn = xs[(m, 2048)]
+        h_in = make_inputs(torch, [2048], [m])[(m, 2048)] * 2
+        g_f = capture(torch, lambda: flows["fused"](h_in, attn))
+        g_fb = capture(torch, lambda: flows["bf16"](h_in, attn))
+        t_f = time_graph(torch, g_f, args.steps, args.warmup)
+        t_fb = time_graph(torch, g_fb, max(5, args.steps // 2), args.warmup)
+        per_m[str(m)]["layer_flow_fused_us"] = round(t_f * 1e3, 2)
+        per_m[str(m)]["layer_flow_bf16_torch_us"] = round(t_fb * 1e3, 2)
+        per_m[str(m)]["layer_flow_speedup_vs_bf16"] = round(t_fb / t_f, 3)
+        del g_q, g_b, g_f, g_fb
         log(f"[bench] M={m}: {per_m[str(m)]}")
 
     # Dominant kernel: gate_up, the largest share of the stack.  Its mean device duration over
@@ -276,7 +288,11 @@ def run_talker_stack(args, torch, ops):
         "data": "synthetic (seeded N(0,0.02) weights per layer, N(0,1) bf16 activations)",
         "config": {"workload": "configs[1]: talker decode linear stack, 28 layers x {qkv,o,gate_up,down}, "
                                "int8 weight-only, one HIP graph per M", "layers": layers, "M": list(ms),
-                   "int8_weight_bytes": int8_bytes, "parallelism": "none (1 GPU)"},
+                   "int8_weight_bytes": int8_bytes, "parallelism": "none (1 GPU)",
+                   "layer_flow": "per_m.layer_flow_*: the same 28 layers in the decode step's data flow "
+                                 "(RMSNorm+qkv, o+residual, RMSNorm+gate_up+SiLU, down+residual fused into the "
+                                 "int8 GEMMs) against bf16 torch (hipBLASLt F.linear, F.rms_norm, F.silu, adds); "
+                                 "o_proj reads a fixed synthetic attention output"},
         "per_m": per_m,
         "roofline": roofline,
     }
@@ -508,29 +524,18 @@ def make_chain_inputs(torch, ops, stack, layers, m, attn, norms):
     return h_in, launches
 
 
-def run_talker_chain(args, torch, ops):
-    """The talker decode step's linears with their real data flow, int8 weight-only, 28 layers,
-    M in {1, 2, 4, 8}, three ways: one fused kernel per linear (input_layernorm + qkv_proj,
-    o_proj + residual, post_attention_layernorm + gate_up_proj + SiLU * mul, down_proj +
-    residual: qtts_w8a16_fused_gemm_strips and qtts_w8a16_gate_up_silu_strips), one persistent
-    chain launch per layer (qtts_w8a16_chain_strips), and bf16 torch (hipBLASLt F.linear,
-    F.rms_norm, F.silu, adds).  The attention between qkv_proj and o_proj is not part of the
-    path; o_proj reads a fixed synthetic attention output."""
+def layer_flows(torch, ops, stack, layers, eps=1e-6):
+    """The talker decode step's linears with their data flow (qtts/models/talker.py:246-271) as
+    callables of (h_in, attn): one fused kernel per linear (input_layernorm + qkv_proj, o_proj +
+    residual, post_attention_layernorm + gate_up_proj + SiLU * mul, down_proj + residual), and
+    bf16 torch (hipBLASLt F.linear, F.rms_norm, F.silu, adds).  Returns (flows, norm weights)."""
     import torch.nn.functional as F
-    ms = (1, 2, 4, 8)
-    layers = 28
-    eps = 1e-6
-    log(f"[bench] packing {layers}x4 talker weights (int8 + bf16 baseline copy)")
-    stack = make_stack(torch, ops, TALKER, layers, keep_bf16=True)
-    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
     g = torch.Generator(device="cuda").manual_seed(5)
     w_in = [(1 + 0.1 * torch.randn(2048, generator=g, device="cuda")).to(torch.bfloat16) for _ in range(layers)]
     w_post = [(1 + 0.1 * torch.randn(2048, generator=g, device="cuda")).to(torch.bfloat16) for _ in range(layers)]
-    xs = make_inputs(torch, [2048], ms)
-    ent = lambda layer, i: stack[4 * layer + i]  # noqa: E731
-    nbytes_of = {m: sum(w8a16_bytes(m, e["n"], e["k"]) for e in stack) for m in ms}
+    ent = lambda layer, i: stack[4 * layer + i]  # noqa: E731  (qkv, o, gate_up, down)
 
-    def per_linear(h_in, attn):
+    def fused(h_in, attn):
         qkv = ops.w8a16_fused_gemm_strips(h_in, ent(0, 0)["qs"], 4096, ent(0, 0)["s"], prologue=ops.PRO_RMS_NORM,
                                           norm_weight=w_in[0], eps=eps)
         h = h_in
@@ -556,6 +561,26 @@ def run_talker_chain(args, torch, ops):
                 qkv = F.linear(F.rms_norm(h, (2048,), w_in[layer + 1], eps), ent(layer + 1, 0)["w_bf16"])
         return h, qkv
 
+    return {"fused": fused, "bf16": bf16}, (w_in, w_post)
+
+
+def run_talker_chain(args, torch, ops):
+    """The talker decode step's linears with their real data flow, int8 weight-only, 28 layers,
+    M in {1, 2, 4, 8}, three ways: one fused kernel per linear (input_layernorm + qkv_proj,
+    o_proj + residual, post_attention_layernorm + gate_up_proj + SiLU * mul, down_proj +
+    residual: qtts_w8a16_fused_gemm_strips and qtts_w8a16_gate_up_silu_strips), one persistent
+    chain launch per layer (qtts_w8a16_chain_strips), and bf16 torch (hipBLASLt F.linear,
+    F.rms_norm, F.silu, adds).  The attention between qkv_proj and o_proj is not part of the
+    path; o_proj reads a fixed synthetic attention output."""
+    ms = (1, 2, 4, 8)
+    layers = 28
+    log(f"[bench] packing {layers}x4 talker weights (int8 + bf16 baseline copy)")
+    stack = make_stack(torch, ops, TALKER, layers, keep_bf16=True)
+    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    flows, (w_in, w_post) = layer_flows(torch, ops, stack, layers)
+    xs = make_inputs(torch, [2048], ms)
+    nbytes_of = {m: sum(w8a16_bytes(m, e["n"], e["k"]) for e in stack) for m in ms}
+
     per_m = {}
     total_bytes, total_ms = 0, 0.0
     layer_bytes, layer_ms = [], []
@@ -564,8 +589,8 @@ def run_talker_chain(args, torch, ops):
         h_in, launches = make_chain_inputs(torch, ops, stack, layers, m, attn, (w_in, w_post))
         plans = [ops.ChainPlan(links) for links in launches]
         g_c = capture(torch, lambda: [plan() for plan in plans])
-        g_p = capture(torch, lambda: per_linear(h_in, attn))
-        g_b = capture(torch, lambda: bf16(h_in, attn))
+        g_p = capture(torch, lambda: flows["fused"](h_in, attn))
+        g_b = capture(torch, lambda: flows["bf16"](h_in, attn))
         t_c = time_graph(torch, g_c, args.steps, args.warmup)
         t_p = time_graph(torch, g_p, args.steps, args.warmup)
         t_b = time_graph(torch, g_b, max(5, args.steps // 2), args.warmup)

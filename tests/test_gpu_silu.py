@@ -119,8 +119,10 @@ def test_silu_down_graph_replays(ops):
 
 
 def test_gated_mlp_fused_forward(ops):
-    """GatedMLP with int8 weight-only projections: the fused forward equals the reference's
-    composition down_proj(F.silu(gate) * up) on the same quantized layers, at decode and prefill rows."""
+    """GatedMLP with int8 weight-only projections against the reference's composition
+    down_proj(F.silu(gate) * up) on the same quantized layers: within the W8A16 bound at decode
+    rows (gate_up's fused launch splits K over other waves than the plain GEMM), bit for bit at
+    prefill rows (the activation then runs as its own kernel)."""
     from qtts_amd import QuantConfig, apply_quantization
     from qtts_amd.layers import GatedMLP, gated_mlp_forward
     torch.manual_seed(0)
@@ -137,7 +139,7 @@ def test_gated_mlp_fused_forward(ops):
         gate, up = mlp.gate_up_proj.split(mlp.gate_up_proj(x))
         assert torch.equal(fused, gated_mlp_forward(mlp, x))
         composed = mlp.down_proj(F.silu(gate) * up)
-        if m > 1:
+        if m > 8:
             assert torch.equal(fused, composed), f"m={m}"
         else:
             assert_close(fused, composed.double().cpu().numpy(), f"m={m}")
