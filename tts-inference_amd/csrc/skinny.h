@@ -48,10 +48,14 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 //     the GEMM multiplies silu(gate) * up (gate = columns [0, K), up = [K, 2K);
 //     qtts/layers/activation.py:142-147);
 //   kProRmsNorm (no split: S == 1): the GEMM multiplies RMSNorm(x) with weight aux
-//     and epsilon eps (qtts/layers/norm.py:50-76), row by row.  Each wave sums x^2 over
-//     its own K range, the workgroup adds the W partials of each row in wave order
-//     behind one fence-free barrier (the weights stay in flight), and each wave
-//     normalizes its range as it stages it.
+//     and epsilon eps (qtts/layers/norm.py:50-76), row by row.  The row's inverse RMS is
+//     a scalar per activation row, i.e. per column of the MFMA result, so it is applied
+//     to the fp32 sums in the epilogue: each wave stages x * aux (rounded to XT) and
+//     runs its MFMAs at once, sums x^2 over its K range meanwhile, and the workgroup adds
+//     the W partials of each row in wave order at the cross-wave reduction it runs
+//     anyway.  No barrier is added to the critical path.  (The reference rounds
+//     x * inv * aux to XT before its GEMM; rounding x * aux instead moves each product
+//     by the same half-ulp relative amount.)
 // RES (staged rows only): y = residual + the linear's output, the output rounded to
 // XT first, as `residual + linear(x)` computes it (qtts/models/talker.py:270-271).
 // PAIR (staged rows, no split): GatedMLP's gate_up_proj followed by its activation
@@ -241,9 +245,9 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     }
     return wave_sum_rows(ss);
   };
-  // Writes the wave's staged rows to LDS (NORM: x * inv * weight, rounded to XT as
-  // the reference's fused norm stores it) and reads the MFMA B operands back.
-  auto stage_x = [&](const float* inv) {
+  // Writes the wave's staged rows to LDS (NORM: x * weight, rounded to XT; the row's
+  // inverse RMS comes in the epilogue) and reads the MFMA B operands back.
+  auto stage_x = [&]() {
     if constexpr (NORM) {
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
@@ -254,8 +258,8 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const uint32_t p = (uint32_t)xr[m][v][i], w2 = (uint32_t)xu[0][v][i];
-            const float h0 = (to_f32(XT{(uint16_t)p}) * inv[m]) * to_f32(XT{(uint16_t)w2});
-            const float h1 = (to_f32(XT{(uint16_t)(p >> 16)}) * inv[m]) * to_f32(XT{(uint16_t)(w2 >> 16)});
+            const float h0 = to_f32(XT{(uint16_t)p}) * to_f32(XT{(uint16_t)w2});
+            const float h1 = to_f32(XT{(uint16_t)(p >> 16)}) * to_f32(XT{(uint16_t)(w2 >> 16)});
             o[i] = (int)pack2_f32<XT>(h0, h1);
           }
           *(i32x4_t*)&xrow[wave][m][e] = o;
@@ -298,44 +302,21 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     // Keep the scheduler from interleaving loads with the MFMAs: every load must
     // be in flight before the first wait.
     __builtin_amdgcn_sched_barrier(0);
+    stage_x();  // waits for the activation rows only; the weights stay in flight
     if constexpr (NORM) {
 #pragma unroll
-      for (int m = 0; m < MX; ++m) {  // waits for the activation rows only
+      for (int m = 0; m < MX; ++m) {  // the row partials, published at the reduction below
         const float ss = norm_partial(m);
         if (lane == 0) nss[wave][m] = ss;
       }
-    } else {
-      stage_x(nullptr);  // waits for the activation rows only; the weights stay in flight
-      consume(wc0);
     }
+    consume(wc0);
   } else {
     issue_epilogue();
     if constexpr (NORM) {
       if (lane == 0)
 #pragma unroll
         for (int m = 0; m < MX; ++m) nss[wave][m] = 0.0f;
-    }
-  }
-  if constexpr (NORM) {
-    // variance = sum / K; inv = 1 / sqrt(variance + eps), both correctly rounded; lane m
-    // computes row m's (the wave partials added in wave order), every lane reads them.
-    wait_lgkmcnt0();
-    barrier_only();
-    float mine;
-    {
-      const int mr = lane < MX ? lane : 0;
-      float ss = 0.0f;
-#pragma unroll
-      for (int w = 0; w < W; ++w) ss += nss[w][mr];
-      mine = 1.0f / __builtin_sqrtf(ss / (float)K + eps);
-    }
-    float inv[MX];
-#pragma unroll
-    for (int m = 0; m < MX; ++m)
-      inv[m] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, mine), m));
-    if (wc0 < wc1) {
-      stage_x(inv);
-      consume(wc0);
     }
   }
 
@@ -353,6 +334,18 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       for (int mb = 0; mb < MB; ++mb) acc[mb] += red[w][mb][lane];
       if constexpr (PAIR) up[0] += red[w][1][lane];
     }
+  }
+
+  // NORM: variance = sum / K and inv = 1 / sqrt(variance + eps), both correctly rounded;
+  // lane m computes row m's from the wave partials in wave order, and lane (r, g) takes
+  // row r's for its column of the result.
+  float inv_r = 1.0f;
+  if constexpr (NORM) {
+    const int mr = lane < MX ? lane : 0;
+    float ss = 0.0f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) ss += nss[w][mr];
+    inv_r = __shfl(1.0f / __builtin_sqrtf(ss / (float)K + eps), r, 64);
   }
 
   if (S > 1) {
@@ -379,11 +372,11 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       for (int i = 0; i < 4; ++i) {
         const int nn = strip * 16 + 4 * g + i;
         if (nn < (PAIR ? N >> 1 : N)) {
-          float v = acc[mb][i] * bits_to_f32<ST>(sc[i]);
+          float v = (NORM ? acc[mb][i] * inv_r : acc[mb][i]) * bits_to_f32<ST>(sc[i]);
           if (bias) v += bits_to_f32<XT>(bi[i]);
           if constexpr (RES) v = bits_to_f32<XT>(rb[i]) + round_through<XT>(v);
           if constexpr (PAIR) {
-            float u = up[0][i] * bits_to_f32<ST>(su[i]);
+            float u = (NORM ? up[0][i] * inv_r : up[0][i]) * bits_to_f32<ST>(su[i]);
             if (bias) u += bits_to_f32<XT>(bu[i]);
             v = silu_mul<XT>(round_through<XT>(v), round_through<XT>(u));
           }
