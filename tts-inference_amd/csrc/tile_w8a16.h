@@ -257,7 +257,9 @@ inline bool pipe_p_ok(int bm, int bn, int p) {
 // and code-predictor shapes at M = 32..1024 (within 3% of the per-shape best on
 // average): 32 x 64 tiles with 4 stages up to M = 128, 64 x 128 with 3 stages
 // above, 128 x 128 from M = 512 when that still makes 512 tiles; then split K until
-// there are 256 workgroups, keeping >= 8 chunks a split.
+// there are 256 workgroups, keeping >= 8 chunks a split, and on to 512 workgroups
+// while a split keeps >= 32 chunks (talker down_proj at M = 1024: 47.6 -> 40.0 us).
+// A workspace too small for the splits drops the automatic choice to one split.
 // shape_req (algo bits 24-30): bits 0-1 log2(BM / 16) in 1..3, bit 2 a 2 x 2 wave grid
 // (else 1 x 4), bits 4-6 log2(BN / 32) in 1..3; 0 = automatic.
 inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int stages_req, int shape_req = 0) {
@@ -286,6 +288,8 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
   if (S <= 0) {
     S = 1;
     while (tiles * S < 256 && nchunks / (S * 2) >= 8) S *= 2;
+    // long K (>= 32 chunks a split): fill the two resident workgroups a CU holds
+    while (tiles * S < 512 && nchunks / (S * 2) >= 32) S *= 2;
   }
   S = std::max(1, std::min(S, nchunks));
   if (tiles > kMaxSplitTiles) S = 1;

@@ -158,7 +158,7 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
             self._decline(layer)
             return
         ops.reserve_workspace(weight.device, max(
-            ops.workspace_bytes(_lib.OP_FP8W, m, layer.out_features, layer.in_features) for m in (16, 64, 128)))
+            ops.workspace_bytes(_lib.OP_FP8W, m, layer.out_features, layer.in_features) for m in (16, 64, 128, 1024)))
         layer.register_buffer("fp8w_weight", qs, persistent=False)
         layer.register_buffer("fp8w_scale", scale, persistent=False)
         layer.weight = torch.nn.Parameter(torch.empty(0, dtype=weight.dtype, device=weight.device),

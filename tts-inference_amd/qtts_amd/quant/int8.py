@@ -138,7 +138,7 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             layer.register_buffer("int8_weight", None, persistent=False)
             return
         ops.reserve_workspace(weight.device, max(
-            ops.workspace_bytes(_lib.OP_W8A16, m, layer.out_features, layer.in_features) for m in (16, 64, 128)))
+            ops.workspace_bytes(_lib.OP_W8A16, m, layer.out_features, layer.in_features) for m in (16, 64, 128, 1024)))
         layer.register_buffer("int8_weight", q, persistent=False)
         layer.register_buffer("int8_scale", scale, persistent=False)
         layer.int8_layout = layout
