@@ -376,7 +376,13 @@ int qtts_w8a8_int8_gemm(const int8_t* qx, const float* sx, int64_t m, int64_t k,
  * qtts_quant_act_int8_rows into the workspace, then qtts_w8a8_int8_gemm.  The
  * reference's padding to 17 rows for torch._int_mm (int8.py:150-155) has no
  * counterpart: every m runs as is.  x: [m, k] of x_dtype; y: [m, n] of x_dtype;
- * bias: [n] of x_dtype or NULL.  Workspace: qtts_workspace_bytes(QTTS_OP_INT8_LINEAR). */
+ * bias: [n] of x_dtype or NULL.  Workspace: qtts_workspace_bytes(QTTS_OP_INT8_LINEAR).
+ * With strip weights, bf16 / fp16 activations (16-byte aligned rows), m <= 8 and
+ * k % 64 == 0, k <= 8192, one kernel quantizes inside the GEMM, with the same output
+ * bits and no workspace: automatically while the per-CU quantization work is small
+ * (every workgroup quantizes all m x k activations), or always when algo is
+ * QTTS_ALGO_SKINNY with only a wave count (a power of two up to 16) set.  Any split
+ * count keeps the two-kernel path. */
 int qtts_int8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
                      const int8_t* qw, int64_t n, int64_t ldqw, const float* sw,
                      const void* bias, void* y, int64_t ldy, int div_mode,

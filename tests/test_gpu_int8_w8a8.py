@@ -8,7 +8,8 @@ rounding to the activation dtype, so the bar here is bit-exact, everywhere:
 * the GEMM against the oracle at small sizes and, at the full talker / code
   predictor shapes, against torch on the GPU (an fp64 matmul of the codes, which is
   exact, followed by the reference's fp32 epilogue expression);
-* whole linears against the golden fixtures written by torch._int_mm on the CPU.
+* whole linears against the golden fixtures written by torch._int_mm on the CPU;
+* the fused decode kernel (quantization inside the GEMM) against the two-kernel path.
 """
 
 from __future__ import annotations
@@ -268,6 +269,73 @@ def test_int8_linear_graph_replays(ops):
         assert torch.equal(out, eager), f"replay {i} differs from eager"
         q_t, s_t = _torch_act_int8(x * (i + 2))
         assert torch.equal(junk, _torch_int8_out(q_t, s_t, qw, sw, None, torch.bfloat16))
+
+
+def _two_kernel(ops, x, qs, n, sw, bias, mode):
+    """The unfused path: quant_act_int8_vec_kernel, then the skinny int8 GEMM."""
+    qx, sx = ops.quant_act_int8(x, mode)
+    return ops.w8a8_int8_gemm_strips(qx, sx, qs, n, sw, bias, x.dtype)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_int8_linear_fused_decode(ops, dtype):
+    """Decode rows (M <= 8, K % 64 == 0) run quantization, GEMM and epilogue in one kernel
+    (int8_linear_fused_kernel), forced here through an explicit wave count (the fewest the
+    shape allows, and 16: runs of 8, 6, 4 and 2 chunks) besides the automatic choice.  Its
+    output is the two-kernel path's, bit for bit, at every M in 1..8, for ragged K (runs
+    shorter than a wave's, waves with no chunk) and N, strided rows, both division modes,
+    with a zero row, a row under the 1e-6 clamp (an fp16 scale of zero: codes +-127 and 0)
+    and a row of rounding ties; and the oracle's on small cases."""
+    for (n, k) in ((100, 64), (48, 320), (2048, 2048), (12288, 2048), (2048, 6144), (1024, 3072), (64, 8192),
+                   (40, 1984)):
+        g = torch.Generator(device="cuda").manual_seed(n * 7 + k)
+        w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(dtype)
+        qw, sw = ops.pack_int8(w, torch.float32)
+        qs = ops.to_strips(qw)
+        bias = (torch.randn(n, device="cuda", generator=g) * 0.1).to(dtype)
+        for m in range(1, 9):
+            base = _acts(max(m, 4), k + 64, dtype, seed=m * 17 + k)[-m:]  # the special rows from m = 4 on
+            x = base[:, 32:32 + k] if m % 3 == 0 else base[:, :k].contiguous()  # strided rows, 16-byte aligned
+            b = bias if m % 2 else None
+            wmin = 1
+            while wmin * 8 < k // 64:
+                wmin *= 2
+            for mode in (O.DIV_DEVICE, O.DIV_IEEE):
+                want = _two_kernel(ops, x, qs, n, sw, b, mode)
+                for algo in (ops.algo_code(0), ops.algo_code(1, 0, wmin), ops.algo_code(1, 0, 16)):
+                    what = f"{dtype} n={n} k={k} m={m} mode={mode} bias={b is not None} ldx={x.stride(0)} algo={algo:#x}"
+                    got = ops.int8_linear_strips(x, qs, n, sw, b, mode, algo)
+                    assert torch.equal(got.view(torch.int16), want.view(torch.int16)), \
+                        (what, int((got.view(torch.int16) != want.view(torch.int16)).sum()))
+                if n * k <= 200_000:
+                    q_ref, s_ref = O.quant_act_int8(_np_bits(x), ODT[dtype], mode)
+                    y_ref = O.int8_linear_out(q_ref, s_ref, qw.cpu().numpy(), sw.cpu().numpy(),
+                                              None if b is None else _np_bits(b), ODT[dtype])
+                    _assert_bits(got, y_ref, what + " vs oracle")
+
+
+def test_int8_linear_fused_graph_replays(ops):
+    """The fused decode kernel captured in a graph: every replay matches eager."""
+    n, k = 4096, 2048
+    g = torch.Generator(device="cuda").manual_seed(6)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    qw, sw = ops.pack_int8(w, torch.float32)
+    qs = ops.to_strips(qw)
+    static_x = _acts(4, k, torch.bfloat16, seed=8)
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        ops.int8_linear_strips(static_x, qs, n, sw)
+    torch.cuda.current_stream().wait_stream(st)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = ops.int8_linear_strips(static_x, qs, n, sw)
+    for i in range(3):
+        static_x.copy_(_acts(4, k, torch.bfloat16, seed=20 + i))
+        graph.replay()
+        torch.cuda.synchronize()
+        want = _two_kernel(ops, static_x, qs, n, sw, None, O.DIV_DEVICE)
+        assert torch.equal(out, want), f"replay {i}"
 
 
 def test_int8_errors(ops):

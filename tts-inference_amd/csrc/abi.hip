@@ -63,6 +63,10 @@ int qtts_launch_w8a16_fused(const void* x, int x_dtype, int64_t m, int64_t k, in
 int qtts_launch_fp8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
                                  int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
                                  hipStream_t st);
+int qtts_int8_fused_ok(int64_t m, int64_t n, int64_t k, int waves);
+int qtts_launch_int8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qws,
+                                  int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
+                                  int waves, hipStream_t st);
 
 static thread_local char g_last_error[512] = "";
 
@@ -421,6 +425,17 @@ static int int8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, in
   QTTS_REQUIRE(ws_bytes >= 0, "int8_linear: negative workspace size");
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(sw && y && (k == 0 || (x && qw)), "int8_linear: null pointer");
+  // Decode rows on strip weights: quantization fused into the GEMM, one kernel, no
+  // workspace.  A wave count alone (family SKINNY or AUTO, no split count or chunk
+  // count) sets the fused kernel's waves; an explicit split count keeps the two-kernel path.
+  const int fused_waves = (algo >> 16) & 0xff;
+  if (layout == qtts::kLayoutStrips && (algo & 0xff) != QTTS_ALGO_TILE && ((algo >> 8) & 0xff) == 0 &&
+      (algo >> 24) == 0 && x_dtype != QTTS_F32 && (uintptr_t)x % 16 == 0 && ldx % 8 == 0 &&
+      qtts_int8_fused_ok(m, n, k, fused_waves)) {
+    QTTS_TRY(current_device_check());
+    return qtts_launch_int8_linear_fused(x, x_dtype, m, k, ldx, qw, n, sw, bias, y, ldy, div_mode, fused_waves,
+                                         (hipStream_t)stream);
+  }
   // Layout: the GEMM's own workspace (split-K counters first) from the start, the
   // quantized activations (rows of k bytes, 16-byte aligned when k % 16 == 0) and
   // their scales at the end.

@@ -239,6 +239,19 @@ __device__ __forceinline__ float scalar_div(float num, float c, int div_mode) {
   return div_mode == QTTS_DIV_DEVICE ? num * (1.0f / c) : num / c;
 }
 
+// Per-token int8 activation quantization (qtts/quant/int8.py:146-149), every step in
+// the activation dtype XT as the reference computes it on an XT tensor:
+// s = XT(max(amax, XT(1e-6)) / 127), code = clamp(rint(XT(x / s)), -127, 127), and a
+// NaN quotient (0 / 0 when an fp16 scale underflows to zero) gives code 0.
+template <typename XT> __device__ __forceinline__ float int8_act_scale(float amax, int div_mode) {
+  return round_through<XT>(scalar_div(fmaxf(amax, round_through<XT>(1e-6f)), 127.0f, div_mode));
+}
+
+template <typename XT> __device__ __forceinline__ int int8_act_code(float x, float s) {
+  const float v = __builtin_rintf(round_through<XT>(x / s));
+  return v != v ? 0 : (int)fminf(fmaxf(v, -127.0f), 127.0f);
+}
+
 // ---- wave64 reductions ----------------------------------------------------------------
 
 __device__ __forceinline__ float wave_max(float v) {

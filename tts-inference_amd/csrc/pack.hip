@@ -147,15 +147,6 @@ __global__ __launch_bounds__(kPackThreads) void quant_act_fp8_vec_kernel(
 // row with absmax below ~3.8e-6 produces, since that scale rounds to zero) stores
 // code 0, what the reference's float -> int8 cast gives it.
 
-template <typename XT> __device__ __forceinline__ float int8_act_scale(float amax, int div_mode) {
-  return round_through<XT>(scalar_div(fmaxf(amax, round_through<XT>(1e-6f)), 127.0f, div_mode));
-}
-
-template <typename XT> __device__ __forceinline__ int int8_act_code(float x, float s) {
-  const float v = __builtin_rintf(round_through<XT>(x / s));
-  return v != v ? 0 : (int)fminf(fmaxf(v, -127.0f), 127.0f);
-}
-
 template <typename XT>
 __global__ __launch_bounds__(kPackThreads) void quant_act_int8_kernel(
     const XT* __restrict__ x, int64_t k, int64_t ld, int8_t* __restrict__ qx, float* __restrict__ sx,
