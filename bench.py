@@ -391,13 +391,13 @@ def run_fp8(args, torch, ops):
 
 
 def run_int8_w8a8(args, torch, ops):
-    """int8 W8A8 (Int8Method) on the talker shapes, M in {1, 8, 64, 256, 1024}: the one-call linear
-    (per-token quantization + int8 MFMA GEMM) against hipBLASLt bf16 and the W8A16 kernel on the
-    same int8 codes."""
+    """int8 W8A8 (Int8Method) on the talker shapes, M in {1, 2, 4, 8, 64, 256, 1024}: the one-call
+    linear (per-token quantization + int8 MFMA GEMM, one fused kernel for small decode batches)
+    against hipBLASLt bf16 and the W8A16 kernel on the same int8 codes."""
     stack = make_stack(torch, ops, TALKER, 1, keep_bf16=True, f32_scale=True)
     ops.reserve_workspace(torch.device("cuda"), 64 << 20)
     res = {}
-    for m in (1, 8, 64, 256, 1024):
+    for m in (1, 2, 4, 8, 64, 256, 1024):
         xs = make_inputs(torch, [2048, 6144], [m], outliers=True)
         for e in stack:
             x = xs[(m, e["k"])]
@@ -415,7 +415,7 @@ def run_int8_w8a8(args, torch, ops):
                                         "TOPs": round(fl / (tq * 1e-3) / 1e12, 1),
                                         "int8_mfma_util": round(fl / (tq * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
     return {"metric": "int8 W8A8 linear us, GB/s and int8 MFMA utilisation", "value": None, "unit": "us",
-            "n_gpus": 1, "config": {"workload": "talker shapes, int8 W8A8 (Int8Method), M in {1, 8, 64, 256, 1024}"},
+            "n_gpus": 1, "config": {"workload": "talker shapes, int8 W8A8 (Int8Method), M in {1, 2, 4, 8, 64, 256, 1024}"},
             "shapes": res}
 
 
@@ -677,8 +677,9 @@ def summarize_pmc(path: str) -> None:
 # rocprofv3 digest
 # ---------------------------------------------------------------------------------------
 
-def summarize_rocprof(path: str) -> None:
-    """Average duration per (kernel, grid) from rocprofv3 --kernel-trace CSV output under ``path``."""
+def summarize_rocprof(path: str, match: str | None = None) -> None:
+    """Average duration per (kernel, grid) from rocprofv3 --kernel-trace CSV output under ``path``:
+    the 40 heaviest rows, or with ``match`` (comma-separated name substrings) every matching row."""
     files = glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True)
     if not files:
         raise SystemExit(f"no *kernel_trace.csv under {path}")
@@ -695,8 +696,13 @@ def summarize_rocprof(path: str) -> None:
                 groups.setdefault((name[:110], grid), []).append((end - start) / 1e3)
     rows = sorted(groups.items(), key=lambda kv: -sum(kv[1]))
     total = sum(sum(v) for _, v in rows)
+    if match:
+        keys = [t for t in match.split(",") if t]
+        rows = [r for r in rows if any(t in r[0][0] for t in keys)]
+    else:
+        rows = rows[:40]
     print(f"{'calls':>7} {'avg_us':>9} {'min_us':>9} {'total_us':>11} {'pct':>6}  grid  kernel")
-    for (name, grid), v in rows[:40]:
+    for (name, grid), v in rows:
         print(f"{len(v):7d} {sum(v) / len(v):9.3f} {min(v):9.3f} {sum(v):11.1f} {100 * sum(v) / total:5.1f}%  "
               f"{grid}  {name}")
 
@@ -712,6 +718,8 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=20.0, help="time budget of the CPU baseline sample")
     ap.add_argument("--summarize-rocprof", metavar="DIR")
+    ap.add_argument("--summarize-match", metavar="NAMES", help="with --summarize-rocprof: every kernel whose "
+                    "name holds one of these comma-separated substrings")
     ap.add_argument("--summarize-pmc", metavar="DIR", help="digest a rocprofv3 --pmc run")
     ap.add_argument("--int8-w8a8", action="store_true",
                     help="time the int8 W8A8 linear (Int8Method) on the talker shapes instead of a config")
@@ -726,7 +734,7 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.summarize_rocprof:
-        summarize_rocprof(args.summarize_rocprof)
+        summarize_rocprof(args.summarize_rocprof, args.summarize_match)
         return 0
     if args.summarize_pmc:
         summarize_pmc(args.summarize_pmc)
