@@ -347,26 +347,36 @@ def run_predictor(args, torch, ops):
 
 
 def run_prefill(args, torch, ops):
-    """talker shapes at M in {64, 256, 1024}: MFMA tile path vs hipBLASLt bf16."""
+    """talker shapes at M in {64, 256, 1024, 2048}: the MFMA tile path and the prefill
+    route (dequantize the int8 codes into a scratch buffer, then hipBLASLt) against hipBLASLt bf16
+    on the resident bf16 weight; ``calibrated`` is the faster of the two int8 routes, the choice the
+    calibration makes per prefill bucket."""
+    from qtts_amd.quant import prefill
     stack = make_stack(torch, ops, TALKER, 1, keep_bf16=True)
     ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    for e in stack:
+        prefill.reserve(torch.device("cuda"), e["n"], e["k"], torch.bfloat16)
     res = {}
-    for m in (64, 256, 1024):
+    for m in (64, 256, 1024, 2048):
         xs = make_inputs(torch, [2048, 6144], [m])
         for e in stack:
-            fq = lambda e=e: ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"])
-            fb = lambda e=e: torch.nn.functional.linear(xs[(m, e["k"])], e["w_bf16"])
-            gq = capture(torch, lambda: [fq() for _ in range(10)])
-            gb = capture(torch, lambda: [fb() for _ in range(10)])
-            tq = time_graph(torch, gq, args.steps, args.warmup) / 10
-            tb = time_graph(torch, gb, args.steps, args.warmup) / 10
+            x = xs[(m, e["k"])]
+            fq = lambda e=e, x=x: ops.w8a16_gemm_strips(x, e["qs"], e["n"], e["s"])
+            fd = lambda e=e, x=x: prefill.dequant_linear(e["qs"], ops.CODE_INT8, e["n"], e["k"], e["s"], x, None)
+            fb = lambda e=e, x=x: torch.nn.functional.linear(x, e["w_bf16"])
+            tq, td, tb = (time_graph(torch, capture(torch, lambda f=f: [f() for _ in range(10)]), args.steps,
+                                     args.warmup) / 10 for f in (fq, fd, fb))
             fl = 2 * m * e["n"] * e["k"]
-            res[f"M{m}_{e['name']}"] = {"us": round(tq * 1e3, 2), "bf16_us": round(tb * 1e3, 2),
-                                        "speedup": round(tb / tq, 3),
+            tc = min(tq, td)
+            res[f"M{m}_{e['name']}"] = {"us": round(tq * 1e3, 2), "dequant_gemm_us": round(td * 1e3, 2),
+                                        "bf16_us": round(tb * 1e3, 2), "speedup": round(tb / tq, 3),
+                                        "calibrated": "tile" if tq <= td else "dequant_gemm",
+                                        "calibrated_speedup": round(tb / tc, 3),
                                         "TFLOPs": round(fl / (tq * 1e-3) / 1e12, 1),
                                         "mfma_util": round(fl / (tq * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4)}
     return {"metric": "prefill W8A16 MFMA utilisation / speedup vs bf16", "value": None, "unit": "TFLOP/s",
-            "n_gpus": 1, "config": {"workload": "configs[3]: talker shapes, M in {64, 256, 1024}"}, "shapes": res}
+            "n_gpus": 1, "config": {"workload": "configs[3]: talker shapes, M in {64, 256, 1024, 2048}"},
+            "shapes": res}
 
 
 def run_fp8(args, torch, ops):

@@ -136,6 +136,20 @@ int64_t qtts_strip_bytes(int64_t n, int64_t k, int kind);
 int qtts_to_strips(const void* src, int64_t n, int64_t k, int64_t ld_src, int kind, void* dst, void* stream);
 int qtts_from_strips(const void* src, int64_t n, int64_t k, int kind, void* dst, int64_t ld_dst, void* stream);
 
+/* Codes a QTTS_STRIP_INT8 matrix can hold: int8 (the int8 weight-only and W8A8
+ * methods) or OCP e4m3 (the fp8 weight-only method). */
+typedef enum { QTTS_CODE_INT8 = 0, QTTS_CODE_E4M3 = 1 } qtts_code_kind;
+
+/* w[r, c] = w_dtype(f32(code[r, c]) * f32(scale[r])): the dequantized weight of the
+ * reference's dequantize-then-matmul form, q.to(dtype) * scale[:, None]
+ * (qtts/quant/kernels.py:144-148), from a QTTS_STRIP_INT8 matrix of `codes`.  The int8
+ * weight-only method runs it ahead of a plain library GEMM for the prefill row counts
+ * its calibration gives to that route (the bf16 baseline the calibration times).
+ * qs: qtts_strip_bytes(n, k, QTTS_STRIP_INT8) bytes.  scale: [n] of scale_dtype (bf16,
+ * fp16 or fp32).  w: [n, k] of w_dtype (bf16, fp16 or fp32), row stride ldw >= k. */
+int qtts_dequant_strips(const void* qs, int codes, int64_t n, int64_t k, const void* scale, int scale_dtype,
+                        void* w, int w_dtype, int64_t ldw, void* stream);
+
 /* --- W8A16: int8 weights, bf16/fp16/fp32 activations ----------------------------- */
 
 /* y[m, n] = cast(sum_c x[m,c] * q[n,c] * f32(scale[n]) + f32(bias[n])), fp32

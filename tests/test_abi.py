@@ -62,6 +62,22 @@ def test_argument_validation_precedes_device_use():
     assert L.qtts_pack_fp8_e4m3_rowwise(None, 1, 0, 16, 16, None, None, 0, None) == 0
 
 
+def test_dequant_strips_argument_checks():
+    """qtts_dequant_strips validates sizes, code kind, dtypes and pointers before any device use."""
+    L = _lib.load()
+    assert L.qtts_dequant_strips(None, 0, 16, 64, None, 1, None, 1, 32, None) == -1  # ldw < k
+    assert "bad sizes" in _lib.last_error()
+    assert L.qtts_dequant_strips(None, 5, 16, 64, None, 1, None, 1, 64, None) == -1
+    assert "code kind" in _lib.last_error()
+    assert L.qtts_dequant_strips(None, 1, 16, 64, None, 1, None, 7, 64, None) == -1
+    assert "dtype" in _lib.last_error()
+    assert L.qtts_dequant_strips(None, 0, 16, 64, None, 1, None, 1, 64, None) == -1
+    assert "null pointer" in _lib.last_error()
+    assert L.qtts_dequant_strips(None, 0, 0, 64, None, 1, None, 1, 64, None) == 0  # empty: no device needed
+    assert re.search(r"\bQTTS_CODE_E4M3\s*=\s*1\b", open(HEADER).read())
+    assert (_lib.CODE_INT8, _lib.CODE_E4M3) == (0, 1)
+
+
 def test_null_pointers_rejected():
     L = _lib.load()
     assert L.qtts_w8a16_gemm(None, 1, 2, 16, 16, None, 8, 16, None, 1, None, None, 8, 0, None, 0, None) == -1

@@ -161,5 +161,5 @@ def test_calibration_failures_are_never_fatal():
 
 
 def test_m_buckets():
-    assert [bucket_of(m) for m in (1, 2, 3, 5, 9, 16, 17, 64, 65, 300, 5000)] == \
-        [1, 2, 4, 8, 16, 16, 32, 64, 128, 1024, 1024]
+    assert [bucket_of(m) for m in (1, 2, 3, 5, 9, 16, 17, 64, 65, 300, 1500, 5000)] == \
+        [1, 2, 4, 8, 16, 16, 32, 64, 128, 1024, 2048, 2048]

@@ -81,7 +81,8 @@ def build(verbose: bool = False) -> str:
     with concurrent.futures.ThreadPoolExecutor(workers) as pool:
         list(pool.map(lambda c: _run(c, verbose), cmds))
     tmp = OUT + ".tmp"
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs], verbose)
+    # -z defs: an entry point declared but not defined fails the link here, not the first import
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs], verbose)
     os.replace(tmp, OUT)
     return OUT
 

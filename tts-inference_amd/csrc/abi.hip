@@ -31,6 +31,8 @@ int qtts_launch_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t 
                          int out_dtype, int64_t ldy, int algo, void* ws, int64_t ws_bytes, hipStream_t st);
 int qtts_launch_to_strips(const void* src, int64_t n, int64_t k, int64_t ld, void* dst, int kind, hipStream_t st);
 int qtts_launch_from_strips(const void* src, int64_t n, int64_t k, void* dst, int64_t ld, int kind, hipStream_t st);
+int qtts_launch_dequant_strips(const void* qs, int codes, int64_t n, int64_t k, const void* scale, int sdt, void* w,
+                               int w_dtype, int64_t ldw, hipStream_t st);
 int64_t qtts_fp8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
 int qtts_fp8_fused_ok(int64_t m, int64_t n, int64_t k);
 int qtts_launch_quant_act_int8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld, int8_t* qx, float* sx,
@@ -606,6 +608,19 @@ int qtts_from_strips(const void* src, int64_t n, int64_t k, int kind, void* dst,
   QTTS_REQUIRE((uintptr_t)src % 16 == 0, "from_strips: source must be 16-byte aligned");
   QTTS_TRY(current_device_check());
   return qtts_launch_from_strips(src, n, k, dst, ld_dst, kind, (hipStream_t)stream);
+}
+
+int qtts_dequant_strips(const void* qs, int codes, int64_t n, int64_t k, const void* scale, int scale_dtype, void* w,
+                        int w_dtype, int64_t ldw, void* stream) {
+  QTTS_REQUIRE(n >= 0 && k >= 0 && ldw >= k, "dequant_strips: bad sizes");
+  QTTS_REQUIRE(n < (1ll << 31) && k < (1ll << 31), "dequant_strips: size too large");
+  QTTS_REQUIRE(codes == QTTS_CODE_INT8 || codes == QTTS_CODE_E4M3, "dequant_strips: bad code kind %d", codes);
+  QTTS_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(w_dtype), "dequant_strips: bad dtype code");
+  if (n == 0 || k == 0) return QTTS_OK;
+  QTTS_REQUIRE(qs && scale && w, "dequant_strips: null pointer");
+  QTTS_REQUIRE((uintptr_t)qs % 16 == 0, "dequant_strips: strip buffer must be 16-byte aligned");
+  QTTS_TRY(current_device_check());
+  return qtts_launch_dequant_strips(qs, codes, n, k, scale, scale_dtype, w, w_dtype, ldw, (hipStream_t)stream);
 }
 
 int qtts_kernel_timer_begin(int max_launches) {

@@ -44,6 +44,10 @@ __device__ __forceinline__ float to_f32(f16_t v) {
 
 // fp32 -> 16-bit float, round to nearest even, by the hardware conversions
 // (v_cvt_pk_bf16_f32 on gfx950, v_cvt_f16_f32): branch-free, NaN becomes a quiet NaN.
+// The fp16 conversion is written as the instruction itself: left to the compiler, a
+// conversion of a product or an fma result is folded into v_fma_mixlo_f16, which rounds
+// the exact result once (and turns -0 * s into +0), where fp32 arithmetic followed by
+// the conversion -- torch's order -- rounds twice.
 typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2_t;
 typedef __attribute__((ext_vector_type(2))) float f32x2_t;
 
@@ -53,7 +57,9 @@ template <> __device__ __forceinline__ bf16_t from_f32<bf16_t>(float v) {
   return bf16_t{__builtin_bit_cast(uint16_t, (__bf16)v)};
 }
 template <> __device__ __forceinline__ f16_t from_f32<f16_t>(float v) {
-  return f16_t{__builtin_bit_cast(uint16_t, (_Float16)v)};
+  uint32_t h;
+  asm("v_cvt_f16_f32 %0, %1" : "=v"(h) : "v"(v));
+  return f16_t{(uint16_t)h};
 }
 
 // Two values rounded to T and packed low-first into 32 bits (one conversion for bf16).

@@ -45,6 +45,8 @@ CHAIN_MAX_LINKS, CHAIN_MAX_ROWS = 8, 8
 CHAIN_MAX_ITEMS, CHAIN_TIMEOUT_BYTE, CHAIN_FLAGS_BYTE = 65536, 0, 256
 # qtts_strip_kind
 STRIP_INT8, STRIP_FP8 = 0, 1
+# qtts_code_kind
+CODE_INT8, CODE_E4M3 = 0, 1
 
 EXPORTS = (
     "qtts_abi_version",
@@ -60,6 +62,7 @@ EXPORTS = (
     "qtts_strip_bytes",
     "qtts_to_strips",
     "qtts_from_strips",
+    "qtts_dequant_strips",
     "qtts_w8a16_gemm_strips",
     "qtts_w8a8_fp8_gemm_strips",
     "qtts_fp8_linear_strips",
@@ -159,6 +162,8 @@ def load() -> ctypes.CDLL:
         L.qtts_to_strips.argtypes = [p, i64, i64, i64, i32, p, p]
         L.qtts_from_strips.restype = i32
         L.qtts_from_strips.argtypes = [p, i64, i64, i32, p, i64, p]
+        L.qtts_dequant_strips.restype = i32
+        L.qtts_dequant_strips.argtypes = [p, i32, i64, i64, p, i32, p, i32, i64, p]
         L.qtts_w8a16_gemm_strips.restype = i32
         L.qtts_w8a16_gemm_strips.argtypes = [p, i32, i64, i64, i64, p, i64, p, i32, p, p, i64, i32, p, i64, p]
         L.qtts_w8a8_fp8_gemm_strips.restype = i32

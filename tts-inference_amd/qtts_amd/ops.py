@@ -17,7 +17,7 @@ from . import _lib
 from ._lib import (ALGO_AUTO, CHAIN_MAX_LINKS, CHAIN_MAX_ROWS, CHAIN_TIMEOUT_BYTE, DIV_DEVICE,  # noqa: F401
                    DIV_IEEE, EPI_RESIDUAL, EPI_SILU_MUL, EPI_STORE, OP_FP8_LINEAR, OP_FP8W, OP_INT8_LINEAR,
                    OP_W8A16, OP_W8A16_FUSED, OP_W8A16_SILU, OP_W8A8_FP8, OP_W8A8_INT8, PRO_NONE,
-                   PRO_RMS_NORM, PRO_SILU_MUL, STRIP_FP8, STRIP_INT8, algo_code)
+                   PRO_RMS_NORM, PRO_SILU_MUL, STRIP_FP8, STRIP_INT8, CODE_E4M3, CODE_INT8, algo_code)
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
@@ -299,6 +299,59 @@ def from_strips(qs: torch.Tensor, n: int, k: int, kind: int | None = None) -> to
     st = _lib.load().qtts_from_strips(_ptr(qs), n, k, kind, _ptr(out), k, _stream(dev))
     _lib.check(st, "from_strips")
     return out
+
+
+def dequant_strips(qs: torch.Tensor, n: int, k: int, scale: torch.Tensor, dtype: torch.dtype,
+                   codes: int = CODE_INT8, out: torch.Tensor | None = None) -> torch.Tensor:
+    """``dtype(code * scale[:, None])`` as a row-major ``[N, K]`` matrix from 64-column strips of
+    int8 (``CODE_INT8``) or e4m3 (``CODE_E4M3``) codes: the reference's dequantized weight,
+    ``q.to(dtype) * scale[:, None]`` (qtts/quant/kernels.py:144-148).  ``out``: an ``[N, K]``
+    (row-contiguous) tensor of ``dtype`` to write into, e.g. a view of :func:`dequant_scratch`."""
+    if qs.dtype not in (torch.int8, torch.uint8) or qs.numel() != strip_bytes(n, k, STRIP_INT8):
+        raise ValueError(f"codes are not a 64-column strip [{n}, {k}] buffer")
+    if scale.numel() != n:
+        raise ValueError(f"scale has {scale.numel()} entries for {n} output channels")
+    dev = _require_cuda(qs, scale)
+    scale = scale.contiguous()
+    if out is None:
+        out = torch.empty((n, k), dtype=dtype, device=dev)
+    elif out.dtype != dtype or tuple(out.shape) != (n, k) or (k > 1 and out.stride(1) != 1):
+        raise ValueError(f"out must be an [{n}, {k}] {dtype} tensor with unit column stride")
+    st = _lib.load().qtts_dequant_strips(_ptr(qs), codes, n, k, _ptr(scale), dtype_code(scale.dtype), _ptr(out),
+                                         dtype_code(dtype), out.stride(0) if n > 1 else k, _stream(dev))
+    _lib.check(st, "dequant_strips")
+    return out
+
+
+# One scratch buffer per device for dequantized weights (the int8 weight-only method's
+# prefill route: dequantize, then a library GEMM).  Grown outside capture only; an
+# outgrown buffer stays alive for the graphs that captured its address.  Calls that
+# share it must be stream-ordered, as for the workspace.
+_dq_scratch: dict[int, torch.Tensor] = {}
+
+
+def reserve_dequant_scratch(device: torch.device, nbytes: int) -> None:
+    """Grow the device's dequantization scratch to at least ``nbytes`` (call outside capture)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    with _ws_lock:
+        buf = _dq_scratch.get(idx)
+        if nbytes <= 0 or (buf is not None and buf.numel() >= nbytes) or torch.cuda.is_current_stream_capturing():
+            return
+        if buf is not None:
+            _retired.append(buf)
+        size = (nbytes + (1 << 20) - 1) & ~((1 << 20) - 1)
+        _dq_scratch[idx] = torch.empty(size, dtype=torch.uint8, device=torch.device("cuda", idx))
+
+
+def dequant_scratch(device: torch.device, n: int, k: int, dtype: torch.dtype) -> torch.Tensor:
+    """An ``[N, K]`` ``dtype`` view of the device's dequantization scratch (reserved beforehand)."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    need = n * k * torch.empty((), dtype=dtype).element_size()
+    buf = _dq_scratch.get(idx)
+    if buf is None or buf.numel() < need:
+        raise ValueError(f"dequantization scratch holds {0 if buf is None else buf.numel()} bytes, {need} needed "
+                         f"(reserve_dequant_scratch before capture)")
+    return buf[:need].view(dtype).view(n, k)
 
 
 def w8a16_gemm_strips(x: torch.Tensor, qs: torch.Tensor, n: int, scale: torch.Tensor,

@@ -19,6 +19,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import _lib, ops
+from . import prefill
 from .base import QuantMethodBase
 from .calibrate import pick_fastest
 from .kernels import kernel_available
@@ -159,6 +160,11 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
             return
         ops.reserve_workspace(weight.device, max(
             ops.workspace_bytes(_lib.OP_FP8W, m, layer.out_features, layer.in_features) for m in (16, 64, 128, 1024)))
+        if self.calibrate:
+            # Prefill buckets: the tile kernel against dequantize + F.linear (quant/prefill.py).
+            n, k = layer.out_features, layer.in_features
+            prefill.calibrate(_FP8W_ALGO, "fp8_wo_prefill", qs, _lib.CODE_E4M3, n, k, scale, weight.dtype,
+                              weight.device, lambda x: ops.fp8w_gemm_strips(x, qs, n, scale, None))
         layer.register_buffer("fp8w_weight", qs, persistent=False)
         layer.register_buffer("fp8w_scale", scale, persistent=False)
         layer.weight = torch.nn.Parameter(torch.empty(0, dtype=weight.dtype, device=weight.device),
@@ -175,4 +181,6 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
         n, k = layer.out_features, layer.in_features
         rows = x.numel() // k if k else 0
         algo = _FP8W_ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
+        if algo == prefill.ALGO_DEQUANT_GEMM:
+            return prefill.dequant_linear(layer.fp8w_weight, _lib.CODE_E4M3, n, k, layer.fp8w_scale, x, bias)
         return ops.fp8w_gemm_strips(x, layer.fp8w_weight, n, layer.fp8w_scale, bias, algo)

@@ -5,7 +5,9 @@ output channel, keeps activations in the model dtype, and runs the gfx950 fused
 dequantize-in-registers GEMM.  With ``calibrate`` it times, per layer shape, the
 HIP kernel candidates against the unquantized F.linear (hipBLASLt on ROCm) inside
 a HIP graph and keeps the fastest; a layer where no candidate wins by 5% keeps
-its original weight and GEMM (qtts/quant/int8.py:79-111).
+its original weight and GEMM (qtts/quant/int8.py:79-111).  For the prefill row
+buckets it also times the tile kernel against dequantizing the codes into a scratch
+buffer and calling F.linear (quant/prefill.py), and keeps the faster route per bucket.
 
 ``Int8Method`` (W8A8) quantizes activations per token at run time and multiplies
 int8 codes on the int8 matrix cores (v_mfma_i32_16x16x64_i8) with exact int32
@@ -21,6 +23,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import _lib, ops
+from . import prefill
 from .base import QuantMethodBase
 from .calibrate import pick_fastest
 from .kernels import kernel_available
@@ -32,7 +35,7 @@ _INT8_MAX = 127.0
 #: Row counts the kernel choice is tuned for: each call uses the entry of the
 #: smallest bucket that holds its row count (decode rows 1..16 go to the skinny
 #: kernel, prefill rows to the tile kernel).
-M_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256, 1024)
+M_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256, 1024, 2048)
 
 #: Per (N, K, bucket) algo codes chosen by calibration; absent means automatic.
 _ALGO: dict[tuple[int, int, int], int] = {}
@@ -139,6 +142,12 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             return
         ops.reserve_workspace(weight.device, max(
             ops.workspace_bytes(_lib.OP_W8A16, m, layer.out_features, layer.in_features) for m in (16, 64, 128, 1024)))
+        if self.calibrate and layout == "strips":
+            # Prefill buckets: the tile kernel against dequantize + F.linear (the bf16 baseline
+            # rebuilt from the stored codes); the faster one serves that bucket's calls.
+            n, k = layer.out_features, layer.in_features
+            prefill.calibrate(_ALGO, "int8_wo_prefill", q, _lib.CODE_INT8, n, k, scale, weight.dtype, weight.device,
+                              lambda x: ops.w8a16_gemm_strips(x, q, n, scale, None))
         layer.register_buffer("int8_weight", q, persistent=False)
         layer.register_buffer("int8_scale", scale, persistent=False)
         layer.int8_layout = layout
@@ -154,6 +163,8 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         n, k = layer.out_features, layer.in_features
         rows = x.numel() // k if k else 0
         algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
+        if algo == prefill.ALGO_DEQUANT_GEMM and layer.int8_layout == "strips":
+            return prefill.dequant_linear(layer.int8_weight, _lib.CODE_INT8, n, k, layer.int8_scale, x, bias)
         if layer.int8_layout == "strips":
             if x.dtype in (torch.bfloat16, torch.float16):
                 return ops.w8a16_gemm_strips(x, layer.int8_weight, n, layer.int8_scale, bias, algo)
@@ -172,6 +183,8 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             return None
         rows = x.numel() // k if k else 0
         algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
+        if algo == prefill.ALGO_DEQUANT_GEMM:
+            return None
         return ops.w8a16_gate_up_silu_strips(x, layer.int8_weight, n, layer.int8_scale, bias, algo=algo)
 
     def apply_silu_mul(self, layer, gate_up: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
@@ -183,7 +196,8 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         if layer.int8_layout == "strips" and gate_up.dtype in (torch.bfloat16, torch.float16):
             rows = gate_up.numel() // (2 * k) if k else 0
             algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
-            return ops.w8a16_silu_mul_gemm_strips(gate_up, layer.int8_weight, n, layer.int8_scale, bias, algo)
+            if algo != prefill.ALGO_DEQUANT_GEMM:
+                return ops.w8a16_silu_mul_gemm_strips(gate_up, layer.int8_weight, n, layer.int8_scale, bias, algo)
         return self.apply(layer, ops.silu_mul(gate_up), bias)
 
 
