@@ -392,12 +392,13 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
 struct SkinnyCfg { int mb, waves, cpw, S, cps, strips; };
 
 // The skinny kernels take up to kSkinnyMaxM rows on strip weights.  The automatic
-// choice keeps them up to 32 rows (two m-blocks) for weights of at most 9 MiB and
-// otherwise moves to the tile kernel past 16 rows: measured on the talker and
-// code-predictor shapes at M = 16..96, where the tile kernel wins on the 12-25 MB
-// weights from 24 rows and everywhere from 48.
+// choice keeps them up to 32 rows (two m-blocks) for weights of at most 9 MiB with
+// K <= 2048 and otherwise moves to the tile kernel past 16 rows: measured on the talker
+// and code-predictor shapes at M = 16..128, where the tile kernel wins on the 12-25 MB
+// weights from 24 rows, on the predictor's down_proj (K = 3072: 8.9 against 9.7 us at
+// 24 rows, 9.1 against 11.3 at 32) and everywhere from 48.
 constexpr int kSkinnyMaxM = 64, kSkinnyAutoMaxM = 32;
-constexpr int64_t kSkinnyAutoMaxBytes = 9 << 20;
+constexpr int64_t kSkinnyAutoMaxBytes = 9 << 20, kSkinnyAutoMaxK = 2048;
 
 // m-blocks of 16 activation rows a skinny call carries.
 inline int skinny_mb(int64_t m) { return m <= 16 ? 1 : (m <= 32 ? 2 : 4); }

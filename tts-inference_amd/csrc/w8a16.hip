@@ -290,8 +290,9 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
   const int splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff;
   const bool wide_ok = LAYOUT == kLayoutStrips && k % 64 == 0;  // skinny beyond 16 rows
   if (family == QTTS_ALGO_AUTO)
-    family = (m <= 16 || (wide_ok && m <= kSkinnyAutoMaxM && n * k <= kSkinnyAutoMaxBytes)) ? QTTS_ALGO_SKINNY
-                                                                                          : QTTS_ALGO_TILE;
+    family = (m <= 16 || (wide_ok && m <= kSkinnyAutoMaxM && n * k <= kSkinnyAutoMaxBytes && k <= kSkinnyAutoMaxK))
+                 ? QTTS_ALGO_SKINNY
+                 : QTTS_ALGO_TILE;
   if (family == QTTS_ALGO_SKINNY && m > 16 && !(wide_ok && m <= kSkinnyMaxM))
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
                           "skinny W8A16 kernel handles M <= 16 (M <= %d on strip weights with K %% 64 == 0), got M=%lld",
