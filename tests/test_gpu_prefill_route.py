@@ -105,9 +105,11 @@ def test_int8_route_bits_and_bound(ops, monkeypatch):
                           lin.bias.float().cpu().numpy())
         err = np.abs(y.double().cpu().numpy() - ref)
         assert (err <= _bound(ref, torch.bfloat16)).all(), (rows, float(err.max()))
-    # rows outside the routed bucket keep the HIP kernels
+    # rows outside the routed bucket keep the HIP kernels, and so do fp32 activations inside it
     x = torch.randn(64, k, device="cuda").to(torch.bfloat16)
     assert torch.equal(lin(x), ops.w8a16_gemm_strips(x, lin.int8_weight, n, lin.int8_scale, lin.bias))
+    x32 = torch.randn(300, k, device="cuda")
+    assert torch.equal(lin(x32), ops.w8a16_gemm(x32, q, lin.int8_scale, lin.bias))
     del w_bf16
 
 

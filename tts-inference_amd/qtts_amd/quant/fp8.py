@@ -181,6 +181,6 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
         n, k = layer.out_features, layer.in_features
         rows = x.numel() // k if k else 0
         algo = _FP8W_ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
-        if algo == prefill.ALGO_DEQUANT_GEMM:
+        if algo == prefill.ALGO_DEQUANT_GEMM:  # x is bf16 / fp16 here, as the scratch was sized for
             return prefill.dequant_linear(layer.fp8w_weight, _lib.CODE_E4M3, n, k, layer.fp8w_scale, x, bias)
         return ops.fp8w_gemm_strips(x, layer.fp8w_weight, n, layer.fp8w_scale, bias, algo)

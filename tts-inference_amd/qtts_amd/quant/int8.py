@@ -163,8 +163,11 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         n, k = layer.out_features, layer.in_features
         rows = x.numel() // k if k else 0
         algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
-        if algo == prefill.ALGO_DEQUANT_GEMM and layer.int8_layout == "strips":
+        if algo == prefill.ALGO_DEQUANT_GEMM and layer.int8_layout == "strips" and x.dtype in (torch.bfloat16,
+                                                                                             torch.float16):
             return prefill.dequant_linear(layer.int8_weight, _lib.CODE_INT8, n, k, layer.int8_scale, x, bias)
+        if algo == prefill.ALGO_DEQUANT_GEMM:  # the route's marker never reaches a kernel
+            algo = _lib.ALGO_AUTO
         if layer.int8_layout == "strips":
             if x.dtype in (torch.bfloat16, torch.float16):
                 return ops.w8a16_gemm_strips(x, layer.int8_weight, n, layer.int8_scale, bias, algo)
