@@ -528,31 +528,37 @@ def _fused_waves(n: int, k: int) -> int:
 
 @pytest.mark.parametrize("n,k", TALKER + PREDICTOR + [(40, 256), (1000, 128)])
 def test_fp8_linear_fused_matches_two_kernel_path(ops, n, k):
-    """Decode rows (M <= 4) take the fused kernel (quantization inside the GEMM).  With the same wave split,
-    the two-kernel path (stand-alone quantization, bit-exact with the reference, then the GEMM)
-    accumulates in the same order, so the results must be identical: any difference in the fused
-    per-token scale or e4m3 codes shows.  Also within tolerance of the oracle, with bias."""
+    """Decode rows (M <= 8) can take the fused kernel (quantization inside the GEMM).  Forced to a
+    wave count (the one rule picks for one row, and twice it, which it picks from two rows), it must
+    equal the two-kernel path (stand-alone quantization, bit-exact with the reference, then the GEMM
+    with the same wave split, so the same accumulation order) bit for bit: any difference in the
+    fused per-token scale or e4m3 codes shows.  The automatic choice at every M is within tolerance
+    of the oracle, with bias."""
     waves = _fused_waves(n, k)
-    for m in (1, 2, 3, 4, 8, 16):
-        print(f"fp8 fused n={n} k={k} m={m} W={waves}", flush=True)
+    for m in (1, 2, 3, 4, 5, 8, 16):
         x, w = _fp8_inputs(m, n, k, seed=n + 5 * m + k)
         b = (torch.randn(n, device="cuda") * 0.1).to(torch.bfloat16)
         qw, sw = ops.pack_fp8(w)
         qws = ops.to_strips(qw)
-        y = ops.fp8_linear_strips(x, qws, n, sw, b)
         qx, sx = ops.quant_act_fp8(x)
-        two = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, torch.bfloat16, ops.algo_code(1, 1, waves))
-        assert torch.equal(y, two), f"fused differs from the two-kernel path: n={n} k={k} m={m}"
+        if m <= 8:
+            for wf in sorted({waves, min(16, 2 * waves)}):
+                print(f"fp8 fused n={n} k={k} m={m} W={wf}", flush=True)
+                y = ops.fp8_linear_strips(x, qws, n, sw, b, ops.DIV_DEVICE, ops.algo_code(1, 0, wf))
+                two = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, torch.bfloat16, ops.algo_code(1, 1, wf))
+                assert torch.equal(y, two), f"fused differs from the two-kernel path: n={n} k={k} m={m} W={wf}"
+        y = ops.fp8_linear_strips(x, qws, n, sw, b)
         ref, inter = _oracle_w8a8(qx, sx, qw, sw, b)
-        assert_close(y, ref, f"fp8 fused n={n} k={k} m={m}", inter)
+        assert_close(y, ref, f"fp8 linear n={n} k={k} m={m}", inter)
     # fp16 activations and the CPU division mode take the same kernel
     x, w = _fp8_inputs(4, n, k, seed=n + k)
     x = x.to(torch.float16)
     qw, sw = ops.pack_fp8(w)
     qws = ops.to_strips(qw)
-    y = ops.fp8_linear_strips(x, qws, n, sw, None, ops.DIV_IEEE)
+    wf = min(16, 2 * waves)  # the automatic choice at 4 rows where the fused kernel takes it
+    y = ops.fp8_linear_strips(x, qws, n, sw, None, ops.DIV_IEEE, ops.algo_code(1, 0, wf))
     qx, sx = ops.quant_act_fp8(x, ops.DIV_IEEE)
-    two = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, None, torch.float16, ops.algo_code(1, 1, waves))
+    two = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, None, torch.float16, ops.algo_code(1, 1, wf))
     assert torch.equal(y, two), f"fused fp16 / IEEE differs: n={n} k={k}"
 
 

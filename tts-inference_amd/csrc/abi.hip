@@ -34,7 +34,7 @@ int qtts_launch_from_strips(const void* src, int64_t n, int64_t k, void* dst, in
 int qtts_launch_dequant_strips(const void* qs, int codes, int64_t n, int64_t k, const void* scale, int sdt, void* w,
                                int w_dtype, int64_t ldw, hipStream_t st);
 int64_t qtts_fp8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo);
-int qtts_fp8_fused_ok(int64_t m, int64_t n, int64_t k);
+int qtts_fp8_fused_ok(int64_t m, int64_t n, int64_t k, int waves);
 int qtts_launch_quant_act_int8(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld, int8_t* qx, float* sx,
                                int div_mode, hipStream_t st);
 int qtts_launch_int8_gemm(const int8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const int8_t* qw,
@@ -64,7 +64,7 @@ int qtts_launch_w8a16_fused(const void* x, int x_dtype, int64_t m, int64_t k, in
                             hipStream_t st);
 int qtts_launch_fp8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
                                  int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
-                                 hipStream_t st);
+                                 int waves, hipStream_t st);
 int qtts_int8_fused_ok(int64_t m, int64_t n, int64_t k, int waves);
 int qtts_launch_int8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qws,
                                   int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
@@ -333,11 +333,15 @@ static int fp8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, int
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(sw && y && (k == 0 || (x && qw)), "fp8_linear: null pointer");
   // Decode rows on strip weights: quantization fused into the GEMM, one kernel, no
-  // workspace (an explicit split count or wave count keeps the two-kernel path).
-  if (layout == qtts::kLayoutStrips && (algo & 0xff) != QTTS_ALGO_TILE && (algo >> 8) == 0 && x_dtype != QTTS_F32 &&
-      (uintptr_t)x % 16 == 0 && ldx % 8 == 0 && qtts_fp8_fused_ok(m, n, k)) {
+  // workspace.  A wave count alone (family SKINNY or AUTO, no split count or chunk
+  // count) sets the fused kernel's waves; an explicit split count keeps the two-kernel path.
+  const int fused_waves = (algo >> 16) & 0xff;
+  if (layout == qtts::kLayoutStrips && (algo & 0xff) != QTTS_ALGO_TILE && ((algo >> 8) & 0xff) == 0 &&
+      (algo >> 24) == 0 && x_dtype != QTTS_F32 && (uintptr_t)x % 16 == 0 && ldx % 8 == 0 &&
+      qtts_fp8_fused_ok(m, n, k, fused_waves)) {
     QTTS_TRY(current_device_check());
-    return qtts_launch_fp8_linear_fused(x, x_dtype, m, k, ldx, qw, n, sw, bias, y, ldy, div_mode, (hipStream_t)stream);
+    return qtts_launch_fp8_linear_fused(x, x_dtype, m, k, ldx, qw, n, sw, bias, y, ldy, div_mode, fused_waves,
+                                        (hipStream_t)stream);
   }
   // Layout: the GEMM's own workspace (split-K counters first) from the start, the
   // quantized activations and their scales at the end.

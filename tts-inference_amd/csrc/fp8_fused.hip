@@ -1,4 +1,4 @@
-// The whole of Fp8Method.apply (qtts/quant/fp8.py:72-89) for decode rows (M <= 4) in
+// The whole of Fp8Method.apply (qtts/quant/fp8.py:72-89) for decode rows (M <= 8) in
 // one gfx950 kernel: per-token e4m3 quantization of the activations, the fp8 GEMM
 // on strip-layout weights, and the reference's epilogue.
 //
@@ -17,12 +17,13 @@
 //      qx[m][128 c + 32 g .. + 31]);
 //   4. one v_mfma_scale_f32_16x16x128_f8f6f4 per chunk, waves meet in LDS, and wave 0
 //      writes y = round(acc * sx[m] * sw[n]) [+ bias] in the activation dtype.
-// The activation work is spread over all lanes (8-element vectors, row-major over
-// the wave's slice), so a lane quantizes M * 16 * C / 64 vectors at most, not one
-// row's share.  That work grows with M: measured on the talker and predictor shapes,
-// the stand-alone quantization kernel plus the GEMM is faster past 4 rows (past 2
-// when a wave owns 3 chunks), so RM = 4 bounds M.  Rows >= M of a written B
-// operand stay unwritten: they only feed output columns that are never stored.
+// A row's slice is 16 C vectors of 8 elements, padded to VP = 16, 32 or 64 lanes, so a
+// wave holds 64 / VP rows per slot and a lane quantizes one vector per row it holds; the
+// row maxima meet through a DPP / shuffle max per row and one LDS atomic per row and
+// wave.  Every workgroup quantizes all M x K activations, so the work grows with M and
+// K: past three rows the launcher takes the fused kernel only for K <= 2048.  RM (1, 4
+// or 8 rows) sizes the slots.  Rows >= M of a written B operand stay unwritten: they only
+// feed output columns that are never stored.
 #include <algorithm>
 
 #include "common.h"
@@ -34,8 +35,10 @@ template <typename XT, int W, int C, int RM>
 __global__ __launch_bounds__(W * 64) void fp8_linear_fused_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const uint8_t* __restrict__ qws, int N,
     const float* sw, const XT* bias, XT* __restrict__ y, int64_t ldy, int strips, int div_mode) {
-  constexpr int VPR = 16 * C;          // 8-element vectors per row in a wave's slice (at most)
-  constexpr int SLOTS = RM * VPR / 64; // vectors per lane for RM (>= M) rows
+  constexpr int VP = C <= 1 ? 16 : (C <= 2 ? 32 : 64);  // lanes per row in a slot (16 C vectors, padded)
+  constexpr int RPS = 64 / VP;                              // rows a slot holds
+  constexpr int SLOTS = (RM + RPS - 1) / RPS;
+  static_assert(16 * C <= VP, "a row's slice must fit its lanes");
   __shared__ f32x4_t red[W > 1 ? W - 1 : 1][64];
   __shared__ unsigned amax_bits[16];
   __shared__ float sx_lds[16], rcp_lds[16];
@@ -51,7 +54,8 @@ __global__ __launch_bounds__(W * 64) void fp8_linear_fused_kernel(
   const int cw = (nchunks + W - 1) / W;  // <= C, guaranteed by the launcher
   const int wc0 = min(wave * cw, nchunks - 1);
   const int nw = max(0, min(cw, nchunks - wave * cw));  // chunks this wave owns
-  const int vr = nw * 16;                                 // vectors per row in its slice
+  const int vr = nw * 16;                                 // live vectors per row in its slice
+  const int sub = lane / VP, v = lane % VP;               // row within a slot, vector within the row
 
   if (tid < 16) amax_bits[tid] = 0u;
 
@@ -64,15 +68,13 @@ __global__ __launch_bounds__(W * 64) void fp8_linear_fused_kernel(
     w0[u] = *(const i32x4_t*)(wp + off);
     w1[u] = *(const i32x4_t*)(wp + off + 1024);
   }
-  // Slot j of a lane: vector idx = 64 j + lane of the slice, row idx / VPR, vector
-  // idx % VPR (column 128 wc0 + 8 (idx % VPR)).  Dead slots read a clamped address.
+  // Slot j: row RPS j + sub, columns 128 wc0 + 8 v ..; dead lanes read a clamped address.
   i32x4_t xv[SLOTS];
 #pragma unroll
   for (int j = 0; j < SLOTS; ++j) {
-    const int idx = 64 * j + lane, row = idx / VPR, v = idx - row * VPR;
+    const int row = RPS * j + sub;
     const bool live = row < M && v < vr;
-    const XT* p = x + (int64_t)(live ? row : 0) * ldx + (int64_t)wc0 * 128 + (live ? 8 * v : 0);
-    xv[j] = *(const i32x4_t*)p;
+    xv[j] = *(const i32x4_t*)(x + (int64_t)(live ? row : 0) * ldx + (int64_t)wc0 * 128 + (live ? 8 * v : 0));
   }
   uint32_t swb[4], bib[4];
   {
@@ -90,18 +92,18 @@ __global__ __launch_bounds__(W * 64) void fp8_linear_fused_kernel(
   // ---- 1. per-row |x| maxima -------------------------------------------------------
 #pragma unroll
   for (int j = 0; j < SLOTS; ++j) {
-    const int idx = 64 * j + lane, row = idx / VPR, v = idx - row * VPR;
-    if (64 * j < M * VPR) {  // wave-uniform: skip slots past the last row
+    if (RPS * j < M) {  // wave-uniform: every lane takes part in the group max
+      const int row = RPS * j + sub;
+      float mx = 0.0f;
       if (row < M && v < vr) {
-        float mx = 0.0f;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const uint32_t pr = (uint32_t)xv[j][e];
-          mx = fmaxf(mx, fabsf(to_f32(XT{(uint16_t)pr})));
-          mx = fmaxf(mx, fabsf(to_f32(XT{(uint16_t)(pr >> 16)})));
+          mx = fmaxf(mx, fmaxf(fabsf(to_f32(XT{(uint16_t)pr})), fabsf(to_f32(XT{(uint16_t)(pr >> 16)}))));
         }
-        atomicMax(&amax_bits[row], __float_as_uint(mx));  // non-negative floats order as their bits
       }
+      mx = group_max<VP>(mx);
+      if (v == 0 && row < M) atomicMax(&amax_bits[row], __float_as_uint(mx));  // non-negative floats order as bits
     }
   }
   __syncthreads();
@@ -118,8 +120,8 @@ __global__ __launch_bounds__(W * 64) void fp8_linear_fused_kernel(
   // ---- 3. quantize this wave's slice into its B operands --------------------------------
 #pragma unroll
   for (int j = 0; j < SLOTS; ++j) {
-    const int idx = 64 * j + lane, row = idx / VPR, v = idx - row * VPR;
-    if (64 * j < M * VPR) {
+    if (RPS * j < M) {
+      const int row = RPS * j + sub;
       if (row < M && v < vr) {
         const float s = sx_lds[row], rs = rcp_lds[row];
         uint32_t lo = 0, hi = 0;
@@ -186,62 +188,87 @@ using namespace qtts;
 namespace {
 
 constexpr int kFusedMaxChunks = 48;  // 16 waves x 3 chunks: K <= 6144
-constexpr int kFusedMaxRows = 4;
+constexpr int kFusedMaxRows = 8;
+// Past three rows the automatic choice takes the fused kernel only for K <= 2048: measured
+// with cold weights on the talker shapes at M = 1..8, it beats the two-kernel path at every
+// M for K = 2048 (qkv 5.6 against 6.8 us, gate_up 10.8 against 11.7 at M = 8) and up to
+// M = 3 for K = 6144 (down_proj: 8.6 against 8.9 us at M = 3, 9.6 against 9.0 at M = 4).
+constexpr int64_t kFp8FusedMaxKPast3 = 2048;
 
-// Waves and chunks per wave: 2 chunks a wave up to 32 chunks, 3 above; at least
-// enough waves to cover K, and more (up to 16) until the call runs 2048 waves.
-bool fused_cfg(int64_t n, int64_t k, int& W, int& C) {
+// Waves and chunks per wave: 2 chunks a wave up to 32 chunks, 3 above; at least enough
+// waves to cover K, and more (up to 16) until the call runs 2048 waves (doubling them from
+// two rows on measured slower: gate_up 9.4 against 7.7 us at M = 2).  A requested wave
+// count (a power of two up to 16 that covers K in runs of at most 3) replaces them.
+// C: the smallest build (1, 2 or 3 chunks) that holds a wave's run.
+bool fused_cfg(int64_t m, int64_t n, int64_t k, int waves_req, int& W, int& C) {
+  (void)m;
   const int nchunks = (int)(k / 128);
   if (nchunks < 1 || nchunks > kFusedMaxChunks) return false;
-  C = nchunks <= 32 ? 2 : 3;
-  W = 1;
-  while (W * C < nchunks) W *= 2;
-  const int64_t strips = (n + 15) / 16;
-  while (W < 16 && strips * W < 2048) W *= 2;
-  return W <= 16;
+  if (waves_req > 0) {
+    if (waves_req > 16 || (waves_req & (waves_req - 1)) || waves_req * 3 < nchunks) return false;
+    W = waves_req;
+  } else {
+    const int c0 = nchunks <= 32 ? 2 : 3;
+    W = 1;
+    while (W * c0 < nchunks) W *= 2;
+    const int64_t strips = (n + 15) / 16;
+    while (W < 16 && strips * W < 2048) W *= 2;
+  }
+  C = (nchunks + W - 1) / W;
+  return W <= 16 && C <= 3;
 }
 
 }  // namespace
 
-// 1 if the fused kernel takes this call (m <= 4, or m <= 2 with 3 chunks a wave;
-// k % 128 == 0, k <= 6144).
-int qtts_fp8_fused_ok(int64_t m, int64_t n, int64_t k) {
+// 1 if the fused kernel takes this call: 1 <= m <= 8, k % 128 == 0, k <= 6144, and either
+// a requested wave count fused_cfg accepts or (waves = 0) m <= 3 or k <= 2048.
+int qtts_fp8_fused_ok(int64_t m, int64_t n, int64_t k, int waves) {
   int W, C;
-  if (m < 1 || m > kFusedMaxRows || k % 128 != 0 || !fused_cfg(n, k, W, C)) return 0;
-  return C == 2 || m <= 2 ? 1 : 0;
+  if (m < 1 || m > kFusedMaxRows || n < 1 || k % 128 != 0 || !fused_cfg(m, n, k, waves, W, C)) return 0;
+  return waves > 0 || m <= 3 || k <= kFp8FusedMaxKPast3 ? 1 : 0;
 }
 
 // x [m, k] bf16/fp16 (16-byte aligned rows), qws e4m3 strip layout.
 int qtts_launch_fp8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
                                  int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
-                                 hipStream_t st) {
+                                 int waves, hipStream_t st) {
   int W, C;
-  if (!qtts_fp8_fused_ok(m, n, k) || !fused_cfg(n, k, W, C))
-    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fused fp8 linear: unsupported shape m=%lld k=%lld",
-                          (long long)m, (long long)k);
+  if (!qtts_fp8_fused_ok(m, n, k, waves) || !fused_cfg(m, n, k, waves, W, C))
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fused fp8 linear: unsupported shape m=%lld k=%lld waves=%d",
+                          (long long)m, (long long)k, waves);
   const unsigned blocks = (unsigned)((n + 15) / 16);
   const int strips = (int)blocks;
-#define QTTS_F8F(XT, WV, CV)                                                                                     \
-  qtts::launch(&fp8_linear_fused_kernel<XT, WV, CV, kFusedMaxRows>, dim3(blocks), dim3(WV * 64), 0, st,          \
-               (const XT*)x, (int)m, (int)k, ldx, qws, (int)n, sw, (const XT*)bias, (XT*)y, ldy, strips, div_mode)
-#define QTTS_F8F_W(XT, CV)                     \
+  const int RM = m <= 1 ? 1 : (m <= 4 ? 4 : 8);
+#define QTTS_F8F(XT, WV, CV, RMV)                                                                          \
+  qtts::launch(&fp8_linear_fused_kernel<XT, WV, CV, RMV>, dim3(blocks), dim3(WV * 64), 0, st, (const XT*)x,  \
+               (int)m, (int)k, ldx, qws, (int)n, sw, (const XT*)bias, (XT*)y, ldy, strips, div_mode)
+#define QTTS_F8F_RM(XT, WV, CV)                \
   do {                                         \
-    switch (W) {                               \
-      case 1: QTTS_F8F(XT, 1, CV); break;      \
-      case 2: QTTS_F8F(XT, 2, CV); break;      \
-      case 4: QTTS_F8F(XT, 4, CV); break;      \
-      case 8: QTTS_F8F(XT, 8, CV); break;      \
-      default: QTTS_F8F(XT, 16, CV); break;    \
-    }                                          \
+    if (RM == 1) QTTS_F8F(XT, WV, CV, 1);      \
+    else if (RM == 4) QTTS_F8F(XT, WV, CV, 4); \
+    else QTTS_F8F(XT, WV, CV, 8);              \
   } while (0)
-  if (x_dtype == QTTS_BF16) {
-    if (C == 2) QTTS_F8F_W(bf16_t, 2);
-    else QTTS_F8F_W(bf16_t, 3);
-  } else {
-    if (C == 2) QTTS_F8F_W(f16_t, 2);
-    else QTTS_F8F_W(f16_t, 3);
-  }
+#define QTTS_F8F_C(XT, WV)                    \
+  do {                                        \
+    if (C == 1) QTTS_F8F_RM(XT, WV, 1);       \
+    else if (C == 2) QTTS_F8F_RM(XT, WV, 2);  \
+    else QTTS_F8F_RM(XT, WV, 3);              \
+  } while (0)
+#define QTTS_F8F_W(XT)                     \
+  do {                                     \
+    switch (W) {                           \
+      case 1: QTTS_F8F_C(XT, 1); break;    \
+      case 2: QTTS_F8F_C(XT, 2); break;    \
+      case 4: QTTS_F8F_C(XT, 4); break;    \
+      case 8: QTTS_F8F_C(XT, 8); break;    \
+      default: QTTS_F8F_C(XT, 16); break; \
+    }                                      \
+  } while (0)
+  if (x_dtype == QTTS_BF16) QTTS_F8F_W(bf16_t);
+  else QTTS_F8F_W(f16_t);
 #undef QTTS_F8F_W
+#undef QTTS_F8F_C
+#undef QTTS_F8F_RM
 #undef QTTS_F8F
   return qtts_check_launch("fp8_linear_fused");
 }

@@ -33,24 +33,6 @@
 
 namespace qtts {
 
-template <int CTRL> __device__ __forceinline__ float dpp_max(float v) {
-  return fmaxf(v, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF,
-                                                                        false)));
-}
-
-// Max over each aligned group of G lanes (16, 32 or 64), in every lane of the group:
-// within rows of 16 by DPP (swap neighbours, swap pairs, mirror half rows, mirror rows),
-// across rows by lane swizzles.
-template <int G> __device__ __forceinline__ float group_max(float v) {
-  v = dpp_max<0xB1>(v);   // quad_perm [1, 0, 3, 2]
-  v = dpp_max<0x4E>(v);   // quad_perm [2, 3, 0, 1]
-  v = dpp_max<0x141>(v);  // row_half_mirror
-  v = dpp_max<0x140>(v);  // row_mirror
-  if constexpr (G >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
-  if constexpr (G >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
-  return v;
-}
-
 // The stand-alone kernel's code (int8_act_code, IEEE x / s) from the reciprocal
 // rs = RN(1 / s): q0 = RN(x rs), the residual x - q0 s exact in one FMA, one FMA step
 // (Markstein) gives the correctly rounded quotient for a normal s.  |x / s| <= 127.3
