@@ -164,7 +164,13 @@ def kernel_ms(ops, launches, reps: int) -> float:
 
 def cpu_baseline_w8a16(torch, stack, xs, ms, budget_s: float, layers_sample: int):
     from oracle import cpu_path
-    threads = torch.get_num_threads()
+    # One thread per core this process may run on, capped by OMP_NUM_THREADS where the host
+    # sets it (a GPU box's CPU share can be smaller than its affinity mask).
+    threads = len(os.sched_getaffinity(0))
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        threads = max(1, min(threads, int(os.environ["OMP_NUM_THREADS"])))
+    saved_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
     sample = [e for e in stack if e["layer"] < layers_sample]
     cpu = [(e, e["q"].cpu(), e["s"].cpu()) for e in sample]
     xcpu = {key: v.cpu() for key, v in xs.items()}
@@ -185,6 +191,7 @@ def cpu_baseline_w8a16(torch, stack, xs, ms, budget_s: float, layers_sample: int
                     break
             total_s += statistics.median(ts)
             total_bytes += w8a16_bytes(m, e["n"], e["k"])
+    torch.set_num_threads(saved_threads)
     return {
         "value": round(total_bytes / total_s / 1e9, 3),
         "unit": "GB/s",
@@ -192,7 +199,8 @@ def cpu_baseline_w8a16(torch, stack, xs, ms, budget_s: float, layers_sample: int
         "kind": "port",
         "sample": (f"reference CPU path F.linear(x_bf16, q.to(bf16)*scale[:,None]) (oracle/cpu_path.py) on "
                    f"{layers_sample} of 28 talker layers x 4 linears x M in {list(ms)}, median of up to 10 "
-                   f"after 3 warm-ups, torch CPU with {threads} threads; "
+                   f"after 3 warm-ups, torch CPU with {threads} threads (len(os.sched_getaffinity(0)) "
+                   f"= {len(os.sched_getaffinity(0))}, OMP_NUM_THREADS = {os.environ.get('OMP_NUM_THREADS')}); "
                    f"{total_s * 1e3:.1f} ms for {total_bytes / 1e6:.1f} MB"),
     }
 
@@ -501,39 +509,6 @@ def run_mlp(args, torch, ops):
                                     "M": list(ms)}, "per_m": per_m}
 
 
-def make_chain_inputs(torch, ops, stack, layers, m, attn, norms):
-    """Buffers and chain links of the decode step as the talker runs it (qtts/models/talker.py:246-271):
-    launch 0 is input_layernorm + qkv_proj of layer 0; launch l + 1 runs layer l's o_proj + residual,
-    post_attention_layernorm + gate_up_proj + SiLU * mul, down_proj + residual and layer l + 1's
-    input_layernorm + qkv_proj.  The attention between qkv and o is not part of this path: every
-    layer's o_proj reads the same synthetic attention output ``attn``."""
-    L = ops.ChainLink
-    bf = dict(dtype=torch.bfloat16, device="cuda")
-    g = torch.Generator(device="cuda").manual_seed(17 + m)
-    h_in = torch.randn(m, 2048, generator=g, device="cuda").to(torch.bfloat16)
-    qkv = [torch.empty(m, 4096, **bf) for _ in range(layers)]
-    h1 = [torch.empty(m, 2048, **bf) for _ in range(layers)]
-    act = [torch.empty(m, 6144, **bf) for _ in range(layers)]
-    h2 = [torch.empty(m, 2048, **bf) for _ in range(layers)]
-    ent = lambda layer, i: stack[4 * layer + i]  # noqa: E731  (qkv, o, gate_up, down)
-    w_in, w_post = norms
-    launches = [[L(h_in, ent(0, 0)["qs"], 4096, ent(0, 0)["s"], qkv[0], prologue=ops.PRO_RMS_NORM,
-                   norm_weight=w_in[0])]]
-    for layer in range(layers):
-        h_prev = h_in if layer == 0 else h2[layer - 1]
-        links = [L(attn, ent(layer, 1)["qs"], 2048, ent(layer, 1)["s"], h1[layer], epilogue=ops.EPI_RESIDUAL,
-                   residual=h_prev),
-                 L(h1[layer], ent(layer, 2)["qs"], 12288, ent(layer, 2)["s"], act[layer], prologue=ops.PRO_RMS_NORM,
-                   norm_weight=w_post[layer], epilogue=ops.EPI_SILU_MUL, after=0),
-                 L(act[layer], ent(layer, 3)["qs"], 2048, ent(layer, 3)["s"], h2[layer], epilogue=ops.EPI_RESIDUAL,
-                   residual=h1[layer], after=1)]
-        if layer + 1 < layers:
-            links.append(L(h2[layer], ent(layer + 1, 0)["qs"], 4096, ent(layer + 1, 0)["s"], qkv[layer + 1],
-                           prologue=ops.PRO_RMS_NORM, norm_weight=w_in[layer + 1], after=2))
-        launches.append(links)
-    return h_in, launches
-
-
 def layer_flows(torch, ops, stack, layers, eps=1e-6):
     """The talker decode step's linears with their data flow (qtts/models/talker.py:246-271) as
     callables of (h_in, attn): one fused kernel per linear (input_layernorm + qkv_proj, o_proj +
@@ -574,80 +549,6 @@ def layer_flows(torch, ops, stack, layers, eps=1e-6):
     return {"fused": fused, "bf16": bf16}, (w_in, w_post)
 
 
-def run_talker_chain(args, torch, ops):
-    """The talker decode step's linears with their real data flow, int8 weight-only, 28 layers,
-    M in {1, 2, 4, 8}, three ways: one fused kernel per linear (input_layernorm + qkv_proj,
-    o_proj + residual, post_attention_layernorm + gate_up_proj + SiLU * mul, down_proj +
-    residual: qtts_w8a16_fused_gemm_strips and qtts_w8a16_gate_up_silu_strips), one persistent
-    chain launch per layer (qtts_w8a16_chain_strips), and bf16 torch (hipBLASLt F.linear,
-    F.rms_norm, F.silu, adds).  The attention between qkv_proj and o_proj is not part of the
-    path; o_proj reads a fixed synthetic attention output."""
-    ms = (1, 2, 4, 8)
-    layers = 28
-    log(f"[bench] packing {layers}x4 talker weights (int8 + bf16 baseline copy)")
-    stack = make_stack(torch, ops, TALKER, layers, keep_bf16=True)
-    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
-    flows, (w_in, w_post) = layer_flows(torch, ops, stack, layers)
-    xs = make_inputs(torch, [2048], ms)
-    nbytes_of = {m: sum(w8a16_bytes(m, e["n"], e["k"]) for e in stack) for m in ms}
-
-    per_m = {}
-    total_bytes, total_ms = 0, 0.0
-    layer_bytes, layer_ms = [], []
-    for m in ms:
-        attn = xs[(m, 2048)]
-        h_in, launches = make_chain_inputs(torch, ops, stack, layers, m, attn, (w_in, w_post))
-        plans = [ops.ChainPlan(links) for links in launches]
-        g_c = capture(torch, lambda: [plan() for plan in plans])
-        g_p = capture(torch, lambda: flows["fused"](h_in, attn))
-        g_b = capture(torch, lambda: flows["bf16"](h_in, attn))
-        t_c = time_graph(torch, g_c, args.steps, args.warmup)
-        t_p = time_graph(torch, g_p, args.steps, args.warmup)
-        t_b = time_graph(torch, g_b, max(5, args.steps // 2), args.warmup)
-        if any(plan.timed_out() for plan in plans):
-            raise RuntimeError("a chain launch gave up waiting for a link")
-        full = [plan for plan, links in zip(plans, launches) if len(links) == 4]
-        dur = kernel_ms(ops, full, reps=2)
-        layer_ms.append(dur)
-        layer_bytes.append(sum(w8a16_bytes(m, ln.n, ln.x.shape[1]) for ln in launches[1]))
-        nbytes = nbytes_of[m]
-        total_bytes += nbytes
-        total_ms += t_c
-        per_m[str(m)] = {
-            "chain_us": round(t_c * 1e3, 2),
-            "GBps": round(nbytes / (t_c * 1e-3) / 1e9, 1),
-            "pct_of_hbm_peak": round(100 * nbytes / (t_c * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1),
-            "per_linear_fused_us": round(t_p * 1e3, 2),
-            "bf16_torch_us": round(t_b * 1e3, 2),
-            "chain_vs_per_linear": round(t_p / t_c, 3),
-            "chain_vs_bf16": round(t_b / t_c, 3),
-            "chain_launch_us": round(dur * 1e3, 3),
-        }
-        del g_c, g_p, g_b
-        log(f"[bench] chain M={m}: {per_m[str(m)]}")
-    dur_ms = statistics.mean(layer_ms)
-    lb = statistics.mean(layer_bytes)
-    achieved = lb / (dur_ms * 1e-3) / 1e9
-    return {
-        "metric": "int8 W-only decode GEMM HBM GB/s (% of peak) + linear-stack us/step, M=1..8",
-        "value": round(total_bytes / (total_ms * 1e-3) / 1e9, 1),
-        "unit": "GB/s",
-        "pct_of_hbm_peak": round(100 * total_bytes / (total_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 1),
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(total_ms, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "int8 weights x bf16 activations, fp32 accumulate",
-        "data": "synthetic (seeded N(0,0.02) weights per layer, N(0,1) bf16 activations)",
-        "config": {"workload": "talker decode step's linears with their data flow: 28 layers x {norm+qkv, "
-                               "o+residual, norm+gate_up+silu*mul, down+residual}, one chain launch per layer, "
-                               "one HIP graph per M", "layers": layers, "M": list(ms)},
-        "per_m": per_m,
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "w8a16_chain_kernel (o, gate_up, down, next qkv of one layer; M in 1,2,4,8)",
-                     "avg_launch_us": round(dur_ms * 1e3, 3), "bytes_per_launch": round(lb)},
-    }
-
-
 def run_traffic_probe(args, torch, ops):
     """Kernels for a rocprofv3 --pmc pass: a 256 MiB device copy (known bytes, the counters' scale)
     and the dominant kernel of configs[1] (gate_up over its 28 distinct weights at M = 1, 2, 4, 8),
@@ -665,6 +566,116 @@ def run_traffic_probe(args, torch, ops):
     torch.cuda.synchronize()
     return {"probe": "traffic", "copy_bytes_each_way": src.numel() * 2, "gate_up_launches": len(ms) * len(stack),
             "gate_up_algorithmic_bytes_mean": round(statistics.mean(w8a16_bytes(m, 12288, 2048) for m in ms))}
+
+
+def run_calibration(args, torch, ops):
+    """The per-bucket calibration of the int8 weight-only method on the 8 talker and code-predictor
+    shapes: at every row bucket the callers produce, the fastest quantized route (skinny / tile
+    kernel configuration, or the prefill route) against F.linear on the bf16 weight (hipBLASLt),
+    each timed as 10 calls in a HIP graph (qtts/quant/calibrate.py:40-63), and the layer verdict
+    taken over the decode buckets."""
+    from qtts_amd.quant import calibrate
+    from qtts_amd.quant.int8 import Int8WeightOnlyMethod, M_BUCKETS
+    from qtts_amd.layers.linear import LinearBase
+    calibrate.clear_cache()
+    method = Int8WeightOnlyMethod(calibrate=True, calibration_batch=16)
+    shapes = [("talker_" + nm, n, k) for nm, n, k in TALKER] + [("predictor_" + nm, n, k) for nm, n, k in PREDICTOR]
+    out = {}
+    worst = None
+    for name, n, k in shapes:
+        lin = LinearBase(k, n, dtype=torch.bfloat16, device="cuda")
+        g = torch.Generator(device="cuda").manual_seed(n + k)
+        lin.weight.data.copy_((torch.randn(n, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16))
+        method.process_weights(lin)
+        rep = method.calibration_report[(n, k)]
+        rows = {}
+        for b in M_BUCKETS:
+            r = rep[b]
+            if r["reference"] is None or r["best"] is None:
+                rows[str(b)] = None
+                continue
+            t = r["timings"][r["best"]]
+            ratio = r["reference"] / t
+            rows[str(b)] = {"best": r["best"], "us": round(t * 1e6, 2), "bf16_us": round(r["reference"] * 1e6, 2),
+                            "speedup": round(ratio, 3)}
+            if worst is None or ratio < worst[0]:
+                worst = (ratio, name, b)
+        out[name] = {"converted": method.applies_to(lin), "buckets": rows}
+        log(f"[bench] calibration {name}: " + ", ".join(f"{b}:{v['speedup'] if v else None}" for b, v in rows.items()))
+    return {"probe": "calibration", "config": {"workload": "int8 weight-only per-bucket calibration, talker and "
+                                                           "code-predictor shapes, buckets " + str(list(M_BUCKETS))},
+            "worst_speedup": {"speedup": round(worst[0], 3), "shape": worst[1], "rows": worst[2]} if worst else None,
+            "shapes": out}
+
+
+def run_floor(args, torch, ops):
+    """The floor of one kernel per linear on this GPU, next to the GEMM stack it bounds.
+
+    * empty: 112 empty launches in one HIP graph (1, 128 and 768 workgroups of 4 waves):
+      the cost of a launch boundary alone.
+    * stream: the configs[1] stack's memory traffic without its arithmetic -- 28 layers x
+      {qkv 8 MiB, o 4 MiB, gate_up 24 MiB, down 12 MiB} streamed by qtts_probe_stream from
+      distinct slices of one 1.31 GiB buffer (5x the 256 MB Infinity Cache, so every byte
+      comes from HBM), one HIP graph of 112 launches, for several (waves a workgroup, 1 KiB
+      loads a wave) shapes; `best` takes the fastest shape per linear.
+    * gemm: the configs[1] int8 W8A16 stack itself (automatic kernel choice) at M = 1 and 8.
+    Per-launch durations by linear come from a rocprofv3 kernel trace of this mode."""
+    sizes = [(name, n * k) for name, n, k in TALKER]
+    layers = 28
+    layer_bytes = sum(b for _, b in sizes)
+    buf = torch.randint(-128, 128, (layers * layer_bytes,), dtype=torch.int8, device="cuda")
+    sink = torch.empty(max(b for _, b in sizes) // 1024, dtype=torch.int32, device="cuda")
+    offs = []
+    for layer in range(layers):
+        o = layer * layer_bytes
+        for name, b in sizes:
+            offs.append((name, o, b))
+            o += b
+    steps = max(5, args.steps)
+    out = {"empty_us_per_launch": {}, "stream_stack_us": {}}
+    for wgs in (1, 128, 768):
+        g = capture(torch, lambda: [ops.probe_empty(wgs, 4) for _ in range(112)])
+        out["empty_us_per_launch"][str(wgs)] = round(time_graph(torch, g, steps, args.warmup) * 1e3 / 112, 3)
+        del g
+    shapes = [(1, 16), (2, 8), (2, 16), (4, 4), (4, 8), (4, 16), (8, 2), (8, 4), (8, 8), (16, 1), (16, 2), (16, 4)]
+    per_kind = {}
+    for waves, loads in shapes:
+        key = f"w{waves}_l{loads}"
+        g = capture(torch, lambda: [ops.probe_stream(buf[o:o + b], b, waves, loads, sink) for _, o, b in offs])
+        t = time_graph(torch, g, steps, args.warmup)
+        out["stream_stack_us"][key] = round(t * 1e3, 2)
+        del g
+        # each linear's size alone: consecutive slices of that size over the whole buffer (28
+        # slices of o would be only 112 MiB, resident in the Infinity Cache after one replay)
+        for name, b in sizes:
+            mine = [(o, b) for o in range(0, buf.numel() - b + 1, b)]
+            g = capture(torch, lambda: [ops.probe_stream(buf[o:o + b], b, waves, loads, sink) for o, b in mine])
+            t_k = time_graph(torch, g, steps, args.warmup) * 1e3 / len(mine)
+            del g
+            per_kind.setdefault(name, {})[key] = round(t_k, 3)
+    out["stream_us_per_launch"] = per_kind
+    best = {name: min(v.items(), key=lambda kv: kv[1]) for name, v in per_kind.items()}
+    out["stream_best_shape"] = {name: kv[0] for name, kv in best.items()}
+    plan = {name: tuple(int(t[1:]) for t in kv[0].split("_")) for name, kv in best.items()}
+    g = capture(torch, lambda: [ops.probe_stream(buf[o:o + b], b, *plan[n_], sink) for n_, o, b in offs])
+    out["stream_stack_best_us"] = round(time_graph(torch, g, steps, args.warmup) * 1e3, 2)
+    del g, buf
+    torch.cuda.empty_cache()
+
+    stack = make_stack(torch, ops, TALKER, layers, keep_bf16=False)
+    ops.reserve_workspace(torch.device("cuda"), max(
+        ops.workspace_bytes(ops.OP_W8A16, m, e["n"], e["k"]) for m in (1, 8) for e in stack[:4]))
+    xs = make_inputs(torch, [k for _, _, k in TALKER], (1, 8))
+    out["gemm_stack_us"] = {}
+    for m in (1, 8):
+        g = capture(torch, lambda: [ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"]) for e in stack])
+        out["gemm_stack_us"][str(m)] = round(time_graph(torch, g, steps, args.warmup) * 1e3, 2)
+        del g
+    nbytes = sum(e["n"] * e["k"] for e in stack)
+    out["weight_bytes"] = nbytes
+    out["stream_best_GBps"] = round(nbytes / (out["stream_stack_best_us"] * 1e-6) / 1e9, 1)
+    return {"probe": "floor", "config": {"workload": "configs[1] talker stack memory traffic (28 x 4 linears, "
+                                                     "1.41 GB int8), streamed without arithmetic"}, **out}
 
 
 def summarize_pmc(path: str) -> None:
@@ -737,8 +748,10 @@ def main() -> int:
                     help="time the configs[1] decode stack with fp8 weight-only weights instead of a config")
     ap.add_argument("--mlp", action="store_true",
                     help="time the talker MLP (gate_up, silu*up, down) with the activation fused into down")
-    ap.add_argument("--chain", action="store_true",
-                    help="time the talker decode step's linears as one chain launch per layer")
+    ap.add_argument("--calibration", action="store_true",
+                    help="print the int8 weight-only per-bucket calibration against hipBLASLt on the model shapes")
+    ap.add_argument("--floor", action="store_true",
+                    help="time the launch and streaming floor of one kernel per linear next to the configs[1] stack")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="launch only the kernels a rocprofv3 --pmc pass measures (copy + gate_up)")
     args = ap.parse_args()
@@ -765,14 +778,16 @@ def main() -> int:
     runner = {0: run_single_linear, 1: run_talker_stack, 2: run_predictor, 3: run_prefill, 4: run_fp8}[args.config]
     if args.traffic_probe:
         runner = run_traffic_probe
+    if args.floor:
+        runner = run_floor
+    if args.calibration:
+        runner = run_calibration
     if args.int8_w8a8:
         runner = run_int8_w8a8
     if args.fp8w:
         runner = run_fp8w_stack
     if args.mlp:
         runner = run_mlp
-    if args.chain:
-        runner = run_talker_chain
     with torch.inference_mode():
         result = runner(args, torch, ops)
     result["device"] = torch.cuda.get_device_name()

@@ -245,79 +245,6 @@ int qtts_w8a16_gate_up_silu_strips(const void* x, int x_dtype, int64_t m, int64_
                                    const void* bias, void* act, int64_t ldact, int algo, void* ws,
                                    int64_t ws_bytes, void* stream);
 
-/* --- a chain of dependent decode linears in one launch ------------------------------ */
-
-#define QTTS_CHAIN_MAX_LINKS 8
-#define QTTS_CHAIN_MAX_ROWS 8
-#define QTTS_CHAIN_MAX_ITEMS 65536
-/* A chain's control block (qtts_w8a16_chain_ctl_bytes): a timeout flag at byte
- * QTTS_CHAIN_TIMEOUT_BYTE (sticky: set when a wait gave up, cleared only by the caller),
- * then one completion flag per work item, QTTS_CHAIN_FLAG_STRIDE bytes apart, from byte
- * QTTS_CHAIN_FLAGS_BYTE. */
-#define QTTS_CHAIN_TIMEOUT_BYTE 0
-#define QTTS_CHAIN_FLAGS_BYTE 256
-#define QTTS_CHAIN_FLAG_STRIDE 256
-
-/* What a chain link does with its output. */
-typedef enum {
-    QTTS_EPI_STORE = 0,     /* y = linear(h) */
-    QTTS_EPI_RESIDUAL = 1,  /* y = dtype(f32(residual) + f32(dtype(linear(h)))) */
-    QTTS_EPI_SILU_MUL = 2   /* y[:, c] = dtype(dtype(silu(g)) * u), g = dtype(linear(h))[:, c],
-                               u = dtype(linear(h))[:, n/2 + c]: y is [m, n/2] */
-} qtts_epilogue;
-
-/* One W8A16 linear of a chain (qtts_w8a16_chain_strips).
- *   h = x                         (prologue QTTS_PRO_NONE)
- *   h = qtts_rms_norm(x, norm_weight, eps)   (QTTS_PRO_RMS_NORM; sums in another order)
- * x: [m, k] of x_dtype, 16-byte aligned rows (stride ldx).  qs: int8 strip weights of
- * [n, k] (qtts_to_strips, QTTS_STRIP_INT8).  scale [n] of scale_dtype, bias [n] of
- * x_dtype or NULL.  residual: [m, n] of x_dtype, 8-byte aligned rows (stride ldr); may be
- * y itself.  y: 8-byte aligned rows (stride ldy).  after: the index of an earlier link
- * whose output this link reads (x or residual), or -1; links that write what another
- * link reads must be ordered through `after` (directly or transitively), and so must a
- * link that overwrites what another one reads. */
-typedef struct {
-    const void* x;
-    int64_t ldx;
-    const int8_t* qs;
-    int64_t n, k;
-    const void* scale;
-    const void* bias;
-    int prologue;
-    const void* norm_weight;
-    float eps;
-    int epilogue;
-    const void* residual;
-    int64_t ldr;
-    void* y;
-    int64_t ldy;
-    int after;
-} qtts_chain_link;
-
-/* Bytes of the control block a chain of these links needs (negative: invalid chain). */
-int64_t qtts_w8a16_chain_ctl_bytes(const qtts_chain_link* links, int count, int64_t m);
-
-/* The linears of a talker decoder layer between two attention calls
- * (qtts/models/talker.py:246-271): o_proj with the residual add, gate_up_proj after
- * post_attention_layernorm with GatedMLP's SiLU * mul (qtts/layers/activation.py:142-147),
- * down_proj with the residual add, and the next layer's qkv_proj after its
- * input_layernorm, in ONE persistent launch of the W8A16 GEMM arithmetic
- * (qtts/quant/kernels.py:113-135): each linear's weights stream in while the link it
- * waits for finishes.  No counterpart in the reference, which launches one kernel per
- * linear, norm and activation; results are those of the separate calls within the
- * GEMM tolerance (the K split differs).  x_dtype bf16 (QTTS_ERR_UNSUPPORTED otherwise),
- * scale_dtype bf16 or fp32.  count 1..8 links, m 0..8 rows, n % 16 == 0, k % 64 == 0,
- * k <= 8192 (k <= 3072 with QTTS_EPI_SILU_MUL, which also needs n % 32 == 0).
- * ctl: this chain's own control block, 256-byte aligned, zero-filled before its first
- * launch and used by launches of this same chain only (the same links, rows and algo;
- * no clearing between launches or graph replays).  algo bits 8-23: workgroups (0, or
- * more than fit on the device at once: as many as fit).  Every workgroup must be
- * resident together, so a chain must not share the device with a concurrent persistent
- * kernel that waits on it; a wait that cannot end gives up after about a second and
- * raises the timeout flag.  Launches of one chain must be ordered (one stream). */
-int qtts_w8a16_chain_strips(const qtts_chain_link* links, int count, int x_dtype, int scale_dtype,
-                            int64_t m, int algo, void* ctl, int64_t ctl_bytes, void* stream);
-
 /* --- fp8 W8A8 --------------------------------------------------------------------- */
 
 /* Per-token e4m3 activation quantization, replacing the activation half of
@@ -341,7 +268,16 @@ int qtts_w8a8_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t k,
 
 /* The whole of Fp8Method.apply (qtts/quant/fp8.py:72-89) in one call:
  * qtts_quant_act_fp8_rows into the workspace, then qtts_w8a8_fp8_gemm.
- * x: [m, k] of x_dtype; y: [m, n] of x_dtype; bias: [n] of x_dtype or NULL. */
+ * x: [m, k] of x_dtype; y: [m, n] of x_dtype, not overlapping x; bias: [n] of x_dtype
+ * or NULL.  Workspace: qtts_workspace_bytes(QTTS_OP_FP8_LINEAR).
+ * Decode rows on strip weights (qtts_fp8_linear_strips) with bf16 / fp16 activations in
+ * 16-byte aligned rows, 1 <= m <= 8 and k % 128 == 0, k <= 6144, run ONE kernel that
+ * quantizes x inside the GEMM, with the same output bits as the two-kernel path and no
+ * workspace (ws may be NULL): automatically for m <= 3, or m <= 8 with k <= 2048; and for
+ * any such m when algo is QTTS_ALGO_AUTO or QTTS_ALGO_SKINNY with only bits 16-23 set, which
+ * then give that kernel's waves per workgroup (a power of two up to 16 with
+ * 3 * waves >= k / 128).  Any split count (bits 8-15) or chunk count (bits 24-29) keeps
+ * the two-kernel path. */
 int qtts_fp8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
                     const uint8_t* qw, int64_t n, int64_t ldqw, const float* sw,
                     const void* bias, void* y, int64_t ldy, int div_mode,
@@ -389,11 +325,11 @@ int qtts_w8a8_int8_gemm(const int8_t* qx, const float* sx, int64_t m, int64_t k,
 /* The whole of Int8Method.apply (qtts/quant/int8.py:145-160) in one call:
  * qtts_quant_act_int8_rows into the workspace, then qtts_w8a8_int8_gemm.  The
  * reference's padding to 17 rows for torch._int_mm (int8.py:150-155) has no
- * counterpart: every m runs as is.  x: [m, k] of x_dtype; y: [m, n] of x_dtype;
- * bias: [n] of x_dtype or NULL.  Workspace: qtts_workspace_bytes(QTTS_OP_INT8_LINEAR).
+ * counterpart: every m runs as is.  x: [m, k] of x_dtype; y: [m, n] of x_dtype, not
+ * overlapping x; bias: [n] of x_dtype or NULL.  Workspace: qtts_workspace_bytes(QTTS_OP_INT8_LINEAR).
  * With strip weights, bf16 / fp16 activations (16-byte aligned rows), m <= 8 and
  * k % 64 == 0, k <= 8192, one kernel quantizes inside the GEMM, with the same output
- * bits and no workspace: automatically while the per-CU quantization work is small
+ * bits and no workspace (ws may be NULL): automatically while the per-CU quantization work is small
  * (every workgroup quantizes all m x k activations), or always when algo is
  * QTTS_ALGO_SKINNY with only a wave count (a power of two up to 16) set.  Any split
  * count keeps the two-kernel path. */
@@ -439,6 +375,19 @@ int qtts_fp8w_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int6
  * threads all land in the same pool. */
 int qtts_kernel_timer_begin(int max_launches);
 int qtts_kernel_timer_end(double* total_ms, int64_t* launches, int64_t* untimed);
+
+/* Measurement kernels (bench.py --floor).  No counterpart in the reference: they bound
+ * what one kernel per linear can reach on this GPU, for the roofline the decode GEMMs
+ * are held to.
+ * qtts_probe_stream reads `bytes` from src (16-byte aligned) the way the decode GEMMs
+ * stream weights: workgroups of `waves` waves (1..16); wave w of workgroup b issues
+ * `loads` (1, 2, 4, 8 or 16) 1 KiB loads, 16 bytes a lane, for blocks
+ * (b * waves + w) * loads ... + loads - 1 before using any, and stores the xor of every
+ * 32-bit word it read to sink[b * waves + w].  bytes must be a multiple of
+ * waves * loads * 1024; sink holds bytes / (loads * 1024) words.
+ * qtts_probe_empty launches an empty kernel of `workgroups` x `waves` waves. */
+int qtts_probe_stream(const void* src, int64_t bytes, int waves, int loads, int32_t* sink, void* stream);
+int qtts_probe_empty(int64_t workgroups, int waves, void* stream);
 
 #ifdef __cplusplus
 }

@@ -141,43 +141,18 @@ def test_kernel_timer_argument_checks():
     assert L.qtts_kernel_timer_end(None, ctypes.byref(n), ctypes.byref(u)) == _lib.ERR_INVALID_ARGUMENT
 
 
-def test_chain_argument_checks():
-    """qtts_w8a16_chain_strips rejects bad chains before any device use."""
+def test_probe_argument_checks():
+    """The measurement kernels reject bad shapes before any device use."""
     L = _lib.load()
-    links = (_lib.ChainLinkC * 2)()
-    for i, c in enumerate(links):
-        c.x, c.ldx, c.qs, c.n, c.k = 4096 * (i + 1), 2048, 1 << 20, 2048, 2048
-        c.scale, c.y, c.ldy, c.after = 1 << 21, 1 << 22, 2048, i - 1
-        c.epilogue, c.prologue = _lib.EPI_STORE, _lib.PRO_NONE
-    ctl = 1 << 24
-    # 2048 / 16 strips, 2 strips an item at k = 2048 (4 waves of 8 chunks a strip): 64 items a link
-    need = _lib.CHAIN_FLAGS_BYTE + 256 * 128
-    assert L.qtts_w8a16_chain_ctl_bytes(links, 2, 1) == need
-
-    def call(count=2, x_dtype=_lib.BF16, s_dtype=_lib.BF16, m=1, ctl_ptr=ctl, ctl_bytes=need):
-        return L.qtts_w8a16_chain_strips(links, count, x_dtype, s_dtype, m, 0, ctl_ptr, ctl_bytes, None)
-
-    assert call(count=0) == _lib.ERR_INVALID_ARGUMENT
-    assert call(count=_lib.CHAIN_MAX_LINKS + 1) == _lib.ERR_INVALID_ARGUMENT
-    assert call(x_dtype=_lib.F16) == _lib.ERR_UNSUPPORTED
-    assert call(s_dtype=_lib.F16) == _lib.ERR_INVALID_ARGUMENT
-    assert call(m=_lib.CHAIN_MAX_ROWS + 1) == _lib.ERR_INVALID_ARGUMENT
-    assert call(ctl_ptr=None) == _lib.ERR_WORKSPACE
-    assert call(ctl_bytes=need - 4) == _lib.ERR_WORKSPACE
-    assert call(ctl_ptr=ctl + 4) == _lib.ERR_WORKSPACE  # 256-byte aligned
-    links[1].after = 1
-    assert call() == _lib.ERR_INVALID_ARGUMENT and "earlier link" in _lib.last_error()
-    assert L.qtts_w8a16_chain_ctl_bytes(links, 2, 1) == _lib.ERR_INVALID_ARGUMENT
-    links[1].after = 0
-    links[1].k = 2048 + 32
-    assert call() == _lib.ERR_INVALID_ARGUMENT
-    links[1].k = 6144  # the SiLU epilogue pairs two strips an item: k <= 3072
-    links[1].epilogue = _lib.EPI_SILU_MUL
-    assert call(ctl_bytes=1 << 20) == _lib.ERR_INVALID_ARGUMENT and "SiLU" in _lib.last_error()
-    links[1].k, links[1].epilogue = 2048, _lib.EPI_RESIDUAL  # residual missing
-    assert call() == _lib.ERR_INVALID_ARGUMENT
-    links[1].epilogue = _lib.EPI_STORE
-    links[1].x = 4096 + 8  # rows must be 16-byte aligned
-    assert call() == _lib.ERR_INVALID_ARGUMENT
-    links[1].x = 8192
-    assert call(m=0) == _lib.OK  # no rows: nothing to launch
+    src, sink = 1 << 20, 1 << 21  # aligned stand-in addresses: never dereferenced on a rejected call
+    assert L.qtts_probe_stream(None, 4096, 4, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
+    assert L.qtts_probe_stream(src + 8, 4096, 4, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
+    assert "aligned" in _lib.last_error()
+    assert L.qtts_probe_stream(src, 4096, 0, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
+    assert L.qtts_probe_stream(src, 4096, 17, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
+    assert L.qtts_probe_stream(src, 4096, 4, 3, sink, None) == _lib.ERR_INVALID_ARGUMENT
+    assert L.qtts_probe_stream(src, 4096 + 1024, 4, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
+    assert "multiple" in _lib.last_error()
+    assert L.qtts_probe_stream(src, 0, 4, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
+    assert L.qtts_probe_empty(0, 4, None) == _lib.ERR_INVALID_ARGUMENT
+    assert L.qtts_probe_empty(1, 17, None) == _lib.ERR_INVALID_ARGUMENT

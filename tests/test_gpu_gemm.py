@@ -529,7 +529,7 @@ def _fused_waves(n: int, k: int) -> int:
 @pytest.mark.parametrize("n,k", TALKER + PREDICTOR + [(40, 256), (1000, 128)])
 def test_fp8_linear_fused_matches_two_kernel_path(ops, n, k):
     """Decode rows (M <= 8) can take the fused kernel (quantization inside the GEMM).  Forced to a
-    wave count (the one rule picks for one row, and twice it, which it picks from two rows), it must
+    wave count (the one the automatic rule picks, which does not depend on M, and twice it), it must
     equal the two-kernel path (stand-alone quantization, bit-exact with the reference, then the GEMM
     with the same wave split, so the same accumulation order) bit for bit: any difference in the
     fused per-token scale or e4m3 codes shows.  The automatic choice at every M is within tolerance
@@ -555,11 +555,11 @@ def test_fp8_linear_fused_matches_two_kernel_path(ops, n, k):
     x = x.to(torch.float16)
     qw, sw = ops.pack_fp8(w)
     qws = ops.to_strips(qw)
-    wf = min(16, 2 * waves)  # the automatic choice at 4 rows where the fused kernel takes it
-    y = ops.fp8_linear_strips(x, qws, n, sw, None, ops.DIV_IEEE, ops.algo_code(1, 0, wf))
     qx, sx = ops.quant_act_fp8(x, ops.DIV_IEEE)
-    two = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, None, torch.float16, ops.algo_code(1, 1, wf))
-    assert torch.equal(y, two), f"fused fp16 / IEEE differs: n={n} k={k}"
+    for wf in sorted({waves, min(16, 2 * waves)}):  # the automatic wave count, and twice it
+        y = ops.fp8_linear_strips(x, qws, n, sw, None, ops.DIV_IEEE, ops.algo_code(1, 0, wf))
+        two = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, None, torch.float16, ops.algo_code(1, 1, wf))
+        assert torch.equal(y, two), f"fused fp16 / IEEE differs: n={n} k={k} W={wf}"
 
 
 @pytest.mark.parametrize("n,k", TALKER + PREDICTOR)

@@ -59,16 +59,26 @@ def test_int8_weight_only_hook(calibrate):
     assert r["excluded"] == 1 and r["converted"] + r["declined"] == 5
     if not calibrate:
         assert r["converted"] == 5 and r["bytes_after"] < r["bytes_before"]
+    else:
+        # calibrated per row bucket: every converted layer's shape has a kernel choice for every
+        # bucket the callers produce (decode rows, code-predictor rows up to 128, prefill)
+        from qtts_amd.quant.int8 import M_BUCKETS, _ALGO
+        for name in ("qkv_proj", "o_proj", "gate_up_proj", "down_proj", "text_proj_fc1"):
+            layer = getattr(model, name)
+            if layer.quant_method is not None:
+                assert all((layer.out_features, layer.in_features, b) in _ALGO for b in M_BUCKETS), name
     assert model.codec_head.quant_method is None and model.codec_head.weight.numel() > 0
-    for m in (1, 4, 8, 17):
+    ms = (1, 2, 3, 4, 8, 16, 17, 32, 48, 64, 100, 128) if calibrate else (1, 4, 8, 17)
+    for m in ms:
         x = torch.randn(m, 1, 2048, device="cuda").to(torch.bfloat16)
-        for name in ("qkv_proj", "o_proj", "text_proj_fc1", "gate_up_proj"):
+        for name in ("qkv_proj", "o_proj", "text_proj_fc1", "gate_up_proj", "down_proj"):
             layer = getattr(model, name)
             if layer.quant_method is None:
                 continue
-            y = layer(x)
+            xin = x if layer.in_features == 2048 else torch.randn(m, 1, layer.in_features, device="cuda").to(x.dtype)
+            y = layer(xin)
             assert y.shape == (m, 1, layer.out_features) and y.dtype == torch.bfloat16
-            assert_close(y.reshape(m, -1), _expected_int8(layer, x.reshape(m, -1)), f"{name} m={m}")
+            assert_close(y.reshape(m, -1), _expected_int8(layer, xin.reshape(m, -1)), f"{name} m={m}")
 
 
 def test_int8_hook_graph_capture_matches_eager():

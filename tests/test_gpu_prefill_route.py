@@ -154,31 +154,33 @@ def test_route_graph_replays_and_gated_mlp(ops, monkeypatch):
 
 
 def test_calibration_records_prefill_verdicts(ops):
-    """Both weight-only methods with calibration: a verdict per prefill bucket (the route or the
-    HIP kernel), and the layer's output at those row counts within the W8A16 bound of the HIP
-    kernel on the same codes, whichever route was kept."""
+    """Both weight-only methods with calibration: every bucket decided, the prefill route kept exactly
+    where it was the fastest candidate at a prefill bucket, and the layer's output at those row
+    counts within the W8A16 bound of the HIP kernel on the same codes, whichever route was kept."""
     from qtts_amd.quant import fp8 as P, int8 as I, prefill
-    from qtts_amd.quant.calibrate import _CACHE, clear_cache
+    from qtts_amd.quant.calibrate import clear_cache
     clear_cache()
     n, k = 12288, 2048
-    for method, table, name, kernel in (
-            (I.Int8WeightOnlyMethod(calibrate=True), I._ALGO, "int8_wo_prefill",
+    for method, table, kernel in (
+            (I.Int8WeightOnlyMethod(calibrate=True), I._ALGO,
              lambda lin, x: ops.w8a16_gemm_strips(x, lin.int8_weight, n, lin.int8_scale)),
-            (P.Fp8WeightOnlyMethod(calibrate=True), P._FP8W_ALGO, "fp8_wo_prefill",
+            (P.Fp8WeightOnlyMethod(calibrate=True), P._FP8W_ALGO,
              lambda lin, x: ops.fp8w_gemm_strips(x, lin.fp8w_weight, n, lin.fp8w_scale))):
-        for rows in prefill.PREFILL_BUCKETS:
+        for rows in method.calibration_rows:
             table.pop((n, k, rows), None)  # a verdict left by an earlier test of this shape
         lin = _layer(n, k, seed=3, bias=False)
         method.process_weights(lin)
+        report = method.calibration_report[(n, k)]
+        assert sorted(report) == list(method.calibration_rows)
         if not method.applies_to(lin):
-            continue  # declined at the calibration batch: stays on F.linear
+            continue  # declined over the decode buckets: stays on F.linear
         lin.quant_method = method
+        assert all((n, k, rows) in table for rows in method.calibration_rows), "every bucket decided"
         for rows in prefill.PREFILL_BUCKETS:
-            verdict = _CACHE[(name, n, k, rows, str(torch.bfloat16))]
-            routed = table.get((n, k, rows)) == prefill.ALGO_DEQUANT_GEMM
-            assert routed == (verdict is not None), (name, rows)
+            routed = table[(n, k, rows)] == prefill.ALGO_DEQUANT_GEMM
+            assert routed == (report[rows]["best"] == "dequant"), (method.name, rows)
             x = torch.randn(rows, k, device="cuda").to(torch.bfloat16)
             y = lin(x)
             ref = kernel(lin, x).double().cpu().numpy()
             err = np.abs(y.double().cpu().numpy() - ref)
-            assert (err <= 2 * _bound(ref, torch.bfloat16)).all(), (name, rows, routed, float(err.max()))
+            assert (err <= 2 * _bound(ref, torch.bfloat16)).all(), (method.name, rows, routed, float(err.max()))

@@ -163,3 +163,106 @@ def test_calibration_failures_are_never_fatal():
 def test_m_buckets():
     assert [bucket_of(m) for m in (1, 2, 3, 5, 9, 16, 17, 64, 65, 300, 1500, 5000)] == \
         [1, 2, 4, 8, 16, 16, 32, 64, 128, 1024, 2048, 2048]
+
+
+def _bucket_fixture(times, fail_ref_at=()):
+    """Fake per-bucket calibration inputs: labels instead of GPU work, times from ``times(label)``."""
+    calls = []
+
+    def kernel(x, algo):
+        return ("kernel", algo, x.shape[0])
+
+    def reference(x):
+        if x.shape[0] in fail_ref_at:
+            raise RuntimeError("capture failed")
+        return ("ref", None, x.shape[0])
+
+    def timer(fn):
+        label = fn()
+        calls.append(label)
+        return times(label)
+
+    def candidates(rows):
+        c = {"skinny": 1, "skinny_w8": 1 | (8 << 16)} if rows <= 64 else {}
+        if rows > 16:
+            c["tile"] = 2
+        return c
+
+    return kernel, reference, timer, candidates, calls
+
+
+def test_calibrate_buckets_decides_every_bucket():
+    """Every bucket gets its fastest route (skinny, tile or the prefill route); the layer verdict
+    is the decode buckets' sum against the reference's (qtts/quant/calibrate.py:77-114 asks the same
+    question at one row count)."""
+    calibrate.clear_cache()
+    buckets = (1, 2, 4, 8, 16, 32, 64, 128, 256, 1024, 2048)
+
+    def times(label):
+        kind, algo, rows = label
+        if kind == "ref":
+            return 10.0 + rows
+        if kind == "route":
+            return 5.0 + rows * 0.1   # beats the tile kernel at the prefill buckets
+        base = {1: 3.0, 1 | (8 << 16): 2.0, 2: 4.0}[algo]
+        return base + rows * (0.2 if algo == 2 else 1.0)  # skinny grows fast with rows, tile slowly
+
+    kernel, reference, timer, candidates, calls = _bucket_fixture(times)
+    routes = {r: {"dequant": (-1, lambda x: ("route", -1, x.shape[0]))} for r in (256, 1024, 2048)}
+    accept, table, report = calibrate.calibrate_buckets("t", 64, 128, torch.float32, torch.device("cpu"), buckets, 16,
+                                                        candidates, kernel, reference, routes, timer=timer)
+    assert accept
+    assert sorted(table) == list(buckets), "every bucket decided"
+    for rows in buckets:
+        t = report[rows]["timings"]
+        assert table[rows] == {"skinny": 1, "skinny_w8": 1 | (8 << 16), "tile": 2, "dequant": -1}[report[rows]["best"]]
+        assert t[report[rows]["best"]] == min(t.values())
+    assert table[1] == 1 | (8 << 16) and table[16] == 1 | (8 << 16)   # skinny_w8 at decode rows
+    assert table[64] == 2 and table[128] == 2                         # tile past the crossover
+    assert table[256] == -1 and table[2048] == -1                      # the prefill route wins there
+    # cached per (tag, n, k, rows, dtype): a second calibration times nothing
+    n_calls = len(calls)
+    assert calibrate.calibrate_buckets("t", 64, 128, torch.float32, torch.device("cpu"), buckets, 16, candidates,
+                                       kernel, reference, routes, timer=timer)[1] == table
+    assert len(calls) == n_calls
+
+
+def test_calibrate_buckets_verdict_from_decode_rows():
+    """The verdict sums the decode buckets: losing one bucket does not decline a layer that wins
+    the sum; losing the sum does (and records nothing); the 1.05 margin holds."""
+    calibrate.clear_cache()
+
+    def times(label):
+        kind, algo, rows = label
+        if kind == "ref":
+            return 10.0
+        return {1: 12.0, 2: 6.0, 4: 9.0, 8: 9.0}[rows] if rows <= 8 else 9.0
+
+    kernel, reference, timer, candidates, _ = _bucket_fixture(times)
+    accept, table, _ = calibrate.calibrate_buckets("v1", 8, 8, torch.float32, torch.device("cpu"), (1, 2, 4, 8, 64),
+                                                   8, candidates, kernel, reference, timer=timer)
+    assert accept and table[1] in (1, 1 | (8 << 16)) and 64 in table   # 36 * 1.05 < 40
+    calibrate.clear_cache()
+
+    def close(label):  # 4% better: inside the margin
+        return 10.0 if label[0] == "ref" else 9.6
+
+    kernel, reference, timer, candidates, _ = _bucket_fixture(close)
+    accept, table, report = calibrate.calibrate_buckets("v2", 8, 8, torch.float32, torch.device("cpu"), (1, 2, 64),
+                                                        2, candidates, kernel, reference, timer=timer)
+    assert not accept and table == {} and report[1]["best"] is not None
+
+
+def test_calibrate_buckets_failures_are_never_fatal():
+    calibrate.clear_cache()
+    kernel, reference, timer, candidates, _ = _bucket_fixture(lambda label: 1.0 if label[0] == "ref" else 0.5,
+                                                              fail_ref_at=(4,))
+    accept, table, _ = calibrate.calibrate_buckets("f", 8, 8, torch.float32, torch.device("cpu"), (1, 4, 256), 16,
+                                                   candidates, kernel, reference, timer=timer)
+    assert not accept and table == {}   # the reference failed at a decode bucket: decline
+    calibrate.clear_cache()
+    kernel, reference, timer, candidates, _ = _bucket_fixture(lambda label: 1.0 if label[0] == "ref" else 0.5,
+                                                              fail_ref_at=(256,))
+    accept, table, _ = calibrate.calibrate_buckets("g", 8, 8, torch.float32, torch.device("cpu"), (1, 4, 256), 16,
+                                                   candidates, kernel, reference, timer=timer)
+    assert accept and sorted(table) == [1, 4]   # a prefill bucket that cannot be timed stays automatic

@@ -132,6 +132,7 @@ constexpr int kMaxDevices = 64;
 std::atomic<int> g_dev_state[kMaxDevices];  // 0 unknown, 1 supported, 2 unsupported
 
 bool dtype_ok(int d) { return d == QTTS_F32 || d == QTTS_BF16 || d == QTTS_F16; }
+int64_t dtype_size(int d) { return d == QTTS_F32 ? 4 : 2; }
 bool div_ok(int d) { return d == QTTS_DIV_DEVICE || d == QTTS_DIV_IEEE; }
 bool algo_ok(int a) {
   const int f = a & 0xff;
@@ -145,6 +146,16 @@ bool ranges_overlap(const void* a, int64_t rows_a, int64_t lda, const void* b, i
                     int64_t cols, int64_t esz) {
   const uintptr_t a0 = (uintptr_t)a, a1 = a0 + (uintptr_t)(((rows_a - 1) * lda + cols) * esz);
   const uintptr_t b0 = (uintptr_t)b, b1 = b0 + (uintptr_t)(((rows_b - 1) * ldb + cols) * esz);
+  return a0 < b1 && b0 < a1;
+}
+
+// Whether an [rows_a, cols_a] matrix at a (row stride lda) and an [rows_b, cols_b] matrix
+// at b (row stride ldb), elements of esz bytes, share any byte of their spans.
+bool spans_overlap(const void* a, int64_t rows_a, int64_t lda, int64_t cols_a, const void* b, int64_t rows_b,
+                   int64_t ldb, int64_t cols_b, int64_t esz) {
+  if (rows_a <= 0 || cols_a <= 0 || rows_b <= 0 || cols_b <= 0) return false;
+  const uintptr_t a0 = (uintptr_t)a, a1 = a0 + (uintptr_t)(((rows_a - 1) * lda + cols_a) * esz);
+  const uintptr_t b0 = (uintptr_t)b, b1 = b0 + (uintptr_t)(((rows_b - 1) * ldb + cols_b) * esz);
   return a0 < b1 && b0 < a1;
 }
 
@@ -330,8 +341,11 @@ static int fp8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, int
   QTTS_REQUIRE(algo_ok(algo), "fp8_linear: bad algo %d", algo);
   QTTS_REQUIRE(ldx >= k && (layout == qtts::kLayoutStrips || ldqw >= k) && ldy >= n,
                "fp8_linear: leading dimension smaller than the row");
+  QTTS_REQUIRE(ws_bytes >= 0, "fp8_linear: negative workspace size");
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(sw && y && (k == 0 || (x && qw)), "fp8_linear: null pointer");
+  // The decode kernel has every workgroup read all of x while others write y.
+  QTTS_REQUIRE(!spans_overlap(x, m, ldx, k, y, m, ldy, n, dtype_size(x_dtype)), "fp8_linear: y overlaps x");
   // Decode rows on strip weights: quantization fused into the GEMM, one kernel, no
   // workspace.  A wave count alone (family SKINNY or AUTO, no split count or chunk
   // count) sets the fused kernel's waves; an explicit split count keeps the two-kernel path.
@@ -431,6 +445,8 @@ static int int8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, in
   QTTS_REQUIRE(ws_bytes >= 0, "int8_linear: negative workspace size");
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(sw && y && (k == 0 || (x && qw)), "int8_linear: null pointer");
+  // The decode kernel has every workgroup read all of x while others write y.
+  QTTS_REQUIRE(!spans_overlap(x, m, ldx, k, y, m, ldy, n, dtype_size(x_dtype)), "int8_linear: y overlaps x");
   // Decode rows on strip weights: quantization fused into the GEMM, one kernel, no
   // workspace.  A wave count alone (family SKINNY or AUTO, no split count or chunk
   // count) sets the fused kernel's waves; an explicit split count keeps the two-kernel path.

@@ -22,8 +22,8 @@ void launch_sk(const void* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* 
                const void* bias, void* y, int64_t ldy, float* part, unsigned* counters, const SkinnyCfg& c,
                unsigned blocks, hipStream_t st) {
   qtts::launch(&w8a16_skinny_kernel<XT, float, W, CPW, kLayoutStrips, true, 1, MX, true>, dim3(blocks),
-               dim3(W * 64), 0, st, (const XT*)x, (int)m, (int)k, ldx, (const int8_t*)qs, (int)n, (int64_t)0, scale,
-               (const XT*)bias, (XT*)y, ldy, part, counters, c.strips, c.S, c.cps, (const XT*)nullptr, 0.0f,
+               dim3(W * 64), 0, st, (const int8_t*)qs, (const XT*)x, ldx, (int)m, (int)k, c.strips, c.S, c.cps, (int)n,
+               scale, (const XT*)bias, (XT*)y, ldy, (int64_t)0, part, counters, (const XT*)nullptr, 0.0f,
                (const XT*)nullptr, (int64_t)0);
 }
 

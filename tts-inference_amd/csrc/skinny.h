@@ -65,14 +65,20 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 //   to two MFMAs, and the workgroup stores y[:, c] = XT(XT(silu(g)) * u) for g, u the
 //   linear's outputs of columns c and c + N/2 rounded to XT: y is [M, N/2].  The
 //   gate_up output itself is never stored.
+// Parameter order: everything the first loads need (q, x, ldx, M, K, strips, S, cps, N)
+// and the scale come first, in the 14 dwords the hardware preloads into SGPRs at wave
+// launch (kernarg preloading, build.py), so no kernel-argument load stands between a
+// wave's start and its weight loads.  Measured on the talker linears (cold weights, M = 1):
+// the former order, whose early values sat in two 64-byte argument lines fetched one after
+// the other, plus the split mapping's division, cost 0.6-1.2 us a launch.
 enum : int { kProNone = 0, kProSiluMul = 1, kProRmsNorm = 2 };
 
 template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1, int MX = 0, bool F8W = false,
           int PRO = kProNone, bool RES = false, bool PAIR = false>
 __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
-    const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ q, int N, int64_t ldq,
-    const ST* scale, const XT* bias, XT* y, int64_t ldy,
-    float* __restrict__ part, unsigned* __restrict__ counters, int strips, int S, int cps,
+    const int8_t* __restrict__ q, const XT* __restrict__ x, int64_t ldx, int M, int K, int strips, int S, int cps,
+    int N, const ST* scale, const XT* bias, XT* y, int64_t ldy, int64_t ldq,
+    float* __restrict__ part, unsigned* __restrict__ counters,
     const XT* __restrict__ aux, float eps, const XT* res, int64_t ldr) {
   typedef mfma16<XT> MM;
   typedef typename MM::vec V;
@@ -88,7 +94,12 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   __shared__ __align__(16) uint16_t xrow[MX > 0 ? W : 1][MX > 0 ? MX : 1][MX > 0 ? CPW * 64 : 8];
 
   int strip, split;
-  decode_wg(blockIdx.x, S, strip, split);
+  if (S == 1) {  // no split: the identity, without decode_wg's division
+    strip = blockIdx.x;
+    split = 0;
+  } else {
+    decode_wg(blockIdx.x, S, strip, split);
+  }
   if (strip >= strips) return;
 
   // wave index through readfirstlane: provably uniform, so per-wave bounds stay scalar
@@ -298,6 +309,9 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   if (wc0 < wc1) {  // wave-uniform: waves past the K range only reduce
     issue_x();
     issue(wc0);
+    // The epilogue's addresses need kernel arguments past the preloaded ones (bias, y):
+    // their scalar load must not be waited for before the last weight load is issued.
+    __builtin_amdgcn_sched_barrier(0);
     issue_epilogue();
     // Keep the scheduler from interleaving loads with the MFMAs: every load must
     // be in flight before the first wait.

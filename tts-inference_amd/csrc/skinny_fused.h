@@ -30,8 +30,8 @@ struct FusedArgs {
 template <typename XT, typename ST, int W, int CPW, int MX, int PRO, bool RES, bool PAIR = false>
 void launch_fused_one(const FusedArgs& a) {
   launch(&w8a16_skinny_kernel<XT, ST, W, CPW, kLayoutStrips, true, 1, MX, false, PRO, RES, PAIR>, dim3(a.blocks),
-         dim3(W * 64), 0, a.st, (const XT*)a.x, (int)a.m, (int)a.k, a.ldx, a.qs, (int)a.n, (int64_t)0,
-         (const ST*)a.scale, (const XT*)a.bias, (XT*)a.y, a.ldy, a.part, a.counters, a.c.strips, a.c.S, a.c.cps,
+         dim3(W * 64), 0, a.st, a.qs, (const XT*)a.x, a.ldx, (int)a.m, (int)a.k, a.c.strips, a.c.S, a.c.cps,
+         (int)a.n, (const ST*)a.scale, (const XT*)a.bias, (XT*)a.y, a.ldy, (int64_t)0, a.part, a.counters,
          (const XT*)a.aux, a.eps, (const XT*)a.res, a.ldr);
 }
 

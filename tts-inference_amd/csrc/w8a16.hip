@@ -331,8 +331,8 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
     if (!grid_ok(blocks)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16: N too large");
 #define QTTS_SK(ST, W, CPW, FK, MBV)                                                                              \
   qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, FK, MBV>, dim3((unsigned)blocks), dim3(W * 64), 0, st, \
-               x, (int)m, (int)k, ldx, q, (int)n, ldq, (const ST*)scale, bias, y, ldy, part, counters, c.strips,    \
-               c.S, c.cps, (const XT*)nullptr, 0.0f, (const XT*)nullptr, (int64_t)0)
+               q, x, ldx, (int)m, (int)k, c.strips, c.S, c.cps, (int)n, (const ST*)scale, bias, y, ldy, ldq, part,  \
+               counters, (const XT*)nullptr, 0.0f, (const XT*)nullptr, (int64_t)0)
 #define QTTS_SK_ST(W, CPW, FK, MBV)                           \
   do {                                                        \
     if (sdt == QTTS_BF16) QTTS_SK(bf16_t, W, CPW, FK, MBV);   \

@@ -38,11 +38,6 @@ ALGO_AUTO, ALGO_SKINNY, ALGO_TILE = 0, 1, 2
 OP_W8A16, OP_W8A8_FP8, OP_FP8_LINEAR, OP_W8A8_INT8, OP_INT8_LINEAR, OP_FP8W, OP_W8A16_SILU, OP_W8A16_FUSED = range(8)
 # qtts_prologue
 PRO_NONE, PRO_SILU_MUL, PRO_RMS_NORM = 0, 1, 2
-# qtts_epilogue (chain links)
-EPI_STORE, EPI_RESIDUAL, EPI_SILU_MUL = 0, 1, 2
-# chain limits and control-block layout (QTTS_CHAIN_*)
-CHAIN_MAX_LINKS, CHAIN_MAX_ROWS = 8, 8
-CHAIN_MAX_ITEMS, CHAIN_TIMEOUT_BYTE, CHAIN_FLAGS_BYTE = 65536, 0, 256
 # qtts_strip_kind
 STRIP_INT8, STRIP_FP8 = 0, 1
 # qtts_code_kind
@@ -77,10 +72,10 @@ EXPORTS = (
     "qtts_rms_norm",
     "qtts_w8a16_fused_gemm_strips",
     "qtts_w8a16_gate_up_silu_strips",
-    "qtts_w8a16_chain_ctl_bytes",
-    "qtts_w8a16_chain_strips",
     "qtts_kernel_timer_begin",
     "qtts_kernel_timer_end",
+    "qtts_probe_stream",
+    "qtts_probe_empty",
 )
 
 
@@ -92,29 +87,6 @@ def algo_code(family: int = ALGO_AUTO, splits: int = 0, waves: int = 0, cpw: int
 
 class QttsError(RuntimeError):
     pass
-
-
-class ChainLinkC(ctypes.Structure):
-    """qtts_chain_link (include/qtts_amd.h), field for field."""
-
-    _fields_ = [
-        ("x", ctypes.c_void_p),
-        ("ldx", ctypes.c_int64),
-        ("qs", ctypes.c_void_p),
-        ("n", ctypes.c_int64),
-        ("k", ctypes.c_int64),
-        ("scale", ctypes.c_void_p),
-        ("bias", ctypes.c_void_p),
-        ("prologue", ctypes.c_int),
-        ("norm_weight", ctypes.c_void_p),
-        ("eps", ctypes.c_float),
-        ("epilogue", ctypes.c_int),
-        ("residual", ctypes.c_void_p),
-        ("ldr", ctypes.c_int64),
-        ("y", ctypes.c_void_p),
-        ("ldy", ctypes.c_int64),
-        ("after", ctypes.c_int),
-    ]
 
 
 _lock = threading.Lock()
@@ -191,10 +163,6 @@ def load() -> ctypes.CDLL:
         L.qtts_w8a16_fused_gemm_strips.restype = i32
         L.qtts_w8a16_fused_gemm_strips.argtypes = [p, i32, i64, i64, i64, i32, p, ctypes.c_float, p, i64, p, i32, p,
                                                    p, i64, p, i64, i32, p, i64, p]
-        L.qtts_w8a16_chain_ctl_bytes.restype = i64
-        L.qtts_w8a16_chain_ctl_bytes.argtypes = [ctypes.POINTER(ChainLinkC), i32, i64]
-        L.qtts_w8a16_chain_strips.restype = i32
-        L.qtts_w8a16_chain_strips.argtypes = [ctypes.POINTER(ChainLinkC), i32, i32, i32, i64, i32, p, i64, p]
         L.qtts_w8a16_gate_up_silu_strips.restype = i32
         L.qtts_w8a16_gate_up_silu_strips.argtypes = [p, i32, i64, i64, i64, i32, p, ctypes.c_float, p, i64, p, i32,
                                                      p, p, i64, i32, p, i64, p]
@@ -203,6 +171,10 @@ def load() -> ctypes.CDLL:
         L.qtts_kernel_timer_end.restype = i32
         L.qtts_kernel_timer_end.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64),
                                             ctypes.POINTER(i64)]
+        L.qtts_probe_stream.restype = i32
+        L.qtts_probe_stream.argtypes = [p, i64, i32, i32, p, p]
+        L.qtts_probe_empty.restype = i32
+        L.qtts_probe_empty.argtypes = [i64, i32, p]
         version = L.qtts_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"libqtts_amd ABI version {version}, expected {ABI_VERSION}; rebuild it")

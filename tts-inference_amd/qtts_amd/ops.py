@@ -8,14 +8,12 @@ CPU or eager-PyTorch fallback: a missing library or an unsupported device raises
 
 from __future__ import annotations
 
-import dataclasses
 import threading
 
 import torch
 
 from . import _lib
-from ._lib import (ALGO_AUTO, CHAIN_MAX_LINKS, CHAIN_MAX_ROWS, CHAIN_TIMEOUT_BYTE, DIV_DEVICE,  # noqa: F401
-                   DIV_IEEE, EPI_RESIDUAL, EPI_SILU_MUL, EPI_STORE, OP_FP8_LINEAR, OP_FP8W, OP_INT8_LINEAR,
+from ._lib import (ALGO_AUTO, DIV_DEVICE, DIV_IEEE, OP_FP8_LINEAR, OP_FP8W, OP_INT8_LINEAR,  # noqa: F401
                    OP_W8A16, OP_W8A16_FUSED, OP_W8A16_SILU, OP_W8A8_FP8, OP_W8A8_INT8, PRO_NONE,
                    PRO_RMS_NORM, PRO_SILU_MUL, STRIP_FP8, STRIP_INT8, CODE_E4M3, CODE_INT8, algo_code)
 
@@ -95,6 +93,35 @@ def reserve_workspace(device: torch.device, nbytes: int) -> torch.Tensor | None:
             ws = torch.zeros(size, dtype=torch.uint8, device=torch.device("cuda", idx))
             _workspaces[idx] = ws
         return ws
+
+
+#: Rows the quant methods reserve workspace for at ``process_weights`` time, so that calls up
+#: to this many rows never allocate (decode and prefill buckets up to 2048 rows).
+WORKSPACE_ROWS = 2048
+
+
+def reserve_for_rows(device: torch.device, op: int, n: int, k: int, max_rows: int = WORKSPACE_ROWS) -> None:
+    """Reserve what ``op`` needs for an ``[N, K]`` weight at every row count up to ``max_rows``
+    (the automatic kernel choice), outside capture: load time, not the hot path."""
+    rows = sorted({r for r in (1, 2, 4, 8, 16, 32, 64, 128, 256, 512, 1024, 2048, 4096, 8192) if r <= max_rows}
+                  | {max(1, int(max_rows))})
+    reserve_workspace(device, max(workspace_bytes(op, r, n, k) for r in rows))
+
+
+def _ensure_workspace(device: torch.device, nbytes: int, what: str) -> None:
+    """Make sure the device's workspace holds ``nbytes`` before a call that needs them.  Under
+    graph capture nothing can be allocated, so a workspace that is too small raises here (the
+    method reserves for ``WORKSPACE_ROWS`` rows at load time; reserve_workspace grows it).
+    In eager mode a call past the reservation grows it once."""
+    idx = device.index if device.index is not None else torch.cuda.current_device()
+    ws = _workspaces.get(idx)
+    if nbytes <= 0 or (ws is not None and ws.numel() >= nbytes):
+        return
+    if torch.cuda.is_current_stream_capturing():
+        have = 0 if ws is None else ws.numel()
+        raise ValueError(f"{what}: needs {nbytes} workspace bytes and {have} are reserved; call "
+                         f"ops.reserve_workspace(device, {nbytes}) before capturing")
+    reserve_workspace(device, nbytes)
 
 
 def workspace_bytes(op: int, m: int, n: int, k: int, algo: int = ALGO_AUTO) -> int:
@@ -409,8 +436,10 @@ def fp8_linear_strips(x: torch.Tensor, qws: torch.Tensor, n: int, sw: torch.Tens
                       algo: int = ALGO_AUTO) -> torch.Tensor:
     """Fp8Method.apply (qtts/quant/fp8.py:72-89) with the e4m3 weight in the strip layout.
 
-    One C call: decode rows (M <= 16) run a single kernel that quantizes x per token
-    inside the GEMM; other rows quantize into the workspace first.
+    One C call.  A single kernel quantizes x per token inside the GEMM for decode rows
+    (M <= 3, or M <= 8 when K <= 2048) with K % 128 == 0, K <= 6144 and 16-byte aligned
+    rows of 16-bit activations (``qtts_fp8_fused_ok``); every other call quantizes into the
+    workspace first and runs the fp8 GEMM (two kernels).
     """
     shape = x.shape
     a = _flatten(x)
@@ -428,7 +457,7 @@ def fp8_linear_strips(x: torch.Tensor, qws: torch.Tensor, n: int, sw: torch.Tens
     sw = sw.reshape(-1).to(torch.float32).contiguous()
     dev = _require_cuda(a, qws, sw, bias)
     out = torch.empty((rows, n), dtype=a.dtype, device=dev)
-    reserve_workspace(dev, workspace_bytes(OP_FP8_LINEAR, rows, n, k, algo))
+    _ensure_workspace(dev, workspace_bytes(OP_FP8_LINEAR, rows, n, k, algo), "fp8_linear")
     ws, ws_n = _ws_for(dev)
     st = _lib.load().qtts_fp8_linear_strips(
         _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else k, _ptr(qws), n, _ptr(sw), _ptr(bias),
@@ -533,7 +562,7 @@ def _int8_linear(x, qw, n, ldqw, sw, bias, div_mode, algo, strips):
     sw = sw.reshape(-1).to(torch.float32).contiguous()
     dev = _require_cuda(a, qw, sw, bias)
     out = torch.empty((rows, n), dtype=a.dtype, device=dev)
-    reserve_workspace(dev, workspace_bytes(OP_INT8_LINEAR, rows, n, k, algo))
+    _ensure_workspace(dev, workspace_bytes(OP_INT8_LINEAR, rows, n, k, algo), "int8_linear")
     ws, ws_n = _ws_for(dev)
     lib = _lib.load()
     if strips:
@@ -654,7 +683,7 @@ def w8a16_silu_mul_gemm_strips(gate_up: torch.Tensor, qs: torch.Tensor, n: int, 
     dev = _require_cuda(a, qs, scale, bias)
     scale = scale.contiguous()
     out = torch.empty((rows, n), dtype=a.dtype, device=dev)
-    reserve_workspace(dev, workspace_bytes(OP_W8A16_SILU, rows, n, k, algo))
+    _ensure_workspace(dev, workspace_bytes(OP_W8A16_SILU, rows, n, k, algo), "w8a16_silu_mul_gemm")
     ws, ws_n = _ws_for(dev)
     st = _lib.load().qtts_w8a16_silu_mul_gemm_strips(
         _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else 2 * k, _ptr(qs), n, _ptr(scale),
@@ -720,7 +749,7 @@ def w8a16_fused_gemm_strips(x: torch.Tensor, qs: torch.Tensor, n: int, scale: to
         y = _flatten(out)
         if y.shape != (rows, n) or y.dtype != a.dtype or y.data_ptr() != out.data_ptr():
             raise ValueError(f"out must be a [{rows}, {n}] {a.dtype} tensor")
-    reserve_workspace(dev, workspace_bytes(OP_W8A16_FUSED, rows, n, k, algo))
+    _ensure_workspace(dev, workspace_bytes(OP_W8A16_FUSED, rows, n, k, algo), "w8a16_fused_gemm")
     ws, ws_n = _ws_for(dev)
     st = _lib.load().qtts_w8a16_fused_gemm_strips(
         _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else a.shape[1], int(prologue),
@@ -763,7 +792,7 @@ def w8a16_gate_up_silu_strips(x: torch.Tensor, qs: torch.Tensor, n: int, scale: 
     dev = _require_cuda(a, qs, scale, bias, norm_weight)
     scale = scale.contiguous()
     act = torch.empty((rows, n // 2), dtype=a.dtype, device=dev)
-    reserve_workspace(dev, workspace_bytes(OP_W8A16_FUSED, rows, n, k, algo))
+    _ensure_workspace(dev, workspace_bytes(OP_W8A16_FUSED, rows, n, k, algo), "w8a16_fused_gemm")
     ws, ws_n = _ws_for(dev)
     st = _lib.load().qtts_w8a16_gate_up_silu_strips(
         _ptr(a), dtype_code(a.dtype), rows, k, a.stride(0) if rows > 1 else k, int(prologue), _ptr(norm_weight),
@@ -771,131 +800,6 @@ def w8a16_gate_up_silu_strips(x: torch.Tensor, qs: torch.Tensor, n: int, scale: 
         _stream(dev))
     _lib.check(st, "w8a16_gate_up_silu_strips")
     return act.reshape(*shape[:-1], n // 2)
-
-
-@dataclasses.dataclass
-class ChainLink:
-    """One int8 weight-only linear of a chain (``w8a16_chain``): ``out = epilogue(linear(prologue(x)))``.
-
-    ``x`` is ``[m, k]`` bf16 (rows may be strided, 16-byte aligned); ``qs`` the int8 strip
-    weight of ``[n, k]`` with its ``scale``; ``out`` a preallocated ``[m, n]`` tensor
-    (``[m, n // 2]`` with EPI_SILU_MUL).  ``prologue``: PRO_NONE or PRO_RMS_NORM (with
-    ``norm_weight`` and ``eps``).  ``epilogue``: EPI_STORE, EPI_RESIDUAL (``out = residual
-    + linear``; ``residual`` may be ``out``) or EPI_SILU_MUL (``out = silu(gate) * up`` of
-    the two output halves).  ``after``: index of the earlier link whose output this one
-    reads, or -1."""
-
-    x: torch.Tensor
-    qs: torch.Tensor
-    n: int
-    scale: torch.Tensor
-    out: torch.Tensor
-    bias: torch.Tensor | None = None
-    prologue: int = PRO_NONE
-    norm_weight: torch.Tensor | None = None
-    eps: float = 1e-6
-    epilogue: int = EPI_STORE
-    residual: torch.Tensor | None = None
-    after: int = -1
-
-
-def _rows2d(t: torch.Tensor, what: str) -> torch.Tensor:
-    if t.dim() != 2 or t.stride(1) != 1:
-        raise ValueError(f"{what} must be a 2-D tensor with unit column stride, got {tuple(t.shape)}")
-    return t
-
-
-class ChainPlan:
-    """Dependent int8 weight-only linears prepared for one persistent launch each time the plan
-    is called (``qtts_w8a16_chain_strips``): the talker decoder layer's o_proj + residual,
-    post_attention_layernorm + gate_up_proj + SiLU * mul, down_proj + residual and the next
-    layer's input_layernorm + qkv_proj (qtts/models/talker.py:246-271) with no launch
-    boundary between them.  Calling it writes every link's ``out`` on the current stream.
-
-    The plan owns the chain's control block (per-item completion flags, zero-filled once
-    here, never cleared again), so build it outside graph capture and call it inside as
-    often as needed; the tensors of its links must stay where they are.  ``algo`` bits
-    8-23: workgroups (0: as many as fit at once)."""
-
-    def __init__(self, links: list[ChainLink], algo: int = 0) -> None:
-        if not 1 <= len(links) <= CHAIN_MAX_LINKS:
-            raise ValueError(f"a chain has 1..{CHAIN_MAX_LINKS} links, got {len(links)}")
-        m = links[0].x.shape[0] if links[0].x.dim() == 2 else -1
-        arr = (_lib.ChainLinkC * len(links))()
-        keep, tensors = [], []
-        for i, ln in enumerate(links):
-            x = _rows2d(ln.x, f"link {i} x")
-            out = _rows2d(ln.out, f"link {i} out")
-            k = x.shape[1]
-            n = int(ln.n)
-            if x.shape[0] != m:
-                raise ValueError(f"link {i} has {x.shape[0]} rows, link 0 has {m}")
-            if x.dtype != torch.bfloat16:
-                raise ValueError(f"link {i}: the chain takes bf16 activations, got {x.dtype}")
-            if ln.qs.dtype != torch.int8 or ln.qs.numel() != strip_bytes(n, k, STRIP_INT8):
-                raise ValueError(f"link {i}: weight is not an int8 strip-layout [{n}, {k}] buffer")
-            if ln.scale.numel() != n or ln.scale.dtype not in (torch.bfloat16, torch.float32):
-                raise ValueError(f"link {i}: scale must hold {n} bf16 or fp32 entries")
-            if ln.scale.dtype != links[0].scale.dtype:
-                raise ValueError("every link's scale must have the same dtype")
-            ocols = n // 2 if ln.epilogue == EPI_SILU_MUL else n
-            if out.shape != (m, ocols) or out.dtype != x.dtype:
-                raise ValueError(f"link {i}: out must be [{m}, {ocols}] {x.dtype}, got {tuple(out.shape)} {out.dtype}")
-            bias = None
-            if ln.bias is not None:
-                if ln.bias.numel() != n:
-                    raise ValueError(f"link {i}: bias has {ln.bias.numel()} entries for {n} outputs")
-                bias = ln.bias.to(x.dtype).contiguous()
-            nw = None
-            if ln.prologue == PRO_RMS_NORM:
-                if ln.norm_weight is None or ln.norm_weight.numel() != k:
-                    raise ValueError(f"link {i}: the RMSNorm prologue needs a norm weight of {k} entries")
-                nw = ln.norm_weight.to(x.dtype).contiguous()
-            res = None
-            if ln.epilogue == EPI_RESIDUAL:
-                if ln.residual is None:
-                    raise ValueError(f"link {i}: the residual epilogue needs a residual")
-                res = _rows2d(ln.residual, f"link {i} residual")
-                if res.shape != (m, n) or res.dtype != x.dtype:
-                    raise ValueError(f"link {i}: residual must be [{m}, {n}] {x.dtype}")
-            scale = ln.scale.contiguous()
-            keep += [x, out, ln.qs, scale, bias, nw, res]
-            tensors += [x, out, ln.qs, scale, bias, nw, res]
-            c = arr[i]
-            c.x, c.ldx, c.qs, c.n, c.k = x.data_ptr(), x.stride(0), ln.qs.data_ptr(), n, k
-            c.scale, c.bias, c.prologue = scale.data_ptr(), _ptr(bias), int(ln.prologue)
-            c.norm_weight, c.eps, c.epilogue = _ptr(nw), float(ln.eps), int(ln.epilogue)
-            c.residual, c.ldr = _ptr(res), (res.stride(0) if res is not None else n)
-            c.y, c.ldy, c.after = out.data_ptr(), out.stride(0), int(ln.after)
-        self.device = _require_cuda(*tensors)
-        nbytes = _lib.load().qtts_w8a16_chain_ctl_bytes(arr, len(links), m)
-        if nbytes < 0:
-            _lib.check(int(nbytes), "w8a16_chain_ctl_bytes")
-        self.ctl = torch.zeros((nbytes + 3) // 4, dtype=torch.int32, device=self.device)
-        self.m, self.algo, self.count = m, int(algo), len(links)
-        self.x_dtype, self.s_dtype = dtype_code(links[0].x.dtype), dtype_code(links[0].scale.dtype)
-        self._arr, self._keep = arr, keep
-
-    def __call__(self) -> None:
-        st = _lib.load().qtts_w8a16_chain_strips(self._arr, self.count, self.x_dtype, self.s_dtype, self.m, self.algo,
-                                                 self.ctl.data_ptr(), self.ctl.numel() * 4, _stream(self.device))
-        _lib.check(st, "w8a16_chain_strips")
-
-    def timed_out(self, clear: bool = True) -> bool:
-        """Whether a launch of this chain gave up waiting for a link (the control block's sticky
-        timeout flag; reads device memory, so call it outside graph capture)."""
-        flag = self.ctl[CHAIN_TIMEOUT_BYTE // 4:CHAIN_TIMEOUT_BYTE // 4 + 1]
-        hit = bool(flag.any().item())
-        if clear and hit:
-            flag.zero_()
-        return hit
-
-
-def w8a16_chain(links: list[ChainLink], algo: int = 0) -> ChainPlan:
-    """Prepare and launch a chain once (``ChainPlan``); returns the plan for further launches."""
-    plan = ChainPlan(links, algo)
-    plan()
-    return plan
 
 
 class KernelTimer:
@@ -926,3 +830,22 @@ class KernelTimer:
     @property
     def mean_ms(self) -> float:
         return self.total_ms / self.launches if self.launches else float("nan")
+
+
+def probe_stream(src: torch.Tensor, nbytes: int, waves: int, loads: int, sink: torch.Tensor) -> None:
+    """Stream ``nbytes`` of ``src`` with the measurement kernel (``qtts_probe_stream``): ``waves``
+    waves a workgroup, ``loads`` 1 KiB loads a wave issued before any is used; each wave stores
+    the xor of what it read to ``sink`` (int32, one word a wave)."""
+    dev = _require_cuda(src, sink)
+    if sink.dtype != torch.int32 or sink.numel() * loads * 1024 < nbytes:
+        raise ValueError("sink must be int32 with one word per wave")
+    if src.numel() * src.element_size() < nbytes:
+        raise ValueError("src is smaller than nbytes")
+    _lib.check(_lib.load().qtts_probe_stream(src.data_ptr(), int(nbytes), int(waves), int(loads), sink.data_ptr(),
+                                             _stream(dev)), "probe_stream")
+
+
+def probe_empty(workgroups: int, waves: int = 1, device: torch.device | None = None) -> None:
+    """Launch an empty kernel of ``workgroups`` x ``waves`` waves (``qtts_probe_empty``)."""
+    dev = device or torch.device("cuda", torch.cuda.current_device())
+    _lib.check(_lib.load().qtts_probe_empty(int(workgroups), int(waves), _stream(dev)), "probe_empty")

@@ -103,5 +103,92 @@ def worth_quantizing(quantized_call: Callable[[], object], reference_call: Calla
     return verdict is not None
 
 
+def time_candidates(candidates: dict[str, Callable[[], object]], reference_call: Callable[[], object], *,
+                    key: tuple, use_graph: bool = True,
+                    timer: Callable[[Callable[[], object]], float] | None = None
+                    ) -> tuple[float | None, dict[str, float]]:
+    """Seconds per call of the reference and of every candidate that times without an exception.
+
+    Cached per ``key`` like pick_fastest's verdicts.  A reference that fails gives ``None`` (the
+    caller then keeps the layer unquantized); a failing candidate is left out."""
+    ck = ("timings",) + tuple(key)
+    if ck in _CACHE:
+        return _CACHE[ck]  # type: ignore[return-value]
+    t = timer or (graph_time if use_graph else eager_time)
+    try:
+        reference = t(reference_call)
+    except Exception as exc:
+        logger.warning("calibration of the reference failed for %s (%s); leaving it unquantized", key, exc)
+        _CACHE[ck] = (None, {})
+        return None, {}
+    timings: dict[str, float] = {}
+    for name, call in candidates.items():
+        try:
+            timings[name] = t(call)
+        except Exception as exc:
+            logger.warning("calibration of %s failed for %s (%s); dropping that candidate", name, key, exc)
+    _CACHE[ck] = (reference, timings)
+    logger.debug("%s: reference %.2f us, %s", key, reference * 1e6,
+                 ", ".join(f"{n} {v * 1e6:.2f} us" for n, v in timings.items()))
+    return reference, timings
+
+
+def calibrate_buckets(tag: str, n: int, k: int, dtype: torch.dtype, device: torch.device,
+                      buckets: tuple[int, ...], decode_rows: int,
+                      candidates: Callable[[int], dict[str, int]],
+                      kernel_call: Callable[[torch.Tensor, int], object],
+                      reference_call: Callable[[torch.Tensor], object],
+                      route_calls: dict[int, dict[str, tuple[int, Callable[[torch.Tensor], object]]]] | None = None,
+                      margin: float = 1.05, use_graph: bool = True,
+                      timer: Callable[[Callable[[], object]], float] | None = None,
+                      ) -> tuple[bool, dict[int, int], dict[int, dict]]:
+    """Per-bucket kernel choice for one ``[n, k]`` weight (qtts/quant/calibrate.py:77-114 asks one
+    question at one row count; this asks it at every row bucket the callers produce).
+
+    At each row count in ``buckets`` it times every candidate algo (``candidates(rows)``, run as
+    ``kernel_call(x, algo)``) and any extra routes for that bucket (``route_calls[rows]``: name ->
+    (algo marker, call)) against ``reference_call(x)`` (F.linear on the bf16 weight), on seeded
+    random activations.  The layer is worth quantizing when, summed over the decode buckets (rows
+    <= ``decode_rows``: the rows a decode step runs), the fastest candidate of each bucket beats
+    the reference by ``margin`` -- one verdict per layer, as in the reference, but taken over the
+    decode rows instead of at one row count.  A reference that cannot be timed at a decode bucket
+    declines the layer; a calibration failure is never fatal.
+
+    Returns ``(accept, {rows: algo}, {rows: {"reference": s, "best": name, "timings": {...}}})``;
+    the table holds the fastest candidate of every bucket that timed (also where it loses to the
+    reference: once quantized, the bf16 weight is gone and the fastest quantized route serves)."""
+    table: dict[int, int] = {}
+    report: dict[int, dict] = {}
+    decode_ref = decode_best = 0.0
+    decode_seen = 0
+    for rows in buckets:
+        gen = torch.Generator(device=device).manual_seed(rows)
+        x = torch.randn(rows, k, device=device, dtype=dtype, generator=gen)
+        algos = dict(candidates(rows))
+        calls = {name: (lambda a=a, x=x: kernel_call(x, a)) for name, a in algos.items()}
+        for name, (marker, call) in (route_calls or {}).get(rows, {}).items():
+            algos[name] = marker
+            calls[name] = (lambda c=call, x=x: c(x))
+        t = timer
+        if t is None and use_graph and rows > 128:  # prefill-sized calls: fewer replays suffice
+            t = lambda fn: graph_time(fn, inner=10, iters=10)  # noqa: E731
+        reference, timings = time_candidates(calls, lambda x=x: reference_call(x),
+                                             key=(tag, n, k, rows, str(dtype)), use_graph=use_graph, timer=t)
+        best = min(timings, key=timings.get) if timings else None
+        report[rows] = {"reference": reference, "best": best, "timings": timings}
+        if best is not None:
+            table[rows] = algos[best]
+        if rows <= decode_rows:
+            if reference is None or best is None:
+                return False, {}, report
+            decode_ref += reference
+            decode_best += timings[best]
+            decode_seen += 1
+    accept = decode_seen > 0 and decode_best * margin < decode_ref
+    logger.debug("%s (%d, %d): decode buckets %.2f us quantized vs %.2f us reference -> %s", tag, n, k,
+                 decode_best * 1e6, decode_ref * 1e6, "quantize" if accept else "keep")
+    return accept, (table if accept else {}), report
+
+
 def clear_cache() -> None:
     _CACHE.clear()

@@ -21,7 +21,7 @@ import torch.nn.functional as F
 from .. import _lib, ops
 from . import prefill
 from .base import QuantMethodBase
-from .calibrate import pick_fastest
+from .calibrate import calibrate_buckets
 from .kernels import kernel_available
 
 _FP8_MAX = 448.0
@@ -54,8 +54,9 @@ class Fp8Method(QuantMethodBase):
             layer.register_buffer("fp8_weight", q.t(), persistent=False)
             layer.fp8_layout = "rowmajor"
         layer.register_buffer("fp8_scale", scale.reshape(1, -1), persistent=False)
-        ops.reserve_workspace(weight.device, max(
-            ops.workspace_bytes(_lib.OP_W8A8_FP8, m, layer.out_features, layer.in_features) for m in (16, 64, 256)))
+        # apply never allocates up to ops.WORKSPACE_ROWS rows (and under capture never does)
+        for op in (_lib.OP_FP8_LINEAR, _lib.OP_W8A8_FP8):
+            ops.reserve_for_rows(weight.device, op, layer.out_features, layer.in_features)
         layer.weight = torch.nn.Parameter(torch.empty(0, dtype=weight.dtype, device=weight.device),
                                           requires_grad=False)
 
@@ -116,33 +117,43 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
 
     name = "fp8_weight_only"
 
-    def __init__(self, calibrate: bool = True, calibration_batch: int = 16, div_mode: int = _lib.DIV_DEVICE) -> None:
+    def __init__(self, calibrate: bool = True, calibration_batch: int = 16, div_mode: int = _lib.DIV_DEVICE,
+                 calibration_rows: tuple[int, ...] | None = None, timer=None) -> None:
+        from .int8 import M_BUCKETS
         available, reason = kernel_available()
         if not available:
             raise RuntimeError(f"fp8 weight-only needs the gfx950 fused kernel: {reason}")
         self.calibrate = calibrate
         self.calibration_batch = calibration_batch
+        self.calibration_rows = tuple(sorted(set(calibration_rows or M_BUCKETS)))
+        self.timer = timer
+        self.calibration_report: dict[tuple[int, int], dict] = {}
         self.div_mode = div_mode
         self.quantized = 0
         self.declined = 0
 
     def _profitable(self, layer, qs: torch.Tensor, scale: torch.Tensor) -> bool:
+        """Per-bucket calibration, as Int8WeightOnlyMethod._profitable (calibrate.calibrate_buckets)."""
         if not self.calibrate:
             return True
         weight = layer.weight
-        rows = max(1, self.calibration_batch)
         n, k = layer.out_features, layer.in_features
-        gen = torch.Generator(device=weight.device).manual_seed(0)
-        x = torch.randn(rows, k, device=weight.device, dtype=weight.dtype, generator=gen)
-        algos = _fp8w_candidates(rows)
-        ops.reserve_workspace(weight.device, max(ops.workspace_bytes(_lib.OP_FP8W, rows, n, k, a)
-                                                 for a in algos.values()))
-        cands = {name: (lambda a=algo: ops.fp8w_gemm_strips(x, qs, n, scale, None, a)) for name, algo in algos.items()}
-        best = pick_fastest(cands, lambda: F.linear(x, weight, None), key=("fp8_wo", n, k, rows, str(weight.dtype)))
-        if best is not None:
-            from .int8 import bucket_of
-            _FP8W_ALGO.setdefault((n, k, bucket_of(rows)), algos[best])
-        return best is not None
+        ops.reserve_workspace(weight.device, max(ops.workspace_bytes(_lib.OP_FP8W, r, n, k, a)
+                                                 for r in self.calibration_rows for a in _fp8w_candidates(r).values()))
+        routes = {}
+        if any(r in prefill.PREFILL_BUCKETS for r in self.calibration_rows):
+            prefill.reserve(weight.device, n, k, weight.dtype)
+            route = (prefill.ALGO_DEQUANT_GEMM,
+                     lambda x: prefill.dequant_linear(qs, _lib.CODE_E4M3, n, k, scale, x, None))
+            routes = {r: {"dequant": route} for r in self.calibration_rows if r in prefill.PREFILL_BUCKETS}
+        accept, table, report = calibrate_buckets(
+            "fp8_wo", n, k, weight.dtype, weight.device, self.calibration_rows, max(1, self.calibration_batch),
+            _fp8w_candidates, lambda x, a: ops.fp8w_gemm_strips(x, qs, n, scale, None, a),
+            lambda x: F.linear(x, weight, None), routes, timer=self.timer)
+        self.calibration_report[(n, k)] = report
+        for rows, algo in table.items():
+            _FP8W_ALGO.setdefault((n, k, rows), algo)
+        return accept
 
     def _decline(self, layer) -> None:
         self.declined += 1
@@ -158,13 +169,7 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
         if not self._profitable(layer, qs, scale):
             self._decline(layer)
             return
-        ops.reserve_workspace(weight.device, max(
-            ops.workspace_bytes(_lib.OP_FP8W, m, layer.out_features, layer.in_features) for m in (16, 64, 128, 1024)))
-        if self.calibrate:
-            # Prefill buckets: the tile kernel against dequantize + F.linear (quant/prefill.py).
-            n, k = layer.out_features, layer.in_features
-            prefill.calibrate(_FP8W_ALGO, "fp8_wo_prefill", qs, _lib.CODE_E4M3, n, k, scale, weight.dtype,
-                              weight.device, lambda x: ops.fp8w_gemm_strips(x, qs, n, scale, None))
+        ops.reserve_for_rows(weight.device, _lib.OP_FP8W, layer.out_features, layer.in_features)
         layer.register_buffer("fp8w_weight", qs, persistent=False)
         layer.register_buffer("fp8w_scale", scale, persistent=False)
         layer.weight = torch.nn.Parameter(torch.empty(0, dtype=weight.dtype, device=weight.device),

@@ -5,9 +5,11 @@ output channel, keeps activations in the model dtype, and runs the gfx950 fused
 dequantize-in-registers GEMM.  With ``calibrate`` it times, per layer shape, the
 HIP kernel candidates against the unquantized F.linear (hipBLASLt on ROCm) inside
 a HIP graph and keeps the fastest; a layer where no candidate wins by 5% keeps
-its original weight and GEMM (qtts/quant/int8.py:79-111).  For the prefill row
-buckets it also times the tile kernel against dequantizing the codes into a scratch
-buffer and calling F.linear (quant/prefill.py), and keeps the faster route per bucket.
+its original weight and GEMM (qtts/quant/int8.py:79-111).  The timing runs at every
+row bucket the callers produce (decode rows 1..16, code-predictor rows up to 128,
+prefill buckets), the verdict comes from the decode buckets, and each bucket keeps
+its fastest route: a skinny or tile kernel configuration, or at the prefill buckets
+dequantizing the codes into a scratch buffer and calling F.linear (quant/prefill.py).
 
 ``Int8Method`` (W8A8) quantizes activations per token at run time and multiplies
 int8 codes on the int8 matrix cores (v_mfma_i32_16x16x64_i8) with exact int32
@@ -25,7 +27,7 @@ import torch.nn.functional as F
 from .. import _lib, ops
 from . import prefill
 from .base import QuantMethodBase
-from .calibrate import pick_fastest
+from .calibrate import calibrate_buckets
 from .kernels import kernel_available
 
 logger = logging.getLogger("qtts_amd.quant.int8")
@@ -93,39 +95,52 @@ class Int8WeightOnlyMethod(QuantMethodBase):
 
     name = "int8_weight_only"
 
-    def __init__(self, calibrate: bool = True, calibration_batch: int = 16, div_mode: int = _lib.DIV_DEVICE) -> None:
+    def __init__(self, calibrate: bool = True, calibration_batch: int = 16, div_mode: int = _lib.DIV_DEVICE,
+                 calibration_rows: tuple[int, ...] = M_BUCKETS, timer=None) -> None:
         available, reason = kernel_available()
         if not available:
             raise RuntimeError(f"int8 weight-only needs the gfx950 fused kernel: {reason}")
         self.calibrate = calibrate
         self.calibration_batch = calibration_batch
+        self.calibration_rows = tuple(sorted(set(calibration_rows)))
+        self.timer = timer
+        #: (N, K) -> per-bucket timings of the last calibration (calibrate_buckets' report)
+        self.calibration_report: dict[tuple[int, int], dict] = {}
         self.div_mode = div_mode
         self.quantized = 0
         self.declined = 0
 
-    def _profitable(self, layer, q: torch.Tensor, scale: torch.Tensor) -> bool:
+    def _profitable(self, layer, q: torch.Tensor, scale: torch.Tensor, layout: str) -> bool:
+        """Per-bucket calibration (calibrate.calibrate_buckets): every HIP candidate, and the
+        prefill route at the prefill buckets, against F.linear at each row bucket in
+        ``calibration_rows``; the layer converts when it wins over the decode buckets (rows up
+        to ``calibration_batch``) and each bucket then runs its fastest route."""
         if not self.calibrate:
             return True
         weight = layer.weight
         if not torch.cuda.is_available() or weight.device.type != "cuda":
             return False
-        rows = max(1, self.calibration_batch)
         n, k = layer.out_features, layer.in_features
-        gen = torch.Generator(device=weight.device).manual_seed(0)
-        x = torch.randn(rows, k, device=weight.device, dtype=weight.dtype, generator=gen)
-        cands_algo = _candidates(rows)
-        ops.reserve_workspace(weight.device, max(ops.workspace_bytes(_lib.OP_W8A16, rows, n, k, a)
-                                                 for a in cands_algo.values()))
-        if _strips_ok(layer):
-            cands = {name: (lambda a=algo: ops.w8a16_gemm_strips(x, q, n, scale, None, a))
-                     for name, algo in cands_algo.items()}
+        strips = layout == "strips"
+        ops.reserve_workspace(weight.device, max(ops.workspace_bytes(_lib.OP_W8A16, r, n, k, a)
+                                                 for r in self.calibration_rows for a in _candidates(r).values()))
+        if strips:
+            kernel = lambda x, a: ops.w8a16_gemm_strips(x, q, n, scale, None, a)  # noqa: E731
         else:
-            cands = {name: (lambda a=algo: ops.w8a16_gemm(x, q, scale, None, a)) for name, algo in cands_algo.items()}
-        best = pick_fastest(cands, lambda: F.linear(x, weight, None),
-                            key=("int8_wo", n, k, rows, str(weight.dtype)))
-        if best is not None:
-            _ALGO.setdefault((n, k, bucket_of(rows)), _candidates(rows)[best])
-        return best is not None
+            kernel = lambda x, a: ops.w8a16_gemm(x, q, scale, None, a)  # noqa: E731
+        routes = {}
+        if strips and any(r in prefill.PREFILL_BUCKETS for r in self.calibration_rows):
+            prefill.reserve(weight.device, n, k, weight.dtype)
+            route = (prefill.ALGO_DEQUANT_GEMM,
+                     lambda x: prefill.dequant_linear(q, _lib.CODE_INT8, n, k, scale, x, None))
+            routes = {r: {"dequant": route} for r in self.calibration_rows if r in prefill.PREFILL_BUCKETS}
+        accept, table, report = calibrate_buckets(
+            "int8_wo", n, k, weight.dtype, weight.device, self.calibration_rows, max(1, self.calibration_batch),
+            _candidates, kernel, lambda x: F.linear(x, weight, None), routes, timer=self.timer)
+        self.calibration_report[(n, k)] = report
+        for rows, algo in table.items():
+            _ALGO.setdefault((n, k, rows), algo)
+        return accept
 
     def process_weights(self, layer) -> None:
         weight = layer.weight
@@ -135,19 +150,14 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         layout = "strips" if _strips_ok(layer) else "rowmajor"
         if layout == "strips":
             q = ops.to_strips(q, _lib.STRIP_INT8)
-        if not self._profitable(layer, q, scale):
+        if not self._profitable(layer, q, scale, layout):
             self.declined += 1
             # Leaving quant_method unset keeps the layer on F.linear.
             layer.register_buffer("int8_weight", None, persistent=False)
             return
-        ops.reserve_workspace(weight.device, max(
-            ops.workspace_bytes(_lib.OP_W8A16, m, layer.out_features, layer.in_features) for m in (16, 64, 128, 1024)))
-        if self.calibrate and layout == "strips":
-            # Prefill buckets: the tile kernel against dequantize + F.linear (the bf16 baseline
-            # rebuilt from the stored codes); the faster one serves that bucket's calls.
-            n, k = layer.out_features, layer.in_features
-            prefill.calibrate(_ALGO, "int8_wo_prefill", q, _lib.CODE_INT8, n, k, scale, weight.dtype, weight.device,
-                              lambda x: ops.w8a16_gemm_strips(x, q, n, scale, None))
+        # apply (and the decoder helpers' fused forms) never allocate up to ops.WORKSPACE_ROWS rows
+        for op in (_lib.OP_W8A16, _lib.OP_W8A16_SILU, _lib.OP_W8A16_FUSED):
+            ops.reserve_for_rows(weight.device, op, layer.out_features, layer.in_features)
         layer.register_buffer("int8_weight", q, persistent=False)
         layer.register_buffer("int8_scale", scale, persistent=False)
         layer.int8_layout = layout
@@ -231,8 +241,7 @@ class Int8Method(QuantMethodBase):
             layer.register_buffer("int8_weight", q, persistent=False)
             layer.int8_layout = "rowmajor"
         layer.register_buffer("int8_scale", scale, persistent=False)
-        ops.reserve_workspace(weight.device, max(
-            ops.workspace_bytes(_lib.OP_INT8_LINEAR, m, n, k) for m in (16, 64, 256, 1024)))
+        ops.reserve_for_rows(weight.device, _lib.OP_INT8_LINEAR, n, k)
         layer.weight = torch.nn.Parameter(torch.empty(0, dtype=weight.dtype, device=weight.device),
                                           requires_grad=False)
 

@@ -6,25 +6,22 @@ can beat the fused dequantize-in-registers tile kernel.  A quantized layer no lo
 holds its bf16 weight, so the route rebuilds it: ``qtts_dequant_strips`` writes
 ``dtype(code * scale[n])`` -- the reference's dequantize-then-matmul form,
 ``q.to(dtype) * scale[:, None]`` (qtts/quant/kernels.py:144-148) -- into a per-device
-scratch buffer, and F.linear multiplies by it.  The calibration times both per prefill
-bucket (qtts/quant/calibrate.py:77-114 answers the same question at the calibration
-batch) and records the route where it wins; every other call keeps the HIP kernels.
+scratch buffer, and F.linear multiplies by it.  The calibration (calibrate.calibrate_buckets)
+times it as one more candidate at each prefill bucket and records the route where it is
+the fastest; every other call keeps the HIP kernels.
 """
 
 from __future__ import annotations
-
-from typing import Callable
 
 import torch
 import torch.nn.functional as F
 
 from .. import ops
-from .calibrate import pick_fastest
 
 #: Algo value (Python side only) that sends a bucket's calls through dequantize + F.linear.
 ALGO_DEQUANT_GEMM = -1
 
-#: Row buckets whose route the calibration decides (the M_BUCKETS entries past 128 rows;
+#: Row buckets where the calibration times this route (the M_BUCKETS entries past 128 rows;
 #: the last one also serves every larger call).
 PREFILL_BUCKETS = (256, 1024, 2048)
 
@@ -40,22 +37,3 @@ def dequant_linear(qs: torch.Tensor, codes: int, n: int, k: int, scale: torch.Te
     w = ops.dequant_scratch(x.device, n, k, x.dtype)
     ops.dequant_strips(qs, n, k, scale, x.dtype, codes, out=w)
     return F.linear(x, w, bias)
-
-
-def calibrate(table: dict, key: str, qs: torch.Tensor, codes: int, n: int, k: int, scale: torch.Tensor,
-              dtype: torch.dtype, device: torch.device,
-              kernel_call: Callable[[torch.Tensor], object]) -> dict[int, bool]:
-    """For each prefill bucket, time ``kernel_call(x)`` (the HIP kernel) against
-    :func:`dequant_linear` on random rows; where the latter is faster by 3%, record
-    ``table[(n, k, bucket)] = ALGO_DEQUANT_GEMM``.  Returns the verdict per bucket."""
-    reserve(device, n, k, dtype)
-    verdicts = {}
-    for rows in PREFILL_BUCKETS:
-        gen = torch.Generator(device=device).manual_seed(rows)
-        x = torch.randn(rows, k, device=device, dtype=dtype, generator=gen)
-        best = pick_fastest({"dequant": lambda x=x: dequant_linear(qs, codes, n, k, scale, x, None)},
-                            lambda x=x: kernel_call(x), key=(key, n, k, rows, str(dtype)), margin=1.03)
-        verdicts[rows] = best is not None
-        if best is not None:
-            table.setdefault((n, k, rows), ALGO_DEQUANT_GEMM)
-    return verdicts
