@@ -92,6 +92,7 @@ def test_int8_route_bits_and_bound(ops, monkeypatch):
     method.process_weights(lin)
     lin.quant_method = method
     prefill.reserve(torch.device("cuda"), n, k, torch.bfloat16)
+    monkeypatch.setattr(I, "_ALGO", {})  # no choice left by another test's calibration of this shape
     monkeypatch.setitem(I._ALGO, (n, k, 1024), prefill.ALGO_DEQUANT_GEMM)
     monkeypatch.setitem(I._ALGO, (n, k, 2048), prefill.ALGO_DEQUANT_GEMM)
     wq = ops.dequant_strips(lin.int8_weight, n, k, lin.int8_scale, torch.bfloat16)
@@ -127,6 +128,7 @@ def test_route_graph_replays_and_gated_mlp(ops, monkeypatch):
         lin.quant_method = method
         prefill.reserve(torch.device("cuda"), lin.out_features, lin.in_features, torch.bfloat16)
     x = torch.randn(512, 2048, device="cuda").to(torch.bfloat16)
+    monkeypatch.setattr(I, "_ALGO", {})  # no choice left by another test's calibration of these shapes
     kernels = mlp(x)  # the HIP tile kernels
     monkeypatch.setitem(I._ALGO, (12288, 2048, 1024), prefill.ALGO_DEQUANT_GEMM)
     monkeypatch.setitem(I._ALGO, (2048, 6144, 1024), prefill.ALGO_DEQUANT_GEMM)

@@ -82,12 +82,12 @@ def test_quantize_module_counts_and_bytes():
 
 def test_apply_quantization_routing():
     assert apply_quantization(QuantConfig(), talker=Block()) == {}
-    with pytest.raises(ValueError, match="unknown quant targets"):
+    with pytest.raises(ValueError, match="name no submodel"):
         apply_quantization(QuantConfig(method="int8_weight_only", targets=("vocoder",)), talker=Block())
 
 
 def test_build_method_errors_without_gpu():
-    with pytest.raises(ValueError, match="unknown quantization method"):
+    with pytest.raises(ValueError, match="no quantization method named"):
         build_method(QuantConfig(method="int4"))  # type: ignore[arg-type]
     if torch.cuda.is_available():
         pytest.skip("checks the no-GPU error path")
@@ -103,7 +103,7 @@ def test_linear_base_matches_f_linear_and_merged_partitions():
     lin = _init(LinearBase(6, 4, bias=True))
     x = torch.randn(2, 3, 6)
     torch.testing.assert_close(lin(x), F.linear(x, lin.weight, lin.bias))
-    assert "quant=none" in lin.extra_repr()
+    assert "quant_method=none" in lin.extra_repr()
     ml = MergedLinear(6, [2, 3])
     ml.load_partition(1, torch.ones(3, 6))
     assert torch.equal(ml.weight[2:], torch.ones(3, 6))

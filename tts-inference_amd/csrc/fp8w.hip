@@ -21,9 +21,9 @@ template <typename XT, int W, int CPW, int MX>
 void launch_sk(const void* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n, const float* scale,
                const void* bias, void* y, int64_t ldy, float* part, unsigned* counters, const SkinnyCfg& c,
                unsigned blocks, hipStream_t st) {
-  qtts::launch(&w8a16_skinny_kernel<XT, float, W, CPW, kLayoutStrips, true, 1, MX, true>, dim3(blocks),
-               dim3(W * 64), 0, st, (const int8_t*)qs, (const XT*)x, ldx, (int)m, (int)k, c.strips, c.S, c.cps, (int)n,
-               scale, (const XT*)bias, (XT*)y, ldy, (int64_t)0, part, counters, (const XT*)nullptr, 0.0f,
+  qtts::launch(&w8a16_skinny_kernel<XT, float, W, CPW, kLayoutStrips, true, 1, MX, true>, dim3(blocks, c.S),
+               dim3(W * 64), 0, st, (const int8_t*)qs, (const XT*)x, scale, (const XT*)bias, (const XT*)nullptr,
+               (int)ldx, (int)(m | (c.S << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0, part, counters, 0.0f,
                (const XT*)nullptr, (int64_t)0);
 }
 
@@ -101,7 +101,9 @@ int qtts_launch_fp8w(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8 weight-only skinny kernel handles M <= 16, got M=%lld",
                           (long long)m);
   SkinnyCfg c = fp8w_skinny_cfg(m, n, k, algo);
-  const bool staged = m <= 8 && !((algo >> 24) & 0x40);
+  const bool staged = m <= 8 && !((algo >> 24) & 0x40) && skinny_scalar_epilogue_ok(n, scale, bias);
+  if (!staged && c.waves == 8 && c.cpw == 12 && ((algo >> 16) & 0xff) == 0)  // 12 chunks a wave: staged rows only
+    c = skinny_cfg(m, n, k, splits, 16, 6);
   const int64_t need = skinny_ws(c);
   if (need > ws_bytes || (need > 0 && !ws)) {
     if (splits > 0)
@@ -112,10 +114,12 @@ int qtts_launch_fp8w(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
       return qtts_set_error(QTTS_ERR_WORKSPACE, "fp8w skinny: K=%lld needs a split-K workspace of %lld bytes",
                             (long long)k, (long long)skinny_ws(c));
   }
+  if (c.S >= (1 << 23)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8w skinny: K too large");
   if (c.S > 1 && c.strips > kMaxSplitTiles)
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8w skinny: too many output strips for a split-K meeting");
-  const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8 * c.S;
-  if (blocks <= 0 || blocks >= ((int64_t)1 << 31)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8w: N too large");
+  const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8;  // grid x; grid y: the K splits
+  if (blocks <= 0 || blocks >= ((int64_t)1 << 31) || ldx > INT32_MAX)
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8w: N or ldx too large");
   unsigned* counters = (unsigned*)ws;
   float* part = ws ? (float*)((char*)ws + kCounterBytes) : nullptr;
   const int mx = staged ? (m == 1 ? 1 : (m <= 4 ? 4 : 8)) : 0;

@@ -303,7 +303,7 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
     const int cpw = (algo >> 24) & 0x3f;
     const bool direct_x = (algo >> 24) & 0x40;
     SkinnyCfg c = skinny_cfg(m, n, k, splits, waves, cpw);
-    const bool staged = c.mb == 1 && wide_ok && m <= 8 && !direct_x;
+    const bool staged = c.mb == 1 && wide_ok && m <= 8 && !direct_x && skinny_scalar_epilogue_ok(n, scale, bias);
     // Staged rows from 2 rows up: 8 waves of 12 chunks beat 16 of 6 (measured on the
     // talker down projection, K = 6144, M = 2..8).
     if (staged && m >= 2 && waves == 0 && cpw == 0 && c.waves == 16 && c.S == 1 && 8 * 12 >= (k + 63) / 64)
@@ -324,15 +324,17 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
         return qtts_set_error(QTTS_ERR_WORKSPACE, "w8a16 skinny: K=%lld needs a split-K workspace of %lld bytes",
                               (long long)k, (long long)skinny_ws(c));
     }
+    if (c.S >= (1 << 23)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: K too large");
     if (c.S > 1 && c.strips > kMaxSplitTiles)
       return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: N=%lld with K=%lld needs a split-K over more "
                             "output strips than the workspace counter block holds", (long long)n, (long long)k);
-    const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8 * c.S;
-    if (!grid_ok(blocks)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16: N too large");
-#define QTTS_SK(ST, W, CPW, FK, MBV)                                                                              \
-  qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, FK, MBV>, dim3((unsigned)blocks), dim3(W * 64), 0, st, \
-               q, x, ldx, (int)m, (int)k, c.strips, c.S, c.cps, (int)n, (const ST*)scale, bias, y, ldy, ldq, part,  \
-               counters, (const XT*)nullptr, 0.0f, (const XT*)nullptr, (int64_t)0)
+    // grid x: the strips rounded up to a multiple of 8; grid y: the K splits
+    const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8;
+    if (!grid_ok(blocks) || ldx > INT32_MAX) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16: N or ldx too large");
+#define QTTS_SK(ST, W, CPW, FK, MBV)                                                                                \
+  qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, FK, MBV>, dim3((unsigned)blocks, (unsigned)c.S),        \
+               dim3(W * 64), 0, st, q, x, (const ST*)scale, bias, (const XT*)nullptr, (int)ldx, (int)(m | (c.S << 8)),   \
+               (int)k, (int)n, y, ldy, ldq, part, counters, 0.0f, (const XT*)nullptr, (int64_t)0)
 #define QTTS_SK_ST(W, CPW, FK, MBV)                           \
   do {                                                        \
     if (sdt == QTTS_BF16) QTTS_SK(bf16_t, W, CPW, FK, MBV);   \

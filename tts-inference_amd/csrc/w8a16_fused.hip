@@ -199,6 +199,7 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
               bool pair = false) {
   const int splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff, cpw = (algo >> 24) & 0x3f;
   const int64_t m = in.m, n = in.n, k = in.k;
+  if (!skinny_scalar_epilogue_ok(n, in.scale, in.bias)) return 1;  // the unfused kernels serve it
   if (pair) {
     if (splits > 1 || m > 8 || n % 32) return 1;
     SkinnyCfg c = skinny_cfg(m, n / 2, k, 1, waves, cpw);  // one workgroup per gate strip
@@ -211,6 +212,7 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
     if (c.S != 1 || !pair_built(c.waves, c.cpw)) return 1;
     FusedArgs a = in;
     a.c = c;
+    if (in.ldx > INT32_MAX) return 1;
     a.blocks = (unsigned)((c.strips + 7) / 8 * 8);
     a.counters = nullptr;
     a.part = nullptr;
@@ -243,8 +245,9 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
   if (!qtts_w8a16_xrows_built(c.waves, c.cpw)) return 1;
   if (pro == kProRmsNorm && c.S > 1) return 1;
   if (c.S > 1 && c.strips > kMaxSplitTiles) return 1;
-  const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8 * c.S;
-  if (blocks >= ((int64_t)1 << 31)) return 1;
+  if (c.S >= (1 << 23)) return 1;
+  const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8;  // grid x; grid y: the K splits
+  if (blocks >= ((int64_t)1 << 31) || in.ldx > INT32_MAX) return 1;
   FusedArgs a = in;
   a.c = c;
   a.blocks = (unsigned)blocks;

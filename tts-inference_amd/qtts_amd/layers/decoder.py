@@ -22,7 +22,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
-from .. import ops
+from .. import ops, torch_ops  # noqa: F401  (torch_ops registers torch.ops.qtts)
 
 
 def _int8_strips(linear: nn.Module, x: torch.Tensor) -> bool:
@@ -43,9 +43,9 @@ def norm_linear(norm: nn.Module, linear: nn.Module, x: torch.Tensor) -> torch.Te
     """``linear(norm(x))``: input_layernorm + qkv_proj (talker.py:249), with the RMSNorm computed
     inside the int8 weight-only GEMM's prologue."""
     if _int8_strips(linear, x):
-        return ops.w8a16_fused_gemm_strips(x, linear.int8_weight, linear.out_features, linear.int8_scale,
-                                           linear.bias, prologue=ops.PRO_RMS_NORM, norm_weight=norm.weight,
-                                           eps=_norm_eps(norm))
+        return torch.ops.qtts.w8a16_fused_gemm_strips(x, linear.int8_weight, linear.out_features, linear.int8_scale,
+                                                      linear.bias, ops.PRO_RMS_NORM, norm.weight, _norm_eps(norm),
+                                                      None, ops.ALGO_AUTO)
     return linear(norm(x))
 
 
@@ -53,8 +53,8 @@ def linear_residual(linear: nn.Module, x: torch.Tensor, residual: torch.Tensor) 
     """``residual + linear(x)``: o_proj and the residual add (talker.py:270), the add in the GEMM's
     epilogue (the linear's output rounded to the activation dtype first, as torch adds two tensors)."""
     if _int8_strips(linear, x) and residual.shape[:-1] == x.shape[:-1] and residual.dtype == x.dtype:
-        return ops.w8a16_fused_gemm_strips(x, linear.int8_weight, linear.out_features, linear.int8_scale,
-                                           linear.bias, residual=residual)
+        return torch.ops.qtts.w8a16_fused_gemm_strips(x, linear.int8_weight, linear.out_features, linear.int8_scale,
+                                                      linear.bias, ops.PRO_NONE, None, 1e-6, residual, ops.ALGO_AUTO)
     return residual + linear(x)
 
 
@@ -65,9 +65,9 @@ def norm_mlp_residual(norm: nn.Module, mlp: nn.Module, hidden: torch.Tensor) -> 
     fused = getattr(mlp, "fuse", False)
     if fused and _int8_strips(mlp.gate_up_proj, hidden) and mlp.gate_up_proj.out_features % 2 == 0:
         up = mlp.gate_up_proj
-        act = ops.w8a16_gate_up_silu_strips(hidden, up.int8_weight, up.out_features, up.int8_scale, up.bias,
-                                            prologue=ops.PRO_RMS_NORM, norm_weight=norm.weight,
-                                            eps=_norm_eps(norm))
+        act = torch.ops.qtts.w8a16_gate_up_silu_strips(hidden, up.int8_weight, up.out_features, up.int8_scale,
+                                                       up.bias, ops.PRO_RMS_NORM, norm.weight, _norm_eps(norm),
+                                                       ops.ALGO_AUTO)
         return linear_residual(mlp.down_proj, act, hidden)
     if fused:
         gate, up = mlp.gate_up_proj.split(mlp.gate_up_proj(norm(hidden)))

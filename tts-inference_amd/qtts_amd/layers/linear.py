@@ -54,7 +54,7 @@ class LinearBase(nn.Module):
 
     def extra_repr(self) -> str:
         q = self.quant_method.name if self.quant_method is not None else "none"
-        return f"in={self.in_features}, out={self.out_features}, bias={self.bias is not None}, quant={q}"
+        return f"{self.in_features} -> {self.out_features}, bias={self.bias is not None}, quant_method={q}"
 
 
 class MergedLinear(LinearBase):
@@ -75,12 +75,12 @@ class MergedLinear(LinearBase):
     def load_partition(self, index: int, tensor: torch.Tensor) -> None:
         lo, hi = self.offsets[index], self.offsets[index + 1]
         if tuple(tensor.shape) != (hi - lo, self.in_features):
-            raise ValueError(f"partition {index} expects shape {(hi - lo, self.in_features)}, got {tuple(tensor.shape)}")
+            raise ValueError(f"weight slice {index} must be {(hi - lo, self.in_features)}, not {tuple(tensor.shape)}")
         self.weight.data[lo:hi].copy_(tensor)
 
     def load_bias_partition(self, index: int, tensor: torch.Tensor) -> None:
         if self.bias is None:
-            raise ValueError("layer has no bias")
+            raise ValueError("this linear was built without a bias")
         lo, hi = self.offsets[index], self.offsets[index + 1]
         self.bias.data[lo:hi].copy_(tensor)
 

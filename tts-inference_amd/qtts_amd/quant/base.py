@@ -67,8 +67,8 @@ def quantize_module(module: nn.Module, method: QuantMethodBase, config: QuantCon
         layer.quant_method = method
         converted += 1
     after = _param_bytes(module) + _buffer_bytes(module)
-    logger.info("%s: %s on %d linears (%d excluded by name, %d declined as not faster), %s -> %s", label,
-                method.name, converted, excluded, declined, _human(before), _human(after))
+    logger.info("%s: %s converted %d linears, skipped %d by exclusion, kept %d on F.linear; weights %s -> %s",
+                label, method.name, converted, excluded, declined, _human(before), _human(after))
     return {"converted": converted, "excluded": excluded, "declined": declined, "bytes_before": before,
             "bytes_after": after}
 
@@ -96,7 +96,7 @@ def build_method(config: QuantConfig, calibration_batch: int = 16) -> QuantMetho
     if method in ("fp8", "fp8_weight_only"):
         supported, reason = fp8_supported()
         if not supported:
-            raise RuntimeError(f"fp8 quantization unavailable: {reason}")
+            raise RuntimeError(f"the fp8 method cannot run here: {reason}")
         if method == "fp8_weight_only":
             return Fp8WeightOnlyMethod(calibrate=config.calibrate, calibration_batch=calibration_batch)
         return Fp8Method()
@@ -104,7 +104,7 @@ def build_method(config: QuantConfig, calibration_batch: int = 16) -> QuantMetho
         return Int8WeightOnlyMethod(calibrate=config.calibrate, calibration_batch=calibration_batch)
     if method == "int8":
         return Int8Method()
-    raise ValueError(f"unknown quantization method {method!r}")
+    raise ValueError(f"no quantization method named {method!r}")
 
 
 def apply_quantization(config: QuantConfig, *, talker: nn.Module | None = None,
@@ -115,7 +115,7 @@ def apply_quantization(config: QuantConfig, *, talker: nn.Module | None = None,
         return {}
     unknown = set(config.targets) - {"talker", "code_predictor", "code2wav"}
     if unknown:
-        raise ValueError(f"unknown quant targets {sorted(unknown)}; pick from talker, code_predictor, code2wav")
+        raise ValueError(f"quant targets {sorted(unknown)} name no submodel (talker, code_predictor, code2wav)")
     method = build_method(config, calibration_batch=calibration_batch)
     report: dict[str, dict[str, int]] = {}
     if config.targets_submodel("talker"):

@@ -65,9 +65,10 @@ class Fp8Method(QuantMethodBase):
 
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
         if layer.fp8_layout == "strips":
-            return ops.fp8_linear_strips(x, layer.fp8_weight, layer.out_features, layer.fp8_scale.reshape(-1), bias,
-                                         self.div_mode)
-        return ops.fp8_linear(x, layer.fp8_weight.t(), layer.fp8_scale.reshape(-1), bias, self.div_mode)
+            return torch.ops.qtts.fp8_linear_strips(x, layer.fp8_weight, layer.out_features,
+                                                    layer.fp8_scale.reshape(-1), bias, self.div_mode, _lib.ALGO_AUTO)
+        return torch.ops.qtts.fp8_linear(x, layer.fp8_weight.t(), layer.fp8_scale.reshape(-1), bias, self.div_mode,
+                                         _lib.ALGO_AUTO)
 
 
 def fp8_weight_rowmajor(layer) -> torch.Tensor:
@@ -188,4 +189,4 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
         algo = _FP8W_ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
         if algo == prefill.ALGO_DEQUANT_GEMM:  # x is bf16 / fp16 here, as the scratch was sized for
             return prefill.dequant_linear(layer.fp8w_weight, _lib.CODE_E4M3, n, k, layer.fp8w_scale, x, bias)
-        return ops.fp8w_gemm_strips(x, layer.fp8w_weight, n, layer.fp8w_scale, bias, algo)
+        return torch.ops.qtts.fp8w_gemm_strips(x, layer.fp8w_weight, n, layer.fp8w_scale, bias, algo)

@@ -180,10 +180,10 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             algo = _lib.ALGO_AUTO
         if layer.int8_layout == "strips":
             if x.dtype in (torch.bfloat16, torch.float16):
-                return ops.w8a16_gemm_strips(x, layer.int8_weight, n, layer.int8_scale, bias, algo)
+                return torch.ops.qtts.w8a16_gemm_strips(x, layer.int8_weight, n, layer.int8_scale, bias, algo)
             # e.g. fp32 activations into a bf16-calibrated layer: correct, not fast
-            return ops.w8a16_gemm(x, int8_weight_rowmajor(layer), layer.int8_scale, bias)
-        return ops.w8a16_gemm(x, layer.int8_weight, layer.int8_scale, bias, algo)
+            return torch.ops.qtts.w8a16_gemm(x, int8_weight_rowmajor(layer), layer.int8_scale, bias, _lib.ALGO_AUTO)
+        return torch.ops.qtts.w8a16_gemm(x, layer.int8_weight, layer.int8_scale, bias, algo)
 
     def apply_gate_up_silu(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor | None:
         """``F.silu(gate) * up`` of this fused gate_up layer's output (qtts/layers/activation.py:142-147)
@@ -198,7 +198,8 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
         if algo == prefill.ALGO_DEQUANT_GEMM:
             return None
-        return ops.w8a16_gate_up_silu_strips(x, layer.int8_weight, n, layer.int8_scale, bias, algo=algo)
+        return torch.ops.qtts.w8a16_gate_up_silu_strips(x, layer.int8_weight, n, layer.int8_scale, bias,
+                                                       ops.PRO_NONE, None, 1e-6, algo)
 
     def apply_silu_mul(self, layer, gate_up: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
         """``layer(F.silu(gate) * up)`` from GatedMLP's fused gate_up output (qtts/layers/activation.py:
@@ -210,8 +211,9 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             rows = gate_up.numel() // (2 * k) if k else 0
             algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
             if algo != prefill.ALGO_DEQUANT_GEMM:
-                return ops.w8a16_silu_mul_gemm_strips(gate_up, layer.int8_weight, n, layer.int8_scale, bias, algo)
-        return self.apply(layer, ops.silu_mul(gate_up), bias)
+                return torch.ops.qtts.w8a16_silu_mul_gemm_strips(gate_up, layer.int8_weight, n, layer.int8_scale,
+                                                                 bias, algo)
+        return self.apply(layer, torch.ops.qtts.silu_mul(gate_up), bias)
 
 
 class Int8Method(QuantMethodBase):
@@ -250,6 +252,6 @@ class Int8Method(QuantMethodBase):
 
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
         if layer.int8_layout == "strips":
-            return ops.int8_linear_strips(x, layer.int8_weight, layer.out_features, layer.int8_scale, bias,
-                                          self.div_mode)
-        return ops.int8_linear(x, layer.int8_weight, layer.int8_scale, bias, self.div_mode)
+            return torch.ops.qtts.int8_linear_strips(x, layer.int8_weight, layer.out_features, layer.int8_scale, bias,
+                                                     self.div_mode, _lib.ALGO_AUTO)
+        return torch.ops.qtts.int8_linear(x, layer.int8_weight, layer.int8_scale, bias, self.div_mode, _lib.ALGO_AUTO)

@@ -14,9 +14,8 @@ the fastest; every other call keeps the HIP kernels.
 from __future__ import annotations
 
 import torch
-import torch.nn.functional as F
 
-from .. import ops
+from .. import ops, torch_ops  # noqa: F401  (torch_ops registers torch.ops.qtts)
 
 #: Algo value (Python side only) that sends a bucket's calls through dequantize + F.linear.
 ALGO_DEQUANT_GEMM = -1
@@ -33,7 +32,6 @@ def reserve(device: torch.device, n: int, k: int, dtype: torch.dtype) -> None:
 
 def dequant_linear(qs: torch.Tensor, codes: int, n: int, k: int, scale: torch.Tensor, x: torch.Tensor,
                    bias: torch.Tensor | None) -> torch.Tensor:
-    """``F.linear(x, dtype(codes * scale[:, None]), bias)`` through the device's scratch buffer."""
-    w = ops.dequant_scratch(x.device, n, k, x.dtype)
-    ops.dequant_strips(qs, n, k, scale, x.dtype, codes, out=w)
-    return F.linear(x, w, bias)
+    """``F.linear(x, dtype(codes * scale[:, None]), bias)`` through the device's scratch buffer
+    (``torch.ops.qtts.dequant_linear``)."""
+    return torch.ops.qtts.dequant_linear(x, qs, codes, n, k, scale, bias)
