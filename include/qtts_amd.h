@@ -294,6 +294,23 @@ int qtts_fp8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, int
                            void* y, int64_t ldy, int div_mode, int algo, void* ws, int64_t ws_bytes,
                            void* stream);
 
+/* qtts_fp8_linear_strips with no workspace argument and no allocation.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Its workspace is a
+ * library-owned device array of QTTS_STATIC_SCRATCH_BYTES on each GPU it runs on, held
+ * until the process ends; the call itself allocates nothing and synchronises nothing.
+ * Every call on one GPU shares that GPU's array and leaves its last contents there, so
+ * calls that overlap on one GPU (concurrent streams or threads) race: order them on one
+ * stream.  A call whose activation codes do not fit (64 KiB of split-K counters, m * k code
+ * bytes and 4 m scale bytes, each rounded up to 256) fails with QTTS_ERR_WORKSPACE; a split-K
+ * choice that does not fit in the rest runs without the split.  Arguments and results are
+ * those of qtts_fp8_linear_strips (decode rows that take the one-kernel path use no
+ * workspace at all). */
+#define QTTS_STATIC_SCRATCH_BYTES (32ll << 20)
+int qtts_fp8_linear_strips_static(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
+                                  const uint8_t* qws, int64_t n, const float* sw, const void* bias,
+                                  void* y, int64_t ldy, int div_mode, int algo, void* stream);
+
 /* --- int8 W8A8 -------------------------------------------------------------------- */
 
 /* Per-token int8 activation quantization, replacing the activation half of

@@ -388,6 +388,73 @@ int qtts_fp8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, int
                          ws_bytes, stream);
 }
 
+}  // extern "C"
+
+// ---- the fp8 linear on a library-owned workspace (qtts_fp8_linear_strips_static) ---------
+// `scratch` is that workspace: one array per GPU, kept until the process ends.  In host code
+// its name is a host-side stand-in, never a device address; the device address of each
+// GPU's copy comes from hipGetSymbolAddress, with that GPU current, and only that address
+// is handed to kernels.
+static __device__ __align__(256) unsigned char scratch[QTTS_STATIC_SCRATCH_BYTES];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+__global__ void zero_words_kernel(uint32_t* p, int n) {
+  const int i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+// The current GPU's scratch address, resolved once per GPU.  On that first call the split-K
+// counter block at its start is cleared with a kernel on `st` (the loader zero-fills the
+// array too; every later call leaves the counters at zero again).
+int scratch_of_current_device(hipStream_t st, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return qtts_set_error(QTTS_ERR_UNSUPPORTED, "no HIP device: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxDevices) return qtts_set_error(QTTS_ERR_UNSUPPORTED, "device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return qtts_set_error(QTTS_ERR_HIP, "static scratch: hipGetSymbolAddress failed on device %d: %s", dev,
+                            hipGetErrorString(e));
+    const int words = (int)(qtts::kCounterBytes / 4);
+    qtts::launch(zero_words_kernel, dim3((words + 255) / 256), dim3(256), 0, st, (uint32_t*)p, words);
+    QTTS_TRY(qtts_check_launch("static scratch clear"));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return QTTS_OK;
+}
+}  // namespace
+
+extern "C" {
+
+int qtts_fp8_linear_strips_static(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
+                                  int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
+                                  int algo, void* stream) {
+  QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "fp8_linear_strips_static: negative size");
+  QTTS_REQUIRE(m < (1ll << 31) && k < (1ll << 31), "fp8_linear_strips_static: size too large");
+  // The activation codes, their scales and the counter block must fit; a split-K choice that
+  // does not fit in what is left runs without the split.
+  const int64_t least = qtts::kCounterBytes + al256(m * k) + al256(m * 4);
+  if (least > QTTS_STATIC_SCRATCH_BYTES)
+    return qtts_set_error(QTTS_ERR_WORKSPACE,
+                          "fp8_linear_strips_static: m * k = %lld activation bytes need %lld workspace bytes, "
+                          "more than the %lld of the static scratch",
+                          (long long)(m * k), (long long)least, (long long)QTTS_STATIC_SCRATCH_BYTES);
+  if (m == 0 || n == 0) return fp8_linear_impl(x, x_dtype, m, k, ldx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y,
+                                               ldy, div_mode, algo, nullptr, 0, stream);
+  QTTS_TRY(current_device_check());
+  void* ws = nullptr;
+  QTTS_TRY(scratch_of_current_device((hipStream_t)stream, &ws));
+  return fp8_linear_impl(x, x_dtype, m, k, ldx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y, ldy, div_mode, algo, ws,
+                         QTTS_STATIC_SCRATCH_BYTES, stream);
+}
+
 int qtts_quant_act_int8_rows(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int8_t* qx, float* sx,
                              int div_mode, void* stream) {
   QTTS_REQUIRE(m >= 0 && k >= 0, "quant_act_int8_rows: negative size");

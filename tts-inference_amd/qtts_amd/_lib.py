@@ -26,6 +26,8 @@ ERR_UNSUPPORTED = -2
 ERR_NOT_IMPLEMENTED = -3
 ERR_HIP = -4
 ERR_WORKSPACE = -5
+#: bytes of the library-owned workspace of qtts_fp8_linear_strips_static (QTTS_STATIC_SCRATCH_BYTES)
+STATIC_SCRATCH_BYTES = 32 << 20
 
 # qtts_dtype
 F32, BF16, F16 = 0, 1, 2
@@ -61,6 +63,7 @@ EXPORTS = (
     "qtts_w8a16_gemm_strips",
     "qtts_w8a8_fp8_gemm_strips",
     "qtts_fp8_linear_strips",
+    "qtts_fp8_linear_strips_static",
     "qtts_quant_act_int8_rows",
     "qtts_w8a8_int8_gemm",
     "qtts_int8_linear",
@@ -142,6 +145,8 @@ def load() -> ctypes.CDLL:
         L.qtts_w8a8_fp8_gemm_strips.argtypes = [p, p, i64, i64, i64, p, i64, p, p, p, i32, i64, i32, p, i64, p]
         L.qtts_fp8_linear_strips.restype = i32
         L.qtts_fp8_linear_strips.argtypes = [p, i32, i64, i64, i64, p, i64, p, p, p, i64, i32, i32, p, i64, p]
+        L.qtts_fp8_linear_strips_static.restype = i32
+        L.qtts_fp8_linear_strips_static.argtypes = [p, i32, i64, i64, i64, p, i64, p, p, p, i64, i32, i32, p]
         L.qtts_quant_act_int8_rows.restype = i32
         L.qtts_quant_act_int8_rows.argtypes = [p, i32, i64, i64, i64, p, p, i32, p]
         L.qtts_w8a8_int8_gemm.restype = i32
