@@ -317,15 +317,9 @@ def test_w8a16_strips_staged_rows_match_direct(ops, xdt, sdt):
                 what = f"m={m} n={n} k={k} S={splits} W={waves} C={cpw} {xdt} {sdt}"
                 assert torch.equal(staged, direct), what
                 assert_close(staged, ref, what)
-            # 8 waves of 12 chunks: staged only (the automatic choice for K = 6144 from 2 rows); the
-            # staged kernels take whole 16-row strips only (their epilogue reads each strip's scale
-            # and bias as one scalar load), so a ragged N cannot have it
-            if n % 16 == 0:
-                y = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, 0, 8, 12))
-                assert_close(y, ref, f"m={m} n={n} k={k} W=8 C=12 {xdt} {sdt}")
-            else:
-                with pytest.raises(ValueError, match="not built"):
-                    ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, 0, 8, 12))
+            # 8 waves of 12 chunks: staged only (the automatic choice for K = 6144 from 2 rows)
+            y = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(1, 0, 8, 12))
+            assert_close(y, ref, f"m={m} n={n} k={k} W=8 C=12 {xdt} {sdt}")
 
 
 def test_w8a16_strips_ragged_and_tile(ops):

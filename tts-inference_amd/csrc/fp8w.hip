@@ -101,7 +101,7 @@ int qtts_launch_fp8w(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8 weight-only skinny kernel handles M <= 16, got M=%lld",
                           (long long)m);
   SkinnyCfg c = fp8w_skinny_cfg(m, n, k, algo);
-  const bool staged = m <= 8 && !((algo >> 24) & 0x40) && skinny_scalar_epilogue_ok(n, scale, bias);
+  const bool staged = m <= 8 && !((algo >> 24) & 0x40);
   if (!staged && c.waves == 8 && c.cpw == 12 && ((algo >> 16) & 0xff) == 0)  // 12 chunks a wave: staged rows only
     c = skinny_cfg(m, n, k, splits, 16, 6);
   const int64_t need = skinny_ws(c);

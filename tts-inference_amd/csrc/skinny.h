@@ -30,34 +30,6 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
   else return to_f32(T{(uint16_t)b});
 }
 
-// The 16 values of one output strip (scale or bias) in SGPRs: 8 dwords of 16-bit values
-// or 16 of fp32, read through the scalar cache (the address is uniform across the
-// workgroup: a constant-address-space pointer lets the compiler use s_load).
-template <typename T> struct StripWords {
-  static constexpr int kWords = sizeof(T) == 2 ? 8 : 16;
-  uint32_t w[kWords];
-};
-typedef const __attribute__((address_space(4))) uint32_t* const_u32_ptr;
-
-template <typename T> __device__ __forceinline__ StripWords<T> sload_strip16(const T* p) {
-  StripWords<T> s;
-  const const_u32_ptr c = (const_u32_ptr)(const void*)p;
-#pragma unroll
-  for (int i = 0; i < StripWords<T>::kWords; ++i) s.w[i] = c[i];
-  return s;
-}
-
-// Raw bits of value 4g + i of the strip (the rows lane group g holds in the MFMA result).
-template <typename T> __device__ __forceinline__ uint32_t strip_bits(const StripWords<T>& s, int g, int i) {
-  if constexpr (sizeof(T) == 2) {
-    const int k = i >> 1;
-    const uint32_t d = g == 0 ? s.w[k] : (g == 1 ? s.w[2 + k] : (g == 2 ? s.w[4 + k] : s.w[6 + k]));
-    return (i & 1) ? d >> 16 : d & 0xffffu;
-  } else {
-    return g == 0 ? s.w[i] : (g == 1 ? s.w[4 + i] : (g == 2 ? s.w[8 + i] : s.w[12 + i]));
-  }
-}
-
 // ------------------------------------------------------------------------------------
 // skinny: M <= 16 * MB (MB m-blocks of 16 activation rows; MB > 1 on strip weights
 // with K % 64 == 0 only)
@@ -93,8 +65,8 @@ template <typename T> __device__ __forceinline__ uint32_t strip_bits(const Strip
 //   to two MFMAs, and the workgroup stores y[:, c] = XT(XT(silu(g)) * u) for g, u the
 //   linear's outputs of columns c and c + N/2 rounded to XT: y is [M, N/2].  The
 //   gate_up output itself is never stored.
-// Parameters: everything the kernel reads before its first loads and its scalar epilogue
-// loads (q, x, scale, bias, aux, ldx, M and the split count, K, N) comes first, in the 14
+// Parameters: everything the kernel reads before its first loads (q, x, scale, bias, aux,
+// ldx, M and the split count, K, N) comes first, in the 14
 // dwords the hardware preloads into SGPRs at wave launch (kernarg preloading, build.py), so
 // no kernel-argument load stands between a wave's start and its weight loads.  Measured on the talker linears (cold weights, M = 1): the former order,
 // whose early values sat in two 64-byte argument lines fetched one after the other, plus the
@@ -231,58 +203,25 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     }
   };
   // Epilogue operands: raw bits, loaded unconditionally (clamped index; y stands in
-  // for a missing bias), so nothing needs their values before the epilogue.
-  // The staged-row kernels (MX > 0) take them through the scalar cache instead: the strip's 16
-  // values are uniform across the workgroup, so each array is one scalar load, and the vector
-  // memory path carries only x and the weights.  The host launches them only on whole strips
-  // of 4-byte aligned arrays (skinny_scalar_epilogue_ok).
-  constexpr bool epi_scalar = MX > 0;
+  // for a missing bias), so nothing needs their values before the epilogue.  (Loading a
+  // strip's scale and bias once per workgroup through the scalar cache instead was measured
+  // 0.1-0.2 us a launch slower on the talker linears: the LDS staging of the rows waits on
+  // every outstanding scalar load, and those miss to HBM like the weights.)
   uint32_t sc[4] = {0u, 0u, 0u, 0u}, bi[4] = {0u, 0u, 0u, 0u}, rb[RES ? 4 : 1] = {0u};
   uint32_t su[PAIR ? 4 : 1] = {0u}, bu[PAIR ? 4 : 1] = {0u};  // PAIR: the up rows' scale and bias
-  StripWords<ST> ssc, ssu;
-  StripWords<XT> sbi, sbu;
-  // The scalar loads go out first of all (their pointers are preloaded): they return within
-  // the round trip of the activation rows, whose LDS staging waits on every outstanding
-  // scalar load.
-  auto issue_epilogue_scalar = [&]() {
-    if constexpr (epi_scalar) {
-      ssc = sload_strip16(scale + strip * 16);
-      if (bias) sbi = sload_strip16(bias + strip * 16);
-      if constexpr (PAIR) {
-        ssu = sload_strip16(scale + (N >> 1) + strip * 16);
-        if (bias) sbu = sload_strip16(bias + (N >> 1) + strip * 16);
-      }
-    }
-  };
   auto issue_epilogue = [&]() {
     const XT* bsrc = bias ? bias : y;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int nn = min(strip * 16 + 4 * g + i, N - 1);
-      if constexpr (!epi_scalar) {
-        sc[i] = load_bits(scale + nn);
-        bi[i] = load_bits(bsrc + nn);
-        if constexpr (PAIR) {
-          const int nu = min(nn + (N >> 1), N - 1);
-          su[i] = load_bits(scale + nu);
-          bu[i] = load_bits(bsrc + nu);
-        }
+      sc[i] = load_bits(scale + nn);
+      bi[i] = load_bits(bsrc + nn);
+      if constexpr (PAIR) {
+        const int nu = min(nn + (N >> 1), N - 1);
+        su[i] = load_bits(scale + nu);
+        bu[i] = load_bits(bsrc + nu);
       }
       if constexpr (RES) rb[i] = load_bits(res + (int64_t)min(r, M - 1) * ldr + nn);
-    }
-  };
-  // The scalar operands into the per-lane form the epilogue reads (rows 4g .. 4g + 3).
-  auto take_scalar_epilogue = [&]() {
-    if constexpr (epi_scalar) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sc[i] = strip_bits(ssc, g, i);
-        bi[i] = bias ? strip_bits(sbi, g, i) : 0u;
-        if constexpr (PAIR) {
-          su[i] = strip_bits(ssu, g, i);
-          bu[i] = bias ? strip_bits(sbu, g, i) : 0u;
-        }
-      }
     }
   };
 
@@ -378,7 +317,6 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   // unit in issue order, and the weight stream is the critical path.  (Every wave
   // fetches them: a branch on the wave index would end in a wait for all loads.)
   if (wc0 < wc1) {  // wave-uniform: waves past the K range only reduce
-    issue_epilogue_scalar();
     issue_x();
     issue(wc0);
     // The epilogue's addresses need kernel arguments past the preloaded ones (bias, y):
@@ -449,7 +387,6 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{a[4 * mb], a[4 * mb + 1], a[4 * mb + 2], a[4 * mb + 3]};
   }
 
-  take_scalar_epilogue();
   // D layout of the 16x16 MFMA: lane (r, g) holds rows 4g..4g+3 (weight rows n) of
   // column r (activation row m = r + 16 mb).
 #pragma unroll
@@ -476,12 +413,6 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
 }
 
 // ---- host side: the skinny configuration ------------------------------------------
-
-// Whether a call may use the staged-row kernels, which read each strip's scale and bias
-// through the scalar cache: whole strips (N % 16 == 0) of 4-byte aligned arrays.
-inline bool skinny_scalar_epilogue_ok(int64_t n, const void* scale, const void* bias) {
-  return n % 16 == 0 && (uintptr_t)scale % 4 == 0 && (uintptr_t)bias % 4 == 0;
-}
 
 struct SkinnyCfg { int mb, waves, cpw, S, cps, strips; };
 

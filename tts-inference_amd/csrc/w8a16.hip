@@ -303,7 +303,7 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
     const int cpw = (algo >> 24) & 0x3f;
     const bool direct_x = (algo >> 24) & 0x40;
     SkinnyCfg c = skinny_cfg(m, n, k, splits, waves, cpw);
-    const bool staged = c.mb == 1 && wide_ok && m <= 8 && !direct_x && skinny_scalar_epilogue_ok(n, scale, bias);
+    const bool staged = c.mb == 1 && wide_ok && m <= 8 && !direct_x;
     // Staged rows from 2 rows up: 8 waves of 12 chunks beat 16 of 6 (measured on the
     // talker down projection, K = 6144, M = 2..8).
     if (staged && m >= 2 && waves == 0 && cpw == 0 && c.waves == 16 && c.S == 1 && 8 * 12 >= (k + 63) / 64)

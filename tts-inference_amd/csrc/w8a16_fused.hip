@@ -199,7 +199,6 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
               bool pair = false) {
   const int splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff, cpw = (algo >> 24) & 0x3f;
   const int64_t m = in.m, n = in.n, k = in.k;
-  if (!skinny_scalar_epilogue_ok(n, in.scale, in.bias)) return 1;  // the unfused kernels serve it
   if (pair) {
     if (splits > 1 || m > 8 || n % 32) return 1;
     SkinnyCfg c = skinny_cfg(m, n / 2, k, 1, waves, cpw);  // one workgroup per gate strip
