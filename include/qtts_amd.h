@@ -40,8 +40,19 @@ typedef enum { QTTS_F32 = 0, QTTS_BF16 = 1, QTTS_F16 = 2 } qtts_dtype;
  * QTTS_DIV_IEEE:   t / c, what torch computes for a CPU tensor. */
 typedef enum { QTTS_DIV_DEVICE = 0, QTTS_DIV_IEEE = 1 } qtts_div_mode;
 
-/* Kernel family for the GEMMs.  AUTO picks by shape; the calibrator pins one. */
-typedef enum { QTTS_ALGO_AUTO = 0, QTTS_ALGO_SKINNY = 1, QTTS_ALGO_TILE = 2 } qtts_algo;
+/* Kernel family for the GEMMs.  AUTO picks by shape; the calibrator pins one.
+ * SKINNY_HALF and SKINNY_QUARTER (qtts_w8a16_gemm_strips, qtts_w8a16_fused_gemm_strips and
+ * qtts_w8a16_silu_mul_gemm_strips only): the skinny kernel with each
+ * 16-row weight strip shared by 2 (or 4) workgroups of 8 (or 4) rows, for at most 8 (or 4)
+ * activation rows, K a multiple of 128 (or 256) and no split; AUTO takes them where the
+ * strips alone would leave compute units idle. */
+typedef enum {
+    QTTS_ALGO_AUTO = 0,
+    QTTS_ALGO_SKINNY = 1,
+    QTTS_ALGO_TILE = 2,
+    QTTS_ALGO_SKINNY_HALF = 3,
+    QTTS_ALGO_SKINNY_QUARTER = 4
+} qtts_algo;
 
 /* Strip layouts (see qtts_to_strips). */
 typedef enum { QTTS_STRIP_INT8 = 0, QTTS_STRIP_FP8 = 1 } qtts_strip_kind;

@@ -134,9 +134,10 @@ def test_residual_epilogue(ops, n, k):
             x = torch.randn(m, k, device="cuda", generator=g).to(dtype)
             r = (torch.randn(m, n, device="cuda", generator=g) * 4).to(dtype)
             b = (torch.randn(n, device="cuda", generator=g) * 0.1).to(dtype) if m % 2 else None
-            for algo in (0, ops.algo_code(1, 0, 4, 8), ops.algo_code(1, 3, 2, 8), ops.algo_code(1, 0, 8, 12)):
-                if m > 8 and algo == ops.algo_code(1, 0, 8, 12):
-                    continue  # 8 waves of 12 chunks are built for staged rows only
+            half = ops.algo_code(ops.ALGO_SKINNY_HALF)
+            for algo in (0, ops.algo_code(1, 0, 4, 8), ops.algo_code(1, 3, 2, 8), ops.algo_code(1, 0, 8, 12), half):
+                if m > 8 and algo in (ops.algo_code(1, 0, 8, 12), half):
+                    continue  # 8 waves of 12 chunks and half strips are built for staged rows only
                 what = f"{dtype} n={n} k={k} m={m} algo={algo:#x}"
                 lin = ops.w8a16_gemm_strips(x, qs, n, s, b, algo)
                 want = r + lin
@@ -159,7 +160,8 @@ def test_silu_and_residual(ops, n, k):
             gu = (torch.randn(m, 2 * k, device="cuda", generator=g) * 3).to(dtype)
             r = torch.randn(m, n, device="cuda", generator=g).to(dtype)
             for scale in (s, f32):
-                for algo in (0, ops.algo_code(1, 0, 16, 6), ops.algo_code(1, 2, 4, 8)):
+                for algo in (0, ops.algo_code(1, 0, 16, 6), ops.algo_code(1, 2, 4, 8),
+                             ops.algo_code(ops.ALGO_SKINNY_HALF)):
                     what = f"{dtype} n={n} k={k} m={m} algo={algo:#x} scale {scale.dtype}"
                     want = r + ops.w8a16_silu_mul_gemm_strips(gu, qs, n, scale, None, algo)
                     y = ops.w8a16_fused_gemm_strips(gu, qs, n, scale, prologue=PRO_SILU_MUL, residual=r, algo=algo)

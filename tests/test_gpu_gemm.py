@@ -591,3 +591,62 @@ def test_w8a16_strips_skinny_blocks_dtypes(ops):
     q, s = ops.pack_int8(w, torch.bfloat16)
     with pytest.raises(ValueError, match="M <= 64"):
         ops.w8a16_gemm_strips(x, ops.to_strips(q), 64, s, None, ops.algo_code(1))
+
+
+# (SUB, waves, units per wave) pairs built for row-split strips (w8a16_xrows_sub.hip)
+SUB_PAIRS = {2: ((1, 8), (2, 8), (4, 4), (4, 8), (8, 6), (16, 3)),
+             4: ((1, 8), (2, 6), (4, 6))}
+
+
+@pytest.mark.parametrize("xdt,sdt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32),
+                                     (torch.float16, torch.float16)])
+def test_w8a16_strips_row_split(ops, xdt, sdt):
+    """Row-split strips (2 or 4 workgroups per 16-row strip, SUB chunks per MFMA) against the oracle:
+    every built (waves, units) pair that covers K in one group, ragged N, a bias on odd M, every M
+    the split allows; the automatic choice too, and the same bits on a second call."""
+    for (n, k) in ((2048, 2048), (2048, 6144), (1024, 3072), (1000, 1024), (40, 512), (24, 256)):
+        nch = k // 64
+        q = s = qs = None
+        for m in range(1, 9):
+            x, w, b = _make(m, n, k, dtype=xdt, bias=(m % 2 == 1), seed=3 * n + k + m)
+            if q is None:
+                q, s = ops.pack_int8(w, sdt)
+                qs = ops.to_strips(q)
+            ref = _oracle_w8a16(x, q, s, b)
+            y = ops.w8a16_gemm_strips(x, qs, n, s, b)
+            assert_close(y, ref, f"auto m={m} n={n} k={k} {xdt} {sdt}")
+            assert torch.equal(y, ops.w8a16_gemm_strips(x, qs, n, s, b)), f"auto not deterministic m={m} n={n}"
+            for sub, family in ((2, ops.ALGO_SKINNY_HALF), (4, ops.ALGO_SKINNY_QUARTER)):
+                if m > 16 // sub or nch % sub:
+                    with pytest.raises(ValueError, match="row-split"):
+                        ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(family))
+                    continue
+                units = nch // sub
+                for waves, cpw in SUB_PAIRS[sub]:
+                    if waves * cpw < units or cpw > 2 * units:
+                        continue
+                    what = f"sub={sub} W={waves} C={cpw} m={m} n={n} k={k} {xdt} {sdt}"
+                    print(what, flush=True)
+                    y = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(family, 0, waves, cpw))
+                    assert_close(y, ref, what)
+                # the default waves for this split
+                assert_close(ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(family)), ref,
+                             f"sub={sub} default m={m} n={n} k={k}")
+
+
+def test_w8a16_strips_row_split_rejects(ops):
+    x, w, b = _make(9, 256, 512, seed=5)
+    q, s = ops.pack_int8(w, torch.bfloat16)
+    qs = ops.to_strips(q)
+    with pytest.raises(ValueError, match="row-split"):  # 9 rows: more than the 8 a half strip takes
+        ops.w8a16_gemm_strips(x, qs, 256, s, b, ops.algo_code(ops.ALGO_SKINNY_HALF))
+    with pytest.raises(ValueError, match="row-split"):  # an explicit split count
+        ops.w8a16_gemm_strips(x[:2], qs, 256, s, b, ops.algo_code(ops.ALGO_SKINNY_HALF, 2))
+    with pytest.raises(ValueError, match="cover less"):  # 1 wave of 3 units for 4 units of K
+        ops.w8a16_gemm_strips(x[:2], qs, 256, s, b, ops.algo_code(ops.ALGO_SKINNY_HALF, 0, 1, 3))
+    with pytest.raises(ValueError, match="not built"):
+        ops.w8a16_gemm_strips(x[:2], qs, 256, s, b, ops.algo_code(ops.ALGO_SKINNY_HALF, 0, 1, 5))
+    xr, wr, _ = _make(2, 64, 640, seed=6)  # K = 10 chunks: not a multiple of 4
+    qr, sr = ops.pack_int8(wr, torch.bfloat16)
+    with pytest.raises(ValueError, match="row-split"):
+        ops.w8a16_gemm_strips(xr, ops.to_strips(qr), 64, sr, None, ops.algo_code(ops.ALGO_SKINNY_QUARTER))

@@ -138,6 +138,11 @@ bool algo_ok(int a) {
   const int f = a & 0xff;
   return f == QTTS_ALGO_AUTO || f == QTTS_ALGO_SKINNY || f == QTTS_ALGO_TILE;
 }
+// The families of the W8A16 strip GEMM: the others plus the row-split skinny kernels.
+bool algo_ok_rows(int a) {
+  const int f = a & 0xff;
+  return algo_ok(a) || f == QTTS_ALGO_SKINNY_HALF || f == QTTS_ALGO_SKINNY_QUARTER;
+}
 int64_t al256(int64_t v) { return (v + 255) & ~(int64_t)255; }
 
 // Whether the byte spans of two [rows, cols] matrices (row strides lda, ldb, elements
@@ -210,7 +215,9 @@ int qtts_device_supported(int device) {
 }
 
 int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo) {
-  if (m < 0 || n < 0 || k < 0 || !algo_ok(algo)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "bad workspace query");
+  const bool rows_ok = op == QTTS_OP_W8A16 || op == QTTS_OP_W8A16_FUSED || op == QTTS_OP_W8A16_SILU;
+  if (m < 0 || n < 0 || k < 0 || !(rows_ok ? algo_ok_rows(algo) : algo_ok(algo)))
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "bad workspace query");
   if (m == 0 || n == 0) return 0;
   switch (op) {
     case QTTS_OP_W8A16: return qtts_w8a16_ws_bytes(m, n, k, algo);
@@ -276,7 +283,7 @@ int qtts_w8a16_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int
                (long long)n, (long long)k);
   QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "w8a16_gemm_strips: size too large");
   QTTS_REQUIRE(dtype_ok(x_dtype) && dtype_ok(scale_dtype), "w8a16_gemm_strips: bad dtype code");
-  QTTS_REQUIRE(algo_ok(algo), "w8a16_gemm_strips: bad algo %d", algo);
+  QTTS_REQUIRE(algo_ok_rows(algo), "w8a16_gemm_strips: bad algo %d", algo);
   QTTS_REQUIRE(ldx >= k && ldy >= n, "w8a16_gemm_strips: leading dimension smaller than the row");
   QTTS_REQUIRE(ws_bytes >= 0, "w8a16_gemm_strips: negative workspace size");
   if (m == 0 || n == 0) return QTTS_OK;
@@ -576,7 +583,7 @@ int qtts_w8a16_silu_mul_gemm_strips(const void* gate_up, int x_dtype, int64_t m,
   QTTS_REQUIRE(m < 65536 && n < (1ll << 31) && k < (1ll << 30), "w8a16_silu_mul_gemm_strips: size too large");
   QTTS_REQUIRE(x_dtype == QTTS_BF16 || x_dtype == QTTS_F16, "w8a16_silu_mul_gemm_strips: activations must be bf16 or fp16");
   QTTS_REQUIRE(dtype_ok(scale_dtype), "w8a16_silu_mul_gemm_strips: bad scale dtype code");
-  QTTS_REQUIRE(algo_ok(algo), "w8a16_silu_mul_gemm_strips: bad algo %d", algo);
+  QTTS_REQUIRE(algo_ok_rows(algo), "w8a16_silu_mul_gemm_strips: bad algo %d", algo);
   QTTS_REQUIRE(k % 16 == 0, "w8a16_silu_mul_gemm_strips: K %% 16 != 0 (K=%lld)", (long long)k);
   QTTS_REQUIRE(ld_gate_up >= 2 * k && ldy >= n, "w8a16_silu_mul_gemm_strips: leading dimension smaller than the row");
   QTTS_REQUIRE(ws_bytes >= 0, "w8a16_silu_mul_gemm_strips: negative workspace size");
@@ -607,7 +614,7 @@ int qtts_w8a16_fused_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t 
   QTTS_REQUIRE(m < 65536 && n < (1ll << 31) && k < (1ll << 30), "w8a16_fused_gemm_strips: size too large");
   QTTS_REQUIRE(x_dtype == QTTS_BF16 || x_dtype == QTTS_F16, "w8a16_fused_gemm_strips: activations must be bf16 or fp16");
   QTTS_REQUIRE(dtype_ok(scale_dtype), "w8a16_fused_gemm_strips: bad scale dtype code");
-  QTTS_REQUIRE(algo_ok(algo), "w8a16_fused_gemm_strips: bad algo %d", algo);
+  QTTS_REQUIRE(algo_ok_rows(algo), "w8a16_fused_gemm_strips: bad algo %d", algo);
   QTTS_REQUIRE(prologue == QTTS_PRO_NONE || prologue == QTTS_PRO_SILU_MUL || prologue == QTTS_PRO_RMS_NORM,
                "w8a16_fused_gemm_strips: bad prologue %d", prologue);
   QTTS_REQUIRE(k % 64 == 0, "w8a16_fused_gemm_strips: K %% 64 != 0 (K=%lld)", (long long)k);

@@ -52,6 +52,44 @@ int launch_wc(const SkinnyCfg& c, const void* x, int64_t m, int64_t k, int64_t l
   return QTTS_OK;
 }
 
+// Row-split strips (skinny.h, SUB = 2), the automatic choice's pairs (skinny_cfg_sub).
+template <typename XT, int W, int CPW, int MX>
+void launch_sub(const void* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n, const float* scale,
+                const void* bias, void* y, int64_t ldy, unsigned blocks, hipStream_t st) {
+  qtts::launch(&w8a16_skinny_kernel<XT, float, W, CPW, kLayoutStrips, true, 1, MX, true, kProNone, false, false, 2>,
+               dim3(blocks, 1), dim3(W * 64), 0, st, (const int8_t*)qs, (const XT*)x, scale, (const XT*)bias,
+               (const XT*)nullptr, (int)ldx, (int)(m | (1 << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0,
+               (float*)nullptr, (unsigned*)nullptr, 0.0f, (const XT*)nullptr, (int64_t)0);
+}
+
+template <typename XT, int MX>
+int launch_sub_wc(const SkinnyCfg& c, const void* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n,
+                  const float* scale, const void* bias, void* y, int64_t ldy, unsigned blocks, hipStream_t st) {
+#define QTTS_F8W_SUB(W, CPW) launch_sub<XT, W, CPW, MX>(x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st)
+  switch (c.waves * 64 + c.cpw) {
+    case 1 * 64 + 8: QTTS_F8W_SUB(1, 8); break;
+    case 2 * 64 + 8: QTTS_F8W_SUB(2, 8); break;
+    case 4 * 64 + 4: QTTS_F8W_SUB(4, 4); break;
+    case 4 * 64 + 8: QTTS_F8W_SUB(4, 8); break;
+    case 8 * 64 + 6: QTTS_F8W_SUB(8, 6); break;
+    case 16 * 64 + 3: QTTS_F8W_SUB(16, 3); break;
+    default: return 1;
+  }
+#undef QTTS_F8W_SUB
+  return QTTS_OK;
+}
+
+template <typename XT>
+int launch_sub_rows(int mx, const SkinnyCfg& c, const void* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs,
+                    int64_t n, const float* scale, const void* bias, void* y, int64_t ldy, unsigned blocks,
+                    hipStream_t st) {
+  switch (mx) {
+    case 1: return launch_sub_wc<XT, 1>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st);
+    case 4: return launch_sub_wc<XT, 4>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st);
+    default: return launch_sub_wc<XT, 8>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st);
+  }
+}
+
 template <typename XT>
 int launch_rows(int mx, const SkinnyCfg& c, const void* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs,
                 int64_t n, const float* scale, const void* bias, void* y, int64_t ldy, float* part, unsigned* counters,
@@ -100,6 +138,18 @@ int qtts_launch_fp8w(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
   if (m > 16)
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8 weight-only skinny kernel handles M <= 16, got M=%lld",
                           (long long)m);
+  // Half strips where whole ones leave compute units idle: the W8A16 launch's automatic rule.
+  if ((algo & 0xff) == QTTS_ALGO_AUTO && (algo >> 8) == 0 && skinny_auto_sub(m, n, k) == 2 && ldx <= INT32_MAX) {
+    const SkinnyCfg c = skinny_cfg_sub(n, k, 2, 0, 0);
+    const int64_t blocks = ((int64_t)c.strips * 2 + 7) / 8 * 8;
+    if (c.waves * c.cpw >= c.cps && blocks < ((int64_t)1 << 31)) {
+      const int mx = m == 1 ? 1 : (m <= 4 ? 4 : 8);
+      const int rc = x_dtype == QTTS_BF16
+                         ? launch_sub_rows<bf16_t>(mx, c, x, m, k, ldx, qs, n, scale, bias, y, ldy, (unsigned)blocks, st)
+                         : launch_sub_rows<f16_t>(mx, c, x, m, k, ldx, qs, n, scale, bias, y, ldy, (unsigned)blocks, st);
+      if (rc != 1) return rc == QTTS_OK ? qtts_check_launch("fp8w_skinny_sub") : rc;
+    }
+  }
   SkinnyCfg c = fp8w_skinny_cfg(m, n, k, algo);
   const bool staged = m <= 8 && !((algo >> 24) & 0x40);
   if (!staged && c.waves == 8 && c.cpw == 12 && ((algo >> 16) & 0xff) == 0)  // 12 chunks a wave: staged rows only

@@ -11,6 +11,9 @@
 #include "pipe.h"
 #include "splitk.h"
 
+// Whether the row-split kernel (w8a16_xrows_sub.hip) is built for (sub, waves, units per wave).
+int qtts_w8a16_sub_built(int sub, int waves, int cpw);
+
 namespace qtts {
 
 // Raw element bits, zero-extended to 32: a load whose value is not needed until the
@@ -65,6 +68,15 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 //   to two MFMAs, and the workgroup stores y[:, c] = XT(XT(silu(g)) * u) for g, u the
 //   linear's outputs of columns c and c + N/2 rounded to XT: y is [M, N/2].  The
 //   gate_up output itself is never stored.
+// SUB > 1 (staged rows, M <= 16 / SUB, no split, no PAIR): row-split strips.  SUB
+//   workgroups share each 16-row strip, workgroup p taking weight rows
+//   [p * RP, (p + 1) * RP) of it (RP = 16 / SUB), so a layer of few strips still spreads
+//   over every compute unit without a split-K meeting.  Each MFMA then covers SUB chunks
+//   ("a unit") of those RP rows: A row b * RP + i holds weight row i of chunk b of the unit
+//   and B column b * RP + j activation row j of the same chunk, so the SUB diagonal
+//   RP x RP blocks of D are the chunks' contributions (the off-diagonal blocks mix chunks
+//   and are never read) and the epilogue adds them, in chunk order, across lanes.  Every
+//   lane loads weight bytes it needs and every MFMA is useful, as with whole strips.
 // Parameters: everything the kernel reads before its first loads (q, x, scale, bias, aux,
 // ldx, M and the split count, K, N) comes first, in the 14
 // dwords the hardware preloads into SGPRs at wave launch (kernarg preloading, build.py), so
@@ -74,7 +86,7 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 enum : int { kProNone = 0, kProSiluMul = 1, kProRmsNorm = 2 };
 
 template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1, int MX = 0, bool F8W = false,
-          int PRO = kProNone, bool RES = false, bool PAIR = false>
+          int PRO = kProNone, bool RES = false, bool PAIR = false, int SUB = 1>
 __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     const int8_t* __restrict__ q, const XT* __restrict__ x, const ST* scale, const XT* bias,
     const XT* __restrict__ aux, int ldx, int MS, int K, int N, XT* y, int64_t ldy, int64_t ldq,
@@ -86,19 +98,23 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   static_assert(PRO == kProNone || MX > 0, "a prologue runs on staged rows");
   static_assert(!RES || MX > 0, "the residual epilogue is built with staged rows");
   static_assert(!PAIR || (MX > 0 && !RES && PRO != kProSiluMul), "the SiLU pair epilogue runs on staged rows");
+  static_assert(SUB == 1 || ((SUB == 2 || SUB == 4) && MX > 0 && MX <= 16 / SUB && !PAIR),
+                "row-split strips run on staged rows, at most 16 / SUB of them");
+  constexpr int RP = 16 / SUB;  // weight rows per workgroup
   constexpr bool SILU = PRO == kProSiluMul, NORM = PRO == kProRmsNorm;
   constexpr int NA = PAIR ? 2 : 1;  // accumulators a wave carries: gate (and up)
   __shared__ f32x4_t red[W > 1 ? W - 1 : 1][MB * NA][64];
   __shared__ float nss[NORM ? W : 1][NORM ? MX : 1];
-  __shared__ __align__(16) uint16_t xrow[MX > 0 ? W : 1][MX > 0 ? MX : 1][MX > 0 ? CPW * 64 : 8];
+  __shared__ __align__(16) uint16_t xrow[MX > 0 ? W : 1][MX > 0 ? MX : 1][MX > 0 ? CPW * SUB * 64 : 8];
 
-  // Grid: x = output strips (rounded up to a multiple of 8), y = K splits.  Workgroups are
+  // Grid: x = output strips (times SUB, rounded up to a multiple of 8), y = K splits.  Workgroups are
   // dealt to the 8 XCDs round-robin in x-fastest order, so with gridDim.x % 8 == 0 every
   // split of a strip runs on one XCD and its split-K meeting stays in one L2.
   // MS = M | S << 8: the rows (at most 64 here) and the split count share one preloaded dword
   // (gridDim.y would be a hidden-argument load).
   const int M = MS & 0xff, S = MS >> 8;
-  const int strip = blockIdx.x, split = blockIdx.y;
+  const int strip = SUB == 1 ? blockIdx.x : blockIdx.x / SUB, split = blockIdx.y;
+  const int part_row = SUB == 1 ? 0 : (blockIdx.x % SUB) * RP;  // this workgroup's first strip row
   const int strips = PAIR ? ((N >> 1) + 15) >> 4 : (N + 15) >> 4;  // PAIR: the gate strips
   if (strip >= strips) return;
 
@@ -108,10 +124,11 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   const int n = strip * 16 + r;
   const bool n_ok = n < N, m_ok = r < M;
   const int nchunks = (K + 63) >> 6;
-  // This workgroup's chunks: split `split` of S of ceil(nchunks / S) chunks each (the host's
-  // split size: ceil(n / ceil(n / ceil(n / s))) = ceil(n / s)).
-  int c0 = 0, c1 = nchunks;
-  if (S > 1) {
+  // This workgroup's units of SUB chunks (SUB divides nchunks, checked by the host): split
+  // `split` of S of ceil(units / S) units each (the host's split size:
+  // ceil(n / ceil(n / ceil(n / s))) = ceil(n / s)).
+  int c0 = 0, c1 = SUB == 1 ? nchunks : nchunks / SUB;
+  if (SUB == 1 && S > 1) {
     const int cps = (nchunks + S - 1) / S;
     c0 = split * cps;
     c1 = min(c0 + cps, nchunks);
@@ -123,7 +140,11 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   int64_t wstride;
   // PAIR: the up strip is strip + strips (strips = the gate strips, N/32).
   const int64_t up_off = PAIR ? (int64_t)strips * nchunks * 1024 : 0;
-  if constexpr (LAYOUT == kLayoutStrips) {
+  if constexpr (LAYOUT == kLayoutStrips && SUB > 1) {
+    // lane (r, g): strip row part_row + r % RP of chunk r / RP of each unit, bytes 16 g .. + 15
+    wp = q + (int64_t)strip * nchunks * 1024 + (r / RP) * 1024 + (part_row + r % RP + 16 * g) * 16;
+    wstride = SUB * 1024;
+  } else if constexpr (LAYOUT == kLayoutStrips) {
     wp = q + (int64_t)strip * nchunks * 1024 + lane * 16;
     wstride = 1024;
   } else {
@@ -213,7 +234,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     const XT* bsrc = bias ? bias : y;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int nn = min(strip * 16 + 4 * g + i, N - 1);
+      const int nn = min(strip * 16 + part_row + 4 * g + i, N - 1);
       sc[i] = load_bits(scale + nn);
       bi[i] = load_bits(bsrc + nn);
       if constexpr (PAIR) {
@@ -227,22 +248,23 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
 
   // Staged activation rows (MX > 0): vector v of lane l holds elements
   // 512 v + 8 l .. + 7 of the wave's K range of each row (XV vectors cover CPW
-  // chunks); lanes past the range repeat its last 8 elements.
-  constexpr int XV = (CPW * 64 + 511) / 512;
+  // units of SUB chunks); lanes past the range repeat its last 8 elements.
+  constexpr int XV = (CPW * SUB * 64 + 511) / 512;
+  const int xlen = (wc1 - wc0) * SUB * 64, xbeg = wc0 * SUB * 64;  // the wave's K range, elements
   // SILU: xu holds the up half; NORM: xu[0] holds the norm weight over the same range.
   i32x4_t xr[MX > 0 ? MX : 1][XV], xu[SILU ? MX : 1][SILU || NORM ? XV : 1];
   auto issue_x = [&]() {
     if constexpr (MX > 0) {
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
-        const int e = min(512 * v + 8 * lane, (wc1 - wc0) * 64 - 8);
+        const int e = min(512 * v + 8 * lane, xlen - 8);
 #pragma unroll
         for (int m = 0; m < MX; ++m) {
-          const XT* row = x + (int64_t)min(m, M - 1) * ldx + (int64_t)wc0 * 64 + e;
+          const XT* row = x + (int64_t)min(m, M - 1) * ldx + xbeg + e;
           xr[m][v] = *(const i32x4_t*)row;
           if constexpr (SILU) xu[m][v] = *(const i32x4_t*)(row + K);
           if constexpr (NORM) {
-            if (m == 0) xu[0][v] = *(const i32x4_t*)(aux + (int64_t)wc0 * 64 + e);
+            if (m == 0) xu[0][v] = *(const i32x4_t*)(aux + xbeg + e);
           }
         }
       }
@@ -254,7 +276,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     float ss = 0.0f;
 #pragma unroll
     for (int v = 0; v < XV; ++v) {
-      if (512 * v + 8 * lane < (wc1 - wc0) * 64) {
+      if (512 * v + 8 * lane < xlen) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const uint32_t p = (uint32_t)xr[m][v][e];
@@ -272,7 +294,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     if constexpr (NORM) {
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
-        const int e = min(512 * v + 8 * lane, (wc1 - wc0) * 64 - 8);
+        const int e = min(512 * v + 8 * lane, xlen - 8);
 #pragma unroll
         for (int m = 0; m < MX; ++m) {
           i32x4_t o;
@@ -289,7 +311,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     } else if constexpr (MX > 0) {
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
-        const int e = min(512 * v + 8 * lane, (wc1 - wc0) * 64 - 8);
+        const int e = min(512 * v + 8 * lane, xlen - 8);
 #pragma unroll
         for (int m = 0; m < MX; ++m) {
           if constexpr (SILU) *(i32x4_t*)&xrow[wave][m][e] = silu_mul8<XT>(xr[m][v], xu[m][v]);
@@ -299,13 +321,16 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     }
     if constexpr (MX > 0) {
       // B operand of lane (r, g): row r (rows >= M read row 0; their D columns are
-      // never stored), elements 64 u + 16 g .. + 15 of chunk u of the range.
-      const int rr = r < M ? r : 0;
+      // never stored), elements 64 u + 16 g .. + 15 of chunk u of the range.  SUB > 1:
+      // row r % RP of chunk r / RP of unit u.
+      const int rj = SUB == 1 ? r : r % RP;
+      const int rr = rj < M ? rj : 0;
 #pragma unroll
       for (int u = 0; u < CPW; ++u) {
         const int cu = min(u, wc1 - wc0 - 1);
-        xa[0][u] = *(const i32x4_t*)&xrow[wave][rr][64 * cu + 16 * g];
-        xb[0][u] = *(const i32x4_t*)&xrow[wave][rr][64 * cu + 16 * g + 8];
+        const int ch = SUB == 1 ? cu : cu * SUB + r / RP;
+        xa[0][u] = *(const i32x4_t*)&xrow[wave][rr][64 * ch + 16 * g];
+        xb[0][u] = *(const i32x4_t*)&xrow[wave][rr][64 * ch + 16 * g + 8];
       }
     }
   };
@@ -373,7 +398,21 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     inv_r = __shfl(1.0f / __builtin_sqrtf(ss / (float)K + eps), r, 64);
   }
 
-  if (S > 1) {
+  if constexpr (SUB == 2) {
+    // D rows 8 + i, columns 8 + j (chunk 1 of each unit) onto rows i, columns j (chunk 0):
+    // lane (j, g) for g < 2 takes lane (j + 8, g + 2), i.e. lane ^ 40.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[0][i] += __shfl_xor(acc[0][i], 40, 64);
+  } else if constexpr (SUB == 4) {
+    // block b (rows and columns 4b .. 4b + 3) of lane (j, 0) sits in lane j + 20 b
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float v = acc[0][i];
+      acc[0][i] = ((v + __shfl(v, lane + 20, 64)) + __shfl(v, lane + 40, 64)) + __shfl(v, lane + 60, 64);
+    }
+  }
+
+  if (SUB == 1 && S > 1) {
     float a[4 * MB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
@@ -395,8 +434,8 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     if (m < M) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int nn = strip * 16 + 4 * g + i;
-        if (nn < (PAIR ? N >> 1 : N)) {
+        const int nn = strip * 16 + part_row + 4 * g + i;
+        if ((SUB == 1 || 4 * g < RP) && nn < (PAIR ? N >> 1 : N)) {
           float v = (NORM ? acc[mb][i] * inv_r : acc[mb][i]) * bits_to_f32<ST>(sc[i]);
           if (bias) v += bits_to_f32<XT>(bi[i]);
           if constexpr (RES) v = bits_to_f32<XT>(rb[i]) + round_through<XT>(v);
@@ -464,6 +503,62 @@ inline SkinnyCfg skinny_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int
   c.cps = (nchunks + S - 1) / S;
   c.S = (nchunks + c.cps - 1) / c.cps;
   return c;
+}
+
+// Row-split strips (SUB = 2 or 4 workgroups per strip; staged rows, M <= 16 / SUB, no
+// split): W waves of CPW units of SUB chunks; cps holds the units of the full K.  By
+// default the fewest waves with at most 6 units each, then the fewest units per wave of a
+// built pair that covers K (6 units per wave measured best on the talker's down_proj and
+// the predictor's down_proj; 4 on the predictor's o_proj, 16 units in all).
+inline SkinnyCfg skinny_cfg_sub(int64_t n, int64_t k, int sub, int waves_req, int cpw_req) {
+  SkinnyCfg c;
+  c.mb = 1;
+  c.strips = (int)((n + 15) / 16);
+  c.S = 1;
+  c.cps = std::max(1, (int)((k + 63) / 64) / sub);
+  int W = waves_req;
+  int C = cpw_req;
+  if (W <= 0 || C <= 0) {
+    bool found = false;
+    int w0 = 1;
+    if (W <= 0 && C <= 0)
+      while (w0 < 16 && (c.cps + w0 - 1) / w0 > 6) w0 *= 2;
+    for (int w = W > 0 ? W : w0; w <= (W > 0 ? W : 16) && !found; w *= 2) {
+      for (int cpw = C > 0 ? C : 1; cpw <= (C > 0 ? C : 16) && !found; ++cpw) {
+        if (w * cpw >= c.cps && qtts_w8a16_sub_built(sub, w, cpw)) {
+          W = w;
+          C = cpw;
+          found = true;
+        }
+      }
+    }
+    if (!found) {  // reported as not built by the launcher
+      W = W > 0 ? W : 16;
+      C = C > 0 ? C : (c.cps + W - 1) / W;
+    }
+  }
+  c.waves = W;
+  c.cpw = C;
+  return c;
+}
+
+// Whether a call can take row-split strips: strip weights, K a multiple of SUB chunks, at
+// most 16 / SUB rows.
+inline bool skinny_sub_ok(int64_t m, int64_t k, int sub) {
+  return sub > 1 && m >= 1 && m <= 16 / sub && m <= 8 && k % 64 == 0 && (k / 64) % sub == 0;
+}
+
+// The automatic row split for a decode call: half strips where whole ones leave most compute
+// units idle (at most 64 strips) or give each of at most 128 workgroups 64 KiB or more
+// (K >= 4096).  Measured, cold weights, M = 1..8: the talker's down_proj (N = 2048, K = 6144)
+// 4.57 against 5.13 us at M = 1 and 5.77 against 6.46 at M = 8; the code predictor's o_proj
+// (N = 1024, K = 2048) 2.98 against 3.11 and down_proj (N = 1024, K = 3072) 3.31 against 3.84;
+// the talker's o_proj (N = 2048, K = 2048) 3.25 against 3.22, so it keeps whole strips.
+// Quarter strips lost on every talker and predictor shape.
+inline int skinny_auto_sub(int64_t m, int64_t n, int64_t k) {
+  const int64_t strips = (n + 15) / 16;
+  if ((strips <= 64 || (strips <= 128 && k >= 4096)) && skinny_sub_ok(m, k, 2)) return 2;
+  return 1;
 }
 
 inline int64_t skinny_ws(const SkinnyCfg& c) {

@@ -23,21 +23,42 @@ struct FusedArgs {
   float* part;
   unsigned* counters;
   SkinnyCfg c;
+  int sub;  // workgroups per strip (row-split strips when > 1)
   unsigned blocks;
   hipStream_t st;
 };
 
-template <typename XT, typename ST, int W, int CPW, int MX, int PRO, bool RES, bool PAIR = false>
+template <typename XT, typename ST, int W, int CPW, int MX, int PRO, bool RES, bool PAIR = false, int SUB = 1>
 void launch_fused_one(const FusedArgs& a) {
-  launch(&w8a16_skinny_kernel<XT, ST, W, CPW, kLayoutStrips, true, 1, MX, false, PRO, RES, PAIR>,
+  launch(&w8a16_skinny_kernel<XT, ST, W, CPW, kLayoutStrips, true, 1, MX, false, PRO, RES, PAIR, SUB>,
          dim3(a.blocks, a.c.S), dim3(W * 64), 0, a.st, a.qs, (const XT*)a.x, (const ST*)a.scale, (const XT*)a.bias,
          (const XT*)a.aux, (int)a.ldx, (int)(a.m | (a.c.S << 8)), (int)a.k, (int)a.n, (XT*)a.y, a.ldy, (int64_t)0, a.part,
          a.counters, a.eps, (const XT*)a.res, a.ldr);
 }
 
-// The (waves, chunks) pairs built with staged rows (qtts_w8a16_xrows_built).
+// The row-split pairs built for the fused kernels: the automatic choices of the half-strip
+// layers (skinny_auto_sub, skinny_cfg_sub), for the residual epilogue and the SiLU prologue.
+inline bool fused_sub_built(int sub, int waves, int cpw) {
+  return sub == 2 && ((waves == 4 && (cpw == 4 || cpw == 8)) || (waves == 8 && cpw == 6));
+}
+
+// The (waves, chunks) pairs built with staged rows (qtts_w8a16_xrows_built), and the
+// half-strip ones of fused_sub_built (at most 8 rows; not with the RMSNorm prologue).
 template <typename XT, typename ST, int MX, int PRO, bool RES>
 int launch_fused_wc(const FusedArgs& a) {
+  if (a.sub > 1) {
+    if constexpr (PRO != kProRmsNorm && MX <= 8) {
+      if (a.sub == 2) {
+        switch (a.c.waves * 64 + a.c.cpw) {
+          case 4 * 64 + 4: launch_fused_one<XT, ST, 4, 4, MX, PRO, RES, false, 2>(a); return 0;
+          case 4 * 64 + 8: launch_fused_one<XT, ST, 4, 8, MX, PRO, RES, false, 2>(a); return 0;
+          case 8 * 64 + 6: launch_fused_one<XT, ST, 8, 6, MX, PRO, RES, false, 2>(a); return 0;
+          default: break;
+        }
+      }
+    }
+    return 1;
+  }
   switch (a.c.waves * 64 + a.c.cpw) {
     case 1 * 64 + 8: launch_fused_one<XT, ST, 1, 8, MX, PRO, RES>(a); break;
     case 2 * 64 + 8: launch_fused_one<XT, ST, 2, 8, MX, PRO, RES>(a); break;

@@ -269,9 +269,14 @@ int qtts_launch_w8a16_pipe(const void* x, int x_dtype, int64_t m, int64_t k, int
                            int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
                            int splits, int stages, int shape, void* ws, int64_t ws_bytes, hipStream_t st);
 
+int qtts_launch_w8a16_skinny_sub(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
+                                 int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
+                                 int sub, int waves, int cpw, unsigned blocks, hipStream_t st);
+
 int64_t qtts_w8a16_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
   const int family = algo & 0xff, splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff;
   int64_t ws = 0;
+  if (family == QTTS_ALGO_SKINNY_HALF || family == QTTS_ALGO_SKINNY_QUARTER) return 0;  // no split
   const int cpw = (algo >> 24) & 0x3f;
   if (family == QTTS_ALGO_SKINNY || family == QTTS_ALGO_AUTO)
     ws = std::max(ws, skinny_ws(skinny_cfg(std::min<int64_t>(m, kSkinnyMaxM), n, k, splits, waves, cpw)));
@@ -289,6 +294,34 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
   int family = algo & 0xff;
   const int splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff;
   const bool wide_ok = LAYOUT == kLayoutStrips && k % 64 == 0;  // skinny beyond 16 rows
+  // Row-split strips: requested by family, or the automatic choice for staged decode rows
+  // where the strips alone would leave compute units idle.
+  int sub = family == QTTS_ALGO_SKINNY_HALF ? 2 : (family == QTTS_ALGO_SKINNY_QUARTER ? 4 : 1);
+  if (sub > 1) {
+    if (LAYOUT != kLayoutStrips || splits != 0 || ((algo >> 24) & 0x40) || !skinny_sub_ok(m, k, sub))
+      return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
+                            "w8a16 row-split strips (%d per strip) need strip weights, at most %d rows (got %lld), "
+                            "K a multiple of %d (got %lld) and no split",
+                            sub, std::min(8, 16 / sub), (long long)m, 64 * sub, (long long)k);
+  } else if (family == QTTS_ALGO_AUTO && LAYOUT == kLayoutStrips && splits == 0 && (algo >> 16) == 0) {
+    sub = skinny_auto_sub(m, n, k);
+  }
+  if (sub > 1) {
+    const int cpw = (algo >> 24) & 0x3f;
+    const SkinnyCfg c = skinny_cfg_sub(n, k, sub, waves, cpw);
+    const int64_t blocks = ((int64_t)c.strips * sub + 7) / 8 * 8;
+    if (c.waves * c.cpw < c.cps)
+      return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 row-split strips: %d waves of %d units cover less "
+                            "than the %d units of K", c.waves, c.cpw, c.cps);
+    if (!grid_ok(blocks) || ldx > INT32_MAX) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16: N or ldx too large");
+    const int rc = qtts_launch_w8a16_skinny_sub(x, std::is_same<XT, bf16_t>::value ? QTTS_BF16 : QTTS_F16, m, k, ldx,
+                                                q, n, scale, sdt, bias, y, ldy, sub, c.waves, c.cpw,
+                                                (unsigned)blocks, st);
+    if (rc != 1) return rc;
+    if (family != QTTS_ALGO_AUTO)
+      return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 row-split strips: %d waves of %d units are not built "
+                            "for %d workgroups per strip", c.waves, c.cpw, sub);
+  }
   if (family == QTTS_ALGO_AUTO)
     family = (m <= 16 || (wide_ok && m <= kSkinnyAutoMaxM && n * k <= kSkinnyAutoMaxBytes && k <= kSkinnyAutoMaxK))
                  ? QTTS_ALGO_SKINNY

@@ -229,6 +229,32 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
     if (rc != 0) return 1;
     return qtts_check_launch("w8a16_gate_up_silu");
   }
+  // Row-split strips: the plain launch's choice (w8a16.hip launch_fast), so a fused call and the
+  // plain GEMM it replaces give the same bits.
+  const int family = algo & 0xff;
+  int sub = family == QTTS_ALGO_SKINNY_HALF ? 2 : (family == QTTS_ALGO_SKINNY_QUARTER ? 4 : 1);
+  if (sub > 1 && (splits != 0 || !skinny_sub_ok(m, k, sub))) return 1;  // the separate path reports it
+  if (family == QTTS_ALGO_AUTO && splits == 0 && (algo >> 16) == 0) sub = skinny_auto_sub(m, n, k);
+  if (sub > 1) {
+    const SkinnyCfg c = skinny_cfg_sub(n, k, sub, waves, cpw);
+    if (!fused_sub_built(sub, c.waves, c.cpw) || c.waves * c.cpw < c.cps || in.ldx > INT32_MAX) return 1;
+    FusedArgs a = in;
+    a.c = c;
+    a.sub = sub;
+    a.blocks = (unsigned)(((int64_t)c.strips * sub + 7) / 8 * 8);
+    a.counters = nullptr;
+    a.part = nullptr;
+    const bool f32s = sdt == QTTS_F32;
+    int rc = 1;
+    if (pro == kProSiluMul) rc = res ? launch_fused<kProSiluMul, true, 1>(x_dtype, f32s, a)
+                                     : launch_fused<kProSiluMul, false, 1>(x_dtype, f32s, a);
+    else if (pro == kProNone && res)
+      rc = m == 1 ? launch_fused<kProNone, true, 1>(x_dtype, f32s, a)
+                  : (m <= 4 ? launch_fused<kProNone, true, 4>(x_dtype, f32s, a)
+                            : launch_fused<kProNone, true, 8>(x_dtype, f32s, a));
+    if (rc != 0) return 1;
+    return qtts_check_launch("w8a16_fused_skinny_sub");
+  }
   SkinnyCfg c = skinny_cfg(m, n, k, splits, waves, cpw);
   // As the plain staged launch: 8 waves of 12 chunks from 2 rows for long K.
   if (m >= 2 && waves == 0 && cpw == 0 && c.waves == 16 && c.S == 1 && 8 * 12 >= (k + 63) / 64)

@@ -36,6 +36,8 @@ DIV_DEVICE, DIV_IEEE = 0, 1
 # qtts_algo (bits 0-7); bits 8-15 split count, bits 16-23 waves per workgroup,
 # bits 24-31 chunks per wave of the skinny kernels (0 = automatic)
 ALGO_AUTO, ALGO_SKINNY, ALGO_TILE = 0, 1, 2
+#: the skinny kernel over row-split strips: 2 (HALF) or 4 (QUARTER) workgroups per 16-row strip
+ALGO_SKINNY_HALF, ALGO_SKINNY_QUARTER = 3, 4
 # qtts_op
 OP_W8A16, OP_W8A8_FP8, OP_FP8_LINEAR, OP_W8A8_INT8, OP_INT8_LINEAR, OP_FP8W, OP_W8A16_SILU, OP_W8A16_FUSED = range(8)
 # qtts_prologue
