@@ -131,14 +131,15 @@ def time_graph(torch, graph, steps: int, warmup: int) -> float:
     return start.elapsed_time(end) / steps
 
 
-def committed_traffic(name: str) -> tuple[int | None, str | None]:
-    """HBM bytes per launch from a committed rocprofv3 --pmc summary (FETCH_SIZE and WRITE_SIZE,
-    each scaled by what the counter reads for a copy of known size) under profiles/."""
+def committed_figure(name: str, key: str) -> tuple[float | None, str | None]:
+    """A figure a committed profile summary under profiles/ states on a ``key: value`` line: the
+    HBM bytes per launch of a rocprofv3 --pmc run (FETCH_SIZE and WRITE_SIZE, each scaled by what
+    the counter reads for a copy of known size), or a kernel's mean duration in a kernel trace."""
     path = os.path.join(ROOT, "profiles", name)
     try:
         for line in open(path):
-            if line.startswith("traffic_bytes_per_launch:"):
-                return int(line.split(":", 1)[1]), f"profiles/{name}"
+            if line.startswith(key + ":"):
+                return float(line.split(":", 1)[1]), f"profiles/{name}"
     except OSError:
         pass
     return None, None
@@ -274,11 +275,15 @@ def run_talker_stack(args, torch, ops):
     dur_ms = kernel_ms(ops, launches, reps=max(2, args.steps // 4))
     g_bytes = statistics.mean(w8a16_bytes(m, 12288, 2048) for m in ms)
     achieved = g_bytes / (dur_ms * 1e-3) / 1e9
-    traffic, traffic_src = committed_traffic("w8a16_skinny_gate_up_pmc.md")
+    traffic, traffic_src = committed_figure("w8a16_skinny_talker_stack_pmc.md", "traffic_bytes_per_launch")
+    prof_us, prof_src = committed_figure("w8a16_skinny_roofline_kernel_trace.md", "avg_launch_us_profile")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic, "traffic_source": traffic_src,
+                "frac": round(achieved / HBM_PEAK_GBPS, 4),
+                "traffic": None if traffic is None else int(traffic), "traffic_source": traffic_src,
                 "kernel": "w8a16_skinny_kernel (gate_up 12288x2048, M in 1,2,4,8)",
-                "avg_launch_us": round(dur_ms * 1e3, 3), "bytes_per_launch": round(g_bytes)}
+                "avg_launch_us": round(dur_ms * 1e3, 3), "bytes_per_launch": round(g_bytes),
+                # the same launches under rocprofv3 --kernel-trace (bench.py --traffic-probe)
+                "profile_avg_launch_us": prof_us, "profile_source": prof_src}
 
     result = {
         "metric": "int8 W-only decode GEMM HBM GB/s (% of peak) + linear-stack us/step, M=1..8",
@@ -550,22 +555,30 @@ def layer_flows(torch, ops, stack, layers, eps=1e-6):
 
 
 def run_traffic_probe(args, torch, ops):
-    """Kernels for a rocprofv3 --pmc pass: a 256 MiB device copy (known bytes, the counters' scale)
-    and the dominant kernel of configs[1] (gate_up over its 28 distinct weights at M = 1, 2, 4, 8),
-    launched eagerly so each dispatch carries its own counters."""
+    """Kernels for a rocprofv3 --pmc pass: a 256 MiB device copy (known bytes, the counters' scale),
+    then the configs[1] stack's kernels, linear by linear (qkv, o, gate_up, down, each over its 28
+    distinct weights at M = 1, 2, 4, 8, automatic kernel choice), launched eagerly so each dispatch
+    carries its own counters."""
     ms = (1, 2, 4, 8)
-    stack = make_stack(torch, ops, [("gate_up", 12288, 2048)], 28, keep_bf16=False)
-    xs = make_inputs(torch, [2048], ms)
+    stack = make_stack(torch, ops, TALKER, 28, keep_bf16=False)
+    ops.reserve_workspace(torch.device("cuda"), max(
+        ops.workspace_bytes(ops.OP_W8A16, m, e["n"], e["k"]) for m in ms for e in stack[:4]))
+    xs = make_inputs(torch, [k for _, _, k in TALKER], ms)
     src = torch.ones(128 << 20, dtype=torch.bfloat16, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
-    for m in ms:
-        for e in stack:
-            ops.w8a16_gemm_strips(xs[(m, 2048)], e["qs"], e["n"], e["s"])
+    launches = {}
+    for name, _, _ in TALKER:
+        for m in ms:
+            for e in stack:
+                if e["name"] == name:
+                    ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"])
+                    launches[name] = launches.get(name, 0) + 1
     torch.cuda.synchronize()
-    return {"probe": "traffic", "copy_bytes_each_way": src.numel() * 2, "gate_up_launches": len(ms) * len(stack),
-            "gate_up_algorithmic_bytes_mean": round(statistics.mean(w8a16_bytes(m, 12288, 2048) for m in ms))}
+    return {"probe": "traffic", "copy_bytes_each_way": src.numel() * 2, "launches": launches,
+            "algorithmic_bytes_mean": {name: round(statistics.mean(w8a16_bytes(m, n, k) for m in ms))
+                                       for name, n, k in TALKER}}
 
 
 def run_calibration(args, torch, ops):
