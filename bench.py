@@ -581,6 +581,30 @@ def run_traffic_probe(args, torch, ops):
                                        for name, n, k in TALKER}}
 
 
+def run_prefill_probe(args, torch, ops):
+    """Kernels for a rocprofv3 --pmc pass over the prefill tile kernel: configs[3]'s gate_up
+    (12288 x 2048) at M = 1024, launched eagerly 8 times each (after 3 warm-up launches) as the automatic tile, as the
+    64 x 256 tile (3 stages, no split), and as F.linear on the bf16 weight (hipBLASLt)."""
+    from qtts_amd import _lib
+    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    n, k, m = 12288, 2048, 1024
+    g = torch.Generator(device="cuda").manual_seed(1)
+    w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    q, s = ops.pack_int8(w, torch.bfloat16)
+    qs = ops.to_strips(q)
+    x = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+    wide = _lib.algo_code(_lib.ALGO_TILE, 1, 3, 2 | (3 << 4))
+    for fn in (lambda: ops.w8a16_gemm_strips(x, qs, n, s), lambda: ops.w8a16_gemm_strips(x, qs, n, s, None, wide),
+               lambda: torch.nn.functional.linear(x, w)):
+        for _ in range(3):  # warm-up: code objects loaded, weights resident
+            fn()
+        torch.cuda.synchronize()
+        for _ in range(8):
+            fn()
+    torch.cuda.synchronize()
+    return {"probe": "prefill", "shape": [m, n, k], "launches_each": 8}
+
+
 def run_calibration(args, torch, ops):
     """The per-bucket calibration of the int8 weight-only method on the 8 talker and code-predictor
     shapes: at every row bucket the callers produce, the fastest quantized route (skinny / tile
@@ -766,7 +790,9 @@ def main() -> int:
     ap.add_argument("--floor", action="store_true",
                     help="time the launch and streaming floor of one kernel per linear next to the configs[1] stack")
     ap.add_argument("--traffic-probe", action="store_true",
-                    help="launch only the kernels a rocprofv3 --pmc pass measures (copy + gate_up)")
+                    help="launch only the kernels a rocprofv3 --pmc pass measures (a copy, then the stack's linears)")
+    ap.add_argument("--prefill-probe", action="store_true",
+                    help="launch only the prefill kernels a rocprofv3 --pmc pass compares (tile kernel, hipBLASLt)")
     args = ap.parse_args()
 
     if args.summarize_rocprof:
@@ -791,6 +817,8 @@ def main() -> int:
     runner = {0: run_single_linear, 1: run_talker_stack, 2: run_predictor, 3: run_prefill, 4: run_fp8}[args.config]
     if args.traffic_probe:
         runner = run_traffic_probe
+    if args.prefill_probe:
+        runner = run_prefill_probe
     if args.floor:
         runner = run_floor
     if args.calibration:

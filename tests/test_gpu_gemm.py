@@ -496,22 +496,25 @@ def test_fp8_strips_tile_vs_oracle(ops, m):
 
 
 def test_w8a16_strips_tile_forced_shapes(ops):
-    """Every tile shape and stage count the tile kernel is built for, against the oracle."""
-    m, n, k = 70, 520, 1024
-    x, w, b = _make(m, n, k, bias=True, seed=4242)
-    q, s = ops.pack_int8(w, torch.bfloat16)
-    qs = ops.to_strips(q)
-    ref = _oracle_w8a16(x, q, s, b)
-    for bmc in (1, 2, 3):
-        for bnc in (1, 2, 3):
-            for stages in (2, 3, 4, 6, 8):
-                algo = ops.algo_code(2, 2, stages, bmc | (bnc << 4))
-                try:
-                    y = ops.w8a16_gemm_strips(x, qs, n, s, b, algo)
-                except ValueError as e:
-                    assert "stages are not built" in str(e), e
-                    continue
-                assert_close(y, ref, f"tile BM={16 << bmc} BN={32 << bnc} P={stages}")
+    """Every tile shape, wave grid and stage count the tile kernel is built for, against the oracle;
+    K ranges longer than the stage ring, as long, and shorter (one and two 64-column stages)."""
+    for m, n, k, splits in ((70, 520, 1024, 2), (40, 200, 128, 1), (40, 200, 128, 2), (33, 72, 256, 1)):
+        x, w, b = _make(m, n, k, bias=True, seed=4242 + k)
+        q, s = ops.pack_int8(w, torch.bfloat16)
+        qs = ops.to_strips(q)
+        ref = _oracle_w8a16(x, q, s, b)
+        for bmc in (1, 2, 3):
+            for bnc in (1, 2, 3):
+                for grid in (0, 4):  # 1 x 4 or 2 x 2 waves over the tile
+                    for stages in (2, 3, 4, 6, 8):
+                        algo = ops.algo_code(2, splits, stages, bmc | grid | (bnc << 4))
+                        what = f"tile m={m} n={n} k={k} S={splits} BM={16 << bmc} BN={32 << bnc} grid={grid} P={stages}"
+                        try:
+                            y = ops.w8a16_gemm_strips(x, qs, n, s, b, algo)
+                        except ValueError as e:
+                            assert "stages are not built" in str(e), (what, e)
+                            continue
+                        assert_close(y, ref, what)
 
 
 def _fused_waves(n: int, k: int) -> int:

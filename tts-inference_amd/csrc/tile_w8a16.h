@@ -81,6 +81,7 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
   static_assert(P >= 2 && P * SB + 64 <= kLdsBytes, "stage ring must fit in LDS");
   static_assert((P - 2) * FPW < 64, "vmcnt is 6 bits");
   __shared__ __align__(1024) uint8_t ring[P * SB];
+  __shared__ uint32_t epi_sc[BN], epi_bi[BN];  // the tile's scale and bias bits, column by column
   __shared__ unsigned flag;
 
   int tile, split;
@@ -97,19 +98,15 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
   const int kc0 = split * cps;
   const int nk = min(cps, nchunks - kc0);
 
-  // Epilogue operands first (raw bits; loads the compiler will not sink): they are
-  // the oldest loads in flight, so the first stage wait covers them.
-  uint32_t scb[NB][4], bib[NB][4];
-  {
-    const XT* bsrc = bias ? bias : y;
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        const int n = min(n0 + (wn * NB + nb) * 16 + 4 * g + t, N - 1);
-        scb[nb][t] = load_scale_bits(scale, sdt, n);
-        bib[nb][t] = __hip_atomic_load((uint16_t*)bsrc + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      }
+  // Epilogue operands: thread t < BN loads column t's scale and bias bits first (the oldest
+  // loads in flight, so waiting for them costs about what waiting for stage 0 does) and
+  // parks them in LDS, where the epilogue reads them; held in registers through the K loop
+  // they would cost 8 NB registers a lane, enough to cut the larger tiles' occupancy.
+  uint32_t my_sc = 0u, my_bi = 0u;
+  if (tid < BN) {
+    const int n = min(n0 + tid, N - 1);
+    my_sc = load_scale_bits(scale, sdt, n);
+    my_bi = __hip_atomic_load((uint16_t*)(bias ? bias : y) + n, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
 
   // This wave's fragments: per-lane source at chunk kc0 and the per-chunk stride.
@@ -130,7 +127,7 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
     }
   }
 
-  auto issue = [&](uint8_t* stage, int i) {
+  auto issue = [&](uint8_t* stage, int i) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < FPW; ++j) load_to_lds16(src[j] + (int64_t)i * stride[j], stage + (wave * FPW + j) * 1024);
   };
@@ -145,7 +142,7 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
   // strip nb, with the dequantization of strip nb+1 issued ahead of them (independent
   // VALU work the wave can issue while the matrix pipe runs), h = 0 before h = 1 so
   // that consecutive MFMAs never share an accumulator.
-  auto compute = [&](const uint8_t* stage) {
+  auto compute = [&](const uint8_t* stage) __attribute__((always_inline)) {
     V xa[MB][2];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
@@ -180,6 +177,14 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
   // consume stage i.
   for (int p = 0; p < P - 1; ++p)
     if (p < nk) issue(ring + p * SB, p);
+  if (tid < BN) {  // visible to the epilogue after the K loop's barriers (every wave's LDS
+    epi_sc[tid] = my_sc;  // reads of a stage, waited for before its MFMAs, come after these
+    epi_bi[tid] = my_bi;  // writes in program order), or the barrier below
+  }
+  if (nk <= 0) {
+    wait_lgkmcnt0();
+    barrier_only();
+  }
   int cur = 0, nxt = P - 1;
   for (int i = 0; i < nk; ++i) {
     wait_stages<FPW, P - 2>(nk - 1 - i);
@@ -217,8 +222,9 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
     float sc[4], bi[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      sc[t] = scale_bits_to_f32(scb[nb][t], sdt);
-      bi[t] = bias ? xbits_to_f32<XT>(bib[nb][t]) : 0.0f;
+      const int col = (wn * NB + nb) * 16 + 4 * g + t;
+      sc[t] = scale_bits_to_f32(epi_sc[col], sdt);
+      bi[t] = bias ? xbits_to_f32<XT>(epi_bi[col]) : 0.0f;
     }
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
@@ -255,8 +261,9 @@ inline bool pipe_p_ok(int bm, int bn, int p) {
 
 // Automatic tile choice, from a sweep of BM x BN x stages x splits over the talker
 // and code-predictor shapes at M = 32..1024 (within 3% of the per-shape best on
-// average): 32 x 64 tiles with 4 stages up to M = 128, 64 x 128 with 3 stages
-// above, 128 x 128 from M = 512 when that still makes 512 tiles; then split K until
+// average): 32 x 64 tiles with 4 stages up to M = 128, and up to M = 256 while that
+// makes at most 512 tiles (at M = 256: qkv 14.8 -> 13.0 us, o_proj 12.4 -> 10.7 against
+// 64 x 128; gate_up's 1536 such tiles were 25.6 -> 35.1), 64 x 128 with 3 stages above, 128 x 128 from M = 512 when that still makes 512 tiles; then split K until
 // there are 256 workgroups, keeping >= 8 chunks a split, and on to 512 workgroups
 // while a split keeps >= 32 chunks (talker down_proj at M = 1024: 47.6 -> 40.0 us).
 // A workspace too small for the splits drops the automatic choice to one split.
@@ -270,7 +277,7 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
     c.bm = 16 << (shape_req & 3);
     c.bn = 32 << ((shape_req >> 4) & 7);
     c.wm = (shape_req >> 2) & 1 ? 2 : 1;
-  } else if (m <= 128) {
+  } else if (m <= 128 || (m <= 256 && ((m + 31) / 32) * ((n + 63) / 64) <= 512)) {
     c.bm = 32;
     c.bn = 64;
   } else if (m >= 512 && ((m + 127) / 128) * ((n + 127) / 128) >= 512) {
