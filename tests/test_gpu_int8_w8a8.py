@@ -202,6 +202,25 @@ def test_int8_gemm_every_config_identical(ops):
         _assert_bits(ops.w8a8_int8_gemm(qx, sx, qw, sw, bias, torch.bfloat16, algo), want, f"rowmajor algo={algo:#x}")
 
 
+def test_int8_gemm_half_strips(ops):
+    """Decode rows on layers with few strips take half strips (two workgroups of 8 weight rows per
+    strip, two chunks per MFMA): exactly the oracle, and exactly the whole-strip kernel, for every
+    M in 1..8, ragged N, bias on and off."""
+    for (n, k) in ((40, 256), (1000, 512), (72, 384), (2048, 6144)):
+        qx8, sx8, qw, sw = _codes(8, n, k, seed=n + k)
+        qs = ops.to_strips(qw)
+        for m in range(1, 9):
+            qx, sx = qx8[:m].contiguous(), sx8[:m].contiguous()
+            bias = (torch.randn(n, device="cuda") * 0.1).to(torch.bfloat16) if m % 2 else None
+            want = _oracle_gemm(qx, sx, qw, sw, bias, torch.bfloat16)
+            what = f"n={n} k={k} m={m}"
+            print(what, flush=True)
+            half = ops.w8a8_int8_gemm_strips(qx, sx, qs, n, sw, bias, torch.bfloat16)
+            _assert_bits(half, want, what + " automatic (half strips)")
+            whole = ops.w8a8_int8_gemm_strips(qx, sx, qs, n, sw, bias, torch.bfloat16, ops.algo_code(1, 0, 16))
+            assert torch.equal(half, whole), what + ": half strips differ from whole strips"
+
+
 @pytest.mark.parametrize("shape", TALKER + PREDICTOR)
 def test_int8_linear_full_shapes(ops, shape):
     """Whole Int8Method.apply at the talker / code predictor shapes, decode and prefill rows,

@@ -12,6 +12,11 @@
 //    issues one MFMA.  Waves split K and meet in LDS; workgroups may split K further
 //    and meet through the workspace (last arrival reduces).  blockIdx.y walks 16-row
 //    blocks, so it serves any M (the decode path for M <= 16, the fallback above).
+//    SUB = 2 (strip weights, M <= 8, no split): half strips, two workgroups of 8 weight
+//    rows per strip, as skinny.h does for W8A16: A rows 0-7 hold chunk 2u and rows 8-15
+//    chunk 2u + 1 of those rows, B columns 0-7 and 8-15 the activation rows for the same
+//    two chunks, and the two diagonal 8 x 8 blocks of D are added at the end (in int32,
+//    exactly: the result is the whole-strip kernel's, bit for bit).
 //  * tile (M > 16, K % 128 == 0): pipe_w8a8.h, in tile_i8.hip / tile_i8_rows.hip.
 //  * generic: any alignment and K; correctness path.
 //
@@ -23,6 +28,7 @@
 
 #include "common.h"
 #include "layout.h"
+#include "skinny.h"
 #include "splitk.h"
 
 namespace qtts {
@@ -32,36 +38,52 @@ template <typename OT> __device__ __forceinline__ float out_bits_f32(uint32_t b)
   else return __uint_as_float(b);
 }
 
-template <typename OT, int WAVES, int U, int LAYOUT>
+template <typename OT, int WAVES, int U, int LAYOUT, int SUB = 1>
 __global__ __launch_bounds__(WAVES * 64) void int8_skinny_kernel(
     const int8_t* __restrict__ qx, const float* sx, int M, int K, int64_t ldqx,
     const int8_t* __restrict__ qw, int N, int64_t ldqw, const float* sw, const OT* bias,
     OT* __restrict__ y, int64_t ldy, int* __restrict__ part, unsigned* __restrict__ counters, int strips, int S,
     int cps) {
+  static_assert(SUB == 1 || (SUB == 2 && LAYOUT == kLayoutStrips), "half strips need strip weights");
+  constexpr int RP = 16 / SUB;  // weight rows per workgroup
   __shared__ i32x4_t red[WAVES > 1 ? WAVES - 1 : 1][64];
   int strip, split;
-  decode_wg(blockIdx.x, S, strip, split);
+  if constexpr (SUB == 1) {
+    decode_wg(blockIdx.x, S, strip, split);
+  } else {  // no split: the host launches half strips with S == 1
+    strip = blockIdx.x / SUB;
+    split = 0;
+  }
+  const int part_row = SUB == 1 ? 0 : (blockIdx.x % SUB) * RP;  // this workgroup's first strip row
   if (strip >= strips) return;
 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int r = lane & 15, g = lane >> 4;
-  const int mrow = (int)blockIdx.y * 16 + r;
+  const int mrow = (int)blockIdx.y * 16 + r;  // the D column lane r holds (half strips: r < 8)
   const int n = strip * 16 + r;
   const bool n_ok = n < N, m_ok = mrow < M;
+  const int xrow = SUB == 1 ? mrow : r % RP;  // the activation row lane r loads (B column r)
+  const bool x_ok = SUB == 1 ? m_ok : xrow < M;
   const int nchunks = (K + 63) >> 6;
-  const int c0 = split * cps, c1 = min(c0 + cps, nchunks);
+  // units of SUB chunks (SUB divides nchunks, checked by the host)
+  const int c0 = split * cps, c1 = min(c0 + cps, SUB == 1 ? nchunks : nchunks / SUB);
   const int cw = (c1 - c0 + WAVES - 1) / WAVES;
   const int wc0 = c0 + wave * cw, wc1 = min(wc0 + cw, c1);
   const int8_t* wp;
   int64_t wstride;
-  if constexpr (LAYOUT == kLayoutStrips) {
+  if constexpr (LAYOUT == kLayoutStrips && SUB > 1) {
+    // lane (r, g): strip row part_row + r % RP of chunk r / RP of each unit, bytes 16 g .. + 15
+    wp = qw + (int64_t)strip * nchunks * 1024 + (r / RP) * 1024 + (part_row + r % RP + 16 * g) * 16;
+    wstride = SUB * 1024;
+  } else if constexpr (LAYOUT == kLayoutStrips) {
     wp = qw + (int64_t)strip * nchunks * 1024 + lane * 16;
     wstride = 1024;
   } else {
     wp = qw + (int64_t)(n_ok ? n : 0) * ldqw + 16 * g;
     wstride = 64;
   }
-  const int8_t* xp = qx + (int64_t)(m_ok ? mrow : 0) * ldqx + 16 * g;
+  const int8_t* xp = qx + (int64_t)(x_ok ? xrow : 0) * ldqx + (SUB == 1 ? 0 : (r / RP) * 64) + 16 * g;
+  const int64_t xstride = SUB * 64;
   const i32x4_t zero = {0, 0, 0, 0};
 
   // A group of U chunks is issued in full before any of it is consumed.
@@ -71,10 +93,10 @@ __global__ __launch_bounds__(WAVES * 64) void int8_skinny_kernel(
     for (int u = 0; u < U; ++u) {
       const int cc = c + u;
       const bool live = cc < wc1;
-      const bool ok = live && cc * 64 + 16 * g < K;
+      const bool ok = live && (SUB > 1 || cc * 64 + 16 * g < K);  // half strips: K % 128 == 0
       const bool wok = LAYOUT == kLayoutStrips ? live : (ok && n_ok);
       wv[u] = wok ? *(const i32x4_t*)(wp + (int64_t)cc * wstride) : zero;
-      xv[u] = (ok && m_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * 64) : zero;
+      xv[u] = (ok && x_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * xstride) : zero;
     }
   };
   i32x4_t acc = zero;
@@ -90,7 +112,7 @@ __global__ __launch_bounds__(WAVES * 64) void int8_skinny_kernel(
     const OT* bsrc = bias ? bias : y;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int nn = min(strip * 16 + 4 * g + i, N - 1);
+      const int nn = min(strip * 16 + part_row + 4 * g + i, N - 1);
       swv[i] = *(const uint32_t*)(sw + nn);
       if constexpr (sizeof(OT) == 2) bi[i] = *(const uint16_t*)(bsrc + nn);
       else bi[i] = *(const uint32_t*)(bsrc + nn);
@@ -121,7 +143,14 @@ __global__ __launch_bounds__(WAVES * 64) void int8_skinny_kernel(
     }
   }
 
-  if (S > 1) {
+  if constexpr (SUB == 2) {
+    // D rows 8 + i, columns 8 + j (the odd chunk of each unit) onto rows i, columns j: lane
+    // (j, g) for g < 2 takes lane (j + 8, g + 2), i.e. lane ^ 40; int32, wrapping like the MFMA
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] = (int)((unsigned)acc[i] + (unsigned)__shfl_xor(acc[i], 40, 64));
+  }
+
+  if (SUB == 1 && S > 1) {
     int a[4] = {acc[0], acc[1], acc[2], acc[3]};
     const int tile = (int)blockIdx.y * strips + strip;
     if (!splitk_meet<4>(a, part + (int64_t)tile * S * 64 * 4, &counters[tile], S, split, lane, 64, nullptr))
@@ -129,11 +158,11 @@ __global__ __launch_bounds__(WAVES * 64) void int8_skinny_kernel(
     acc = i32x4_t{a[0], a[1], a[2], a[3]};
   }
 
-  if (m_ok) {
+  if (m_ok && (SUB == 1 || r < RP)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int nn = strip * 16 + 4 * g + i;
-      if (nn < N) {
+      const int nn = strip * 16 + part_row + 4 * g + i;
+      if ((SUB == 1 || 4 * g < RP) && nn < N) {
         const float v = int8_epilogue(acc[i], __uint_as_float(sxv), __uint_as_float(swv[i]), out_bits_f32<OT>(bi[i]),
                                       bias != nullptr);
         y[(int64_t)mrow * ldy + nn] = from_f32<OT>(v);
@@ -259,6 +288,30 @@ int int8_launch_typed(const int8_t* qx, const float* sx, int64_t m, int64_t k, i
     qtts::launch(&int8_generic_kernel<OT>, grid, dim3(64), 0, st, qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw,
                  bias, y, ldy);
     return qtts_check_launch("w8a8_int8_generic");
+  }
+  // Half strips for decode rows where whole strips leave compute units idle (skinny.h's
+  // rule: the talker's down_proj); automatic choice only.  Bit-identical to whole strips.
+  if ((algo & 0xff) == QTTS_ALGO_AUTO && (algo >> 8) == 0 && layout == kLayoutStrips && m <= 8 &&
+      skinny_auto_sub(m, n, k) == 2) {
+    const int strips = (int)((n + 15) / 16), units = (int)(k / 128);
+    int W = 1;
+    while (W < 16 && ((units + W - 1) / W > kI8CPW || (int64_t)strips * 2 * W < 2048)) W *= 2;
+    const int64_t blocks = ((int64_t)strips * 2 + 7) / 8 * 8;
+    if ((units + W - 1) / W <= kI8CPW && blocks < ((int64_t)1 << 31)) {
+#define QTTS_I8H(WV)                                                                                             \
+  qtts::launch(&int8_skinny_kernel<OT, WV, kI8CPW, kLayoutStrips, 2>, dim3((unsigned)blocks, 1), dim3(WV * 64), 0, \
+               st, qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy, (int*)nullptr,              \
+               (unsigned*)nullptr, strips, 1, units)
+      switch (W) {
+        case 1: QTTS_I8H(1); break;
+        case 2: QTTS_I8H(2); break;
+        case 4: QTTS_I8H(4); break;
+        case 8: QTTS_I8H(8); break;
+        default: QTTS_I8H(16); break;
+      }
+#undef QTTS_I8H
+      return qtts_check_launch("w8a8_int8_skinny_half");
+    }
   }
   // Skinny kernel: the decode path, and the fallback for tile requests the pipeline
   // cannot take (K % 128 != 0); a forced tile request keeps only its split count.
