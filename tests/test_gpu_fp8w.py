@@ -89,6 +89,10 @@ def test_fp8w_prefill_and_ragged(ops, dtype):
             for splits, shape in ((1, 0), (2, 0), (0, 0x21), (0, 0x12), (0, 0x23)):
                 y = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, 0, shape))
                 assert_close(y, ref, f"tile m={m} n={n} k={k} S={splits} shape={shape:#x} {dtype}")
+                if shape:  # 4 stages with and without read-ahead: the same MFMAs, the same bits
+                    y4 = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, 4, shape))
+                    y4ra = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, 4 | ops.TILE_READ_AHEAD, shape))
+                    assert torch.equal(y4, y4ra), f"read-ahead m={m} n={n} k={k} shape={shape:#x} {dtype}"
 
 
 def test_fp8w_graph_replays(ops):

@@ -496,9 +496,11 @@ def test_fp8_strips_tile_vs_oracle(ops, m):
 
 
 def test_w8a16_strips_tile_forced_shapes(ops):
-    """Every tile shape, wave grid and stage count the tile kernel is built for, against the oracle;
-    K ranges longer than the stage ring, as long, and shorter (one and two 64-column stages)."""
-    for m, n, k, splits in ((70, 520, 1024, 2), (40, 200, 128, 1), (40, 200, 128, 2), (33, 72, 256, 1)):
+    """Every tile shape, wave grid and stage count the tile kernel is built for, against the oracle,
+    and each with read-ahead (bit-identical to it); K ranges longer than the stage ring, as long,
+    and shorter (one, two and three 64-column stages)."""
+    for m, n, k, splits in ((70, 520, 1024, 2), (40, 200, 128, 1), (40, 200, 128, 2), (33, 72, 256, 1),
+                            (48, 96, 192, 1)):
         x, w, b = _make(m, n, k, bias=True, seed=4242 + k)
         q, s = ops.pack_int8(w, torch.bfloat16)
         qs = ops.to_strips(q)
@@ -515,6 +517,14 @@ def test_w8a16_strips_tile_forced_shapes(ops):
                             assert "stages are not built" in str(e), (what, e)
                             continue
                         assert_close(y, ref, what)
+                        # read-ahead: the same MFMAs in the same order, so the same bits
+                        ra = ops.algo_code(2, splits, stages | ops.TILE_READ_AHEAD, bmc | grid | (bnc << 4))
+                        if stages < 3:
+                            with pytest.raises(ValueError, match="read-ahead needs 3 stages"):
+                                ops.w8a16_gemm_strips(x, qs, n, s, b, ra)
+                            continue
+                        y_ra = ops.w8a16_gemm_strips(x, qs, n, s, b, ra)
+                        assert torch.equal(y_ra, y), what + " read-ahead"
 
 
 def _fused_waves(n: int, k: int) -> int:

@@ -122,7 +122,8 @@ SkinnyCfg fp8w_skinny_cfg(int64_t m, int64_t n, int64_t k, int algo) {
 int64_t qtts_fp8w_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
   const int family = family_of(m, algo);
   if (family == QTTS_ALGO_SKINNY) return skinny_ws(fp8w_skinny_cfg(std::min<int64_t>(m, 16), n, k, algo));
-  return pipe_ws(pipe_cfg(m, n, k, (algo >> 8) & 0xff, 0, pipe_shape_ok((algo >> 24) & 0xff) ? (algo >> 24) & 0xff : 0));
+  const int stages = pipe_stages_ok((algo >> 16) & 0xff) ? (algo >> 16) & 0xff : 0;
+  return pipe_ws(pipe_cfg(m, n, k, (algo >> 8) & 0xff, stages, pipe_shape_ok((algo >> 24) & 0xff) ? (algo >> 24) & 0xff : 0));
 }
 
 // x [m, k] bf16 / fp16 (16-byte aligned rows), qs e4m3 codes in the 64-column strip

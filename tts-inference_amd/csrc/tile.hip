@@ -5,9 +5,9 @@
 
 using namespace qtts;
 
-int64_t qtts_w8a16_pipe_ws_bytes(int64_t m, int64_t n, int64_t k, int splits, int shape) {
-  if (!pipe_shape_ok(shape)) return 0;
-  return pipe_ws(pipe_cfg(m, n, k, splits, 0, shape));
+int64_t qtts_w8a16_pipe_ws_bytes(int64_t m, int64_t n, int64_t k, int splits, int stages, int shape) {
+  if (!pipe_shape_ok(shape) || !pipe_stages_ok(stages)) return 0;
+  return pipe_ws(pipe_cfg(m, n, k, splits, stages, shape));
 }
 
 // x [m, k] (bf16 or fp16, 16-byte aligned rows), qs strip layout, k % 64 == 0, m > 0.

@@ -8,7 +8,11 @@
 // A workgroup of 4 waves owns a BM x BN output tile and a K range; it walks the K
 // range in 64-column stages through a P-deep LDS ring.  Stage loads are direct
 // global -> LDS transfers (global_load_lds_dwordx4, 16 bytes per lane), so P-1
-// stages are in flight while one is consumed, with no registers held for them.  Every load writes one 1 KiB MFMA fragment in lane order:
+// stages are in flight while one is consumed, with no registers held for them.  With
+// read-ahead (PF, 3 stages or more) a wave reads the next stage's operands from LDS
+// into a second register set while the MFMAs of the current one run, so no LDS
+// latency sits between a stage's barrier and its first MFMA; P-2 stages of global
+// loads are then in flight.  Every load writes one 1 KiB MFMA fragment in lane order:
 //   * activation fragment (m-block mb, half h): lane l carries
 //     x[m0 + 16 mb + l % 16][k + 16 (l / 16) + 8 h .. + 7]  (8 bf16);
 //   * weight fragment (strip sb): the strip layout's 1 KiB block, lane l carries
@@ -60,7 +64,7 @@ __device__ __forceinline__ float scale_bits_to_f32(uint32_t b, int dt) {
 
 template <typename XT> __device__ __forceinline__ float xbits_to_f32(uint32_t b) { return to_f32(XT{(uint16_t)b}); }
 
-template <typename XT, int BM, int BN, int P, int WM, bool F8W>
+template <typename XT, int BM, int BN, int P, int WM, bool F8W, bool PF = false>
 __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ qs, int N,
     const void* __restrict__ scale, int sdt, const XT* __restrict__ bias, XT* __restrict__ y, int64_t ldy,
@@ -138,19 +142,10 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // One stage: every operand read from LDS first, then strip by strip the MFMAs of
-  // strip nb, with the dequantization of strip nb+1 issued ahead of them (independent
-  // VALU work the wave can issue while the matrix pipe runs), h = 0 before h = 1 so
-  // that consecutive MFMAs never share an accumulator.
-  auto compute = [&](const uint8_t* stage) __attribute__((always_inline)) {
-    V xa[MB][2];
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) xa[mb][h] = *(const V*)(stage + (2 * (wm * MB + mb) + h) * 1024 + lane * 16);
-    i32x4_t wq[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) wq[nb] = *(const i32x4_t*)(stage + (XF + wn * NB + nb) * 1024 + lane * 16);
+  // One stage from registers: strip by strip the MFMAs of strip nb, with the conversion
+  // of strip nb+1 issued ahead of them, h = 0 before h = 1 so that consecutive MFMAs
+  // never share an accumulator.
+  auto mma = [&](const V (&xa)[MB][2], const i32x4_t (&wq)[NB]) __attribute__((always_inline)) {
     V cur[2], nxt[2];
     cur[0] = wcvt<F8W, XT>((uint32_t)wq[0][0], (uint32_t)wq[0][1]);
     cur[1] = wcvt<F8W, XT>((uint32_t)wq[0][2], (uint32_t)wq[0][3]);
@@ -170,11 +165,15 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
       }
     }
   };
+  auto read = [&](V (&xa)[MB][2], i32x4_t (&wq)[NB], const uint8_t* stage) __attribute__((always_inline)) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) xa[mb][h] = *(const V*)(stage + (2 * (wm * MB + mb) + h) * 1024 + lane * 16);
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) wq[nb] = *(const i32x4_t*)(stage + (XF + wn * NB + nb) * 1024 + lane * 16);
+  };
 
-  // Stage i: wait for this wave's loads of stage i (up to P-2 later stages may stay
-  // in flight), barrier (every wave's loads of stage i have landed, and every wave
-  // is done with stage i-1, whose buffer the next issue reuses), issue stage i+P-1,
-  // consume stage i.
   for (int p = 0; p < P - 1; ++p)
     if (p < nk) issue(ring + p * SB, p);
   if (tid < BN) {  // visible to the epilogue after the K loop's barriers (every wave's LDS
@@ -185,14 +184,58 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
     wait_lgkmcnt0();
     barrier_only();
   }
-  int cur = 0, nxt = P - 1;
-  for (int i = 0; i < nk; ++i) {
-    wait_stages<FPW, P - 2>(nk - 1 - i);
-    barrier_only();
-    if (i + P - 1 < nk) issue(ring + nxt * SB, i + P - 1);
-    compute(ring + cur * SB);
-    cur = cur + 1 == P ? 0 : cur + 1;
-    nxt = nxt + 1 == P ? 0 : nxt + 1;
+  if constexpr (!PF) {
+    // Stage i: wait for this wave's loads of stage i (up to P-2 later stages may stay
+    // in flight), barrier, issue stage i+P-1, read and consume stage i.
+    int cur = 0, nxt = P - 1;
+    for (int i = 0; i < nk; ++i) {
+      wait_stages<FPW, P - 2>(nk - 1 - i);
+      barrier_only();
+      if (i + P - 1 < nk) issue(ring + nxt * SB, i + P - 1);
+      V xa[MB][2];
+      i32x4_t wq[NB];
+      read(xa, wq, ring + cur * SB);
+      mma(xa, wq);
+      cur = cur + 1 == P ? 0 : cur + 1;
+      nxt = nxt + 1 == P ? 0 : nxt + 1;
+    }
+  } else {
+    // Operands read one stage ahead into a second register set: step i waits for stage
+    // i+1's loads (up to P-3 later stages may stay in flight), barrier (stage i+1 has
+    // landed for every wave, and every wave is done with stage i-1, whose buffer the
+    // issue of stage i+P-1 reuses), issues stage i+P-1, starts the LDS reads of stage
+    // i+1, then runs stage i's MFMAs from the registers read the step before.
+    V xa0[MB][2], xa1[MB][2];
+    i32x4_t wq0[NB], wq1[NB];
+    if (nk > 0) {
+      wait_stages<FPW, P - 2>(nk - 1);
+      barrier_only();
+      read(xa0, wq0, ring);
+    }
+    // Steps i with a next stage: wait for stage i+1, barrier, issue stage i+P-1, read
+    // stage i+1 into the other register set, then stage i's MFMAs.  The loop runs the
+    // steps in pairs with no branch around the MFMAs (a join there makes the register
+    // allocator copy every accumulator); the last one or two stages follow it.
+    auto advance = [&](int i, V (&xn)[MB][2], i32x4_t (&wn_)[NB]) __attribute__((always_inline)) {
+      wait_stages<FPW, (P >= 3 ? P - 3 : 0)>(nk - 2 - i);
+      barrier_only();
+      if (i + P - 1 < nk) issue(ring + ((i + P - 1) % P) * SB, i + P - 1);
+      read(xn, wn_, ring + ((i + 1) % P) * SB);
+    };
+    int i = 0;
+    for (; i + 2 < nk; i += 2) {
+      advance(i, xa1, wq1);
+      mma(xa0, wq0);
+      advance(i + 1, xa0, wq0);
+      mma(xa1, wq1);
+    }
+    if (i + 1 < nk) {
+      advance(i, xa1, wq1);
+      mma(xa0, wq0);
+      mma(xa1, wq1);
+    } else if (i < nk) {
+      mma(xa0, wq0);
+    }
   }
 
   if (S > 1) {
@@ -248,55 +291,72 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
 }
 
 
-struct PipeCfg { int bm, bn, P, wm, S, cps, mtiles, ntiles; };
+struct PipeCfg { int bm, bn, P, wm, S, cps, mtiles, ntiles, pf; };
 
 constexpr int pipe_stage_bytes_c(int bm, int bn) { return (bm / 8 + bn / 16) * 1024; }
 
-// Stage counts built per tile shape; a calibrator may pick one through algo bits 16-23.
+// Stage counts built per tile shape (read-ahead from 3); a calibrator may pick one through
+// algo bits 16-23.
 inline bool pipe_p_ok(int bm, int bn, int p) {
   if (p != 2 && p != 3 && p != 4 && p != 6 && p != 8) return false;
   const int fpw = (bm / 8 + bn / 16) / 4;
   return p * pipe_stage_bytes_c(bm, bn) + 64 <= kLdsBytes && (p - 2) * fpw < 64;
 }
 
-// Automatic tile choice, from a sweep of BM x BN x stages x splits over the talker
-// and code-predictor shapes at M = 32..1024 (within 3% of the per-shape best on
-// average): 32 x 64 tiles with 4 stages up to M = 128, and up to M = 256 while that
-// makes at most 512 tiles (at M = 256: qkv 14.8 -> 13.0 us, o_proj 12.4 -> 10.7 against
-// 64 x 128; gate_up's 1536 such tiles were 25.6 -> 35.1), 64 x 128 with 3 stages above, 128 x 128 from M = 512 when that still makes 512 tiles; then split K until
-// there are 256 workgroups, keeping >= 8 chunks a split, and on to 512 workgroups
-// while a split keeps >= 32 chunks (talker down_proj at M = 1024: 47.6 -> 40.0 us).
+// Automatic choice, from a sweep of tile shapes x stages x read-ahead x splits over the
+// talker shapes at M = 64..2048:
+//   * 32 x 64 tiles up to M = 128, and up to M = 256 while that makes at most 512 tiles
+//     and K is at most 4096 (at M = 256: qkv 13.0, o_proj 9.4 us);
+//   * 64 x 128 tiles otherwise up to M = 256 (gate_up 26.6, down_proj 18.4 us);
+//   * above M = 256, 128 x 128 tiles while they number at least 256 (qkv at M = 1024:
+//     27.9 us), else 64 x 128 (o_proj 16.4, down_proj 40.5 us at M = 1024);
+// all with 4 stages read one stage ahead (PF) -- except where 128 x 128 tiles number
+// 512 or more (gate_up at M >= 1024): there 3 stages without read-ahead, whose 72 KiB
+// leave room for two workgroups a CU (76.6 against 80.1 us).  Then split K until there
+// are 256 workgroups, keeping >= 8 chunks a split; without read-ahead on to 512
+// workgroups while a split keeps >= 32 chunks (the second resident workgroup).
 // A workspace too small for the splits drops the automatic choice to one split.
 // shape_req (algo bits 24-30): bits 0-1 log2(BM / 16) in 1..3, bit 2 a 2 x 2 wave grid
-// (else 1 x 4), bits 4-6 log2(BN / 32) in 1..3; 0 = automatic.
+// (else 1 x 4), bits 4-6 log2(BN / 32) in 1..3; 0 = automatic.  stages_req (algo bits
+// 16-23): bits 0-5 the stage count (0 = automatic), bit 6 read-ahead; 0 = automatic.
 inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int stages_req, int shape_req = 0) {
   PipeCfg c;
   const int nchunks = std::max(1, (int)(k / 64));
+  const int64_t t128 = ((m + 127) / 128) * ((n + 127) / 128);
   c.wm = 1;
+  bool wide = false;  // 128 x 128 tiles enough to fill the GPU twice: 3 stages, no read-ahead
   if (shape_req != 0) {
     c.bm = 16 << (shape_req & 3);
     c.bn = 32 << ((shape_req >> 4) & 7);
     c.wm = (shape_req >> 2) & 1 ? 2 : 1;
-  } else if (m <= 128 || (m <= 256 && ((m + 31) / 32) * ((n + 63) / 64) <= 512)) {
+  } else if (m <= 128 || (m <= 256 && ((m + 31) / 32) * ((n + 63) / 64) <= 512 && nchunks <= 64)) {
     c.bm = 32;
     c.bn = 64;
-  } else if (m >= 512 && ((m + 127) / 128) * ((n + 127) / 128) >= 512) {
-    c.bm = 128;  // enough 128 x 128 tiles to fill the GPU twice: fewer re-reads per MFMA
+  } else if (m > 256 && t128 >= 256) {
+    c.bm = 128;
     c.bn = 128;
+    wide = t128 >= 512;
   } else {
     c.bm = 64;
     c.bn = 128;
   }
   c.mtiles = (int)((m + c.bm - 1) / c.bm);
   c.ntiles = (int)((n + c.bn - 1) / c.bn);
-  c.P = stages_req > 0 ? stages_req : (c.bm * c.bn <= 32 * 64 ? 4 : 3);
+  if (stages_req == 0) {
+    c.P = wide ? 3 : 4;
+    c.pf = wide ? 0 : 1;
+  } else {
+    c.P = (stages_req & 0x3f) > 0 ? (stages_req & 0x3f) : (c.bm * c.bn <= 32 * 64 ? 4 : 3);
+    c.pf = (stages_req >> 6) & 1;
+  }
   const int64_t tiles = (int64_t)c.mtiles * c.ntiles;
   int S = splits_req;
   if (S <= 0) {
     S = 1;
     while (tiles * S < 256 && nchunks / (S * 2) >= 8) S *= 2;
     // long K (>= 32 chunks a split): fill the two resident workgroups a CU holds
-    while (tiles * S < 512 && nchunks / (S * 2) >= 32) S *= 2;
+    if (!c.pf)
+      while (tiles * S < 512 && nchunks / (S * 2) >= 32) S *= 2;
   }
   S = std::max(1, std::min(S, nchunks));
   if (tiles > kMaxSplitTiles) S = 1;
@@ -319,9 +379,14 @@ struct PipeArgs {
 template <bool F8W, typename XT, int BM, int BN, int P, int WM>
 inline void launch_pipe_p(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
   if constexpr (P * pipe_stage_bytes_c(BM, BN) + 64 <= kLdsBytes) {
-    qtts::launch(&w8a16_pipe_kernel<XT, BM, BN, P, WM, F8W>, dim3(blocks), dim3(256), 0, st, (const XT*)a.x, (int)a.m,
-                 (int)a.k, a.ldx, a.qs, (int)a.n, a.scale, a.sdt, (const XT*)a.bias, (XT*)a.y, a.ldy, a.part,
-                 a.counters, c.mtiles, c.ntiles, c.S, c.cps);
+    if (c.pf)
+      qtts::launch(&w8a16_pipe_kernel<XT, BM, BN, P, WM, F8W, true>, dim3(blocks), dim3(256), 0, st, (const XT*)a.x,
+                   (int)a.m, (int)a.k, a.ldx, a.qs, (int)a.n, a.scale, a.sdt, (const XT*)a.bias, (XT*)a.y, a.ldy, a.part,
+                   a.counters, c.mtiles, c.ntiles, c.S, c.cps);
+    else
+      qtts::launch(&w8a16_pipe_kernel<XT, BM, BN, P, WM, F8W>, dim3(blocks), dim3(256), 0, st, (const XT*)a.x, (int)a.m,
+                   (int)a.k, a.ldx, a.qs, (int)a.n, a.scale, a.sdt, (const XT*)a.bias, (XT*)a.y, a.ldy, a.part,
+                   a.counters, c.mtiles, c.ntiles, c.S, c.cps);
   }
 }
 
@@ -356,6 +421,9 @@ inline void launch_pipe_bm(const PipeCfg& c, const PipeArgs& a, unsigned blocks,
   else launch_pipe_bn<F8W, XT, 128>(c, a, blocks, st);
 }
 
+// stages_req: bits 0-5 the count, bit 6 read-ahead, nothing above.
+inline bool pipe_stages_ok(int stages) { return stages >= 0 && (stages >> 7) == 0; }
+
 inline bool pipe_shape_ok(int shape) {
   if (shape == 0) return true;
   const int b = shape & 3, c = (shape >> 4) & 7;
@@ -370,7 +438,11 @@ inline int w8a16_pipe_launch(const char* what, const void* x, int x_dtype, int64
                               hipStream_t st) {
   if (!pipe_shape_ok(shape))
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: bad tile shape code %d", what, shape);
+  if (!pipe_stages_ok(stages))
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: bad stages code %d", what, stages);
   PipeCfg c = pipe_cfg(m, n, k, splits, stages, shape);
+  if (c.pf && c.P < 3)
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: read-ahead needs 3 stages", what);
   if (!pipe_p_ok(c.bm, c.bn, c.P))
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: %d stages are not built for a %dx%d tile", what, c.P,
                           c.bm, c.bn);

@@ -259,7 +259,7 @@ bool grid_ok(int64_t blocks) { return blocks > 0 && blocks < (int64_t)1 << 31; }
 
 }  // namespace
 
-int64_t qtts_w8a16_pipe_ws_bytes(int64_t m, int64_t n, int64_t k, int splits, int shape);
+int64_t qtts_w8a16_pipe_ws_bytes(int64_t m, int64_t n, int64_t k, int splits, int stages, int shape);
 int qtts_launch_w8a16_skinny_xrows(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
                                    int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
                                    int waves, int cpw, float* part, unsigned* counters, int strips, int S, int cps,
@@ -282,7 +282,7 @@ int64_t qtts_w8a16_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
     ws = std::max(ws, skinny_ws(skinny_cfg(std::min<int64_t>(m, kSkinnyMaxM), n, k, splits, waves, cpw)));
   if (family == QTTS_ALGO_TILE || (family == QTTS_ALGO_AUTO && m > 16)) {
     ws = std::max(ws, tile_ws(tile_cfg(m, n, k, splits)));
-    if (k % 64 == 0) ws = std::max(ws, qtts_w8a16_pipe_ws_bytes(m, n, k, splits, (algo >> 24) & 0xff));
+    if (k % 64 == 0) ws = std::max(ws, qtts_w8a16_pipe_ws_bytes(m, n, k, splits, waves, (algo >> 24) & 0xff));
   }
   return ws;
 }

@@ -34,7 +34,10 @@ F32, BF16, F16 = 0, 1, 2
 # qtts_div_mode
 DIV_DEVICE, DIV_IEEE = 0, 1
 # qtts_algo (bits 0-7); bits 8-15 split count, bits 16-23 waves per workgroup,
-# bits 24-31 chunks per wave of the skinny kernels (0 = automatic)
+# bits 24-31 chunks per wave of the skinny kernels (0 = automatic); for the tile
+# kernels bits 16-21 the stage count, bit 22 read-ahead, bits 24-30 the tile shape
+#: read-ahead flag of a tile kernel's stage field (the `waves` argument of algo_code)
+TILE_READ_AHEAD = 64
 ALGO_AUTO, ALGO_SKINNY, ALGO_TILE = 0, 1, 2
 #: the skinny kernel over row-split strips: 2 (HALF) or 4 (QUARTER) workgroups per 16-row strip
 ALGO_SKINNY_HALF, ALGO_SKINNY_QUARTER = 3, 4

@@ -75,6 +75,8 @@ def _candidates(rows: int) -> dict[str, int]:
             for bn in (1, 2):
                 for p in (3, 4):
                     c[f"tile_bm{16 << bm}_bn{32 << bn}_p{p}"] = _lib.algo_code(_lib.ALGO_TILE, 0, p, bm | (bn << 4))
+                c[f"tile_bm{16 << bm}_bn{32 << bn}_p4ra"] = _lib.algo_code(_lib.ALGO_TILE, 0, 4 | _lib.TILE_READ_AHEAD,
+                                                                        bm | (bn << 4))
     return c
 
 
