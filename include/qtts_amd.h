@@ -103,10 +103,9 @@ int qtts_device_supported(int device);
  * stage their activation rows through
  * LDS; bit 30 makes them load the MFMA operands straight from memory instead (same
  * bits out, for timing both).  For the tile kernels, bits
- * 16-21 are the LDS pipeline stages (2, 3, 4, 6, 8; the int8 W8A8 tile builds 2-4);
- * for the W8A16 and fp8 weight-only tiles bit 22 reads each stage's operands from LDS
- * one stage ahead (3 stages or more), and bits 16-23 all zero pick stages and
- * read-ahead automatically.  Bits 24-30 are a tile shape code c: bits 28-30 (c >> 4) log2(BN / 32) in 1..3;
+ * 16-21 are the LDS pipeline stages (2, 3, 4, 6, 8; the int8 W8A8 tile builds 2-4),
+ * bit 22 reads each stage's operands from LDS one stage ahead (3 stages or more), and
+ * bits 16-23 all zero pick stages and read-ahead automatically.  Bits 24-30 are a tile shape code c: bits 28-30 (c >> 4) log2(BN / 32) in 1..3;
  * for W8A16 bits 24-25 (c & 3) log2(BM / 16) in 1..3 and bit 26 (c & 4) a 2 x 2
  * wave grid in place of 1 x 4; for W8A8 (fp8, int8) bits 24-27 (c & 15)
  * log2(BM / 16) in 1..3.  0 = automatic everywhere.  The calibrator uses these to

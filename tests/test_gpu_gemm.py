@@ -474,7 +474,7 @@ def test_w8a16_strips_tile_graph_replays_split(ops):
 @pytest.mark.parametrize("m", [17, 40, 128, 200])
 def test_fp8_strips_tile_vs_oracle(ops, m):
     """The pipelined fp8 tile kernel (M > 16, K % 128 == 0): ragged M and N, bias, every output dtype,
-    forced tile shapes and split counts."""
+    forced tile shapes and split counts, with and without read-ahead."""
     for n, k, odt in ((2048, 2048, torch.bfloat16), (1000, 1024, torch.float16), (24, 256, torch.float32),
                       (2080, 3072, torch.bfloat16)):
         print(f"fp8 strips tile m={m} n={n} k={k} out={odt}", flush=True)
@@ -493,6 +493,10 @@ def test_fp8_strips_tile_vs_oracle(ops, m):
             if splits > 1:
                 assert torch.equal(y2, ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, odt, algo)), \
                     f"fp8 split-K not deterministic m={m} n={n} k={k} S={splits}"
+            if stages >= 3:  # read-ahead: the same MFMAs in the same order, so the same bits
+                ra = ops.algo_code(2, splits, stages | ops.TILE_READ_AHEAD, shape)
+                assert torch.equal(y2, ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, odt, ra)), \
+                    f"fp8 read-ahead m={m} n={n} k={k} S={splits} P={stages} shape={shape:#x}"
 
 
 def test_w8a16_strips_tile_forced_shapes(ops):

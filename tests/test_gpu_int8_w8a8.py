@@ -192,9 +192,12 @@ def test_int8_gemm_every_config_identical(ops):
     algos = [ops.algo_code(1, s, w) for s in (0, 1, 2, 4, 8) for w in (0, 1, 4, 16)]
     def fits(p, shape):  # the stage ring must fit the 160 KiB of LDS
         bm, bn = (32, 64) if shape == 0 else (16 << (shape & 15), 32 << (shape >> 4))
-        return p * (bm // 8 + bn // 8) * 1024 + 64 <= 160 * 1024
-    algos += [ops.algo_code(2, s, p, shape) for s in (0, 1, 2, 4) for p in (2, 3, 4)
+        return (p & 0x3f) * (bm // 8 + bn // 8) * 1024 + 64 <= 160 * 1024
+    ra = ops.TILE_READ_AHEAD  # operands read one stage ahead
+    algos += [ops.algo_code(2, s, p, shape) for s in (0, 1, 2, 4) for p in (2, 3, 4, 3 | ra, 4 | ra)
               for shape in (0, 0x11, 0x21, 0x12, 0x22, 0x32, 0x13, 0x23) if fits(p, shape)]
+    with pytest.raises(ValueError, match="read-ahead needs 3 stages"):
+        ops.w8a8_int8_gemm_strips(qx, sx, qs, n, sw, bias, torch.bfloat16, ops.algo_code(2, 0, 2 | ra, 0x11))
     for algo in algos:
         _assert_bits(ops.w8a8_int8_gemm_strips(qx, sx, qs, n, sw, bias, torch.bfloat16, algo), want,
                      f"strips algo={algo:#x}")

@@ -77,7 +77,7 @@ struct PipeI8 {
   }
 };
 
-template <typename Kind, typename OT, int BM, int BN, int P, int LAYOUT>
+template <typename Kind, typename OT, int BM, int BN, int P, int LAYOUT, bool PF = false>
 __global__ __launch_bounds__(256) void w8a8_pipe_kernel(
     const typename Kind::code_t* __restrict__ qx_, const float* __restrict__ sx, int M, int K, int64_t ldqx,
     const typename Kind::code_t* __restrict__ qw_, int N, int64_t ldqw, const float* __restrict__ sw,
@@ -166,32 +166,76 @@ __global__ __launch_bounds__(256) void w8a8_pipe_kernel(
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = acc_t{0, 0, 0, 0};
 
-  auto compute = [&](const uint8_t* stage) {
-    i32x4_t x0[MB], x1[MB];
+  // A stage's operands: every activation half of the tile, and this wave's weight halves.
+  struct Ops { i32x4_t x0[MB], x1[MB], w0[NB], w1[NB]; };
+  auto read = [&](Ops& o, const uint8_t* stage) __attribute__((always_inline)) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb) {
-      x0[mb] = *(const i32x4_t*)(stage + (2 * mb) * 1024 + lane * 16);
-      x1[mb] = *(const i32x4_t*)(stage + (2 * mb + 1) * 1024 + lane * 16);
+      o.x0[mb] = *(const i32x4_t*)(stage + (2 * mb) * 1024 + lane * 16);
+      o.x1[mb] = *(const i32x4_t*)(stage + (2 * mb + 1) * 1024 + lane * 16);
     }
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) {
       const uint8_t* wsrc = stage + (XF + 2 * (wave * NB + nb)) * 1024 + lane * 16;
-      const i32x4_t w0 = *(const i32x4_t*)wsrc, w1 = *(const i32x4_t*)(wsrc + 1024);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = Kind::mma(w0, w1, x0[mb], x1[mb], acc[nb][mb]);
+      o.w0[nb] = *(const i32x4_t*)wsrc;
+      o.w1[nb] = *(const i32x4_t*)(wsrc + 1024);
     }
+  };
+  auto mma = [&](const Ops& o) __attribute__((always_inline)) {
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) acc[nb][mb] = Kind::mma(o.w0[nb], o.w1[nb], o.x0[mb], o.x1[mb], acc[nb][mb]);
   };
 
   for (int p = 0; p < P - 1; ++p)
     if (p < nk) issue(ring + p * SB, p);
-  int cur = 0, nxt = P - 1;
-  for (int i = 0; i < nk; ++i) {
-    wait_stages<FPW, P - 2>(nk - 1 - i);
-    barrier_only();
-    if (i + P - 1 < nk) issue(ring + nxt * SB, i + P - 1);
-    compute(ring + cur * SB);
-    cur = cur + 1 == P ? 0 : cur + 1;
-    nxt = nxt + 1 == P ? 0 : nxt + 1;
+  if constexpr (!PF) {
+    // Stage i: wait for this wave's loads of stage i (up to P-2 later stages may stay in
+    // flight), barrier, issue stage i+P-1, read and consume stage i.
+    int cur = 0, nxt = P - 1;
+    for (int i = 0; i < nk; ++i) {
+      wait_stages<FPW, P - 2>(nk - 1 - i);
+      barrier_only();
+      if (i + P - 1 < nk) issue(ring + nxt * SB, i + P - 1);
+      Ops o;
+      read(o, ring + cur * SB);
+      mma(o);
+      cur = cur + 1 == P ? 0 : cur + 1;
+      nxt = nxt + 1 == P ? 0 : nxt + 1;
+    }
+  } else {
+    // Read-ahead, as in the W8A16 tile kernel: step i waits for stage i+1 (up to P-3
+    // later stages in flight), barrier (stage i+1 landed for every wave; every wave is
+    // done with stage i-1, whose buffer the issue of stage i+P-1 reuses), issues stage
+    // i+P-1, reads stage i+1 into the other register set, then runs stage i's MFMAs.
+    // Steps go in pairs with no branch around the MFMAs.
+    Ops o0, o1;
+    if (nk > 0) {
+      wait_stages<FPW, P - 2>(nk - 1);
+      barrier_only();
+      read(o0, ring);
+    }
+    auto advance = [&](int i, Ops& on) __attribute__((always_inline)) {
+      wait_stages<FPW, (P >= 3 ? P - 3 : 0)>(nk - 2 - i);
+      barrier_only();
+      if (i + P - 1 < nk) issue(ring + ((i + P - 1) % P) * SB, i + P - 1);
+      read(on, ring + ((i + 1) % P) * SB);
+    };
+    int i = 0;
+    for (; i + 2 < nk; i += 2) {
+      advance(i, o1);
+      mma(o0);
+      advance(i + 1, o0);
+      mma(o1);
+    }
+    if (i + 1 < nk) {
+      advance(i, o1);
+      mma(o0);
+      mma(o1);
+    } else if (i < nk) {
+      mma(o0);
+    }
   }
 
   if (S > 1) {
@@ -258,7 +302,7 @@ __global__ __launch_bounds__(256) void w8a8_pipe_kernel(
 
 // ---- host side: configuration and launch --------------------------------------------
 
-struct W8A8PipeCfg { int bm, bn, P, S, cps, mtiles, ntiles; };
+struct W8A8PipeCfg { int bm, bn, P, S, cps, mtiles, ntiles, pf; };
 
 constexpr int w8a8_stage_bytes(int bm, int bn) { return (bm / 8 + bn / 8) * 1024; }
 
@@ -268,17 +312,24 @@ inline bool w8a8_p_ok(int bm, int bn, int p) {
   return p * w8a8_stage_bytes(bm, bn) + 64 <= kLdsBytes && (p - 2) * fpw < 64;
 }
 
-// The W8A16 tile kernel's measured choice (tile.hip), with 128-column stages: 32 x 64
-// tiles and 4 stages up to M = 128, 64 x 128 and 3 stages above; split K until there
-// are 256 workgroups, keeping >= 4 stages a split.  shape_req: bits 0-3 log2(BM / 16)
-// in 1..3, bits 4-6 log2(BN / 32) in 1..3, 0 = automatic.
+// Automatic choice, from a sweep of tile shapes x stages x read-ahead over the talker
+// shapes at M = 64, 256 and 1024 (int8 and fp8 alike; 128-column stages):
+//   * 32 x 64 tiles with 4 stages up to M = 128, and up to M = 256 while that makes at
+//     most 512 tiles (at M = 256: o_proj 13.8 -> 9.5 us, down_proj 19.3 -> 17.8 us,
+//     qkv 14.6 -> 12.4 us against 64 x 128);
+//   * 64 x 128 tiles above: 4 stages read one stage ahead while they number at most 256
+//     (o_proj at M = 1024: 17.5 -> 16.0 us, down_proj 37.1 -> 31.9 us), else 3 stages
+//     without read-ahead (qkv, gate_up: 2 workgroups a CU);
+// then split K until there are 256 workgroups, keeping >= 4 stages a split.  shape_req:
+// bits 0-3 log2(BM / 16) in 1..3, bits 4-6 log2(BN / 32) in 1..3, 0 = automatic;
+// stages_req: bits 0-5 the stage count, bit 6 read-ahead, 0 = automatic.
 inline W8A8PipeCfg w8a8_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int stages_req, int shape_req) {
   W8A8PipeCfg c;
   const int nchunks = std::max(1, (int)(k / 128));
   if (shape_req != 0) {
     c.bm = 16 << (shape_req & 15);
     c.bn = 32 << ((shape_req >> 4) & 7);
-  } else if (m <= 128) {
+  } else if (m <= 128 || (m <= 256 && ((m + 31) / 32) * ((n + 63) / 64) <= 512)) {
     c.bm = 32;
     c.bn = 64;
   } else {
@@ -287,8 +338,15 @@ inline W8A8PipeCfg w8a8_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int
   }
   c.mtiles = (int)((m + c.bm - 1) / c.bm);
   c.ntiles = (int)((n + c.bn - 1) / c.bn);
-  c.P = stages_req > 0 ? stages_req : (c.bm * c.bn <= 32 * 64 ? 4 : 3);
   const int64_t tiles = (int64_t)c.mtiles * c.ntiles;
+  if (stages_req == 0) {
+    const bool ra = c.bm == 64 && c.bn == 128 && tiles <= 256;
+    c.P = c.bm * c.bn <= 32 * 64 || ra ? 4 : 3;
+    c.pf = ra ? 1 : 0;
+  } else {
+    c.pf = (stages_req >> 6) & 1;
+    c.P = (stages_req & 0x3f) > 0 ? (stages_req & 0x3f) : (c.bm * c.bn <= 32 * 64 ? 4 : 3);
+  }
   int S = splits_req;
   if (S <= 0) {
     S = 1;
@@ -323,9 +381,14 @@ template <typename Kind> struct W8A8Args {
 template <typename Kind, typename OT, int LAYOUT, int BM, int BN, int P>
 void w8a8_launch_p(const W8A8PipeCfg& c, const W8A8Args<Kind>& a, unsigned blocks, hipStream_t st) {
   if constexpr (P * w8a8_stage_bytes(BM, BN) + 64 <= kLdsBytes) {
-    qtts::launch(&w8a8_pipe_kernel<Kind, OT, BM, BN, P, LAYOUT>, dim3(blocks), dim3(256), 0, st, a.qx, a.sx, (int)a.m,
-                 (int)a.k, a.ldqx, a.qw, (int)a.n, a.ldqw, a.sw, (const OT*)a.bias, (OT*)a.y, a.ldy, a.part,
-                 a.counters, c.mtiles, c.ntiles, c.S, c.cps);
+    if (c.pf)
+      qtts::launch(&w8a8_pipe_kernel<Kind, OT, BM, BN, P, LAYOUT, true>, dim3(blocks), dim3(256), 0, st, a.qx, a.sx,
+                   (int)a.m, (int)a.k, a.ldqx, a.qw, (int)a.n, a.ldqw, a.sw, (const OT*)a.bias, (OT*)a.y, a.ldy,
+                   a.part, a.counters, c.mtiles, c.ntiles, c.S, c.cps);
+    else
+      qtts::launch(&w8a8_pipe_kernel<Kind, OT, BM, BN, P, LAYOUT>, dim3(blocks), dim3(256), 0, st, a.qx, a.sx,
+                   (int)a.m, (int)a.k, a.ldqx, a.qw, (int)a.n, a.ldqw, a.sw, (const OT*)a.bias, (OT*)a.y, a.ldy,
+                   a.part, a.counters, c.mtiles, c.ntiles, c.S, c.cps);
   }
 }
 
@@ -362,7 +425,10 @@ template <typename Kind, int LAYOUT, int kMaxP>
 int w8a8_pipe_launch(const char* what, W8A8Args<Kind> a, int out_dtype, int splits, int stages, int shape, void* ws,
                      int64_t ws_bytes, hipStream_t st) {
   if (!w8a8_shape_ok(shape)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: bad tile shape code %d", what, shape);
+  if (stages < 0 || (stages >> 7) != 0)
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: bad stages code %d", what, stages);
   W8A8PipeCfg c = w8a8_cfg(a.m, a.n, a.k, splits, stages, shape);
+  if (c.pf && c.P < 3) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: read-ahead needs 3 stages", what);
   if (!w8a8_p_ok(c.bm, c.bn, c.P) || c.P > kMaxP)
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: %d stages are not built for a %dx%d tile", what, c.P, c.bm,
                           c.bn);
