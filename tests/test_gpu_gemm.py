@@ -379,6 +379,27 @@ def test_fp8_strips_vs_oracle(ops, n, k):
         assert_close(y3, ref, f"fp8 linear strips m={m} n={n} k={k}")
 
 
+def test_fp8_strips_half_strips(ops):
+    """Decode rows on layers with few strips (at most 64, or 128 with K >= 4096) take half strips in
+    the fp8 GEMM: two workgroups of 8 weight rows per strip, two 128-column chunks per MFMA on its
+    diagonal blocks.  Every M in 1..8, ragged N, bias on and off, and every output dtype, against
+    the oracle and the whole-strip kernel (forced), which sums the chunks in another order."""
+    for n, k in ((2048, 6144), (1000, 512), (40, 256), (72, 768)):
+        print(f"fp8 half strips n={n} k={k}", flush=True)
+        x8, w = _fp8_inputs(8, n, k, seed=n + k + 5)
+        qw, sw = ops.pack_fp8(w)
+        qws = ops.to_strips(qw)
+        for m in range(1, 9):
+            qx, sx = ops.quant_act_fp8(x8[:m].contiguous())
+            odt = (torch.bfloat16, torch.float16, torch.float32)[m % 3]
+            b = (torch.randn(n, device="cuda") * 0.1).to(odt) if m % 2 else None
+            ref, inter = _oracle_w8a8(qx, sx, qw, sw, b)
+            y = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, odt)
+            assert_close(y, ref, f"fp8 half strips m={m} n={n} k={k} {odt}", inter)
+            whole = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, odt, ops.algo_code(1))
+            assert_close(whole, ref, f"fp8 whole strips m={m} n={n} k={k} {odt}", inter)
+
+
 def test_kernel_timer_times_eager_launches_only(ops):
     """The bench's kernel timer: one event pair per eager launch, none for captured launches,
     and the timed launches still compute the same result."""

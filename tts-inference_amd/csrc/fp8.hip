@@ -23,6 +23,7 @@
 
 #include "common.h"
 #include "layout.h"
+#include "skinny.h"
 #include "splitk.h"
 
 namespace qtts {
@@ -48,15 +49,28 @@ __device__ __forceinline__ float e4m3_decode(uint32_t c) {
 
 // ------------------------------------------------------------------------------------
 
-template <typename OT, int WAVES, int U, int LAYOUT>
+// SUB = 2 (half strips, strip weights, M <= 8, K % 256 == 0, no split): two workgroups
+// share each 16-row strip, 8 weight rows each.  One MFMA covers a unit of two chunks:
+// A rows 0-7 hold chunk 2u and rows 8-15 chunk 2u + 1 of the workgroup's 8 rows, B
+// columns 0-7 the activation rows for chunk 2u and 8-15 the same rows for chunk 2u + 1,
+// so D's diagonal 8 x 8 blocks are the two chunks' contributions, added at the end.
+template <typename OT, int WAVES, int U, int LAYOUT, int SUB = 1>
 __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
     const uint8_t* __restrict__ qx, const float* sx, int M, int K, int64_t ldqx,
     const uint8_t* __restrict__ qw, int N, int64_t ldqw, const float* sw, const OT* bias,
     OT* __restrict__ y, int64_t ldy, float* __restrict__ part, unsigned* __restrict__ counters, int strips, int S,
     int cps) {
+  static_assert(SUB == 1 || (SUB == 2 && LAYOUT == kLayoutStrips), "half strips need strip weights");
+  constexpr int RP = 16 / SUB;  // weight rows per workgroup
   __shared__ f32x4_t red[WAVES > 1 ? WAVES - 1 : 1][64];
   int strip, split;
-  decode_wg(blockIdx.x, S, strip, split);
+  if constexpr (SUB == 1) {
+    decode_wg(blockIdx.x, S, strip, split);
+  } else {  // no split: the host launches half strips with S == 1
+    strip = blockIdx.x / SUB;
+    split = 0;
+  }
+  const int part_row = SUB == 1 ? 0 : (blockIdx.x % SUB) * RP;  // this workgroup's first strip row
   if (strip >= strips) return;
 
   // wave index through readfirstlane: provably uniform, so per-wave bounds stay scalar
@@ -64,13 +78,21 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
   const int r = lane & 15, g = lane >> 4;
   const int n = strip * 16 + r;
   const bool n_ok = n < N, m_ok = r < M;
+  const int xrow = SUB == 1 ? r : r % RP;  // the activation row lane r loads (B column r)
+  const bool x_ok = xrow < M;
   const int nchunks = (K + 127) >> 7;
-  const int c0 = split * cps, c1 = min(c0 + cps, nchunks);
+  // units of SUB chunks (SUB divides nchunks, checked by the host)
+  const int c0 = split * cps, c1 = min(c0 + cps, SUB == 1 ? nchunks : nchunks / SUB);
   const int cw = (c1 - c0 + WAVES - 1) / WAVES;
   const int wc0 = c0 + wave * cw, wc1 = min(wc0 + cw, c1);
   const uint8_t* wp;
   int64_t wstride, whalf;
-  if constexpr (LAYOUT == kLayoutStrips) {
+  if constexpr (LAYOUT == kLayoutStrips && SUB > 1) {
+    // lane (r, g): strip row part_row + r % RP of chunk r / RP of each unit
+    wp = qw + (int64_t)strip * nchunks * 2048 + (r / RP) * 2048 + (part_row + r % RP + 16 * g) * 16;
+    wstride = SUB * 2048;
+    whalf = 1024;
+  } else if constexpr (LAYOUT == kLayoutStrips) {
     wp = qw + (int64_t)strip * nchunks * 2048 + lane * 16;
     wstride = 2048;
     whalf = 1024;
@@ -79,7 +101,8 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
     wstride = 128;
     whalf = 16;
   }
-  const uint8_t* xp = qx + (int64_t)(m_ok ? r : 0) * ldqx + 32 * g;
+  const uint8_t* xp = qx + (int64_t)(x_ok ? xrow : 0) * ldqx + (SUB == 1 ? 0 : (r / RP) * 128) + 32 * g;
+  const int64_t xstride = SUB * 128;
   const i32x4_t zero = {0, 0, 0, 0};
 
   // A group of U chunks is issued in full before any of it is consumed.
@@ -89,12 +112,12 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
     for (int u = 0; u < U; ++u) {
       const int cc = c + u;
       const bool live = cc < wc1;
-      const bool ok = live && cc * 128 + 32 * g < K;
+      const bool ok = live && (SUB > 1 || cc * 128 + 32 * g < K);  // half strips: K % 256 == 0
       const bool wok = LAYOUT == kLayoutStrips ? live : (ok && n_ok);
       w0[u] = wok ? *(const i32x4_t*)(wp + (int64_t)cc * wstride) : zero;
       w1[u] = wok ? *(const i32x4_t*)(wp + (int64_t)cc * wstride + whalf) : zero;
-      x0[u] = (ok && m_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * 128) : zero;
-      x1[u] = (ok && m_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * 128 + 16) : zero;
+      x0[u] = (ok && x_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * xstride) : zero;
+      x1[u] = (ok && x_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * xstride + 16) : zero;
     }
   };
   f32x4_t acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -115,7 +138,7 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
     const OT* bsrc = bias ? bias : y;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int nn = min(strip * 16 + 4 * g + i, N - 1);
+      const int nn = min(strip * 16 + part_row + 4 * g + i, N - 1);
       swv[i] = *(const uint32_t*)(sw + nn);
       if constexpr (sizeof(OT) == 2) bi[i] = *(const uint16_t*)(bsrc + nn);
       else bi[i] = *(const uint32_t*)(bsrc + nn);
@@ -142,18 +165,25 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
     for (int w = 0; w < WAVES - 1; ++w) acc += red[w][lane];
   }
 
-  if (S > 1) {
+  if constexpr (SUB == 2) {
+    // D rows 8 + i, columns 8 + j (the odd chunk of each unit) onto rows i, columns j: lane
+    // (j, g) for g < 2 takes lane (j + 8, g + 2), i.e. lane ^ 40
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[i] += __shfl_xor(acc[i], 40, 64);
+  }
+
+  if (SUB == 1 && S > 1) {
     float a[4] = {acc[0], acc[1], acc[2], acc[3]};
     if (!splitk_meet<4>(a, part + (int64_t)strip * S * 64 * 4, &counters[strip], S, split, lane, 64, nullptr))
       return;
     acc = f32x4_t{a[0], a[1], a[2], a[3]};
   }
 
-  if (m_ok) {
+  if (m_ok && (SUB == 1 || r < RP)) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int nn = strip * 16 + 4 * g + i;
-      if (nn < N) {
+      const int nn = strip * 16 + part_row + 4 * g + i;
+      if ((SUB == 1 || 4 * g < RP) && nn < N) {
         float v = round_through<OT>(acc[i] * __uint_as_float(sxv) * __uint_as_float(swv[i]));
         if (bias) {
           if constexpr (sizeof(OT) == 2) v += to_f32(OT{(uint16_t)bi[i]});
@@ -426,6 +456,31 @@ static int fp8_launch_fast(const uint8_t* qx, const float* sx, int64_t m, int64_
   }
   unsigned* counters = (unsigned*)ws;
   float* part = ws ? (float*)((char*)ws + kCounterBytes) : nullptr;
+  // Half strips for decode rows where whole strips leave compute units idle (skinny.h's
+  // rule: the talker's down_proj from M = 4, below which the fused linear runs);
+  // automatic choice only.  Units of two 128-column chunks, so K % 256 == 0.
+  if (LAYOUT == kLayoutStrips && c.family == QTTS_ALGO_SKINNY && algo == QTTS_ALGO_AUTO && m <= 8 &&
+      k % 256 == 0 && skinny_auto_sub(m, n, k) == 2) {
+    const int strips = (int)((n + 15) / 16), units = (int)(k / 256);
+    int W = 1;
+    while (W < 16 && ((units + W - 1) / W > kF8CPW || (int64_t)strips * 2 * W < 2048)) W *= 2;
+    const int64_t blocks = ((int64_t)strips * 2 + 7) / 8 * 8;
+    if ((units + W - 1) / W <= kF8CPW && blocks < ((int64_t)1 << 31)) {
+#define QTTS_F8H(WV)                                                                                             \
+  qtts::launch(&fp8_skinny_kernel<OT, WV, kF8CPW, kLayoutStrips, 2>, dim3((unsigned)blocks), dim3(WV * 64), 0, st, \
+               qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy, (float*)nullptr, (unsigned*)nullptr, \
+               strips, 1, units)
+      switch (W) {
+        case 1: QTTS_F8H(1); break;
+        case 2: QTTS_F8H(2); break;
+        case 4: QTTS_F8H(4); break;
+        case 8: QTTS_F8H(8); break;
+        default: QTTS_F8H(16); break;
+      }
+#undef QTTS_F8H
+      return qtts_check_launch("w8a8_fp8_skinny_half");
+    }
+  }
   if (c.family == QTTS_ALGO_SKINNY) {
     const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8 * c.S;
 #define QTTS_F8S(W, U)                                                                                             \
