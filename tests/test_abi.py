@@ -156,3 +156,17 @@ def test_probe_argument_checks():
     assert L.qtts_probe_stream(src, 0, 4, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
     assert L.qtts_probe_empty(0, 4, None) == _lib.ERR_INVALID_ARGUMENT
     assert L.qtts_probe_empty(1, 17, None) == _lib.ERR_INVALID_ARGUMENT
+
+
+def test_size_queries_reject_sizes_past_2_31():
+    """The workspace query and the strip sizes reject sizes past 2^31, as the GEMM entry points
+    do (m * k and the padded strip bytes would overflow 64 bits for the largest)."""
+    L = _lib.load()
+    for big in (1 << 31, 1 << 40, 1 << 62):
+        assert L.qtts_workspace_bytes(_lib.OP_FP8_LINEAR, big, 4096, 2048, 0) == -1
+        assert L.qtts_workspace_bytes(_lib.OP_W8A16, 8, big, 2048, 0) == -1
+        assert L.qtts_workspace_bytes(_lib.OP_INT8_LINEAR, 8, 4096, big, 0) == -1
+        assert L.qtts_strip_bytes(big, 4096, _lib.STRIP_INT8) == -1
+        assert L.qtts_strip_bytes(4096, big, _lib.STRIP_FP8) == -1
+    assert L.qtts_workspace_bytes(_lib.OP_FP8_LINEAR, 8, 4096, 2048, 0) > 0
+    assert L.qtts_strip_bytes(16, 64, _lib.STRIP_INT8) == 1024

@@ -2,6 +2,7 @@
 
     python tts-inference_amd/build.py            # build
     python tts-inference_amd/build.py --verbose  # echo the hipcc lines
+    python tts-inference_amd/build.py --sanitize # libqtts_amd_san.so: host code under ASan + UBSan
 
 Each csrc/*.hip compiles to an object under _build/ (parallel), then one link
 produces qtts_amd/libqtts_amd.so next to the Python package that loads it.
@@ -22,6 +23,15 @@ ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "qtts_amd", "libqtts_amd.so")
 BUILD_DIR = os.path.join(HERE, "_build")
+# The host-side checking build: argument validation, workspace sizing and launch
+# configuration under AddressSanitizer and UndefinedBehaviorSanitizer (device code as
+# usual; it never runs there).  tests/test_abi_sanitized.py loads it with the ASan runtime
+# preloaded, in a process without torch.
+SAN_OUT = os.path.join(HERE, "qtts_amd", "libqtts_amd_san.so")
+SAN_BUILD_DIR = os.path.join(HERE, "_build_san")
+SAN_FLAGS = [f for flag in ("-fsanitize=address", "-fsanitize=undefined", "-fno-sanitize-recover=undefined",
+                            "-fno-omit-frame-pointer") for f in ("-Xarch_host", flag)]
+SAN_LINK = ["-fsanitize=address,undefined", "-shared-libsan"]
 ARCH = "gfx950"
 
 # -packed-fp32-ops: keep hipcc from forming v_pk_{add,mul,fma}_f32.  The host pass
@@ -66,25 +76,36 @@ def _run(cmd: list[str], verbose: bool) -> None:
         print(err, file=sys.stderr)
 
 
-def build(verbose: bool = False) -> str:
+def build(verbose: bool = False, sanitize: bool = False) -> str:
     cc = hipcc()
-    os.makedirs(BUILD_DIR, exist_ok=True)
+    out, build_dir = (SAN_OUT, SAN_BUILD_DIR) if sanitize else (OUT, BUILD_DIR)
+    extra, link = (SAN_FLAGS, SAN_LINK) if sanitize else ([], [])
+    os.makedirs(build_dir, exist_ok=True)
     sources = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
     objs = []
     cmds = []
     for src in sources:
-        obj = os.path.join(BUILD_DIR, src.replace(".hip", ".o"))
+        obj = os.path.join(build_dir, src.replace(".hip", ".o"))
         objs.append(obj)
-        cmds.append([cc, *HIPCC_FLAGS, *FILE_FLAGS.get(src, []), "-c", os.path.join(CSRC, src), "-o", obj])
+        cmds.append([cc, *HIPCC_FLAGS, *FILE_FLAGS.get(src, []), *extra, "-c", os.path.join(CSRC, src), "-o", obj])
     workers = min(len(cmds), max(1, min(8, os.cpu_count() or 1)))
     with concurrent.futures.ThreadPoolExecutor(workers) as pool:
         list(pool.map(lambda c: _run(c, verbose), cmds))
-    tmp = OUT + ".tmp"
+    tmp = out + ".tmp"
     # -z defs: an entry point declared but not defined fails the link here, not the first import
-    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", "-o", tmp, *objs], verbose)
-    os.replace(tmp, OUT)
-    return OUT
+    _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,-z,defs", *link, "-o", tmp, *objs], verbose)
+    os.replace(tmp, out)
+    return out
+
+
+def sanitized_stale() -> bool:
+    """True when libqtts_amd_san.so is missing or older than a source it is built from."""
+    if not os.path.exists(SAN_OUT):
+        return True
+    built = os.path.getmtime(SAN_OUT)
+    srcs = [os.path.join(CSRC, f) for f in os.listdir(CSRC)] + [os.path.join(ROOT, "include", "qtts_amd.h")]
+    return any(os.path.getmtime(f) > built for f in srcs)
 
 
 if __name__ == "__main__":
-    print(build(verbose="--verbose" in sys.argv))
+    print(build(verbose="--verbose" in sys.argv, sanitize="--sanitize" in sys.argv))

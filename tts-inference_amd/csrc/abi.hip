@@ -216,7 +216,9 @@ int qtts_device_supported(int device) {
 
 int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo) {
   const bool rows_ok = op == QTTS_OP_W8A16 || op == QTTS_OP_W8A16_FUSED || op == QTTS_OP_W8A16_SILU;
-  if (m < 0 || n < 0 || k < 0 || !(rows_ok ? algo_ok_rows(algo) : algo_ok(algo)))
+  // sizes past 2^31 are rejected as every entry point rejects them (and m * k stays in range)
+  if (m < 0 || n < 0 || k < 0 || m >= (1ll << 31) || n >= (1ll << 31) || k >= (1ll << 31) ||
+      !(rows_ok ? algo_ok_rows(algo) : algo_ok(algo)))
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "bad workspace query");
   if (m == 0 || n == 0) return 0;
   switch (op) {
@@ -679,13 +681,13 @@ int qtts_fp8w_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int6
 }
 
 int64_t qtts_strip_bytes(int64_t n, int64_t k, int kind) {
-  if (n < 0 || k < 0 || (kind != QTTS_STRIP_INT8 && kind != QTTS_STRIP_FP8))
+  if (n < 0 || k < 0 || n >= (1ll << 31) || k >= (1ll << 31) || (kind != QTTS_STRIP_INT8 && kind != QTTS_STRIP_FP8))
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "strip_bytes: bad arguments");
   return qtts::strip_bytes(n, k, kind);
 }
 
 int qtts_to_strips(const void* src, int64_t n, int64_t k, int64_t ld_src, int kind, void* dst, void* stream) {
-  QTTS_REQUIRE(n >= 0 && k >= 0 && ld_src >= k, "to_strips: bad sizes");
+  QTTS_REQUIRE(n >= 0 && k >= 0 && n < (1ll << 31) && k < (1ll << 31) && ld_src >= k, "to_strips: bad sizes");
   QTTS_REQUIRE(kind == QTTS_STRIP_INT8 || kind == QTTS_STRIP_FP8, "to_strips: bad kind %d", kind);
   if (n == 0 || k == 0) return QTTS_OK;
   QTTS_REQUIRE(src && dst, "to_strips: null pointer");
@@ -695,7 +697,7 @@ int qtts_to_strips(const void* src, int64_t n, int64_t k, int64_t ld_src, int ki
 }
 
 int qtts_from_strips(const void* src, int64_t n, int64_t k, int kind, void* dst, int64_t ld_dst, void* stream) {
-  QTTS_REQUIRE(n >= 0 && k >= 0 && ld_dst >= k, "from_strips: bad sizes");
+  QTTS_REQUIRE(n >= 0 && k >= 0 && n < (1ll << 31) && k < (1ll << 31) && ld_dst >= k, "from_strips: bad sizes");
   QTTS_REQUIRE(kind == QTTS_STRIP_INT8 || kind == QTTS_STRIP_FP8, "from_strips: bad kind %d", kind);
   if (n == 0 || k == 0) return QTTS_OK;
   QTTS_REQUIRE(src && dst, "from_strips: null pointer");
@@ -706,7 +708,7 @@ int qtts_from_strips(const void* src, int64_t n, int64_t k, int kind, void* dst,
 
 int qtts_dequant_strips(const void* qs, int codes, int64_t n, int64_t k, const void* scale, int scale_dtype, void* w,
                         int w_dtype, int64_t ldw, void* stream) {
-  QTTS_REQUIRE(n >= 0 && k >= 0 && ldw >= k, "dequant_strips: bad sizes");
+  QTTS_REQUIRE(n >= 0 && k >= 0 && n < (1ll << 31) && k < (1ll << 31) && ldw >= k, "dequant_strips: bad sizes");
   QTTS_REQUIRE(n < (1ll << 31) && k < (1ll << 31), "dequant_strips: size too large");
   QTTS_REQUIRE(codes == QTTS_CODE_INT8 || codes == QTTS_CODE_E4M3, "dequant_strips: bad code kind %d", codes);
   QTTS_REQUIRE(dtype_ok(scale_dtype) && dtype_ok(w_dtype), "dequant_strips: bad dtype code");
