@@ -15,7 +15,9 @@ import os
 import threading
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "libqtts_amd.so")
+#: QTTS_AMD_LIB names another build of the same library to load instead (e.g. the
+#: sanitized one of build.py --sanitize, run with the ASan runtime preloaded)
+LIB_PATH = os.environ.get("QTTS_AMD_LIB") or os.path.join(HERE, "libqtts_amd.so")
 
 ABI_VERSION = 1
 
