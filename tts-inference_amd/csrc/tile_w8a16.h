@@ -203,8 +203,11 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
     // Operands read one stage ahead into a second register set: step i waits for stage
     // i+1's loads (up to P-3 later stages may stay in flight), barrier (stage i+1 has
     // landed for every wave, and every wave is done with stage i-1, whose buffer the
-    // issue of stage i+P-1 reuses), issues stage i+P-1, starts the LDS reads of stage
-    // i+1, then runs stage i's MFMAs from the registers read the step before.
+    // issue of stage i+P-1 reuses), issues stage i+P-1, reads stage i+1, and runs stage
+    // i's MFMAs from the registers read the step before.  The compiler places those reads
+    // after the MFMAs; their latency then passes during the next step's wait and barrier
+    // instead of between a barrier and the first MFMA of the stage they feed (pinning them
+    // ahead of the MFMAs measured slower: the wait-count pass then waits for them there).
     V xa0[MB][2], xa1[MB][2];
     i32x4_t wq0[NB], wq1[NB];
     if (nk > 0) {
