@@ -552,6 +552,33 @@ def test_w8a16_strips_tile_forced_shapes(ops):
                         assert torch.equal(y_ra, y), what + " read-ahead"
 
 
+def test_w8a16_strips_tile_eight_waves(ops):
+    """Every 8-wave tile the kernel is built for (two waves a SIMD), 3 and 4 stages, with and without
+    read-ahead: against the oracle, and bit for bit equal to the 4-wave 32 x 64 tile with the same
+    split (same K ranges, same MFMAs in the same order); ragged M and N, short and long K."""
+    built = ((32, 64, True), (64, 128, False), (64, 128, True), (64, 256, False), (128, 128, True),
+             (256, 128, True), (128, 256, False), (128, 256, True))
+    for m, n, k, splits in ((70, 520, 1024, 2), (40, 200, 128, 1), (300, 1040, 2048, 1), (130, 272, 192, 3)):
+        x, w, b = _make(m, n, k, bias=True, seed=5151 + k + m)
+        q, s = ops.pack_int8(w, torch.bfloat16)
+        qs = ops.to_strips(q)
+        ref = _oracle_w8a16(x, q, s, b)
+        y4 = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, 3, ops.tile_shape(32, 64)))
+        assert_close(y4, ref, f"tile m={m} n={n} k={k} S={splits} 4 waves")
+        for bm, bn, grid2 in built:
+            shape = ops.tile_shape(bm, bn, 8, grid2)
+            for stages in (3, 4):
+                for ra in (0, ops.TILE_READ_AHEAD):
+                    what = f"tile m={m} n={n} k={k} S={splits} {bm}x{bn} 8 waves grid2={grid2} P={stages} ra={ra}"
+                    print(what, flush=True)
+                    try:
+                        y = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, stages | ra, shape))
+                    except ValueError as e:
+                        assert stages == 4 and bm == 256 and "stages are not built" in str(e), (what, e)
+                        continue
+                    assert torch.equal(y, y4), what
+
+
 def _fused_waves(n: int, k: int) -> int:
     """The fused fp8 linear's wave count (fp8_fused.hip: fused_cfg)."""
     nch = k // 128

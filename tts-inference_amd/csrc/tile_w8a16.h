@@ -64,23 +64,23 @@ __device__ __forceinline__ float scale_bits_to_f32(uint32_t b, int dt) {
 
 template <typename XT> __device__ __forceinline__ float xbits_to_f32(uint32_t b) { return to_f32(XT{(uint16_t)b}); }
 
-template <typename XT, int BM, int BN, int P, int WM, bool F8W, bool PF = false>
-__global__ __launch_bounds__(256) void w8a16_pipe_kernel(
+template <typename XT, int BM, int BN, int P, int WM, bool F8W, bool PF = false, int NW = 4>
+__global__ __launch_bounds__(NW * 64) void w8a16_pipe_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ qs, int N,
     const void* __restrict__ scale, int sdt, const XT* __restrict__ bias, XT* __restrict__ y, int64_t ldy,
     float* __restrict__ part, unsigned* __restrict__ counters, int mtiles, int ntiles, int S, int cps) {
   typedef mfma16<XT> MM;
   typedef typename MM::vec V;
-  constexpr int WN = 4 / WM;           // the 4 waves form a WM x WN grid over the tile
+  constexpr int WN = NW / WM;          // the NW waves form a WM x WN grid over the tile
   constexpr int TMB = BM / 16;         // 16-row m-blocks per tile
   constexpr int MB = TMB / WM;         // 16-row m-blocks per wave
   constexpr int NB = BN / 16 / WN;     // 16-column strips per wave
   constexpr int XF = 2 * TMB;          // activation fragments per stage
   constexpr int WF = BN / 16;          // weight fragments per stage
   constexpr int F = XF + WF;
-  constexpr int FPW = F / 4;           // fragments each wave loads per stage
+  constexpr int FPW = F / NW;          // fragments each wave loads per stage
   constexpr int SB = F * 1024;         // stage bytes
-  static_assert(F % 4 == 0, "fragments must split evenly over 4 waves");
+  static_assert(F % NW == 0 && (NW == 4 || NW == 8), "fragments must split evenly over the waves");
   static_assert((WM == 1 || WM == 2) && MB >= 1 && NB >= 1, "wave grid must cover the tile");
   static_assert(P >= 2 && P * SB + 64 <= kLdsBytes, "stage ring must fit in LDS");
   static_assert((P - 2) * FPW < 64, "vmcnt is 6 bits");
@@ -250,7 +250,7 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int t = 0; t < 4; ++t) a[(nb * MB + mb) * 4 + t] = acc[nb][mb][t];
-    if (!splitk_meet<NV>(a, part + (int64_t)tile * S * 256 * NV, &counters[tile], S, split, tid, 256, &flag))
+    if (!splitk_meet<NV>(a, part + (int64_t)tile * S * (NW * 64) * NV, &counters[tile], S, split, tid, NW * 64, &flag))
       return;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -294,60 +294,79 @@ __global__ __launch_bounds__(256) void w8a16_pipe_kernel(
 }
 
 
-struct PipeCfg { int bm, bn, P, wm, S, cps, mtiles, ntiles, pf; };
+struct PipeCfg { int bm, bn, P, wm, S, cps, mtiles, ntiles, pf, nw; };
 
 constexpr int pipe_stage_bytes_c(int bm, int bn) { return (bm / 8 + bn / 16) * 1024; }
 
 // Stage counts built per tile shape (read-ahead from 3); a calibrator may pick one through
 // algo bits 16-23.
-inline bool pipe_p_ok(int bm, int bn, int p) {
+inline bool pipe_p_ok(int bm, int bn, int p, int nw = 4) {
   if (p != 2 && p != 3 && p != 4 && p != 6 && p != 8) return false;
-  const int fpw = (bm / 8 + bn / 16) / 4;
+  if (nw == 8 && p != 3 && p != 4) return false;
+  const int fpw = (bm / 8 + bn / 16) / nw;
   return p * pipe_stage_bytes_c(bm, bn) + 64 <= kLdsBytes && (p - 2) * fpw < 64;
 }
 
-// Automatic choice, from a sweep of tile shapes x stages x read-ahead x splits over the
-// talker shapes at M = 64..2048:
-//   * 32 x 64 tiles up to M = 128, and up to M = 256 while that makes at most 512 tiles
-//     and K is at most 4096 (at M = 256: qkv 13.0, o_proj 9.4 us);
-//   * 64 x 128 tiles otherwise up to M = 256 (gate_up 26.6, down_proj 18.4 us);
-//   * above M = 256, 128 x 128 tiles while they number at least 256 (qkv at M = 1024:
-//     27.9 us), else 64 x 128 (o_proj 16.4, down_proj 40.5 us at M = 1024);
-// all with 4 stages read one stage ahead (PF) -- except where 128 x 128 tiles number
-// 512 or more (gate_up at M >= 1024): there 3 stages without read-ahead, whose 72 KiB
-// leave room for two workgroups a CU (76.6 against 80.1 us).  Then split K until there
-// are 256 workgroups, keeping >= 8 chunks a split; without read-ahead on to 512
-// workgroups while a split keeps >= 32 chunks (the second resident workgroup).
+// Automatic choice, from sweeps of tile shape x wave count x stages x read-ahead x splits
+// over the talker shapes at M = 64..2048 (configs[3]; µs at M = 256 / 1024 / 2048 below):
+//   * 32 x 64 tiles and 4 waves where they number at most 256, up to M = 128, and up to
+//     M = 256 for K <= 4096 (o_proj at M = 256: 9.1; the decode-sized shapes), and where
+//     they number at most 512 for K <= 1024 up to M = 256 (the code predictor's qkv at
+//     M = 256: 8.2 against 10.3 with 8 waves; its gate_up at M = 128: 8.0 against 9.7);
+//   * otherwise 8 waves (two a SIMD) on a 1 x 8 grid, each wave dequantizing only its own
+//     weight columns, with 4 stages read one stage ahead:
+//       - 128 x 256 tiles where they number at least 192, or at least 128 with K >= 4096
+//         (gate_up from M = 512: 39.9 / 74.8 / 124.2, against 51.5 / 78.1 / 142.9 with
+//         the former 4-wave 64 x 128 and 128 x 128 tiles; qkv at M = 2048 43.5 against
+//         52.3; down_proj at M = 2048 68.4 against 72.0);
+//       - else 64 x 256 tiles where they number at least 192 (gate_up at M = 256: 23.3
+//         against 25.7; qkv at M = 1024 25.4 against 26.8);
+//       - else 64 x 128 (down_proj 17.1 / 37.7 against 18.4 / 39.7, o_proj at M = 1024
+//         15.4 against 16.7, gate_up at M = 128 14.9 against 18.5).
+//   Splits: with 4 waves, split K until there are 256 workgroups, keeping >= 8 chunks a
+//   split; with 8 waves only while that keeps the workgroups within 256 (a split-K meeting
+//   costs more than the idle compute units it fills: gate_up at M = 128, 192 tiles, 14.9
+//   unsplit against 18.7 in two splits).
 // A workspace too small for the splits drops the automatic choice to one split.
-// shape_req (algo bits 24-30): bits 0-1 log2(BM / 16) in 1..3, bit 2 a 2 x 2 wave grid
-// (else 1 x 4), bits 4-6 log2(BN / 32) in 1..3; 0 = automatic.  stages_req (algo bits
-// 16-23): bits 0-5 the stage count (0 = automatic), bit 6 read-ahead; 0 = automatic.
+// shape_req (algo bits 24-30): bits 0-1 log2(BM / 16) in 1..3 (0 = 256 rows, 8 waves
+// only), bit 2 a 2 x 2 (2 x 4 with 8 waves) wave grid in place of 1 x 4 (1 x 8), bit 3
+// 8 waves in place of 4, bits 4-6 log2(BN / 32) in 1..3; 0 = automatic.  stages_req
+// (algo bits 16-23): bits 0-5 the stage count (0 = automatic), bit 6 read-ahead; 0 =
+// automatic.
 inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int stages_req, int shape_req = 0) {
   PipeCfg c;
   const int nchunks = std::max(1, (int)(k / 64));
-  const int64_t t128 = ((m + 127) / 128) * ((n + 127) / 128);
+  auto tiles_of = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
   c.wm = 1;
-  bool wide = false;  // 128 x 128 tiles enough to fill the GPU twice: 3 stages, no read-ahead
+  c.nw = 4;
   if (shape_req != 0) {
-    c.bm = 16 << (shape_req & 3);
+    c.nw = (shape_req & 8) ? 8 : 4;
+    c.bm = (shape_req & 3) == 0 ? 256 : 16 << (shape_req & 3);
     c.bn = 32 << ((shape_req >> 4) & 7);
     c.wm = (shape_req >> 2) & 1 ? 2 : 1;
-  } else if (m <= 128 || (m <= 256 && ((m + 31) / 32) * ((n + 63) / 64) <= 512 && nchunks <= 64)) {
+  } else if (m <= 256 && ((tiles_of(32, 64) <= 256 && (m <= 128 || nchunks <= 64)) ||
+                          (tiles_of(32, 64) <= 512 && nchunks <= 16))) {
     c.bm = 32;
     c.bn = 64;
-  } else if (m > 256 && t128 >= 256) {
-    c.bm = 128;
-    c.bn = 128;
-    wide = t128 >= 512;
   } else {
-    c.bm = 64;
-    c.bn = 128;
+    c.nw = 8;
+    const int64_t t256 = tiles_of(128, 256);
+    if (t256 >= 192 || (t256 >= 128 && nchunks >= 64)) {
+      c.bm = 128;
+      c.bn = 256;
+    } else if (tiles_of(64, 256) >= 192) {
+      c.bm = 64;
+      c.bn = 256;
+    } else {
+      c.bm = 64;
+      c.bn = 128;
+    }
   }
   c.mtiles = (int)((m + c.bm - 1) / c.bm);
   c.ntiles = (int)((n + c.bn - 1) / c.bn);
   if (stages_req == 0) {
-    c.P = wide ? 3 : 4;
-    c.pf = wide ? 0 : 1;
+    c.P = 4 * pipe_stage_bytes_c(c.bm, c.bn) + 64 <= kLdsBytes ? 4 : 3;
+    c.pf = 1;
   } else {
     c.P = (stages_req & 0x3f) > 0 ? (stages_req & 0x3f) : (c.bm * c.bn <= 32 * 64 ? 4 : 3);
     c.pf = (stages_req >> 6) & 1;
@@ -356,10 +375,10 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
   int S = splits_req;
   if (S <= 0) {
     S = 1;
-    while (tiles * S < 256 && nchunks / (S * 2) >= 8) S *= 2;
-    // long K (>= 32 chunks a split): fill the two resident workgroups a CU holds
-    if (!c.pf)
-      while (tiles * S < 512 && nchunks / (S * 2) >= 32) S *= 2;
+    if (c.nw == 8)
+      while (tiles * S * 2 <= 256 && nchunks / (S * 2) >= 8) S *= 2;
+    else
+      while (tiles * S < 256 && nchunks / (S * 2) >= 8) S *= 2;
   }
   S = std::max(1, std::min(S, nchunks));
   if (tiles > kMaxSplitTiles) S = 1;
@@ -370,8 +389,8 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
 
 inline int64_t pipe_ws(const PipeCfg& c) {
   if (c.S <= 1) return 0;
-  const int64_t nv = (int64_t)(c.bn / 64) * (c.bm / 16) * 4;
-  return kCounterBytes + (int64_t)c.mtiles * c.ntiles * c.S * 256 * nv * 4;
+  // one fp32 partial tile per (tile, split)
+  return kCounterBytes + (int64_t)c.mtiles * c.ntiles * c.S * c.bm * c.bn * 4;
 }
 
 struct PipeArgs {
@@ -417,9 +436,49 @@ inline void launch_pipe_bn(const PipeCfg& c, const PipeArgs& a, unsigned blocks,
   else launch_pipe_grid<F8W, XT, BM, 64>(c, a, blocks, st);
 }
 
+template <bool F8W, typename XT, int BM, int BN, int WM>
+inline void launch_pipe8_p(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
+#define QTTS_P8(P, PF)                                                                                             \
+  do {                                                                                                             \
+    if constexpr (P * pipe_stage_bytes_c(BM, BN) + 64 <= kLdsBytes)                                                \
+      qtts::launch(&w8a16_pipe_kernel<XT, BM, BN, P, WM, F8W, PF, 8>, dim3(blocks), dim3(512), 0, st,              \
+                   (const XT*)a.x, (int)a.m, (int)a.k, a.ldx, a.qs, (int)a.n, a.scale, a.sdt, (const XT*)a.bias,   \
+                   (XT*)a.y, a.ldy, a.part, a.counters, c.mtiles, c.ntiles, c.S, c.cps);                           \
+  } while (0)
+  if (c.P == 3) {
+    if (c.pf) QTTS_P8(3, true);
+    else QTTS_P8(3, false);
+  } else {
+    if (c.pf) QTTS_P8(4, true);
+    else QTTS_P8(4, false);
+  }
+#undef QTTS_P8
+}
+
+// Eight waves (two a SIMD): 128 x 128 and 256 x 128 tiles on a 2 x 4 grid, 128 x 256 on
+// 1 x 8 or 2 x 4.
+template <bool F8W, typename XT>
+inline void launch_pipe8(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
+  if (c.bm == 32) launch_pipe8_p<F8W, XT, 32, 64, 2>(c, a, blocks, st);
+  else if (c.bm == 64 && c.bn == 256) launch_pipe8_p<F8W, XT, 64, 256, 1>(c, a, blocks, st);
+  else if (c.bm == 64 && c.wm == 1) launch_pipe8_p<F8W, XT, 64, 128, 1>(c, a, blocks, st);
+  else if (c.bm == 64) launch_pipe8_p<F8W, XT, 64, 128, 2>(c, a, blocks, st);
+  else if (c.bm == 128 && c.bn == 128) launch_pipe8_p<F8W, XT, 128, 128, 2>(c, a, blocks, st);
+  else if (c.bm == 256 && c.bn == 128) launch_pipe8_p<F8W, XT, 256, 128, 2>(c, a, blocks, st);
+  else if (c.bm == 128 && c.bn == 256 && c.wm == 1) launch_pipe8_p<F8W, XT, 128, 256, 1>(c, a, blocks, st);
+  else launch_pipe8_p<F8W, XT, 128, 256, 2>(c, a, blocks, st);
+}
+
+inline bool pipe8_shape_built(int bm, int bn, int wm) {
+  return (bm == 32 && bn == 64 && wm == 2) || (bm == 64 && bn == 128) || (bm == 64 && bn == 256 && wm == 1) ||
+         (bm == 128 && bn == 128 && wm == 2) ||
+         (bm == 256 && bn == 128 && wm == 2) || (bm == 128 && bn == 256);
+}
+
 template <bool F8W, typename XT>
 inline void launch_pipe_bm(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
-  if (c.bm == 32) launch_pipe_bn<F8W, XT, 32>(c, a, blocks, st);
+  if (c.nw == 8) launch_pipe8<F8W, XT>(c, a, blocks, st);
+  else if (c.bm == 32) launch_pipe_bn<F8W, XT, 32>(c, a, blocks, st);
   else if (c.bm == 64) launch_pipe_bn<F8W, XT, 64>(c, a, blocks, st);
   else launch_pipe_bn<F8W, XT, 128>(c, a, blocks, st);
 }
@@ -430,7 +489,11 @@ inline bool pipe_stages_ok(int stages) { return stages >= 0 && (stages >> 7) == 
 inline bool pipe_shape_ok(int shape) {
   if (shape == 0) return true;
   const int b = shape & 3, c = (shape >> 4) & 7;
-  return (shape >> 7) == 0 && (shape & 8) == 0 && b >= 1 && c >= 1 && c <= 3;
+  if (shape & 8) {  // eight waves: the built tiles only
+    const int bm = b == 0 ? 256 : 16 << b, bn = 32 << c;
+    return (shape >> 7) == 0 && c >= 1 && c <= 3 && pipe8_shape_built(bm, bn, (shape & 4) ? 2 : 1);
+  }
+  return (shape >> 7) == 0 && b >= 1 && c >= 1 && c <= 3;
 }
 
 // x [m, k] (bf16 or fp16, 16-byte aligned rows), qs strip layout, k % 64 == 0, m > 0.
@@ -446,7 +509,7 @@ inline int w8a16_pipe_launch(const char* what, const void* x, int x_dtype, int64
   PipeCfg c = pipe_cfg(m, n, k, splits, stages, shape);
   if (c.pf && c.P < 3)
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: read-ahead needs 3 stages", what);
-  if (!pipe_p_ok(c.bm, c.bn, c.P))
+  if (!pipe_p_ok(c.bm, c.bn, c.P, c.nw))
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: %d stages are not built for a %dx%d tile", what, c.P,
                           c.bm, c.bn);
   const int64_t need = pipe_ws(c);

@@ -22,6 +22,7 @@ from .. import _lib, ops
 from . import prefill
 from .base import QuantMethodBase
 from .calibrate import calibrate_buckets
+from .int8 import tile8_candidates
 from .kernels import kernel_available
 
 _FP8_MAX = 448.0
@@ -94,9 +95,10 @@ def _fp8w_candidates(rows: int) -> dict[str, int]:
         c["tile"] = _lib.algo_code(_lib.ALGO_TILE)
         for s in (1, 2, 4):
             c[f"tile_s{s}"] = _lib.algo_code(_lib.ALGO_TILE, splits=s)
-        for bm in (1, 2, 3):
-            for bn in (1, 2):
-                c[f"tile_bm{16 << bm}_bn{32 << bn}"] = _lib.algo_code(_lib.ALGO_TILE, 0, 0, bm | (bn << 4))
+        for bm in (32, 64, 128):
+            for bn in (64, 128):
+                c[f"tile_bm{bm}_bn{bn}"] = _lib.algo_code(_lib.ALGO_TILE, 0, 0, _lib.tile_shape(bm, bn))
+        c.update(tile8_candidates())
     return c
 
 

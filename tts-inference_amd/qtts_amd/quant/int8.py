@@ -67,16 +67,27 @@ def _candidates(rows: int) -> dict[str, int]:
         for s in (1, 2, 4):
             for w in (4, 8, 16):
                 c[f"skinny_s{s}_w{w}"] = _lib.algo_code(_lib.ALGO_SKINNY, splits=s, waves=w)
-    if rows > 16:  # tile: split counts, stages and tile shapes (BM 32/64/128 x BN 64/128)
+    if rows > 16:  # tile: split counts, stages and tile shapes (4 waves: BM 32/64/128 x BN 64/128)
         c["tile"] = _lib.algo_code(_lib.ALGO_TILE)
         for s in (1, 2, 4):
             c[f"tile_s{s}"] = _lib.algo_code(_lib.ALGO_TILE, splits=s)
-        for bm in (1, 2, 3):
-            for bn in (1, 2):
+        for bm in (32, 64, 128):
+            for bn in (64, 128):
+                shape = _lib.tile_shape(bm, bn)
                 for p in (3, 4):
-                    c[f"tile_bm{16 << bm}_bn{32 << bn}_p{p}"] = _lib.algo_code(_lib.ALGO_TILE, 0, p, bm | (bn << 4))
-                c[f"tile_bm{16 << bm}_bn{32 << bn}_p4ra"] = _lib.algo_code(_lib.ALGO_TILE, 0, 4 | _lib.TILE_READ_AHEAD,
-                                                                        bm | (bn << 4))
+                    c[f"tile_bm{bm}_bn{bn}_p{p}"] = _lib.algo_code(_lib.ALGO_TILE, 0, p, shape)
+                c[f"tile_bm{bm}_bn{bn}_p4ra"] = _lib.algo_code(_lib.ALGO_TILE, 0, 4 | _lib.TILE_READ_AHEAD, shape)
+        c.update(tile8_candidates())
+    return c
+
+
+def tile8_candidates() -> dict[str, int]:
+    """The 8-wave tiles (4 stages read ahead) in one and two splits."""
+    c: dict[str, int] = {}
+    for bm, bn, grid2 in ((64, 128, False), (64, 256, False), (128, 256, False), (128, 128, True)):
+        for s in (1, 2):
+            c[f"tile8_bm{bm}_bn{bn}{'_g2' if grid2 else ''}_s{s}"] = _lib.algo_code(
+                _lib.ALGO_TILE, s, 4 | _lib.TILE_READ_AHEAD, _lib.tile_shape(bm, bn, 8, grid2))
     return c
 
 
