@@ -507,7 +507,8 @@ def test_fp8_strips_tile_vs_oracle(ops, m):
         ref, inter = _oracle_w8a8(qx, sx, qw, sw, b)
         y = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, odt)
         assert_close(y, ref, f"fp8 strips tile auto m={m} n={n} k={k}", inter)
-        for splits, stages, shape in ((1, 2, 0x11), (2, 3, 0x22), (3, 4, 0x21), (4, 3, 0x12)):
+        for splits, stages, shape in ((1, 2, 0x11), (2, 3, 0x22), (3, 4, 0x21), (4, 3, 0x12),
+                                      (1, 4, 0x2A), (2, 3, 0x3A), (1, 4, 0x2B), (3, 3, 0x3B)):  # 8 waves: 0x_A, 0x_B
             algo = ops.algo_code(2, splits, stages, shape)
             y2 = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, odt, algo)
             assert_close(y2, ref, f"fp8 strips tile m={m} n={n} k={k} S={splits} P={stages} shape={shape:#x}", inter)
@@ -518,6 +519,10 @@ def test_fp8_strips_tile_vs_oracle(ops, m):
                 ra = ops.algo_code(2, splits, stages | ops.TILE_READ_AHEAD, shape)
                 assert torch.equal(y2, ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, odt, ra)), \
                     f"fp8 read-ahead m={m} n={n} k={k} S={splits} P={stages} shape={shape:#x}"
+            if shape & 8:  # 8 waves: the same sums as 4 waves over the same split
+                four = ops.algo_code(2, splits, 3, 0x11)
+                assert torch.equal(y2, ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, b, odt, four)), \
+                    f"fp8 8 waves m={m} n={n} k={k} S={splits} P={stages} shape={shape:#x}"
 
 
 def test_w8a16_strips_tile_forced_shapes(ops):

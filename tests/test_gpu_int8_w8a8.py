@@ -190,12 +190,13 @@ def test_int8_gemm_every_config_identical(ops):
     bias = torch.randn(n, device="cuda").to(torch.bfloat16)
     want = _oracle_gemm(qx, sx, qw, sw, bias, torch.bfloat16)
     algos = [ops.algo_code(1, s, w) for s in (0, 1, 2, 4, 8) for w in (0, 1, 4, 16)]
-    def fits(p, shape):  # the stage ring must fit the 160 KiB of LDS
-        bm, bn = (32, 64) if shape == 0 else (16 << (shape & 15), 32 << (shape >> 4))
-        return (p & 0x3f) * (bm // 8 + bn // 8) * 1024 + 64 <= 160 * 1024
+    def fits(p, shape):  # the stage ring must fit the 160 KiB of LDS; 8 waves build 3 and 4 stages
+        bm, bn = (32, 64) if shape == 0 else (16 << (shape & 7), 32 << (shape >> 4))
+        return (p & 0x3f) * (bm // 8 + bn // 8) * 1024 + 64 <= 160 * 1024 and not (shape & 8 and p & 0x3f == 2)
     ra = ops.TILE_READ_AHEAD  # operands read one stage ahead
+    eight = (0x2A, 0x3A, 0x2B, 0x3B)  # 8 waves: 64 x 128, 64 x 256, 128 x 128, 128 x 256
     algos += [ops.algo_code(2, s, p, shape) for s in (0, 1, 2, 4) for p in (2, 3, 4, 3 | ra, 4 | ra)
-              for shape in (0, 0x11, 0x21, 0x12, 0x22, 0x32, 0x13, 0x23) if fits(p, shape)]
+              for shape in (0, 0x11, 0x21, 0x12, 0x22, 0x32, 0x13, 0x23) + eight if fits(p, shape)]
     with pytest.raises(ValueError, match="read-ahead needs 3 stages"):
         ops.w8a8_int8_gemm_strips(qx, sx, qs, n, sw, bias, torch.bfloat16, ops.algo_code(2, 0, 2 | ra, 0x11))
     for algo in algos:

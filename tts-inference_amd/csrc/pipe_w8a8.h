@@ -7,11 +7,11 @@
 //   int8: y = round((f32(acc_i32) * sx[m]) * sw[n] [+ f32(bias)])     torch._int_mm and
 //         the fp32 epilogue of qtts/quant/int8.py:151-160 (one rounding at the end)
 //
-// Same pipeline as the W8A16 tile kernel (tile.hip): 4 waves own a BM x BN tile and
-// walk K through a P-deep LDS ring filled by direct global -> LDS loads, one barrier
-// per stage.  A stage is 128 K columns, and every load writes one 1 KiB half of the
-// stage's MFMA fragments in lane order (lane l: row l % 16 of a 16-row block, 16
-// bytes at stage column Kind::col(l / 16, h)):
+// Same pipeline as the W8A16 tile kernel (tile.hip): 4 waves (8, two a SIMD, on the
+// larger tiles) own a BM x BN tile and walk K through a P-deep LDS ring filled by
+// direct global -> LDS loads, one barrier per stage.  A stage is 128 K columns, and
+// every load writes one 1 KiB half of the stage's MFMA fragments in lane order (lane l:
+// row l % 16 of a 16-row block, 16 bytes at stage column Kind::col(l / 16, h)):
 //   * fp8: the two halves are the 32-byte operand of one
 //     v_mfma_scale_f32_16x16x128_f8f6f4 (unit block scales); col = 32 g + 16 h, the
 //     QTTS_STRIP_FP8 block's lane order;
@@ -19,7 +19,7 @@
 //     64-column chunk; col = 64 h + 16 g, two consecutive QTTS_STRIP_INT8 blocks.
 // With strip weights a weight half is 1 KiB of contiguous memory; with row-major
 // weights (int8 only) it is gathered like an activation half, 64 contiguous bytes a
-// row.  Wave w owns columns [n0 + w BN/4, n0 + (w+1) BN/4) for all BM rows.
+// row.  Of NW waves, wave w owns columns [n0 + w BN/NW, n0 + (w+1) BN/NW) for all BM rows.
 #pragma once
 
 #include <algorithm>
@@ -77,8 +77,8 @@ struct PipeI8 {
   }
 };
 
-template <typename Kind, typename OT, int BM, int BN, int P, int LAYOUT, bool PF = false>
-__global__ __launch_bounds__(256) void w8a8_pipe_kernel(
+template <typename Kind, typename OT, int BM, int BN, int P, int LAYOUT, bool PF = false, int NW = 4>
+__global__ __launch_bounds__(NW * 64) void w8a8_pipe_kernel(
     const typename Kind::code_t* __restrict__ qx_, const float* __restrict__ sx, int M, int K, int64_t ldqx,
     const typename Kind::code_t* __restrict__ qw_, int N, int64_t ldqw, const float* __restrict__ sw,
     const OT* __restrict__ bias, OT* __restrict__ y, int64_t ldy, typename Kind::part_t* __restrict__ part,
@@ -86,13 +86,13 @@ __global__ __launch_bounds__(256) void w8a8_pipe_kernel(
   typedef typename Kind::acc_t acc_t;
   typedef typename Kind::part_t part_t;
   constexpr int MB = BM / 16;          // 16-row m-blocks per tile
-  constexpr int NB = BN / 64;          // 16-column strips per wave
+  constexpr int NB = BN / 16 / NW;     // 16-column strips per wave
   constexpr int XF = 2 * MB;           // activation halves per stage
   constexpr int WF = 2 * (BN / 16);    // weight halves per stage
   constexpr int F = XF + WF;
-  constexpr int FPW = F / 4;           // halves each wave loads per stage
+  constexpr int FPW = F / NW;          // halves each wave loads per stage
   constexpr int SB = F * 1024;         // stage bytes
-  static_assert(F % 4 == 0, "fragments must split evenly over 4 waves");
+  static_assert(F % NW == 0 && NB >= 1 && (NW == 4 || NW == 8), "fragments must split evenly over the waves");
   static_assert(P >= 2 && P * SB + 64 <= kLdsBytes, "stage ring must fit in LDS");
   static_assert((P - 2) * FPW < 64, "vmcnt is 6 bits");
   __shared__ __align__(1024) uint8_t ring[P * SB];
@@ -247,7 +247,7 @@ __global__ __launch_bounds__(256) void w8a8_pipe_kernel(
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
         for (int t = 0; t < 4; ++t) a[(nb * MB + mb) * 4 + t] = acc[nb][mb][t];
-    if (!splitk_meet<NV>(a, part + (int64_t)tile * S * 256 * NV, &counters[tile], S, split, tid, 256, &flag))
+    if (!splitk_meet<NV>(a, part + (int64_t)tile * S * (NW * 64) * NV, &counters[tile], S, split, tid, NW * 64, &flag))
       return;
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
@@ -302,47 +302,75 @@ __global__ __launch_bounds__(256) void w8a8_pipe_kernel(
 
 // ---- host side: configuration and launch --------------------------------------------
 
-struct W8A8PipeCfg { int bm, bn, P, S, cps, mtiles, ntiles, pf; };
+struct W8A8PipeCfg { int bm, bn, P, S, cps, mtiles, ntiles, pf, nw; };
 
 constexpr int w8a8_stage_bytes(int bm, int bn) { return (bm / 8 + bn / 8) * 1024; }
 
-inline bool w8a8_p_ok(int bm, int bn, int p) {
+inline bool w8a8_p_ok(int bm, int bn, int p, int nw = 4) {
   if (p != 2 && p != 3 && p != 4 && p != 6 && p != 8) return false;
-  const int fpw = (bm / 8 + bn / 8) / 4;
+  if (nw == 8 && p != 3 && p != 4) return false;
+  const int fpw = (bm / 8 + bn / 8) / nw;
   return p * w8a8_stage_bytes(bm, bn) + 64 <= kLdsBytes && (p - 2) * fpw < 64;
 }
 
-// Automatic choice, from a sweep of tile shapes x stages x read-ahead over the talker
-// shapes at M = 64, 256 and 1024 (int8 and fp8 alike; 128-column stages):
-//   * 32 x 64 tiles with 4 stages up to M = 128, and up to M = 256 while that makes at
-//     most 512 tiles (at M = 256: o_proj 13.8 -> 9.5 us, down_proj 19.3 -> 17.8 us,
-//     qkv 14.6 -> 12.4 us against 64 x 128);
-//   * 64 x 128 tiles above: 4 stages read one stage ahead while they number at most 256
-//     (o_proj at M = 1024: 17.5 -> 16.0 us, down_proj 37.1 -> 31.9 us), else 3 stages
-//     without read-ahead (qkv, gate_up: 2 workgroups a CU);
-// then split K until there are 256 workgroups, keeping >= 4 stages a split.  shape_req:
-// bits 0-3 log2(BM / 16) in 1..3, bits 4-6 log2(BN / 32) in 1..3, 0 = automatic;
-// stages_req: bits 0-5 the stage count, bit 6 read-ahead, 0 = automatic.
+// Automatic choice, from sweeps of tile shape x wave count x stages x read-ahead x splits
+// over the talker shapes at M = 64..2048 (int8 and fp8 alike; 128-column stages; µs for
+// int8, the former choice in brackets):
+//   * 32 x 64 tiles, 4 waves, 4 stages up to M = 256 while they number at most 512 (the
+//     4-wave kernel stays ahead there: qkv at M = 128 6.3 against 9.0 with 8 waves);
+//   * otherwise 8 waves (two a SIMD), each owning BN / 8 columns of all BM rows:
+//       - 128 x 256 tiles, 3 stages, where they number at least 192 (gate_up from
+//         M = 512: 24.6 / 45.2 / 76.7 at M = 512 / 1024 / 2048 [27.0 / 50.7 / 97.6]; qkv
+//         at M = 2048 26.4 [36.6]);
+//       - else 64 x 256 tiles, 3 stages, where they number at least 192 (qkv at M = 1024
+//         16.2 [18.8], o_proj at M = 2048 16.9 [19.4], gate_up at M = 256 15.6 [18.4]);
+//       - else 64 x 128 tiles, 4 stages read one stage ahead (o_proj at M = 512 / 1024
+//         9.3 / 9.8 [10.9 / 10.7], down_proj 16.6 / 22.2 [18.9 / 25.3], gate_up at M = 128
+//         9.7 [13.2]);
+// then split K: with 4 waves until there are 256 workgroups, keeping >= 4 stages a split;
+// with 8 waves only while the workgroups stay within 256 and each split keeps >= 16
+// stages (a split-K meeting costs more than idle compute units on short K: o_proj at
+// M = 512, 128 tiles, 9.3 unsplit against 10.2 in two splits).  shape_req: bits 0-2
+// log2(BM / 16) in 1..3, bit 3 8 waves (BM 64 or 128, BN 128 or 256), bits 4-6
+// log2(BN / 32) in 1..3, 0 = automatic; stages_req: bits 0-5 the stage count, bit 6
+// read-ahead, 0 = automatic.
 inline W8A8PipeCfg w8a8_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int stages_req, int shape_req) {
   W8A8PipeCfg c;
   const int nchunks = std::max(1, (int)(k / 128));
+  auto tiles_of = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
+  c.nw = 4;
   if (shape_req != 0) {
-    c.bm = 16 << (shape_req & 15);
+    c.bm = 16 << (shape_req & 7);
     c.bn = 32 << ((shape_req >> 4) & 7);
-  } else if (m <= 128 || (m <= 256 && ((m + 31) / 32) * ((n + 63) / 64) <= 512)) {
+    c.nw = shape_req & 8 ? 8 : 4;
+  } else if (m <= 256 && tiles_of(32, 64) <= 512) {
     c.bm = 32;
     c.bn = 64;
   } else {
-    c.bm = 64;
-    c.bn = 128;
+    c.nw = 8;
+    if (tiles_of(128, 256) >= 192) {
+      c.bm = 128;
+      c.bn = 256;
+    } else if (tiles_of(64, 256) >= 192) {
+      c.bm = 64;
+      c.bn = 256;
+    } else {
+      c.bm = 64;
+      c.bn = 128;
+    }
   }
   c.mtiles = (int)((m + c.bm - 1) / c.bm);
   c.ntiles = (int)((n + c.bn - 1) / c.bn);
   const int64_t tiles = (int64_t)c.mtiles * c.ntiles;
   if (stages_req == 0) {
-    const bool ra = c.bm == 64 && c.bn == 128 && tiles <= 256;
-    c.P = c.bm * c.bn <= 32 * 64 || ra ? 4 : 3;
-    c.pf = ra ? 1 : 0;
+    if (c.nw == 8) {  // read-ahead where 4 stages fit
+      c.P = 4 * w8a8_stage_bytes(c.bm, c.bn) + 64 <= kLdsBytes ? 4 : 3;
+      c.pf = c.P == 4 ? 1 : 0;
+    } else {
+      const bool ra = c.bm == 64 && c.bn == 128 && tiles <= 256;
+      c.P = c.bm * c.bn <= 32 * 64 || ra ? 4 : 3;
+      c.pf = ra ? 1 : 0;
+    }
   } else {
     c.pf = (stages_req >> 6) & 1;
     c.P = (stages_req & 0x3f) > 0 ? (stages_req & 0x3f) : (c.bm * c.bn <= 32 * 64 ? 4 : 3);
@@ -350,7 +378,10 @@ inline W8A8PipeCfg w8a8_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int
   int S = splits_req;
   if (S <= 0) {
     S = 1;
-    while (tiles * S < 256 && nchunks / (S * 2) >= 4) S *= 2;
+    if (c.nw == 8)
+      while (tiles * S * 2 <= 256 && nchunks / (S * 2) >= 16) S *= 2;
+    else
+      while (tiles * S < 256 && nchunks / (S * 2) >= 4) S *= 2;
   }
   S = std::max(1, std::min(S, nchunks));
   if (tiles > kMaxSplitTiles) S = 1;
@@ -362,14 +393,15 @@ inline W8A8PipeCfg w8a8_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int
 // Split-K workspace: the counter block, then 4-byte partials (fp32 or int32).
 inline int64_t w8a8_ws(const W8A8PipeCfg& c) {
   if (c.S <= 1) return 0;
-  const int64_t nv = (int64_t)(c.bn / 64) * (c.bm / 16) * 4;
-  return kCounterBytes + (int64_t)c.mtiles * c.ntiles * c.S * 256 * nv * 4;
+  return kCounterBytes + (int64_t)c.mtiles * c.ntiles * c.S * c.bm * c.bn * 4;  // one partial tile a split
 }
 
+// 8 waves (bit 3 of the shape code): BM 64 or 128, BN 128 or 256.
 inline bool w8a8_shape_ok(int shape) {
   if (shape == 0) return true;
-  const int b = shape & 15, c = (shape >> 4) & 7;
-  return (shape >> 7) == 0 && b >= 1 && b <= 3 && c >= 1 && c <= 3;
+  const int b = shape & 7, c = (shape >> 4) & 7;
+  if ((shape >> 7) != 0 || b < 1 || b > 3 || c < 1 || c > 3) return false;
+  return !(shape & 8) || (b >= 2 && c >= 2);
 }
 
 template <typename Kind> struct W8A8Args {
@@ -412,9 +444,38 @@ void w8a8_launch_bn(const W8A8PipeCfg& c, const W8A8Args<Kind>& a, unsigned bloc
   else w8a8_launch_stages<Kind, OT, LAYOUT, kMaxP, BM, 64>(c, a, blocks, st);
 }
 
+template <typename Kind, typename OT, int LAYOUT, int BM, int BN>
+void w8a8_launch8_p(const W8A8PipeCfg& c, const W8A8Args<Kind>& a, unsigned blocks, hipStream_t st) {
+#define QTTS_W8P8(P, PF)                                                                                             \
+  do {                                                                                                               \
+    if constexpr (P * w8a8_stage_bytes(BM, BN) + 64 <= kLdsBytes)                                                    \
+      qtts::launch(&w8a8_pipe_kernel<Kind, OT, BM, BN, P, LAYOUT, PF, 8>, dim3(blocks), dim3(512), 0, st, a.qx, a.sx, \
+                   (int)a.m, (int)a.k, a.ldqx, a.qw, (int)a.n, a.ldqw, a.sw, (const OT*)a.bias, (OT*)a.y, a.ldy,      \
+                   a.part, a.counters, c.mtiles, c.ntiles, c.S, c.cps);                                              \
+  } while (0)
+  if (c.P == 3) {
+    if (c.pf) QTTS_W8P8(3, true);
+    else QTTS_W8P8(3, false);
+  } else {
+    if (c.pf) QTTS_W8P8(4, true);
+    else QTTS_W8P8(4, false);
+  }
+#undef QTTS_W8P8
+}
+
+// Eight waves (two a SIMD), each owning BN / 8 columns of all BM rows.
+template <typename Kind, typename OT, int LAYOUT>
+void w8a8_launch8(const W8A8PipeCfg& c, const W8A8Args<Kind>& a, unsigned blocks, hipStream_t st) {
+  if (c.bm == 64 && c.bn == 128) w8a8_launch8_p<Kind, OT, LAYOUT, 64, 128>(c, a, blocks, st);
+  else if (c.bm == 64) w8a8_launch8_p<Kind, OT, LAYOUT, 64, 256>(c, a, blocks, st);
+  else if (c.bn == 128) w8a8_launch8_p<Kind, OT, LAYOUT, 128, 128>(c, a, blocks, st);
+  else w8a8_launch8_p<Kind, OT, LAYOUT, 128, 256>(c, a, blocks, st);
+}
+
 template <typename Kind, typename OT, int LAYOUT, int kMaxP>
 void w8a8_launch_bm(const W8A8PipeCfg& c, const W8A8Args<Kind>& a, unsigned blocks, hipStream_t st) {
-  if (c.bm == 32) w8a8_launch_bn<Kind, OT, LAYOUT, kMaxP, 32>(c, a, blocks, st);
+  if (c.nw == 8) w8a8_launch8<Kind, OT, LAYOUT>(c, a, blocks, st);
+  else if (c.bm == 32) w8a8_launch_bn<Kind, OT, LAYOUT, kMaxP, 32>(c, a, blocks, st);
   else if (c.bm == 64) w8a8_launch_bn<Kind, OT, LAYOUT, kMaxP, 64>(c, a, blocks, st);
   else w8a8_launch_bn<Kind, OT, LAYOUT, kMaxP, 128>(c, a, blocks, st);
 }
@@ -429,7 +490,7 @@ int w8a8_pipe_launch(const char* what, W8A8Args<Kind> a, int out_dtype, int spli
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: bad stages code %d", what, stages);
   W8A8PipeCfg c = w8a8_cfg(a.m, a.n, a.k, splits, stages, shape);
   if (c.pf && c.P < 3) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: read-ahead needs 3 stages", what);
-  if (!w8a8_p_ok(c.bm, c.bn, c.P) || c.P > kMaxP)
+  if (!w8a8_p_ok(c.bm, c.bn, c.P, c.nw) || c.P > kMaxP)
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: %d stages are not built for a %dx%d tile", what, c.P, c.bm,
                           c.bn);
   const int64_t need = w8a8_ws(c);
