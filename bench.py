@@ -583,8 +583,9 @@ def run_traffic_probe(args, torch, ops):
 
 def run_prefill_probe(args, torch, ops):
     """Kernels for a rocprofv3 --pmc pass over the prefill tile kernel: configs[3]'s gate_up
-    (12288 x 2048) at M = 1024, launched eagerly 8 times each (after 3 warm-up launches) as the automatic tile, as the
-    64 x 256 tile (3 stages, no split), and as F.linear on the bf16 weight (hipBLASLt)."""
+    (12288 x 2048) at M = 1024, launched eagerly 8 times each (after 3 warm-up launches) as the automatic tile
+    (8 waves, 128 x 256), as the 4-wave 128 x 128 tile (3 stages, no read-ahead, no split), and as F.linear on the
+    bf16 weight (hipBLASLt)."""
     from qtts_amd import _lib
     ops.reserve_workspace(torch.device("cuda"), 64 << 20)
     n, k, m = 12288, 2048, 1024
@@ -593,7 +594,7 @@ def run_prefill_probe(args, torch, ops):
     q, s = ops.pack_int8(w, torch.bfloat16)
     qs = ops.to_strips(q)
     x = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
-    wide = _lib.algo_code(_lib.ALGO_TILE, 1, 3, 2 | (3 << 4))
+    wide = _lib.algo_code(_lib.ALGO_TILE, 1, 3, _lib.tile_shape(128, 128))
     for fn in (lambda: ops.w8a16_gemm_strips(x, qs, n, s), lambda: ops.w8a16_gemm_strips(x, qs, n, s, None, wide),
                lambda: torch.nn.functional.linear(x, w)):
         for _ in range(3):  # warm-up: code objects loaded, weights resident
