@@ -106,10 +106,14 @@ int qtts_device_supported(int device);
  * 16-21 are the LDS pipeline stages (2, 3, 4, 6, 8; the int8 W8A8 tile builds 2-4),
  * bit 22 reads each stage's operands from LDS one stage ahead (3 stages or more), and
  * bits 16-23 all zero pick stages and read-ahead automatically.  Bits 24-30 are a tile shape code c: bits 28-30 (c >> 4) log2(BN / 32) in 1..3;
- * for W8A16 bits 24-25 (c & 3) log2(BM / 16) in 1..3 and bit 26 (c & 4) a 2 x 2
- * wave grid in place of 1 x 4; for W8A8 (fp8, int8) bits 24-27 (c & 15)
- * log2(BM / 16) in 1..3.  0 = automatic everywhere.  The calibrator uses these to
- * time variants. */
+ * bit 27 (c & 8) 8 waves a workgroup in place of 4 (two a SIMD; 3 or 4 stages);
+ * for W8A16 bits 24-25 (c & 3) log2(BM / 16) in 1..3 (0: 256 rows, 8 waves only) and
+ * bit 26 (c & 4) a 2 x 2 (2 x 4) wave grid in place of 1 x 4 (1 x 8); for W8A8 (fp8,
+ * int8) bits 24-26 (c & 7) log2(BM / 16) in 1..3, 8 waves on BM 64 or 128 and BN 128
+ * or 256.  Tiles with 8 waves are built where the grid divides the tile (W8A16:
+ * 64 x 128, 64 x 256, 128 x 256 on 1 x 8; 32 x 64, 64 x 128, 128 x 128, 128 x 256,
+ * 256 x 128 on 2 x 4).  0 = automatic everywhere.  The calibrator uses these to time
+ * variants. */
 int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo);
 
 /* --- weight packers ------------------------------------------------------------ */
