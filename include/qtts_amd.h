@@ -111,9 +111,9 @@ int qtts_device_supported(int device);
  * bit 26 (c & 4) a 2 x 2 (2 x 4) wave grid in place of 1 x 4 (1 x 8); for W8A8 (fp8,
  * int8) bits 24-26 (c & 7) log2(BM / 16) in 1..3, 8 waves on BM 64 or 128 and BN 128
  * or 256.  Tiles with 8 waves are built where the grid divides the tile (W8A16:
- * 64 x 128, 64 x 256, 128 x 256 on 1 x 8; 32 x 64, 64 x 128, 128 x 128, 128 x 256,
- * 256 x 128 on 2 x 4).  0 = automatic everywhere.  The calibrator uses these to time
- * variants. */
+ * 64 x 128, 64 x 256, 128 x 256 and, with BN code 4, 128 x 384 (3 stages, no read-ahead)
+ * on 1 x 8; 32 x 64, 64 x 128, 128 x 128, 128 x 256, 256 x 128 on 2 x 4).  0 = automatic
+ * everywhere.  The calibrator uses these to time variants. */
 int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo);
 
 /* --- weight packers ------------------------------------------------------------ */

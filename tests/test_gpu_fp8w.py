@@ -87,11 +87,11 @@ def test_fp8w_prefill_and_ragged(ops, dtype):
         assert_close(ops.fp8w_gemm_strips(x, qs, n, s, b), ref, f"auto m={m} n={n} k={k} {dtype}")
         if m > 16:
             eight = (ops.tile_shape(64, 128, 8), ops.tile_shape(64, 256, 8), ops.tile_shape(128, 256, 8),
-                     ops.tile_shape(128, 128, 8, grid2=True))
+                     ops.tile_shape(128, 128, 8, grid2=True), ops.tile_shape(128, 384, 8))
             for splits, shape in ((1, 0), (2, 0), (0, 0x21), (0, 0x12), (0, 0x23)) + tuple((0, e) for e in eight):
                 y = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, 0, shape))
                 assert_close(y, ref, f"tile m={m} n={n} k={k} S={splits} shape={shape:#x} {dtype}")
-                if shape:  # 4 stages with and without read-ahead: the same MFMAs, the same bits
+                if shape and shape != ops.tile_shape(128, 384, 8):  # 4 stages with and without read-ahead: the same bits
                     y4 = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, 4, shape))
                     y4ra = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, 4 | ops.TILE_READ_AHEAD, shape))
                     assert torch.equal(y4, y4ra), f"read-ahead m={m} n={n} k={k} shape={shape:#x} {dtype}"

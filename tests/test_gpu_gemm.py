@@ -562,7 +562,7 @@ def test_w8a16_strips_tile_eight_waves(ops):
     read-ahead: against the oracle, and bit for bit equal to the 4-wave 32 x 64 tile with the same
     split (same K ranges, same MFMAs in the same order); ragged M and N, short and long K."""
     built = ((32, 64, True), (64, 128, False), (64, 128, True), (64, 256, False), (128, 128, True),
-             (256, 128, True), (128, 256, False), (128, 256, True))
+             (256, 128, True), (128, 256, False), (128, 256, True), (128, 384, False))
     for m, n, k, splits in ((70, 520, 1024, 2), (40, 200, 128, 1), (300, 1040, 2048, 1), (130, 272, 192, 3)):
         x, w, b = _make(m, n, k, bias=True, seed=5151 + k + m)
         q, s = ops.pack_int8(w, torch.bfloat16)
@@ -579,7 +579,10 @@ def test_w8a16_strips_tile_eight_waves(ops):
                     try:
                         y = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, stages | ra, shape))
                     except ValueError as e:
-                        assert stages == 4 and bm == 256 and "stages are not built" in str(e), (what, e)
+                        if bn == 384:  # 3 stages without read-ahead only
+                            assert (stages, ra) != (3, 0) and "128x384 tiles are built" in str(e), (what, e)
+                        else:
+                            assert stages == 4 and bm == 256 and "stages are not built" in str(e), (what, e)
                         continue
                     assert torch.equal(y, y4), what
 

@@ -315,7 +315,12 @@ inline bool pipe_p_ok(int bm, int bn, int p, int nw = 4) {
 //     M = 256: 8.2 against 10.3 with 8 waves; its gate_up at M = 128: 8.0 against 9.7);
 //   * otherwise 8 waves (two a SIMD) on a 1 x 8 grid, each wave dequantizing only its own
 //     weight columns, with 4 stages read one stage ahead:
-//       - 128 x 256 tiles where they number at least 192, or at least 128 with K >= 4096
+//       - 128 x 384 tiles (3 stages, no read-ahead: 197 registers, the read-ahead set would
+//         spill) where N is a multiple of 384, they number at least 256 and they fill
+//         whole rounds of 256 workgroups at least as well as 128 x 256 would (gate_up at
+//         M = 1024: 256 tiles, 52.7 against 65.9 us on 384 tiles of 128 x 256; 106.7
+//         against 111.7 at M = 2048);
+//       - else 128 x 256 tiles where they number at least 192, or at least 128 with K >= 4096
 //         (gate_up from M = 512: 39.9 / 74.8 / 124.2, against 51.5 / 78.1 / 142.9 with
 //         the former 4-wave 64 x 128 and 128 x 128 tiles; qkv at M = 2048 43.5 against
 //         52.3; down_proj at M = 2048 68.4 against 72.0);
@@ -330,7 +335,8 @@ inline bool pipe_p_ok(int bm, int bn, int p, int nw = 4) {
 // A workspace too small for the splits drops the automatic choice to one split.
 // shape_req (algo bits 24-30): bits 0-1 log2(BM / 16) in 1..3 (0 = 256 rows, 8 waves
 // only), bit 2 a 2 x 2 (2 x 4 with 8 waves) wave grid in place of 1 x 4 (1 x 8), bit 3
-// 8 waves in place of 4, bits 4-6 log2(BN / 32) in 1..3; 0 = automatic.  stages_req
+// 8 waves in place of 4, bits 4-6 log2(BN / 32) in 1..3 (4: 384 columns, 8 waves, 128
+// rows); 0 = automatic.  stages_req
 // (algo bits 16-23): bits 0-5 the stage count (0 = automatic), bit 6 read-ahead; 0 =
 // automatic.
 inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int stages_req, int shape_req = 0) {
@@ -342,7 +348,7 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
   if (shape_req != 0) {
     c.nw = (shape_req & 8) ? 8 : 4;
     c.bm = (shape_req & 3) == 0 ? 256 : 16 << (shape_req & 3);
-    c.bn = 32 << ((shape_req >> 4) & 7);
+    c.bn = ((shape_req >> 4) & 7) == 4 ? 384 : 32 << ((shape_req >> 4) & 7);
     c.wm = (shape_req >> 2) & 1 ? 2 : 1;
   } else if (m <= 256 && ((tiles_of(32, 64) <= 256 && (m <= 128 || nchunks <= 64)) ||
                           (tiles_of(32, 64) <= 512 && nchunks <= 16))) {
@@ -351,7 +357,12 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
   } else {
     c.nw = 8;
     const int64_t t256 = tiles_of(128, 256);
-    if (t256 >= 192 || (t256 >= 128 && nchunks >= 64)) {
+    // the share of a whole number of rounds (256 compute units, one workgroup each) tiles fill
+    auto fill = [](int64_t t) { return (double)t / (double)(((t + 255) / 256) * 256); };
+    if (n % 384 == 0 && tiles_of(128, 384) >= 256 && fill(tiles_of(128, 384)) >= fill(t256)) {
+      c.bm = 128;
+      c.bn = 384;
+    } else if (t256 >= 192 || (t256 >= 128 && nchunks >= 64)) {
       c.bm = 128;
       c.bn = 256;
     } else if (tiles_of(64, 256) >= 192) {
@@ -366,7 +377,7 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
   c.ntiles = (int)((n + c.bn - 1) / c.bn);
   if (stages_req == 0) {
     c.P = 4 * pipe_stage_bytes_c(c.bm, c.bn) + 64 <= kLdsBytes ? 4 : 3;
-    c.pf = 1;
+    c.pf = c.bn == 384 ? 0 : 1;  // 384 columns: 3 stages, no room for a second register set
   } else {
     c.P = (stages_req & 0x3f) > 0 ? (stages_req & 0x3f) : (c.bm * c.bn <= 32 * 64 ? 4 : 3);
     c.pf = (stages_req >> 6) & 1;
@@ -445,7 +456,9 @@ inline void launch_pipe8_p(const PipeCfg& c, const PipeArgs& a, unsigned blocks,
                    (const XT*)a.x, (int)a.m, (int)a.k, a.ldx, a.qs, (int)a.n, a.scale, a.sdt, (const XT*)a.bias,   \
                    (XT*)a.y, a.ldy, a.part, a.counters, c.mtiles, c.ntiles, c.S, c.cps);                           \
   } while (0)
-  if (c.P == 3) {
+  if constexpr (BN == 384) {  // built with 3 stages and no read-ahead only (the launcher checks)
+    QTTS_P8(3, false);
+  } else if (c.P == 3) {
     if (c.pf) QTTS_P8(3, true);
     else QTTS_P8(3, false);
   } else {
@@ -455,8 +468,8 @@ inline void launch_pipe8_p(const PipeCfg& c, const PipeArgs& a, unsigned blocks,
 #undef QTTS_P8
 }
 
-// Eight waves (two a SIMD): 128 x 128 and 256 x 128 tiles on a 2 x 4 grid, 128 x 256 on
-// 1 x 8 or 2 x 4.
+// Eight waves (two a SIMD): 32 x 64, 128 x 128 and 256 x 128 tiles on a 2 x 4 grid,
+// 64 x 256 and 128 x 384 (3 stages, no read-ahead) on 1 x 8, 64 x 128 and 128 x 256 on either.
 template <bool F8W, typename XT>
 inline void launch_pipe8(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
   if (c.bm == 32) launch_pipe8_p<F8W, XT, 32, 64, 2>(c, a, blocks, st);
@@ -466,12 +479,13 @@ inline void launch_pipe8(const PipeCfg& c, const PipeArgs& a, unsigned blocks, h
   else if (c.bm == 128 && c.bn == 128) launch_pipe8_p<F8W, XT, 128, 128, 2>(c, a, blocks, st);
   else if (c.bm == 256 && c.bn == 128) launch_pipe8_p<F8W, XT, 256, 128, 2>(c, a, blocks, st);
   else if (c.bm == 128 && c.bn == 256 && c.wm == 1) launch_pipe8_p<F8W, XT, 128, 256, 1>(c, a, blocks, st);
+  else if (c.bn == 384) launch_pipe8_p<F8W, XT, 128, 384, 1>(c, a, blocks, st);
   else launch_pipe8_p<F8W, XT, 128, 256, 2>(c, a, blocks, st);
 }
 
 inline bool pipe8_shape_built(int bm, int bn, int wm) {
   return (bm == 32 && bn == 64 && wm == 2) || (bm == 64 && bn == 128) || (bm == 64 && bn == 256 && wm == 1) ||
-         (bm == 128 && bn == 128 && wm == 2) ||
+         (bm == 128 && bn == 384 && wm == 1) || (bm == 128 && bn == 128 && wm == 2) ||
          (bm == 256 && bn == 128 && wm == 2) || (bm == 128 && bn == 256);
 }
 
@@ -489,9 +503,9 @@ inline bool pipe_stages_ok(int stages) { return stages >= 0 && (stages >> 7) == 
 inline bool pipe_shape_ok(int shape) {
   if (shape == 0) return true;
   const int b = shape & 3, c = (shape >> 4) & 7;
-  if (shape & 8) {  // eight waves: the built tiles only
-    const int bm = b == 0 ? 256 : 16 << b, bn = 32 << c;
-    return (shape >> 7) == 0 && c >= 1 && c <= 3 && pipe8_shape_built(bm, bn, (shape & 4) ? 2 : 1);
+  if (shape & 8) {  // eight waves: the built tiles only (BN code 4: 384 columns)
+    const int bm = b == 0 ? 256 : 16 << b, bn = c == 4 ? 384 : 32 << c;
+    return (shape >> 7) == 0 && c >= 1 && c <= 4 && pipe8_shape_built(bm, bn, (shape & 4) ? 2 : 1);
   }
   return (shape >> 7) == 0 && b >= 1 && c >= 1 && c <= 3;
 }
@@ -509,6 +523,8 @@ inline int w8a16_pipe_launch(const char* what, const void* x, int x_dtype, int64
   PipeCfg c = pipe_cfg(m, n, k, splits, stages, shape);
   if (c.pf && c.P < 3)
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: read-ahead needs 3 stages", what);
+  if (c.bn == 384 && (c.P != 3 || c.pf))
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: 128x384 tiles are built with 3 stages and no read-ahead", what);
   if (!pipe_p_ok(c.bm, c.bn, c.P, c.nw))
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: %d stages are not built for a %dx%d tile", what, c.P,
                           c.bm, c.bn);

@@ -44,12 +44,13 @@ TILE_READ_AHEAD = 64
 
 def tile_shape(bm: int, bn: int, waves: int = 4, grid2: bool = False) -> int:
     """A tile kernel's shape code (the `cpw` argument of algo_code): BM x BN output tiles, 4 or
-    8 waves a workgroup on a 1 x waves grid (or 2 x waves/2 with ``grid2``).  BM = 256 only
-    with 8 waves."""
-    if bm not in (32, 64, 128, 256) or bn not in (64, 128, 256) or waves not in (4, 8) or (bm == 256 and waves != 8):
+    8 waves a workgroup on a 1 x waves grid (or 2 x waves/2 with ``grid2``).  BM = 256 and
+    BN = 384 only with 8 waves."""
+    if (bm not in (32, 64, 128, 256) or bn not in (64, 128, 256, 384) or waves not in (4, 8)
+            or (bm == 256 and waves != 8) or (bn == 384 and waves != 8)):
         raise ValueError(f"no tile shape {bm}x{bn} with {waves} waves")
     return {32: 1, 64: 2, 128: 3, 256: 0}[bm] | (4 if grid2 else 0) | (8 if waves == 8 else 0) | (
-        {64: 1, 128: 2, 256: 3}[bn] << 4)
+        {64: 1, 128: 2, 256: 3, 384: 4}[bn] << 4)
 ALGO_AUTO, ALGO_SKINNY, ALGO_TILE = 0, 1, 2
 #: the skinny kernel over row-split strips: 2 (HALF) or 4 (QUARTER) workgroups per 16-row strip
 ALGO_SKINNY_HALF, ALGO_SKINNY_QUARTER = 3, 4
