@@ -349,7 +349,9 @@ int qtts_quant_act_int8_rows(const void* x, int x_dtype, int64_t m, int64_t k, i
  * reference stores the transpose, [k, n]).  sx: [m] fp32.  sw: [n] fp32 (the
  * unrounded per-channel scale, int8.py:140).  bias: [n] of out_dtype or NULL.
  * y: [m, n] of out_dtype.  algo as for the other GEMMs: SKINNY serves any m, TILE
- * needs k % 128 == 0 and 16-byte aligned rows (else the skinny kernel runs). */
+ * needs k % 128 == 0 and 16-byte aligned rows (else the skinny kernel runs).  AUTO
+ * takes SKINNY for m <= 16 and, on strip weights, up to m = 128 while
+ * ceil(m / 16) * n * k <= 24 MiB; TILE otherwise. */
 int qtts_w8a8_int8_gemm(const int8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx,
                         const int8_t* qw, int64_t n, int64_t ldqw, const float* sw,
                         const void* bias, void* y, int out_dtype, int64_t ldy,

@@ -228,19 +228,25 @@ def test_int8_gemm_half_strips(ops):
 @pytest.mark.parametrize("shape", TALKER + PREDICTOR)
 def test_int8_linear_full_shapes(ops, shape):
     """Whole Int8Method.apply at the talker / code predictor shapes, decode and prefill rows,
-    against torch on the GPU evaluating the reference's expressions."""
+    against torch on the GPU evaluating the reference's expressions.  From 17 to 128 rows the
+    automatic choice on strips is the skinny kernel where ceil(M / 16) * N * K <= 24 MiB and the
+    tile kernel elsewhere; both are checked against the other family too."""
     n, k = shape
     g = torch.Generator(device="cuda").manual_seed(n + k)
     w = (torch.randn(n, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
     qw, sw = ops.pack_int8(w, torch.float32)
     qs = ops.to_strips(qw)
     bias = (torch.randn(n, device="cuda", generator=g) * 0.1).to(torch.bfloat16)
-    for m in (1, 4, 8, 16, 17, 64, 256):
+    for m in (1, 4, 8, 16, 17, 64, 128, 256):
         x = _acts(m, k, torch.bfloat16, seed=m)
         q_t, s_t = _torch_act_int8(x)
         b = bias if m % 2 else None
         want = _np_bits(_torch_int8_out(q_t, s_t, qw, sw, b, torch.bfloat16))
         _assert_bits(ops.int8_linear_strips(x, qs, n, sw, b), want, f"strips n={n} k={k} m={m}")
+        if 17 <= m <= 128:
+            for fam in (1, 2):
+                _assert_bits(ops.int8_linear_strips(x, qs, n, sw, b, O.DIV_DEVICE, ops.algo_code(fam)), want,
+                             f"strips n={n} k={k} m={m} family={fam}")
         if m in (1, 64):
             _assert_bits(ops.int8_linear(x, qw, sw, b), want, f"rowmajor n={n} k={k} m={m}")
 

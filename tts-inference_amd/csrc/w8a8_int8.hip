@@ -11,13 +11,14 @@
 //    per 64-column chunk of K a lane loads 16 weight bytes and 16 activation bytes and
 //    issues one MFMA.  Waves split K and meet in LDS; workgroups may split K further
 //    and meet through the workspace (last arrival reduces).  blockIdx.y walks 16-row
-//    blocks, so it serves any M (the decode path for M <= 16, the fallback above).
+//    blocks, so it serves any M (the decode path for M <= 16; on strips, up to 128 rows
+//    while the row blocks times the weight stay within 24 MiB: skinny_rows_auto).
 //    SUB = 2 (strip weights, M <= 8, no split): half strips, two workgroups of 8 weight
 //    rows per strip, as skinny.h does for W8A16: A rows 0-7 hold chunk 2u and rows 8-15
 //    chunk 2u + 1 of those rows, B columns 0-7 and 8-15 the activation rows for the same
 //    two chunks, and the two diagonal 8 x 8 blocks of D are added at the end (in int32,
 //    exactly: the result is the whole-strip kernel's, bit for bit).
-//  * tile (M > 16, K % 128 == 0): pipe_w8a8.h, in tile_i8.hip / tile_i8_rows.hip.
+//  * tile (the other M > 16, K % 128 == 0): pipe_w8a8.h, in tile_i8.hip / tile_i8_rows.hip.
 //  * generic: any alignment and K; correctness path.
 //
 // Weights come row-major [N, K] or in the QTTS_STRIP_INT8 layout of layout.h (one
@@ -260,9 +261,21 @@ bool skinny_ok(int64_t k, int64_t ldqx, const int8_t* qx, int layout, int64_t ld
   return x_ok && (uintptr_t)qw % 16 == 0 && ldqw % 16 == 0;
 }
 
-int family_of(int64_t m, int algo) {
+// Up to 128 rows on strip weights the skinny kernel (one split, each 16-row block of
+// activations against every strip) beats the tile kernel while the row blocks times the
+// weight bytes stay within 24 MiB.  Measured (two launches with the quantization, warm
+// weights, µs): talker o_proj at M = 64 9.65 -> 7.84, down_proj at M = 32 12.03 -> 9.87,
+// qkv at M = 32 9.57 -> 7.77; predictor o_proj at M = 128 9.73 -> 7.92, down_proj at
+// M = 64 9.84 -> 7.77; 1.01-1.36x everywhere within the bound, 0.59-0.93x past it
+// (32 MiB and more).
+bool skinny_rows_auto(int64_t m, int64_t n, int64_t k) {
+  return m > 16 && m <= 128 && (m + 15) / 16 * n * k <= (24ll << 20);
+}
+
+int family_of(int64_t m, int64_t n, int64_t k, int layout, int algo) {
   const int f = algo & 0xff;
-  return f == QTTS_ALGO_AUTO ? (m <= 16 ? QTTS_ALGO_SKINNY : QTTS_ALGO_TILE) : f;
+  if (f != QTTS_ALGO_AUTO) return f;
+  return (m <= 16 || (layout == kLayoutStrips && skinny_rows_auto(m, n, k))) ? QTTS_ALGO_SKINNY : QTTS_ALGO_TILE;
 }
 
 template <typename OT>
@@ -270,7 +283,7 @@ int int8_launch_typed(const int8_t* qx, const float* sx, int64_t m, int64_t k, i
                       int64_t n, int64_t ldqw, int layout, const float* sw, const OT* bias, OT* y, int64_t ldy,
                       int algo, void* ws, int64_t ws_bytes, hipStream_t st) {
   constexpr int odt = std::is_same<OT, bf16_t>::value ? QTTS_BF16 : (std::is_same<OT, f16_t>::value ? QTTS_F16 : QTTS_F32);
-  const int family = family_of(m, algo);
+  const int family = family_of(m, n, k, layout, algo);
   const bool fast = skinny_ok(k, ldqx, qx, layout, ldqw, qw);
   if (layout == kLayoutStrips && !fast)
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
@@ -316,6 +329,12 @@ int int8_launch_typed(const int8_t* qx, const float* sx, int64_t m, int64_t k, i
   // Skinny kernel: the decode path, and the fallback for tile requests the pipeline
   // cannot take (K % 128 != 0); a forced tile request keeps only its split count.
   I8Cfg c = int8_skinny_cfg(m, n, k, family == QTTS_ALGO_SKINNY ? algo : (algo & 0xff00));
+  if ((algo & 0xff) == QTTS_ALGO_AUTO && (algo >> 8) == 0 && layout == kLayoutStrips && m > 8) {
+    // 9-128 rows on strips: one split; 8 waves while the grid has at most 256 workgroups,
+    // else 4 (the measured best of 4, 8 and 16 on every talker and predictor shape)
+    const int64_t wgs = (n + 15) / 16 * ((m + 15) / 16);
+    c = int8_skinny_cfg(m, n, k, QTTS_ALGO_SKINNY | (1 << 8) | ((wgs <= 256 ? 8 : 4) << 16));
+  }
   const int64_t need = int8_skinny_ws(c);
   if (need > ws_bytes || (need > 0 && !ws)) {
     if ((algo >> 8) & 0xff)
@@ -355,7 +374,7 @@ int int8_launch_typed(const int8_t* qx, const float* sx, int64_t m, int64_t k, i
 
 // Workspace of the largest automatic (or the requested) choice.
 int64_t qtts_int8_gemm_ws_bytes(int64_t m, int64_t n, int64_t k, int algo) {
-  const int family = family_of(m, algo);
+  const int family = family_of(m, n, k, kLayoutRowMajor, algo);  // the tile's workspace too, past 16 rows
   int64_t a = 0;
   if (family == QTTS_ALGO_SKINNY || (algo & 0xff) == QTTS_ALGO_AUTO || k % 128 != 0)
     a = int8_skinny_ws(int8_skinny_cfg(m, n, k, family == QTTS_ALGO_SKINNY ? algo : (algo & 0xff00)));
