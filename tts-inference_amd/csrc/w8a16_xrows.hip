@@ -24,6 +24,8 @@ void launch_mx(int mx, const void* x, int64_t m, int64_t k, int64_t ldx, const i
                int S, int cps, unsigned blocks, hipStream_t st) {
   if (mx == 1)
     launch_xrows<XT, ST, W, CPW, 1>(x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, strips, S, cps, blocks, st);
+  else if (mx == 2)
+    launch_xrows<XT, ST, W, CPW, 2>(x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, strips, S, cps, blocks, st);
   else if (mx == 4)
     launch_xrows<XT, ST, W, CPW, 4>(x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, strips, S, cps, blocks, st);
   else
@@ -59,7 +61,7 @@ int qtts_launch_w8a16_skinny_xrows(const void* x, int x_dtype, int64_t m, int64_
                                    int waves, int cpw, float* part, unsigned* counters, int strips, int S, int cps,
                                    unsigned blocks, hipStream_t st) {
   if (m < 1 || m > 8) return 1;
-  const int mx = m == 1 ? 1 : (m <= 4 ? 4 : 8);
+  const int mx = m <= 2 ? (int)m : (m <= 4 ? 4 : 8);
   int rc;
 #define QTTS_XR_ST(XT)                                                                                                \
   do {                                                                                                                \

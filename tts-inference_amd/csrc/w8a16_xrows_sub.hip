@@ -27,6 +27,7 @@ template <typename XT, typename ST, int SUB, int W, int CPW>
 void launch_sub_mx(int mx, const void* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qs, int64_t n,
                    const void* scale, const void* bias, void* y, int64_t ldy, unsigned blocks, hipStream_t st) {
   if (mx == 1) launch_sub<XT, ST, SUB, W, CPW, 1>(x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st);
+  else if (mx == 2) launch_sub<XT, ST, SUB, W, CPW, 2>(x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st);
   else if (mx == 4) launch_sub<XT, ST, SUB, W, CPW, 4>(x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st);
   else if constexpr (SUB == 2) launch_sub<XT, ST, SUB, W, CPW, 8>(x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st);
 }
@@ -67,7 +68,7 @@ int qtts_launch_w8a16_skinny_sub(const void* x, int x_dtype, int64_t m, int64_t 
                                  int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
                                  int sub, int waves, int cpw, unsigned blocks, hipStream_t st) {
   if (!skinny_sub_ok(m, k, sub)) return 1;
-  const int mx = m == 1 ? 1 : (m <= 4 ? 4 : 8);
+  const int mx = m <= 2 ? (int)m : (m <= 4 ? 4 : 8);
   int rc;
 #define QTTS_SUB_ST(XT)                                                                                          \
   do {                                                                                                           \
