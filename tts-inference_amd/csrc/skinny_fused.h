@@ -111,19 +111,23 @@ int launch_fused(int x_dtype, bool f32_scale, const FusedArgs& a) {
   }
 }
 
-// Residual-only variants (w8a16_fused_res.hip) for 1, 4 and 8 staged rows.
+// Residual-only variants (w8a16_fused_res.hip) for 1, 2, 4 and 8 staged rows.
 extern template int launch_fused<kProNone, true, 1>(int, bool, const FusedArgs&);
+extern template int launch_fused<kProNone, true, 2>(int, bool, const FusedArgs&);
 extern template int launch_fused<kProNone, true, 4>(int, bool, const FusedArgs&);
 extern template int launch_fused<kProNone, true, 8>(int, bool, const FusedArgs&);
-// RMSNorm prologue for 4 and 8 staged rows (w8a16_fused_norm.hip).
+// RMSNorm prologue for 2, 4 and 8 staged rows (w8a16_fused_norm.hip).
+extern template int launch_fused<kProRmsNorm, false, 2>(int, bool, const FusedArgs&);
 extern template int launch_fused<kProRmsNorm, false, 4>(int, bool, const FusedArgs&);
 extern template int launch_fused<kProRmsNorm, false, 8>(int, bool, const FusedArgs&);
 // SiLU-pair gate_up, with or without the RMSNorm prologue (w8a16_fused_pair.hip,
 // w8a16_fused_pair_norm.hip).
 extern template int launch_fused<kProNone, false, 1, true>(int, bool, const FusedArgs&);
+extern template int launch_fused<kProNone, false, 2, true>(int, bool, const FusedArgs&);
 extern template int launch_fused<kProNone, false, 4, true>(int, bool, const FusedArgs&);
 extern template int launch_fused<kProNone, false, 8, true>(int, bool, const FusedArgs&);
 extern template int launch_fused<kProRmsNorm, false, 1, true>(int, bool, const FusedArgs&);
+extern template int launch_fused<kProRmsNorm, false, 2, true>(int, bool, const FusedArgs&);
 extern template int launch_fused<kProRmsNorm, false, 4, true>(int, bool, const FusedArgs&);
 extern template int launch_fused<kProRmsNorm, false, 8, true>(int, bool, const FusedArgs&);
 

@@ -216,14 +216,16 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
     a.counters = nullptr;
     a.part = nullptr;
     const bool f32s = sdt == QTTS_F32;
-    const int mx = m == 1 ? 1 : (m <= 4 ? 4 : 8);
+    const int mx = m <= 2 ? (int)m : (m <= 4 ? 4 : 8);  // staged rows: the fewest built that cover m
     int rc;
     if (pro == kProRmsNorm)
       rc = mx == 1 ? launch_fused<kProRmsNorm, false, 1, true>(x_dtype, f32s, a)
+                   : mx == 2 ? launch_fused<kProRmsNorm, false, 2, true>(x_dtype, f32s, a)
                    : (mx == 4 ? launch_fused<kProRmsNorm, false, 4, true>(x_dtype, f32s, a)
                               : launch_fused<kProRmsNorm, false, 8, true>(x_dtype, f32s, a));
     else
       rc = mx == 1 ? launch_fused<kProNone, false, 1, true>(x_dtype, f32s, a)
+                   : mx == 2 ? launch_fused<kProNone, false, 2, true>(x_dtype, f32s, a)
                    : (mx == 4 ? launch_fused<kProNone, false, 4, true>(x_dtype, f32s, a)
                               : launch_fused<kProNone, false, 8, true>(x_dtype, f32s, a));
     if (rc != 0) return 1;
@@ -250,6 +252,7 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
                                      : launch_fused<kProSiluMul, false, 1>(x_dtype, f32s, a);
     else if (pro == kProNone && res)
       rc = m == 1 ? launch_fused<kProNone, true, 1>(x_dtype, f32s, a)
+                  : m == 2 ? launch_fused<kProNone, true, 2>(x_dtype, f32s, a)
                   : (m <= 4 ? launch_fused<kProNone, true, 4>(x_dtype, f32s, a)
                             : launch_fused<kProNone, true, 8>(x_dtype, f32s, a));
     if (rc != 0) return 1;
@@ -284,10 +287,12 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
                                    : launch_fused<kProSiluMul, false, 1>(x_dtype, f32s, a);
   else if (pro == kProRmsNorm && !res)
     rc = m == 1 ? launch_fused<kProRmsNorm, false, 1>(x_dtype, f32s, a)
+                : m == 2 ? launch_fused<kProRmsNorm, false, 2>(x_dtype, f32s, a)
                 : (m <= 4 ? launch_fused<kProRmsNorm, false, 4>(x_dtype, f32s, a)
                           : launch_fused<kProRmsNorm, false, 8>(x_dtype, f32s, a));
   else if (pro == kProNone && res)
     rc = m == 1 ? launch_fused<kProNone, true, 1>(x_dtype, f32s, a)
+                : m == 2 ? launch_fused<kProNone, true, 2>(x_dtype, f32s, a)
                 : (m <= 4 ? launch_fused<kProNone, true, 4>(x_dtype, f32s, a) : launch_fused<kProNone, true, 8>(x_dtype, f32s, a));
   if (rc != 0) return 1;
   return qtts_check_launch("w8a16_fused_skinny");

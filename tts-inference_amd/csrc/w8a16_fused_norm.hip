@@ -6,6 +6,7 @@
 
 namespace qtts {
 
+template int launch_fused<kProRmsNorm, false, 2>(int, bool, const FusedArgs&);
 template int launch_fused<kProRmsNorm, false, 4>(int, bool, const FusedArgs&);
 template int launch_fused<kProRmsNorm, false, 8>(int, bool, const FusedArgs&);
 

@@ -6,6 +6,7 @@
 namespace qtts {
 
 template int launch_fused<kProNone, false, 1, true>(int, bool, const FusedArgs&);
+template int launch_fused<kProNone, false, 2, true>(int, bool, const FusedArgs&);
 template int launch_fused<kProNone, false, 4, true>(int, bool, const FusedArgs&);
 template int launch_fused<kProNone, false, 8, true>(int, bool, const FusedArgs&);
 

@@ -6,6 +6,7 @@
 namespace qtts {
 
 template int launch_fused<kProRmsNorm, false, 1, true>(int, bool, const FusedArgs&);
+template int launch_fused<kProRmsNorm, false, 2, true>(int, bool, const FusedArgs&);
 template int launch_fused<kProRmsNorm, false, 4, true>(int, bool, const FusedArgs&);
 template int launch_fused<kProRmsNorm, false, 8, true>(int, bool, const FusedArgs&);
 

@@ -7,6 +7,7 @@
 namespace qtts {
 
 template int launch_fused<kProNone, true, 1>(int, bool, const FusedArgs&);
+template int launch_fused<kProNone, true, 2>(int, bool, const FusedArgs&);
 template int launch_fused<kProNone, true, 4>(int, bool, const FusedArgs&);
 template int launch_fused<kProNone, true, 8>(int, bool, const FusedArgs&);
 
