@@ -85,6 +85,7 @@ int launch_sub_rows(int mx, const SkinnyCfg& c, const void* x, int64_t m, int64_
                     hipStream_t st) {
   switch (mx) {
     case 1: return launch_sub_wc<XT, 1>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st);
+    case 2: return launch_sub_wc<XT, 2>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st);
     case 4: return launch_sub_wc<XT, 4>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st);
     default: return launch_sub_wc<XT, 8>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, blocks, st);
   }
@@ -97,6 +98,7 @@ int launch_rows(int mx, const SkinnyCfg& c, const void* x, int64_t m, int64_t k,
   switch (mx) {
     case 0: return launch_wc<XT, 0>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, blocks, st);
     case 1: return launch_wc<XT, 1>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, blocks, st);
+    case 2: return launch_wc<XT, 2>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, blocks, st);
     case 4: return launch_wc<XT, 4>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, blocks, st);
     default: return launch_wc<XT, 8>(c, x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters, blocks, st);
   }
@@ -144,7 +146,7 @@ int qtts_launch_fp8w(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
     const SkinnyCfg c = skinny_cfg_sub(n, k, 2, 0, 0);
     const int64_t blocks = ((int64_t)c.strips * 2 + 7) / 8 * 8;
     if (c.waves * c.cpw >= c.cps && blocks < ((int64_t)1 << 31)) {
-      const int mx = m == 1 ? 1 : (m <= 4 ? 4 : 8);
+      const int mx = m <= 2 ? (int)m : (m <= 4 ? 4 : 8);  // the fewest staged rows built that cover m
       const int rc = x_dtype == QTTS_BF16
                          ? launch_sub_rows<bf16_t>(mx, c, x, m, k, ldx, qs, n, scale, bias, y, ldy, (unsigned)blocks, st)
                          : launch_sub_rows<f16_t>(mx, c, x, m, k, ldx, qs, n, scale, bias, y, ldy, (unsigned)blocks, st);
@@ -173,7 +175,7 @@ int qtts_launch_fp8w(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8w: N or ldx too large");
   unsigned* counters = (unsigned*)ws;
   float* part = ws ? (float*)((char*)ws + kCounterBytes) : nullptr;
-  const int mx = staged ? (m == 1 ? 1 : (m <= 4 ? 4 : 8)) : 0;
+  const int mx = staged ? (m <= 2 ? (int)m : (m <= 4 ? 4 : 8)) : 0;
   const int rc = x_dtype == QTTS_BF16
                      ? launch_rows<bf16_t>(mx, c, x, m, k, ldx, qs, n, scale, bias, y, ldy, part, counters,
                                            (unsigned)blocks, st)
