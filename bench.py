@@ -627,7 +627,9 @@ def run_calibration(args, torch, ops):
     shapes: at every row bucket the callers produce, the fastest quantized route (skinny / tile
     kernel configuration, or the prefill route) against F.linear on the bf16 weight (hipBLASLt),
     each timed as 10 calls in a HIP graph (qtts/quant/calibrate.py:40-63), and the layer verdict
-    taken over the decode buckets."""
+    taken over the decode buckets.  A bucket where F.linear beat every quantized route is routed
+    to F.linear on the kept weight: its served speedup is 1.0 (``route: "F.linear"``), and
+    ``worst_served_speedup`` is the lowest over the buckets of converted layers as they run."""
     from qtts_amd.quant import calibrate
     from qtts_amd.quant.int8 import Int8WeightOnlyMethod, M_BUCKETS
     from qtts_amd.layers.linear import LinearBase
@@ -635,12 +637,14 @@ def run_calibration(args, torch, ops):
     method = Int8WeightOnlyMethod(calibrate=True, calibration_batch=16)
     shapes = [("talker_" + nm, n, k) for nm, n, k in TALKER] + [("predictor_" + nm, n, k) for nm, n, k in PREDICTOR]
     out = {}
-    worst = None
+    worst = worst_served = None
     for name, n, k in shapes:
         lin = LinearBase(k, n, dtype=torch.bfloat16, device="cuda")
         g = torch.Generator(device="cuda").manual_seed(n + k)
         lin.weight.data.copy_((torch.randn(n, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16))
         method.process_weights(lin)
+        converted = method.applies_to(lin)
+        algos = getattr(lin, "quant_algos", {})
         rep = method.calibration_report[(n, k)]
         rows = {}
         for b in M_BUCKETS:
@@ -650,15 +654,24 @@ def run_calibration(args, torch, ops):
                 continue
             t = r["timings"][r["best"]]
             ratio = r["reference"] / t
+            routed_ref = algos.get(b) == calibrate.ALGO_REFERENCE_GEMM
+            served = 1.0 if routed_ref or not converted else ratio
             rows[str(b)] = {"best": r["best"], "us": round(t * 1e6, 2), "bf16_us": round(r["reference"] * 1e6, 2),
-                            "speedup": round(ratio, 3)}
+                            "speedup": round(ratio, 3), "route": "F.linear" if routed_ref else r["best"],
+                            "served_speedup": round(served, 3)}
             if worst is None or ratio < worst[0]:
                 worst = (ratio, name, b)
-        out[name] = {"converted": method.applies_to(lin), "buckets": rows}
-        log(f"[bench] calibration {name}: " + ", ".join(f"{b}:{v['speedup'] if v else None}" for b, v in rows.items()))
+            if converted and (worst_served is None or served < worst_served[0]):
+                worst_served = (served, name, b)
+        out[name] = {"converted": converted, "kept_weight": converted and lin.weight.numel() > 0, "buckets": rows}
+        log(f"[bench] calibration {name}: " + ", ".join(
+            f"{b}:{v['speedup'] if v else None}{'->F.linear' if v and v['route'] == 'F.linear' else ''}"
+            for b, v in rows.items()))
     return {"probe": "calibration", "config": {"workload": "int8 weight-only per-bucket calibration, talker and "
                                                            "code-predictor shapes, buckets " + str(list(M_BUCKETS))},
             "worst_speedup": {"speedup": round(worst[0], 3), "shape": worst[1], "rows": worst[2]} if worst else None,
+            "worst_served_speedup": ({"speedup": round(worst_served[0], 3), "shape": worst_served[1],
+                                      "rows": worst_served[2]} if worst_served else None),
             "shapes": out}
 
 
@@ -688,14 +701,14 @@ def run_floor(args, torch, ops):
     steps = max(5, args.steps)
     out = {"empty_us_per_launch": {}, "stream_stack_us": {}}
     for wgs in (1, 128, 768):
-        g = capture(torch, lambda: [ops.probe_empty(wgs, 4) for _ in range(112)])
+        g = capture(torch, lambda: [probe_empty(torch, wgs, 4) for _ in range(112)])
         out["empty_us_per_launch"][str(wgs)] = round(time_graph(torch, g, steps, args.warmup) * 1e3 / 112, 3)
         del g
     shapes = [(1, 16), (2, 8), (2, 16), (4, 4), (4, 8), (4, 16), (8, 2), (8, 4), (8, 8), (16, 1), (16, 2), (16, 4)]
     per_kind = {}
     for waves, loads in shapes:
         key = f"w{waves}_l{loads}"
-        g = capture(torch, lambda: [ops.probe_stream(buf[o:o + b], b, waves, loads, sink) for _, o, b in offs])
+        g = capture(torch, lambda: [probe_stream(torch, buf[o:o + b], b, waves, loads, sink) for _, o, b in offs])
         t = time_graph(torch, g, steps, args.warmup)
         out["stream_stack_us"][key] = round(t * 1e3, 2)
         del g
@@ -703,7 +716,7 @@ def run_floor(args, torch, ops):
         # slices of o would be only 112 MiB, resident in the Infinity Cache after one replay)
         for name, b in sizes:
             mine = [(o, b) for o in range(0, buf.numel() - b + 1, b)]
-            g = capture(torch, lambda: [ops.probe_stream(buf[o:o + b], b, waves, loads, sink) for o, b in mine])
+            g = capture(torch, lambda: [probe_stream(torch, buf[o:o + b], b, waves, loads, sink) for o, b in mine])
             t_k = time_graph(torch, g, steps, args.warmup) * 1e3 / len(mine)
             del g
             per_kind.setdefault(name, {})[key] = round(t_k, 3)
@@ -711,7 +724,7 @@ def run_floor(args, torch, ops):
     best = {name: min(v.items(), key=lambda kv: kv[1]) for name, v in per_kind.items()}
     out["stream_best_shape"] = {name: kv[0] for name, kv in best.items()}
     plan = {name: tuple(int(t[1:]) for t in kv[0].split("_")) for name, kv in best.items()}
-    g = capture(torch, lambda: [ops.probe_stream(buf[o:o + b], b, *plan[n_], sink) for n_, o, b in offs])
+    g = capture(torch, lambda: [probe_stream(torch, buf[o:o + b], b, *plan[n_], sink) for n_, o, b in offs])
     out["stream_stack_best_us"] = round(time_graph(torch, g, steps, args.warmup) * 1e3, 2)
     del g, buf
     torch.cuda.empty_cache()
@@ -730,6 +743,55 @@ def run_floor(args, torch, ops):
     out["stream_best_GBps"] = round(nbytes / (out["stream_stack_best_us"] * 1e-6) / 1e9, 1)
     return {"probe": "floor", "config": {"workload": "configs[1] talker stack memory traffic (28 x 4 linears, "
                                                      "1.41 GB int8), streamed without arithmetic"}, **out}
+
+
+PROBE_LIB = os.path.join(ROOT, "tts-inference_amd", "probe", "libqtts_probe.so")
+_probe = None
+
+
+def probe_lib():
+    """The floor probes' own library (tts-inference_amd/probe/probe.hip), loaded once."""
+    global _probe
+    if _probe is None:
+        import ctypes
+        if not os.path.exists(PROBE_LIB):
+            raise RuntimeError(f"{PROBE_LIB} is not built (python tts-inference_amd/build.py --probe)")
+        lib = ctypes.CDLL(PROBE_LIB)
+        p, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+        lib.qtts_probe_stream.restype = i32
+        lib.qtts_probe_stream.argtypes = [p, i64, i32, i32, p, p]
+        lib.qtts_probe_empty.restype = i32
+        lib.qtts_probe_empty.argtypes = [i64, i32, p]
+        lib.qtts_probe_last_error.restype = ctypes.c_char_p
+        _probe = lib
+    return _probe
+
+
+def _probe_check(status: int, what: str) -> None:
+    if status != 0:
+        msg = probe_lib().qtts_probe_last_error().decode()
+        raise (ValueError if status == -1 else RuntimeError)(f"{what}: {msg}")
+
+
+def probe_stream(torch, src, nbytes: int, waves: int, loads: int, sink) -> None:
+    """Stream ``nbytes`` of ``src`` with the measurement kernel: ``waves`` waves a workgroup,
+    ``loads`` 1 KiB loads a wave issued before any is used; each wave stores the xor of what it
+    read to ``sink`` (int32, one word a wave)."""
+    if not (src.is_cuda and sink.is_cuda and src.is_contiguous() and sink.is_contiguous()):
+        raise ValueError("probe_stream takes contiguous device tensors")
+    if sink.dtype != torch.int32 or sink.numel() * loads * 1024 < nbytes:
+        raise ValueError("sink must be int32 with one word per wave")
+    if src.numel() * src.element_size() < nbytes:
+        raise ValueError("src is smaller than nbytes")
+    st = torch.cuda.current_stream(src.device).cuda_stream
+    _probe_check(probe_lib().qtts_probe_stream(src.data_ptr(), int(nbytes), int(waves), int(loads),
+                                               sink.data_ptr(), st), "probe_stream")
+
+
+def probe_empty(torch, workgroups: int, waves: int = 1) -> None:
+    """Launch an empty kernel of ``workgroups`` x ``waves`` waves on the current stream."""
+    _probe_check(probe_lib().qtts_probe_empty(int(workgroups), int(waves), torch.cuda.current_stream().cuda_stream),
+                 "probe_empty")
 
 
 def summarize_pmc(path: str) -> None:

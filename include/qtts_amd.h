@@ -411,19 +411,6 @@ int qtts_fp8w_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int6
 int qtts_kernel_timer_begin(int max_launches);
 int qtts_kernel_timer_end(double* total_ms, int64_t* launches, int64_t* untimed);
 
-/* Measurement kernels (bench.py --floor).  No counterpart in the reference: they bound
- * what one kernel per linear can reach on this GPU, for the roofline the decode GEMMs
- * are held to.
- * qtts_probe_stream reads `bytes` from src (16-byte aligned) the way the decode GEMMs
- * stream weights: workgroups of `waves` waves (1..16); wave w of workgroup b issues
- * `loads` (1, 2, 4, 8 or 16) 1 KiB loads, 16 bytes a lane, for blocks
- * (b * waves + w) * loads ... + loads - 1 before using any, and stores the xor of every
- * 32-bit word it read to sink[b * waves + w].  bytes must be a multiple of
- * waves * loads * 1024; sink holds bytes / (loads * 1024) words.
- * qtts_probe_empty launches an empty kernel of `workgroups` x `waves` waves. */
-int qtts_probe_stream(const void* src, int64_t bytes, int waves, int loads, int32_t* sink, void* stream);
-int qtts_probe_empty(int64_t workgroups, int waves, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

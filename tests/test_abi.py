@@ -141,21 +141,97 @@ def test_kernel_timer_argument_checks():
     assert L.qtts_kernel_timer_end(None, ctypes.byref(n), ctypes.byref(u)) == _lib.ERR_INVALID_ARGUMENT
 
 
-def test_probe_argument_checks():
-    """The measurement kernels reject bad shapes before any device use."""
-    L = _lib.load()
+def test_probe_library_is_separate():
+    """The floor probes live in their own library (bench.py --floor), not in libqtts_amd.so, and
+    reject bad shapes before any device use."""
+    L = ctypes.CDLL(_lib.LIB_PATH)
+    assert not hasattr(L, "qtts_probe_stream") and not hasattr(L, "qtts_probe_empty")
+    import bench
+    if not os.path.exists(bench.PROBE_LIB):
+        pytest.skip("libqtts_probe.so not built")
+    P = bench.probe_lib()
     src, sink = 1 << 20, 1 << 21  # aligned stand-in addresses: never dereferenced on a rejected call
-    assert L.qtts_probe_stream(None, 4096, 4, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
-    assert L.qtts_probe_stream(src + 8, 4096, 4, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
-    assert "aligned" in _lib.last_error()
-    assert L.qtts_probe_stream(src, 4096, 0, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
-    assert L.qtts_probe_stream(src, 4096, 17, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
-    assert L.qtts_probe_stream(src, 4096, 4, 3, sink, None) == _lib.ERR_INVALID_ARGUMENT
-    assert L.qtts_probe_stream(src, 4096 + 1024, 4, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
-    assert "multiple" in _lib.last_error()
-    assert L.qtts_probe_stream(src, 0, 4, 1, sink, None) == _lib.ERR_INVALID_ARGUMENT
-    assert L.qtts_probe_empty(0, 4, None) == _lib.ERR_INVALID_ARGUMENT
-    assert L.qtts_probe_empty(1, 17, None) == _lib.ERR_INVALID_ARGUMENT
+    assert P.qtts_probe_stream(None, 4096, 4, 1, sink, None) == -1
+    assert P.qtts_probe_stream(src + 8, 4096, 4, 1, sink, None) == -1
+    assert b"aligned" in P.qtts_probe_last_error()
+    assert P.qtts_probe_stream(src, 4096, 0, 1, sink, None) == -1
+    assert P.qtts_probe_stream(src, 4096, 17, 1, sink, None) == -1
+    assert P.qtts_probe_stream(src, 4096, 4, 3, sink, None) == -1
+    assert P.qtts_probe_stream(src, 4096 + 1024, 4, 1, sink, None) == -1
+    assert b"multiple" in P.qtts_probe_last_error()
+    assert P.qtts_probe_stream(src, 0, 4, 1, sink, None) == -1
+    assert P.qtts_probe_empty(0, 4, None) == -1
+    assert P.qtts_probe_empty(1, 17, None) == -1
+
+
+def _no_gpu():
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("calls that pass validation would launch on stand-in addresses")
+
+
+def _alias_calls(L, x, ldx, y, ldy, m=4, k=64, n=64):
+    """Every entry point whose kernels read the activations while others write the output, called
+    with x at ``x`` (row stride ldx) and the output at ``y`` (row stride ldy), bf16, stand-in
+    addresses for everything else (16-byte aligned, never dereferenced)."""
+    q, s, ws, nw = 1 << 30, 1 << 31, 1 << 32, 1 << 33
+    BF = _lib.BF16
+    return {
+        "w8a16_gemm": L.qtts_w8a16_gemm(x, BF, m, k, ldx, q, n, k, s, BF, None, y, ldy, 0, ws, 1 << 20, None),
+        "w8a16_gemm_strips": L.qtts_w8a16_gemm_strips(x, BF, m, k, ldx, q, n, s, BF, None, y, ldy, 0, ws, 1 << 20,
+                                                      None),
+        "fp8w_gemm_strips": L.qtts_fp8w_gemm_strips(x, BF, m, k, ldx, q, n, s, None, y, ldy, 0, ws, 1 << 20, None),
+        "w8a16_fused_gemm_strips": L.qtts_w8a16_fused_gemm_strips(x, BF, m, k, ldx, _lib.PRO_RMS_NORM, nw, 1e-6, q,
+                                                                  n, s, BF, None, None, 0, y, ldy, 0, ws, 1 << 20,
+                                                                  None),
+        "w8a16_gate_up_silu_strips": L.qtts_w8a16_gate_up_silu_strips(x, BF, m, k, ldx, _lib.PRO_NONE, None, 1e-6,
+                                                                      q, 2 * n, s, BF, None, y, ldy, 0, ws, 1 << 20,
+                                                                      None),
+        "w8a16_silu_mul_gemm_strips": L.qtts_w8a16_silu_mul_gemm_strips(x, BF, m, k // 2, ldx, q, n, s, BF, None,
+                                                                        y, ldy, 0, ws, 1 << 20, None),
+        "fp8_linear_strips": L.qtts_fp8_linear_strips(x, BF, m, k, ldx, q, n, s, None, y, ldy, 0, 0, ws, 1 << 20,
+                                                      None),
+        "int8_linear_strips": L.qtts_int8_linear_strips(x, BF, m, k, ldx, q, n, s, None, y, ldy, 0, 0, ws, 1 << 20,
+                                                        None),
+    }
+
+
+def test_output_overlapping_activations_is_rejected():
+    """y sharing bytes with x races (every workgroup reads all x rows of its K range while others
+    write y): each entry point rejects it before any device use, the W8A16 family included."""
+    L = _lib.load()
+    x = 1 << 24
+    for y, ldy in ((x, 64), (x + 64, 64), (x + 3 * 128 + 32, 64)):   # the same rows; a shifted span
+        for name, st in _alias_calls(L, x, 64, y, ldy).items():
+            assert st == _lib.ERR_INVALID_ARGUMENT, (name, y - x, st)
+            assert "overlaps" in _lib.last_error(), (name, _lib.last_error())
+    # x's and y's row blocks of one buffer that share bytes in the first row; and y on another
+    # row stride whose second row lands on x's second row
+    for y, ldy in ((x + 100, 256), (x + 128, 192)):
+        for name, st in _alias_calls(L, x, 256, y, ldy).items():
+            assert st == _lib.ERR_INVALID_ARGUMENT and "overlaps" in _lib.last_error(), (name, y - x, ldy)
+    # the residual may be y itself, but x may not
+    st = L.qtts_w8a16_fused_gemm_strips(x, _lib.BF16, 4, 64, 64, _lib.PRO_NONE, None, 1e-6, 1 << 30, 64, 1 << 31,
+                                        _lib.BF16, None, x, 64, x, 64, 0, 1 << 32, 1 << 20, None)
+    assert st == _lib.ERR_INVALID_ARGUMENT and "overlaps x" in _lib.last_error()
+
+
+def test_interleaved_column_blocks_pass_validation():
+    """x = buf[:, :k] and y = buf[:, k:k + n] of one buffer interleave their rows without sharing a
+    byte: the overlap check lets them through (F.linear accepts that layout), so the call reaches
+    the device check, which fails here with no GPU."""
+    _no_gpu()
+    L = _lib.load()
+    base = 1 << 24
+    # bf16 rows of 256 elements: x columns [0, 64), y columns [64, 128) (128 bytes in)
+    for name, st in _alias_calls(L, base, 256, base + 128, 256).items():
+        assert st == _lib.ERR_UNSUPPORTED, (name, st, _lib.last_error())
+    # y's block before x's in each row; and y on another row stride (256 bytes against x's 512)
+    # whose rows fall in the gaps between x's
+    for name, st in _alias_calls(L, base + 256, 256, base, 256).items():
+        assert st == _lib.ERR_UNSUPPORTED, (name, st, _lib.last_error())
+    for name, st in _alias_calls(L, base, 256, base + 128, 128).items():
+        assert st == _lib.ERR_UNSUPPORTED, (name, st, _lib.last_error())
 
 
 def test_size_queries_reject_sizes_past_2_31():

@@ -7,6 +7,7 @@ from __future__ import annotations
 
 import pytest
 import torch
+import torch.nn.functional as F
 from torch import nn
 
 from test_gpu_gemm import assert_close
@@ -57,16 +58,18 @@ def test_int8_weight_only_hook(calibrate):
                                 calibration_batch=8)
     r = report["talker"]
     assert r["excluded"] == 1 and r["converted"] + r["declined"] == 5
+    from qtts_amd.quant.calibrate import ALGO_REFERENCE_GEMM
+    from qtts_amd.quant.int8 import layer_algo
     if not calibrate:
-        assert r["converted"] == 5 and r["bytes_after"] < r["bytes_before"]
+        assert r["converted"] == 5 and r["bytes_after"] < r["bytes_before"] and r["kept_weight"] == 0
     else:
         # calibrated per row bucket: every converted layer's shape has a kernel choice for every
         # bucket the callers produce (decode rows, code-predictor rows up to 128, prefill)
-        from qtts_amd.quant.int8 import M_BUCKETS, _ALGO
+        from qtts_amd.quant.int8 import M_BUCKETS
         for name in ("qkv_proj", "o_proj", "gate_up_proj", "down_proj", "text_proj_fc1"):
             layer = getattr(model, name)
             if layer.quant_method is not None:
-                assert all((layer.out_features, layer.in_features, b) in _ALGO for b in M_BUCKETS), name
+                assert sorted(layer.quant_algos) == list(M_BUCKETS), name
     assert model.codec_head.quant_method is None and model.codec_head.weight.numel() > 0
     ms = (1, 2, 3, 4, 8, 16, 17, 32, 48, 64, 100, 128) if calibrate else (1, 4, 8, 17)
     for m in ms:
@@ -78,6 +81,9 @@ def test_int8_weight_only_hook(calibrate):
             xin = x if layer.in_features == 2048 else torch.randn(m, 1, layer.in_features, device="cuda").to(x.dtype)
             y = layer(xin)
             assert y.shape == (m, 1, layer.out_features) and y.dtype == torch.bfloat16
+            if layer_algo(layer, m) == ALGO_REFERENCE_GEMM:  # F.linear beat every kernel at this bucket
+                assert torch.equal(y, F.linear(xin, layer.weight, layer.bias)), f"{name} m={m}"
+                continue
             assert_close(y.reshape(m, -1), _expected_int8(layer, xin.reshape(m, -1)), f"{name} m={m}")
 
 

@@ -92,9 +92,7 @@ def test_int8_route_bits_and_bound(ops, monkeypatch):
     method.process_weights(lin)
     lin.quant_method = method
     prefill.reserve(torch.device("cuda"), n, k, torch.bfloat16)
-    monkeypatch.setattr(I, "_ALGO", {})  # no choice left by another test's calibration of this shape
-    monkeypatch.setitem(I._ALGO, (n, k, 1024), prefill.ALGO_DEQUANT_GEMM)
-    monkeypatch.setitem(I._ALGO, (n, k, 2048), prefill.ALGO_DEQUANT_GEMM)
+    lin.quant_algos = {1024: prefill.ALGO_DEQUANT_GEMM, 2048: prefill.ALGO_DEQUANT_GEMM}
     wq = ops.dequant_strips(lin.int8_weight, n, k, lin.int8_scale, torch.bfloat16)
     q = I.int8_weight_rowmajor(lin)
     assert torch.equal(wq, q.to(torch.bfloat16) * lin.int8_scale[:, None])
@@ -128,10 +126,9 @@ def test_route_graph_replays_and_gated_mlp(ops, monkeypatch):
         lin.quant_method = method
         prefill.reserve(torch.device("cuda"), lin.out_features, lin.in_features, torch.bfloat16)
     x = torch.randn(512, 2048, device="cuda").to(torch.bfloat16)
-    monkeypatch.setattr(I, "_ALGO", {})  # no choice left by another test's calibration of these shapes
     kernels = mlp(x)  # the HIP tile kernels
-    monkeypatch.setitem(I._ALGO, (12288, 2048, 1024), prefill.ALGO_DEQUANT_GEMM)
-    monkeypatch.setitem(I._ALGO, (2048, 6144, 1024), prefill.ALGO_DEQUANT_GEMM)
+    mlp.gate_up_proj.quant_algos = {1024: prefill.ALGO_DEQUANT_GEMM}
+    mlp.down_proj.quant_algos = {1024: prefill.ALGO_DEQUANT_GEMM}
     routed = mlp(x)
     assert torch.equal(routed, mlp.down_proj(ops.silu_mul(mlp.gate_up_proj(x))))  # both GEMMs on the route
     # against the HIP tile kernels: two GEMMs, each within the bar, and the rounded activation between
@@ -156,33 +153,76 @@ def test_route_graph_replays_and_gated_mlp(ops, monkeypatch):
 
 
 def test_calibration_records_prefill_verdicts(ops):
-    """Both weight-only methods with calibration: every bucket decided, the prefill route kept exactly
-    where it was the fastest candidate at a prefill bucket, and the layer's output at those row
-    counts within the W8A16 bound of the HIP kernel on the same codes, whichever route was kept."""
+    """Both weight-only methods with calibration: every bucket decided; F.linear on the kept weight
+    exactly where it beat every quantized route, else the prefill route exactly where it was the
+    fastest candidate; the layer's output at the prefill row counts is F.linear of the original
+    weight bit for bit on the F.linear route, and otherwise within the W8A16 bound of the HIP kernel
+    on the same codes."""
     from qtts_amd.quant import fp8 as P, int8 as I, prefill
-    from qtts_amd.quant.calibrate import clear_cache
+    from qtts_amd.quant.calibrate import ALGO_REFERENCE_GEMM, clear_cache
     clear_cache()
     n, k = 12288, 2048
-    for method, table, kernel in (
-            (I.Int8WeightOnlyMethod(calibrate=True), I._ALGO,
+    for method, kernel in (
+            (I.Int8WeightOnlyMethod(calibrate=True),
              lambda lin, x: ops.w8a16_gemm_strips(x, lin.int8_weight, n, lin.int8_scale)),
-            (P.Fp8WeightOnlyMethod(calibrate=True), P._FP8W_ALGO,
+            (P.Fp8WeightOnlyMethod(calibrate=True),
              lambda lin, x: ops.fp8w_gemm_strips(x, lin.fp8w_weight, n, lin.fp8w_scale))):
-        for rows in method.calibration_rows:
-            table.pop((n, k, rows), None)  # a verdict left by an earlier test of this shape
         lin = _layer(n, k, seed=3, bias=False)
+        w_bf16 = lin.weight.detach().clone()
         method.process_weights(lin)
         report = method.calibration_report[(n, k)]
         assert sorted(report) == list(method.calibration_rows)
         if not method.applies_to(lin):
             continue  # declined over the decode buckets: stays on F.linear
         lin.quant_method = method
-        assert all((n, k, rows) in table for rows in method.calibration_rows), "every bucket decided"
+        table = lin.quant_algos
+        assert sorted(table) == list(method.calibration_rows), "every bucket decided"
+        loses = {rows for rows in method.calibration_rows
+                 if report[rows]["timings"][report[rows]["best"]] > report[rows]["reference"]}
+        assert {r for r, a in table.items() if a == ALGO_REFERENCE_GEMM} == loses, method.name
+        assert (lin.weight.numel() > 0) == bool(loses), "the weight stays exactly when F.linear serves a bucket"
         for rows in prefill.PREFILL_BUCKETS:
-            routed = table[(n, k, rows)] == prefill.ALGO_DEQUANT_GEMM
-            assert routed == (report[rows]["best"] == "dequant"), (method.name, rows)
             x = torch.randn(rows, k, device="cuda").to(torch.bfloat16)
             y = lin(x)
+            if rows in loses:
+                assert torch.equal(y, F.linear(x, w_bf16)), (method.name, rows)
+                continue
+            routed = table[rows] == prefill.ALGO_DEQUANT_GEMM
+            assert routed == (report[rows]["best"] == "dequant"), (method.name, rows)
             ref = kernel(lin, x).double().cpu().numpy()
             err = np.abs(y.double().cpu().numpy() - ref)
             assert (err <= 2 * _bound(ref, torch.bfloat16)).all(), (method.name, rows, routed, float(err.max()))
+
+
+def test_reference_route_keeps_weight_and_calls_f_linear(ops, monkeypatch):
+    """Calibration where F.linear wins the 256-row bucket (timings forced on the host): the layer
+    converts on its decode buckets, keeps its weight, reports it, and its 256-row calls are
+    F.linear of that weight bit for bit while decode calls stay on the HIP kernel."""
+    from qtts_amd import QuantConfig, quantize_module
+    from qtts_amd.quant import calibrate as cal, int8 as I
+
+    def fake_times(candidates, reference_call, *, key, use_graph=True, timer=None):
+        rows = key[3]
+        return 1.0, {name: (2.0 if rows == 256 else 0.5) for name in candidates}
+
+    monkeypatch.setattr(cal, "time_candidates", fake_times)
+    n, k = 2048, 2048
+    lin = _layer(n, k, seed=4, bias=True)
+    w_bf16 = lin.weight.detach().clone()
+    model = torch.nn.Module()
+    model.o_proj = lin
+    method = I.Int8WeightOnlyMethod(calibrate=True, calibration_rows=(1, 8, 256))
+    report = quantize_module(model, method, QuantConfig(method="int8_weight_only"), "talker")
+    assert report["converted"] == 1 and report["kept_weight"] == 1 and method.kept_reference == 1
+    assert lin.quant_algos[256] == cal.ALGO_REFERENCE_GEMM and lin.quant_algos[1] >= 0
+    assert torch.equal(lin.weight, w_bf16)
+    x = torch.randn(256, k, device="cuda").to(torch.bfloat16)
+    assert torch.equal(lin(x), F.linear(x, w_bf16, lin.bias))
+    x1 = torch.randn(1, k, device="cuda").to(torch.bfloat16)
+    assert torch.equal(lin(x1), ops.w8a16_gemm_strips(x1, lin.int8_weight, n, lin.int8_scale, lin.bias,
+                                                      lin.quant_algos[1]))
+    # without keep_reference_routes the bucket keeps its fastest quantized route and the weight goes
+    lin2 = _layer(n, k, seed=4, bias=True)
+    method2 = I.Int8WeightOnlyMethod(calibrate=True, calibration_rows=(1, 8, 256), keep_reference_routes=False)
+    method2.process_weights(lin2)
+    assert lin2.quant_algos[256] >= 0 and lin2.weight.numel() == 0

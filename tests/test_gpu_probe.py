@@ -1,6 +1,6 @@
-"""The measurement kernels behind ``bench.py --floor``: the streaming probe reads every byte
-of its slice exactly once, in the blocks the header promises (each wave's xor against numpy),
-and the empty kernel runs."""
+"""The measurement kernels behind ``bench.py --floor`` (their own library, probe/probe.hip):
+the streaming probe reads every byte of its slice exactly once, in the blocks its comment
+promises (each wave's xor against numpy), and the empty kernel runs."""
 
 from __future__ import annotations
 
@@ -11,11 +11,25 @@ import torch
 pytestmark = pytest.mark.gpu
 
 
+class _Probes:
+    """bench.py's wrappers of the probe library, bound to torch."""
+
+    def __init__(self):
+        import bench
+        self.bench = bench
+
+    def probe_stream(self, src, nbytes, waves, loads, sink):
+        self.bench.probe_stream(torch, src, nbytes, waves, loads, sink)
+
+    def probe_empty(self, workgroups, waves=1):
+        self.bench.probe_empty(torch, workgroups, waves)
+
+
 @pytest.fixture(scope="module")
 def ops():
     from qtts_amd import ops as _ops
     assert _ops.device_supported(), "GPU is not a gfx950"
-    return _ops
+    return _Probes()
 
 
 @pytest.mark.parametrize("waves,loads", [(1, 1), (4, 8), (16, 2), (2, 16), (8, 4)])
@@ -55,3 +69,6 @@ def test_probe_wrapper_checks(ops):
         ops.probe_stream(src, 8192, 4, 1, torch.zeros(8, dtype=torch.int32, device="cuda"))
     with pytest.raises(ValueError):
         ops.probe_stream(src, 4096, 4, 1, torch.zeros(2, dtype=torch.int32, device="cuda"))
+    with pytest.raises(ValueError):  # a strided view would be read past its storage
+        ops.probe_stream(torch.zeros(4096, 2, dtype=torch.int8, device="cuda")[:, 0], 4096, 4, 1,
+                         torch.zeros(8, dtype=torch.int32, device="cuda"))

@@ -266,3 +266,52 @@ def test_calibrate_buckets_failures_are_never_fatal():
     accept, table, _ = calibrate.calibrate_buckets("g", 8, 8, torch.float32, torch.device("cpu"), (1, 4, 256), 16,
                                                    candidates, kernel, reference, timer=timer)
     assert accept and sorted(table) == [1, 4]   # a prefill bucket that cannot be timed stays automatic
+
+
+def test_calibrate_buckets_routes_losing_buckets_to_reference():
+    """A converted layer that loses to F.linear at some bucket: with keep_reference that bucket
+    goes to F.linear on the kept weight (no bucket slower than the layer it replaced); without,
+    it keeps its fastest quantized route.  The layer verdict is unchanged."""
+    calibrate.clear_cache()
+
+    def times(label):
+        kind, algo, rows = label
+        if kind == "ref":
+            return 10.0
+        return {16: 12.0, 256: 20.0}.get(rows, 5.0)
+
+    kernel, reference, timer, candidates, _ = _bucket_fixture(times)
+    buckets = (1, 2, 16, 64, 256)
+    accept, table, report = calibrate.calibrate_buckets("r1", 8, 8, torch.float32, torch.device("cpu"), buckets, 16,
+                                                        candidates, kernel, reference, timer=timer,
+                                                        keep_reference=True)
+    assert accept   # decode rows: (5 + 5 + 12) * 1.05 < 30
+    assert table[16] == calibrate.ALGO_REFERENCE_GEMM and table[256] == calibrate.ALGO_REFERENCE_GEMM
+    assert table[1] >= 0 and table[2] >= 0 and table[64] >= 0
+    calibrate.clear_cache()
+    accept, table, _ = calibrate.calibrate_buckets("r1", 8, 8, torch.float32, torch.device("cpu"), buckets, 16,
+                                                   candidates, kernel, reference, timer=timer)
+    assert accept and all(a >= 0 for a in table.values())
+    assert table[256] == 2   # the tile kernel, the only candidate past 64 rows
+
+
+def test_reference_route_dispatch():
+    """The weight-only method's per-layer table: a bucket routed to F.linear computes F.linear on the
+    layer's weight exactly; routes_to_kernel and the fused activation entry say so; another
+    layer's table (same shape) is not consulted."""
+    from qtts_amd.quant.int8 import Int8WeightOnlyMethod, layer_algo
+    from qtts_amd import _lib
+    method = object.__new__(Int8WeightOnlyMethod)   # no GPU here: only the host-side routing runs
+    lin = _init(LinearBase(8, 4, bias=True, dtype=torch.bfloat16))
+    lin.int8_layout = "strips"
+    lin.quant_algos = {1: calibrate.ALGO_REFERENCE_GEMM, 256: calibrate.ALGO_REFERENCE_GEMM, 2: 1}
+    other = _init(LinearBase(8, 4, bias=True, dtype=torch.bfloat16))
+    other.quant_algos = {}
+    x = torch.randn(1, 8).to(torch.bfloat16)
+    assert torch.equal(method.apply(lin, x, lin.bias), F.linear(x, lin.weight, lin.bias))
+    x200 = torch.randn(200, 8).to(torch.bfloat16)
+    assert torch.equal(method.apply(lin, x200, lin.bias), F.linear(x200, lin.weight, lin.bias))
+    assert layer_algo(lin, 200) == calibrate.ALGO_REFERENCE_GEMM and layer_algo(lin, 2) == 1
+    assert layer_algo(other, 1) == _lib.ALGO_AUTO
+    assert not method.routes_to_kernel(lin, x) and method.routes_to_kernel(lin, torch.randn(2, 8))
+    assert method.apply_gate_up_silu(lin, x, None) is None   # the plain path then calls apply

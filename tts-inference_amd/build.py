@@ -3,6 +3,7 @@
     python tts-inference_amd/build.py            # build
     python tts-inference_amd/build.py --verbose  # echo the hipcc lines
     python tts-inference_amd/build.py --sanitize # libqtts_amd_san.so: host code under ASan + UBSan
+    python tts-inference_amd/build.py --probe    # probe/libqtts_probe.so: bench.py --floor's kernels
 
 Each csrc/*.hip compiles to an object under _build/ (parallel), then one link
 produces qtts_amd/libqtts_amd.so next to the Python package that loads it.
@@ -98,6 +99,20 @@ def build(verbose: bool = False, sanitize: bool = False) -> str:
     return out
 
 
+PROBE_SRC = os.path.join(HERE, "probe", "probe.hip")
+PROBE_OUT = os.path.join(HERE, "probe", "libqtts_probe.so")
+
+
+def build_probe(verbose: bool = False) -> str:
+    """libqtts_probe.so: bench.py --floor's measurement kernels (probe/probe.hip), a library of
+    their own so that nothing but the quantized linear is in libqtts_amd.so."""
+    cc = hipcc()
+    tmp = PROBE_OUT + ".tmp"
+    _run([cc, *HIPCC_FLAGS, "-shared", "-Wl,-z,defs", PROBE_SRC, "-o", tmp], verbose)
+    os.replace(tmp, PROBE_OUT)
+    return PROBE_OUT
+
+
 def sanitized_stale() -> bool:
     """True when libqtts_amd_san.so is missing or older than a source it is built from."""
     if not os.path.exists(SAN_OUT):
@@ -108,4 +123,7 @@ def sanitized_stale() -> bool:
 
 
 if __name__ == "__main__":
-    print(build(verbose="--verbose" in sys.argv, sanitize="--sanitize" in sys.argv))
+    if "--probe" in sys.argv:
+        print(build_probe(verbose="--verbose" in sys.argv))
+    else:
+        print(build(verbose="--verbose" in sys.argv, sanitize="--sanitize" in sys.argv))

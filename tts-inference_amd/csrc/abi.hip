@@ -154,14 +154,31 @@ bool ranges_overlap(const void* a, int64_t rows_a, int64_t lda, const void* b, i
   return a0 < b1 && b0 < a1;
 }
 
-// Whether an [rows_a, cols_a] matrix at a (row stride lda) and an [rows_b, cols_b] matrix
-// at b (row stride ldb), elements of esz bytes, share any byte of their spans.
-bool spans_overlap(const void* a, int64_t rows_a, int64_t lda, int64_t cols_a, const void* b, int64_t rows_b,
-                   int64_t ldb, int64_t cols_b, int64_t esz) {
+// Floor division for a positive divisor.
+int64_t floor_div(int64_t a, int64_t d) { return a >= 0 ? a / d : -((-a + d - 1) / d); }
+
+// Whether an [rows_a, cols_a] matrix at a (row stride lda, elements of esz_a bytes) and an
+// [rows_b, cols_b] matrix at b (row stride ldb, elements of esz_b bytes) share a byte.  Row by
+// row: two column blocks of one buffer whose rows interleave (x = buf[:, :k], y = buf[:, k:])
+// share none.  Row i of a covers [a + i * La, a + i * La + Ca) (La = lda * esz_a, Ca = cols_a *
+// esz_a), likewise for b; for each row i of a, the rows j of b that meet it satisfy
+// j * Lb in (a + i * La - b - Cb, a + i * La - b + Ca).  The loop runs over a's rows once the
+// whole spans are known to intersect; more than 2^22 rows are taken to overlap.
+bool spans_overlap(const void* a, int64_t rows_a, int64_t lda, int64_t cols_a, int64_t esz_a, const void* b,
+                   int64_t rows_b, int64_t ldb, int64_t cols_b, int64_t esz_b) {
   if (rows_a <= 0 || cols_a <= 0 || rows_b <= 0 || cols_b <= 0) return false;
-  const uintptr_t a0 = (uintptr_t)a, a1 = a0 + (uintptr_t)(((rows_a - 1) * lda + cols_a) * esz);
-  const uintptr_t b0 = (uintptr_t)b, b1 = b0 + (uintptr_t)(((rows_b - 1) * ldb + cols_b) * esz);
-  return a0 < b1 && b0 < a1;
+  const int64_t La = lda * esz_a, Ca = cols_a * esz_a, Lb = ldb * esz_b, Cb = cols_b * esz_b;
+  const uintptr_t a0 = (uintptr_t)a, a1 = a0 + (uintptr_t)((rows_a - 1) * La + Ca);
+  const uintptr_t b0 = (uintptr_t)b, b1 = b0 + (uintptr_t)((rows_b - 1) * Lb + Cb);
+  if (!(a0 < b1 && b0 < a1)) return false;
+  if (rows_a > (1 << 22) || La <= 0 || Lb <= 0) return true;
+  const int64_t d = (int64_t)(a0 - b0);  // a - b, bytes (the spans intersect, so this is small)
+  for (int64_t i = 0; i < rows_a; ++i) {
+    const int64_t lo = d + i * La - Cb, hi = d + i * La + Ca;  // open interval for j * Lb
+    const int64_t j0 = std::max<int64_t>(floor_div(lo, Lb) + 1, 0);
+    if (j0 < rows_b && j0 * Lb < hi) return true;
+  }
+  return false;
 }
 
 // Workspace of the one-call linears: the GEMM's own part (its split-K counter block
@@ -273,6 +290,9 @@ int qtts_w8a16_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
   QTTS_REQUIRE(ws_bytes >= 0, "w8a16_gemm: negative workspace size");
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(scale && y && (k == 0 || (x && q)), "w8a16_gemm: null pointer");
+  // Every workgroup reads all x rows of its K range while others write y.
+  QTTS_REQUIRE(!spans_overlap(x, m, ldx, k, dtype_size(x_dtype), y, m, ldy, n, dtype_size(x_dtype)),
+               "w8a16_gemm: y overlaps x");
   QTTS_TRY(current_device_check());
   return qtts_launch_w8a16(x, x_dtype, m, k, ldx, q, n, ldq, qtts::kLayoutRowMajor, scale, scale_dtype, bias, y, ldy,
                            algo, ws, ws_bytes, (hipStream_t)stream);
@@ -290,6 +310,8 @@ int qtts_w8a16_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int
   QTTS_REQUIRE(ws_bytes >= 0, "w8a16_gemm_strips: negative workspace size");
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(scale && y && x && qs, "w8a16_gemm_strips: null pointer");
+  QTTS_REQUIRE(!spans_overlap(x, m, ldx, k, dtype_size(x_dtype), y, m, ldy, n, dtype_size(x_dtype)),
+               "w8a16_gemm_strips: y overlaps x");
   QTTS_TRY(current_device_check());
   return qtts_launch_w8a16(x, x_dtype, m, k, ldx, qs, n, 0, qtts::kLayoutStrips, scale, scale_dtype, bias, y, ldy,
                            algo, ws, ws_bytes, (hipStream_t)stream);
@@ -319,6 +341,7 @@ int qtts_w8a8_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t k,
   QTTS_REQUIRE(ws_bytes >= 0, "w8a8_fp8_gemm: negative workspace size");
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(sx && sw && y && (k == 0 || (qx && qw)), "w8a8_fp8_gemm: null pointer");
+  QTTS_REQUIRE(!spans_overlap(qx, m, ldqx, k, 1, y, m, ldy, n, dtype_size(out_dtype)), "w8a8_fp8_gemm: y overlaps qx");
   QTTS_TRY(current_device_check());
   return qtts_launch_fp8_gemm(qx, sx, m, k, ldqx, qw, n, ldqw, qtts::kLayoutRowMajor, sw, bias, y, out_dtype, ldy,
                               algo, ws, ws_bytes, (hipStream_t)stream);
@@ -335,6 +358,8 @@ int qtts_w8a8_fp8_gemm_strips(const uint8_t* qx, const float* sx, int64_t m, int
   QTTS_REQUIRE(ws_bytes >= 0, "w8a8_fp8_gemm_strips: negative workspace size");
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(qx && sx && qws && sw && y, "w8a8_fp8_gemm_strips: null pointer");
+  QTTS_REQUIRE(!spans_overlap(qx, m, ldqx, k, 1, y, m, ldy, n, dtype_size(out_dtype)),
+               "w8a8_fp8_gemm_strips: y overlaps qx");
   QTTS_TRY(current_device_check());
   return qtts_launch_fp8_gemm(qx, sx, m, k, ldqx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y, out_dtype, ldy, algo,
                               ws, ws_bytes, (hipStream_t)stream);
@@ -354,7 +379,8 @@ static int fp8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, int
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(sw && y && (k == 0 || (x && qw)), "fp8_linear: null pointer");
   // The decode kernel has every workgroup read all of x while others write y.
-  QTTS_REQUIRE(!spans_overlap(x, m, ldx, k, y, m, ldy, n, dtype_size(x_dtype)), "fp8_linear: y overlaps x");
+  QTTS_REQUIRE(!spans_overlap(x, m, ldx, k, dtype_size(x_dtype), y, m, ldy, n, dtype_size(x_dtype)),
+               "fp8_linear: y overlaps x");
   // Decode rows on strip weights: quantization fused into the GEMM, one kernel, no
   // workspace.  A wave count alone (family SKINNY or AUTO, no split count or chunk
   // count) sets the fused kernel's waves; an explicit split count keeps the two-kernel path.
@@ -489,6 +515,7 @@ static int int8_gemm_impl(const char* what, const int8_t* qx, const float* sx, i
   QTTS_REQUIRE(ws_bytes >= 0, "%s: negative workspace size", what);
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(sx && sw && y && (k == 0 || (qx && qw)), "%s: null pointer", what);
+  QTTS_REQUIRE(!spans_overlap(qx, m, ldqx, k, 1, y, m, ldy, n, dtype_size(out_dtype)), "%s: y overlaps qx", what);
   QTTS_TRY(current_device_check());
   return qtts_launch_int8_gemm(qx, sx, m, k, ldqx, qw, n, ldqw, layout, sw, bias, y, out_dtype, ldy, algo, ws, ws_bytes,
                                (hipStream_t)stream);
@@ -522,7 +549,8 @@ static int int8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, in
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(sw && y && (k == 0 || (x && qw)), "int8_linear: null pointer");
   // The decode kernel has every workgroup read all of x while others write y.
-  QTTS_REQUIRE(!spans_overlap(x, m, ldx, k, y, m, ldy, n, dtype_size(x_dtype)), "int8_linear: y overlaps x");
+  QTTS_REQUIRE(!spans_overlap(x, m, ldx, k, dtype_size(x_dtype), y, m, ldy, n, dtype_size(x_dtype)),
+               "int8_linear: y overlaps x");
   // Decode rows on strip weights: quantization fused into the GEMM, one kernel, no
   // workspace.  A wave count alone (family SKINNY or AUTO, no split count or chunk
   // count) sets the fused kernel's waves; an explicit split count keeps the two-kernel path.
@@ -591,6 +619,8 @@ int qtts_w8a16_silu_mul_gemm_strips(const void* gate_up, int x_dtype, int64_t m,
   QTTS_REQUIRE(ws_bytes >= 0, "w8a16_silu_mul_gemm_strips: negative workspace size");
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(gate_up && qs && scale && y, "w8a16_silu_mul_gemm_strips: null pointer");
+  QTTS_REQUIRE(!spans_overlap(gate_up, m, ld_gate_up, 2 * k, 2, y, m, ldy, n, 2),
+               "w8a16_silu_mul_gemm_strips: y overlaps gate_up");
   QTTS_TRY(current_device_check());
   return qtts_launch_w8a16_silu(gate_up, x_dtype, m, k, ld_gate_up, qs, n, scale, scale_dtype, bias, y, ldy, algo, ws,
                                 ws_bytes, (hipStream_t)stream);
@@ -631,6 +661,8 @@ int qtts_w8a16_fused_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t 
   QTTS_REQUIRE(!residual || residual == y || !ranges_overlap(residual, m, ldr, y, m, ldy, n, 2),
                "w8a16_fused_gemm_strips: residual overlaps y without being y");
   QTTS_REQUIRE(!residual || residual != y || ldr == ldy, "w8a16_fused_gemm_strips: residual is y with another stride");
+  QTTS_REQUIRE(!spans_overlap(x, m, ldx, prologue == QTTS_PRO_SILU_MUL ? 2 * k : k, 2, y, m, ldy, n, 2),
+               "w8a16_fused_gemm_strips: y overlaps x");
   QTTS_TRY(current_device_check());
   return qtts_launch_w8a16_fused(x, x_dtype, m, k, ldx, prologue, norm_weight, eps, qs, n, scale, scale_dtype, bias,
                                  residual, ldr, y, ldy, algo, ws, ws_bytes, (hipStream_t)stream);
@@ -657,6 +689,7 @@ int qtts_w8a16_gate_up_silu_strips(const void* x, int x_dtype, int64_t m, int64_
                "w8a16_gate_up_silu_strips: null pointer");
   QTTS_REQUIRE((uintptr_t)x % 16 == 0 && (m == 1 || ldx % 8 == 0),
                "w8a16_gate_up_silu_strips: activation rows must be 16-byte aligned");
+  QTTS_REQUIRE(!spans_overlap(x, m, ldx, k, 2, act, m, ldact, n / 2, 2), "w8a16_gate_up_silu_strips: act overlaps x");
   QTTS_TRY(current_device_check());
   return qtts_launch_w8a16_gate_up_silu(x, x_dtype, m, k, ldx, prologue, norm_weight, eps, qs, n, scale, scale_dtype,
                                         bias, act, ldact, algo, ws, ws_bytes, (hipStream_t)stream);
@@ -676,6 +709,7 @@ int qtts_fp8w_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int6
   if (m == 0 || n == 0) return QTTS_OK;
   QTTS_REQUIRE(x && qs && scale && y, "fp8w_gemm_strips: null pointer");
   QTTS_REQUIRE((uintptr_t)x % 16 == 0 && (m == 1 || ldx % 8 == 0), "fp8w_gemm_strips: activation rows must be 16-byte aligned");
+  QTTS_REQUIRE(!spans_overlap(x, m, ldx, k, 2, y, m, ldy, n, 2), "fp8w_gemm_strips: y overlaps x");
   QTTS_TRY(current_device_check());
   return qtts_launch_fp8w(x, x_dtype, m, k, ldx, qs, n, scale, bias, y, ldy, algo, ws, ws_bytes, (hipStream_t)stream);
 }

@@ -167,7 +167,7 @@ int qtts_launch_fp8w(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
       return qtts_set_error(QTTS_ERR_WORKSPACE, "fp8w skinny: K=%lld needs a split-K workspace of %lld bytes",
                             (long long)k, (long long)skinny_ws(c));
   }
-  if (c.S >= (1 << 23)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8w skinny: K too large");
+  if (c.S > 65535) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8w skinny: K too large (%d splits, past the grid's y limit of 65535)", c.S);
   if (c.S > 1 && c.strips > kMaxSplitTiles)
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8w skinny: too many output strips for a split-K meeting");
   const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8;  // grid x; grid y: the K splits

@@ -357,7 +357,7 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
         return qtts_set_error(QTTS_ERR_WORKSPACE, "w8a16 skinny: K=%lld needs a split-K workspace of %lld bytes",
                               (long long)k, (long long)skinny_ws(c));
     }
-    if (c.S >= (1 << 23)) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: K too large");
+    if (c.S > 65535) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: K too large (%d splits, past the grid's y limit of 65535)", c.S);
     if (c.S > 1 && c.strips > kMaxSplitTiles)
       return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16 skinny: N=%lld with K=%lld needs a split-K over more "
                             "output strips than the workspace counter block holds", (long long)n, (long long)k);

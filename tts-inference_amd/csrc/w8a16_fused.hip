@@ -273,7 +273,7 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
   if (!qtts_w8a16_xrows_built(c.waves, c.cpw)) return 1;
   if (pro == kProRmsNorm && c.S > 1) return 1;
   if (c.S > 1 && c.strips > kMaxSplitTiles) return 1;
-  if (c.S >= (1 << 23)) return 1;
+  if (c.S > 65535) return 1;  // past the grid's y limit
   const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8;  // grid x; grid y: the K splits
   if (blocks >= ((int64_t)1 << 31) || in.ldx > INT32_MAX) return 1;
   FusedArgs a = in;

@@ -95,8 +95,6 @@ EXPORTS = (
     "qtts_w8a16_gate_up_silu_strips",
     "qtts_kernel_timer_begin",
     "qtts_kernel_timer_end",
-    "qtts_probe_stream",
-    "qtts_probe_empty",
 )
 
 
@@ -194,10 +192,6 @@ def load() -> ctypes.CDLL:
         L.qtts_kernel_timer_end.restype = i32
         L.qtts_kernel_timer_end.argtypes = [ctypes.POINTER(ctypes.c_double), ctypes.POINTER(i64),
                                             ctypes.POINTER(i64)]
-        L.qtts_probe_stream.restype = i32
-        L.qtts_probe_stream.argtypes = [p, i64, i32, i32, p, p]
-        L.qtts_probe_empty.restype = i32
-        L.qtts_probe_empty.argtypes = [i64, i32, p]
         version = L.qtts_abi_version()
         if version != ABI_VERSION:
             raise RuntimeError(f"libqtts_amd ABI version {version}, expected {ABI_VERSION}; rebuild it")

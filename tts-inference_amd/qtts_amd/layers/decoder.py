@@ -26,10 +26,16 @@ from .. import ops, torch_ops  # noqa: F401  (torch_ops registers torch.ops.qtts
 
 
 def _int8_strips(linear: nn.Module, x: torch.Tensor) -> bool:
+    """Whether ``linear`` runs x through the int8 weight-only strip kernels: its method, layout and
+    x's dtype allow it, and its calibration routed x's row bucket to a kernel (not to F.linear on
+    the kept weight, nor to the prefill route)."""
     method = getattr(linear, "quant_method", None)
-    return (getattr(method, "name", None) == "int8_weight_only" and getattr(linear, "int8_weight", None) is not None
+    if not (getattr(method, "name", None) == "int8_weight_only" and getattr(linear, "int8_weight", None) is not None
             and getattr(linear, "int8_layout", None) == "strips" and x.is_cuda
-            and x.dtype in (torch.bfloat16, torch.float16) and linear.in_features % 64 == 0)
+            and x.dtype in (torch.bfloat16, torch.float16) and linear.in_features % 64 == 0):
+        return False
+    routed = getattr(method, "routes_to_kernel", None)
+    return routed is None or routed(linear, x)
 
 
 def _norm_eps(norm: nn.Module) -> float:

@@ -831,21 +831,3 @@ class KernelTimer:
     def mean_ms(self) -> float:
         return self.total_ms / self.launches if self.launches else float("nan")
 
-
-def probe_stream(src: torch.Tensor, nbytes: int, waves: int, loads: int, sink: torch.Tensor) -> None:
-    """Stream ``nbytes`` of ``src`` with the measurement kernel (``qtts_probe_stream``): ``waves``
-    waves a workgroup, ``loads`` 1 KiB loads a wave issued before any is used; each wave stores
-    the xor of what it read to ``sink`` (int32, one word a wave)."""
-    dev = _require_cuda(src, sink)
-    if sink.dtype != torch.int32 or sink.numel() * loads * 1024 < nbytes:
-        raise ValueError("sink must be int32 with one word per wave")
-    if src.numel() * src.element_size() < nbytes:
-        raise ValueError("src is smaller than nbytes")
-    _lib.check(_lib.load().qtts_probe_stream(src.data_ptr(), int(nbytes), int(waves), int(loads), sink.data_ptr(),
-                                             _stream(dev)), "probe_stream")
-
-
-def probe_empty(workgroups: int, waves: int = 1, device: torch.device | None = None) -> None:
-    """Launch an empty kernel of ``workgroups`` x ``waves`` waves (``qtts_probe_empty``)."""
-    dev = device or torch.device("cuda", torch.cuda.current_device())
-    _lib.check(_lib.load().qtts_probe_empty(int(workgroups), int(waves), _stream(dev)), "probe_empty")

@@ -55,7 +55,7 @@ def _human(n: int) -> str:
 def quantize_module(module: nn.Module, method: QuantMethodBase, config: QuantConfig, label: str) -> dict[str, int]:
     """Attach ``method`` to every eligible linear under ``module`` (qtts/quant/base.py:74-113)."""
     before = _param_bytes(module) + _buffer_bytes(module)
-    converted = excluded = declined = 0
+    converted = excluded = declined = kept_weight = 0
     for name, layer in iter_linears(module):
         if config.excludes(name):
             excluded += 1
@@ -66,11 +66,15 @@ def quantize_module(module: nn.Module, method: QuantMethodBase, config: QuantCon
             continue
         layer.quant_method = method
         converted += 1
+        # a converted layer whose calibration routed some row bucket to F.linear keeps its weight
+        weight = getattr(layer, "weight", None)
+        kept_weight += int(weight is not None and weight.numel() > 0)
     after = _param_bytes(module) + _buffer_bytes(module)
-    logger.info("%s: %s converted %d linears, skipped %d by exclusion, kept %d on F.linear; weights %s -> %s",
-                label, method.name, converted, excluded, declined, _human(before), _human(after))
+    logger.info("%s: %s converted %d linears (%d keeping their weight for F.linear at some row bucket), "
+                "skipped %d by exclusion, kept %d on F.linear; weights %s -> %s",
+                label, method.name, converted, kept_weight, excluded, declined, _human(before), _human(after))
     return {"converted": converted, "excluded": excluded, "declined": declined, "bytes_before": before,
-            "bytes_after": after}
+            "bytes_after": after, "kept_weight": kept_weight}
 
 
 def fp8_supported() -> tuple[bool, str]:

@@ -12,6 +12,14 @@ Timing runs ``inner`` calls captured in one graph and replays it ``iters`` times
 engine's decode graph amortises it.  Any exception while timing a candidate drops
 that candidate; an exception while timing the reference declines the layer.  A
 calibration failure is never fatal (qtts/quant/calibrate.py:96-103).
+
+``calibrate_buckets`` asks the reference's question at every row bucket the callers
+produce.  A layer the reference would keep (slower over the decode rows) is declined
+here too; a layer it would convert can still lose to F.linear at some bucket (a
+prefill row count, say), and with ``keep_reference`` that bucket is routed to F.linear
+on the layer's retained weight (``ALGO_REFERENCE_GEMM``), so no bucket runs slower than
+the layer it replaced -- the reference's rule that a layer measured slower keeps its
+original GEMM (qtts/quant/int8.py:59-67), applied per bucket.
 """
 
 from __future__ import annotations
@@ -25,6 +33,10 @@ import torch
 logger = logging.getLogger("qtts_amd.quant.calibrate")
 
 _CACHE: dict[tuple, object] = {}
+
+#: Algo value (Python side only) that sends a bucket's calls to F.linear on the layer's own
+#: retained weight: the bucket where every quantized route lost to that GEMM.
+ALGO_REFERENCE_GEMM = -2
 
 
 def graph_time(fn: Callable[[], object], inner: int = 10, iters: int = 50) -> float:
@@ -141,6 +153,7 @@ def calibrate_buckets(tag: str, n: int, k: int, dtype: torch.dtype, device: torc
                       route_calls: dict[int, dict[str, tuple[int, Callable[[torch.Tensor], object]]]] | None = None,
                       margin: float = 1.05, use_graph: bool = True,
                       timer: Callable[[Callable[[], object]], float] | None = None,
+                      keep_reference: bool = False,
                       ) -> tuple[bool, dict[int, int], dict[int, dict]]:
     """Per-bucket kernel choice for one ``[n, k]`` weight (qtts/quant/calibrate.py:77-114 asks one
     question at one row count; this asks it at every row bucket the callers produce).
@@ -155,8 +168,9 @@ def calibrate_buckets(tag: str, n: int, k: int, dtype: torch.dtype, device: torc
     declines the layer; a calibration failure is never fatal.
 
     Returns ``(accept, {rows: algo}, {rows: {"reference": s, "best": name, "timings": {...}}})``;
-    the table holds the fastest candidate of every bucket that timed (also where it loses to the
-    reference: once quantized, the bf16 weight is gone and the fastest quantized route serves)."""
+    the table holds the fastest candidate of every bucket that timed.  Where that candidate is
+    slower than the reference, the bucket gets ``ALGO_REFERENCE_GEMM`` with ``keep_reference``
+    (the caller keeps the weight for F.linear there), else the fastest quantized route anyway."""
     table: dict[int, int] = {}
     report: dict[int, dict] = {}
     decode_ref = decode_best = 0.0
@@ -177,7 +191,8 @@ def calibrate_buckets(tag: str, n: int, k: int, dtype: torch.dtype, device: torc
         best = min(timings, key=timings.get) if timings else None
         report[rows] = {"reference": reference, "best": best, "timings": timings}
         if best is not None:
-            table[rows] = algos[best]
+            loses = reference is not None and timings[best] > reference
+            table[rows] = ALGO_REFERENCE_GEMM if keep_reference and loses else algos[best]
         if rows <= decode_rows:
             if reference is None or best is None:
                 return False, {}, report

@@ -9,7 +9,8 @@ uniformly, as in the reference (qtts/quant/fp8.py:52-89).
 the reference's stub names as the right home for fp8 weights (qtts/quant/fp8.py:92-123,
 where it raises NotImplementedError because Triton could not load e4m3): the W8A16
 kernels with the e4m3 codes converted in registers.  Calibrated per layer shape
-like the int8 weight-only method.
+like the int8 weight-only method, with the same per-layer bucket table and the same
+F.linear route for buckets no quantized route wins.
 """
 
 from __future__ import annotations
@@ -21,8 +22,8 @@ import torch.nn.functional as F
 from .. import _lib, ops
 from . import prefill
 from .base import QuantMethodBase
-from .calibrate import calibrate_buckets
-from .int8 import tile8_candidates
+from .calibrate import ALGO_REFERENCE_GEMM, calibrate_buckets
+from .int8 import layer_algo, tile8_candidates
 from .kernels import kernel_available
 
 _FP8_MAX = 448.0
@@ -79,13 +80,11 @@ def fp8_weight_rowmajor(layer) -> torch.Tensor:
     return layer.fp8_weight.t()
 
 
-#: Per (N, K, bucket) algo codes chosen by calibration for fp8 weight-only layers.
-_FP8W_ALGO: dict[tuple[int, int, int], int] = {}
-
-
 def _fp8w_candidates(rows: int) -> dict[str, int]:
     """Kernel configurations worth timing at ``rows`` (the algo bits of include/qtts_amd.h)."""
     c: dict[str, int] = {}
+    if rows <= 8:  # the automatic choice: row-split strips where whole strips leave compute units idle
+        c["auto"] = _lib.ALGO_AUTO
     if rows <= 16:
         c["skinny"] = _lib.algo_code(_lib.ALGO_SKINNY)
         for s in (1, 2, 4):
@@ -121,7 +120,7 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
     name = "fp8_weight_only"
 
     def __init__(self, calibrate: bool = True, calibration_batch: int = 16, div_mode: int = _lib.DIV_DEVICE,
-                 calibration_rows: tuple[int, ...] | None = None, timer=None) -> None:
+                 calibration_rows: tuple[int, ...] | None = None, timer=None, keep_reference_routes: bool = True) -> None:
         from .int8 import M_BUCKETS
         available, reason = kernel_available()
         if not available:
@@ -130,15 +129,17 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
         self.calibration_batch = calibration_batch
         self.calibration_rows = tuple(sorted(set(calibration_rows or M_BUCKETS)))
         self.timer = timer
+        self.keep_reference_routes = keep_reference_routes
         self.calibration_report: dict[tuple[int, int], dict] = {}
         self.div_mode = div_mode
         self.quantized = 0
         self.declined = 0
+        self.kept_reference = 0
 
-    def _profitable(self, layer, qs: torch.Tensor, scale: torch.Tensor) -> bool:
+    def _profitable(self, layer, qs: torch.Tensor, scale: torch.Tensor) -> tuple[bool, dict[int, int]]:
         """Per-bucket calibration, as Int8WeightOnlyMethod._profitable (calibrate.calibrate_buckets)."""
         if not self.calibrate:
-            return True
+            return True, {}
         weight = layer.weight
         n, k = layer.out_features, layer.in_features
         ops.reserve_workspace(weight.device, max(ops.workspace_bytes(_lib.OP_FP8W, r, n, k, a)
@@ -152,11 +153,9 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
         accept, table, report = calibrate_buckets(
             "fp8_wo", n, k, weight.dtype, weight.device, self.calibration_rows, max(1, self.calibration_batch),
             _fp8w_candidates, lambda x, a: ops.fp8w_gemm_strips(x, qs, n, scale, None, a),
-            lambda x: F.linear(x, weight, None), routes, timer=self.timer)
+            lambda x: F.linear(x, weight, None), routes, timer=self.timer, keep_reference=self.keep_reference_routes)
         self.calibration_report[(n, k)] = report
-        for rows, algo in table.items():
-            _FP8W_ALGO.setdefault((n, k, rows), algo)
-        return accept
+        return accept, table
 
     def _decline(self, layer) -> None:
         self.declined += 1
@@ -169,15 +168,20 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
             return
         q, scale = quantize_weight_fp8(weight, self.div_mode)
         qs = ops.fp8w_strips(q)
-        if not self._profitable(layer, qs, scale):
+        accept, table = self._profitable(layer, qs, scale)
+        if not accept:
             self._decline(layer)
             return
         ops.reserve_for_rows(weight.device, _lib.OP_FP8W, layer.out_features, layer.in_features)
         layer.register_buffer("fp8w_weight", qs, persistent=False)
         layer.register_buffer("fp8w_scale", scale, persistent=False)
+        layer.quant_algos = dict(table)
+        self.quantized += 1
+        if ALGO_REFERENCE_GEMM in table.values():
+            self.kept_reference += 1  # F.linear serves some bucket: the weight stays
+            return
         layer.weight = torch.nn.Parameter(torch.empty(0, dtype=weight.dtype, device=weight.device),
                                           requires_grad=False)
-        self.quantized += 1
 
     def applies_to(self, layer) -> bool:
         return getattr(layer, "fp8w_weight", None) is not None
@@ -185,10 +189,11 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
         if x.dtype not in (torch.bfloat16, torch.float16):
             raise ValueError(f"fp8 weight-only layers take bf16 or fp16 activations, got {x.dtype}")
-        from .int8 import bucket_of
         n, k = layer.out_features, layer.in_features
         rows = x.numel() // k if k else 0
-        algo = _FP8W_ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
+        algo = layer_algo(layer, rows)
+        if algo == ALGO_REFERENCE_GEMM and layer.weight.numel() > 0 and x.dtype == layer.weight.dtype:
+            return F.linear(x, layer.weight, bias)
         if algo == prefill.ALGO_DEQUANT_GEMM:  # x is bf16 / fp16 here, as the scratch was sized for
             return prefill.dequant_linear(layer.fp8w_weight, _lib.CODE_E4M3, n, k, layer.fp8w_scale, x, bias)
-        return torch.ops.qtts.fp8w_gemm_strips(x, layer.fp8w_weight, n, layer.fp8w_scale, bias, algo)
+        return torch.ops.qtts.fp8w_gemm_strips(x, layer.fp8w_weight, n, layer.fp8w_scale, bias, max(algo, 0))

@@ -10,6 +10,10 @@ row bucket the callers produce (decode rows 1..16, code-predictor rows up to 128
 prefill buckets), the verdict comes from the decode buckets, and each bucket keeps
 its fastest route: a skinny or tile kernel configuration, or at the prefill buckets
 dequantizing the codes into a scratch buffer and calling F.linear (quant/prefill.py).
+A converted layer that still loses to F.linear at some bucket keeps its weight too and
+sends that bucket's calls to F.linear (``keep_reference_routes``), so no bucket runs
+slower than the unquantized layer.  The per-bucket choices live on the layer
+(``layer.quant_algos``), so layers of one shape but another dtype or device never share them.
 
 ``Int8Method`` (W8A8) quantizes activations per token at run time and multiplies
 int8 codes on the int8 matrix cores (v_mfma_i32_16x16x64_i8) with exact int32
@@ -27,7 +31,7 @@ import torch.nn.functional as F
 from .. import _lib, ops
 from . import prefill
 from .base import QuantMethodBase
-from .calibrate import calibrate_buckets
+from .calibrate import ALGO_REFERENCE_GEMM, calibrate_buckets
 from .kernels import kernel_available
 
 logger = logging.getLogger("qtts_amd.quant.int8")
@@ -38,9 +42,6 @@ _INT8_MAX = 127.0
 #: smallest bucket that holds its row count (decode rows 1..16 go to the skinny
 #: kernel, prefill rows to the tile kernel).
 M_BUCKETS = (1, 2, 4, 8, 16, 32, 64, 128, 256, 1024, 2048)
-
-#: Per (N, K, bucket) algo codes chosen by calibration; absent means automatic.
-_ALGO: dict[tuple[int, int, int], int] = {}
 
 
 def bucket_of(rows: int) -> int:
@@ -59,9 +60,20 @@ def quantize_weight_per_channel(weight: torch.Tensor, div_mode: int = _lib.DIV_D
     return ops.pack_int8(weight, torch.float32, div_mode)
 
 
-def _candidates(rows: int) -> dict[str, int]:
-    """Kernel configurations worth timing at ``rows`` (the algo bits of include/qtts_amd.h)."""
+def layer_algo(layer, rows: int) -> int:
+    """The calibrated route of ``layer`` for a call of ``rows`` rows (``ALGO_AUTO`` if none)."""
+    return getattr(layer, "quant_algos", {}).get(bucket_of(rows), _lib.ALGO_AUTO)
+
+
+def _candidates(rows: int, k: int | None = None) -> dict[str, int]:
+    """Kernel configurations worth timing at ``rows`` for a weight of ``k`` input features (the
+    algo bits of include/qtts_amd.h)."""
     c: dict[str, int] = {}
+    if rows <= 8:
+        # the automatic choice (row-split strips where whole strips leave compute units idle)
+        c["auto"] = _lib.ALGO_AUTO
+        if k is not None and k % 128 == 0:
+            c["skinny_half"] = _lib.algo_code(_lib.ALGO_SKINNY_HALF)
     if rows <= 64:  # skinny: up to 16 rows, or 64 on strip weights
         c["skinny"] = _lib.algo_code(_lib.ALGO_SKINNY)
         for s in (1, 2, 4):
@@ -109,7 +121,7 @@ class Int8WeightOnlyMethod(QuantMethodBase):
     name = "int8_weight_only"
 
     def __init__(self, calibrate: bool = True, calibration_batch: int = 16, div_mode: int = _lib.DIV_DEVICE,
-                 calibration_rows: tuple[int, ...] = M_BUCKETS, timer=None) -> None:
+                 calibration_rows: tuple[int, ...] = M_BUCKETS, timer=None, keep_reference_routes: bool = True) -> None:
         available, reason = kernel_available()
         if not available:
             raise RuntimeError(f"int8 weight-only needs the gfx950 fused kernel: {reason}")
@@ -117,26 +129,35 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         self.calibration_batch = calibration_batch
         self.calibration_rows = tuple(sorted(set(calibration_rows)))
         self.timer = timer
+        #: Keep a converted layer's weight for the buckets where F.linear on it beat every
+        #: quantized route (else those buckets run the fastest quantized route anyway).
+        self.keep_reference_routes = keep_reference_routes
         #: (N, K) -> per-bucket timings of the last calibration (calibrate_buckets' report)
         self.calibration_report: dict[tuple[int, int], dict] = {}
         self.div_mode = div_mode
         self.quantized = 0
         self.declined = 0
+        #: converted layers that kept their weight for F.linear at some bucket
+        self.kept_reference = 0
 
-    def _profitable(self, layer, q: torch.Tensor, scale: torch.Tensor, layout: str) -> bool:
+    def _profitable(self, layer, q: torch.Tensor, scale: torch.Tensor, layout: str) -> tuple[bool, dict[int, int]]:
         """Per-bucket calibration (calibrate.calibrate_buckets): every HIP candidate, and the
         prefill route at the prefill buckets, against F.linear at each row bucket in
         ``calibration_rows``; the layer converts when it wins over the decode buckets (rows up
-        to ``calibration_batch``) and each bucket then runs its fastest route."""
+        to ``calibration_batch``) and each bucket then runs its fastest route, F.linear on the
+        kept weight where that was faster than every quantized one.  Returns the verdict and
+        the per-bucket table."""
         if not self.calibrate:
-            return True
+            return True, {}
         weight = layer.weight
         if not torch.cuda.is_available() or weight.device.type != "cuda":
-            return False
+            return False, {}
         n, k = layer.out_features, layer.in_features
         strips = layout == "strips"
+        kk = k if strips else None  # row-split strips exist on strip weights only
         ops.reserve_workspace(weight.device, max(ops.workspace_bytes(_lib.OP_W8A16, r, n, k, a)
-                                                 for r in self.calibration_rows for a in _candidates(r).values()))
+                                                 for r in self.calibration_rows
+                                                 for a in _candidates(r, kk).values()))
         if strips:
             kernel = lambda x, a: ops.w8a16_gemm_strips(x, q, n, scale, None, a)  # noqa: E731
         else:
@@ -149,11 +170,10 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             routes = {r: {"dequant": route} for r in self.calibration_rows if r in prefill.PREFILL_BUCKETS}
         accept, table, report = calibrate_buckets(
             "int8_wo", n, k, weight.dtype, weight.device, self.calibration_rows, max(1, self.calibration_batch),
-            _candidates, kernel, lambda x: F.linear(x, weight, None), routes, timer=self.timer)
+            lambda rows: _candidates(rows, kk), kernel, lambda x: F.linear(x, weight, None), routes,
+            timer=self.timer, keep_reference=self.keep_reference_routes)
         self.calibration_report[(n, k)] = report
-        for rows, algo in table.items():
-            _ALGO.setdefault((n, k, rows), algo)
-        return accept
+        return accept, table
 
     def process_weights(self, layer) -> None:
         weight = layer.weight
@@ -163,7 +183,8 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         layout = "strips" if _strips_ok(layer) else "rowmajor"
         if layout == "strips":
             q = ops.to_strips(q, _lib.STRIP_INT8)
-        if not self._profitable(layer, q, scale, layout):
+        accept, table = self._profitable(layer, q, scale, layout)
+        if not accept:
             self.declined += 1
             # Leaving quant_method unset keeps the layer on F.linear.
             layer.register_buffer("int8_weight", None, persistent=False)
@@ -174,22 +195,40 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         layer.register_buffer("int8_weight", q, persistent=False)
         layer.register_buffer("int8_scale", scale, persistent=False)
         layer.int8_layout = layout
+        layer.quant_algos = dict(table)
+        self.quantized += 1
+        if ALGO_REFERENCE_GEMM in table.values():
+            # F.linear serves some bucket: the weight stays (and counts in the memory report).
+            self.kept_reference += 1
+            return
         # Drop the full-precision weight, or the memory report would claim a saving it did not make.
         layer.weight = torch.nn.Parameter(torch.empty(0, dtype=weight.dtype, device=weight.device),
                                           requires_grad=False)
-        self.quantized += 1
 
     def applies_to(self, layer) -> bool:
         return getattr(layer, "int8_weight", None) is not None
 
+    @staticmethod
+    def _reference_route(layer, x: torch.Tensor, algo: int) -> bool:
+        """Whether this call goes to F.linear on the layer's kept weight."""
+        return algo == ALGO_REFERENCE_GEMM and layer.weight.numel() > 0 and x.dtype == layer.weight.dtype
+
+    def routes_to_kernel(self, layer, x: torch.Tensor) -> bool:
+        """Whether a call of ``x`` on this layer runs a HIP kernel (not F.linear or the prefill route)."""
+        k = layer.in_features
+        algo = layer_algo(layer, x.numel() // k if k else 0)
+        return algo not in (ALGO_REFERENCE_GEMM, prefill.ALGO_DEQUANT_GEMM)
+
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
         n, k = layer.out_features, layer.in_features
         rows = x.numel() // k if k else 0
-        algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
+        algo = layer_algo(layer, rows)
+        if self._reference_route(layer, x, algo):
+            return F.linear(x, layer.weight, bias)
         if algo == prefill.ALGO_DEQUANT_GEMM and layer.int8_layout == "strips" and x.dtype in (torch.bfloat16,
                                                                                              torch.float16):
             return prefill.dequant_linear(layer.int8_weight, _lib.CODE_INT8, n, k, layer.int8_scale, x, bias)
-        if algo == prefill.ALGO_DEQUANT_GEMM:  # the route's marker never reaches a kernel
+        if algo < 0:  # a route's marker never reaches a kernel
             algo = _lib.ALGO_AUTO
         if layer.int8_layout == "strips":
             if x.dtype in (torch.bfloat16, torch.float16):
@@ -208,9 +247,11 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         if n % 2:
             return None
         rows = x.numel() // k if k else 0
-        algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
-        if algo == prefill.ALGO_DEQUANT_GEMM:
+        algo = layer_algo(layer, rows)
+        if algo < 0:  # F.linear or the prefill route serves this bucket: the plain path
             return None
+        if (algo & 0xFF) in (_lib.ALGO_SKINNY_HALF, _lib.ALGO_SKINNY_QUARTER):
+            algo = _lib.ALGO_AUTO  # the pair kernel runs whole strips (two per workgroup)
         return torch.ops.qtts.w8a16_gate_up_silu_strips(x, layer.int8_weight, n, layer.int8_scale, bias,
                                                        ops.PRO_NONE, None, 1e-6, algo)
 
@@ -222,8 +263,8 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             raise ValueError(f"gate_up has {gate_up.shape[-1]} columns for a down projection with K={k}")
         if layer.int8_layout == "strips" and gate_up.dtype in (torch.bfloat16, torch.float16):
             rows = gate_up.numel() // (2 * k) if k else 0
-            algo = _ALGO.get((n, k, bucket_of(rows)), _lib.ALGO_AUTO)
-            if algo != prefill.ALGO_DEQUANT_GEMM:
+            algo = layer_algo(layer, rows)
+            if algo >= 0:
                 return torch.ops.qtts.w8a16_silu_mul_gemm_strips(gate_up, layer.int8_weight, n, layer.int8_scale,
                                                                  bias, algo)
         return self.apply(layer, torch.ops.qtts.silu_mul(gate_up), bias)

@@ -1,8 +1,8 @@
-"""The fused dequantize-in-registers GEMM and its availability check.
+"""Availability of the fused dequantize-in-registers GEMM.
 
-Mirrors qtts/quant/kernels.py:83-84 (``kernel_available``) and :138-178
-(``w8_gemm``), backed by the hand-written gfx950 kernels in libqtts_amd.so
-instead of a Triton kernel.
+Mirrors qtts/quant/kernels.py:83-84 (``kernel_available``), backed by the hand-written
+gfx950 kernels in libqtts_amd.so instead of a Triton kernel.  The reference's wrapper
+(``w8_gemm``, kernels.py:138-178) is ``ops.w8a16_gemm`` / ``ops.w8a16_gemm_strips``.
 """
 
 from __future__ import annotations
@@ -24,9 +24,3 @@ def kernel_available() -> tuple[bool, str]:
         name = torch.cuda.get_device_name()
         return False, f"device {name!r} is not a gfx950 (MI355X-class) GPU"
     return True, ""
-
-
-def w8_gemm(x: torch.Tensor, weight: torch.Tensor, scale: torch.Tensor, bias: torch.Tensor | None = None,
-            algo: int = _lib.ALGO_AUTO) -> torch.Tensor:
-    """``x @ (weight * scale).T + bias``, dequantizing ``weight`` in registers."""
-    return ops.w8a16_gemm(x, weight, scale, bias, algo)
