@@ -421,6 +421,37 @@ def run_predictor(args, torch, ops):
         out[f"batch{b}"] = {"frame_us": round(t_q * 1e3, 2), "pass_us": round(t_q * 1e3 / 15, 2),
                             "bf16_frame_us": round(t_b * 1e3, 2), "speedup_vs_bf16": round(t_b / t_q, 3),
                             "launches_per_frame": len(ms) * len(stack)}
+        del g_q, g_b
+    if args.calibrated:
+        # The same frames through LinearBase layers converted by the calibrated int8 weight-only method
+        # (per-bucket kernel choice; F.linear on the kept weight at the buckets where it won).
+        from qtts_amd.layers.linear import LinearBase
+        from qtts_amd.quant import calibrate
+        from qtts_amd.quant.int8 import Int8WeightOnlyMethod
+        calibrate.clear_cache()
+        method = Int8WeightOnlyMethod(calibrate=True, calibration_batch=16,
+                                      calibration_rows=(1, 2, 4, 8, 16, 32, 64, 128))
+        layers_q = []
+        for e in stack:
+            lin = LinearBase(e["k"], e["n"], dtype=torch.bfloat16, device="cuda")
+            lin.weight.data.copy_(e["w_bf16"])
+            method.process_weights(lin)
+            if method.applies_to(lin):
+                lin.quant_method = method
+            layers_q.append(lin)
+        routed = sorted({f"{PREDICTOR[i % 4][0]}@{r}" for i, lin in enumerate(layers_q)
+                         for r, a in getattr(lin, "quant_algos", {}).items() if a == calibrate.ALGO_REFERENCE_GEMM})
+        for b in (1, 8):
+            ms = [b * p for p in range(2, 17)]
+            xs = make_inputs(torch, [k for _, _, k in PREDICTOR], ms)
+            g_c = capture(torch, lambda: [lin(xs[(m, lin.in_features)]) for m in ms for lin in layers_q])
+            t_c = time_graph(torch, g_c, args.steps, args.warmup)
+            del g_c
+            r = out[f"batch{b}"]
+            r["calibrated_frame_us"] = round(t_c * 1e3, 2)
+            r["calibrated_speedup_vs_bf16"] = round(r["bf16_frame_us"] / (t_c * 1e3), 3)
+        out["calibrated_routes_to_f_linear"] = routed
+        out["calibrated_converted"] = sum(method.applies_to(lin) for lin in layers_q)
     return {"metric": "code-predictor linear stack us/frame", "value": out["batch1"]["frame_us"], "unit": "us",
             "higher_is_better": False, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
             "config": {"workload": "configs[2]: 5 layers x 4 linears x 15 prefix passes, int8 weight-only"},
@@ -928,6 +959,8 @@ def main() -> int:
                     help="time the configs[1] decode stack with fp8 weight-only weights instead of a config")
     ap.add_argument("--mlp", action="store_true",
                     help="time the talker MLP (gate_up, silu*up, down) with the activation fused into down")
+    ap.add_argument("--calibrated", action="store_true",
+                    help="with --config 2: also time the frames through layers converted by the calibrated method")
     ap.add_argument("--calibration", action="store_true",
                     help="print the int8 weight-only per-bucket calibration against hipBLASLt on the model shapes")
     ap.add_argument("--floor", action="store_true",

@@ -315,3 +315,31 @@ def test_reference_route_dispatch():
     assert layer_algo(other, 1) == _lib.ALGO_AUTO
     assert not method.routes_to_kernel(lin, x) and method.routes_to_kernel(lin, torch.randn(2, 8))
     assert method.apply_gate_up_silu(lin, x, None) is None   # the plain path then calls apply
+
+
+def test_weight_rotation_for_timing():
+    """The calibration rotates through copies of a weight that together pass the L2s: the copy count
+    follows the weight size (at least 1, at most 64), and the rotating callable runs the copies in
+    turn, one per call, so a graph of as many calls reads each copy once."""
+    assert calibrate.rotation(calibrate.ROTATE_BYTES) == 1
+    assert calibrate.rotation(calibrate.ROTATE_BYTES * 4) == 1
+    assert calibrate.rotation(2 << 20) == 32 and calibrate.rotation(25 << 20) == 3
+    assert calibrate.rotation(1) == 64 and calibrate.rotation(1, limit=8) == 8
+    seen = []
+    run = calibrate.rotating([lambda a, i=i: seen.append((i, a)) for i in range(3)])
+    for a in range(7):
+        run(a)
+    assert seen == [(0, 0), (1, 1), (2, 2), (0, 3), (1, 4), (2, 5), (0, 6)]
+
+
+def test_calibrate_buckets_inner_calls_reach_the_timer_key():
+    """A calibration that rotates over more than 10 weight copies caches its timings apart from one
+    that times 10 calls of one weight (the reference's harness)."""
+    calibrate.clear_cache()
+    kernel, reference, timer, candidates, calls = _bucket_fixture(lambda label: 1.0 if label[0] == "ref" else 0.5)
+    calibrate.calibrate_buckets("k", 8, 8, torch.float32, torch.device("cpu"), (1,), 1, candidates, kernel, reference,
+                                timer=timer)
+    n = len(calls)
+    calibrate.calibrate_buckets("k", 8, 8, torch.float32, torch.device("cpu"), (1,), 1, candidates, kernel, reference,
+                                timer=timer, inner=32)
+    assert len(calls) > n   # timed again: another key

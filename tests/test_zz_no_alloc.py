@@ -41,6 +41,40 @@ def _static_call(_lib, x, qws, n, sw, b, algo=0):
     return rc, y
 
 
+def test_static_entry_first_called_under_graph_capture(env):
+    """The entry point's first call in the process is made inside a HIP graph capture (torch's
+    global capture mode, where an allocating or synchronizing call fails the capture): the scratch
+    address is resolved and the counter block cleared there.  Two-kernel rows, with and without a
+    forced split; every replay, with eager work between them, equals the caller-workspace entry
+    point bit for bit."""
+    _lib, ops = env
+    ops.reserve_workspace(torch.device("cuda"), 64 << 20)
+    m, n, k = 64, 2048, 2048
+    x, qws, sw, b = _operands(ops, m, n, k, seed=7)
+    split = _lib.algo_code(_lib.ALGO_TILE, splits=2)
+    static_x = x.clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm the caller-workspace path only
+        ops.fp8_linear_strips(static_x, qws, n, sw, b)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc0, y0 = _static_call(_lib, static_x, qws, n, sw, b)
+        rc1, y1 = _static_call(_lib, static_x, qws, n, sw, b, split)
+    assert rc0 == 0 and rc1 == 0, _lib.last_error()
+    g = torch.Generator(device="cuda").manual_seed(8)
+    for i in range(3):
+        fresh = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+        static_x.copy_(fresh)
+        ops.fp8_linear_strips(fresh * 0.5, qws, n, sw, b)  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(y0, ops.fp8_linear_strips(fresh, qws, n, sw, b)), f"replay {i}"
+        assert torch.equal(y1, ops.fp8_linear_strips(fresh, qws, n, sw, b, ops.DIV_DEVICE, split)), f"replay {i} split"
+
+
 def test_static_workspace_matches_caller_workspace(env):
     _lib, ops = env
     ops.reserve_workspace(torch.device("cuda"), 64 << 20)

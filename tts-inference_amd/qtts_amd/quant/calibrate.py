@@ -14,7 +14,11 @@ that candidate; an exception while timing the reference declines the layer.  A
 calibration failure is never fatal (qtts/quant/calibrate.py:96-103).
 
 ``calibrate_buckets`` asks the reference's question at every row bucket the callers
-produce.  A layer the reference would keep (slower over the decode rows) is declined
+produce.  The reference times one weight's repeated calls, which keeps a small weight in
+the L2 caches and times it as if it never streamed; here the callers may hand in several
+copies of the weight (``rotate``) that together exceed the L2s, each call of a graph reading
+the next one, so both the kernels and F.linear are timed with their weights streaming as
+they do in a decode step (each layer's weight read once).  A layer the reference would keep (slower over the decode rows) is declined
 here too; a layer it would convert can still lose to F.linear at some bucket (a
 prefill row count, say), and with ``keep_reference`` that bucket is routed to F.linear
 on the layer's retained weight (``ALGO_REFERENCE_GEMM``), so no bucket runs slower than
@@ -60,6 +64,30 @@ def graph_time(fn: Callable[[], object], inner: int = 10, iters: int = 50) -> fl
     elapsed = time.perf_counter() - started
     del graph
     return elapsed / (iters * inner)
+
+
+#: Bytes of weight copies the weight-only methods rotate through when timing a shape: well past
+#: the 8 x 4 MiB of L2, within the 256 MiB Infinity Cache (as the code predictor's 78 MB of int8
+#: weights are during its 15 prefix passes).
+ROTATE_BYTES = 64 << 20
+
+
+def rotation(weight_bytes: int, limit: int = 64) -> int:
+    """How many copies of a weight of ``weight_bytes`` the calibration rotates through."""
+    return max(1, min(limit, -(-ROTATE_BYTES // max(1, weight_bytes))))
+
+
+def rotating(calls: list[Callable[..., object]]) -> Callable[..., object]:
+    """One callable that runs the next of ``calls`` each time it is called (in capture too, so a
+    graph of len(calls) calls reads every copy once)."""
+    state = [0]
+
+    def run(*args):
+        i = state[0]
+        state[0] = (i + 1) % len(calls)
+        return calls[i](*args)
+
+    return run
 
 
 def eager_time(fn: Callable[[], object], iters: int = 200) -> float:
@@ -153,13 +181,14 @@ def calibrate_buckets(tag: str, n: int, k: int, dtype: torch.dtype, device: torc
                       route_calls: dict[int, dict[str, tuple[int, Callable[[torch.Tensor], object]]]] | None = None,
                       margin: float = 1.05, use_graph: bool = True,
                       timer: Callable[[Callable[[], object]], float] | None = None,
-                      keep_reference: bool = False,
+                      keep_reference: bool = False, inner: int = 10,
                       ) -> tuple[bool, dict[int, int], dict[int, dict]]:
     """Per-bucket kernel choice for one ``[n, k]`` weight (qtts/quant/calibrate.py:77-114 asks one
     question at one row count; this asks it at every row bucket the callers produce).
 
     At each row count in ``buckets`` it times every candidate algo (``candidates(rows)``, run as
-    ``kernel_call(x, algo)``) and any extra routes for that bucket (``route_calls[rows]``: name ->
+    ``kernel_call(x, algo)``; ``inner`` calls a graph, at least 10) and any extra routes for that
+    bucket (``route_calls[rows]``: name ->
     (algo marker, call)) against ``reference_call(x)`` (F.linear on the bf16 weight), on seeded
     random activations.  The layer is worth quantizing when, summed over the decode buckets (rows
     <= ``decode_rows``: the rows a decode step runs), the fastest candidate of each bucket beats
@@ -184,10 +213,12 @@ def calibrate_buckets(tag: str, n: int, k: int, dtype: torch.dtype, device: torc
             algos[name] = marker
             calls[name] = (lambda c=call, x=x: c(x))
         t = timer
-        if t is None and use_graph and rows > 128:  # prefill-sized calls: fewer replays suffice
-            t = lambda fn: graph_time(fn, inner=10, iters=10)  # noqa: E731
-        reference, timings = time_candidates(calls, lambda x=x: reference_call(x),
-                                             key=(tag, n, k, rows, str(dtype)), use_graph=use_graph, timer=t)
+        if t is None and use_graph:  # ``inner`` calls a graph (one per weight copy the calls rotate over)
+            # prefill-sized calls: fewer replays suffice
+            t = lambda fn, r=rows: graph_time(fn, inner=max(10, inner), iters=10 if r > 128 else 50)  # noqa: E731
+        key = (tag, n, k, rows, str(dtype)) + ((("calls_per_graph", inner),) if inner > 10 else ())
+        reference, timings = time_candidates(calls, lambda x=x: reference_call(x), key=key, use_graph=use_graph,
+                                             timer=t)
         best = min(timings, key=timings.get) if timings else None
         report[rows] = {"reference": reference, "best": best, "timings": timings}
         if best is not None:

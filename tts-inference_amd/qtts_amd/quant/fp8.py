@@ -22,7 +22,7 @@ import torch.nn.functional as F
 from .. import _lib, ops
 from . import prefill
 from .base import QuantMethodBase
-from .calibrate import ALGO_REFERENCE_GEMM, calibrate_buckets
+from .calibrate import ALGO_REFERENCE_GEMM, calibrate_buckets, rotating, rotation
 from .int8 import layer_algo, tile8_candidates
 from .kernels import kernel_available
 
@@ -120,7 +120,8 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
     name = "fp8_weight_only"
 
     def __init__(self, calibrate: bool = True, calibration_batch: int = 16, div_mode: int = _lib.DIV_DEVICE,
-                 calibration_rows: tuple[int, ...] | None = None, timer=None, keep_reference_routes: bool = True) -> None:
+                 calibration_rows: tuple[int, ...] | None = None, timer=None, keep_reference_routes: bool = True,
+                 rotate_weights: bool = True) -> None:
         from .int8 import M_BUCKETS
         available, reason = kernel_available()
         if not available:
@@ -130,6 +131,7 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
         self.calibration_rows = tuple(sorted(set(calibration_rows or M_BUCKETS)))
         self.timer = timer
         self.keep_reference_routes = keep_reference_routes
+        self.rotate_weights = rotate_weights
         self.calibration_report: dict[tuple[int, int], dict] = {}
         self.div_mode = div_mode
         self.quantized = 0
@@ -144,16 +146,22 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
         n, k = layer.out_features, layer.in_features
         ops.reserve_workspace(weight.device, max(ops.workspace_bytes(_lib.OP_FP8W, r, n, k, a)
                                                  for r in self.calibration_rows for a in _fp8w_candidates(r).values()))
+        copies = rotation(n * k) if self.rotate_weights else 1
+        qss = [qs] + [qs.clone() for _ in range(copies - 1)]
+        ws = [weight] + [weight.detach().clone() for _ in range(copies - 1)]
         routes = {}
         if any(r in prefill.PREFILL_BUCKETS for r in self.calibration_rows):
             prefill.reserve(weight.device, n, k, weight.dtype)
             route = (prefill.ALGO_DEQUANT_GEMM,
-                     lambda x: prefill.dequant_linear(qs, _lib.CODE_E4M3, n, k, scale, x, None))
+                     rotating([lambda x, q=q_: prefill.dequant_linear(q, _lib.CODE_E4M3, n, k, scale, x, None)
+                               for q_ in qss]))
             routes = {r: {"dequant": route} for r in self.calibration_rows if r in prefill.PREFILL_BUCKETS}
         accept, table, report = calibrate_buckets(
             "fp8_wo", n, k, weight.dtype, weight.device, self.calibration_rows, max(1, self.calibration_batch),
-            _fp8w_candidates, lambda x, a: ops.fp8w_gemm_strips(x, qs, n, scale, None, a),
-            lambda x: F.linear(x, weight, None), routes, timer=self.timer, keep_reference=self.keep_reference_routes)
+            _fp8w_candidates, rotating([lambda x, a, q=q_: ops.fp8w_gemm_strips(x, q, n, scale, None, a) for q_ in qss]),
+            rotating([lambda x, w=w_: F.linear(x, w, None) for w_ in ws]), routes, timer=self.timer,
+            keep_reference=self.keep_reference_routes, inner=copies)
+        del qss, ws
         self.calibration_report[(n, k)] = report
         return accept, table
 

@@ -31,7 +31,7 @@ import torch.nn.functional as F
 from .. import _lib, ops
 from . import prefill
 from .base import QuantMethodBase
-from .calibrate import ALGO_REFERENCE_GEMM, calibrate_buckets
+from .calibrate import ALGO_REFERENCE_GEMM, calibrate_buckets, rotating, rotation
 from .kernels import kernel_available
 
 logger = logging.getLogger("qtts_amd.quant.int8")
@@ -121,7 +121,8 @@ class Int8WeightOnlyMethod(QuantMethodBase):
     name = "int8_weight_only"
 
     def __init__(self, calibrate: bool = True, calibration_batch: int = 16, div_mode: int = _lib.DIV_DEVICE,
-                 calibration_rows: tuple[int, ...] = M_BUCKETS, timer=None, keep_reference_routes: bool = True) -> None:
+                 calibration_rows: tuple[int, ...] = M_BUCKETS, timer=None, keep_reference_routes: bool = True,
+                 rotate_weights: bool = True) -> None:
         available, reason = kernel_available()
         if not available:
             raise RuntimeError(f"int8 weight-only needs the gfx950 fused kernel: {reason}")
@@ -132,6 +133,9 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         #: Keep a converted layer's weight for the buckets where F.linear on it beat every
         #: quantized route (else those buckets run the fastest quantized route anyway).
         self.keep_reference_routes = keep_reference_routes
+        #: Time each shape over copies of its weight that together exceed the L2s (calibrate.rotation),
+        #: as the weights stream in a decode step, rather than one weight's repeated calls.
+        self.rotate_weights = rotate_weights
         #: (N, K) -> per-bucket timings of the last calibration (calibrate_buckets' report)
         self.calibration_report: dict[tuple[int, int], dict] = {}
         self.div_mode = div_mode
@@ -158,20 +162,25 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         ops.reserve_workspace(weight.device, max(ops.workspace_bytes(_lib.OP_W8A16, r, n, k, a)
                                                  for r in self.calibration_rows
                                                  for a in _candidates(r, kk).values()))
+        copies = rotation(n * k) if self.rotate_weights else 1
+        qs = [q] + [q.clone() for _ in range(copies - 1)]
+        ws = [weight] + [weight.detach().clone() for _ in range(copies - 1)]
         if strips:
-            kernel = lambda x, a: ops.w8a16_gemm_strips(x, q, n, scale, None, a)  # noqa: E731
+            kernel = rotating([lambda x, a, q=q_: ops.w8a16_gemm_strips(x, q, n, scale, None, a) for q_ in qs])
         else:
-            kernel = lambda x, a: ops.w8a16_gemm(x, q, scale, None, a)  # noqa: E731
+            kernel = rotating([lambda x, a, q=q_: ops.w8a16_gemm(x, q, scale, None, a) for q_ in qs])
         routes = {}
         if strips and any(r in prefill.PREFILL_BUCKETS for r in self.calibration_rows):
             prefill.reserve(weight.device, n, k, weight.dtype)
             route = (prefill.ALGO_DEQUANT_GEMM,
-                     lambda x: prefill.dequant_linear(q, _lib.CODE_INT8, n, k, scale, x, None))
+                     rotating([lambda x, q=q_: prefill.dequant_linear(q, _lib.CODE_INT8, n, k, scale, x, None)
+                               for q_ in qs]))
             routes = {r: {"dequant": route} for r in self.calibration_rows if r in prefill.PREFILL_BUCKETS}
         accept, table, report = calibrate_buckets(
             "int8_wo", n, k, weight.dtype, weight.device, self.calibration_rows, max(1, self.calibration_batch),
-            lambda rows: _candidates(rows, kk), kernel, lambda x: F.linear(x, weight, None), routes,
-            timer=self.timer, keep_reference=self.keep_reference_routes)
+            lambda rows: _candidates(rows, kk), kernel, rotating([lambda x, w=w_: F.linear(x, w, None) for w_ in ws]),
+            routes, timer=self.timer, keep_reference=self.keep_reference_routes, inner=copies)
+        del qs, ws
         self.calibration_report[(n, k)] = report
         return accept, table
 
