@@ -74,6 +74,14 @@ def _oracle_w8a16(x, q, scale, b):
                        None if b is None else b.float().cpu().numpy())
 
 
+def _sample_rows(m: int) -> torch.Tensor:
+    """Rows of a large-M output checked against the fp64 oracle: the first and last, both sides of
+    every 64- and 128-row tile edge up to 256, and about 20 more spread over M."""
+    rows = {0, m - 1} | {r for e in (32, 64, 128, 256) for r in (e - 1, e) if r < m}
+    rows |= set(range(1, m, max(1, m // 20)))
+    return torch.tensor(sorted(rows), device="cuda")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 def test_w8a16_brute_force_small(ops, dtype):
     """Tails in M, N and K, bias on and off, every dtype; includes the generic path (K % 16 != 0)."""
@@ -371,6 +379,10 @@ def test_fp8_strips_vs_oracle(ops, n, k):
             ref = ((qx.float() * sx[:, None]) @ (qw.float() * sw[:, None]).t()).double().cpu().numpy()
         y = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, None, torch.bfloat16)
         assert_close(y, ref, f"fp8 strips m={m} n={n} k={k}")
+        if m > 64:  # and the fp64 oracle itself on a sample of the rows
+            idx = _sample_rows(m)
+            assert_close(y[idx], _oracle_w8a8(qx[idx].contiguous(), sx[idx].contiguous(), qw, sw, None)[0],
+                         f"fp8 strips m={m} n={n} k={k} oracle")
         if m <= 16:
             for splits, waves in ((1, 4), (2, 8), (4, 16)):
                 y2 = ops.w8a8_fp8_gemm_strips(qx, sx, qws, n, sw, None, torch.bfloat16, ops.algo_code(1, splits, waves))
@@ -468,6 +480,9 @@ def test_w8a16_strips_prefill_vs_fp32(ops, n, k):
         if b is not None:
             ref = ref + b.float()
         assert_close(y, ref.double().cpu().numpy(), f"strips prefill m={m} n={n} k={k}")
+        # and the fp64 oracle itself on a sample of the rows (every tile edge up to 256 among them)
+        idx = _sample_rows(m)
+        assert_close(y[idx], _oracle_w8a16(x[idx].contiguous(), q, s, b), f"strips prefill m={m} n={n} k={k} oracle")
 
 
 def test_w8a16_strips_tile_graph_replays_split(ops):
