@@ -493,36 +493,62 @@ def run_prefill(args, torch, ops):
             "shapes": res}
 
 
+def streamed_times(torch, args, calls: dict) -> dict:
+    """ms per call of each entry of ``calls`` (name -> list of callables, one per layer's distinct
+    weight): one graph per name over the whole list, median of rotating rounds."""
+    gs = {nm: capture(torch, lambda fs=fs: [f() for f in fs]) for nm, fs in calls.items()}
+    tm = time_rounds(torch, gs, args.steps, args.warmup)
+    del gs
+    return {nm: tm[nm] / len(calls[nm]) for nm in calls}
+
+
 def run_fp8(args, torch, ops):
-    """fp8 W8A8 on the talker shapes, M in {1, 8, 256}, x with 1% outliers at 20 sigma."""
-    stack = make_stack(torch, ops, TALKER, 1, keep_bf16=True, fp8=True)
+    """fp8 W8A8 on the talker shapes, M in {1, 8, 256}, x with 1% outliers at 20 sigma.
+    Each shape two ways: 10 calls on one weight in a graph (the weight resident in the caches, for
+    every path), and ``streamed``: one call on each of the 28 talker layers' distinct weights in a
+    graph, as a decode step streams them (per call; 28 x the weight is past the L2s and, but for qkv
+    and o, past the Infinity Cache)."""
+    layers = 28
+    stack = make_stack(torch, ops, TALKER, layers, keep_bf16=True, fp8=True)
     ops.reserve_workspace(torch.device("cuda"), 64 << 20)
     res = {}
     for m in (1, 8, 256):
         xs = make_inputs(torch, [2048, 6144], [m], outliers=True)
-        for e in stack:
+        for e in stack[:4]:
             fq = lambda e=e: ops.fp8_linear_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"])
             fb = lambda e=e: torch.nn.functional.linear(xs[(m, e["k"])], e["w_bf16"])
             tm = time_rounds(torch, {"q": capture(torch, lambda: [fq() for _ in range(10)]),
                                      "b": capture(torch, lambda: [fb() for _ in range(10)])}, args.steps, args.warmup)
             tq, tb = tm["q"] / 10, tm["b"] / 10
+            same = [d for d in stack if d["name"] == e["name"]]
+            ts = streamed_times(torch, args, {
+                "q": [lambda d=d: ops.fp8_linear_strips(xs[(m, d["k"])], d["qs"], d["n"], d["s"]) for d in same],
+                "b": [lambda d=d: torch.nn.functional.linear(xs[(m, d["k"])], d["w_bf16"]) for d in same]})
             nb = fp8_bytes(m, e["n"], e["k"])
-            res[f"M{m}_{e['name']}"] = {"us": round(tq * 1e3, 2), "bf16_us": round(tb * 1e3, 2),
-                                        "speedup": round(tb / tq, 3), "GBps": round(nb / (tq * 1e-3) / 1e9, 1)}
+            key = f"M{m}_{e['name']}"
+            res[key] = {"us": round(tq * 1e3, 2), "bf16_us": round(tb * 1e3, 2), "speedup": round(tb / tq, 3),
+                        "GBps": round(nb / (tq * 1e-3) / 1e9, 1), "streamed_us": round(ts["q"] * 1e3, 2),
+                        "streamed_bf16_us": round(ts["b"] * 1e3, 2), "streamed_speedup": round(ts["b"] / ts["q"], 3),
+                        "streamed_GBps": round(nb / (ts["q"] * 1e-3) / 1e9, 1)}
+            log(f"[bench] fp8 {key}: {res[key]}")
     return {"metric": "fp8 W8A8 linear us and GB/s", "value": None, "unit": "GB/s", "n_gpus": 1,
-            "config": {"workload": "configs[4]: talker shapes, fp8 W8A8, M in {1, 8, 256}"}, "shapes": res}
+            "config": {"workload": "configs[4]: talker shapes, fp8 W8A8, M in {1, 8, 256}; resident weights and "
+                                   "the 28 layers' distinct weights streamed"}, "shapes": res}
 
 
 def run_int8_w8a8(args, torch, ops):
     """int8 W8A8 (Int8Method) on the talker shapes, M in {1, 2, 4, 8, 64, 256, 1024}: the one-call
     linear (per-token quantization + int8 MFMA GEMM, one fused kernel for small decode batches)
-    against hipBLASLt bf16 and the W8A16 kernel on the same int8 codes."""
-    stack = make_stack(torch, ops, TALKER, 1, keep_bf16=True, f32_scale=True)
+    against hipBLASLt bf16 and the W8A16 kernel on the same int8 codes; each shape with its weight
+    resident (10 calls on one weight) and ``streamed`` (one call on each of the 28 talker layers'
+    distinct weights, as a decode step reads them)."""
+    layers = 28
+    stack = make_stack(torch, ops, TALKER, layers, keep_bf16=True, f32_scale=True)
     ops.reserve_workspace(torch.device("cuda"), 64 << 20)
     res = {}
     for m in (1, 2, 4, 8, 64, 256, 1024):
         xs = make_inputs(torch, [2048, 6144], [m], outliers=True)
-        for e in stack:
+        for e in stack[:4]:
             x = xs[(m, e["k"])]
             s_b = e["s"].to(torch.bfloat16)
             fq = lambda e=e, x=x: ops.int8_linear_strips(x, e["qs"], e["n"], e["s"])
@@ -532,13 +558,21 @@ def run_int8_w8a8(args, torch, ops):
             tm = time_rounds(torch, gs, args.steps, args.warmup)
             del gs
             tq, tw, tb = tm["q"] / 10, tm["w"] / 10, tm["b"] / 10
+            same = [d for d in stack if d["name"] == e["name"]]
+            ts = streamed_times(torch, args, {
+                "q": [lambda d=d: ops.int8_linear_strips(x, d["qs"], d["n"], d["s"]) for d in same],
+                "b": [lambda d=d: torch.nn.functional.linear(x, d["w_bf16"]) for d in same]})
             fl = 2 * m * e["n"] * e["k"]
             nb = fp8_bytes(m, e["n"], e["k"])
-            res[f"M{m}_{e['name']}"] = {"us": round(tq * 1e3, 2), "w8a16_us": round(tw * 1e3, 2),
-                                        "bf16_us": round(tb * 1e3, 2), "speedup": round(tb / tq, 3),
-                                        "GBps": round(nb / (tq * 1e-3) / 1e9, 1),
-                                        "TOPs": round(fl / (tq * 1e-3) / 1e12, 1),
-                                        "int8_mfma_util": round(fl / (tq * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4)}
+            key = f"M{m}_{e['name']}"
+            res[key] = {"us": round(tq * 1e3, 2), "w8a16_us": round(tw * 1e3, 2),
+                        "bf16_us": round(tb * 1e3, 2), "speedup": round(tb / tq, 3),
+                        "GBps": round(nb / (tq * 1e-3) / 1e9, 1),
+                        "TOPs": round(fl / (tq * 1e-3) / 1e12, 1),
+                        "int8_mfma_util": round(fl / (tq * 1e-3) / 1e12 / INT8_PEAK_TOPS, 4),
+                        "streamed_us": round(ts["q"] * 1e3, 2), "streamed_bf16_us": round(ts["b"] * 1e3, 2),
+                        "streamed_speedup": round(ts["b"] / ts["q"], 3)}
+            log(f"[bench] int8 W8A8 {key}: {res[key]}")
     return {"metric": "int8 W8A8 linear us, GB/s and int8 MFMA utilisation", "value": None, "unit": "us",
             "n_gpus": 1, "config": {"workload": "talker shapes, int8 W8A8 (Int8Method), M in {1, 2, 4, 8, 64, 256, 1024}"},
             "shapes": res}
