@@ -226,3 +226,47 @@ def test_reference_route_keeps_weight_and_calls_f_linear(ops, monkeypatch):
     method2 = I.Int8WeightOnlyMethod(calibrate=True, calibration_rows=(1, 8, 256), keep_reference_routes=False)
     method2.process_weights(lin2)
     assert lin2.quant_algos[256] >= 0 and lin2.weight.numel() == 0
+
+
+def test_calibrated_half_strips_reach_the_kernel(ops, monkeypatch):
+    """A talker down_proj whose calibration finds half strips fastest at the decode buckets (timings
+    forced on the host): its table holds the half-strip code there, and its calls run that kernel --
+    bit for bit the explicit half-strip call, and within the bar of the oracle -- with graph replays
+    equal to eager."""
+    from qtts_amd import _lib
+    from qtts_amd.quant import calibrate as cal, int8 as I
+
+    def fake_times(candidates, reference_call, *, key, use_graph=True, timer=None):
+        return 1.0, {name: (0.1 if name == "skinny_half" else 0.5) for name in candidates}
+
+    monkeypatch.setattr(cal, "time_candidates", fake_times)
+    n, k = 2048, 6144
+    lin = _layer(n, k, seed=6, bias=False)
+    method = I.Int8WeightOnlyMethod(calibrate=True, calibration_rows=(1, 2, 4, 8, 16))
+    method.process_weights(lin)
+    lin.quant_method = method
+    half = _lib.algo_code(_lib.ALGO_SKINNY_HALF)
+    assert all(lin.quant_algos[r] == half for r in (1, 2, 4, 8)) and lin.quant_algos[16] != half
+    q = I.int8_weight_rowmajor(lin)
+    for m in (1, 3, 8):
+        x = torch.randn(m, k, device="cuda").to(torch.bfloat16)
+        y = lin(x)
+        assert torch.equal(y, ops.w8a16_gemm_strips(x, lin.int8_weight, n, lin.int8_scale, None, half)), m
+        ref = O.w8a16_ref(x.float().cpu().numpy(), q.cpu().numpy(), lin.int8_scale.float().cpu().numpy())
+        err = np.abs(y.double().cpu().numpy() - ref)
+        assert (err <= _bound(ref, torch.bfloat16)).all(), (m, float(err.max()))
+    static_x = torch.randn(4, k, device="cuda").to(torch.bfloat16)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        lin(static_x)
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = lin(static_x)
+    for i in range(3):
+        static_x.copy_(torch.randn(4, k, device="cuda").to(torch.bfloat16))
+        lin(static_x * 0.5)  # eager work between replays
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, lin(static_x)), f"replay {i}"

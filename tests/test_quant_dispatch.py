@@ -343,3 +343,18 @@ def test_calibrate_buckets_inner_calls_reach_the_timer_key():
     calibrate.calibrate_buckets("k", 8, 8, torch.float32, torch.device("cpu"), (1,), 1, candidates, kernel, reference,
                                 timer=timer, inner=32)
     assert len(calls) > n   # timed again: another key
+
+
+def test_decode_candidates_include_the_automatic_choice_and_half_strips():
+    """Decode buckets time the automatic choice (which takes row-split strips where whole strips leave
+    compute units idle) and, on strip weights with K a multiple of 128, half strips explicitly."""
+    from qtts_amd import _lib
+    from qtts_amd.quant.fp8 import _fp8w_candidates
+    from qtts_amd.quant.int8 import _candidates
+    for rows in (1, 2, 4, 8):
+        c = _candidates(rows, 6144)
+        assert c["auto"] == _lib.ALGO_AUTO and c["skinny_half"] == _lib.algo_code(_lib.ALGO_SKINNY_HALF)
+        assert "skinny_half" not in _candidates(rows, 6144 + 64) and "skinny_half" not in _candidates(rows)
+        assert _fp8w_candidates(rows)["auto"] == _lib.ALGO_AUTO
+    for rows in (16, 32, 256):
+        assert "auto" not in _candidates(rows, 6144) and "skinny_half" not in _candidates(rows, 6144)
