@@ -85,7 +85,14 @@ def test_gate_up_silu_matches_separate_and_oracle(ops, n, k):
                 gu = ops.w8a16_fused_gemm_strips(x, qs, n, s, bias, prologue=pro, norm_weight=nw, eps=EPS, algo=cfg)
                 sep = ops.silu_mul(gu)
                 assert torch.equal(act8, sep), (what, int((act8 != sep).sum()))
-                # the automatic configuration (twice the waves, half the chunks) within tolerance below
+                if m <= 8:
+                    # half strips (8 gate rows and their 8 up rows a workgroup, the plain GEMM's grid): bit
+                    # for bit the separate calls at the same configuration too
+                    half = ops.algo_code(3, 0, max(1, (k // 64) // 8), 8)
+                    act_h = ops.w8a16_gate_up_silu_strips(x, qs, n, s, bias, prologue=pro, norm_weight=nw, eps=EPS,
+                                                          algo=half)
+                    assert torch.equal(act_h, sep), (what, "half strips", int((act_h != sep).sum()))
+                # the automatic configuration (half strips up to 8 rows) within tolerance below
                 act = ops.w8a16_gate_up_silu_strips(x, qs, n, s, bias, prologue=pro, norm_weight=nw, eps=EPS)
                 # the oracle on the same GEMM input (normalized rows as the kernel stages them)
                 if pro == PRO_RMS_NORM:

@@ -677,7 +677,7 @@ int qtts_w8a16_gate_up_silu_strips(const void* x, int x_dtype, int64_t m, int64_
   QTTS_REQUIRE(x_dtype == QTTS_BF16 || x_dtype == QTTS_F16,
                "w8a16_gate_up_silu_strips: activations must be bf16 or fp16");
   QTTS_REQUIRE(dtype_ok(scale_dtype), "w8a16_gate_up_silu_strips: bad scale dtype code");
-  QTTS_REQUIRE(algo_ok(algo), "w8a16_gate_up_silu_strips: bad algo %d", algo);
+  QTTS_REQUIRE(algo_ok_rows(algo), "w8a16_gate_up_silu_strips: bad algo %d", algo);
   QTTS_REQUIRE(prologue == QTTS_PRO_NONE || prologue == QTTS_PRO_RMS_NORM,
                "w8a16_gate_up_silu_strips: prologue must be none or RMSNorm, got %d", prologue);
   QTTS_REQUIRE(k % 64 == 0, "w8a16_gate_up_silu_strips: K %% 64 != 0 (K=%lld)", (long long)k);

@@ -68,6 +68,14 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 //   to two MFMAs, and the workgroup stores y[:, c] = XT(XT(silu(g)) * u) for g, u the
 //   linear's outputs of columns c and c + N/2 rounded to XT: y is [M, N/2].  The
 //   gate_up output itself is never stored.
+// PAIR with SUB = 2 (staged rows, up to 8 of them, no split): the gate_up GEMM on half strips.
+//   Workgroup p takes gate rows [8p, 8p + 8) and the matching up rows N/2 + [8p, 8p + 8) as the 16
+//   rows of its MFMA A operand (lanes of rows 0-7 load the gate strip's half, rows 8-15 the up
+//   strip's), so one accumulator holds both and the grid has the plain GEMM's N/16 workgroups
+//   (the two-strip PAIR has N/32, each with twice the bytes).  Each output element sums the
+//   same K chunks in the same order as the plain GEMM's, so the result equals the GEMM followed
+//   by the activation bit for bit at the same wave configuration; lane (j, g) for g < 2 takes
+//   the up value of lane (j, g + 2), i.e. lane ^ 32, in the epilogue.
 // SUB > 1 (staged rows, M <= 16 / SUB, no split, no PAIR): row-split strips.  SUB
 //   workgroups share each 16-row strip, workgroup p taking weight rows
 //   [p * RP, (p + 1) * RP) of it (RP = 16 / SUB), so a layer of few strips still spreads
@@ -98,14 +106,18 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   static_assert(PRO == kProNone || MX > 0, "a prologue runs on staged rows");
   static_assert(!RES || MX > 0, "the residual epilogue is built with staged rows");
   static_assert(!PAIR || (MX > 0 && !RES && PRO != kProSiluMul), "the SiLU pair epilogue runs on staged rows");
-  static_assert(SUB == 1 || ((SUB == 2 || SUB == 4) && MX > 0 && MX <= 16 / SUB && !PAIR),
+  static_assert(SUB == 1 || ((SUB == 2 || SUB == 4) && MX > 0 && MX <= 16 / SUB && !PAIR) ||
+                    (PAIR && SUB == 2 && MX > 0 && MX <= 8),
                 "row-split strips run on staged rows, at most 16 / SUB of them");
-  constexpr int RP = 16 / SUB;  // weight rows per workgroup
+  constexpr bool PH = PAIR && SUB == 2;  // the gate_up GEMM on half strips: 8 gate + 8 up rows
+  constexpr bool P2 = PAIR && !PH;       // the two-strip pair: a gate strip and its up strip
+  constexpr int CS = PH ? 1 : SUB;       // chunks one MFMA covers (a unit)
+  constexpr int RP = 16 / SUB;  // weight rows per workgroup (PH: gate rows)
   constexpr bool SILU = PRO == kProSiluMul, NORM = PRO == kProRmsNorm;
-  constexpr int NA = PAIR ? 2 : 1;  // accumulators a wave carries: gate (and up)
+  constexpr int NA = P2 ? 2 : 1;  // accumulators a wave carries: gate (and up)
   __shared__ f32x4_t red[W > 1 ? W - 1 : 1][MB * NA][64];
   __shared__ float nss[NORM ? W : 1][NORM ? MX : 1];
-  __shared__ __align__(16) uint16_t xrow[MX > 0 ? W : 1][MX > 0 ? MX : 1][MX > 0 ? CPW * SUB * 64 : 8];
+  __shared__ __align__(16) uint16_t xrow[MX > 0 ? W : 1][MX > 0 ? MX : 1][MX > 0 ? CPW * CS * 64 : 8];
 
   // Grid: x = output strips (times SUB, rounded up to a multiple of 8), y = K splits.  Workgroups are
   // dealt to the 8 XCDs round-robin in x-fastest order, so with gridDim.x % 8 == 0 every
@@ -127,7 +139,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   // This workgroup's units of SUB chunks (SUB divides nchunks, checked by the host): split
   // `split` of S of ceil(units / S) units each (the host's split size:
   // ceil(n / ceil(n / ceil(n / s))) = ceil(n / s)).
-  int c0 = 0, c1 = SUB == 1 ? nchunks : nchunks / SUB;
+  int c0 = 0, c1 = CS == 1 ? nchunks : nchunks / CS;
   if (SUB == 1 && S > 1) {
     const int cps = (nchunks + S - 1) / S;
     c0 = split * cps;
@@ -138,9 +150,15 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
 
   const int8_t* wp;
   int64_t wstride;
-  // PAIR: the up strip is strip + strips (strips = the gate strips, N/32).
-  const int64_t up_off = PAIR ? (int64_t)strips * nchunks * 1024 : 0;
-  if constexpr (LAYOUT == kLayoutStrips && SUB > 1) {
+  // P2: the up strip is strip + strips (strips = the gate strips, N/32).
+  const int64_t up_off = P2 ? (int64_t)strips * nchunks * 1024 : 0;
+  if constexpr (PH) {
+    // lane (r, g): gate row 16 strip + part_row + r % 8 (r < 8) or the up row N/2 above it,
+    // bytes 16 g .. + 15 of each chunk (N % 32 == 0: both halves sit in whole strips)
+    const int R = strip * 16 + part_row + (r & 7) + (r < 8 ? 0 : (N >> 1));
+    wp = q + (int64_t)(R >> 4) * nchunks * 1024 + ((R & 15) + 16 * g) * 16;
+    wstride = 1024;
+  } else if constexpr (LAYOUT == kLayoutStrips && SUB > 1) {
     // lane (r, g): strip row part_row + r % RP of chunk r / RP of each unit, bytes 16 g .. + 15
     wp = q + (int64_t)strip * nchunks * 1024 + (r / RP) * 1024 + (part_row + r % RP + 16 * g) * 16;
     wstride = SUB * 1024;
@@ -161,14 +179,14 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   // A group of CPW chunks is issued in full before any of it is consumed.  With
   // FULLK (K % 64 == 0, strip layout) the loads are branch-free: chunk indices past
   // the wave's range are clamped to its last chunk (consume zeroes their weights).
-  i32x4_t w[CPW], wu[PAIR ? CPW : 1], xa[MB][CPW], xb[MB][CPW];
+  i32x4_t w[CPW], wu[P2 ? CPW : 1], xa[MB][CPW], xb[MB][CPW];
   auto issue = [&](int base) {
 #pragma unroll
     for (int u = 0; u < CPW; ++u) {
       if constexpr (FULLK) {
         const int c = min(base + u, wc1 - 1);
         w[u] = *(const i32x4_t*)(wp + (int64_t)c * wstride);
-        if constexpr (PAIR) wu[u] = *(const i32x4_t*)(wp + up_off + (int64_t)c * wstride);
+        if constexpr (P2) wu[u] = *(const i32x4_t*)(wp + up_off + (int64_t)c * wstride);
         if constexpr (MX == 0) {
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) {
@@ -187,10 +205,10 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       }
     }
   };
-  f32x4_t acc[MB], up[PAIR ? MB : 1];  // PAIR: up holds the up strip's sums
+  f32x4_t acc[MB], up[P2 ? MB : 1];  // P2: up holds the up strip's sums
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  if constexpr (PAIR) up[0] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if constexpr (P2) up[0] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   auto consume = [&](int base) {
 #pragma unroll
     for (int u = 0; u < CPW; ++u) {
@@ -201,7 +219,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
         const i32x4_t wv = live ? w[u] : zero;
         const V wlo = wcvt<F8W, XT>((uint32_t)wv[0], (uint32_t)wv[1]);
         const V whi = wcvt<F8W, XT>((uint32_t)wv[2], (uint32_t)wv[3]);
-        if constexpr (PAIR) {  // the up strip's chunk on the same B operands, in the same order
+        if constexpr (P2) {  // the up strip's chunk on the same B operands, in the same order
           const i32x4_t uv = live ? wu[u] : zero;
           const V ulo = wcvt<F8W, XT>((uint32_t)uv[0], (uint32_t)uv[1]);
           const V uhi = wcvt<F8W, XT>((uint32_t)uv[2], (uint32_t)uv[3]);
@@ -229,15 +247,17 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   // 0.1-0.2 us a launch slower on the talker linears: the LDS staging of the rows waits on
   // every outstanding scalar load, and those miss to HBM like the weights.)
   uint32_t sc[4] = {0u, 0u, 0u, 0u}, bi[4] = {0u, 0u, 0u, 0u}, rb[RES ? 4 : 1] = {0u};
-  uint32_t su[PAIR ? 4 : 1] = {0u}, bu[PAIR ? 4 : 1] = {0u};  // PAIR: the up rows' scale and bias
+  uint32_t su[P2 ? 4 : 1] = {0u}, bu[P2 ? 4 : 1] = {0u};  // P2: the up rows' scale and bias
   auto issue_epilogue = [&]() {
     const XT* bsrc = bias ? bias : y;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int nn = min(strip * 16 + part_row + 4 * g + i, N - 1);
+      // PH: lane (r, g) holds D rows 4 g .. + 3: gate rows for g < 2, the matching up rows above
+      const int nn = PH ? strip * 16 + part_row + 4 * (g & 1) + i + (g < 2 ? 0 : (N >> 1))
+                        : min(strip * 16 + part_row + 4 * g + i, N - 1);
       sc[i] = load_bits(scale + nn);
       bi[i] = load_bits(bsrc + nn);
-      if constexpr (PAIR) {
+      if constexpr (P2) {
         const int nu = min(nn + (N >> 1), N - 1);
         su[i] = load_bits(scale + nu);
         bu[i] = load_bits(bsrc + nu);
@@ -248,9 +268,9 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
 
   // Staged activation rows (MX > 0): vector v of lane l holds elements
   // 512 v + 8 l .. + 7 of the wave's K range of each row (XV vectors cover CPW
-  // units of SUB chunks); lanes past the range repeat its last 8 elements.
-  constexpr int XV = (CPW * SUB * 64 + 511) / 512;
-  const int xlen = (wc1 - wc0) * SUB * 64, xbeg = wc0 * SUB * 64;  // the wave's K range, elements
+  // units of CS chunks); lanes past the range repeat its last 8 elements.
+  constexpr int XV = (CPW * CS * 64 + 511) / 512;
+  const int xlen = (wc1 - wc0) * CS * 64, xbeg = wc0 * CS * 64;  // the wave's K range, elements
   // SILU: xu holds the up half; NORM: xu[0] holds the norm weight over the same range.
   i32x4_t xr[MX > 0 ? MX : 1][XV], xu[SILU ? MX : 1][SILU || NORM ? XV : 1];
   auto issue_x = [&]() {
@@ -323,12 +343,12 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       // B operand of lane (r, g): row r (rows >= M read row 0; their D columns are
       // never stored), elements 64 u + 16 g .. + 15 of chunk u of the range.  SUB > 1:
       // row r % RP of chunk r / RP of unit u.
-      const int rj = SUB == 1 ? r : r % RP;
+      const int rj = CS == 1 ? r : r % RP;
       const int rr = rj < M ? rj : 0;
 #pragma unroll
       for (int u = 0; u < CPW; ++u) {
         const int cu = min(u, wc1 - wc0 - 1);
-        const int ch = SUB == 1 ? cu : cu * SUB + r / RP;
+        const int ch = CS == 1 ? cu : cu * SUB + r / RP;
         xa[0][u] = *(const i32x4_t*)&xrow[wave][rr][64 * ch + 16 * g];
         xb[0][u] = *(const i32x4_t*)&xrow[wave][rr][64 * ch + 16 * g + 8];
       }
@@ -374,7 +394,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     if (wave > 0) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) red[wave - 1][mb][lane] = acc[mb];
-      if constexpr (PAIR) red[wave - 1][1][lane] = up[0];
+      if constexpr (P2) red[wave - 1][1][lane] = up[0];
     }
     __syncthreads();
     if (wave > 0) return;
@@ -382,7 +402,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     for (int w = 0; w < W - 1; ++w) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) acc[mb] += red[w][mb][lane];
-      if constexpr (PAIR) up[0] += red[w][1][lane];
+      if constexpr (P2) up[0] += red[w][1][lane];
     }
   }
 
@@ -398,7 +418,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     inv_r = __shfl(1.0f / __builtin_sqrtf(ss / (float)K + eps), r, 64);
   }
 
-  if constexpr (SUB == 2) {
+  if constexpr (SUB == 2 && !PAIR) {
     // D rows 8 + i, columns 8 + j (chunk 1 of each unit) onto rows i, columns j (chunk 0):
     // lane (j, g) for g < 2 takes lane (j + 8, g + 2), i.e. lane ^ 40.
 #pragma unroll
@@ -426,6 +446,23 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     for (int mb = 0; mb < MB; ++mb) acc[mb] = f32x4_t{a[4 * mb], a[4 * mb + 1], a[4 * mb + 2], a[4 * mb + 3]};
   }
 
+  if constexpr (PH) {
+    // lanes g < 2: gate rows 8p + 4 g + i; lanes g >= 2 the up rows N/2 above them.  Every lane
+    // scales and rounds its own (as the plain GEMM's output), then lane (j, g < 2) takes its up
+    // value from lane ^ 32 and writes XT(XT(silu(g)) * u).
+    const int m = r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v = (NORM ? acc[0][i] * inv_r : acc[0][i]) * bits_to_f32<ST>(sc[i]);
+      if (bias) v += bits_to_f32<XT>(bi[i]);
+      v = round_through<XT>(v);
+      const float u = __shfl_xor(v, 32, 64);
+      const int nn = strip * 16 + part_row + 4 * g + i;
+      if (g < 2 && m < M && nn < (N >> 1)) y[(int64_t)m * ldy + nn] = from_f32<XT>(silu_mul<XT>(v, u));
+    }
+    return;
+  }
+
   // D layout of the 16x16 MFMA: lane (r, g) holds rows 4g..4g+3 (weight rows n) of
   // column r (activation row m = r + 16 mb).
 #pragma unroll
@@ -439,7 +476,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
           float v = (NORM ? acc[mb][i] * inv_r : acc[mb][i]) * bits_to_f32<ST>(sc[i]);
           if (bias) v += bits_to_f32<XT>(bi[i]);
           if constexpr (RES) v = bits_to_f32<XT>(rb[i]) + round_through<XT>(v);
-          if constexpr (PAIR) {
+          if constexpr (P2) {
             float u = (NORM ? up[0][i] * inv_r : up[0][i]) * bits_to_f32<ST>(su[i]);
             if (bias) u += bits_to_f32<XT>(bu[i]);
             v = silu_mul<XT>(round_through<XT>(v), round_through<XT>(u));

@@ -71,12 +71,22 @@ int launch_fused_wc(const FusedArgs& a) {
   return 0;
 }
 
-// The SiLU-pair variants (PAIR): each wave carries both strips' chunks.  Built: 2, 4,
-// 8 and 16 waves of 4 chunks (the automatic choice: as many waves as the plain GEMM
-// of the same K would run, each with half its chunks, so the same weight bytes per
-// wave), and 1, 2, 4 and 8 waves of 8 chunks.
+// The SiLU-pair variants (PAIR).  Two-strip (a gate strip and its up strip a workgroup, each
+// wave carrying both strips' chunks): 2, 4, 8 and 16 waves of 4 chunks and 1, 2, 4 and 8 waves
+// of 8 chunks.  Half strips (sub = 2: 8 gate rows and their up rows a workgroup): 1, 2, 4 and 8
+// waves of 8 chunks, the plain GEMM's automatic choices up to K = 4096.
 template <typename XT, typename ST, int MX, int PRO>
 int launch_pair_wc(const FusedArgs& a) {
+  if (a.sub == 2) {  // half strips (skinny.h: PAIR with SUB = 2), the plain GEMM's configurations
+    switch (a.c.waves * 64 + a.c.cpw) {
+      case 1 * 64 + 8: launch_fused_one<XT, ST, 1, 8, MX, PRO, false, true, 2>(a); break;
+      case 2 * 64 + 8: launch_fused_one<XT, ST, 2, 8, MX, PRO, false, true, 2>(a); break;
+      case 4 * 64 + 8: launch_fused_one<XT, ST, 4, 8, MX, PRO, false, true, 2>(a); break;
+      case 8 * 64 + 8: launch_fused_one<XT, ST, 8, 8, MX, PRO, false, true, 2>(a); break;
+      default: return 1;
+    }
+    return 0;
+  }
   switch (a.c.waves * 64 + a.c.cpw) {
     case 2 * 64 + 4: launch_fused_one<XT, ST, 2, 4, MX, PRO, false, true>(a); break;
     case 4 * 64 + 4: launch_fused_one<XT, ST, 4, 4, MX, PRO, false, true>(a); break;
@@ -89,6 +99,9 @@ int launch_pair_wc(const FusedArgs& a) {
     default: return 1;
   }
   return 0;
+}
+inline bool pair_half_built(int waves, int cpw) {
+  return cpw == 8 && (waves == 1 || waves == 2 || waves == 4 || waves == 8);
 }
 inline bool pair_built(int waves, int cpw) {
   return (cpw == 4 && (waves == 2 || waves == 4 || waves == 8 || waves == 16)) ||

@@ -200,7 +200,44 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
   const int splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff, cpw = (algo >> 24) & 0x3f;
   const int64_t m = in.m, n = in.n, k = in.k;
   if (pair) {
-    if (splits > 1 || m > 8 || n % 32) return 1;
+    const int family = algo & 0xff;
+    if (splits > 1 || m > 8 || n % 32 || family == QTTS_ALGO_SKINNY_QUARTER) return 1;
+    // Half strips: each workgroup's MFMA operand holds 8 gate rows and their 8 up rows, so the
+    // grid and the wave configuration are the plain GEMM's (N/16 workgroups); requested by
+    // family, and the automatic choice without a prologue or with more than 256 gate strips.
+    // Measured over 28 distinct weights (µs a call, two-strip -> half strips, M = 1 / 8): the
+    // talker's gate_up 8.10 -> 6.92 / 8.79 -> 7.97, with the RMSNorm prologue 8.20 -> 7.19 /
+    // 10.32 -> 9.97; the code predictor's 4.36 -> 4.16 / 4.55 -> 4.41, but with the prologue
+    // 4.37 -> 4.42 / 5.50 -> 5.82 (every workgroup repeats the norm's per-row work, and its 192
+    // two-strip workgroups leave fewer of it).
+    const bool auto_half = family == QTTS_ALGO_AUTO && (pro == kProNone || n / 32 > 256);
+    if (family == QTTS_ALGO_SKINNY_HALF || auto_half) {
+      const SkinnyCfg c = skinny_cfg(m, n, k, 1, waves, cpw);
+      if (c.S == 1 && pair_half_built(c.waves, c.cpw) && in.ldx <= INT32_MAX) {
+        FusedArgs a = in;
+        a.c = c;
+        a.sub = 2;
+        a.blocks = (unsigned)(((int64_t)c.strips + 7) / 8 * 8);
+        a.counters = nullptr;
+        a.part = nullptr;
+        const bool f32s = sdt == QTTS_F32;
+        const int mx = m <= 2 ? (int)m : (m <= 4 ? 4 : 8);
+        int rc;
+        if (pro == kProRmsNorm)
+          rc = mx == 1 ? launch_fused<kProRmsNorm, false, 1, true>(x_dtype, f32s, a)
+                       : mx == 2 ? launch_fused<kProRmsNorm, false, 2, true>(x_dtype, f32s, a)
+                       : (mx == 4 ? launch_fused<kProRmsNorm, false, 4, true>(x_dtype, f32s, a)
+                                  : launch_fused<kProRmsNorm, false, 8, true>(x_dtype, f32s, a));
+        else
+          rc = mx == 1 ? launch_fused<kProNone, false, 1, true>(x_dtype, f32s, a)
+                       : mx == 2 ? launch_fused<kProNone, false, 2, true>(x_dtype, f32s, a)
+                       : (mx == 4 ? launch_fused<kProNone, false, 4, true>(x_dtype, f32s, a)
+                                  : launch_fused<kProNone, false, 8, true>(x_dtype, f32s, a));
+        if (rc == 0) return qtts_check_launch("w8a16_gate_up_silu_half");
+      }
+      if (family == QTTS_ALGO_SKINNY_HALF) return 1;  // the separate path runs it
+    }
+    if (family == QTTS_ALGO_SKINNY_HALF) return 1;
     SkinnyCfg c = skinny_cfg(m, n / 2, k, 1, waves, cpw);  // one workgroup per gate strip
     // Automatic, without a prologue: twice the plain choice's waves with half its chunks
     // each (measured 4% faster on the talker gate_up at M = 1..8).  With the RMSNorm
