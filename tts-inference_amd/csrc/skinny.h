@@ -290,43 +290,38 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       }
     }
   };
-  // NORM, before the barrier: this wave's sum of x^2 over its range for row m (fp32,
-  // lane partials over its vectors in element order, then the wave's butterfly).
-  auto norm_partial = [&](int m) {
-    float ss = 0.0f;
-#pragma unroll
-    for (int v = 0; v < XV; ++v) {
-      if (512 * v + 8 * lane < xlen) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t p = (uint32_t)xr[m][v][e];
-          const float a = to_f32(XT{(uint16_t)p}), b = to_f32(XT{(uint16_t)(p >> 16)});
-          ss = __builtin_fmaf(a, a, ss);
-          ss = __builtin_fmaf(b, b, ss);
-        }
-      }
-    }
-    return wave_sum_rows(ss);
-  };
   // Writes the wave's staged rows to LDS (NORM: x * weight, rounded to XT; the row's
-  // inverse RMS comes in the epilogue) and reads the MFMA B operands back.
+  // inverse RMS comes in the epilogue) and reads the MFMA B operands back.  NORM also
+  // publishes this wave's sum of x^2 over its range for each row (fp32, lane partials over
+  // its vectors in element order, then the wave's butterfly), from the same converted
+  // elements: a pass of its own after the staging kept every converted row live until
+  // then (twice the registers at 8 rows, half the waves resident).
   auto stage_x = [&]() {
     if constexpr (NORM) {
+      float ss[MX];
+#pragma unroll
+      for (int m = 0; m < MX; ++m) ss[m] = 0.0f;
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
         const int e = min(512 * v + 8 * lane, xlen - 8);
+        const bool in = 512 * v + 8 * lane < xlen;  // lanes past the range repeat its last 8
 #pragma unroll
         for (int m = 0; m < MX; ++m) {
           i32x4_t o;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const uint32_t p = (uint32_t)xr[m][v][i], w2 = (uint32_t)xu[0][v][i];
-            const float h0 = to_f32(XT{(uint16_t)p}) * to_f32(XT{(uint16_t)w2});
-            const float h1 = to_f32(XT{(uint16_t)(p >> 16)}) * to_f32(XT{(uint16_t)(w2 >> 16)});
-            o[i] = (int)pack2_f32<XT>(h0, h1);
+            const float a = to_f32(XT{(uint16_t)p}), b = to_f32(XT{(uint16_t)(p >> 16)});
+            if (in) ss[m] = __builtin_fmaf(b, b, __builtin_fmaf(a, a, ss[m]));
+            o[i] = (int)pack2_f32<XT>(a * to_f32(XT{(uint16_t)w2}), b * to_f32(XT{(uint16_t)(w2 >> 16)}));
           }
           *(i32x4_t*)&xrow[wave][m][e] = o;
         }
+      }
+#pragma unroll
+      for (int m = 0; m < MX; ++m) {  // the row partials, published at the reduction below
+        const float t = wave_sum_rows(ss[m]);
+        if (lane == 0) nss[wave][m] = t;
       }
     } else if constexpr (MX > 0) {
 #pragma unroll
@@ -372,13 +367,6 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     // be in flight before the first wait.
     __builtin_amdgcn_sched_barrier(0);
     stage_x();  // waits for the activation rows only; the weights stay in flight
-    if constexpr (NORM) {
-#pragma unroll
-      for (int m = 0; m < MX; ++m) {  // the row partials, published at the reduction below
-        const float ss = norm_partial(m);
-        if (lane == 0) nss[wave][m] = ss;
-      }
-    }
     consume(wc0);
   } else {
     // A wave past the K range only adds zeros to the reduction and never reaches the epilogue
