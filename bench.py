@@ -289,10 +289,11 @@ def run_talker_stack(args, torch, ops):
     # the dispatches COLD_REPS x 28 + 1 .. + ROOFLINE_REPS x 28 of each M are exactly the timed ones
     # (bench.py --summarize-skip / --summarize-first).
     gate = [e for e in stack if e["name"] == "gate_up"]
-    cold_ms = kernel_ms(ops, [lambda e=e, m=m: ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"])
+    st = ops.ALGO_STREAM  # the stack's weight policy: 1.41 GB is past the Infinity Cache
+    cold_ms = kernel_ms(ops, [lambda e=e, m=m: ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"], None, st)
                               for m in ms for e in gate], reps=COLD_REPS)
     busy = kernel_ms_busy(torch, ops, {m: [lambda e=e, m=m: ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"],
-                                                                                   e["s"]) for e in gate]
+                                                                                   e["s"], None, st) for e in gate]
                                        for m in ms}, reps=ROOFLINE_REPS)
     flows, _ = layer_flows(torch, ops, stack, layers)
 
@@ -301,7 +302,7 @@ def run_talker_stack(args, torch, ops):
     total_ms = 0.0
     for m in ms:
         log(f"[bench] M={m}: capture + time int8 stack and bf16 stack")
-        g_q = capture(torch, lambda m=m: [ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"])
+        g_q = capture(torch, lambda m=m: [ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"], None, st)
                                           for e in stack])
         g_b = capture(torch, lambda m=m: [torch.nn.functional.linear(xs[(m, e["k"])], e["w_bf16"]) for e in stack])
         t_q = time_graph(torch, g_q, args.steps, args.warmup)
@@ -370,6 +371,8 @@ def run_talker_stack(args, torch, ops):
         "config": {"workload": "configs[1]: talker decode linear stack, 28 layers x {qkv,o,gate_up,down}, "
                                "int8 weight-only, one HIP graph per M", "layers": layers, "M": list(ms),
                    "int8_weight_bytes": int8_bytes, "parallelism": "none (1 GPU)",
+                   "weight_policy": "stream (QTTS_ALGO_STREAM: non-temporal weight loads, as quantize_module picks "
+                                    "for a submodel whose codes exceed the 256 MiB Infinity Cache)",
                    "layer_flow": "per_m.layer_flow_*: the same 28 layers in the decode step's data flow "
                                  "(RMSNorm+qkv, o+residual, RMSNorm+gate_up+SiLU, down+residual fused into the "
                                  "int8 GEMMs) against bf16 torch (hipBLASLt F.linear, F.rms_norm, F.silu, adds); "
@@ -389,10 +392,11 @@ def run_single_linear(args, torch, ops):
     copies = 24
     stack = make_stack(torch, ops, [("gate_up", 12288, 2048)], copies, keep_bf16=False)
     xs = make_inputs(torch, [2048], [1])
-    g = capture(torch, lambda: [ops.w8a16_gemm_strips(xs[(1, 2048)], e["qs"], e["n"], e["s"]) for e in stack])
+    st = ops.ALGO_STREAM  # 24 copies, 604 MB: past the Infinity Cache
+    g = capture(torch, lambda: [ops.w8a16_gemm_strips(xs[(1, 2048)], e["qs"], e["n"], e["s"], None, st) for e in stack])
     t = time_graph(torch, g, args.steps, args.warmup)
     nbytes = copies * w8a16_bytes(1, 12288, 2048)
-    dur_ms = kernel_ms(ops, [lambda e=e: ops.w8a16_gemm_strips(xs[(1, 2048)], e["qs"], e["n"], e["s"])
+    dur_ms = kernel_ms(ops, [lambda e=e: ops.w8a16_gemm_strips(xs[(1, 2048)], e["qs"], e["n"], e["s"], None, st)
                              for e in stack], 2)
     per = w8a16_bytes(1, 12288, 2048)
     return {"metric": "int8 W-only GEMM HBM GB/s, single gate_up linear", "value": round(nbytes / (t * 1e-3) / 1e9, 1),
@@ -534,7 +538,8 @@ def run_fp8(args, torch, ops):
             tq, tb = tm["q"] / 10, tm["b"] / 10
             same = [d for d in stack if d["name"] == e["name"]]
             ts = streamed_times(torch, args, {
-                "q": [lambda d=d: ops.fp8_linear_strips(xs[(m, d["k"])], d["qs"], d["n"], d["s"]) for d in same],
+                "q": [lambda d=d: ops.fp8_linear_strips(xs[(m, d["k"])], d["qs"], d["n"], d["s"], None, ops.DIV_DEVICE,
+                                                        ops.ALGO_STREAM) for d in same],
                 "b": [lambda d=d: torch.nn.functional.linear(xs[(m, d["k"])], d["w_bf16"]) for d in same]})
             nb = fp8_bytes(m, e["n"], e["k"])
             key = f"M{m}_{e['name']}"
@@ -572,7 +577,8 @@ def run_int8_w8a8(args, torch, ops):
             tq, tw, tb = tm["q"] / 10, tm["w"] / 10, tm["b"] / 10
             same = [d for d in stack if d["name"] == e["name"]]
             ts = streamed_times(torch, args, {
-                "q": [lambda d=d: ops.int8_linear_strips(x, d["qs"], d["n"], d["s"]) for d in same],
+                "q": [lambda d=d: ops.int8_linear_strips(x, d["qs"], d["n"], d["s"], None, ops.DIV_DEVICE,
+                                                         ops.ALGO_STREAM) for d in same],
                 "b": [lambda d=d: torch.nn.functional.linear(x, d["w_bf16"]) for d in same]})
             fl = 2 * m * e["n"] * e["k"]
             nb = fp8_bytes(m, e["n"], e["k"])
@@ -607,7 +613,8 @@ def run_fp8w_stack(args, torch, ops):
     xs = make_inputs(torch, [k for _, _, k in TALKER], ms)
     per_m = {}
     for m in ms:
-        g_q = capture(torch, lambda m=m: [ops.fp8w_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"]) for e in stack])
+        g_q = capture(torch, lambda m=m: [ops.fp8w_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"], None,
+                                                               ops.ALGO_STREAM) for e in stack])
         t_q = time_graph(torch, g_q, args.steps, args.warmup)
         nbytes = sum(fp8_bytes(m, e["n"], e["k"]) for e in stack)
         per_m[str(m)] = {"stack_us": round(t_q * 1e3, 2), "GBps": round(nbytes / (t_q * 1e-3) / 1e9, 1),
@@ -641,10 +648,11 @@ def run_mlp(args, torch, ops):
     per_m = {}
     for m in ms:
         x = xs[(m, 2048)]
-        composed = lambda: [ops.w8a16_gemm_strips(act(ops.w8a16_gemm_strips(x, g["qs"], g["n"], g["s"])), d["qs"], d["n"],
-                                                  d["s"]) for g, d in pairs]
-        fused = lambda: [ops.w8a16_silu_mul_gemm_strips(ops.w8a16_gemm_strips(x, g["qs"], g["n"], g["s"]), d["qs"],
-                                                        d["n"], d["s"]) for g, d in pairs]
+        st = ops.ALGO_STREAM  # 28 layers' MLPs, 1.06 GB: past the Infinity Cache
+        composed = lambda: [ops.w8a16_gemm_strips(act(ops.w8a16_gemm_strips(x, g["qs"], g["n"], g["s"], None, st)),
+                                                  d["qs"], d["n"], d["s"], None, st) for g, d in pairs]
+        fused = lambda: [ops.w8a16_silu_mul_gemm_strips(ops.w8a16_gemm_strips(x, g["qs"], g["n"], g["s"], None, st),
+                                                        d["qs"], d["n"], d["s"], None, st) for g, d in pairs]
         bf16 = lambda: [F.linear(act(F.linear(x, g["w_bf16"])), d["w_bf16"]) for g, d in pairs]
         t = {}
         for name, fn in (("composed", composed), ("fused", fused), ("bf16", bf16)):
@@ -673,18 +681,24 @@ def layer_flows(torch, ops, stack, layers, eps=1e-6):
     w_post = [(1 + 0.1 * torch.randn(2048, generator=g, device="cuda")).to(torch.bfloat16) for _ in range(layers)]
     ent = lambda layer, i: stack[4 * layer + i]  # noqa: E731  (qkv, o, gate_up, down)
 
+    st = ops.ALGO_STREAM  # the talker's weight policy
+
     def fused(h_in, attn):
         qkv = ops.w8a16_fused_gemm_strips(h_in, ent(0, 0)["qs"], 4096, ent(0, 0)["s"], prologue=ops.PRO_RMS_NORM,
-                                          norm_weight=w_in[0], eps=eps)
+                                          norm_weight=w_in[0], eps=eps, algo=st)
         h = h_in
         for layer in range(layers):
-            h1 = ops.w8a16_fused_gemm_strips(attn, ent(layer, 1)["qs"], 2048, ent(layer, 1)["s"], residual=h)
+            h1 = ops.w8a16_fused_gemm_strips(attn, ent(layer, 1)["qs"], 2048, ent(layer, 1)["s"], residual=h,
+                                             algo=st)
             act = ops.w8a16_gate_up_silu_strips(h1, ent(layer, 2)["qs"], 12288, ent(layer, 2)["s"],
-                                                prologue=ops.PRO_RMS_NORM, norm_weight=w_post[layer], eps=eps)
-            h = ops.w8a16_fused_gemm_strips(act, ent(layer, 3)["qs"], 2048, ent(layer, 3)["s"], residual=h1)
+                                                prologue=ops.PRO_RMS_NORM, norm_weight=w_post[layer], eps=eps,
+                                                algo=st)
+            h = ops.w8a16_fused_gemm_strips(act, ent(layer, 3)["qs"], 2048, ent(layer, 3)["s"], residual=h1,
+                                            algo=st)
             if layer + 1 < layers:
                 qkv = ops.w8a16_fused_gemm_strips(h, ent(layer + 1, 0)["qs"], 4096, ent(layer + 1, 0)["s"],
-                                                  prologue=ops.PRO_RMS_NORM, norm_weight=w_in[layer + 1], eps=eps)
+                                                  prologue=ops.PRO_RMS_NORM, norm_weight=w_in[layer + 1], eps=eps,
+                                                  algo=st)
         return h, qkv
 
     def bf16(h_in, attn):

@@ -54,6 +54,15 @@ typedef enum {
     QTTS_ALGO_SKINNY_QUARTER = 4
 } qtts_algo;
 
+/* Weight policy flag, OR-ed into any `algo` of the GEMM and linear entry points (and of
+ * qtts_workspace_bytes, which ignores it).  With it the decode kernels (the skinny and fused
+ * W8A16, fp8 weight-only, fp8 and int8 W8A8 kernels, at most 16 activation rows) load the
+ * weight non-temporally: for weights that each step reads once and that are too large to
+ * stay in the Infinity Cache between steps, so that their stream does not evict the cached
+ * activations or the lines of smaller, reused weights.  Results are the same bits either
+ * way; the tile kernels ignore it (their tiles re-read the weight). */
+#define QTTS_ALGO_STREAM 0x80
+
 /* Strip layouts (see qtts_to_strips). */
 typedef enum { QTTS_STRIP_INT8 = 0, QTTS_STRIP_FP8 = 1 } qtts_strip_kind;
 

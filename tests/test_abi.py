@@ -96,6 +96,19 @@ def test_workspace_query():
     assert L.qtts_workspace_bytes(_lib.OP_W8A16, 4, 2048, 0, 0) >= 0  # K = 0 is a valid query
 
 
+def test_weight_policy_flag_is_outside_the_kernel_choice():
+    """QTTS_ALGO_STREAM changes how weights are loaded, never what runs or what it needs."""
+    L = _lib.load()
+    assert re.search(r"#define QTTS_ALGO_STREAM 0x80\b", open(HEADER).read())
+    assert _lib.ALGO_STREAM == 0x80
+    for op in (_lib.OP_W8A16, _lib.OP_W8A16_FUSED, _lib.OP_W8A16_SILU, _lib.OP_FP8W, _lib.OP_FP8_LINEAR,
+               _lib.OP_INT8_LINEAR, _lib.OP_W8A8_FP8, _lib.OP_W8A8_INT8):
+        for m in (1, 8, 16, 64):
+            for algo in (0, _lib.algo_code(_lib.ALGO_SKINNY, 4), _lib.algo_code(_lib.ALGO_TILE, 2)):
+                assert (L.qtts_workspace_bytes(op, m, 4096, 2048, algo | _lib.ALGO_STREAM) ==
+                        L.qtts_workspace_bytes(op, m, 4096, 2048, algo)), (op, m, algo)
+
+
 def test_strip_bytes():
     L = _lib.load()
     assert L.qtts_strip_bytes(2048, 2048, _lib.STRIP_INT8) == 2048 * 2048

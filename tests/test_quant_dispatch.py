@@ -80,6 +80,40 @@ def test_quantize_module_counts_and_bytes():
     assert len(m.qkv_proj.split(m.qkv_proj(x))) == 3
 
 
+class PolicyRecorder(FakeMethod):
+    """FakeMethod that records the weight policy each process_weights call saw."""
+
+    def __init__(self):
+        self.seen = []
+
+    def process_weights(self, layer):
+        self.seen.append(self.stream_weights)
+        super().process_weights(layer)
+
+
+def test_weight_policy_follows_the_submodel_size(monkeypatch):
+    """A submodel whose eligible codes exceed the Infinity Cache streams its weights (ALGO_STREAM on
+    every converted layer, seen by process_weights for calibration); one that fits keeps them cached."""
+    from qtts_amd import _lib
+    from qtts_amd.quant import base
+
+    cfg = QuantConfig(method="int8_weight_only")
+    m = _init(Block())
+    eligible = sum(l.weight.numel() for n, l in iter_linears(m) if not cfg.excludes(n))
+    assert eligible == 16 * 8 + 8 * 8 + 8 * 8 + 5 * 8  # codec_head excluded, the declined layer counted
+    for limit, stream in ((eligible, False), (eligible - 1, True)):
+        monkeypatch.setattr(base, "CACHE_RESIDENT_BYTES", limit)
+        m = _init(Block())
+        method = PolicyRecorder()
+        report = quantize_module(m, method, cfg, "talker")
+        assert report["stream_weights"] == int(stream) and method.seen == [stream] * 4
+        for name in ("qkv_proj", "o_proj", "text_proj_fc1"):
+            layer = getattr(m, name)
+            assert layer.quant_stream is stream
+            assert base.weight_flags(layer) == (_lib.ALGO_STREAM if stream else 0)
+        assert base.weight_flags(m.odd) == 0 and base.weight_flags(m.codec_head) == 0  # not converted
+
+
 def test_apply_quantization_routing():
     assert apply_quantization(QuantConfig(), talker=Block()) == {}
     with pytest.raises(ValueError, match="name no submodel"):

@@ -72,6 +72,9 @@ int qtts_launch_int8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t
 
 static thread_local char g_last_error[512] = "";
 
+// The weight policy of the entry point running on this thread (common.h: WeightPolicy).
+thread_local int qtts::g_weight_policy = 0;
+
 int qtts_set_error(int status, const char* fmt, ...) {
   va_list ap;
   va_start(ap, fmt);
@@ -232,6 +235,7 @@ int qtts_device_supported(int device) {
 }
 
 int64_t qtts_workspace_bytes(int op, int64_t m, int64_t n, int64_t k, int algo) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   const bool rows_ok = op == QTTS_OP_W8A16 || op == QTTS_OP_W8A16_FUSED || op == QTTS_OP_W8A16_SILU;
   // sizes past 2^31 are rejected as every entry point rejects them (and m * k stays in range)
   if (m < 0 || n < 0 || k < 0 || m >= (1ll << 31) || n >= (1ll << 31) || k >= (1ll << 31) ||
@@ -281,6 +285,7 @@ int qtts_pack_fp8_e4m3_rowwise(const void* src, int src_dtype, int64_t n, int64_
 int qtts_w8a16_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* q, int64_t n,
                     int64_t ldq, const void* scale, int scale_dtype, const void* bias, void* y, int64_t ldy, int algo,
                     void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a16_gemm: negative size (m=%lld, n=%lld, k=%lld)", (long long)m,
                (long long)n, (long long)k);
   QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "w8a16_gemm: size too large");
@@ -301,6 +306,7 @@ int qtts_w8a16_gemm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
 int qtts_w8a16_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs, int64_t n,
                            const void* scale, int scale_dtype, const void* bias, void* y, int64_t ldy, int algo,
                            void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a16_gemm_strips: negative size (m=%lld, n=%lld, k=%lld)", (long long)m,
                (long long)n, (long long)k);
   QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "w8a16_gemm_strips: size too large");
@@ -333,6 +339,7 @@ int qtts_quant_act_fp8_rows(const void* x, int x_dtype, int64_t m, int64_t k, in
 int qtts_w8a8_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const uint8_t* qw,
                        int64_t n, int64_t ldqw, const float* sw, const void* bias, void* y, int out_dtype,
                        int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a8_fp8_gemm: negative size");
   QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "w8a8_fp8_gemm: size too large");
   QTTS_REQUIRE(dtype_ok(out_dtype), "w8a8_fp8_gemm: bad dtype code");
@@ -350,6 +357,7 @@ int qtts_w8a8_fp8_gemm(const uint8_t* qx, const float* sx, int64_t m, int64_t k,
 int qtts_w8a8_fp8_gemm_strips(const uint8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx,
                               const uint8_t* qws, int64_t n, const float* sw, const void* bias, void* y, int out_dtype,
                               int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a8_fp8_gemm_strips: negative size");
   QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "w8a8_fp8_gemm_strips: size too large");
   QTTS_REQUIRE(dtype_ok(out_dtype), "w8a8_fp8_gemm_strips: bad dtype code");
@@ -412,6 +420,7 @@ static int fp8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, int
 int qtts_fp8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qw, int64_t n,
                     int64_t ldqw, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode, int algo,
                     void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   return fp8_linear_impl(x, x_dtype, m, k, ldx, qw, n, ldqw, qtts::kLayoutRowMajor, sw, bias, y, ldy, div_mode, algo, ws,
                          ws_bytes, stream);
 }
@@ -419,6 +428,7 @@ int qtts_fp8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ld
 int qtts_fp8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
                            int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode, int algo,
                            void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   return fp8_linear_impl(x, x_dtype, m, k, ldx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y, ldy, div_mode, algo, ws,
                          ws_bytes, stream);
 }
@@ -471,6 +481,7 @@ extern "C" {
 int qtts_fp8_linear_strips_static(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qws,
                                   int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode,
                                   int algo, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "fp8_linear_strips_static: negative size");
   QTTS_REQUIRE(m < (1ll << 31) && k < (1ll << 31), "fp8_linear_strips_static: size too large");
   // The activation codes, their scales and the counter block must fit; a split-K choice that
@@ -524,6 +535,7 @@ static int int8_gemm_impl(const char* what, const int8_t* qx, const float* sx, i
 int qtts_w8a8_int8_gemm(const int8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx, const int8_t* qw,
                         int64_t n, int64_t ldqw, const float* sw, const void* bias, void* y, int out_dtype,
                         int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   return int8_gemm_impl("w8a8_int8_gemm", qx, sx, m, k, ldqx, qw, n, ldqw, qtts::kLayoutRowMajor, sw, bias, y,
                         out_dtype, ldy, algo, ws, ws_bytes, stream);
 }
@@ -531,6 +543,7 @@ int qtts_w8a8_int8_gemm(const int8_t* qx, const float* sx, int64_t m, int64_t k,
 int qtts_w8a8_int8_gemm_strips(const int8_t* qx, const float* sx, int64_t m, int64_t k, int64_t ldqx,
                                const int8_t* qws, int64_t n, const float* sw, const void* bias, void* y, int out_dtype,
                                int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   return int8_gemm_impl("w8a8_int8_gemm_strips", qx, sx, m, k, ldqx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y,
                         out_dtype, ldy, algo, ws, ws_bytes, stream);
 }
@@ -583,6 +596,7 @@ static int int8_linear_impl(const void* x, int x_dtype, int64_t m, int64_t k, in
 int qtts_int8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qw, int64_t n,
                      int64_t ldqw, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode, int algo,
                      void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   return int8_linear_impl(x, x_dtype, m, k, ldx, qw, n, ldqw, qtts::kLayoutRowMajor, sw, bias, y, ldy, div_mode, algo,
                           ws, ws_bytes, stream);
 }
@@ -590,6 +604,7 @@ int qtts_int8_linear(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
 int qtts_int8_linear_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qws,
                             int64_t n, const float* sw, const void* bias, void* y, int64_t ldy, int div_mode, int algo,
                             void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   return int8_linear_impl(x, x_dtype, m, k, ldx, qws, n, 0, qtts::kLayoutStrips, sw, bias, y, ldy, div_mode, algo, ws,
                           ws_bytes, stream);
 }
@@ -609,6 +624,7 @@ int qtts_silu_mul(const void* gate_up, int x_dtype, int64_t m, int64_t k, int64_
 int qtts_w8a16_silu_mul_gemm_strips(const void* gate_up, int x_dtype, int64_t m, int64_t k, int64_t ld_gate_up,
                                     const int8_t* qs, int64_t n, const void* scale, int scale_dtype, const void* bias,
                                     void* y, int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a16_silu_mul_gemm_strips: negative size");
   QTTS_REQUIRE(m < 65536 && n < (1ll << 31) && k < (1ll << 30), "w8a16_silu_mul_gemm_strips: size too large");
   QTTS_REQUIRE(x_dtype == QTTS_BF16 || x_dtype == QTTS_F16, "w8a16_silu_mul_gemm_strips: activations must be bf16 or fp16");
@@ -642,6 +658,7 @@ int qtts_w8a16_fused_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t 
                                  const void* norm_weight, float eps, const int8_t* qs, int64_t n, const void* scale,
                                  int scale_dtype, const void* bias, const void* residual, int64_t ldr, void* y,
                                  int64_t ldy, int algo, void* ws, int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a16_fused_gemm_strips: negative size");
   QTTS_REQUIRE(m < 65536 && n < (1ll << 31) && k < (1ll << 30), "w8a16_fused_gemm_strips: size too large");
   QTTS_REQUIRE(x_dtype == QTTS_BF16 || x_dtype == QTTS_F16, "w8a16_fused_gemm_strips: activations must be bf16 or fp16");
@@ -672,6 +689,7 @@ int qtts_w8a16_gate_up_silu_strips(const void* x, int x_dtype, int64_t m, int64_
                                    const void* norm_weight, float eps, const int8_t* qs, int64_t n, const void* scale,
                                    int scale_dtype, const void* bias, void* act, int64_t ldact, int algo, void* ws,
                                    int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "w8a16_gate_up_silu_strips: negative size");
   QTTS_REQUIRE(m < 65536 && n < (1ll << 31) && k < (1ll << 30), "w8a16_gate_up_silu_strips: size too large");
   QTTS_REQUIRE(x_dtype == QTTS_BF16 || x_dtype == QTTS_F16,
@@ -698,6 +716,7 @@ int qtts_w8a16_gate_up_silu_strips(const void* x, int x_dtype, int64_t m, int64_
 int qtts_fp8w_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n,
                           const float* scale, const void* bias, void* y, int64_t ldy, int algo, void* ws,
                           int64_t ws_bytes, void* stream) {
+  const qtts::WeightPolicy policy(algo);  // takes QTTS_ALGO_STREAM out of algo
   QTTS_REQUIRE(m >= 0 && n >= 0 && k >= 0, "fp8w_gemm_strips: negative size (m=%lld, n=%lld, k=%lld)", (long long)m,
                (long long)n, (long long)k);
   QTTS_REQUIRE(m < (1ll << 31) && n < (1ll << 31) && k < (1ll << 31), "fp8w_gemm_strips: size too large");

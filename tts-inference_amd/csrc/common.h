@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "qtts_amd.h"
 
 typedef __attribute__((ext_vector_type(8))) __bf16 bf16x8_t;
@@ -22,6 +24,19 @@ constexpr int64_t kCounterBytes = 65536;
 constexpr int64_t kMaxSplitTiles = kCounterBytes / 4;
 
 __host__ __device__ constexpr int64_t align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+// A weight block of 16 bytes, loaded as the caller's weight policy asks: NT for weights
+// that a step reads once and that cannot stay cached between steps (`global_load_dwordx4
+// ... nt`, so the stream neither evicts the activation rows and scales nor the Infinity
+// Cache lines of weights that are reused); plain loads for weights small enough to stay
+// resident (QTTS_ALGO_STREAM in include/qtts_amd.h picks NT per call).  The decode kernels
+// take NT as a template parameter: a run-time branch around the loads joins before their
+// first use, where the compiler's wait counting loses the per-load order and waits for every
+// weight block before the first MFMA (measured 8% slower on the talker stack).
+template <bool NT> __device__ __forceinline__ i32x4_t load_weight(const void* p) {
+  if constexpr (NT) return __builtin_nontemporal_load((const i32x4_t*)p);
+  else return *(const i32x4_t*)p;
+}
 
 // Reset a split-K counter: an agent-scope atomic store (written through to the
 // coherence point), so the next kernel's atomics see zero from any XCD.
@@ -106,17 +121,20 @@ __device__ __forceinline__ bf16x8_t i8x8_to_bf16x8(uint32_t lo, uint32_t hi) {
   return __builtin_bit_cast(bf16x8_t, v);
 }
 
+// Exact, by the exponent trick: code c becomes the fp16 bit pattern 0x6400 | (c + 128), i.e.
+// 1024 + 128 + c (the ulp at 1024 is 1), then one v_pk_add_f16 of -1152 per two codes leaves
+// c (+0 for c = 0, as the integer conversion gives).  Five instructions per four codes.
 __device__ __forceinline__ f16x8_t i8x8_to_f16x8(uint32_t lo, uint32_t hi) {
-  f16x8_t r;
-  r[0] = (_Float16)(float)(int8_t)(lo);
-  r[1] = (_Float16)(float)(int8_t)(lo >> 8);
-  r[2] = (_Float16)(float)(int8_t)(lo >> 16);
-  r[3] = (_Float16)(float)(int8_t)(lo >> 24);
-  r[4] = (_Float16)(float)(int8_t)(hi);
-  r[5] = (_Float16)(float)(int8_t)(hi >> 8);
-  r[6] = (_Float16)(float)(int8_t)(hi >> 16);
-  r[7] = (_Float16)(float)(int8_t)(hi >> 24);
-  return r;
+  typedef __attribute__((ext_vector_type(2))) _Float16 f16x2_t;
+  const uint32_t tl = lo ^ 0x80808080u, th = hi ^ 0x80808080u;  // c + 128 in each byte
+  const f16x2_t off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  // v_perm_b32: bytes 0-3 from the second operand, 4-7 from the first (0x64 each)
+  auto pair = [&](uint32_t t, uint32_t sel) {
+    return __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2_t, __builtin_amdgcn_perm(0x64646464u, t, sel)) + off);
+  };
+  typedef __attribute__((ext_vector_type(4))) uint32_t u4;
+  const u4 v = {pair(tl, 0x04010400u), pair(tl, 0x04030402u), pair(th, 0x04010400u), pair(th, 0x04030402u)};
+  return __builtin_bit_cast(f16x8_t, v);
 }
 
 // ---- OCP e4m3 -> 16-bit float vectors (fp8 weight-only GEMM) ---------------------
@@ -339,6 +357,49 @@ inline void launch(void (*kernel)(Params...), dim3 grid, dim3 block, uint32_t sh
   hipEvent_t a = nullptr, b = nullptr;
   qtts_timer_slot(st, &a, &b);
   hipExtLaunchKernelGGL(kernel, grid, block, shmem, st, a, b, 0u, static_cast<Params>(args)...);
+}
+
+}  // namespace qtts
+
+// ---- the weight policy of the call in progress (abi.hip) ----------------------------------
+// A public entry point whose `algo` carries QTTS_ALGO_STREAM holds a WeightPolicy for the
+// call; the decode launchers on the same thread read it with weight_policy() and launch the
+// kernels' NT instantiation where one is built.  Launches happen on the calling thread, inside
+// the entry point, so a thread-local value is exactly the call's.
+
+namespace qtts {
+
+extern thread_local int g_weight_policy;
+
+inline bool weight_policy() { return g_weight_policy != 0; }
+
+class WeightPolicy {
+ public:
+  // Takes QTTS_ALGO_STREAM out of `algo` (the kernels' choice never sees it) and sets the
+  // policy until the scope ends.
+  explicit WeightPolicy(int& algo) : saved_(g_weight_policy) {
+    g_weight_policy = (algo & QTTS_ALGO_STREAM) ? 1 : 0;
+    algo &= ~QTTS_ALGO_STREAM;
+  }
+  ~WeightPolicy() { g_weight_policy = saved_; }
+  WeightPolicy(const WeightPolicy&) = delete;
+  WeightPolicy& operator=(const WeightPolicy&) = delete;
+
+ private:
+  int saved_;
+};
+
+// f(std::true_type{}) when the NT instantiation is built (NT_BUILT) and the caller's weight
+// policy streams, else f(std::false_type{}); f launches its kernel's NT or plain instantiation
+// (a generic lambda: the NT one is instantiated only where NT_BUILT).
+template <bool NT_BUILT, typename F> inline void launch_by_policy(F&& f) {
+  if constexpr (NT_BUILT) {
+    if (weight_policy()) {
+      f(std::true_type{});
+      return;
+    }
+  }
+  f(std::false_type{});
 }
 
 }  // namespace qtts

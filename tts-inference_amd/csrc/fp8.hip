@@ -54,7 +54,7 @@ __device__ __forceinline__ float e4m3_decode(uint32_t c) {
 // A rows 0-7 hold chunk 2u and rows 8-15 chunk 2u + 1 of the workgroup's 8 rows, B
 // columns 0-7 the activation rows for chunk 2u and 8-15 the same rows for chunk 2u + 1,
 // so D's diagonal 8 x 8 blocks are the two chunks' contributions, added at the end.
-template <typename OT, int WAVES, int U, int LAYOUT, int SUB = 1>
+template <typename OT, int WAVES, int U, int LAYOUT, int SUB = 1, bool NT = false>
 __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
     const uint8_t* __restrict__ qx, const float* sx, int M, int K, int64_t ldqx,
     const uint8_t* __restrict__ qw, int N, int64_t ldqw, const float* sw, const OT* bias,
@@ -114,8 +114,8 @@ __global__ __launch_bounds__(WAVES * 64) void fp8_skinny_kernel(
       const bool live = cc < wc1;
       const bool ok = live && (SUB > 1 || cc * 128 + 32 * g < K);  // half strips: K % 256 == 0
       const bool wok = LAYOUT == kLayoutStrips ? live : (ok && n_ok);
-      w0[u] = wok ? *(const i32x4_t*)(wp + (int64_t)cc * wstride) : zero;
-      w1[u] = wok ? *(const i32x4_t*)(wp + (int64_t)cc * wstride + whalf) : zero;
+      w0[u] = wok ? load_weight<NT>(wp + (int64_t)cc * wstride) : zero;
+      w1[u] = wok ? load_weight<NT>(wp + (int64_t)cc * wstride + whalf) : zero;
       x0[u] = (ok && x_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * xstride) : zero;
       x1[u] = (ok && x_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * xstride + 16) : zero;
     }
@@ -466,10 +466,12 @@ static int fp8_launch_fast(const uint8_t* qx, const float* sx, int64_t m, int64_
     while (W < 16 && ((units + W - 1) / W > kF8CPW || (int64_t)strips * 2 * W < 2048)) W *= 2;
     const int64_t blocks = ((int64_t)strips * 2 + 7) / 8 * 8;
     if ((units + W - 1) / W <= kF8CPW && blocks < ((int64_t)1 << 31)) {
-#define QTTS_F8H(WV)                                                                                             \
-  qtts::launch(&fp8_skinny_kernel<OT, WV, kF8CPW, kLayoutStrips, 2>, dim3((unsigned)blocks), dim3(WV * 64), 0, st, \
-               qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy, (float*)nullptr, (unsigned*)nullptr, \
-               strips, 1, units)
+#define QTTS_F8H(WV)                                                                                            \
+  qtts::launch_by_policy<std::is_same<OT, bf16_t>::value>([&](auto nt) {                                        \
+    qtts::launch(&fp8_skinny_kernel<OT, WV, kF8CPW, kLayoutStrips, 2, decltype(nt)::value>, dim3((unsigned)blocks), \
+                 dim3(WV * 64), 0, st, qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy,          \
+                 (float*)nullptr, (unsigned*)nullptr, strips, 1, units);                                           \
+  })
       switch (W) {
         case 1: QTTS_F8H(1); break;
         case 2: QTTS_F8H(2); break;
@@ -483,10 +485,12 @@ static int fp8_launch_fast(const uint8_t* qx, const float* sx, int64_t m, int64_
   }
   if (c.family == QTTS_ALGO_SKINNY) {
     const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8 * c.S;
-#define QTTS_F8S(W, U)                                                                                             \
-  qtts::launch(&fp8_skinny_kernel<OT, W, U, LAYOUT>, dim3((unsigned)blocks), dim3(W * 64), 0, st, qx, sx, (int)m, (int)k, ldqx, qw, (int)n, \
-                                                                           ldqw, sw, bias, y, ldy, part, counters,   \
-                                                                           c.strips, c.S, c.cps)
+#define QTTS_F8S(W, U)                                                                                          \
+  qtts::launch_by_policy<std::is_same<OT, bf16_t>::value && LAYOUT == kLayoutStrips>([&](auto nt) {             \
+    qtts::launch(&fp8_skinny_kernel<OT, W, U, LAYOUT, 1, decltype(nt)::value>, dim3((unsigned)blocks),          \
+                 dim3(W * 64), 0, st, qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy, part,    \
+                 counters, c.strips, c.S, c.cps);                                                               \
+  })
     switch (c.waves) {
       case 1: QTTS_F8S(1, kF8CPW); break;
       case 2: QTTS_F8S(2, kF8CPW); break;

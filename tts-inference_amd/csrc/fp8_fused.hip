@@ -31,7 +31,7 @@
 
 namespace qtts {
 
-template <typename XT, int W, int C, int RM>
+template <typename XT, int W, int C, int RM, bool NT = false>
 __global__ __launch_bounds__(W * 64) void fp8_linear_fused_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const uint8_t* __restrict__ qws, int N,
     const float* sw, const XT* bias, XT* __restrict__ y, int64_t ldy, int strips, int div_mode) {
@@ -65,8 +65,8 @@ __global__ __launch_bounds__(W * 64) void fp8_linear_fused_kernel(
 #pragma unroll
   for (int u = 0; u < C; ++u) {
     const int64_t off = (int64_t)min(u, max(nw - 1, 0)) * 2048;  // clamped: stays inside the strip
-    w0[u] = *(const i32x4_t*)(wp + off);
-    w1[u] = *(const i32x4_t*)(wp + off + 1024);
+    w0[u] = load_weight<NT>(wp + off);
+    w1[u] = load_weight<NT>(wp + off + 1024);
   }
   // Slot j: row RPS j + sub, columns 128 wc0 + 8 v ..; dead lanes read a clamped address.
   i32x4_t xv[SLOTS];
@@ -239,9 +239,12 @@ int qtts_launch_fp8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t 
   const unsigned blocks = (unsigned)((n + 15) / 16);
   const int strips = (int)blocks;
   const int RM = m <= 1 ? 1 : (m <= 4 ? 4 : 8);
-#define QTTS_F8F(XT, WV, CV, RMV)                                                                          \
-  qtts::launch(&fp8_linear_fused_kernel<XT, WV, CV, RMV>, dim3(blocks), dim3(WV * 64), 0, st, (const XT*)x,  \
-               (int)m, (int)k, ldx, qws, (int)n, sw, (const XT*)bias, (XT*)y, ldy, strips, div_mode)
+#define QTTS_F8F(XT, WV, CV, RMV)                                                                           \
+  qtts::launch_by_policy<std::is_same<XT, bf16_t>::value>([&](auto nt) {                                     \
+    qtts::launch(&fp8_linear_fused_kernel<XT, WV, CV, RMV, decltype(nt)::value>, dim3(blocks), dim3(WV * 64), \
+                 0, st, (const XT*)x, (int)m, (int)k, ldx, qws, (int)n, sw, (const XT*)bias, (XT*)y, ldy, strips, \
+                 div_mode);                                                                                   \
+  })
 #define QTTS_F8F_RM(XT, WV, CV)                \
   do {                                         \
     if (RM == 1) QTTS_F8F(XT, WV, CV, 1);      \

@@ -21,10 +21,10 @@ template <typename XT, int W, int CPW, int MX>
 void launch_sk(const void* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n, const float* scale,
                const void* bias, void* y, int64_t ldy, float* part, unsigned* counters, const SkinnyCfg& c,
                unsigned blocks, hipStream_t st) {
-  qtts::launch(&w8a16_skinny_kernel<XT, float, W, CPW, kLayoutStrips, true, 1, MX, true>, dim3(blocks, c.S),
-               dim3(W * 64), 0, st, (const int8_t*)qs, (const XT*)x, scale, (const XT*)bias, (const XT*)nullptr,
-               (int)ldx, (int)(m | (c.S << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0, part, counters, 0.0f,
-               (const XT*)nullptr, (int64_t)0);
+  qtts::launch_skinny<XT, float, W, CPW, kLayoutStrips, true, 1, MX, true>(
+      dim3(blocks, c.S), dim3(W * 64), st, (const int8_t*)qs, (const XT*)x, scale, (const XT*)bias, (const XT*)nullptr,
+      (int)ldx, (int)(m | (c.S << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0, part, counters, 0.0f,
+      (const XT*)nullptr, (int64_t)0);
 }
 
 // Returns QTTS_OK after a launch, 1 when (waves, chunks) is not built for this row mode.
@@ -56,10 +56,10 @@ int launch_wc(const SkinnyCfg& c, const void* x, int64_t m, int64_t k, int64_t l
 template <typename XT, int W, int CPW, int MX>
 void launch_sub(const void* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n, const float* scale,
                 const void* bias, void* y, int64_t ldy, unsigned blocks, hipStream_t st) {
-  qtts::launch(&w8a16_skinny_kernel<XT, float, W, CPW, kLayoutStrips, true, 1, MX, true, kProNone, false, false, 2>,
-               dim3(blocks, 1), dim3(W * 64), 0, st, (const int8_t*)qs, (const XT*)x, scale, (const XT*)bias,
-               (const XT*)nullptr, (int)ldx, (int)(m | (1 << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0,
-               (float*)nullptr, (unsigned*)nullptr, 0.0f, (const XT*)nullptr, (int64_t)0);
+  qtts::launch_skinny<XT, float, W, CPW, kLayoutStrips, true, 1, MX, true, kProNone, false, false, 2>(
+      dim3(blocks, 1), dim3(W * 64), st, (const int8_t*)qs, (const XT*)x, scale, (const XT*)bias,
+      (const XT*)nullptr, (int)ldx, (int)(m | (1 << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0,
+      (float*)nullptr, (unsigned*)nullptr, 0.0f, (const XT*)nullptr, (int64_t)0);
 }
 
 template <typename XT, int MX>

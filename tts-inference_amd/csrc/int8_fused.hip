@@ -48,7 +48,7 @@ template <typename XT> __device__ __forceinline__ uint32_t act_code_rcp(float x,
 // Slice padding (vectors a row) for C chunks a wave.
 template <int C> constexpr int fused_vp() { return C <= 2 ? 16 : (C <= 4 ? 32 : 64); }
 
-template <typename XT, int W, int C, int RM>
+template <typename XT, int W, int C, int RM, bool NT = false>
 __global__ __launch_bounds__(W * 64) void int8_linear_fused_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ qws, int N,
     const float* sw, const XT* bias, XT* __restrict__ y, int64_t ldy, int strips, int div_mode) {
@@ -80,8 +80,8 @@ __global__ __launch_bounds__(W * 64) void int8_linear_fused_kernel(
   const int8_t* wp = qws + ((int64_t)strip * nchunks + wc0) * 1024 + lane * 16;
   i32x4_t wv[C];
 #pragma unroll
-  for (int u = 0; u < C; ++u)
-    wv[u] = *(const i32x4_t*)(wp + (int64_t)min(u, max(nw - 1, 0)) * 1024);  // clamped: inside the strip
+  for (int u = 0; u < C; ++u)  // clamped: inside the strip
+    wv[u] = load_weight<NT>(wp + (int64_t)min(u, max(nw - 1, 0)) * 1024);
   // Slot j: row RPS j + sub, columns 64 wc0 + 8 v ..; dead lanes read a clamped address.
   i32x4_t xv[SLOTS];
 #pragma unroll
@@ -263,9 +263,12 @@ int qtts_launch_int8_linear_fused(const void* x, int x_dtype, int64_t m, int64_t
   const unsigned blocks = (unsigned)((n + 15) / 16);
   const int strips = (int)blocks;
   const int RM = rows_build(m);
-#define QTTS_I8F(XT, WV, CV, RMV)                                                                          \
-  qtts::launch(&int8_linear_fused_kernel<XT, WV, CV, RMV>, dim3(blocks), dim3(WV * 64), 0, st, (const XT*)x, \
-               (int)m, (int)k, ldx, qws, (int)n, sw, (const XT*)bias, (XT*)y, ldy, strips, div_mode)
+#define QTTS_I8F(XT, WV, CV, RMV)                                                                            \
+  qtts::launch_by_policy<std::is_same<XT, bf16_t>::value>([&](auto nt) {                                      \
+    qtts::launch(&int8_linear_fused_kernel<XT, WV, CV, RMV, decltype(nt)::value>, dim3(blocks), dim3(WV * 64), \
+                 0, st, (const XT*)x, (int)m, (int)k, ldx, qws, (int)n, sw, (const XT*)bias, (XT*)y, ldy, strips,  \
+                 div_mode);                                                                                    \
+  })
 #define QTTS_I8F_RM(XT, WV, CV)           \
   do {                                    \
     if (RM == 1) QTTS_I8F(XT, WV, CV, 1); \

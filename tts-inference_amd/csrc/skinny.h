@@ -94,7 +94,7 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 enum : int { kProNone = 0, kProSiluMul = 1, kProRmsNorm = 2 };
 
 template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1, int MX = 0, bool F8W = false,
-          int PRO = kProNone, bool RES = false, bool PAIR = false, int SUB = 1>
+          int PRO = kProNone, bool RES = false, bool PAIR = false, int SUB = 1, bool NT = false>
 __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     const int8_t* __restrict__ q, const XT* __restrict__ x, const ST* scale, const XT* bias,
     const XT* __restrict__ aux, int ldx, int MS, int K, int N, XT* y, int64_t ldy, int64_t ldq,
@@ -185,8 +185,8 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     for (int u = 0; u < CPW; ++u) {
       if constexpr (FULLK) {
         const int c = min(base + u, wc1 - 1);
-        w[u] = *(const i32x4_t*)(wp + (int64_t)c * wstride);
-        if constexpr (P2) wu[u] = *(const i32x4_t*)(wp + up_off + (int64_t)c * wstride);
+        w[u] = load_weight<NT>(wp + (int64_t)c * wstride);
+        if constexpr (P2) wu[u] = load_weight<NT>(wp + up_off + (int64_t)c * wstride);
         if constexpr (MX == 0) {
 #pragma unroll
           for (int mb = 0; mb < MB; ++mb) {
@@ -198,8 +198,8 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
         const int c = base + u;
         const bool live = c < wc1;  // wave-uniform
         const bool kin = c * 64 + 16 * g < K;
-        if (LAYOUT == kLayoutStrips) w[u] = live ? *(const i32x4_t*)(wp + (int64_t)c * wstride) : zero;
-        else w[u] = (live && n_ok && kin) ? *(const i32x4_t*)(wp + (int64_t)c * wstride) : zero;
+        if (LAYOUT == kLayoutStrips) w[u] = live ? load_weight<NT>(wp + (int64_t)c * wstride) : zero;
+        else w[u] = (live && n_ok && kin) ? load_weight<NT>(wp + (int64_t)c * wstride) : zero;
         xa[0][u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp[0] + (int64_t)c * 64) : zero;
         xb[0][u] = (live && m_ok && kin) ? *(const i32x4_t*)(xp[0] + (int64_t)c * 64 + 8) : zero;
       }
@@ -477,6 +477,24 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
 }
 
 // ---- host side: the skinny configuration ------------------------------------------
+
+// Launches w8a16_skinny_kernel under the calling entry point's weight policy: the NT
+// (streaming) instantiation for bf16 activations on full-K strip weights (the decode layers of a
+// bf16 model) when QTTS_ALGO_STREAM is set, plain loads otherwise (the other activation types
+// and layouts are built without NT: they give the same bits, with cached weight loads).
+template <typename XT, typename ST, int W, int CPW, int LAYOUT, bool FULLK, int MB = 1, int MX = 0, bool F8W = false,
+          int PRO = kProNone, bool RES = false, bool PAIR = false, int SUB = 1, typename... Args>
+inline void launch_skinny(dim3 grid, dim3 block, hipStream_t st, Args... args) {
+  if constexpr (std::is_same<XT, bf16_t>::value && LAYOUT == kLayoutStrips && FULLK) {
+    if (weight_policy()) {
+      launch(&w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, FULLK, MB, MX, F8W, PRO, RES, PAIR, SUB, true>, grid, block,
+             0, st, args...);
+      return;
+    }
+  }
+  launch(&w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, FULLK, MB, MX, F8W, PRO, RES, PAIR, SUB>, grid, block, 0, st,
+         args...);
+}
 
 struct SkinnyCfg { int mb, waves, cpw, S, cps, strips; };
 

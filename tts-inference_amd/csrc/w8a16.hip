@@ -365,9 +365,10 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
     const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8;
     if (!grid_ok(blocks) || ldx > INT32_MAX) return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "w8a16: N or ldx too large");
 #define QTTS_SK(ST, W, CPW, FK, MBV)                                                                                \
-  qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, LAYOUT, FK, MBV>, dim3((unsigned)blocks, (unsigned)c.S),        \
-               dim3(W * 64), 0, st, q, x, (const ST*)scale, bias, (const XT*)nullptr, (int)ldx, (int)(m | (c.S << 8)),   \
-               (int)k, (int)n, y, ldy, ldq, part, counters, 0.0f, (const XT*)nullptr, (int64_t)0)
+  qtts::launch_skinny<XT, ST, W, CPW, LAYOUT, FK, MBV>(dim3((unsigned)blocks, (unsigned)c.S), dim3(W * 64), st, q, x, \
+                                                       (const ST*)scale, bias, (const XT*)nullptr, (int)ldx,         \
+                                                       (int)(m | (c.S << 8)), (int)k, (int)n, y, ldy, ldq, part,    \
+                                                       counters, 0.0f, (const XT*)nullptr, (int64_t)0)
 #define QTTS_SK_ST(W, CPW, FK, MBV)                           \
   do {                                                        \
     if (sdt == QTTS_BF16) QTTS_SK(bf16_t, W, CPW, FK, MBV);   \

@@ -13,9 +13,10 @@ void launch_xrows(const void* x, int64_t m, int64_t k, int64_t ldx, const int8_t
                   unsigned blocks, hipStream_t st) {
   (void)strips;
   (void)cps;
-  qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, kLayoutStrips, true, 1, MX>, dim3(blocks, S), dim3(W * 64), 0, st,
-               qs, (const XT*)x, (const ST*)scale, (const XT*)bias, (const XT*)nullptr, (int)ldx, (int)(m | (S << 8)),
-               (int)k, (int)n, (XT*)y, ldy, (int64_t)0, part, counters, 0.0f, (const XT*)nullptr, (int64_t)0);
+  qtts::launch_skinny<XT, ST, W, CPW, kLayoutStrips, true, 1, MX>(
+      dim3(blocks, S), dim3(W * 64), st, qs, (const XT*)x, (const ST*)scale, (const XT*)bias, (const XT*)nullptr,
+      (int)ldx, (int)(m | (S << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0, part, counters, 0.0f, (const XT*)nullptr,
+      (int64_t)0);
 }
 
 template <typename XT, typename ST, int W, int CPW>

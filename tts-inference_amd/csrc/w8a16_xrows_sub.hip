@@ -17,10 +17,10 @@ namespace {
 template <typename XT, typename ST, int SUB, int W, int CPW, int MX>
 void launch_sub(const void* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qs, int64_t n, const void* scale,
                 const void* bias, void* y, int64_t ldy, unsigned blocks, hipStream_t st) {
-  qtts::launch(&w8a16_skinny_kernel<XT, ST, W, CPW, kLayoutStrips, true, 1, MX, false, kProNone, false, false, SUB>,
-               dim3(blocks, 1), dim3(W * 64), 0, st, qs, (const XT*)x, (const ST*)scale, (const XT*)bias,
-               (const XT*)nullptr, (int)ldx, (int)(m | (1 << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0,
-               (float*)nullptr, (unsigned*)nullptr, 0.0f, (const XT*)nullptr, (int64_t)0);
+  qtts::launch_skinny<XT, ST, W, CPW, kLayoutStrips, true, 1, MX, false, kProNone, false, false, SUB>(
+      dim3(blocks, 1), dim3(W * 64), st, qs, (const XT*)x, (const ST*)scale, (const XT*)bias, (const XT*)nullptr,
+      (int)ldx, (int)(m | (1 << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0, (float*)nullptr, (unsigned*)nullptr,
+      0.0f, (const XT*)nullptr, (int64_t)0);
 }
 
 template <typename XT, typename ST, int SUB, int W, int CPW>

@@ -39,7 +39,7 @@ template <typename OT> __device__ __forceinline__ float out_bits_f32(uint32_t b)
   else return __uint_as_float(b);
 }
 
-template <typename OT, int WAVES, int U, int LAYOUT, int SUB = 1>
+template <typename OT, int WAVES, int U, int LAYOUT, int SUB = 1, bool NT = false>
 __global__ __launch_bounds__(WAVES * 64) void int8_skinny_kernel(
     const int8_t* __restrict__ qx, const float* sx, int M, int K, int64_t ldqx,
     const int8_t* __restrict__ qw, int N, int64_t ldqw, const float* sw, const OT* bias,
@@ -96,7 +96,7 @@ __global__ __launch_bounds__(WAVES * 64) void int8_skinny_kernel(
       const bool live = cc < wc1;
       const bool ok = live && (SUB > 1 || cc * 64 + 16 * g < K);  // half strips: K % 128 == 0
       const bool wok = LAYOUT == kLayoutStrips ? live : (ok && n_ok);
-      wv[u] = wok ? *(const i32x4_t*)(wp + (int64_t)cc * wstride) : zero;
+      wv[u] = wok ? load_weight<NT>(wp + (int64_t)cc * wstride) : zero;
       xv[u] = (ok && x_ok) ? *(const i32x4_t*)(xp + (int64_t)cc * xstride) : zero;
     }
   };
@@ -311,10 +311,12 @@ int int8_launch_typed(const int8_t* qx, const float* sx, int64_t m, int64_t k, i
     while (W < 16 && ((units + W - 1) / W > kI8CPW || (int64_t)strips * 2 * W < 2048)) W *= 2;
     const int64_t blocks = ((int64_t)strips * 2 + 7) / 8 * 8;
     if ((units + W - 1) / W <= kI8CPW && blocks < ((int64_t)1 << 31)) {
-#define QTTS_I8H(WV)                                                                                             \
-  qtts::launch(&int8_skinny_kernel<OT, WV, kI8CPW, kLayoutStrips, 2>, dim3((unsigned)blocks, 1), dim3(WV * 64), 0, \
-               st, qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy, (int*)nullptr,              \
-               (unsigned*)nullptr, strips, 1, units)
+#define QTTS_I8H(WV)                                                                                            \
+  qtts::launch_by_policy<std::is_same<OT, bf16_t>::value>([&](auto nt) {                                        \
+    qtts::launch(&int8_skinny_kernel<OT, WV, kI8CPW, kLayoutStrips, 2, decltype(nt)::value>,                    \
+                 dim3((unsigned)blocks, 1), dim3(WV * 64), 0, st, qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw,  \
+                 sw, bias, y, ldy, (int*)nullptr, (unsigned*)nullptr, strips, 1, units);                         \
+  })
       switch (W) {
         case 1: QTTS_I8H(1); break;
         case 2: QTTS_I8H(2); break;
@@ -351,8 +353,17 @@ int int8_launch_typed(const int8_t* qx, const float* sx, int64_t m, int64_t k, i
 #define QTTS_I8S(W)                                                                                             \
   do {                                                                                                          \
     if (layout == kLayoutStrips)                                                                                \
-      qtts::launch(&int8_skinny_kernel<OT, W, kI8CPW, kLayoutStrips>, grid, dim3(W * 64), 0, st, qx, sx, (int)m, \
-                   (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy, part, counters, c.strips, c.S, c.cps);     \
+      /* the weight policy holds for one row block only: more row blocks re-read the weight */                \
+      qtts::launch_by_policy<std::is_same<OT, bf16_t>::value>([&](auto nt) {                                    \
+        if (decltype(nt)::value && c.mblocks > 1)                                                               \
+          qtts::launch(&int8_skinny_kernel<OT, W, kI8CPW, kLayoutStrips>, grid, dim3(W * 64), 0, st, qx, sx,    \
+                       (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy, part, counters, c.strips, c.S,  \
+                       c.cps);                                                                                  \
+        else                                                                                                    \
+          qtts::launch(&int8_skinny_kernel<OT, W, kI8CPW, kLayoutStrips, 1, decltype(nt)::value>, grid,         \
+                       dim3(W * 64), 0, st, qx, sx, (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy,    \
+                       part, counters, c.strips, c.S, c.cps);                                                   \
+      });                                                                                                       \
     else                                                                                                        \
       qtts::launch(&int8_skinny_kernel<OT, W, kI8CPW, kLayoutRowMajor>, grid, dim3(W * 64), 0, st, qx, sx,      \
                    (int)m, (int)k, ldqx, qw, (int)n, ldqw, sw, bias, y, ldy, part, counters, c.strips, c.S,     \

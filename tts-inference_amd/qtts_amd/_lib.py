@@ -54,6 +54,9 @@ def tile_shape(bm: int, bn: int, waves: int = 4, grid2: bool = False) -> int:
 ALGO_AUTO, ALGO_SKINNY, ALGO_TILE = 0, 1, 2
 #: the skinny kernel over row-split strips: 2 (HALF) or 4 (QUARTER) workgroups per 16-row strip
 ALGO_SKINNY_HALF, ALGO_SKINNY_QUARTER = 3, 4
+#: QTTS_ALGO_STREAM: OR-ed into any algo, the decode kernels load the weight non-temporally
+#: (for weights read once a step and too large to stay cached between steps); same bits out.
+ALGO_STREAM = 0x80
 # qtts_op
 OP_W8A16, OP_W8A8_FP8, OP_FP8_LINEAR, OP_W8A8_INT8, OP_INT8_LINEAR, OP_FP8W, OP_W8A16_SILU, OP_W8A16_FUSED = range(8)
 # qtts_prologue

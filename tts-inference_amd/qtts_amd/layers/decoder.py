@@ -23,6 +23,7 @@ import torch.nn.functional as F
 from torch import nn
 
 from .. import ops, torch_ops  # noqa: F401  (torch_ops registers torch.ops.qtts)
+from ..quant.base import weight_flags
 
 
 def _int8_strips(linear: nn.Module, x: torch.Tensor) -> bool:
@@ -51,7 +52,7 @@ def norm_linear(norm: nn.Module, linear: nn.Module, x: torch.Tensor) -> torch.Te
     if _int8_strips(linear, x):
         return torch.ops.qtts.w8a16_fused_gemm_strips(x, linear.int8_weight, linear.out_features, linear.int8_scale,
                                                       linear.bias, ops.PRO_RMS_NORM, norm.weight, _norm_eps(norm),
-                                                      None, ops.ALGO_AUTO)
+                                                      None, ops.ALGO_AUTO | weight_flags(linear))
     return linear(norm(x))
 
 
@@ -60,7 +61,8 @@ def linear_residual(linear: nn.Module, x: torch.Tensor, residual: torch.Tensor) 
     epilogue (the linear's output rounded to the activation dtype first, as torch adds two tensors)."""
     if _int8_strips(linear, x) and residual.shape[:-1] == x.shape[:-1] and residual.dtype == x.dtype:
         return torch.ops.qtts.w8a16_fused_gemm_strips(x, linear.int8_weight, linear.out_features, linear.int8_scale,
-                                                      linear.bias, ops.PRO_NONE, None, 1e-6, residual, ops.ALGO_AUTO)
+                                                      linear.bias, ops.PRO_NONE, None, 1e-6, residual,
+                                                      ops.ALGO_AUTO | weight_flags(linear))
     return residual + linear(x)
 
 
@@ -73,7 +75,7 @@ def norm_mlp_residual(norm: nn.Module, mlp: nn.Module, hidden: torch.Tensor) -> 
         up = mlp.gate_up_proj
         act = torch.ops.qtts.w8a16_gate_up_silu_strips(hidden, up.int8_weight, up.out_features, up.int8_scale,
                                                        up.bias, ops.PRO_RMS_NORM, norm.weight, _norm_eps(norm),
-                                                       ops.ALGO_AUTO)
+                                                       ops.ALGO_AUTO | weight_flags(up))
         return linear_residual(mlp.down_proj, act, hidden)
     if fused:
         gate, up = mlp.gate_up_proj.split(mlp.gate_up_proj(norm(hidden)))

@@ -19,11 +19,28 @@ from ..layers.linear import iter_linears
 
 logger = logging.getLogger("qtts_amd.quant")
 
+#: The MI355X Infinity Cache.  A submodel whose quantized weights exceed it cannot keep them
+#: cached from one decode step to the next, so each step streams every weight byte from HBM
+#: once; its layers then load weights non-temporally (the weight policy, ALGO_STREAM), which
+#: keeps that stream from evicting what is reused: the activations, and the weights of a
+#: smaller submodel (the code predictor's, read 15 times a frame).
+CACHE_RESIDENT_BYTES = 256 << 20
+
+
+def weight_flags(layer) -> int:
+    """The algo flags of ``layer``'s weight policy: ``ALGO_STREAM`` for a streamed submodel."""
+    from .. import _lib
+
+    return _lib.ALGO_STREAM if getattr(layer, "quant_stream", False) else 0
+
 
 class QuantMethodBase:
     """Base of the assign-after-load quant methods (qtts/quant/base.py:41-63)."""
 
     name = "base"
+    #: The weight policy of the submodel being converted (set by quantize_module before its
+    #: layers are processed; process_weights records it on each layer as ``quant_stream``).
+    stream_weights = False
 
     def process_weights(self, layer) -> None:
         raise NotImplementedError
@@ -52,10 +69,19 @@ def _human(n: int) -> str:
     return str(n)
 
 
+def streams_weights(module: nn.Module, config: QuantConfig) -> bool:
+    """Whether the eligible linears' codes (one byte per weight) exceed ``CACHE_RESIDENT_BYTES``."""
+    codes = sum(layer.weight.numel() for name, layer in iter_linears(module)
+                if not config.excludes(name) and getattr(layer, "weight", None) is not None)
+    return codes > CACHE_RESIDENT_BYTES
+
+
 def quantize_module(module: nn.Module, method: QuantMethodBase, config: QuantConfig, label: str) -> dict[str, int]:
     """Attach ``method`` to every eligible linear under ``module`` (qtts/quant/base.py:74-113)."""
     before = _param_bytes(module) + _buffer_bytes(module)
     converted = excluded = declined = kept_weight = 0
+    stream = streams_weights(module, config)
+    method.stream_weights = stream
     for name, layer in iter_linears(module):
         if config.excludes(name):
             excluded += 1
@@ -65,16 +91,18 @@ def quantize_module(module: nn.Module, method: QuantMethodBase, config: QuantCon
             declined += 1
             continue
         layer.quant_method = method
+        layer.quant_stream = stream
         converted += 1
         # a converted layer whose calibration routed some row bucket to F.linear keeps its weight
         weight = getattr(layer, "weight", None)
         kept_weight += int(weight is not None and weight.numel() > 0)
     after = _param_bytes(module) + _buffer_bytes(module)
     logger.info("%s: %s converted %d linears (%d keeping their weight for F.linear at some row bucket), "
-                "skipped %d by exclusion, kept %d on F.linear; weights %s -> %s",
-                label, method.name, converted, kept_weight, excluded, declined, _human(before), _human(after))
+                "skipped %d by exclusion, kept %d on F.linear; weights %s -> %s, %s",
+                label, method.name, converted, kept_weight, excluded, declined, _human(before), _human(after),
+                "streamed past the caches" if stream else "cache-resident")
     return {"converted": converted, "excluded": excluded, "declined": declined, "bytes_before": before,
-            "bytes_after": after, "kept_weight": kept_weight}
+            "bytes_after": after, "kept_weight": kept_weight, "stream_weights": int(stream)}
 
 
 def fp8_supported() -> tuple[bool, str]:

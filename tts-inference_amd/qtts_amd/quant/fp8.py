@@ -21,7 +21,7 @@ import torch.nn.functional as F
 
 from .. import _lib, ops
 from . import prefill
-from .base import QuantMethodBase
+from .base import QuantMethodBase, weight_flags
 from .calibrate import ALGO_REFERENCE_GEMM, calibrate_buckets, rotating, rotation
 from .int8 import layer_algo, tile8_candidates
 from .kernels import kernel_available
@@ -66,11 +66,12 @@ class Fp8Method(QuantMethodBase):
         return getattr(layer, "fp8_weight", None) is not None
 
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        algo = _lib.ALGO_AUTO | weight_flags(layer)
         if layer.fp8_layout == "strips":
             return torch.ops.qtts.fp8_linear_strips(x, layer.fp8_weight, layer.out_features,
-                                                    layer.fp8_scale.reshape(-1), bias, self.div_mode, _lib.ALGO_AUTO)
+                                                    layer.fp8_scale.reshape(-1), bias, self.div_mode, algo)
         return torch.ops.qtts.fp8_linear(x, layer.fp8_weight.t(), layer.fp8_scale.reshape(-1), bias, self.div_mode,
-                                         _lib.ALGO_AUTO)
+                                         algo)
 
 
 def fp8_weight_rowmajor(layer) -> torch.Tensor:
@@ -156,9 +157,11 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
                      rotating([lambda x, q=q_: prefill.dequant_linear(q, _lib.CODE_E4M3, n, k, scale, x, None)
                                for q_ in qss]))
             routes = {r: {"dequant": route} for r in self.calibration_rows if r in prefill.PREFILL_BUCKETS}
+        f = _lib.ALGO_STREAM if self.stream_weights else 0  # timed under the layer's weight policy
         accept, table, report = calibrate_buckets(
             "fp8_wo", n, k, weight.dtype, weight.device, self.calibration_rows, max(1, self.calibration_batch),
-            _fp8w_candidates, rotating([lambda x, a, q=q_: ops.fp8w_gemm_strips(x, q, n, scale, None, a) for q_ in qss]),
+            _fp8w_candidates,
+            rotating([lambda x, a, q=q_: ops.fp8w_gemm_strips(x, q, n, scale, None, a | f) for q_ in qss]),
             rotating([lambda x, w=w_: F.linear(x, w, None) for w_ in ws]), routes, timer=self.timer,
             keep_reference=self.keep_reference_routes, inner=copies)
         del qss, ws
@@ -204,4 +207,5 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
             return F.linear(x, layer.weight, bias)
         if algo == prefill.ALGO_DEQUANT_GEMM:  # x is bf16 / fp16 here, as the scratch was sized for
             return prefill.dequant_linear(layer.fp8w_weight, _lib.CODE_E4M3, n, k, layer.fp8w_scale, x, bias)
-        return torch.ops.qtts.fp8w_gemm_strips(x, layer.fp8w_weight, n, layer.fp8w_scale, bias, max(algo, 0))
+        return torch.ops.qtts.fp8w_gemm_strips(x, layer.fp8w_weight, n, layer.fp8w_scale, bias,
+                                               max(algo, 0) | weight_flags(layer))

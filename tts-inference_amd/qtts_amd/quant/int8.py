@@ -30,7 +30,7 @@ import torch.nn.functional as F
 
 from .. import _lib, ops
 from . import prefill
-from .base import QuantMethodBase
+from .base import QuantMethodBase, weight_flags
 from .calibrate import ALGO_REFERENCE_GEMM, calibrate_buckets, rotating, rotation
 from .kernels import kernel_available
 
@@ -165,10 +165,11 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         copies = rotation(n * k) if self.rotate_weights else 1
         qs = [q] + [q.clone() for _ in range(copies - 1)]
         ws = [weight] + [weight.detach().clone() for _ in range(copies - 1)]
+        f = _lib.ALGO_STREAM if self.stream_weights else 0  # timed under the layer's weight policy
         if strips:
-            kernel = rotating([lambda x, a, q=q_: ops.w8a16_gemm_strips(x, q, n, scale, None, a) for q_ in qs])
+            kernel = rotating([lambda x, a, q=q_: ops.w8a16_gemm_strips(x, q, n, scale, None, a | f) for q_ in qs])
         else:
-            kernel = rotating([lambda x, a, q=q_: ops.w8a16_gemm(x, q, scale, None, a) for q_ in qs])
+            kernel = rotating([lambda x, a, q=q_: ops.w8a16_gemm(x, q, scale, None, a | f) for q_ in qs])
         routes = {}
         if strips and any(r in prefill.PREFILL_BUCKETS for r in self.calibration_rows):
             prefill.reserve(weight.device, n, k, weight.dtype)
@@ -239,12 +240,13 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             return prefill.dequant_linear(layer.int8_weight, _lib.CODE_INT8, n, k, layer.int8_scale, x, bias)
         if algo < 0:  # a route's marker never reaches a kernel
             algo = _lib.ALGO_AUTO
+        f = weight_flags(layer)
         if layer.int8_layout == "strips":
             if x.dtype in (torch.bfloat16, torch.float16):
-                return torch.ops.qtts.w8a16_gemm_strips(x, layer.int8_weight, n, layer.int8_scale, bias, algo)
+                return torch.ops.qtts.w8a16_gemm_strips(x, layer.int8_weight, n, layer.int8_scale, bias, algo | f)
             # e.g. fp32 activations into a bf16-calibrated layer: correct, not fast
             return torch.ops.qtts.w8a16_gemm(x, int8_weight_rowmajor(layer), layer.int8_scale, bias, _lib.ALGO_AUTO)
-        return torch.ops.qtts.w8a16_gemm(x, layer.int8_weight, layer.int8_scale, bias, algo)
+        return torch.ops.qtts.w8a16_gemm(x, layer.int8_weight, layer.int8_scale, bias, algo | f)
 
     def apply_gate_up_silu(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor | None:
         """``F.silu(gate) * up`` of this fused gate_up layer's output (qtts/layers/activation.py:142-147)
@@ -262,7 +264,7 @@ class Int8WeightOnlyMethod(QuantMethodBase):
         if (algo & 0xFF) in (_lib.ALGO_SKINNY_HALF, _lib.ALGO_SKINNY_QUARTER):
             algo = _lib.ALGO_AUTO  # the pair kernel runs whole strips (two per workgroup)
         return torch.ops.qtts.w8a16_gate_up_silu_strips(x, layer.int8_weight, n, layer.int8_scale, bias,
-                                                       ops.PRO_NONE, None, 1e-6, algo)
+                                                       ops.PRO_NONE, None, 1e-6, algo | weight_flags(layer))
 
     def apply_silu_mul(self, layer, gate_up: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
         """``layer(F.silu(gate) * up)`` from GatedMLP's fused gate_up output (qtts/layers/activation.py:
@@ -275,7 +277,7 @@ class Int8WeightOnlyMethod(QuantMethodBase):
             algo = layer_algo(layer, rows)
             if algo >= 0:
                 return torch.ops.qtts.w8a16_silu_mul_gemm_strips(gate_up, layer.int8_weight, n, layer.int8_scale,
-                                                                 bias, algo)
+                                                                 bias, algo | weight_flags(layer))
         return self.apply(layer, torch.ops.qtts.silu_mul(gate_up), bias)
 
 
@@ -314,7 +316,8 @@ class Int8Method(QuantMethodBase):
         return getattr(layer, "int8_weight", None) is not None
 
     def apply(self, layer, x: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+        algo = _lib.ALGO_AUTO | weight_flags(layer)
         if layer.int8_layout == "strips":
             return torch.ops.qtts.int8_linear_strips(x, layer.int8_weight, layer.out_features, layer.int8_scale, bias,
-                                                     self.div_mode, _lib.ALGO_AUTO)
-        return torch.ops.qtts.int8_linear(x, layer.int8_weight, layer.int8_scale, bias, self.div_mode, _lib.ALGO_AUTO)
+                                                     self.div_mode, algo)
+        return torch.ops.qtts.int8_linear(x, layer.int8_weight, layer.int8_scale, bias, self.div_mode, algo)
