@@ -593,14 +593,16 @@ inline bool skinny_sub_ok(int64_t m, int64_t k, int sub) {
 
 // The automatic row split for a decode call: half strips where whole ones leave most compute
 // units idle (at most 64 strips) or give each of at most 128 workgroups 64 KiB or more
-// (K >= 4096).  Measured, cold weights, M = 1..8: the talker's down_proj (N = 2048, K = 6144)
-// 4.57 against 5.13 us at M = 1 and 5.77 against 6.46 at M = 8; the code predictor's o_proj
-// (N = 1024, K = 2048) 2.98 against 3.11 and down_proj (N = 1024, K = 3072) 3.31 against 3.84;
-// the talker's o_proj (N = 2048, K = 2048) 3.25 against 3.22, so it keeps whole strips.
-// Quarter strips lost on every talker and predictor shape.
+// (K >= 4096), or at most 128 strips from 2 rows up.  Measured, cold weights, M = 1..8: the
+// talker's down_proj (N = 2048, K = 6144) 4.57 against 5.13 us at M = 1 and 5.77 against 6.46
+// at M = 8; the code predictor's o_proj (N = 1024, K = 2048) 2.98 against 3.11 and down_proj
+// (N = 1024, K = 3072) 3.31 against 3.84; the talker's o_proj (N = 2048, K = 2048, streamed
+// over 28 weights) 3.41 against 3.41 at M = 1, but 3.39 against 3.54 at M = 2, 3.53 against
+// 3.65 at M = 4 and 3.70 against 3.78 at M = 8.  Quarter strips lost on every talker and
+// predictor shape.
 inline int skinny_auto_sub(int64_t m, int64_t n, int64_t k) {
   const int64_t strips = (n + 15) / 16;
-  if ((strips <= 64 || (strips <= 128 && k >= 4096)) && skinny_sub_ok(m, k, 2)) return 2;
+  if ((strips <= 64 || (strips <= 128 && (k >= 4096 || m >= 2))) && skinny_sub_ok(m, k, 2)) return 2;
   return 1;
 }
 
