@@ -719,8 +719,8 @@ def layer_flows(torch, ops, stack, layers, eps=1e-6):
 def run_traffic_probe(args, torch, ops):
     """Kernels for a rocprofv3 --pmc pass: a 256 MiB device copy (known bytes, the counters' scale),
     then the configs[1] stack's kernels, linear by linear (qkv, o, gate_up, down, each over its 28
-    distinct weights at M = 1, 2, 4, 8, automatic kernel choice), launched eagerly so each dispatch
-    carries its own counters."""
+    distinct weights at M = 1, 2, 4, 8, automatic kernel choice, the stack's streaming weight policy),
+    launched eagerly so each dispatch carries its own counters."""
     ms = (1, 2, 4, 8)
     stack = make_stack(torch, ops, TALKER, 28, keep_bf16=False)
     ops.reserve_workspace(torch.device("cuda"), max(
@@ -735,7 +735,7 @@ def run_traffic_probe(args, torch, ops):
         for m in ms:
             for e in stack:
                 if e["name"] == name:
-                    ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"])
+                    ops.w8a16_gemm_strips(xs[(m, e["k"])], e["qs"], e["n"], e["s"], None, ops.ALGO_STREAM)
                     launches[name] = launches.get(name, 0) + 1
     torch.cuda.synchronize()
     return {"probe": "traffic", "copy_bytes_each_way": src.numel() * 2, "launches": launches,
@@ -788,6 +788,8 @@ def run_calibration(args, torch, ops):
         lin = LinearBase(k, n, dtype=torch.bfloat16, device="cuda")
         g = torch.Generator(device="cuda").manual_seed(n + k)
         lin.weight.data.copy_((torch.randn(n, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16))
+        # the weight policy quantize_module picks: the talker's 1.41 GB streams, the predictor's 79 MB stays cached
+        method.stream_weights = name.startswith("talker_")
         method.process_weights(lin)
         converted = method.applies_to(lin)
         algos = getattr(lin, "quant_algos", {})

@@ -158,8 +158,9 @@ class Fp8WeightOnlyMethod(QuantMethodBase):
                                for q_ in qss]))
             routes = {r: {"dequant": route} for r in self.calibration_rows if r in prefill.PREFILL_BUCKETS}
         f = _lib.ALGO_STREAM if self.stream_weights else 0  # timed under the layer's weight policy
-        accept, table, report = calibrate_buckets(
-            "fp8_wo", n, k, weight.dtype, weight.device, self.calibration_rows, max(1, self.calibration_batch),
+        accept, table, report = calibrate_buckets(  # the policy is part of the cache key
+            "fp8_wo_stream" if self.stream_weights else "fp8_wo", n, k, weight.dtype, weight.device,
+            self.calibration_rows, max(1, self.calibration_batch),
             _fp8w_candidates,
             rotating([lambda x, a, q=q_: ops.fp8w_gemm_strips(x, q, n, scale, None, a | f) for q_ in qss]),
             rotating([lambda x, w=w_: F.linear(x, w, None) for w_ in ws]), routes, timer=self.timer,

@@ -177,8 +177,9 @@ class Int8WeightOnlyMethod(QuantMethodBase):
                      rotating([lambda x, q=q_: prefill.dequant_linear(q, _lib.CODE_INT8, n, k, scale, x, None)
                                for q_ in qs]))
             routes = {r: {"dequant": route} for r in self.calibration_rows if r in prefill.PREFILL_BUCKETS}
-        accept, table, report = calibrate_buckets(
-            "int8_wo", n, k, weight.dtype, weight.device, self.calibration_rows, max(1, self.calibration_batch),
+        accept, table, report = calibrate_buckets(  # the policy is part of the cache key
+            "int8_wo_stream" if self.stream_weights else "int8_wo", n, k, weight.dtype, weight.device,
+            self.calibration_rows, max(1, self.calibration_batch),
             lambda rows: _candidates(rows, kk), kernel, rotating([lambda x, w=w_: F.linear(x, w, None) for w_ in ws]),
             routes, timer=self.timer, keep_reference=self.keep_reference_routes, inner=copies)
         del qs, ws
