@@ -115,7 +115,9 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   constexpr int RP = 16 / SUB;  // weight rows per workgroup (PH: gate rows)
   constexpr bool SILU = PRO == kProSiluMul, NORM = PRO == kProRmsNorm;
   constexpr int NA = P2 ? 2 : 1;  // accumulators a wave carries: gate (and up)
-  __shared__ f32x4_t red[W > 1 ? W - 1 : 1][MB * NA][64];
+  // DIST: the epilogue shared by the waves (below); every wave, wave 0 included, publishes its sums.
+  constexpr bool DIST = W > 1 && MB == 1 && !P2;
+  __shared__ f32x4_t red[DIST ? W : (W > 1 ? W - 1 : 1)][MB * NA][64];
   __shared__ float nss[NORM ? W : 1][NORM ? MX : 1];
   __shared__ __align__(16) uint16_t xrow[MX > 0 ? W : 1][MX > 0 ? MX : 1][MX > 0 ? CPW * CS * 64 : 8];
 
@@ -369,12 +371,71 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     stage_x();  // waits for the activation rows only; the weights stay in flight
     consume(wc0);
   } else {
-    // A wave past the K range only adds zeros to the reduction and never reaches the epilogue
-    // (wave 0 always has chunks), so it loads nothing.
+    // A wave past the K range only adds zeros to the reduction; with the shared epilogue (DIST)
+    // it finishes elements too, so it loads their operands, else nothing (wave 0 always has chunks).
+    if constexpr (DIST) issue_epilogue();
     if constexpr (NORM) {
       if (lane == 0)
 #pragma unroll
         for (int m = 0; m < MX; ++m) nss[wave][m] = 0.0f;
+    }
+  }
+
+  // The epilogue shared by the waves (DIST: one m-block, no two-strip pair, no split): wave w
+  // finishes element w of each lane's four (fewer than 4 waves: elements w, w + W, ...), so the
+  // scale, bias, rounding, residual and the SiLU pair's activation of a workgroup run on up to 4
+  // waves at once instead of on wave 0 alone (measured: the SiLU pair's epilogue cost 0.35-0.42
+  // us a launch on wave 0).  Each element adds the waves' sums in wave order, as wave 0 does
+  // below, so the bits are the same.
+  if constexpr (DIST) {
+    if (SUB != 1 || S == 1) {
+      red[wave][0][lane] = acc[0];
+      __syncthreads();
+      if (wave >= 4) return;
+      float inv = 1.0f;
+      if constexpr (NORM) {  // as below
+        const int mr = lane < MX ? lane : 0;
+        float ss = 0.0f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) ss += nss[w][mr];
+        inv = __shfl(1.0f / __builtin_sqrtf(ss / (float)K + eps), r, 64);
+      }
+      // Element I of this lane's four (compile-time, so sc, bi and rb stay in registers).
+      auto finish = [&](auto I) {
+        constexpr int i = decltype(I)::value;
+        float a = red[0][0][lane][i];
+#pragma unroll
+        for (int w = 1; w < W; ++w) a += red[w][0][lane][i];
+        if constexpr (SUB == 2 && !PAIR) {
+          a += __shfl_xor(a, 40, 64);  // as below
+        } else if constexpr (SUB == 4) {
+          a = ((a + __shfl(a, lane + 20, 64)) + __shfl(a, lane + 40, 64)) + __shfl(a, lane + 60, 64);
+        }
+        float v = (NORM ? a * inv : a) * bits_to_f32<ST>(sc[i]);
+        if (bias) v += bits_to_f32<XT>(bi[i]);
+        const int nn = strip * 16 + part_row + 4 * g + i;
+        if constexpr (PH) {
+          v = round_through<XT>(v);
+          const float u = __shfl_xor(v, 32, 64);
+          if (g < 2 && r < M && nn < (N >> 1)) y[(int64_t)r * ldy + nn] = from_f32<XT>(silu_mul<XT>(v, u));
+        } else if (r < M && (SUB == 1 || 4 * g < RP) && nn < (PAIR ? N >> 1 : N)) {
+          if constexpr (RES) v = bits_to_f32<XT>(rb[i]) + round_through<XT>(v);
+          y[(int64_t)r * ldy + nn] = from_f32<XT>(v);
+        }
+      };
+      // wave w: elements w, w + W, ... (wave-uniform branches)
+      if (wave == 0) {
+        finish(std::integral_constant<int, 0>{});
+        if constexpr (W == 2) finish(std::integral_constant<int, 2>{});
+      } else if (wave == 1) {
+        finish(std::integral_constant<int, 1>{});
+        if constexpr (W == 2) finish(std::integral_constant<int, 3>{});
+      } else if (wave == 2) {
+        finish(std::integral_constant<int, 2>{});
+      } else {
+        finish(std::integral_constant<int, 3>{});
+      }
+      return;
     }
   }
 
