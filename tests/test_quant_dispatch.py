@@ -380,8 +380,8 @@ def test_calibrate_buckets_inner_calls_reach_the_timer_key():
 
 
 def test_decode_candidates_include_the_automatic_choice_and_half_strips():
-    """Decode buckets time the automatic choice (which takes row-split strips where whole strips leave
-    compute units idle) and, on strip weights with K a multiple of 128, half strips explicitly."""
+    """Every bucket times the automatic choice (which takes row-split strips where whole strips leave
+    compute units idle); decode buckets on strip weights with K a multiple of 128 also half strips."""
     from qtts_amd import _lib
     from qtts_amd.quant.fp8 import _fp8w_candidates
     from qtts_amd.quant.int8 import _candidates
@@ -391,4 +391,32 @@ def test_decode_candidates_include_the_automatic_choice_and_half_strips():
         assert "skinny_half" not in _candidates(rows, 6144 + 64) and "skinny_half" not in _candidates(rows)
         assert _fp8w_candidates(rows)["auto"] == _lib.ALGO_AUTO
     for rows in (16, 32, 256):
-        assert "auto" not in _candidates(rows, 6144) and "skinny_half" not in _candidates(rows, 6144)
+        assert _candidates(rows, 6144)["auto"] == _lib.ALGO_AUTO and "skinny_half" not in _candidates(rows, 6144)
+        assert _fp8w_candidates(rows)["auto"] == _lib.ALGO_AUTO
+
+
+def test_calibrate_buckets_keeps_the_automatic_choice_on_near_ties():
+    """A pinned configuration replaces "auto" only when it is AUTO_MARGIN faster."""
+    calibrate.clear_cache()
+    pin = 1 | (8 << 16)
+
+    def times(label):
+        kind, algo, rows = label
+        if kind == "ref":
+            return 10.0
+        return {0: 2.0, pin: 2.0 / (1.01 if rows == 1 else 1.05)}[algo]  # 1% faster at 1 row, 5% at 2
+
+    def kernel(x, a):
+        return ("k", a, x.shape[0])
+
+    def reference(x):
+        return ("ref", None, x.shape[0])
+
+    def timer(fn):
+        return times(fn())
+
+    accept, table, report = calibrate.calibrate_buckets("near", 8, 8, torch.float32, torch.device("cpu"), (1, 2), 2,
+                                                        lambda rows: {"auto": 0, "pin": pin}, kernel, reference,
+                                                        timer=timer)
+    assert accept and table[1] == 0 and report[1]["best"] == "auto"   # 1%: a near-tie, auto stays
+    assert table[2] == pin and report[2]["best"] == "pin"             # 5%: the pin wins

@@ -173,6 +173,13 @@ def time_candidates(candidates: dict[str, Callable[[], object]], reference_call:
     return reference, timings
 
 
+#: A pinned kernel configuration replaces the automatic choice (the candidate named "auto") at a
+#: bucket only when it is this much faster: candidates within a few percent of each other trade
+#: places from run to run, and a pin that won a near-tie in the calibration's timing (weights rotated
+#: past the L2s) can lose it in the caller's regime.
+AUTO_MARGIN = 1.02
+
+
 def calibrate_buckets(tag: str, n: int, k: int, dtype: torch.dtype, device: torch.device,
                       buckets: tuple[int, ...], decode_rows: int,
                       candidates: Callable[[int], dict[str, int]],
@@ -220,6 +227,8 @@ def calibrate_buckets(tag: str, n: int, k: int, dtype: torch.dtype, device: torc
         reference, timings = time_candidates(calls, lambda x=x: reference_call(x), key=key, use_graph=use_graph,
                                              timer=t)
         best = min(timings, key=timings.get) if timings else None
+        if best is not None and "auto" in timings and timings[best] * AUTO_MARGIN > timings["auto"]:
+            best = "auto"
         report[rows] = {"reference": reference, "best": best, "timings": timings}
         if best is not None:
             loses = reference is not None and timings[best] > reference

@@ -83,9 +83,9 @@ def fp8_weight_rowmajor(layer) -> torch.Tensor:
 
 def _fp8w_candidates(rows: int) -> dict[str, int]:
     """Kernel configurations worth timing at ``rows`` (the algo bits of include/qtts_amd.h)."""
-    c: dict[str, int] = {}
-    if rows <= 8:  # the automatic choice: row-split strips where whole strips leave compute units idle
-        c["auto"] = _lib.ALGO_AUTO
+    # the automatic choice (row-split strips where whole strips leave compute units idle), kept
+    # unless a pin beats it clearly (calibrate.AUTO_MARGIN)
+    c: dict[str, int] = {"auto": _lib.ALGO_AUTO}
     if rows <= 16:
         c["skinny"] = _lib.algo_code(_lib.ALGO_SKINNY)
         for s in (1, 2, 4):

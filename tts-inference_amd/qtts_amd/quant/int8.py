@@ -68,10 +68,11 @@ def layer_algo(layer, rows: int) -> int:
 def _candidates(rows: int, k: int | None = None) -> dict[str, int]:
     """Kernel configurations worth timing at ``rows`` for a weight of ``k`` input features (the
     algo bits of include/qtts_amd.h)."""
-    c: dict[str, int] = {}
+    # the automatic choice (row-split strips where whole strips leave compute units idle; the
+    # skinny kernel, its m-blocks or the tile kernel by rows), kept unless a pin beats it clearly
+    # (calibrate.AUTO_MARGIN)
+    c: dict[str, int] = {"auto": _lib.ALGO_AUTO}
     if rows <= 8:
-        # the automatic choice (row-split strips where whole strips leave compute units idle)
-        c["auto"] = _lib.ALGO_AUTO
         if k is not None and k % 128 == 0:
             c["skinny_half"] = _lib.algo_code(_lib.ALGO_SKINNY_HALF)
     if rows <= 64:  # skinny: up to 16 rows, or 64 on strip weights
