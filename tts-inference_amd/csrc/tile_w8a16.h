@@ -329,9 +329,11 @@ inline bool pipe_p_ok(int bm, int bn, int p, int nw = 4) {
 //       - else 64 x 128 (down_proj 17.1 / 37.7 against 18.4 / 39.7, o_proj at M = 1024
 //         15.4 against 16.7, gate_up at M = 128 14.9 against 18.5).
 //   Splits: with 4 waves, split K until there are 256 workgroups, keeping >= 8 chunks a
-//   split; with 8 waves only while that keeps the workgroups within 256 (a split-K meeting
-//   costs more than the idle compute units it fills: gate_up at M = 128, 192 tiles, 14.9
-//   unsplit against 18.7 in two splits).
+//   split, except for K <= 1024 with at least 128 tiles (the code predictor's qkv and
+//   gate_up at 40-96 rows, cache-resident: 192 tiles 1.0-1.3 µs a call faster unsplit than
+//   in two splits, 128 tiles 0.3 µs); with 8 waves only while that keeps the workgroups
+//   within 256 (a split-K meeting costs more than the idle compute units it fills: gate_up
+//   at M = 128, 192 tiles, 14.9 unsplit against 18.7 in two splits).
 // A workspace too small for the splits drops the automatic choice to one split.
 // shape_req (algo bits 24-30): bits 0-1 log2(BM / 16) in 1..3 (0 = 256 rows, 8 waves
 // only), bit 2 a 2 x 2 (2 x 4 with 8 waves) wave grid in place of 1 x 4 (1 x 8), bit 3
@@ -388,7 +390,7 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
     S = 1;
     if (c.nw == 8)
       while (tiles * S * 2 <= 256 && nchunks / (S * 2) >= 8) S *= 2;
-    else
+    else if (!(nchunks <= 16 && tiles >= 128))
       while (tiles * S < 256 && nchunks / (S * 2) >= 8) S *= 2;
   }
   S = std::max(1, std::min(S, nchunks));

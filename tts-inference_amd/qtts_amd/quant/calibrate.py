@@ -174,10 +174,11 @@ def time_candidates(candidates: dict[str, Callable[[], object]], reference_call:
 
 
 #: A pinned kernel configuration replaces the automatic choice (the candidate named "auto") at a
-#: bucket only when it is this much faster: candidates within a few percent of each other trade
-#: places from run to run, and a pin that won a near-tie in the calibration's timing (weights rotated
-#: past the L2s) can lose it in the caller's regime.
-AUTO_MARGIN = 1.02
+#: bucket only when it is this much faster, the margin the accept/decline verdict asks of a
+#: quantized layer: candidates within a few percent of each other trade places from run to run, and
+#: a pin that won by 2-3% in the calibration's timing (one shape's calls back to back, weights
+#: rotated past the L2s) lost by about 1% in the code predictor's frame, where the shapes interleave.
+AUTO_MARGIN = 1.05
 
 
 def calibrate_buckets(tag: str, n: int, k: int, dtype: torch.dtype, device: torch.device,
