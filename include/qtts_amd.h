@@ -45,7 +45,9 @@ typedef enum { QTTS_DIV_DEVICE = 0, QTTS_DIV_IEEE = 1 } qtts_div_mode;
  * qtts_w8a16_silu_mul_gemm_strips only): the skinny kernel with each
  * 16-row weight strip shared by 2 (or 4) workgroups of 8 (or 4) rows, for at most 8 (or 4)
  * activation rows, K a multiple of 128 (or 256) and no split; AUTO takes them where the
- * strips alone would leave compute units idle. */
+ * strips alone would leave compute units idle.  qtts_w8a16_gemm_strips also runs SKINNY_HALF on
+ * 9-16 activation rows, as two row parts of 8 (twice the workgroups, each staging its own rows;
+ * the fused entry points then run the plain GEMM and the separate step). */
 typedef enum {
     QTTS_ALGO_AUTO = 0,
     QTTS_ALGO_SKINNY = 1,
@@ -108,8 +110,9 @@ int qtts_device_supported(int device);
  * until each wave's share fits its in-flight group).  For the skinny kernels, bits
  * 16-23 are the waves per workgroup (1, 2, 4, 8, 16) and bits 24-29 the chunks in
  * flight per wave (4 or 8; 4 or 6 with 16 waves; W8A16 calls of up to 8 rows on
- * strip weights with K % 64 == 0 also take 12 with 8 waves).  Those W8A16 calls
- * stage their activation rows through
+ * strip weights with K % 64 == 0 also take 12 with 8 waves).  Those W8A16 calls, and
+ * calls of 9-16 rows with one split on at most 128 strips (two row parts of 8), stage
+ * their activation rows through
  * LDS; bit 30 makes them load the MFMA operands straight from memory instead (same
  * bits out, for timing both).  For the tile kernels, bits
  * 16-21 are the LDS pipeline stages (2, 3, 4, 6, 8; the int8 W8A8 tile builds 2-4),

@@ -308,11 +308,12 @@ def test_w8a16_strips_decode_shapes(ops, n, k):
 @pytest.mark.parametrize("xdt,sdt", [(torch.bfloat16, torch.bfloat16), (torch.float16, torch.float16),
                                       (torch.bfloat16, torch.float32)])
 def test_w8a16_strips_staged_rows_match_direct(ops, xdt, sdt):
-    """Decode rows (M <= 8) stage their activation rows through LDS; algo bit 30 loads them
-    straight from global memory instead.  Same operands in the same order: equal bits, for
-    every (waves, chunks) pair built with staging, ragged N and a bias, and the oracle bound."""
+    """Decode rows (M <= 8, and 9-16 in two row parts of 8 without a split) stage their
+    activation rows through LDS; algo bit 30 loads them straight from global memory instead.  Same
+    operands in the same order: equal bits, for every (waves, chunks) pair built with staging,
+    ragged N and a bias, and the oracle bound."""
     for (n, k) in ((2048, 2048), (2048, 6144), (1000, 1024), (1030, 3072), (48, 512)):
-        for m in (1, 2, 3, 4, 5, 8):
+        for m in (1, 2, 3, 4, 5, 8, 9, 12, 16):
             x, w, b = _make(m, n, k, dtype=xdt, bias=(m % 2 == 1), seed=n + k + m)
             q, s = ops.pack_int8(w, sdt)
             qs = ops.to_strips(q)
@@ -691,11 +692,12 @@ SUB_PAIRS = {2: ((1, 8), (2, 8), (4, 4), (4, 8), (8, 6), (16, 3)),
 def test_w8a16_strips_row_split(ops, xdt, sdt):
     """Row-split strips (2 or 4 workgroups per 16-row strip, SUB chunks per MFMA) against the oracle:
     every built (waves, units) pair that covers K in one group, ragged N, a bias on odd M, every M
-    the split allows; the automatic choice too, and the same bits on a second call."""
+    the split allows (half strips: 9-16 rows in two row parts of 8); the automatic choice too, and
+    the same bits on a second call."""
     for (n, k) in ((2048, 2048), (2048, 6144), (1024, 3072), (1000, 1024), (40, 512), (24, 256)):
         nch = k // 64
         q = s = qs = None
-        for m in range(1, 9):
+        for m in range(1, 17):
             x, w, b = _make(m, n, k, dtype=xdt, bias=(m % 2 == 1), seed=3 * n + k + m)
             if q is None:
                 q, s = ops.pack_int8(w, sdt)
@@ -705,7 +707,7 @@ def test_w8a16_strips_row_split(ops, xdt, sdt):
             assert_close(y, ref, f"auto m={m} n={n} k={k} {xdt} {sdt}")
             assert torch.equal(y, ops.w8a16_gemm_strips(x, qs, n, s, b)), f"auto not deterministic m={m} n={n}"
             for sub, family in ((2, ops.ALGO_SKINNY_HALF), (4, ops.ALGO_SKINNY_QUARTER)):
-                if m > 16 // sub or nch % sub:
+                if m > (16 if sub == 2 else 16 // sub) or nch % sub:
                     with pytest.raises(ValueError, match="row-split"):
                         ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(family))
                     continue
@@ -723,11 +725,13 @@ def test_w8a16_strips_row_split(ops, xdt, sdt):
 
 
 def test_w8a16_strips_row_split_rejects(ops):
-    x, w, b = _make(9, 256, 512, seed=5)
+    x, w, b = _make(17, 256, 512, seed=5)
     q, s = ops.pack_int8(w, torch.bfloat16)
     qs = ops.to_strips(q)
-    with pytest.raises(ValueError, match="row-split"):  # 9 rows: more than the 8 a half strip takes
+    with pytest.raises(ValueError, match="row-split"):  # 17 rows: more than two row parts of 8
         ops.w8a16_gemm_strips(x, qs, 256, s, b, ops.algo_code(ops.ALGO_SKINNY_HALF))
+    with pytest.raises(ValueError, match="row-split"):  # 5 rows: more than the 4 a quarter strip takes
+        ops.w8a16_gemm_strips(x[:5], qs, 256, s, b, ops.algo_code(ops.ALGO_SKINNY_QUARTER))
     with pytest.raises(ValueError, match="row-split"):  # an explicit split count
         ops.w8a16_gemm_strips(x[:2], qs, 256, s, b, ops.algo_code(ops.ALGO_SKINNY_HALF, 2))
     with pytest.raises(ValueError, match="cover less"):  # 1 wave of 3 units for 4 units of K

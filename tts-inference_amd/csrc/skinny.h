@@ -38,7 +38,8 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 // with K % 64 == 0 only)
 // ------------------------------------------------------------------------------------
 
-// MX > 0 (one m-block, full-K strip weights, M <= MX): the activation operands come
+// MX > 0 (one m-block, full-K strip weights, M <= MX, or up to 2 MX rows in row parts: y0
+// below): the activation operands come
 // through LDS instead of one 16-byte global load per lane and MFMA.  Each wave loads
 // the MX rows of its own K range once, 16 bytes a lane with no duplicates (rows past
 // M repeat row M - 1), writes them to a wave-private LDS block and reads its MFMA
@@ -126,7 +127,13 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   // split of a strip runs on one XCD and its split-K meeting stays in one L2.
   // MS = M | S << 8: the rows (at most 64 here) and the split count share one preloaded dword
   // (gridDim.y would be a hidden-argument load).
-  const int M = MS & 0xff, S = MS >> 8;
+  // Row parts (staged rows, one split, plain GEMM): grid z = p takes the call's rows MX p .. MX p +
+  // MX - 1, so a call of MX + 1 .. 2 MX rows runs as MX-row workgroups, two per strip (or per half
+  // strip).  M is this workgroup's row count, y0 its first row.  (The fused forms take at most MX
+  // rows and are built without it.)
+  constexpr bool ROWP = MX > 0 && PRO == kProNone && !RES && !PAIR;
+  const int y0 = ROWP ? (int)blockIdx.z * MX : 0;
+  const int M = ROWP ? min((MS & 0xff) - y0, MX) : MS & 0xff, S = MS >> 8;
   const int strip = SUB == 1 ? blockIdx.x : blockIdx.x / SUB, split = blockIdx.y;
   const int part_row = SUB == 1 ? 0 : (blockIdx.x % SUB) * RP;  // this workgroup's first strip row
   const int strips = PAIR ? ((N >> 1) + 15) >> 4 : (N + 15) >> 4;  // PAIR: the gate strips
@@ -264,7 +271,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
         su[i] = load_bits(scale + nu);
         bu[i] = load_bits(bsrc + nu);
       }
-      if constexpr (RES) rb[i] = load_bits(res + (int64_t)min(r, M - 1) * ldr + nn);
+      if constexpr (RES) rb[i] = load_bits(res + (int64_t)(y0 + min(r, M - 1)) * ldr + nn);
     }
   };
 
@@ -282,7 +289,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
         const int e = min(512 * v + 8 * lane, xlen - 8);
 #pragma unroll
         for (int m = 0; m < MX; ++m) {
-          const XT* row = x + (int64_t)min(m, M - 1) * ldx + xbeg + e;
+          const XT* row = x + (int64_t)(y0 + min(m, M - 1)) * ldx + xbeg + e;
           xr[m][v] = *(const i32x4_t*)row;
           if constexpr (SILU) xu[m][v] = *(const i32x4_t*)(row + K);
           if constexpr (NORM) {
@@ -417,10 +424,10 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
         if constexpr (PH) {
           v = round_through<XT>(v);
           const float u = __shfl_xor(v, 32, 64);
-          if (g < 2 && r < M && nn < (N >> 1)) y[(int64_t)r * ldy + nn] = from_f32<XT>(silu_mul<XT>(v, u));
+          if (g < 2 && r < M && nn < (N >> 1)) y[(int64_t)(y0 + r) * ldy + nn] = from_f32<XT>(silu_mul<XT>(v, u));
         } else if (r < M && (SUB == 1 || 4 * g < RP) && nn < (PAIR ? N >> 1 : N)) {
           if constexpr (RES) v = bits_to_f32<XT>(rb[i]) + round_through<XT>(v);
-          y[(int64_t)r * ldy + nn] = from_f32<XT>(v);
+          y[(int64_t)(y0 + r) * ldy + nn] = from_f32<XT>(v);
         }
       };
       // wave w: elements w, w + W, ... (wave-uniform branches)
@@ -507,7 +514,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       v = round_through<XT>(v);
       const float u = __shfl_xor(v, 32, 64);
       const int nn = strip * 16 + part_row + 4 * g + i;
-      if (g < 2 && m < M && nn < (N >> 1)) y[(int64_t)m * ldy + nn] = from_f32<XT>(silu_mul<XT>(v, u));
+      if (g < 2 && m < M && nn < (N >> 1)) y[(int64_t)(y0 + m) * ldy + nn] = from_f32<XT>(silu_mul<XT>(v, u));
     }
     return;
   }
@@ -530,7 +537,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
             if (bias) u += bits_to_f32<XT>(bu[i]);
             v = silu_mul<XT>(round_through<XT>(v), round_through<XT>(u));
           }
-          y[(int64_t)m * ldy + nn] = from_f32<XT>(v);
+          y[(int64_t)(y0 + m) * ldy + nn] = from_f32<XT>(v);
         }
       }
     }
@@ -650,6 +657,20 @@ inline SkinnyCfg skinny_cfg_sub(int64_t n, int64_t k, int sub, int waves_req, in
 // most 16 / SUB rows.
 inline bool skinny_sub_ok(int64_t m, int64_t k, int sub) {
   return sub > 1 && m >= 1 && m <= 16 / sub && m <= 8 && k % 64 == 0 && (k / 64) % sub == 0;
+}
+
+// Row parts of the staged W8A16 kernel (grid z; skinny.h kernel, y0): calls of 9-16 rows run as
+// two 8-row workgroups per strip or half strip (one split), each staging its own rows.
+inline int skinny_row_parts(int64_t m) { return m > 8 ? (int)((m + 7) / 8) : 1; }
+// Whether the automatic choice takes row parts at 9-16 rows: on at most 128 strips, where the
+// doubled grid fills idle compute units (half strips on at most 64).  Measured per call against
+// direct loads in the stack graphs at M = 9 / 12 / 16: the code predictor's down_proj (64 strips,
+// half strips) 1.36 / 1.60 / 2.12 us faster, its o_proj 0.63 / 0.75 / 1.06; the talker's down_proj
+// (128 strips, whole) 0.85 / 1.54 / 2.53, its o_proj 0.47 / 0.62 / 0.90.  On more strips each
+// extra workgroup re-reads its strip's weight: qkv 0.5-1.0 us and gate_up up to 3.4 us slower.
+inline bool skinny_row_parts_auto(int64_t m, int64_t n) { return m > 8 && m <= 16 && (n + 15) / 16 <= 128; }
+inline bool skinny_sub_rows_ok(int64_t m, int64_t k, int sub) {
+  return m >= 1 && m <= 16 && (m <= 8 ? skinny_sub_ok(m, k, sub) : sub == 2 && skinny_sub_ok(8, k, sub));
 }
 
 // The automatic row split for a decode call: half strips where whole ones leave most compute

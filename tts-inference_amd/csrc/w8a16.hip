@@ -298,13 +298,15 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
   // where the strips alone would leave compute units idle.
   int sub = family == QTTS_ALGO_SKINNY_HALF ? 2 : (family == QTTS_ALGO_SKINNY_QUARTER ? 4 : 1);
   if (sub > 1) {
-    if (LAYOUT != kLayoutStrips || splits != 0 || ((algo >> 24) & 0x40) || !skinny_sub_ok(m, k, sub))
+    if (LAYOUT != kLayoutStrips || splits != 0 || ((algo >> 24) & 0x40) || !skinny_sub_rows_ok(m, k, sub))
       return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
                             "w8a16 row-split strips (%d per strip) need strip weights, at most %d rows (got %lld), "
                             "K a multiple of %d (got %lld) and no split",
-                            sub, std::min(8, 16 / sub), (long long)m, 64 * sub, (long long)k);
+                            sub, sub == 2 ? 16 : 16 / sub, (long long)m, 64 * sub, (long long)k);
   } else if (family == QTTS_ALGO_AUTO && LAYOUT == kLayoutStrips && splits == 0 && (algo >> 16) == 0) {
-    sub = skinny_auto_sub(m, n, k);
+    // 9-16 rows: half strips in two row parts of 8 on at most 64 strips
+    sub = m <= 8 ? skinny_auto_sub(m, n, k)
+                 : (skinny_row_parts_auto(m, n) && (n + 15) / 16 <= 64 && skinny_sub_rows_ok(m, k, 2) ? 2 : 1);
   }
   if (sub > 1) {
     const int cpw = (algo >> 24) & 0x3f;
@@ -336,7 +338,8 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
     const int cpw = (algo >> 24) & 0x3f;
     const bool direct_x = (algo >> 24) & 0x40;
     SkinnyCfg c = skinny_cfg(m, n, k, splits, waves, cpw);
-    const bool staged = c.mb == 1 && wide_ok && m <= 8 && !direct_x;
+    // 9-16 rows with one split on at most 128 strips: two row parts of 8 staged rows (the kernel's y0)
+    const bool staged = c.mb == 1 && wide_ok && (m <= 8 || (c.S == 1 && skinny_row_parts_auto(m, n))) && !direct_x;
     // Staged rows from 2 rows up: 8 waves of 12 chunks beat 16 of 6 (measured on the
     // talker down projection, K = 6144, M = 2..8).
     if (staged && m >= 2 && waves == 0 && cpw == 0 && c.waves == 16 && c.S == 1 && 8 * 12 >= (k + 63) / 64)

@@ -14,7 +14,7 @@ void launch_xrows(const void* x, int64_t m, int64_t k, int64_t ldx, const int8_t
   (void)strips;
   (void)cps;
   qtts::launch_skinny<XT, ST, W, CPW, kLayoutStrips, true, 1, MX>(
-      dim3(blocks, S), dim3(W * 64), st, qs, (const XT*)x, (const ST*)scale, (const XT*)bias, (const XT*)nullptr,
+      dim3(blocks, S, skinny_row_parts(m)), dim3(W * 64), st, qs, (const XT*)x, (const ST*)scale, (const XT*)bias, (const XT*)nullptr,
       (int)ldx, (int)(m | (S << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0, part, counters, 0.0f, (const XT*)nullptr,
       (int64_t)0);
 }
@@ -55,13 +55,14 @@ int launch_wc(int waves, int cpw, int mx, const void* x, int64_t m, int64_t k, i
 }  // namespace
 
 // Launches the staged-row skinny kernel for m <= 8 rows of 16-bit activations on full-K
-// strip weights.  Returns QTTS_OK after a launch, 1 when (waves, cpw) is not built with
-// staged rows (the caller then loads the activations directly), or an error status.
+// strip weights, or 9-16 rows in two row parts of 8 (grid z) with one split.  Returns QTTS_OK
+// after a launch, 1 when (waves, cpw) is not built with staged rows (the caller then loads the
+// activations directly), or an error status.
 int qtts_launch_w8a16_skinny_xrows(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
                                    int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
                                    int waves, int cpw, float* part, unsigned* counters, int strips, int S, int cps,
                                    unsigned blocks, hipStream_t st) {
-  if (m < 1 || m > 8) return 1;
+  if (m < 1 || m > 16 || (m > 8 && S != 1)) return 1;
   const int mx = m <= 2 ? (int)m : (m <= 4 ? 4 : 8);
   int rc;
 #define QTTS_XR_ST(XT)                                                                                                \

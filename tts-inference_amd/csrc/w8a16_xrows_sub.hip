@@ -18,7 +18,7 @@ template <typename XT, typename ST, int SUB, int W, int CPW, int MX>
 void launch_sub(const void* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qs, int64_t n, const void* scale,
                 const void* bias, void* y, int64_t ldy, unsigned blocks, hipStream_t st) {
   qtts::launch_skinny<XT, ST, W, CPW, kLayoutStrips, true, 1, MX, false, kProNone, false, false, SUB>(
-      dim3(blocks, 1), dim3(W * 64), st, qs, (const XT*)x, (const ST*)scale, (const XT*)bias, (const XT*)nullptr,
+      dim3(blocks, 1, skinny_row_parts(m)), dim3(W * 64), st, qs, (const XT*)x, (const ST*)scale, (const XT*)bias, (const XT*)nullptr,
       (int)ldx, (int)(m | (1 << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0, (float*)nullptr, (unsigned*)nullptr,
       0.0f, (const XT*)nullptr, (int64_t)0);
 }
@@ -62,12 +62,13 @@ int qtts_w8a16_sub_built(int sub, int waves, int cpw) {
 }
 
 // Launches the row-split staged kernel: m <= 16 / sub (and <= 8) rows of 16-bit activations on
-// full-K strip weights, grid x = blocks (the strips times sub, rounded up to a multiple of 8).
+// full-K strip weights, or 9-16 rows on half strips in two row parts of 8 (grid z); grid x =
+// blocks (the strips times sub, rounded up to a multiple of 8).
 // Returns QTTS_OK after a launch, 1 when (sub, waves, cpw) is not built, or an error status.
 int qtts_launch_w8a16_skinny_sub(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
                                  int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
                                  int sub, int waves, int cpw, unsigned blocks, hipStream_t st) {
-  if (!skinny_sub_ok(m, k, sub)) return 1;
+  if (!skinny_sub_rows_ok(m, k, sub)) return 1;
   const int mx = m <= 2 ? (int)m : (m <= 4 ? 4 : 8);
   int rc;
 #define QTTS_SUB_ST(XT)                                                                                          \
