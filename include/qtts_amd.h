@@ -46,8 +46,9 @@ typedef enum { QTTS_DIV_DEVICE = 0, QTTS_DIV_IEEE = 1 } qtts_div_mode;
  * 16-row weight strip shared by 2 (or 4) workgroups of 8 (or 4) rows, for at most 8 (or 4)
  * activation rows, K a multiple of 128 (or 256) and no split; AUTO takes them where the
  * strips alone would leave compute units idle.  qtts_w8a16_gemm_strips also runs SKINNY_HALF on
- * 9-16 activation rows, as two row parts of 8 (twice the workgroups, each staging its own rows;
- * the fused entry points then run the plain GEMM and the separate step). */
+ * 9-64 activation rows, in row parts of 8 (ceil(m / 8) workgroups per half strip, each staging
+ * its own rows; AUTO takes them on layers of few strips and small weights; the fused entry points
+ * then run the plain GEMM and the separate step). */
 typedef enum {
     QTTS_ALGO_AUTO = 0,
     QTTS_ALGO_SKINNY = 1,

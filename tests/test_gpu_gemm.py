@@ -692,12 +692,12 @@ SUB_PAIRS = {2: ((1, 8), (2, 8), (4, 4), (4, 8), (8, 6), (16, 3)),
 def test_w8a16_strips_row_split(ops, xdt, sdt):
     """Row-split strips (2 or 4 workgroups per 16-row strip, SUB chunks per MFMA) against the oracle:
     every built (waves, units) pair that covers K in one group, ragged N, a bias on odd M, every M
-    the split allows (half strips: 9-16 rows in two row parts of 8); the automatic choice too, and
+    the split allows (half strips: up to 64 rows in row parts of 8); the automatic choice too, and
     the same bits on a second call."""
     for (n, k) in ((2048, 2048), (2048, 6144), (1024, 3072), (1000, 1024), (40, 512), (24, 256)):
         nch = k // 64
         q = s = qs = None
-        for m in range(1, 17):
+        for m in list(range(1, 17)) + [23, 40, 64]:
             x, w, b = _make(m, n, k, dtype=xdt, bias=(m % 2 == 1), seed=3 * n + k + m)
             if q is None:
                 q, s = ops.pack_int8(w, sdt)
@@ -707,7 +707,7 @@ def test_w8a16_strips_row_split(ops, xdt, sdt):
             assert_close(y, ref, f"auto m={m} n={n} k={k} {xdt} {sdt}")
             assert torch.equal(y, ops.w8a16_gemm_strips(x, qs, n, s, b)), f"auto not deterministic m={m} n={n}"
             for sub, family in ((2, ops.ALGO_SKINNY_HALF), (4, ops.ALGO_SKINNY_QUARTER)):
-                if m > (16 if sub == 2 else 16 // sub) or nch % sub:
+                if m > (64 if sub == 2 else 16 // sub) or nch % sub:
                     with pytest.raises(ValueError, match="row-split"):
                         ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(family))
                     continue
@@ -725,10 +725,10 @@ def test_w8a16_strips_row_split(ops, xdt, sdt):
 
 
 def test_w8a16_strips_row_split_rejects(ops):
-    x, w, b = _make(17, 256, 512, seed=5)
+    x, w, b = _make(65, 256, 512, seed=5)
     q, s = ops.pack_int8(w, torch.bfloat16)
     qs = ops.to_strips(q)
-    with pytest.raises(ValueError, match="row-split"):  # 17 rows: more than two row parts of 8
+    with pytest.raises(ValueError, match="row-split"):  # 65 rows: more than eight row parts of 8
         ops.w8a16_gemm_strips(x, qs, 256, s, b, ops.algo_code(ops.ALGO_SKINNY_HALF))
     with pytest.raises(ValueError, match="row-split"):  # 5 rows: more than the 4 a quarter strip takes
         ops.w8a16_gemm_strips(x[:5], qs, 256, s, b, ops.algo_code(ops.ALGO_SKINNY_QUARTER))

@@ -381,17 +381,17 @@ def test_calibrate_buckets_inner_calls_reach_the_timer_key():
 
 def test_decode_candidates_include_the_automatic_choice_and_half_strips():
     """Every bucket times the automatic choice (which takes row-split strips where whole strips leave
-    compute units idle); decode buckets of up to 16 rows on strip weights with K a multiple of 128 also
+    compute units idle); buckets of up to 64 rows on strip weights with K a multiple of 128 also
     half strips."""
     from qtts_amd import _lib
     from qtts_amd.quant.fp8 import _fp8w_candidates
     from qtts_amd.quant.int8 import _candidates
-    for rows in (1, 2, 4, 8, 16):
+    for rows in (1, 2, 4, 8, 16, 32, 64):
         c = _candidates(rows, 6144)
         assert c["auto"] == _lib.ALGO_AUTO and c["skinny_half"] == _lib.algo_code(_lib.ALGO_SKINNY_HALF)
         assert "skinny_half" not in _candidates(rows, 6144 + 64) and "skinny_half" not in _candidates(rows)
         assert _fp8w_candidates(rows)["auto"] == _lib.ALGO_AUTO
-    for rows in (32, 256):
+    for rows in (128, 256):
         assert _candidates(rows, 6144)["auto"] == _lib.ALGO_AUTO and "skinny_half" not in _candidates(rows, 6144)
         assert _fp8w_candidates(rows)["auto"] == _lib.ALGO_AUTO
 

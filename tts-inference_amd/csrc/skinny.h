@@ -659,9 +659,15 @@ inline bool skinny_sub_ok(int64_t m, int64_t k, int sub) {
   return sub > 1 && m >= 1 && m <= 16 / sub && m <= 8 && k % 64 == 0 && (k / 64) % sub == 0;
 }
 
-// Row parts of the staged W8A16 kernel (grid z; skinny.h kernel, y0): calls of 9-16 rows run as
-// two 8-row workgroups per strip or half strip (one split), each staging its own rows.
+// Row parts of the staged W8A16 kernel (grid z; skinny.h kernel, y0): calls of more than 8 rows
+// run as 8-row workgroups, ceil(M / 8) per strip or half strip (one split), each staging its own
+// rows.  Half strips take them up to 64 rows, whole strips up to 16; the automatic choice takes
+// them where they pay (skinny_row_parts_auto, skinny_row_parts_sub).
+constexpr int kRowPartsMaxM = 64;
 inline int skinny_row_parts(int64_t m) { return m > 8 ? (int)((m + 7) / 8) : 1; }
+inline bool skinny_sub_rows_ok(int64_t m, int64_t k, int sub) {
+  return m >= 1 && m <= kRowPartsMaxM && (m <= 8 ? skinny_sub_ok(m, k, sub) : sub == 2 && skinny_sub_ok(8, k, sub));
+}
 // Whether the automatic choice takes row parts at 9-16 rows: on at most 128 strips, where the
 // doubled grid fills idle compute units (half strips on at most 64).  Measured per call against
 // direct loads in the stack graphs at M = 9 / 12 / 16: the code predictor's down_proj (64 strips,
@@ -669,8 +675,18 @@ inline int skinny_row_parts(int64_t m) { return m > 8 ? (int)((m + 7) / 8) : 1; 
 // (128 strips, whole) 0.85 / 1.54 / 2.53, its o_proj 0.47 / 0.62 / 0.90.  On more strips each
 // extra workgroup re-reads its strip's weight: qkv 0.5-1.0 us and gate_up up to 3.4 us slower.
 inline bool skinny_row_parts_auto(int64_t m, int64_t n) { return m > 8 && m <= 16 && (n + 15) / 16 <= 128; }
-inline bool skinny_sub_rows_ok(int64_t m, int64_t k, int sub) {
-  return m >= 1 && m <= 16 && (m <= 8 ? skinny_sub_ok(m, k, sub) : sub == 2 && skinny_sub_ok(8, k, sub));
+// The automatic choice of half strips in row parts: at 9-16 rows on at most 64 strips (above), and
+// at 17-64 rows on at most 128 strips while the parts' weight reads (parts x N x K bytes, the
+// re-reads served by the L2s and the Infinity Cache) stay within 20 MiB.  Measured per call against
+// the automatic tile or m-block choice in the stack graphs, M = 24 / 32 / 40 / 48 / 64: the code
+// predictor's o_proj (2 MiB) 1.85 / 2.49 / 2.42 / 2.38 / 1.81 us faster, its down_proj (3 MiB)
+// 2.62 / 2.60 / 0.95 / 0.75 faster and 0.28 slower (24 MiB); the talker's o_proj (4 MiB) 1.07 /
+// 1.23 / 1.93 / 1.19 faster and even at 32 MiB; its down_proj (12 MiB) 2.0-17.9 slower.
+inline int skinny_row_parts_sub(int64_t m, int64_t n, int64_t k) {
+  const int64_t strips = (n + 15) / 16;
+  if (!skinny_sub_rows_ok(m, k, 2) || m <= 8) return 1;
+  if (m <= 16) return strips <= 64 ? 2 : 1;
+  return strips <= 128 && skinny_row_parts(m) * n * k <= (int64_t)20 << 20 ? 2 : 1;
 }
 
 // The automatic row split for a decode call: half strips where whole ones leave most compute

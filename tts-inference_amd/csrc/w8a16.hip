@@ -302,11 +302,10 @@ static int launch_fast(const XT* x, int64_t m, int64_t k, int64_t ldx, const int
       return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
                             "w8a16 row-split strips (%d per strip) need strip weights, at most %d rows (got %lld), "
                             "K a multiple of %d (got %lld) and no split",
-                            sub, sub == 2 ? 16 : 16 / sub, (long long)m, 64 * sub, (long long)k);
+                            sub, sub == 2 ? kRowPartsMaxM : 16 / sub, (long long)m, 64 * sub, (long long)k);
   } else if (family == QTTS_ALGO_AUTO && LAYOUT == kLayoutStrips && splits == 0 && (algo >> 16) == 0) {
-    // 9-16 rows: half strips in two row parts of 8 on at most 64 strips
-    sub = m <= 8 ? skinny_auto_sub(m, n, k)
-                 : (skinny_row_parts_auto(m, n) && (n + 15) / 16 <= 64 && skinny_sub_rows_ok(m, k, 2) ? 2 : 1);
+    // more than 8 rows: half strips in row parts of 8 where they pay (skinny_row_parts_sub)
+    sub = m <= 8 ? skinny_auto_sub(m, n, k) : skinny_row_parts_sub(m, n, k);
   }
   if (sub > 1) {
     const int cpw = (algo >> 24) & 0x3f;

@@ -55,14 +55,14 @@ int launch_wc(int waves, int cpw, int mx, const void* x, int64_t m, int64_t k, i
 }  // namespace
 
 // Launches the staged-row skinny kernel for m <= 8 rows of 16-bit activations on full-K
-// strip weights, or 9-16 rows in two row parts of 8 (grid z) with one split.  Returns QTTS_OK
+// strip weights, or more rows in row parts of 8 (grid z) with one split.  Returns QTTS_OK
 // after a launch, 1 when (waves, cpw) is not built with staged rows (the caller then loads the
 // activations directly), or an error status.
 int qtts_launch_w8a16_skinny_xrows(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
                                    int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
                                    int waves, int cpw, float* part, unsigned* counters, int strips, int S, int cps,
                                    unsigned blocks, hipStream_t st) {
-  if (m < 1 || m > 16 || (m > 8 && S != 1)) return 1;
+  if (m < 1 || m > kRowPartsMaxM || (m > 8 && S != 1)) return 1;
   const int mx = m <= 2 ? (int)m : (m <= 4 ? 4 : 8);
   int rc;
 #define QTTS_XR_ST(XT)                                                                                                \

@@ -62,7 +62,7 @@ int qtts_w8a16_sub_built(int sub, int waves, int cpw) {
 }
 
 // Launches the row-split staged kernel: m <= 16 / sub (and <= 8) rows of 16-bit activations on
-// full-K strip weights, or 9-16 rows on half strips in two row parts of 8 (grid z); grid x =
+// full-K strip weights, or up to 64 rows on half strips in row parts of 8 (grid z); grid x =
 // blocks (the strips times sub, rounded up to a multiple of 8).
 // Returns QTTS_OK after a launch, 1 when (sub, waves, cpw) is not built, or an error status.
 int qtts_launch_w8a16_skinny_sub(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,

@@ -72,7 +72,7 @@ def _candidates(rows: int, k: int | None = None) -> dict[str, int]:
     # skinny kernel, its m-blocks or the tile kernel by rows), kept unless a pin beats it clearly
     # (calibrate.AUTO_MARGIN)
     c: dict[str, int] = {"auto": _lib.ALGO_AUTO}
-    if rows <= 16 and k is not None and k % 128 == 0:  # half strips (9-16 rows: two row parts of 8)
+    if rows <= 64 and k is not None and k % 128 == 0:  # half strips (past 8 rows: in row parts of 8)
         c["skinny_half"] = _lib.algo_code(_lib.ALGO_SKINNY_HALF)
     if rows <= 64:  # skinny: up to 16 rows, or 64 on strip weights
         c["skinny"] = _lib.algo_code(_lib.ALGO_SKINNY)
