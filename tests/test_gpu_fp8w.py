@@ -64,7 +64,7 @@ def test_fp8w_every_code_every_position(ops, dtype):
 
 @pytest.mark.parametrize("n,k", TALKER + PREDICTOR)
 def test_fp8w_decode_shapes(ops, n, k):
-    for m in (1, 2, 3, 4, 8, 16):
+    for m in (1, 2, 3, 4, 8, 12, 16):
         x, q, s, b = _make(ops, m, n, k, bias=(m % 2 == 0), seed=n + 3 * k + m)
         qs = ops.fp8w_strips(q)
         ref = _oracle(x, q, s, b)
@@ -72,15 +72,16 @@ def test_fp8w_decode_shapes(ops, n, k):
         for splits, waves, cpw in ((1, 4, 8), (2, 8, 8), (1, 16, 6), (3, 2, 8)):
             y = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(1, splits, waves, cpw))
             assert_close(y, ref, f"m={m} n={n} k={k} S={splits} W={waves} C={cpw}")
-            if m <= 8:
-                direct = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(1, splits, waves, cpw | 0x40))
-                assert torch.equal(y, direct), f"staged != direct m={m} n={n} k={k} S={splits} W={waves}"
+            # staged rows (9-16: in row parts of 8 on at most 128 strips with one split) and direct loads
+            direct = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(1, splits, waves, cpw | 0x40))
+            assert torch.equal(y, direct), f"staged != direct m={m} n={n} k={k} S={splits} W={waves}"
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 def test_fp8w_prefill_and_ragged(ops, dtype):
     for m, n, k in ((17, 4096, 2048), (64, 2048, 6144), (256, 12288, 2048), (130, 1030, 1024), (5, 100, 128),
-                    (33, 48, 64)):
+                    (33, 48, 64), (24, 1024, 3072), (40, 2048, 2048), (64, 1000, 2048)):  # the last three: half
+        # strips in row parts of 8 by the automatic choice
         x, q, s, b = _make(ops, m, n, k, dtype=dtype, bias=True, seed=m + n + k)
         qs = ops.fp8w_strips(q)
         ref = _oracle(x, q, s, b)

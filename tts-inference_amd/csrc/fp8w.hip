@@ -22,7 +22,7 @@ void launch_sk(const void* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* 
                const void* bias, void* y, int64_t ldy, float* part, unsigned* counters, const SkinnyCfg& c,
                unsigned blocks, hipStream_t st) {
   qtts::launch_skinny<XT, float, W, CPW, kLayoutStrips, true, 1, MX, true>(
-      dim3(blocks, c.S), dim3(W * 64), st, (const int8_t*)qs, (const XT*)x, scale, (const XT*)bias, (const XT*)nullptr,
+      dim3(blocks, c.S, MX > 0 ? skinny_row_parts(m) : 1), dim3(W * 64), st, (const int8_t*)qs, (const XT*)x, scale, (const XT*)bias, (const XT*)nullptr,
       (int)ldx, (int)(m | (c.S << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0, part, counters, 0.0f,
       (const XT*)nullptr, (int64_t)0);
 }
@@ -57,7 +57,7 @@ template <typename XT, int W, int CPW, int MX>
 void launch_sub(const void* x, int64_t m, int64_t k, int64_t ldx, const uint8_t* qs, int64_t n, const float* scale,
                 const void* bias, void* y, int64_t ldy, unsigned blocks, hipStream_t st) {
   qtts::launch_skinny<XT, float, W, CPW, kLayoutStrips, true, 1, MX, true, kProNone, false, false, 2>(
-      dim3(blocks, 1), dim3(W * 64), st, (const int8_t*)qs, (const XT*)x, scale, (const XT*)bias,
+      dim3(blocks, 1, skinny_row_parts(m)), dim3(W * 64), st, (const int8_t*)qs, (const XT*)x, scale, (const XT*)bias,
       (const XT*)nullptr, (int)ldx, (int)(m | (1 << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0,
       (float*)nullptr, (unsigned*)nullptr, 0.0f, (const XT*)nullptr, (int64_t)0);
 }
@@ -109,10 +109,16 @@ int family_of(int64_t m, int algo) {
   return f == QTTS_ALGO_AUTO ? (m <= 16 ? QTTS_ALGO_SKINNY : QTTS_ALGO_TILE) : f;
 }
 
+// Staged rows as the W8A16 launch stages them: up to 8, or 9-16 in row parts of 8 on at most 128
+// strips with one split (skinny_row_parts_auto; the split is known once the configuration is).
+bool fp8w_staged(int64_t m, int64_t n, int algo, int S) {
+  return (m <= 8 || (S == 1 && skinny_row_parts_auto(m, n))) && !((algo >> 24) & 0x40);
+}
+
 // The W8A16 skinny choice, including 8 waves of 12 chunks for long K from 2 rows.
 SkinnyCfg fp8w_skinny_cfg(int64_t m, int64_t n, int64_t k, int algo) {
   const int splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff, cpw = (algo >> 24) & 0x3f;
-  const bool staged = m <= 8 && !((algo >> 24) & 0x40);
+  const bool staged = fp8w_staged(m, n, algo, skinny_cfg(m, n, k, splits, waves, cpw).S);
   SkinnyCfg c = skinny_cfg(m, n, k, splits, waves, cpw);
   if (staged && m >= 2 && waves == 0 && cpw == 0 && c.waves == 16 && c.S == 1 && 8 * 12 >= (k + 63) / 64)
     c = skinny_cfg(m, n, k, splits, 8, 12);
@@ -135,14 +141,12 @@ int qtts_launch_fp8w(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
                      hipStream_t st) {
   const int family = family_of(m, algo);
   const int splits = (algo >> 8) & 0xff;
-  if (family == QTTS_ALGO_TILE)
-    return w8a16_pipe_launch<true>("fp8w_tile", x, x_dtype, m, k, ldx, (const int8_t*)qs, n, scale, QTTS_F32, bias, y,
-                                   ldy, splits, (algo >> 16) & 0xff, (algo >> 24) & 0xff, ws, ws_bytes, st);
-  if (m > 16)
-    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8 weight-only skinny kernel handles M <= 16, got M=%lld",
-                          (long long)m);
-  // Half strips where whole ones leave compute units idle: the W8A16 launch's automatic rule.
-  if ((algo & 0xff) == QTTS_ALGO_AUTO && (algo >> 8) == 0 && skinny_auto_sub(m, n, k) == 2 && ldx <= INT32_MAX) {
+  // Half strips where whole ones leave compute units idle: the W8A16 launch's automatic rule (past
+  // 8 rows in row parts of 8, also in place of the tile kernel up to 64 rows).
+  const int auto_sub = (algo & 0xff) == QTTS_ALGO_AUTO && (algo >> 8) == 0
+                           ? (m <= 8 ? skinny_auto_sub(m, n, k) : skinny_row_parts_sub(m, n, k))
+                           : 1;
+  if (auto_sub == 2 && ldx <= INT32_MAX) {
     const SkinnyCfg c = skinny_cfg_sub(n, k, 2, 0, 0);
     const int64_t blocks = ((int64_t)c.strips * 2 + 7) / 8 * 8;
     if (c.waves * c.cpw >= c.cps && blocks < ((int64_t)1 << 31)) {
@@ -153,8 +157,14 @@ int qtts_launch_fp8w(const void* x, int x_dtype, int64_t m, int64_t k, int64_t l
       if (rc != 1) return rc == QTTS_OK ? qtts_check_launch("fp8w_skinny_sub") : rc;
     }
   }
+  if (family == QTTS_ALGO_TILE)
+    return w8a16_pipe_launch<true>("fp8w_tile", x, x_dtype, m, k, ldx, (const int8_t*)qs, n, scale, QTTS_F32, bias, y,
+                                   ldy, splits, (algo >> 16) & 0xff, (algo >> 24) & 0xff, ws, ws_bytes, st);
+  if (m > 16)
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "fp8 weight-only skinny kernel handles M <= 16, got M=%lld",
+                          (long long)m);
   SkinnyCfg c = fp8w_skinny_cfg(m, n, k, algo);
-  const bool staged = m <= 8 && !((algo >> 24) & 0x40);
+  const bool staged = fp8w_staged(m, n, algo, c.S);
   if (!staged && c.waves == 8 && c.cpw == 12 && ((algo >> 16) & 0xff) == 0)  // 12 chunks a wave: staged rows only
     c = skinny_cfg(m, n, k, splits, 16, 6);
   const int64_t need = skinny_ws(c);
