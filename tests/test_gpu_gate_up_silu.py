@@ -72,7 +72,7 @@ def test_gate_up_silu_matches_separate_and_oracle(ops, n, k):
     from qtts_amd.ops import PRO_NONE, PRO_RMS_NORM
     for dtype, sdtype in ((torch.bfloat16, torch.bfloat16), (torch.float16, torch.float32)):
         q, s, qs, b, nw = _case(ops, n, k, dtype, sdtype, seed=n + 7 * k, bias=True)
-        for m in (1, 2, 3, 4, 5, 8, 11):
+        for m in (1, 2, 3, 4, 5, 8, 11, 16):
             g = torch.Generator(device="cuda").manual_seed(m * 13 + k)
             x = (torch.randn(m, k, device="cuda", generator=g) * 2).to(dtype)
             for pro in (PRO_NONE, PRO_RMS_NORM):
@@ -85,9 +85,9 @@ def test_gate_up_silu_matches_separate_and_oracle(ops, n, k):
                 gu = ops.w8a16_fused_gemm_strips(x, qs, n, s, bias, prologue=pro, norm_weight=nw, eps=EPS, algo=cfg)
                 sep = ops.silu_mul(gu)
                 assert torch.equal(act8, sep), (what, int((act8 != sep).sum()))
-                if m <= 8:
-                    # half strips (8 gate rows and their 8 up rows a workgroup, the plain GEMM's grid): bit
-                    # for bit the separate calls at the same configuration too
+                if m <= 16:
+                    # half strips (8 gate rows and their 8 up rows a workgroup, the plain GEMM's grid; 9-16
+                    # rows in two row parts of 8): bit for bit the separate calls at the same configuration too
                     half = ops.algo_code(3, 0, max(1, (k // 64) // 8), 8)
                     act_h = ops.w8a16_gate_up_silu_strips(x, qs, n, s, bias, prologue=pro, norm_weight=nw, eps=EPS,
                                                           algo=half)

@@ -89,6 +89,16 @@ template <> __device__ __forceinline__ uint32_t pack2_f32<f16_t>(float a, float 
 // Round to T and widen back (identity for fp32).
 template <typename T> __device__ __forceinline__ float round_through(float v) { return to_f32(from_f32<T>(v)); }
 
+// acc + lo^2 + hi^2 of a packed pair of 16-bit floats in one v_dot2c_f32_{bf16,f16} (the
+// products are exact in fp32).
+template <typename XT> __device__ __forceinline__ float sq2_acc(uint32_t p, float acc) {
+  typedef __attribute__((ext_vector_type(2))) _Float16 h2_t;
+  if constexpr (std::is_same<XT, bf16_t>::value)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, p), __builtin_bit_cast(bf16x2_t, p), acc, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, p), __builtin_bit_cast(h2_t, p), acc, false);
+}
+
 // ---- int8 -> 16-bit float vectors for the MFMA operands ---------------------------
 // Every int8 value is exact in bf16 and fp16.  Each byte goes through one
 // v_cvt_f32_i32 with an SDWA sign-extended byte select (written out: the compiler

@@ -52,14 +52,11 @@ template <typename T> __device__ __forceinline__ float bits_to_f32(uint32_t b) {
 //     the GEMM multiplies silu(gate) * up (gate = columns [0, K), up = [K, 2K);
 //     qtts/layers/activation.py:142-147);
 //   kProRmsNorm (no split: S == 1): the GEMM multiplies RMSNorm(x) with weight aux
-//     and epsilon eps (qtts/layers/norm.py:50-76), row by row.  The row's inverse RMS is
-//     a scalar per activation row, i.e. per column of the MFMA result, so it is applied
-//     to the fp32 sums in the epilogue: each wave stages x * aux (rounded to XT) and
-//     runs its MFMAs at once, sums x^2 over its K range meanwhile, and the workgroup adds
-//     the W partials of each row in wave order at the cross-wave reduction it runs
-//     anyway.  No barrier is added to the critical path.  (The reference rounds
-//     x * inv * aux to XT before its GEMM; rounding x * aux instead moves each product
-//     by the same half-ulp relative amount.)
+//     and epsilon eps (qtts/layers/norm.py:50-76), row by row, staged as the reference
+//     rounds it: XT((x * inv) * aux), inv = 1 / sqrt(sum of x^2 / K + eps) in fp32.  Each
+//     wave sums x^2 over its K range, the workgroup meets at one fence-free barrier
+//     while the weight loads stay in flight, and every wave adds the W partials in wave
+//     order before it stages its range (stage_x).
 // RES (staged rows only): y = residual + the linear's output, the output rounded to
 // XT first, as `residual + linear(x)` computes it (qtts/models/talker.py:270-271).
 // PAIR (staged rows, no split): GatedMLP's gate_up_proj followed by its activation
@@ -127,13 +124,11 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
   // split of a strip runs on one XCD and its split-K meeting stays in one L2.
   // MS = M | S << 8: the rows (at most 64 here) and the split count share one preloaded dword
   // (gridDim.y would be a hidden-argument load).
-  // Row parts (staged rows, one split, plain GEMM): grid z = p takes the call's rows MX p .. MX p +
-  // MX - 1, so a call of MX + 1 .. 2 MX rows runs as MX-row workgroups, two per strip (or per half
-  // strip).  M is this workgroup's row count, y0 its first row.  (The fused forms take at most MX
-  // rows and are built without it.)
-  constexpr bool ROWP = MX > 0 && PRO == kProNone && !RES && !PAIR;
-  const int y0 = ROWP ? (int)blockIdx.z * MX : 0;
-  const int M = ROWP ? min((MS & 0xff) - y0, MX) : MS & 0xff, S = MS >> 8;
+  // Row parts (staged rows, one split): grid z = p takes the call's rows MX p .. MX p + MX - 1 (of x,
+  // the residual and y), so a call of more than MX rows runs as MX-row workgroups, ceil(M / MX) per
+  // strip (or half strip).  M is this workgroup's row count, y0 its first row.
+  const int y0 = MX > 0 ? (int)blockIdx.z * MX : 0;
+  const int M = MX > 0 ? min((MS & 0xff) - y0, MX) : MS & 0xff, S = MS >> 8;
   const int strip = SUB == 1 ? blockIdx.x : blockIdx.x / SUB, split = blockIdx.y;
   const int part_row = SUB == 1 ? 0 : (blockIdx.x % SUB) * RP;  // this workgroup's first strip row
   const int strips = PAIR ? ((N >> 1) + 15) >> 4 : (N + 15) >> 4;  // PAIR: the gate strips
@@ -299,12 +294,12 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       }
     }
   };
-  // Writes the wave's staged rows to LDS (NORM: x * weight, rounded to XT; the row's
-  // inverse RMS comes in the epilogue) and reads the MFMA B operands back.  NORM also
-  // publishes this wave's sum of x^2 over its range for each row (fp32, lane partials over
-  // its vectors in element order, then the wave's butterfly), from the same converted
-  // elements: a pass of its own after the staging kept every converted row live until
-  // then (twice the registers at 8 rows, half the waves resident).
+  // Writes the wave's staged rows to LDS and reads the MFMA B operands back.  NORM stages the
+  // normalized rows as the reference computes them, XT((x * inv) * weight) with inv = 1 / sqrt(sum
+  // of x^2 / K + eps): each wave sums x^2 over its range for each row (fp32, lane partials over
+  // its vectors in element order, a pair per v_dot2, then the wave's butterfly) and publishes it; after one barrier
+  // (no fence: the weight loads stay in flight) every wave adds the partials in wave order and
+  // scales its own elements.
   auto stage_x = [&]() {
     if constexpr (NORM) {
       float ss[MX];
@@ -312,25 +307,53 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       for (int m = 0; m < MX; ++m) ss[m] = 0.0f;
 #pragma unroll
       for (int v = 0; v < XV; ++v) {
-        const int e = min(512 * v + 8 * lane, xlen - 8);
         const bool in = 512 * v + 8 * lane < xlen;  // lanes past the range repeat its last 8
 #pragma unroll
-        for (int m = 0; m < MX; ++m) {
+        for (int m = 0; m < MX; ++m)
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (in) ss[m] = sq2_acc<XT>((uint32_t)xr[m][v][i], ss[m]);
+      }
+#pragma unroll
+      for (int m = 0; m < MX; ++m) {
+        const float t = wave_sum_rows(ss[m]);
+        if (lane == 0) nss[wave][m] = t;
+      }
+      wait_lgkmcnt0();
+      barrier_only();  // every wave's partials (waves without chunks publish zeros)
+      // The raw rows stay in registers across the barrier and are converted after it (an empty
+      // asm hides their values from the compiler, which would otherwise keep all MX x 8 converted
+      // floats of a lane live across the barrier).
+#pragma unroll
+      for (int v = 0; v < XV; ++v)
+#pragma unroll
+        for (int m = 0; m < MX; ++m)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            int t = xr[m][v][i];
+            asm volatile("" : "+v"(t));
+            xr[m][v][i] = t;
+          }
+      // lane m computes row m's inverse RMS (partials in wave order), read back per row as a scalar
+      float tl = 0.0f;
+#pragma unroll
+      for (int w = 0; w < W; ++w) tl += nss[w][lane < MX ? lane : 0];
+      const int invl = __builtin_bit_cast(int, 1.0f / __builtin_sqrtf(tl / (float)K + eps));
+#pragma unroll
+      for (int m = 0; m < MX; ++m) {
+        const float inv = __builtin_bit_cast(float, __builtin_amdgcn_readlane(invl, m));
+#pragma unroll
+        for (int v = 0; v < XV; ++v) {
+          const int e = min(512 * v + 8 * lane, xlen - 8);
           i32x4_t o;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const uint32_t p = (uint32_t)xr[m][v][i], w2 = (uint32_t)xu[0][v][i];
             const float a = to_f32(XT{(uint16_t)p}), b = to_f32(XT{(uint16_t)(p >> 16)});
-            if (in) ss[m] = __builtin_fmaf(b, b, __builtin_fmaf(a, a, ss[m]));
-            o[i] = (int)pack2_f32<XT>(a * to_f32(XT{(uint16_t)w2}), b * to_f32(XT{(uint16_t)(w2 >> 16)}));
+            o[i] = (int)pack2_f32<XT>((a * inv) * to_f32(XT{(uint16_t)w2}), (b * inv) * to_f32(XT{(uint16_t)(w2 >> 16)}));
           }
           *(i32x4_t*)&xrow[wave][m][e] = o;
         }
-      }
-#pragma unroll
-      for (int m = 0; m < MX; ++m) {  // the row partials, published at the reduction below
-        const float t = wave_sum_rows(ss[m]);
-        if (lane == 0) nss[wave][m] = t;
       }
     } else if constexpr (MX > 0) {
 #pragma unroll
@@ -381,10 +404,12 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     // A wave past the K range only adds zeros to the reduction; with the shared epilogue (DIST)
     // it finishes elements too, so it loads their operands, else nothing (wave 0 always has chunks).
     if constexpr (DIST) issue_epilogue();
-    if constexpr (NORM) {
+    if constexpr (NORM) {  // zeros for the norm's partials, then the staging's barrier
       if (lane == 0)
 #pragma unroll
         for (int m = 0; m < MX; ++m) nss[wave][m] = 0.0f;
+      wait_lgkmcnt0();
+      barrier_only();
     }
   }
 
@@ -399,14 +424,6 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       red[wave][0][lane] = acc[0];
       __syncthreads();
       if (wave >= 4) return;
-      float inv = 1.0f;
-      if constexpr (NORM) {  // as below
-        const int mr = lane < MX ? lane : 0;
-        float ss = 0.0f;
-#pragma unroll
-        for (int w = 0; w < W; ++w) ss += nss[w][mr];
-        inv = __shfl(1.0f / __builtin_sqrtf(ss / (float)K + eps), r, 64);
-      }
       // Element I of this lane's four (compile-time, so sc, bi and rb stay in registers).
       auto finish = [&](auto I) {
         constexpr int i = decltype(I)::value;
@@ -418,7 +435,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
         } else if constexpr (SUB == 4) {
           a = ((a + __shfl(a, lane + 20, 64)) + __shfl(a, lane + 40, 64)) + __shfl(a, lane + 60, 64);
         }
-        float v = (NORM ? a * inv : a) * bits_to_f32<ST>(sc[i]);
+        float v = a * bits_to_f32<ST>(sc[i]);
         if (bias) v += bits_to_f32<XT>(bi[i]);
         const int nn = strip * 16 + part_row + 4 * g + i;
         if constexpr (PH) {
@@ -462,18 +479,6 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     }
   }
 
-  // NORM: variance = sum / K and inv = 1 / sqrt(variance + eps), both correctly rounded;
-  // lane m computes row m's from the wave partials in wave order, and lane (r, g) takes
-  // row r's for its column of the result.
-  float inv_r = 1.0f;
-  if constexpr (NORM) {
-    const int mr = lane < MX ? lane : 0;
-    float ss = 0.0f;
-#pragma unroll
-    for (int w = 0; w < W; ++w) ss += nss[w][mr];
-    inv_r = __shfl(1.0f / __builtin_sqrtf(ss / (float)K + eps), r, 64);
-  }
-
   if constexpr (SUB == 2 && !PAIR) {
     // D rows 8 + i, columns 8 + j (chunk 1 of each unit) onto rows i, columns j (chunk 0):
     // lane (j, g) for g < 2 takes lane (j + 8, g + 2), i.e. lane ^ 40.
@@ -509,7 +514,7 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
     const int m = r;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      float v = (NORM ? acc[0][i] * inv_r : acc[0][i]) * bits_to_f32<ST>(sc[i]);
+      float v = acc[0][i] * bits_to_f32<ST>(sc[i]);
       if (bias) v += bits_to_f32<XT>(bi[i]);
       v = round_through<XT>(v);
       const float u = __shfl_xor(v, 32, 64);
@@ -529,11 +534,11 @@ __global__ __launch_bounds__(W * 64) void w8a16_skinny_kernel(
       for (int i = 0; i < 4; ++i) {
         const int nn = strip * 16 + part_row + 4 * g + i;
         if ((SUB == 1 || 4 * g < RP) && nn < (PAIR ? N >> 1 : N)) {
-          float v = (NORM ? acc[mb][i] * inv_r : acc[mb][i]) * bits_to_f32<ST>(sc[i]);
+          float v = acc[mb][i] * bits_to_f32<ST>(sc[i]);
           if (bias) v += bits_to_f32<XT>(bi[i]);
           if constexpr (RES) v = bits_to_f32<XT>(rb[i]) + round_through<XT>(v);
           if constexpr (P2) {
-            float u = (NORM ? up[0][i] * inv_r : up[0][i]) * bits_to_f32<ST>(su[i]);
+            float u = up[0][i] * bits_to_f32<ST>(su[i]);
             if (bias) u += bits_to_f32<XT>(bu[i]);
             v = silu_mul<XT>(round_through<XT>(v), round_through<XT>(u));
           }

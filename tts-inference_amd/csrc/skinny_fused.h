@@ -31,7 +31,7 @@ struct FusedArgs {
 template <typename XT, typename ST, int W, int CPW, int MX, int PRO, bool RES, bool PAIR = false, int SUB = 1>
 void launch_fused_one(const FusedArgs& a) {
   launch_skinny<XT, ST, W, CPW, kLayoutStrips, true, 1, MX, false, PRO, RES, PAIR, SUB>(
-      dim3(a.blocks, a.c.S), dim3(W * 64), a.st, a.qs, (const XT*)a.x, (const ST*)a.scale, (const XT*)a.bias,
+      dim3(a.blocks, a.c.S, skinny_row_parts(a.m)), dim3(W * 64), a.st, a.qs, (const XT*)a.x, (const ST*)a.scale, (const XT*)a.bias,
       (const XT*)a.aux, (int)a.ldx, (int)(a.m | (a.c.S << 8)), (int)a.k, (int)a.n, (XT*)a.y, a.ldy, (int64_t)0, a.part,
       a.counters, a.eps, (const XT*)a.res, a.ldr);
 }

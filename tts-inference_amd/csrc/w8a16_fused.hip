@@ -19,9 +19,10 @@
 //    (skinny.h: PRO, RES) when the call allows it, otherwise the separate kernels
 //    around the plain W8A16 GEMM.  Fused: SiLU for one row (for two rows it no longer
 //    hides under the weight stream: talker down 9.4 us fused against 9.0 us for the
-//    two passes at M = 2; 7.0 against 9.1 us at M = 1); RMSNorm for one row without a
-//    split-K (every workgroup needs the whole row's sum); the residual for up to 8
-//    staged rows.  A fused and a separate RMSNorm sum in different orders: the fused
+//    two passes at M = 2; 7.0 against 9.1 us at M = 1); RMSNorm for up to 16 rows without
+//    a split-K (every workgroup needs the whole row's sum); the residual for up to 16
+//    staged rows (9-16 in two row parts of 8, one split).  A fused and a separate RMSNorm
+//    sum in different orders: the fused
 //    result is within the GEMM tolerance of the separate one, not bit-identical.
 #include "skinny_fused.h"
 
@@ -201,7 +202,7 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
   const int64_t m = in.m, n = in.n, k = in.k;
   if (pair) {
     const int family = algo & 0xff;
-    if (splits > 1 || m > 8 || n % 32 || family == QTTS_ALGO_SKINNY_QUARTER) return 1;
+    if (splits > 1 || m > 16 || n % 32 || family == QTTS_ALGO_SKINNY_QUARTER) return 1;
     // Half strips: each workgroup's MFMA operand holds 8 gate rows and their 8 up rows, so the
     // grid and the wave configuration are the plain GEMM's (N/16 workgroups); requested by
     // family, and the automatic choice without a prologue or with more than 256 gate strips.
@@ -271,9 +272,11 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
   // Row-split strips: the plain launch's choice (w8a16.hip launch_fast), so a fused call and the
   // plain GEMM it replaces give the same bits.
   const int family = algo & 0xff;
+  if (m > 16) return 1;  // up to 16 rows: 9-16 in two row parts of 8
   int sub = family == QTTS_ALGO_SKINNY_HALF ? 2 : (family == QTTS_ALGO_SKINNY_QUARTER ? 4 : 1);
-  if (sub > 1 && (splits != 0 || !skinny_sub_ok(m, k, sub))) return 1;  // the separate path reports it
-  if (family == QTTS_ALGO_AUTO && splits == 0 && (algo >> 16) == 0) sub = skinny_auto_sub(m, n, k);
+  if (sub > 1 && (splits != 0 || !skinny_sub_rows_ok(m, k, sub))) return 1;  // the separate path reports it
+  if (family == QTTS_ALGO_AUTO && splits == 0 && (algo >> 16) == 0)
+    sub = m <= 8 ? skinny_auto_sub(m, n, k) : skinny_row_parts_sub(m, n, k);
   if (sub > 1) {
     const SkinnyCfg c = skinny_cfg_sub(n, k, sub, waves, cpw);
     if (!fused_sub_built(sub, c.waves, c.cpw) || c.waves * c.cpw < c.cps || in.ldx > INT32_MAX) return 1;
@@ -308,7 +311,7 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
     if (c.S > 1) return 1;
   }
   if (!qtts_w8a16_xrows_built(c.waves, c.cpw)) return 1;
-  if (pro == kProRmsNorm && c.S > 1) return 1;
+  if ((pro == kProRmsNorm || m > 8) && c.S > 1) return 1;  // row parts need one split
   if (c.S > 1 && c.strips > kMaxSplitTiles) return 1;
   if (c.S > 65535) return 1;  // past the grid's y limit
   const int64_t blocks = (int64_t)((c.strips + 7) / 8) * 8;  // grid x; grid y: the K splits
@@ -365,9 +368,9 @@ int qtts_launch_w8a16_fused(const void* x, int x_dtype, int64_t m, int64_t k, in
   a.ldy = ldy;
   a.st = st;
   const bool x_aligned = (uintptr_t)x % 16 == 0 && (m == 1 || ldx % 8 == 0);
-  // 1. The prologue inside the GEMM: SiLU * mul for one row, RMSNorm for up to 8.
+  // 1. The prologue inside the GEMM: SiLU * mul for one row, RMSNorm for up to 16.
   if (pro != kProNone && kernel_ok && x_aligned &&
-      ((pro == kProSiluMul && m == 1) || (pro == kProRmsNorm && m <= 8 && !res && (uintptr_t)nw % 16 == 0))) {
+      ((pro == kProSiluMul && m == 1) || (pro == kProRmsNorm && m <= 16 && !res && (uintptr_t)nw % 16 == 0))) {
     a.x = x;
     a.ldx = ldx;
     const int rc = try_fused(pro, res != nullptr, a, x_dtype, sdt, algo, ws, ws_bytes);
@@ -389,8 +392,8 @@ int qtts_launch_w8a16_fused(const void* x, int x_dtype, int64_t m, int64_t k, in
     xin = h;
     ldin = k;
   }
-  // 3. The residual in the GEMM's epilogue (up to 8 staged rows).
-  if (res && kernel_ok && m <= 8 && (uintptr_t)xin % 16 == 0 && (m == 1 || ldin % 8 == 0)) {
+  // 3. The residual in the GEMM's epilogue (up to 16 staged rows).
+  if (res && kernel_ok && m <= 16 && (uintptr_t)xin % 16 == 0 && (m == 1 || ldin % 8 == 0)) {
     a.x = xin;
     a.ldx = ldin;
     const int rc = try_fused(kProNone, true, a, x_dtype, sdt, algo, ws, avail);
@@ -427,7 +430,7 @@ int64_t qtts_w8a16_silu_ws_bytes(int64_t m, int64_t n, int64_t k, int algo, int 
 // act = silu(gate) * up of GatedMLP's gate_up_proj(prologue(x)) on strip weights
 // (qtts/layers/activation.py:142-147): x [m, k]; prologue none or RMSNorm (nw, eps);
 // qs the fused [n, k] gate_up weight (gate rows then up rows, n % 2 == 0); act [m, n/2]
-// with row stride ldact.  Up to 8 decode rows (n % 32 == 0): one launch, the activation
+// with row stride ldact.  Up to 16 decode rows (n % 32 == 0): one launch, the activation
 // in the GEMM's epilogue.  Otherwise the norm, the GEMM into the workspace and
 // silu_mul run one after another.
 int qtts_launch_w8a16_gate_up_silu(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, int pro,
