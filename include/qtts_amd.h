@@ -46,9 +46,9 @@ typedef enum { QTTS_DIV_DEVICE = 0, QTTS_DIV_IEEE = 1 } qtts_div_mode;
  * 16-row weight strip shared by 2 (or 4) workgroups of 8 (or 4) rows, for at most 8 (or 4)
  * activation rows, K a multiple of 128 (or 256) and no split; AUTO takes them where the
  * strips alone would leave compute units idle.  qtts_w8a16_gemm_strips also runs SKINNY_HALF on
- * 9-64 activation rows, in row parts of 8 (ceil(m / 8) workgroups per half strip, each staging
- * its own rows; AUTO takes them on layers of few strips and small weights; the fused entry points
- * then run the plain GEMM and the separate step). */
+ * 9-64 activation rows, and the fused entry points on 9-16, in row parts of 8 (ceil(m / 8)
+ * workgroups per half strip, each staging its own rows; AUTO takes them on layers of few strips
+ * and small weights). */
 typedef enum {
     QTTS_ALGO_AUTO = 0,
     QTTS_ALGO_SKINNY = 1,
@@ -244,11 +244,12 @@ int qtts_rms_norm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
  *   f32(linear)), the linear rounded to x_dtype first, as `residual + o_proj(...)`
  *   (talker.py:270-271).  residual may be y itself (an in-place hidden-state update).
  * Fused into the GEMM launch (prologue computed while the activation rows are staged,
- * residual added in the epilogue): SiLU for m == 1, RMSNorm for m <= 8 (without a
- * residual and without split-K), the residual for m <= 8.  Otherwise the separate
- * kernels run around qtts_w8a16_gemm_strips, through the workspace.  SiLU and the
- * residual give the same bits either way; a fused RMSNorm sums its squares in another
- * order than qtts_rms_norm.  scale_dtype: x_dtype or fp32 for the fused launches (any
+ * residual added in the epilogue): SiLU for m == 1, RMSNorm for m <= 16 (without a
+ * residual and without split-K), the residual for m <= 16 (9-16 rows in two row parts of
+ * 8 with one split).  Otherwise the separate kernels run around qtts_w8a16_gemm_strips,
+ * through the workspace.  SiLU and the residual give the same bits either way; a fused
+ * RMSNorm stages dtype((x * inv) * w) as qtts_rms_norm does, with its sum of squares in
+ * another order.  scale_dtype: x_dtype or fp32 for the fused launches (any
  * for the separate ones).  Workspace: qtts_workspace_bytes(QTTS_OP_W8A16_FUSED). */
 int qtts_w8a16_fused_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
                                  int prologue, const void* norm_weight, float eps,
@@ -261,7 +262,7 @@ int qtts_w8a16_fused_gemm_strips(const void* x, int x_dtype, int64_t m, int64_t 
  *   h = x (QTTS_PRO_NONE) or qtts_rms_norm(x, norm_weight, eps) (QTTS_PRO_RMS_NORM),
  *   g | u = w8a16_linear(h) (qs: the fused [n, k] gate_up weight, gate rows first),
  *   act[r, c] = dtype(dtype(silu(g[r, c])) * u[r, c])   for c < n / 2
- * with the rounding of qtts_w8a16_fused_gemm_strips followed by qtts_silu_mul.  Up to 8
+ * with the rounding of qtts_w8a16_fused_gemm_strips followed by qtts_silu_mul.  Up to 16
  * decode rows with n % 32 == 0 run as ONE launch (a workgroup holds gate strip s and up
  * strip s + n/32 and writes the activation from its epilogue; the gate_up output is
  * never stored); otherwise the prologue, the GEMM and qtts_silu_mul run in turn through
