@@ -115,12 +115,12 @@ bool fp8w_staged(int64_t m, int64_t n, int algo, int S) {
   return (m <= 8 || (S == 1 && skinny_row_parts_auto(m, n))) && !((algo >> 24) & 0x40);
 }
 
-// The W8A16 skinny choice, including 8 waves of 12 chunks for long K from 2 rows.
+// The W8A16 skinny choice, including 8 waves of 12 chunks for long K from 2 to 8 rows.
 SkinnyCfg fp8w_skinny_cfg(int64_t m, int64_t n, int64_t k, int algo) {
   const int splits = (algo >> 8) & 0xff, waves = (algo >> 16) & 0xff, cpw = (algo >> 24) & 0x3f;
   const bool staged = fp8w_staged(m, n, algo, skinny_cfg(m, n, k, splits, waves, cpw).S);
   SkinnyCfg c = skinny_cfg(m, n, k, splits, waves, cpw);
-  if (staged && m >= 2 && waves == 0 && cpw == 0 && c.waves == 16 && c.S == 1 && 8 * 12 >= (k + 63) / 64)
+  if (staged && m >= 2 && m <= 8 && waves == 0 && cpw == 0 && c.waves == 16 && c.S == 1 && 8 * 12 >= (k + 63) / 64)
     c = skinny_cfg(m, n, k, splits, 8, 12);
   return c;
 }

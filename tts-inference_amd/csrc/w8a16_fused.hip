@@ -299,8 +299,8 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
     return qtts_check_launch("w8a16_fused_skinny_sub");
   }
   SkinnyCfg c = skinny_cfg(m, n, k, splits, waves, cpw);
-  // As the plain staged launch: 8 waves of 12 chunks from 2 rows for long K.
-  if (m >= 2 && waves == 0 && cpw == 0 && c.waves == 16 && c.S == 1 && 8 * 12 >= (k + 63) / 64)
+  // As the plain staged launch: 8 waves of 12 chunks from 2 to 8 rows for long K.
+  if (m >= 2 && m <= 8 && waves == 0 && cpw == 0 && c.waves == 16 && c.S == 1 && 8 * 12 >= (k + 63) / 64)
     c = skinny_cfg(m, n, k, splits, 8, 12);
   const int64_t need = skinny_ws(c);
   if (need > ws_bytes || (need > 0 && !ws)) {
