@@ -18,7 +18,7 @@ template <typename XT, typename ST, int SUB, int W, int CPW, int MX>
 void launch_sub(const void* x, int64_t m, int64_t k, int64_t ldx, const int8_t* qs, int64_t n, const void* scale,
                 const void* bias, void* y, int64_t ldy, unsigned blocks, hipStream_t st) {
   qtts::launch_skinny<XT, ST, W, CPW, kLayoutStrips, true, 1, MX, false, kProNone, false, false, SUB>(
-      dim3(blocks, 1, skinny_row_parts(m)), dim3(W * 64), st, qs, (const XT*)x, (const ST*)scale, (const XT*)bias, (const XT*)nullptr,
+      dim3(blocks, 1, (unsigned)((m + MX - 1) / MX)), dim3(W * 64), st, qs, (const XT*)x, (const ST*)scale, (const XT*)bias, (const XT*)nullptr,
       (int)ldx, (int)(m | (1 << 8)), (int)k, (int)n, (XT*)y, ldy, (int64_t)0, (float*)nullptr, (unsigned*)nullptr,
       0.0f, (const XT*)nullptr, (int64_t)0);
 }
@@ -62,14 +62,20 @@ int qtts_w8a16_sub_built(int sub, int waves, int cpw) {
 }
 
 // Launches the row-split staged kernel: m <= 16 / sub (and <= 8) rows of 16-bit activations on
-// full-K strip weights, or up to 64 rows on half strips in row parts of 8 (grid z); grid x =
+// full-K strip weights, or up to 64 rows on half strips in row parts of 8 (grid z: ceil(m / MX)
+// parts of MX staged rows); grid x =
 // blocks (the strips times sub, rounded up to a multiple of 8).
 // Returns QTTS_OK after a launch, 1 when (sub, waves, cpw) is not built, or an error status.
 int qtts_launch_w8a16_skinny_sub(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx, const int8_t* qs,
                                  int64_t n, const void* scale, int sdt, const void* bias, void* y, int64_t ldy,
                                  int sub, int waves, int cpw, unsigned blocks, hipStream_t st) {
   if (!skinny_sub_rows_ok(m, k, sub)) return 1;
-  const int mx = m <= 2 ? (int)m : (m <= 4 ? 4 : 8);
+  // 5-8 rows on at most 64 strips of weights the caller keeps cached (no streaming policy): two
+  // row parts of 4, which fill the compute units half strips leave idle.  Measured on the code
+  // predictor's frame at batch 1 (o_proj and down_proj, 64 strips): 1017.7 -> 1005.3 us; on the
+  // talker's streamed 128-strip layers the second part's re-read cost 44 us a step at M = 6 and 8.
+  const bool halves = sub == 2 && m >= 5 && m <= 8 && (n + 15) / 16 <= 64 && !weight_policy();
+  const int mx = halves ? 4 : (m <= 2 ? (int)m : (m <= 4 ? 4 : 8));
   int rc;
 #define QTTS_SUB_ST(XT)                                                                                          \
   do {                                                                                                           \
