@@ -331,6 +331,20 @@ def run_talker_stack(args, torch, ops):
         del g_q, g_b, g_f, g_fb
         log(f"[bench] M={m}: {per_m[str(m)]}")
 
+    # The layer flow at 16 rows, outside the line's M = 1..8 (a decode step padded to 9-16 rows): the
+    # fused forms run there in two row parts of 8.
+    m16 = 16
+    attn16 = make_inputs(torch, [2048], [m16])[(m16, 2048)]
+    h16 = attn16 * 2
+    g_f = capture(torch, lambda: flows["fused"](h16, attn16))
+    g_fb = capture(torch, lambda: flows["bf16"](h16, attn16))
+    t_f = time_graph(torch, g_f, args.steps, args.warmup)
+    t_fb = time_graph(torch, g_fb, max(5, args.steps // 2), args.warmup)
+    flow16 = {"fused_us": round(t_f * 1e3, 2), "bf16_torch_us": round(t_fb * 1e3, 2),
+              "speedup_vs_bf16": round(t_fb / t_f, 3)}
+    del g_f, g_fb
+    log(f"[bench] layer flow at M={m16}: {flow16}")
+
     # The roofline entry: the mean device duration of gate_up over its 28 distinct weights at each
     # M of the step (the mix the graphs replay), each launch timed by HIP events bound to its
     # dispatch while the GPU is busy (kernel_ms_busy); algorithmic bytes averaged over the mix.
@@ -376,8 +390,10 @@ def run_talker_stack(args, torch, ops):
                    "layer_flow": "per_m.layer_flow_*: the same 28 layers in the decode step's data flow "
                                  "(RMSNorm+qkv, o+residual, RMSNorm+gate_up+SiLU, down+residual fused into the "
                                  "int8 GEMMs) against bf16 torch (hipBLASLt F.linear, F.rms_norm, F.silu, adds); "
-                                 "o_proj reads a fixed synthetic attention output"},
+                                 "o_proj reads a fixed synthetic attention output; layer_flow_m16: the same at "
+                                 "16 rows (not part of the value)"},
         "per_m": per_m,
+        "layer_flow_m16": flow16,
         "roofline": roofline,
     }
     if not args.no_cpu_baseline:
