@@ -246,7 +246,7 @@ int qtts_rms_norm(const void* x, int x_dtype, int64_t m, int64_t k, int64_t ldx,
  * Fused into the GEMM launch (prologue computed while the activation rows are staged,
  * residual added in the epilogue): SiLU for m == 1, RMSNorm for m <= 16 (without a
  * residual and without split-K), the residual for m <= 16 (9-16 rows in two row parts of
- * 8 with one split).  Otherwise the separate kernels run around qtts_w8a16_gemm_strips,
+ * 8 with one split) and up to 64 on half strips (row parts of 8).  Otherwise the separate kernels run around qtts_w8a16_gemm_strips,
  * through the workspace.  SiLU and the residual give the same bits either way; a fused
  * RMSNorm stages dtype((x * inv) * w) as qtts_rms_norm does, with its sum of squares in
  * another order.  scale_dtype: x_dtype or fp32 for the fused launches (any

@@ -129,14 +129,16 @@ def test_norm_prologue(ops, n, k):
 def test_residual_epilogue(ops, n, k):
     for dtype in (torch.bfloat16, torch.float16):
         q, s, qs = _weights(ops, n, k, dtype, seed=3 * n + k)
-        for m in (1, 2, 3, 5, 8, 12, 16):
+        for m in (1, 2, 3, 5, 8, 12, 16, 24, 40):  # past 16: half strips in row parts, else the separate add
             g = torch.Generator(device="cuda").manual_seed(m + n)
             x = torch.randn(m, k, device="cuda", generator=g).to(dtype)
             r = (torch.randn(m, n, device="cuda", generator=g) * 4).to(dtype)
             b = (torch.randn(n, device="cuda", generator=g) * 0.1).to(dtype) if m % 2 else None
             half = ops.algo_code(ops.ALGO_SKINNY_HALF)
             for algo in (0, ops.algo_code(1, 0, 4, 8), ops.algo_code(1, 3, 2, 8), ops.algo_code(1, 0, 8, 12), half):
-                if m > 8 and algo == ops.algo_code(1, 0, 8, 12) and n > 2048:
+                if m > 16 and algo not in (0, half):
+                    continue  # past 16 rows: the automatic choice and half strips in row parts
+                if algo == ops.algo_code(1, 0, 8, 12) and m > 8 and n > 2048:
                     continue  # 8 waves of 12 chunks: staged rows only (9-16 rows: on at most 128 strips)
                 what = f"{dtype} n={n} k={k} m={m} algo={algo:#x}"
                 lin = ops.w8a16_gemm_strips(x, qs, n, s, b, algo)

@@ -272,11 +272,13 @@ int try_fused(int pro, bool res, const FusedArgs& in, int x_dtype, int sdt, int 
   // Row-split strips: the plain launch's choice (w8a16.hip launch_fast), so a fused call and the
   // plain GEMM it replaces give the same bits.
   const int family = algo & 0xff;
-  if (m > 16) return 1;  // up to 16 rows: 9-16 in two row parts of 8
   int sub = family == QTTS_ALGO_SKINNY_HALF ? 2 : (family == QTTS_ALGO_SKINNY_QUARTER ? 4 : 1);
   if (sub > 1 && (splits != 0 || !skinny_sub_rows_ok(m, k, sub))) return 1;  // the separate path reports it
   if (family == QTTS_ALGO_AUTO && splits == 0 && (algo >> 16) == 0)
     sub = m <= 8 ? skinny_auto_sub(m, n, k) : skinny_row_parts_sub(m, n, k);
+  // Up to 16 rows (9-16 in two row parts of 8); past 16 only on half strips in row parts, where
+  // the plain GEMM takes them too.
+  if (m > 16 && sub != 2) return 1;
   if (sub > 1) {
     const SkinnyCfg c = skinny_cfg_sub(n, k, sub, waves, cpw);
     if (!fused_sub_built(sub, c.waves, c.cpw) || c.waves * c.cpw < c.cps || in.ldx > INT32_MAX) return 1;
@@ -392,8 +394,8 @@ int qtts_launch_w8a16_fused(const void* x, int x_dtype, int64_t m, int64_t k, in
     xin = h;
     ldin = k;
   }
-  // 3. The residual in the GEMM's epilogue (up to 16 staged rows).
-  if (res && kernel_ok && m <= 16 && (uintptr_t)xin % 16 == 0 && (m == 1 || ldin % 8 == 0)) {
+  // 3. The residual in the GEMM's epilogue (up to 16 staged rows, up to 64 on half strips).
+  if (res && kernel_ok && m <= kRowPartsMaxM && (uintptr_t)xin % 16 == 0 && (m == 1 || ldin % 8 == 0)) {
     a.x = xin;
     a.ldx = ldin;
     const int rc = try_fused(kProNone, true, a, x_dtype, sdt, algo, ws, avail);
