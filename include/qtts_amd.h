@@ -117,8 +117,11 @@ int qtts_device_supported(int device);
  * LDS; bit 30 makes them load the MFMA operands straight from memory instead (same
  * bits out, for timing both).  For the tile kernels, bits
  * 16-21 are the LDS pipeline stages (2, 3, 4, 6, 8; the int8 W8A8 tile builds 2-4),
- * bit 22 reads each stage's operands from LDS one stage ahead (3 stages or more), and
- * bits 16-23 all zero pick stages and read-ahead automatically.  Bits 24-30 are a tile shape code c: bits 28-30 (c >> 4) log2(BN / 32) in 1..3;
+ * bit 22 reads each stage's operands from LDS one stage ahead (3 stages or more), bit
+ * 23 (W8A16 and fp8 weight-only) makes a stage two 64-column chunks (4-wave 32 x 64
+ * tiles with 3 or 4 stages and read-ahead, an even chunk count per split; same bits as
+ * one chunk a stage), and bits 16-23 all zero pick stages, read-ahead and chunks a
+ * stage automatically.  Bits 24-30 are a tile shape code c: bits 28-30 (c >> 4) log2(BN / 32) in 1..3;
  * bit 27 (c & 8) 8 waves a workgroup in place of 4 (two a SIMD; 3 or 4 stages);
  * for W8A16 bits 24-25 (c & 3) log2(BM / 16) in 1..3 (0: 256 rows, 8 waves only) and
  * bit 26 (c & 4) a 2 x 2 (2 x 4) wave grid in place of 1 x 4 (1 x 8); for W8A8 (fp8,

@@ -53,7 +53,7 @@ A = lib.algo_code
 ra = lib.TILE_READ_AHEAD
 algos = [0, A(lib.ALGO_SKINNY), A(lib.ALGO_TILE), A(lib.ALGO_SKINNY_HALF), A(lib.ALGO_SKINNY_QUARTER)]
 algos += [A(lib.ALGO_SKINNY, s, w, c) for s in (0, 1, 3, 8) for w in (0, 1, 4, 16) for c in (0, 4, 8, 12)]
-algos += [A(lib.ALGO_TILE, s, p, shape) for s in (0, 1, 2, 5) for p in (0, 2, 3, 4, 6, 8, 3 | ra, 4 | ra, 8 | ra)
+algos += [A(lib.ALGO_TILE, s, p, shape) for s in (0, 1, 2, 5) for p in (0, 2, 3, 4, 6, 8, 3 | ra, 4 | ra, 8 | ra, 0x80, 0xC3, 0xC4, 0xC8)
           for shape in (0, 0x11, 0x12, 0x13, 0x21, 0x22, 0x23, 0x31, 0x32, 0x33, 0x15, 0x26, 0x37)]
 algos += [255, 1 << 30, -1]  # malformed words: rejected, never crash
 shapes = [(4096, 2048), (2048, 2048), (12288, 2048), (2048, 6144), (4096, 1024), (1024, 2048), (6144, 1024),

@@ -96,6 +96,12 @@ def test_fp8w_prefill_and_ragged(ops, dtype):
                     y4 = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, 4, shape))
                     y4ra = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, 4 | ops.TILE_READ_AHEAD, shape))
                     assert torch.equal(y4, y4ra), f"read-ahead m={m} n={n} k={k} shape={shape:#x} {dtype}"
+            if (k // 64) % 2 == 0:  # two chunks a stage on the 4-wave 32 x 64 tile: the same bits as one
+                t3264, ra = ops.tile_shape(32, 64), ops.TILE_READ_AHEAD
+                for splits in (1, 2):
+                    y1 = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, 4 | ra, t3264))
+                    y2 = ops.fp8w_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, 4 | ra | ops.TILE_TWO_CHUNKS, t3264))
+                    assert torch.equal(y1, y2), f"two chunks m={m} n={n} k={k} S={splits} {dtype}"
 
 
 def test_fp8w_graph_replays(ops):

@@ -573,6 +573,42 @@ def test_w8a16_strips_tile_forced_shapes(ops):
                         assert torch.equal(y_ra, y), what + " read-ahead"
 
 
+def test_w8a16_strips_tile_two_chunks_a_stage(ops):
+    """Two 64-column chunks a stage (stage bit 23) on the 4-wave 32 x 64 tile with read-ahead: against the
+    oracle and bit for bit the one-chunk kernel with the same split (the same MFMAs in the same order),
+    over one to eight stages a split; the automatic choice, which takes it on at most 256 such tiles,
+    gives the same bits; an odd chunk count a split, another tile or no read-ahead is rejected."""
+    two = ops.TILE_TWO_CHUNKS | ops.TILE_READ_AHEAD
+    t3264 = ops.tile_shape(32, 64)
+    for m, n, k, splits in ((70, 520, 1024, 2), (40, 200, 128, 1), (33, 72, 256, 1), (48, 96, 384, 3),
+                            (130, 272, 2048, 4), (64, 4096, 1024, 0), (17, 1040, 3072, 0)):
+        x, w, b = _make(m, n, k, bias=True, seed=6161 + k + m)
+        q, s = ops.pack_int8(w, torch.bfloat16)
+        qs = ops.to_strips(q)
+        ref = _oracle_w8a16(x, q, s, b)
+        for p in (3, 4):
+            what = f"two chunks m={m} n={n} k={k} S={splits} P={p}"
+            print(what, flush=True)
+            y1 = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, p | ops.TILE_READ_AHEAD, t3264))
+            y2 = ops.w8a16_gemm_strips(x, qs, n, s, b, ops.algo_code(2, splits, p | two, t3264))
+            assert_close(y2, ref, what)
+            assert torch.equal(y1, y2), what
+        if (m, n, k) == (64, 4096, 1024):  # 128 tiles, 16 chunks, one split: the automatic choice takes two a stage
+            assert torch.equal(ops.w8a16_gemm_strips(x, qs, n, s, b), y1), "auto"
+    x, w, b = _make(48, 200, 640, bias=True, seed=17)
+    q, s = ops.pack_int8(w, torch.bfloat16)
+    qs = ops.to_strips(q)
+    with pytest.raises(ValueError, match="even chunk count"):  # 10 chunks in two splits of 5
+        ops.w8a16_gemm_strips(x, qs, 200, s, b, ops.algo_code(2, 2, 4 | two, t3264))
+    with pytest.raises(ValueError, match="even chunk count"):  # 3 chunks
+        ops.w8a16_gemm_strips(x[:, :192].contiguous(), ops.to_strips(q[:, :192].contiguous()), 200, s, b,
+                              ops.algo_code(2, 1, 4 | two, t3264))
+    with pytest.raises(ValueError, match="two chunks a stage are built"):
+        ops.w8a16_gemm_strips(x, qs, 200, s, b, ops.algo_code(2, 1, 4 | two, ops.tile_shape(64, 128)))
+    with pytest.raises(ValueError, match="two chunks a stage are built"):
+        ops.w8a16_gemm_strips(x, qs, 200, s, b, ops.algo_code(2, 1, 4 | ops.TILE_TWO_CHUNKS, t3264))
+
+
 def test_w8a16_strips_tile_eight_waves(ops):
     """Every 8-wave tile the kernel is built for (two waves a SIMD), 3 and 4 stages, with and without
     read-ahead: against the oracle, and bit for bit equal to the 4-wave 32 x 64 tile with the same

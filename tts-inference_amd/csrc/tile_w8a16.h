@@ -64,7 +64,9 @@ __device__ __forceinline__ float scale_bits_to_f32(uint32_t b, int dt) {
 
 template <typename XT> __device__ __forceinline__ float xbits_to_f32(uint32_t b) { return to_f32(XT{(uint16_t)b}); }
 
-template <typename XT, int BM, int BN, int P, int WM, bool F8W, bool PF = false, int NW = 4>
+// CPS: chunks a stage (2: half the stage barriers and load waits of a small-K call; the host
+// keeps every split's chunk count a multiple of it).
+template <typename XT, int BM, int BN, int P, int WM, bool F8W, bool PF = false, int NW = 4, int CPS = 1>
 __global__ __launch_bounds__(NW * 64) void w8a16_pipe_kernel(
     const XT* __restrict__ x, int M, int K, int64_t ldx, const int8_t* __restrict__ qs, int N,
     const void* __restrict__ scale, int sdt, const XT* __restrict__ bias, XT* __restrict__ y, int64_t ldy,
@@ -79,11 +81,12 @@ __global__ __launch_bounds__(NW * 64) void w8a16_pipe_kernel(
   constexpr int WF = BN / 16;          // weight fragments per stage
   constexpr int F = XF + WF;
   constexpr int FPW = F / NW;          // fragments each wave loads per stage
-  constexpr int SB = F * 1024;         // stage bytes
+  constexpr int SB = F * 1024 * CPS;   // stage bytes
   static_assert(F % NW == 0 && (NW == 4 || NW == 8), "fragments must split evenly over the waves");
+  static_assert(CPS == 1 || CPS == 2, "one or two chunks a stage");
   static_assert((WM == 1 || WM == 2) && MB >= 1 && NB >= 1, "wave grid must cover the tile");
   static_assert(P >= 2 && P * SB + 64 <= kLdsBytes, "stage ring must fit in LDS");
-  static_assert((P - 2) * FPW < 64, "vmcnt is 6 bits");
+  static_assert((P - 2) * FPW * CPS < 64, "vmcnt is 6 bits");
   __shared__ __align__(1024) uint8_t ring[P * SB];
   __shared__ uint32_t epi_sc[BN], epi_bi[BN];  // the tile's scale and bias bits, column by column
   __shared__ unsigned flag;
@@ -100,7 +103,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_pipe_kernel(
   const int nchunks = K >> 6;
   const int strips = (N + 15) >> 4;
   const int kc0 = split * cps;
-  const int nk = min(cps, nchunks - kc0);
+  const int nk = min(cps, nchunks - kc0) / CPS;  // stages of this split
 
   // Epilogue operands: thread t < BN loads column t's scale and bias bits first (the oldest
   // loads in flight, so waiting for them costs about what waiting for stage 0 does) and
@@ -133,7 +136,10 @@ __global__ __launch_bounds__(NW * 64) void w8a16_pipe_kernel(
 
   auto issue = [&](uint8_t* stage, int i) __attribute__((always_inline)) {
 #pragma unroll
-    for (int j = 0; j < FPW; ++j) load_to_lds16(src[j] + (int64_t)i * stride[j], stage + (wave * FPW + j) * 1024);
+    for (int c = 0; c < CPS; ++c)
+#pragma unroll
+      for (int j = 0; j < FPW; ++j)
+        load_to_lds16(src[j] + (int64_t)(i * CPS + c) * stride[j], stage + c * F * 1024 + (wave * FPW + j) * 1024);
   };
 
   f32x4_t acc[NB][MB];
@@ -189,13 +195,16 @@ __global__ __launch_bounds__(NW * 64) void w8a16_pipe_kernel(
     // in flight), barrier, issue stage i+P-1, read and consume stage i.
     int cur = 0, nxt = P - 1;
     for (int i = 0; i < nk; ++i) {
-      wait_stages<FPW, P - 2>(nk - 1 - i);
+      wait_stages<FPW * CPS, P - 2>(nk - 1 - i);
       barrier_only();
       if (i + P - 1 < nk) issue(ring + nxt * SB, i + P - 1);
-      V xa[MB][2];
-      i32x4_t wq[NB];
-      read(xa, wq, ring + cur * SB);
-      mma(xa, wq);
+#pragma unroll
+      for (int c = 0; c < CPS; ++c) {
+        V xa[MB][2];
+        i32x4_t wq[NB];
+        read(xa, wq, ring + cur * SB + c * F * 1024);
+        mma(xa, wq);
+      }
       cur = cur + 1 == P ? 0 : cur + 1;
       nxt = nxt + 1 == P ? 0 : nxt + 1;
     }
@@ -208,36 +217,44 @@ __global__ __launch_bounds__(NW * 64) void w8a16_pipe_kernel(
     // after the MFMAs; their latency then passes during the next step's wait and barrier
     // instead of between a barrier and the first MFMA of the stage they feed (pinning them
     // ahead of the MFMAs measured slower: the wait-count pass then waits for them there).
-    V xa0[MB][2], xa1[MB][2];
-    i32x4_t wq0[NB], wq1[NB];
+    V xa0[CPS][MB][2], xa1[CPS][MB][2];
+    i32x4_t wq0[CPS][NB], wq1[CPS][NB];
+    auto read_st = [&](V (&xs)[CPS][MB][2], i32x4_t (&ws)[CPS][NB], const uint8_t* stage) __attribute__((always_inline)) {
+#pragma unroll
+      for (int c = 0; c < CPS; ++c) read(xs[c], ws[c], stage + c * F * 1024);
+    };
+    auto mma_st = [&](const V (&xs)[CPS][MB][2], const i32x4_t (&ws)[CPS][NB]) __attribute__((always_inline)) {
+#pragma unroll
+      for (int c = 0; c < CPS; ++c) mma(xs[c], ws[c]);
+    };
     if (nk > 0) {
-      wait_stages<FPW, P - 2>(nk - 1);
+      wait_stages<FPW * CPS, P - 2>(nk - 1);
       barrier_only();
-      read(xa0, wq0, ring);
+      read_st(xa0, wq0, ring);
     }
     // Steps i with a next stage: wait for stage i+1, barrier, issue stage i+P-1, read
     // stage i+1 into the other register set, then stage i's MFMAs.  The loop runs the
     // steps in pairs with no branch around the MFMAs (a join there makes the register
     // allocator copy every accumulator); the last one or two stages follow it.
-    auto advance = [&](int i, V (&xn)[MB][2], i32x4_t (&wn_)[NB]) __attribute__((always_inline)) {
-      wait_stages<FPW, (P >= 3 ? P - 3 : 0)>(nk - 2 - i);
+    auto advance = [&](int i, V (&xn)[CPS][MB][2], i32x4_t (&wn_)[CPS][NB]) __attribute__((always_inline)) {
+      wait_stages<FPW * CPS, (P >= 3 ? P - 3 : 0)>(nk - 2 - i);
       barrier_only();
       if (i + P - 1 < nk) issue(ring + ((i + P - 1) % P) * SB, i + P - 1);
-      read(xn, wn_, ring + ((i + 1) % P) * SB);
+      read_st(xn, wn_, ring + ((i + 1) % P) * SB);
     };
     int i = 0;
     for (; i + 2 < nk; i += 2) {
       advance(i, xa1, wq1);
-      mma(xa0, wq0);
+      mma_st(xa0, wq0);
       advance(i + 1, xa0, wq0);
-      mma(xa1, wq1);
+      mma_st(xa1, wq1);
     }
     if (i + 1 < nk) {
       advance(i, xa1, wq1);
-      mma(xa0, wq0);
-      mma(xa1, wq1);
+      mma_st(xa0, wq0);
+      mma_st(xa1, wq1);
     } else if (i < nk) {
-      mma(xa0, wq0);
+      mma_st(xa0, wq0);
     }
   }
 
@@ -294,7 +311,7 @@ __global__ __launch_bounds__(NW * 64) void w8a16_pipe_kernel(
 }
 
 
-struct PipeCfg { int bm, bn, P, wm, S, cps, mtiles, ntiles, pf, nw; };
+struct PipeCfg { int bm, bn, P, wm, S, cps, mtiles, ntiles, pf, nw, cps2; };
 
 constexpr int pipe_stage_bytes_c(int bm, int bn) { return (bm / 8 + bn / 16) * 1024; }
 
@@ -334,6 +351,13 @@ inline bool pipe_p_ok(int bm, int bn, int p, int nw = 4) {
 //   in two splits, 128 tiles 0.3 µs); with 8 waves only while that keeps the workgroups
 //   within 256 (a split-K meeting costs more than the idle compute units it fills: gate_up
 //   at M = 128, 192 tiles, 14.9 unsplit against 18.7 in two splits).
+// Two chunks a stage: the 4-wave 32 x 64 tiles with 4 stages and read-ahead where they number
+//   at most 256 and every split's chunk count is even (half the stage waits and barriers of
+//   a latency-bound call; a call minus the same kernel with one chunk a stage, µs, over 5
+//   layers: code predictor qkv -0.53 to -0.59 at M = 48-128, down_proj -0.21 to -0.39 at
+//   64-128, gate_up -0.51 / -0.58 at 48 / 64; talker qkv -1.0 at 48 / 64 and -3.25 at 128,
+//   down_proj -5.48 and o_proj -1.65 at 128).  Past 256 tiles it lost (predictor gate_up
+//   +0.3 at 96 / 128 rows, 288 / 384 tiles; qkv +0.33 at 256 rows, 512 tiles).
 // A workspace too small for the splits drops the automatic choice to one split.
 // shape_req (algo bits 24-30): bits 0-1 log2(BM / 16) in 1..3 (0 = 256 rows, 8 waves
 // only), bit 2 a 2 x 2 (2 x 4 with 8 waves) wave grid in place of 1 x 4 (1 x 8), bit 3
@@ -347,6 +371,7 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
   auto tiles_of = [&](int bm, int bn) { return ((m + bm - 1) / bm) * ((n + bn - 1) / bn); };
   c.wm = 1;
   c.nw = 4;
+  c.cps2 = (stages_req >> 7) & 1;
   if (shape_req != 0) {
     c.nw = (shape_req & 8) ? 8 : 4;
     c.bm = (shape_req & 3) == 0 ? 256 : 16 << (shape_req & 3);
@@ -397,6 +422,9 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
   if (tiles > kMaxSplitTiles) S = 1;
   c.cps = (nchunks + S - 1) / S;
   c.S = (nchunks + c.cps - 1) / c.cps;
+  if (stages_req == 0 && c.nw == 4 && c.bm == 32 && c.bn == 64 && c.P == 4 && c.pf && tiles <= 256 &&
+      c.cps % 2 == 0 && nchunks % 2 == 0)
+    c.cps2 = 1;
   return c;
 }
 
@@ -414,6 +442,14 @@ struct PipeArgs {
 template <bool F8W, typename XT, int BM, int BN, int P, int WM>
 inline void launch_pipe_p(const PipeCfg& c, const PipeArgs& a, unsigned blocks, hipStream_t st) {
   if constexpr (P * pipe_stage_bytes_c(BM, BN) + 64 <= kLdsBytes) {
+    if constexpr (BM == 32 && BN == 64 && WM == 1 && (P == 3 || P == 4)) {
+      if (c.cps2) {
+        qtts::launch(&w8a16_pipe_kernel<XT, BM, BN, P, WM, F8W, true, 4, 2>, dim3(blocks), dim3(256), 0, st,
+                     (const XT*)a.x, (int)a.m, (int)a.k, a.ldx, a.qs, (int)a.n, a.scale, a.sdt, (const XT*)a.bias,
+                     (XT*)a.y, a.ldy, a.part, a.counters, c.mtiles, c.ntiles, c.S, c.cps);
+        return;
+      }
+    }
     if (c.pf)
       qtts::launch(&w8a16_pipe_kernel<XT, BM, BN, P, WM, F8W, true>, dim3(blocks), dim3(256), 0, st, (const XT*)a.x,
                    (int)a.m, (int)a.k, a.ldx, a.qs, (int)a.n, a.scale, a.sdt, (const XT*)a.bias, (XT*)a.y, a.ldy, a.part,
@@ -499,8 +535,8 @@ inline void launch_pipe_bm(const PipeCfg& c, const PipeArgs& a, unsigned blocks,
   else launch_pipe_bn<F8W, XT, 128>(c, a, blocks, st);
 }
 
-// stages_req: bits 0-5 the count, bit 6 read-ahead, nothing above.
-inline bool pipe_stages_ok(int stages) { return stages >= 0 && (stages >> 7) == 0; }
+// stages_req: bits 0-5 the count, bit 6 read-ahead, bit 7 two chunks a stage, nothing above.
+inline bool pipe_stages_ok(int stages) { return stages >= 0 && (stages >> 8) == 0; }
 
 inline bool pipe_shape_ok(int shape) {
   if (shape == 0) return true;
@@ -527,6 +563,9 @@ inline int w8a16_pipe_launch(const char* what, const void* x, int x_dtype, int64
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: read-ahead needs 3 stages", what);
   if (c.bn == 384 && (c.P != 3 || c.pf))
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: 128x384 tiles are built with 3 stages and no read-ahead", what);
+  if (c.cps2 && !(c.nw == 4 && c.bm == 32 && c.bn == 64 && c.wm == 1 && c.pf && (c.P == 3 || c.P == 4)))
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT,
+                          "%s: two chunks a stage are built for 32x64 tiles of 4 waves, 3 or 4 stages, read-ahead", what);
   if (!pipe_p_ok(c.bm, c.bn, c.P, c.nw))
     return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: %d stages are not built for a %dx%d tile", what, c.P,
                           c.bm, c.bn);
@@ -537,6 +576,9 @@ inline int w8a16_pipe_launch(const char* what, const void* x, int x_dtype, int64
                             c.S, (long long)need, (long long)ws_bytes);
     c = pipe_cfg(m, n, k, 1, stages, shape);
   }
+  if (c.cps2 && (c.cps % 2 != 0 || (k / 64) % 2 != 0))
+    return qtts_set_error(QTTS_ERR_INVALID_ARGUMENT, "%s: two chunks a stage need an even chunk count per split (%d)",
+                          what, c.cps);
   const int64_t tiles = (int64_t)c.mtiles * c.ntiles;
   const int64_t blocks = (tiles + 7) / 8 * 8 * c.S;
   if (blocks <= 0 || blocks >= ((int64_t)1 << 31))

@@ -37,9 +37,11 @@ F32, BF16, F16 = 0, 1, 2
 DIV_DEVICE, DIV_IEEE = 0, 1
 # qtts_algo (bits 0-7); bits 8-15 split count, bits 16-23 waves per workgroup,
 # bits 24-31 chunks per wave of the skinny kernels (0 = automatic); for the tile
-# kernels bits 16-21 the stage count, bit 22 read-ahead, bits 24-30 the tile shape
+# kernels bits 16-21 the stage count, bit 22 read-ahead, bit 23 two chunks a stage, bits 24-30 the tile shape
 #: read-ahead flag of a tile kernel's stage field (the `waves` argument of algo_code)
 TILE_READ_AHEAD = 64
+#: two 64-column chunks a stage (W8A16 / fp8 weight-only 32 x 64 tiles of 4 waves, 3 or 4 stages with read-ahead)
+TILE_TWO_CHUNKS = 128
 
 
 def tile_shape(bm: int, bn: int, waves: int = 4, grid2: bool = False) -> int:

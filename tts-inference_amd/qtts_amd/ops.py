@@ -15,7 +15,8 @@ import torch
 from . import _lib
 from ._lib import (ALGO_AUTO, ALGO_SKINNY_HALF, ALGO_SKINNY_QUARTER, ALGO_STREAM, DIV_DEVICE, DIV_IEEE,  # noqa: F401
                    OP_FP8_LINEAR, OP_FP8W, OP_INT8_LINEAR, OP_W8A16, OP_W8A16_FUSED, OP_W8A16_SILU, OP_W8A8_FP8, OP_W8A8_INT8, PRO_NONE,
-                   PRO_RMS_NORM, PRO_SILU_MUL, STRIP_FP8, STRIP_INT8, CODE_E4M3, CODE_INT8, TILE_READ_AHEAD, algo_code, tile_shape)
+                   PRO_RMS_NORM, PRO_SILU_MUL, STRIP_FP8, STRIP_INT8, CODE_E4M3, CODE_INT8, TILE_READ_AHEAD, TILE_TWO_CHUNKS, algo_code,
+                   tile_shape)
 
 _DTYPES = {torch.float32: _lib.F32, torch.bfloat16: _lib.BF16, torch.float16: _lib.F16}
 
