@@ -329,7 +329,9 @@ inline bool pipe_p_ok(int bm, int bn, int p, int nw = 4) {
 //   * 32 x 64 tiles and 4 waves where they number at most 256, up to M = 128, and up to
 //     M = 256 for K <= 4096 (o_proj at M = 256: 9.1; the decode-sized shapes), and where
 //     they number at most 512 for K <= 1024 up to M = 256 (the code predictor's qkv at
-//     M = 256: 8.2 against 10.3 with 8 waves; its gate_up at M = 128: 8.0 against 9.7);
+//     M = 256: 8.2 against 10.3 with 8 waves; its gate_up at M = 128: 8.0 against 9.7),
+//     and where they number at most 384 up to M = 64 (the talker's gate_up at 40 / 48 rows:
+//     -0.7 / -0.4 µs a call against 8 waves on 64 x 128, level at 64);
 //   * otherwise 8 waves (two a SIMD) on a 1 x 8 grid, each wave dequantizing only its own
 //     weight columns, with 4 stages read one stage ahead:
 //       - 128 x 384 tiles (3 stages, no read-ahead: 197 registers, the read-ahead set would
@@ -345,19 +347,24 @@ inline bool pipe_p_ok(int bm, int bn, int p, int nw = 4) {
 //         against 25.7; qkv at M = 1024 25.4 against 26.8);
 //       - else 64 x 128 (down_proj 17.1 / 37.7 against 18.4 / 39.7, o_proj at M = 1024
 //         15.4 against 16.7, gate_up at M = 128 14.9 against 18.5).
-//   Splits: with 4 waves, split K until there are 256 workgroups, keeping >= 8 chunks a
-//   split, except for K <= 1024 with at least 128 tiles (the code predictor's qkv and
-//   gate_up at 40-96 rows, cache-resident: 192 tiles 1.0-1.3 µs a call faster unsplit than
-//   in two splits, 128 tiles 0.3 µs); with 8 waves only while that keeps the workgroups
-//   within 256 (a split-K meeting costs more than the idle compute units it fills: gate_up
-//   at M = 128, 192 tiles, 14.9 unsplit against 18.7 in two splits).
+//   Splits: with 4 waves, split K while the workgroups stay within 256, keeping >= 8 chunks
+//   a split, except for K <= 1024 with at least 128 tiles and for at least 192 tiles (the
+//   code predictor's qkv and gate_up at 40-96 rows, cache-resident: 192 tiles 1.0-1.3 µs a
+//   call faster unsplit than in two splits, 128 tiles 0.3 µs; the talker's gate_up at 17-32
+//   rows and qkv at 72-96, 192 tiles: 0.9-1.6 µs faster unsplit); the former rule split until
+//   there were at least 256 workgroups, up to 384 (the talker's o_proj at 72-96 rows, 96
+//   tiles, 0.8-1.0 µs faster in two splits than in four; at 160-192 rows 1.7-1.9 µs faster
+//   unsplit than in two; the predictor's o_proj and down_proj at 160-192 rows 0.8-1.2);
+//   with 8 waves likewise (a split-K meeting costs more than the idle compute units it
+//   fills: gate_up at M = 128, 192 tiles, 14.9 unsplit against 18.7 in two splits).
 // Two chunks a stage: the 4-wave 32 x 64 tiles with 4 stages and read-ahead where they number
-//   at most 256 and every split's chunk count is even (half the stage waits and barriers of
+//   at most 256 or K >= 2048, and every split's chunk count is even (half the stage waits and barriers of
 //   a latency-bound call; a call minus the same kernel with one chunk a stage, µs, over 5
 //   layers: code predictor qkv -0.53 to -0.59 at M = 48-128, down_proj -0.21 to -0.39 at
 //   64-128, gate_up -0.51 / -0.58 at 48 / 64; talker qkv -1.0 at 48 / 64 and -3.25 at 128,
-//   down_proj -5.48 and o_proj -1.65 at 128).  Past 256 tiles it lost (predictor gate_up
-//   +0.3 at 96 / 128 rows, 288 / 384 tiles; qkv +0.33 at 256 rows, 512 tiles).
+//   down_proj -5.48 and o_proj -1.65 at 128; the talker's gate_up at 40-64 rows, 384 tiles,
+//   -0.1 to -0.8).  Past 256 tiles with K = 1024 it lost (predictor gate_up +0.3 at 96 / 128
+//   rows, 288 / 384 tiles; qkv +0.33 at 256 rows, 512 tiles).
 // A workspace too small for the splits drops the automatic choice to one split.
 // shape_req (algo bits 24-30): bits 0-1 log2(BM / 16) in 1..3 (0 = 256 rows, 8 waves
 // only), bit 2 a 2 x 2 (2 x 4 with 8 waves) wave grid in place of 1 x 4 (1 x 8), bit 3
@@ -378,7 +385,7 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
     c.bn = ((shape_req >> 4) & 7) == 4 ? 384 : 32 << ((shape_req >> 4) & 7);
     c.wm = (shape_req >> 2) & 1 ? 2 : 1;
   } else if (m <= 256 && ((tiles_of(32, 64) <= 256 && (m <= 128 || nchunks <= 64)) ||
-                          (tiles_of(32, 64) <= 512 && nchunks <= 16))) {
+                          (tiles_of(32, 64) <= 512 && nchunks <= 16) || (tiles_of(32, 64) <= 384 && m <= 64))) {
     c.bm = 32;
     c.bn = 64;
   } else {
@@ -415,14 +422,14 @@ inline PipeCfg pipe_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int sta
     S = 1;
     if (c.nw == 8)
       while (tiles * S * 2 <= 256 && nchunks / (S * 2) >= 8) S *= 2;
-    else if (!(nchunks <= 16 && tiles >= 128))
-      while (tiles * S < 256 && nchunks / (S * 2) >= 8) S *= 2;
+    else if (!((nchunks <= 16 && tiles >= 128) || tiles >= 192))
+      while (tiles * S * 2 <= 256 && nchunks / (S * 2) >= 8) S *= 2;
   }
   S = std::max(1, std::min(S, nchunks));
   if (tiles > kMaxSplitTiles) S = 1;
   c.cps = (nchunks + S - 1) / S;
   c.S = (nchunks + c.cps - 1) / c.cps;
-  if (stages_req == 0 && c.nw == 4 && c.bm == 32 && c.bn == 64 && c.P == 4 && c.pf && tiles <= 256 &&
+  if (stages_req == 0 && c.nw == 4 && c.bm == 32 && c.bn == 64 && c.P == 4 && c.pf && (tiles <= 256 || nchunks >= 32) &&
       c.cps % 2 == 0 && nchunks % 2 == 0)
     c.cps2 = 1;
   return c;
