@@ -394,6 +394,13 @@ def test_decode_candidates_include_the_automatic_choice_and_half_strips():
     for rows in (128, 256):
         assert _candidates(rows, 6144)["auto"] == _lib.ALGO_AUTO and "skinny_half" not in _candidates(rows, 6144)
         assert _fp8w_candidates(rows)["auto"] == _lib.ALGO_AUTO
+    # two chunks a tile stage: tile buckets (past 16 rows) with an even chunk count, in one and two splits
+    two = _lib.TILE_READ_AHEAD | _lib.TILE_TWO_CHUNKS
+    for rows in (32, 128):
+        c = _candidates(rows, 6144)
+        assert c["tile_bm32_bn64_c2_s2"] == _lib.algo_code(_lib.ALGO_TILE, 2, 4 | two, _lib.tile_shape(32, 64))
+        assert "tile_bm32_bn64_c2_s1" in c and "tile_bm32_bn64_c2_s1" not in _candidates(rows, 6144 + 64)
+    assert not any("_c2_" in name for name in _candidates(16, 6144))
 
 
 def test_calibrate_buckets_keeps_the_automatic_choice_on_near_ties():

@@ -89,6 +89,10 @@ def _candidates(rows: int, k: int | None = None) -> dict[str, int]:
                 for p in (3, 4):
                     c[f"tile_bm{bm}_bn{bn}_p{p}"] = _lib.algo_code(_lib.ALGO_TILE, 0, p, shape)
                 c[f"tile_bm{bm}_bn{bn}_p4ra"] = _lib.algo_code(_lib.ALGO_TILE, 0, 4 | _lib.TILE_READ_AHEAD, shape)
+        if k is not None and k % 128 == 0:  # two chunks a stage (an odd chunk count a split drops the candidate)
+            for s in (1, 2):
+                c[f"tile_bm32_bn64_c2_s{s}"] = _lib.algo_code(
+                    _lib.ALGO_TILE, s, 4 | _lib.TILE_READ_AHEAD | _lib.TILE_TWO_CHUNKS, _lib.tile_shape(32, 64))
         c.update(tile8_candidates())
     return c
 
