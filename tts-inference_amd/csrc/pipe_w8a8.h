@@ -327,7 +327,14 @@ inline bool w8a8_p_ok(int bm, int bn, int p, int nw = 4) {
 //       - else 64 x 128 tiles, 4 stages read one stage ahead (o_proj at M = 512 / 1024
 //         9.3 / 9.8 [10.9 / 10.7], down_proj 16.6 / 22.2 [18.9 / 25.3], gate_up at M = 128
 //         9.7 [13.2]);
-// then split K: with 4 waves until there are 256 workgroups, keeping >= 4 stages a split;
+// then split K: with 4 waves while the workgroups stay within 256 and the tiles number fewer
+// than 192, keeping >= 4 stages a split (the former rule split until there were at least 256
+// workgroups, up to 384, and from 192 tiles into two; a linear with its activation
+// quantization, over 5 layers, µs, fp8 / int8: the talker's gate_up at 17-32 rows 11.8-12.3
+// -> 10.0-10.3, qkv at 96 rows 11.3 / 11.5 -> 9.5 / 9.7, o_proj at 160-192 rows 11.1-11.5
+// -> 9.3-10.0, down_proj at 160-192 rows 17.4-18.5 -> 16.1-17.3; the predictor's gate_up at
+// 48-64 rows 9.9-10.2 -> 8.1-8.2 (fp8), its o_proj and down_proj at 160-192 rows 0.7-1.1
+// faster; the one loss over 17-256 rows the talker's int8 qkv at 192 rows, +0.18);
 // with 8 waves only while the workgroups stay within 256 and each split keeps >= 16
 // stages (a split-K meeting costs more than idle compute units on short K: o_proj at
 // M = 512, 128 tiles, 9.3 unsplit against 10.2 in two splits).  shape_req: bits 0-2
@@ -380,8 +387,8 @@ inline W8A8PipeCfg w8a8_cfg(int64_t m, int64_t n, int64_t k, int splits_req, int
     S = 1;
     if (c.nw == 8)
       while (tiles * S * 2 <= 256 && nchunks / (S * 2) >= 16) S *= 2;
-    else
-      while (tiles * S < 256 && nchunks / (S * 2) >= 4) S *= 2;
+    else if (tiles < 192)
+      while (tiles * S * 2 <= 256 && nchunks / (S * 2) >= 4) S *= 2;
   }
   S = std::max(1, std::min(S, nchunks));
   if (tiles > kMaxSplitTiles) S = 1;
